@@ -1,0 +1,215 @@
+/*
+ * nanoengine_hip.h - C ABI of libnanoengine_hip.so, the gfx950 (MI355X) kernels
+ * behind nanoengine's speculative-decoding verify step.
+ *
+ * Every entry point takes raw device pointers, plain integer sizes/strides, a
+ * dtype enum and the hipStream_t to launch on (passed as void* so this header
+ * needs no HIP include).  Nothing here allocates, frees or synchronises; a
+ * caller-owned workspace is passed where a kernel needs scratch memory.  All
+ * launches are asynchronous on `stream`.
+ *
+ * Return value: NE_OK (0) or a negative NE_E* code; ne_last_error() then gives a
+ * message for the calling thread.  Shapes are validated on the host before any
+ * launch, so an invalid call launches nothing.
+ *
+ * Reference interfaces each entry point replaces are cited as
+ * path:line relative to the reference tree, with
+ *   ne/ = nanoengine/src/nanoengine/
+ */
+#ifndef NANOENGINE_HIP_H
+#define NANOENGINE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NE_ABI_VERSION 1
+
+/* status codes */
+#define NE_OK 0
+#define NE_EINVAL (-1)       /* bad argument (shape, dtype, null pointer, size) */
+#define NE_EUNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim != 128) */
+#define NE_ELAUNCH (-3)      /* hipLaunchKernel / hipGetLastError reported an error */
+#define NE_EWORKSPACE (-4)   /* workspace too small: query the *_workspace_size call */
+
+/* element types */
+#define NE_DTYPE_BF16 0
+#define NE_DTYPE_FP16 1
+#define NE_DTYPE_FP32 2
+#define NE_DTYPE_INT8 3
+
+/* GEMM epilogues */
+#define NE_EPILOGUE_STORE 0  /* y = bf16(acc * scale[n]) */
+#define NE_EPILOGUE_SWIGLU 1 /* y[:, j] = bf16(silu(gate_j) * up_j), weight rows paired per 16 */
+
+/* acceptance modes */
+#define NE_ACCEPT_GREEDY 0
+#define NE_ACCEPT_SAMPLED 1
+
+int ne_abi_version(void);
+const char* ne_last_error(void);
+
+/*
+ * A1 - n-gram prompt-lookup drafting (replaces NgramProposer.propose,
+ * ne/engine/speculative/proposers.py:39-57, one sequence per call there).
+ * For each sequence b: for n = max_ngram..min_ngram, skip when len <= n; the
+ * suffix is the last n tokens; scan start = len-n-1 down to 0 and take the first
+ * window equal to the suffix; drafts = history[start+n : start+n+num_tokens[b]]
+ * (clipped to len, never empty).  No match or num_tokens[b] == 0 gives 0 drafts.
+ *   history      [num_seqs, history_stride] int32, history_len[b] valid tokens
+ *   num_tokens   [num_seqs] int32, guesses requested (<= max_drafts)
+ *   drafts       [num_seqs, max_drafts] int32 out (unused tail untouched)
+ *   num_drafts   [num_seqs] int32 out
+ */
+int ne_ngram_propose(const int32_t* history, int64_t history_stride, const int32_t* history_len,
+                     const int32_t* num_tokens, int32_t num_seqs, int32_t max_ngram,
+                     int32_t min_ngram, int32_t max_drafts, int32_t* drafts, int32_t* num_drafts,
+                     void* stream);
+
+/*
+ * A7 - quantise-and-scatter new key or value vectors into one layer's slot pool
+ * (replaces write_to_cache + quantize_vectors, ne/models/attention_context.py:42-54,
+ * ne/models/int8_quantization.py:30-34).
+ *   vectors      [n, num_heads, head_dim] bf16 or fp16 (vec_dtype), contiguous
+ *   slot_mapping [n] int32 target slot per vector row
+ *   cache        [num_slots+1, num_heads, head_dim], int8 when cache_dtype is
+ *                NE_DTYPE_INT8, else vec_dtype (plain scatter)
+ *   scales       [num_slots+1, num_heads] in scale_dtype (int8 cache only)
+ * int8: s = max(max|x|, 1e-8) / 127 in fp32 (IEEE division); q = rint(x / s)
+ * clamped to [-127, 127]; the stored scale is s rounded to scale_dtype.
+ */
+int ne_kv_write(const void* vectors, int32_t vec_dtype, int64_t n, int32_t num_heads,
+                int32_t head_dim, const int32_t* slot_mapping, void* cache, int32_t cache_dtype,
+                void* scales, int32_t scale_dtype, void* stream);
+
+/*
+ * A6 - paged multi-query verify attention over a slot pool read in place
+ * (replaces read_from_cache + scaled_dot_product_attention in
+ * run_cached_attention, ne/models/attention_context.py:57-109, and the padded
+ * context-slot / mask construction of ne/engine/generation/batch_builder.py:22-65
+ * and ne/engine/memory/paged_allocator.py:69-79).
+ * Sequence b owns query rows q_start[b] .. q_start[b]+q_len[b]-1 of q/out; its
+ * context is ctx_len[b] tokens (cached tokens plus this step's q_len[b]); the
+ * query at row i sits at position ctx_len[b]-q_len[b]+i and sees keys 0..pos.
+ * Key position p lives in slot block_tables[b, p / block_size] * block_size +
+ * p % block_size.  Query head h uses KV head h / (num_q_heads / num_kv_heads).
+ *   q, out       bf16, element (row, head, d) at row*token_stride + head*head_stride + d
+ *   k/v_cache    [num_slots+1, num_kv_heads, 128] bf16 or int8 (kv_dtype)
+ *   k/v_scale    [num_slots+1, num_kv_heads] bf16 or fp16 (int8 cache only)
+ *   workspace    ne_paged_attention_workspace_size() bytes.  Bytes 0..3 hold an
+ *                error flag (non-zero: a sequence's context exceeded
+ *                max_ctx_len), bytes 256.. the per-unit split tickets.  Zero-fill
+ *                it before its first use and whenever the shape arguments (and
+ *                so its layout) change; every call leaves flag-free tickets at 0.
+ * split_len: keys per work-group (multiple of 128, 0 = choose).  head_dim must be
+ * 128 and block_size a multiple of 16.
+ */
+size_t ne_paged_attention_workspace_size(int32_t num_seqs, int32_t num_q_heads,
+                                         int32_t num_kv_heads, int32_t max_q_len,
+                                         int32_t max_ctx_len, int32_t split_len);
+int ne_paged_verify_attention(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                              const void* k_cache, const void* v_cache, const void* k_scale,
+                              const void* v_scale, int32_t kv_dtype, int32_t scale_dtype,
+                              const int32_t* block_tables, int32_t block_table_stride,
+                              int32_t block_size, const int32_t* ctx_len, const int32_t* q_start,
+                              const int32_t* q_len, int32_t num_seqs, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t max_q_len,
+                              int32_t max_ctx_len, float softmax_scale, void* out,
+                              int64_t out_token_stride, int64_t out_head_stride, int32_t split_len,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * A8 - W8A16 projection: y[m, n] = bf16(sum_k x[m, k] * w[n, k] * scale[n])
+ * with int8 weights dequantised in registers onto bf16 MFMA (replaces
+ * Int8Linear.forward, ne/models/int8_quantization.py:55-57, which materialises
+ * bf16(int8 * scale) and calls F.linear).
+ *   x [m, k] bf16 (row stride ldx), w [n, k] int8, scale [n] bf16/fp16/fp32,
+ *   y [m, n_out] bf16 (row stride ldy); n_out = n, or n/2 for NE_EPILOGUE_SWIGLU
+ *   where weight rows come in groups of 32 (16 gate rows then 16 up rows) and
+ *   y[:, 16*i + j] = bf16(silu(gate) * up) for the pair in group i, row j.
+ * Requires k % 64 == 0.
+ */
+int ne_w8a16_gemm(const void* x, int64_t ldx, const int8_t* w, const void* scale,
+                  int32_t scale_dtype, int32_t m, int32_t n, int32_t k, void* y, int64_t ldy,
+                  int32_t epilogue, void* stream);
+
+/*
+ * A8b - bf16 GEMM for the tied LM head: logits[m, n] = bf16(sum_k x[m,k] w[n,k])
+ * (replaces compute_logits, ne/models/qwen3.py:197-203).  Either output may be
+ * null.  When argmax_partials is given, it receives per (row, 64-column tile) the
+ * largest bf16-rounded logit and its first index, packed for an ordered max, for
+ * ne_accept to finish; ne_lm_head_num_tiles(n) gives the tile count per row.
+ */
+int32_t ne_lm_head_num_tiles(int32_t n);
+int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, int32_t n, int32_t k,
+               void* logits, int64_t ld_logits, uint64_t* argmax_partials, void* stream);
+
+/*
+ * RMSNorm pieces of the Qwen3 layer (ne/models/qwen3.py:31-44, 147-150, 178):
+ * out = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * weight).
+ * ne_rmsnorm:      h = x
+ * ne_add_rmsnorm:  h = bf16(residual + delta); residual is updated in place
+ * ne_embed_rmsnorm: h = embed[token]; residual = h (ne/models/qwen3.py:167)
+ * All tensors bf16, rows of `hidden` elements, contiguous.
+ */
+int ne_rmsnorm(const void* x, const void* weight, void* out, int32_t rows, int32_t hidden,
+               float eps, void* stream);
+int ne_add_rmsnorm(void* residual, const void* delta, const void* weight, void* out, int32_t rows,
+                   int32_t hidden, float eps, void* stream);
+int ne_embed_rmsnorm(const int32_t* tokens, const void* embed, const void* weight, void* residual,
+                     void* out, int32_t rows, int32_t hidden, float eps, void* stream);
+
+/*
+ * Fused QK-norm + RoPE + KV write for one layer (ne/models/qwen3.py:100-104,
+ * 47-68, ne/models/attention_context.py:77-94).  qkv [rows, (Hq+2*Hkv)*128] bf16
+ * holds q | k | v per row.  q_out [rows, Hq, 128] receives RoPE(q_norm(q)); the
+ * key RoPE(k_norm(k)) and value v are written (quantised for an int8 cache) at
+ * slot_mapping[row].  inv_freq [64] fp32 holds 1/theta^(2i/128).
+ */
+int ne_qk_norm_rope_kv_write(const void* qkv, int32_t rows, int32_t num_q_heads,
+                             int32_t num_kv_heads, int32_t head_dim, const void* q_norm_weight,
+                             const void* k_norm_weight, float eps, const int32_t* positions,
+                             const float* inv_freq, const int32_t* slot_mapping, void* k_cache,
+                             void* v_cache, void* k_scale, void* v_scale, int32_t kv_dtype,
+                             int32_t scale_dtype, void* q_out, void* stream);
+
+/*
+ * A9/A10 - fused acceptance (replaces verify_proposal and the sampling helpers,
+ * ne/engine/speculative/verifier.py:21-60, ne/engine/sampling.py:30-42, and the
+ * rollback of ne/engine/speculative/speculative_generator.py:78-83).
+ * Sequence b has num_drafts[b] guesses drafts[b, :] and target rows
+ * row_start[b] .. row_start[b]+num_drafts[b] (one more than its guesses).
+ * Greedy: target token of a row = argmax of its bf16 logits, first index on
+ * ties, from `logits` or, when logits is null, from the ne_lm_head partials.
+ * Keep guesses while guess == target; then append the target of the first
+ * mismatching row (or the bonus row).
+ * Sampled (temperature > 0): p = softmax(fp32(logit) / T) with the fixed-order
+ * contract documented in accept.hip; guess i is kept iff p_i >= 1 or
+ * (p_i > 0 and u_i < p_i); a rejection resamples from p with the guess removed
+ * (p itself if that is empty) and the bonus samples p of the last row, both by
+ * inverse CDF with u_draw.  Uniforms u_i, u_draw come from Philox4x32-10 keyed
+ * by seeds[b] at counter (steps[b], j/4), word j%4, j = i (guesses) and 63.
+ * Outputs: out_tokens[b, 0..num_out[b]-1] (kept guesses + 1 target token);
+ * num_out[b] = kept + 1.  When history is given, the kept tokens and the target
+ * token are appended at history[b, history_len[b]..] and history_len[b] and
+ * num_cached[b] (set to history_len_before + kept) are updated.
+ */
+int ne_accept(int32_t mode, const void* logits, int64_t ld_logits, const uint64_t* argmax_partials,
+              int32_t num_tiles, int32_t vocab, const int32_t* drafts, int32_t max_drafts,
+              const int32_t* num_drafts, const int32_t* row_start, int32_t num_seqs,
+              float temperature, const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens,
+              int32_t* num_out, int32_t* history, int64_t history_stride, int32_t* history_len,
+              int32_t* num_cached, void* stream);
+
+/* Plain device copy of `bytes` bytes (16-byte aligned); used to calibrate the
+ * hardware byte counters against a kernel of known traffic. */
+int ne_copy_bytes(const void* src, void* dst, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOENGINE_HIP_H */

@@ -1,0 +1,431 @@
+"""Tensor-level wrappers over the C ABI: shape/dtype/device checks, then one launch.
+
+Every function here requires device tensors on a ROCm GPU and launches on the
+current torch stream of that device.  None of them has a CPU or PyTorch
+fallback; a missing library or a CPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from nanoengine_amd import _native
+from nanoengine_amd._native import (
+    ACCEPT_GREEDY,
+    ACCEPT_SAMPLED,
+    DTYPE_BF16,
+    DTYPE_FP16,
+    DTYPE_FP32,
+    DTYPE_INT8,
+    EPILOGUE_STORE,
+    EPILOGUE_SWIGLU,
+)
+
+_DTYPE_CODES = {
+    torch.bfloat16: DTYPE_BF16,
+    torch.float16: DTYPE_FP16,
+    torch.float32: DTYPE_FP32,
+    torch.int8: DTYPE_INT8,
+}
+
+HEAD_DIM = 128
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError as error:
+        raise TypeError(f"unsupported dtype {dtype}") from error
+
+
+def _ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for tensor in tensors:
+        if tensor is None:
+            continue
+        if tensor.device.type != "cuda":
+            raise RuntimeError(
+                f"nanoengine HIP kernels need GPU tensors; got one on {tensor.device}"
+            )
+        if device is None:
+            device = tensor.device
+        elif tensor.device != device:
+            raise RuntimeError(f"tensors on different devices: {device} and {tensor.device}")
+    if device is None:
+        raise RuntimeError("no GPU tensor given")
+    return device
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check(cond: bool, message: str) -> None:
+    if not cond:
+        raise ValueError(message)
+
+
+def _contig(tensor: torch.Tensor, name: str) -> None:
+    _check(tensor.is_contiguous(), f"{name} must be contiguous")
+
+
+def _int32(tensor: torch.Tensor, name: str) -> None:
+    _check(tensor.dtype == torch.int32, f"{name} must be int32, got {tensor.dtype}")
+    _contig(tensor, name)
+
+
+# --------------------------------------------------------------------------- A1
+def ngram_propose(
+    history: torch.Tensor,
+    history_len: torch.Tensor,
+    num_tokens: torch.Tensor,
+    max_ngram: int,
+    max_drafts: int,
+    min_ngram: int = 1,
+    drafts: torch.Tensor | None = None,
+    num_drafts: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Drafts ``[b, max_drafts]`` (tail unused) and their counts ``[b]`` from each history."""
+    device = _require_gpu(history, history_len, num_tokens)
+    _int32(history, "history")
+    _int32(history_len, "history_len")
+    _int32(num_tokens, "num_tokens")
+    _check(history.dim() == 2, "history must be [num_seqs, capacity]")
+    num_seqs = history.shape[0]
+    if drafts is None:
+        drafts = torch.zeros((num_seqs, max_drafts), dtype=torch.int32, device=device)
+    if num_drafts is None:
+        num_drafts = torch.empty((num_seqs,), dtype=torch.int32, device=device)
+    _native.call(
+        "ne_ngram_propose",
+        _ptr(history), history.stride(0), _ptr(history_len), _ptr(num_tokens), num_seqs,
+        max_ngram, min_ngram, max_drafts, _ptr(drafts), _ptr(num_drafts), _stream(device),
+    )
+    return drafts, num_drafts
+
+
+# --------------------------------------------------------------------------- A7
+def kv_write(
+    vectors: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    cache: torch.Tensor,
+    scales: torch.Tensor | None,
+) -> None:
+    """Write ``vectors [n, heads, 128]`` to ``cache`` at ``slot_mapping`` (quantising to int8)."""
+    device = _require_gpu(vectors, slot_mapping, cache, scales)
+    _contig(vectors, "vectors")
+    _int32(slot_mapping, "slot_mapping")
+    _check(vectors.dim() == 3 and vectors.shape[2] == HEAD_DIM, "vectors must be [n, heads, 128]")
+    _check(cache.dim() == 3 and cache.shape[1:] == vectors.shape[1:], "cache shape mismatch")
+    _check(slot_mapping.numel() == vectors.shape[0], "one slot per vector row")
+    if cache.dtype == torch.int8:
+        _check(scales is not None and scales.shape[0] == cache.shape[0], "int8 cache needs scales")
+    _native.call(
+        "ne_kv_write",
+        _ptr(vectors), dtype_code(vectors.dtype), vectors.shape[0], vectors.shape[1], HEAD_DIM,
+        _ptr(slot_mapping), _ptr(cache), dtype_code(cache.dtype), _ptr(scales),
+        dtype_code(scales.dtype) if scales is not None else DTYPE_BF16, _stream(device),
+    )
+
+
+# --------------------------------------------------------------------------- A6
+@dataclass
+class AttentionWorkspace:
+    """Caller-owned scratch for split-K attention; re-zeroed when its layout changes."""
+
+    buffer: torch.Tensor | None = None
+    layout: tuple | None = None
+
+    def get(self, device: torch.device, nbytes: int, layout: tuple) -> torch.Tensor:
+        if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
+            self.buffer = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self.layout = layout
+        elif self.layout != layout:
+            self.buffer.zero_()
+            self.layout = layout
+        return self.buffer
+
+    def error_flag(self) -> int:
+        if self.buffer is None:
+            return 0
+        return int(self.buffer[:4].view(torch.int32).item())
+
+
+_default_workspaces: dict[torch.device, AttentionWorkspace] = {}
+
+
+def default_workspace(device: torch.device) -> AttentionWorkspace:
+    return _default_workspaces.setdefault(device, AttentionWorkspace())
+
+
+def paged_verify_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    block_tables: torch.Tensor,
+    block_size: int,
+    ctx_len: torch.Tensor,
+    q_start: torch.Tensor,
+    q_len: torch.Tensor,
+    max_q_len: int,
+    max_ctx_len: int,
+    softmax_scale: float | None = None,
+    out: torch.Tensor | None = None,
+    workspace: AttentionWorkspace | None = None,
+    split_len: int = 0,
+) -> torch.Tensor:
+    """Paged multi-query attention; ``q``/``out`` are ``[rows, q_heads, 128]`` bf16."""
+    device = _require_gpu(q, k_cache, v_cache, k_scale, v_scale, block_tables, ctx_len, q_start,
+                          q_len)
+    _check(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == HEAD_DIM,
+           "q must be [rows, heads, 128] bf16")
+    _check(q.stride(2) == 1, "q head_dim must be contiguous")
+    _check(k_cache.shape == v_cache.shape and k_cache.dim() == 3, "k/v cache shape mismatch")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    is_int8 = k_cache.dtype == torch.int8
+    if is_int8:
+        _check(k_scale is not None and v_scale is not None, "int8 cache needs scales")
+        _check(k_scale.is_contiguous() and v_scale.is_contiguous(), "scales must be contiguous")
+        _check(k_scale.numel() == k_cache.shape[0] * k_cache.shape[1], "k_scale shape mismatch")
+    else:
+        _check(k_cache.dtype == torch.bfloat16, "cache must be int8 or bf16")
+    _int32(block_tables, "block_tables")
+    for name, t in (("ctx_len", ctx_len), ("q_start", q_start), ("q_len", q_len)):
+        _int32(t, name)
+    num_seqs = ctx_len.shape[0]
+    num_q_heads = q.shape[1]
+    num_kv_heads = k_cache.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    _check(out.shape == q.shape and out.dtype == torch.bfloat16 and out.stride(2) == 1,
+           "out must match q")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(HEAD_DIM)
+    nbytes = _native.load().ne_paged_attention_workspace_size(
+        num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len
+    )
+    _check(nbytes > 0, "bad attention shape")
+    ws = (workspace or default_workspace(device)).get(
+        device, nbytes, (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len)
+    )
+    _native.call(
+        "ne_paged_verify_attention",
+        _ptr(q), q.stride(0), q.stride(1),
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        dtype_code(k_cache.dtype), dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16,
+        _ptr(block_tables), block_tables.stride(0), block_size,
+        _ptr(ctx_len), _ptr(q_start), _ptr(q_len),
+        num_seqs, num_q_heads, num_kv_heads, HEAD_DIM, max_q_len, max_ctx_len,
+        float(softmax_scale),
+        _ptr(out), out.stride(0), out.stride(1),
+        split_len, _ptr(ws), ws.numel(), _stream(device),
+    )
+    return out
+
+
+# --------------------------------------------------------------------------- A8
+def w8a16_gemm(
+    x: torch.Tensor,
+    weight_int8: torch.Tensor,
+    weight_scale: torch.Tensor,
+    epilogue: int = EPILOGUE_STORE,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``bf16(x @ (int8 * scale).T)``; SwiGLU epilogue pairs 16 gate rows with 16 up rows."""
+    device = _require_gpu(x, weight_int8, weight_scale)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1, "x must be [m, k] bf16")
+    _check(weight_int8.dtype == torch.int8 and weight_int8.dim() == 2, "weight must be [n, k] int8")
+    _contig(weight_int8, "weight_int8")
+    _contig(weight_scale, "weight_scale")
+    m, k = x.shape
+    n = weight_int8.shape[0]
+    _check(weight_int8.shape[1] == k, f"k mismatch: x has {k}, weight {weight_int8.shape[1]}")
+    _check(weight_scale.numel() == n, "one scale per weight row")
+    n_out = n // 2 if epilogue == EPILOGUE_SWIGLU else n
+    if out is None:
+        out = torch.empty((m, n_out), dtype=torch.bfloat16, device=device)
+    _check(out.shape == (m, n_out) and out.stride(1) == 1, "bad out shape")
+    _native.call(
+        "ne_w8a16_gemm",
+        _ptr(x), x.stride(0), _ptr(weight_int8), _ptr(weight_scale),
+        dtype_code(weight_scale.dtype), m, n, k, _ptr(out), out.stride(0), epilogue,
+        _stream(device),
+    )
+    return out
+
+
+def lm_head_num_tiles(vocab: int) -> int:
+    return int(_native.load().ne_lm_head_num_tiles(vocab))
+
+
+def lm_head(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    logits: torch.Tensor | bool = True,
+    argmax_partials: torch.Tensor | bool = False,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """``x [m, k] @ weight[n, k].T`` in bf16; optionally only per-tile argmax partials."""
+    device = _require_gpu(x, weight)
+    _check(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "bf16 inputs required")
+    _check(x.dim() == 2 and x.stride(1) == 1, "x must be [m, k]")
+    _contig(weight, "weight")
+    m, k = x.shape
+    n = weight.shape[0]
+    if logits is True:
+        logits = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    elif logits is False:
+        logits = None
+    if argmax_partials is True:
+        argmax_partials = torch.empty((m, lm_head_num_tiles(n)), dtype=torch.int64, device=device)
+    elif argmax_partials is False:
+        argmax_partials = None
+    _native.call(
+        "ne_lm_head",
+        _ptr(x), x.stride(0), _ptr(weight), m, n, k, _ptr(logits),
+        logits.stride(0) if logits is not None else 0, _ptr(argmax_partials), _stream(device),
+    )
+    return logits, argmax_partials
+
+
+# ------------------------------------------------------------------- norms, RoPE
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out=None) -> torch.Tensor:
+    device = _require_gpu(x, weight)
+    _contig(x, "x")
+    out = torch.empty_like(x) if out is None else out
+    rows, hidden = x.shape
+    _native.call("ne_rmsnorm", _ptr(x), _ptr(weight), _ptr(out), rows, hidden, float(eps),
+                 _stream(device))
+    return out
+
+
+def add_rmsnorm(residual: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps: float,
+                out=None) -> torch.Tensor:
+    """``residual += delta`` (bf16) in place, then RMSNorm of the new residual."""
+    device = _require_gpu(residual, delta, weight)
+    _contig(residual, "residual")
+    _contig(delta, "delta")
+    out = torch.empty_like(residual) if out is None else out
+    rows, hidden = residual.shape
+    _native.call("ne_add_rmsnorm", _ptr(residual), _ptr(delta), _ptr(weight), _ptr(out), rows,
+                 hidden, float(eps), _stream(device))
+    return out
+
+
+def embed_rmsnorm(tokens: torch.Tensor, embed: torch.Tensor, weight: torch.Tensor, eps: float,
+                  residual=None, out=None) -> tuple[torch.Tensor, torch.Tensor]:
+    device = _require_gpu(tokens, embed, weight)
+    _int32(tokens, "tokens")
+    rows = tokens.numel()
+    hidden = embed.shape[1]
+    if residual is None:
+        residual = torch.empty((rows, hidden), dtype=embed.dtype, device=device)
+    if out is None:
+        out = torch.empty((rows, hidden), dtype=embed.dtype, device=device)
+    _native.call("ne_embed_rmsnorm", _ptr(tokens), _ptr(embed), _ptr(weight), _ptr(residual),
+                 _ptr(out), rows, hidden, float(eps), _stream(device))
+    return residual, out
+
+
+def qk_norm_rope_kv_write(
+    qkv: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    eps: float,
+    positions: torch.Tensor,
+    inv_freq: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    q_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    device = _require_gpu(qkv, q_norm_weight, k_norm_weight, positions, inv_freq, slot_mapping,
+                          k_cache, v_cache)
+    _contig(qkv, "qkv")
+    _int32(positions, "positions")
+    _int32(slot_mapping, "slot_mapping")
+    _check(inv_freq.dtype == torch.float32 and inv_freq.numel() == HEAD_DIM // 2, "inv_freq [64] fp32")
+    rows = qkv.shape[0]
+    _check(qkv.shape[1] == (num_q_heads + 2 * num_kv_heads) * HEAD_DIM, "qkv width mismatch")
+    if q_out is None:
+        q_out = torch.empty((rows, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    is_int8 = k_cache.dtype == torch.int8
+    _native.call(
+        "ne_qk_norm_rope_kv_write",
+        _ptr(qkv), rows, num_q_heads, num_kv_heads, HEAD_DIM,
+        _ptr(q_norm_weight), _ptr(k_norm_weight), float(eps),
+        _ptr(positions), _ptr(inv_freq), _ptr(slot_mapping),
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        dtype_code(k_cache.dtype), dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16,
+        _ptr(q_out), _stream(device),
+    )
+    return q_out
+
+
+# ------------------------------------------------------------------------ A9/A10
+def accept(
+    drafts: torch.Tensor,
+    num_drafts: torch.Tensor,
+    row_start: torch.Tensor,
+    vocab: int,
+    logits: torch.Tensor | None = None,
+    argmax_partials: torch.Tensor | None = None,
+    temperature: float = 0.0,
+    seeds: torch.Tensor | None = None,
+    steps: torch.Tensor | None = None,
+    out_tokens: torch.Tensor | None = None,
+    num_out: torch.Tensor | None = None,
+    history: torch.Tensor | None = None,
+    history_len: torch.Tensor | None = None,
+    num_cached: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Accepted guesses plus one target token per sequence: ``(out_tokens [b, k+1], num_out [b])``."""
+    device = _require_gpu(drafts, num_drafts, row_start, logits, argmax_partials)
+    _int32(drafts, "drafts")
+    _int32(num_drafts, "num_drafts")
+    _int32(row_start, "row_start")
+    num_seqs, max_drafts = drafts.shape
+    mode = ACCEPT_GREEDY if temperature == 0.0 else ACCEPT_SAMPLED
+    if logits is not None:
+        _check(logits.dtype == torch.bfloat16 and logits.stride(1) == 1, "logits must be bf16 rows")
+        _check(logits.shape[1] == vocab, "logits width must equal vocab")
+    if mode == ACCEPT_SAMPLED:
+        _check(logits is not None, "sampled acceptance needs logits")
+        _check(seeds is not None and steps is not None, "sampled acceptance needs seeds and steps")
+        _check(seeds.dtype == torch.int64 and steps.dtype == torch.int64, "seeds/steps int64")
+    if out_tokens is None:
+        out_tokens = torch.empty((num_seqs, max_drafts + 1), dtype=torch.int32, device=device)
+    if num_out is None:
+        num_out = torch.empty((num_seqs,), dtype=torch.int32, device=device)
+    num_tiles = argmax_partials.shape[1] if argmax_partials is not None else 0
+    _native.call(
+        "ne_accept",
+        mode, _ptr(logits), logits.stride(0) if logits is not None else 0,
+        _ptr(argmax_partials), num_tiles, vocab,
+        _ptr(drafts), max_drafts, _ptr(num_drafts), _ptr(row_start), num_seqs,
+        float(temperature), _ptr(seeds), _ptr(steps),
+        _ptr(out_tokens), _ptr(num_out),
+        _ptr(history), history.stride(0) if history is not None else 0,
+        _ptr(history_len), _ptr(num_cached), _stream(device),
+    )
+    return out_tokens, num_out
+
+
+def copy_bytes(src: torch.Tensor, dst: torch.Tensor) -> None:
+    device = _require_gpu(src, dst)
+    nbytes = src.numel() * src.element_size()
+    _check(dst.numel() * dst.element_size() >= nbytes, "dst too small")
+    _native.call("ne_copy_bytes", _ptr(src), _ptr(dst), nbytes, _stream(device))

@@ -1,0 +1,101 @@
+"""Acceptance under this build's explicit-uniform contract (test infrastructure only).
+
+Greedy (ne/engine/speculative/verifier.py:27-60 with one-hot p and q): keep guesses
+while they equal the row argmax (first index on ties, numpy/torch order), then
+append the argmax of the first mismatching row or of the bonus row.
+
+Sampled: the C oracle in ``csrc/accept_oracle.c`` (built by ``oracle/Makefile``)
+restates the contract documented in the HIP kernel; this module loads it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "_build" / "libaccept_oracle.so"
+
+_lib: ctypes.CDLL | None = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        handle = ctypes.CDLL(str(LIB_PATH))
+        handle.oracle_cephes_exp.restype = ctypes.c_float
+        handle.oracle_cephes_exp.argtypes = [ctypes.c_float]
+        handle.oracle_uniform.restype = ctypes.c_float
+        handle.oracle_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
+        handle.oracle_philox4x32_10.restype = None
+        handle.oracle_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        handle.oracle_accept_sampled.restype = ctypes.c_int
+        handle.oracle_accept_sampled.argtypes = [
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+            ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        _lib = handle
+    return _lib
+
+
+def cephes_exp(x: float) -> float:
+    return float(lib().oracle_cephes_exp(ctypes.c_float(x)))
+
+
+def philox4x32_10(counter: list[int], key: list[int]) -> list[int]:
+    ctr = (ctypes.c_uint32 * 4)(*counter)
+    k = (ctypes.c_uint32 * 2)(*key)
+    lib().oracle_philox4x32_10(ctr, k)
+    return list(ctr)
+
+
+def uniform(seed: int, step: int, j: int) -> float:
+    return float(lib().oracle_uniform(seed, step, j))
+
+
+def bf16_bits(values: np.ndarray) -> np.ndarray:
+    """float32 values that are exact bf16 -> their 16-bit patterns."""
+    bits = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32)
+    return (bits >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def greedy_accept(rows: np.ndarray, drafts: list[int]) -> list[int]:
+    """``rows [g+1, V]`` float logits (already bf16-rounded) -> kept guesses + target token."""
+    targets = np.argmax(rows, axis=-1)
+    kept: list[int] = []
+    for i, guess in enumerate(drafts):
+        if guess != int(targets[i]):
+            return [*kept, int(targets[i])]
+        kept.append(guess)
+    return [*kept, int(targets[len(drafts)])]
+
+
+def sampled_accept(row_bits: np.ndarray, drafts: list[int], temperature: float, seed: int,
+                   step: int) -> list[int]:
+    """``row_bits [g+1, V]`` uint16 bf16 patterns -> kept guesses + drawn token (C oracle)."""
+    rows = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    g = len(drafts)
+    assert rows.shape[0] == g + 1
+    vocab = rows.shape[1]
+    d = np.ascontiguousarray(np.asarray(drafts, dtype=np.int32))
+    out = np.zeros(g + 1, dtype=np.int32)
+    scratch = np.zeros(vocab, dtype=np.float32)
+    n = lib().oracle_accept_sampled(
+        rows.ctypes.data, vocab, vocab, d.ctypes.data if g else None, g, ctypes.c_float(temperature),
+        seed, step, out.ctypes.data, scratch.ctypes.data,
+    )
+    return out[:n].tolist()

@@ -1,0 +1,118 @@
+"""A6: the HIP paged verify attention against the oracle (fp32 restatement of the reference's
+gather + dequant + masked SDPA, ne/models/attention_context.py:57-109).
+
+Bar: relative error <= 2e-2 (bf16), checked on the rows of real queries.  Shapes
+follow the kernel-only attention configurations: 16 Q / 8 KV heads, head_dim 128,
+16-token blocks drawn from a seeded permutation of a 4096-block pool, 5 query
+tokens per sequence with causal masking among them.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import make_batch, make_pool, real_rows, rel_err
+from oracle.attention import paged_attention_reference
+from nanoengine_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+HQ, HKV = 16, 8
+
+
+def run_case(device, ctx_lens, q_lens, kv_dtype, scale_dtype=torch.bfloat16, block_size=16,
+             num_blocks=None, split_len=0, padded_q=None, seed=0):
+    num_blocks = num_blocks or max(64, sum((c + block_size - 1) // block_size for c in ctx_lens) + 8)
+    kc, vc, ks, vs = make_pool(num_blocks, block_size, HKV, kv_dtype, scale_dtype, seed=seed)
+    tables, ctx, qs, ql, rows = make_batch(ctx_lens, q_lens, num_blocks, block_size, seed=seed + 1,
+                                           padded_q=padded_q)
+    g = torch.Generator().manual_seed(seed + 2)
+    q = torch.randn(rows, HQ, 128, generator=g).to(torch.bfloat16)
+    ref = paged_attention_reference(q, kc, vc, ks, vs, tables, block_size, ctx, qs, ql,
+                                    model_dtype=scale_dtype if kv_dtype == "int8" else torch.bfloat16)
+    d = lambda t: None if t is None else t.to(device)
+    out = kernels.paged_verify_attention(
+        d(q), d(kc), d(vc), d(ks), d(vs), d(tables), block_size, d(ctx), d(qs), d(ql),
+        max_q_len=max(q_lens), max_ctx_len=max(ctx_lens), split_len=split_len,
+    )
+    torch.cuda.synchronize()
+    idx = real_rows(qs, ql)
+    return out.cpu()[idx], ref[idx], out
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "int8"])
+def test_small_ragged_batch(device, kv_dtype):
+    got, ref, _ = run_case(device, [5, 17, 40, 129, 300], [5, 1, 3, 5, 2], kv_dtype)
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "int8"])
+@pytest.mark.parametrize("split_len", [128, 256])
+def test_split_k_merge_and_fully_masked_split_rows(device, kv_dtype, split_len):
+    # contexts just past a split boundary: the last split holds keys that early
+    # queries may not see, so some rows of that split are fully masked
+    ctx = [split_len + 1, split_len + 3, 2 * split_len + 2, 3 * split_len, 1000]
+    got, ref, _ = run_case(device, ctx, [5, 5, 5, 5, 5], kv_dtype, split_len=split_len)
+    assert rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.bfloat16])
+def test_int8_scale_dtypes(device, scale_dtype):
+    got, ref, _ = run_case(device, [64, 200, 513], [5, 5, 5], "int8", scale_dtype=scale_dtype)
+    assert rel_err(got, ref) < TOL
+
+
+def test_padded_layout_and_block_size_32(device):
+    got, ref, _ = run_case(device, [33, 90, 250], [4, 5, 1], "int8", block_size=32, padded_q=5)
+    assert rel_err(got, ref) < TOL
+
+
+def test_prefill_shape_many_query_rows(device):
+    # q_len 64 -> 128 query rows per KV head: eight 16-row M tiles with per-tile key bounds
+    got, ref, _ = run_case(device, [64, 100], [64, 37], "bf16")
+    assert rel_err(got, ref) < TOL
+
+
+def test_k8_drafts_use_two_row_tiles(device):
+    got, ref, _ = run_case(device, [300, 1500], [9, 9], "int8")
+    assert rel_err(got, ref) < TOL
+
+
+def test_deterministic(device):
+    _, _, a = run_case(device, [100, 700, 1500], [5, 5, 5], "int8", split_len=128)
+    _, _, b = run_case(device, [100, 700, 1500], [5, 5, 5], "int8", split_len=128)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_cfg1_bf16_full_shape(device):
+    """16 sequences, context U{256..2048} (seed 1), 5 queries, bf16 KV, 4096-block pool."""
+    rng = np.random.default_rng(1)
+    ctx = rng.integers(256, 2049, size=16).tolist()
+    got, ref, _ = run_case(device, ctx, [5] * 16, "bf16", num_blocks=4096)
+    assert rel_err(got, ref) < TOL
+
+
+def test_cfg2_int8_full_shape(device):
+    """64 sequences, context U{128..1024}, int8 KV with fp16 scales, 4096-block pool."""
+    rng = np.random.default_rng(1)
+    ctx = rng.integers(128, 1025, size=64).tolist()
+    got, ref, _ = run_case(device, ctx, [5] * 64, "int8", scale_dtype=torch.float16, num_blocks=4096)
+    assert rel_err(got, ref) < TOL
+
+
+def test_workspace_error_flag_stays_clear(device):
+    ws = kernels.AttentionWorkspace()
+    kc, vc, ks, vs = make_pool(64, 16, HKV, "int8")
+    tables, ctx, qs, ql, rows = make_batch([500, 20], [5, 5], 64, 16)
+    q = torch.randn(rows, HQ, 128).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    kernels.paged_verify_attention(d(q), d(kc), d(vc), d(ks), d(vs), d(tables), 16, d(ctx), d(qs), d(ql),
+                                   max_q_len=5, max_ctx_len=500, workspace=ws, split_len=128)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    counters = ws.buffer[256:256 + 4 * 64].view(torch.int32)
+    assert int(counters.abs().sum()) == 0  # tickets left at zero for the next call

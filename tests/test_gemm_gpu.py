@@ -1,0 +1,108 @@
+"""A8 / A8b: the W8A16 projection GEMMs and the bf16 LM head against the oracle.
+
+W8A16 is checked against the reference's Int8Linear (ne/models/int8_quantization.py:55-57,
+dequantise then F.linear) evaluated in fp32 on the CPU: relative error <= 2e-2.
+The LM head is checked against an fp32 product: logits within 1e-2 max-abs at the
+model's scale (hidden ~ N(0,1) * 0.02-scale norm weight, embedding ~ N(0, 0.02)),
+relative error <= 2e-2, and its fused argmax partials reduce to exactly the argmax of
+the kernel's own bf16 logits.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import rel_err
+from oracle.quant import int8_linear, quantize_linear
+from nanoengine_amd import kernels
+from nanoengine_amd._native import EPILOGUE_SWIGLU
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+# (N, K) of q, k, v, o, gate, up, down in Qwen3-0.6B, plus the fused qkv and gate|up shapes
+PROJECTIONS = [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (3072, 1024),
+               (1024, 3072), (4096, 1024)]
+
+
+def make_weight(n, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    return quantize_linear(w)
+
+
+@pytest.mark.parametrize("n,k", PROJECTIONS)
+@pytest.mark.parametrize("m", [320, 37, 5])
+def test_w8a16_matches_int8_linear(device, m, n, k):
+    wq, ws = make_weight(n, k, seed=n + k)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    ref = int8_linear(x.float(), wq, ws.float())
+    ref_bf16 = int8_linear(x, wq, ws)  # the reference's own bf16 path
+    out = kernels.w8a16_gemm(x.to(device), wq.to(device), ws.to(device))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < TOL
+    assert rel_err(out, ref_bf16) < TOL
+
+
+def test_w8a16_fp16_overflow_free(device):
+    """int8_quantization.py:41-43: large activations must not overflow (scale is applied in fp32)."""
+    wq, ws = make_weight(256, 1024, seed=3)
+    x = (torch.randn(16, 1024) * 60).to(torch.bfloat16)
+    out = kernels.w8a16_gemm(x.to(device), wq.to(device), ws.to(device))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert rel_err(out, int8_linear(x.float(), wq, ws.float())) < TOL
+
+
+def pair_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """Interleave rows in groups of 32: 16 gate rows then the same 16 up rows."""
+    n, k = gate.shape
+    return torch.stack([gate.view(n // 16, 16, k), up.view(n // 16, 16, k)], dim=1).reshape(2 * n, k)
+
+
+@pytest.mark.parametrize("m", [320, 21])
+def test_swiglu_epilogue(device, m):
+    gq, gs = make_weight(3072, 1024, seed=11)
+    uq, us = make_weight(3072, 1024, seed=12)
+    wq = pair_gate_up(gq, uq)
+    ws = pair_gate_up(gs[:, None], us[:, None])[:, 0].contiguous()
+    x = torch.randn(m, 1024).to(torch.bfloat16)
+    gate = int8_linear(x.float(), gq, gs.float())
+    up = int8_linear(x.float(), uq, us.float())
+    ref = torch.nn.functional.silu(gate) * up
+    out = kernels.w8a16_gemm(x.to(device), wq.to(device), ws.to(device), epilogue=EPILOGUE_SWIGLU)
+    torch.cuda.synchronize()
+    assert out.shape == (m, 3072)
+    assert rel_err(out, ref) < TOL
+
+
+@pytest.mark.parametrize("m,vocab", [(320, 151936), (5, 4096), (70, 8192)])
+def test_lm_head_logits_and_argmax(device, m, vocab):
+    g = torch.Generator().manual_seed(vocab + m)
+    hidden = (torch.randn(m, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    embed = (torch.randn(vocab, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    ref = hidden.float() @ embed.float().T
+    logits, partials = kernels.lm_head(hidden.to(device), embed.to(device), logits=True,
+                                       argmax_partials=True)
+    torch.cuda.synchronize()
+    assert float((logits.float().cpu() - ref).abs().max()) < 1e-2
+    assert rel_err(logits, ref) < TOL
+    # partial argmax reduces to the first-index argmax of the kernel's own bf16 logits
+    p = partials.cpu()
+    best = p.max(dim=1).values
+    idx = (0xFFFFFFFF - (best & 0xFFFFFFFF)).to(torch.int64)
+    assert torch.equal(idx, torch.argmax(logits.float().cpu(), dim=1))
+    # and equals the fp32 argmax wherever the top-2 margin exceeds the bf16 error
+    top2 = torch.topk(ref, 2, dim=1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 2e-3
+    assert torch.equal(idx[clear], torch.argmax(ref, dim=1)[clear])
+
+
+def test_lm_head_argmax_only_matches_logits_path(device):
+    hidden = (torch.randn(64, 1024) * 0.02).to(torch.bfloat16).to(device)
+    embed = (torch.randn(8192, 1024) * 0.02).to(torch.bfloat16).to(device)
+    logits, p1 = kernels.lm_head(hidden, embed, logits=True, argmax_partials=True)
+    _, p2 = kernels.lm_head(hidden, embed, logits=False, argmax_partials=True)
+    torch.cuda.synchronize()
+    assert torch.equal(p1, p2)

@@ -1,0 +1,184 @@
+"""A1, A9, A10: n-gram drafting and fused acceptance, bit-exact against the oracle.
+
+n-gram: oracle.ngram.propose restates NgramProposer.propose
+(ne/engine/speculative/proposers.py:44-57); drafts and counts must be identical.
+Greedy acceptance: oracle.accept.greedy_accept restates verify_proposal's greedy
+path (ne/engine/speculative/verifier.py:27-60); accepted counts, tokens, history
+append and the rolled-back cached count must be identical.
+Sampled acceptance: the C oracle implements the explicit-uniform contract; results
+must be identical token for token.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as oracle_accept
+from oracle import ngram as oracle_ngram
+from nanoengine_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def run_ngram(device, histories, num_tokens, max_ngram=3, max_drafts=4):
+    cap = max(max(len(h) for h in histories), 1)
+    hist = torch.zeros(len(histories), cap, dtype=torch.int32)
+    for i, h in enumerate(histories):
+        hist[i, : len(h)] = torch.tensor(h, dtype=torch.int32)
+    lens = torch.tensor([len(h) for h in histories], dtype=torch.int32)
+    nt = torch.tensor(num_tokens, dtype=torch.int32)
+    drafts, counts = kernels.ngram_propose(hist.to(device), lens.to(device), nt.to(device), max_ngram,
+                                           max_drafts)
+    torch.cuda.synchronize()
+    counts = counts.cpu().tolist()
+    return [drafts.cpu()[i, : counts[i]].tolist() for i in range(len(histories))]
+
+
+def test_ngram_reference_kats(device):
+    # nt/engine/test_speculative_decoding.py:35-42
+    got = run_ngram(device, [[1, 2, 3, 4, 5, 9, 1, 2], [1, 2, 3, 4]], [3, 3], max_ngram=2, max_drafts=3)
+    assert got == [[3, 4, 5], []]
+
+
+@pytest.mark.parametrize("vocab", [3, 8, 50])
+def test_ngram_random_matches_oracle(device, vocab):
+    rng = np.random.default_rng(vocab)
+    histories = [rng.integers(0, vocab, size=int(n)).tolist() for n in rng.integers(0, 600, size=64)]
+    histories += [[], [7], [7, 7], [1, 2, 1, 2, 1]]
+    num_tokens = rng.integers(0, 5, size=len(histories)).tolist()
+    got = run_ngram(device, histories, num_tokens)
+    want = [oracle_ngram.propose(h, n, 3) if n else [] for h, n in zip(histories, num_tokens)]
+    assert got == want
+
+
+def test_ngram_long_history_k8(device):
+    rng = np.random.default_rng(5)
+    histories = [rng.integers(0, 20, size=17417).tolist() for _ in range(4)]
+    got = run_ngram(device, histories, [8, 8, 3, 0], max_drafts=8)
+    want = [oracle_ngram.propose(h, n, 3) if n else [] for h, n in zip(histories, [8, 8, 3, 0])]
+    assert got == want
+
+
+def bf16_logits(rows, vocab, rng, scale=1.0):
+    return torch.tensor(rng.standard_normal((rows, vocab)) * scale, dtype=torch.float32).to(torch.bfloat16)
+
+
+def make_accept_case(rng, num_seqs, vocab, max_drafts, match_prob=0.7, scale=1.0):
+    num_drafts = rng.integers(0, max_drafts + 1, size=num_seqs)
+    row_start = np.concatenate([[0], np.cumsum(num_drafts + 1)[:-1]]).astype(np.int32)
+    logits = bf16_logits(int((num_drafts + 1).sum()), vocab, rng, scale)
+    targets = torch.argmax(logits.float(), dim=1).numpy()
+    drafts = np.zeros((num_seqs, max_drafts), dtype=np.int32)
+    for b in range(num_seqs):
+        for i in range(num_drafts[b]):
+            t = targets[row_start[b] + i]
+            drafts[b, i] = t if rng.random() < match_prob else rng.integers(0, vocab)
+    return logits, drafts, num_drafts.astype(np.int32), row_start
+
+
+@pytest.mark.parametrize("vocab", [1000, 151936])
+def test_greedy_accept_matches_oracle_and_updates_state(device, vocab):
+    rng = np.random.default_rng(vocab)
+    b, k = 64, 4
+    logits, drafts, nd, rs = make_accept_case(rng, b, vocab, k)
+    cap = 64
+    hist_len = rng.integers(5, 30, size=b).astype(np.int32)
+    history = torch.zeros(b, cap, dtype=torch.int32)
+    d = lambda a: torch.as_tensor(a).to(device)
+    h_dev, hl_dev = history.to(device), d(hist_len)
+    cached = torch.zeros(b, dtype=torch.int32, device=device)
+    out, nout = kernels.accept(d(drafts), d(nd), d(rs), vocab, logits=logits.to(device),
+                               history=h_dev, history_len=hl_dev, num_cached=cached)
+    torch.cuda.synchronize()
+    out, nout = out.cpu(), nout.cpu()
+    lf = logits.float().numpy()
+    for s in range(b):
+        want = oracle_accept.greedy_accept(lf[rs[s] : rs[s] + nd[s] + 1], drafts[s, : nd[s]].tolist())
+        assert out[s, : nout[s]].tolist() == want
+        assert h_dev[s, hist_len[s] : hist_len[s] + len(want)].cpu().tolist() == want
+        assert int(hl_dev[s]) == hist_len[s] + len(want)
+        assert int(cached[s]) == hist_len[s] + len(want) - 1
+
+
+def test_greedy_reference_kat(device):
+    # nt/engine/test_speculative_decoding.py:45-55: rows best = [2, 4, 1, 5]
+    logits = torch.full((8, 6), -10.0)
+    for row, best in enumerate([2, 4, 1, 5, 2, 4, 1, 5]):
+        logits[row, best] = 10.0
+    drafts = torch.tensor([[2, 4, 1], [2, 3, 1]], dtype=torch.int32)
+    out, nout = kernels.accept(drafts.to(device), torch.tensor([3, 3], dtype=torch.int32).to(device),
+                               torch.tensor([0, 4], dtype=torch.int32).to(device), 6,
+                               logits=logits.to(torch.bfloat16).to(device))
+    torch.cuda.synchronize()
+    assert out[0, : nout[0]].tolist() == [2, 4, 1, 5]
+    assert out[1, : nout[1]].tolist() == [2, 4]
+
+
+def test_greedy_ties_take_first_index(device):
+    logits = torch.zeros(2, 300, dtype=torch.bfloat16)
+    logits[0, [7, 9, 200]] = 3.0
+    logits[1, [5, 6]] = 1.0
+    out, nout = kernels.accept(torch.tensor([[7]], dtype=torch.int32).to(device),
+                               torch.tensor([1], dtype=torch.int32).to(device),
+                               torch.tensor([0], dtype=torch.int32).to(device), 300,
+                               logits=logits.to(device))
+    torch.cuda.synchronize()
+    assert out[0, : nout[0]].tolist() == [7, 5]
+
+
+def test_greedy_from_lm_head_partials(device):
+    rng = np.random.default_rng(3)
+    vocab, b = 8192, 16
+    hidden = torch.tensor(rng.standard_normal((b * 5, 1024)) * 0.02, dtype=torch.float32).to(torch.bfloat16)
+    embed = torch.tensor(rng.standard_normal((vocab, 1024)) * 0.02, dtype=torch.float32).to(torch.bfloat16)
+    logits, partials = kernels.lm_head(hidden.to(device), embed.to(device), logits=True, argmax_partials=True)
+    tg = torch.argmax(logits.float(), dim=1).cpu().numpy()
+    drafts = np.stack([tg[5 * s : 5 * s + 4] for s in range(b)]).astype(np.int32)
+    drafts[::3, 2] = (drafts[::3, 2] + 1) % vocab
+    nd = np.full(b, 4, dtype=np.int32)
+    rs = (np.arange(b) * 5).astype(np.int32)
+    d = lambda a: torch.as_tensor(a).to(device)
+    o1, n1 = kernels.accept(d(drafts), d(nd), d(rs), vocab, logits=logits)
+    o2, n2 = kernels.accept(d(drafts), d(nd), d(rs), vocab, argmax_partials=partials)
+    torch.cuda.synchronize()
+    assert torch.equal(n1, n2) and torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("vocab,temperature", [(151936, 0.8), (1000, 1.0), (50, 0.3)])
+def test_sampled_accept_matches_c_oracle(device, vocab, temperature):
+    rng = np.random.default_rng(vocab)
+    b, k = 32, 4
+    logits, drafts, nd, rs = make_accept_case(rng, b, vocab, k, match_prob=0.5, scale=3.0)
+    seeds = rng.integers(0, 2**62, size=b).astype(np.int64)
+    steps = rng.integers(0, 1000, size=b).astype(np.int64)
+    d = lambda a: torch.as_tensor(a).to(device)
+    out, nout = kernels.accept(d(drafts), d(nd), d(rs), vocab, logits=logits.to(device),
+                               temperature=temperature, seeds=d(seeds), steps=d(steps))
+    torch.cuda.synchronize()
+    out, nout = out.cpu(), nout.cpu()
+    bits = logits.view(torch.int16).numpy().view(np.uint16)
+    for s in range(b):
+        want = oracle_accept.sampled_accept(bits[rs[s] : rs[s] + nd[s] + 1], drafts[s, : nd[s]].tolist(),
+                                            temperature, int(seeds[s]), int(steps[s]))
+        assert out[s, : nout[s]].tolist() == want, f"sequence {s}"
+
+
+def test_sampled_golden_fixture(device):
+    from pathlib import Path
+    import json
+
+    path = Path(__file__).parent / "golden" / "sampled_accept.json"
+    case = json.loads(path.read_text())
+    vocab = case["vocab"]
+    bits = np.array(case["logit_bits"], dtype=np.uint16).reshape(-1, vocab)
+    logits = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    d = lambda a: torch.as_tensor(np.asarray(a)).to(device)
+    out, nout = kernels.accept(d(np.array(case["drafts"], dtype=np.int32)), d(np.array(case["num_drafts"], dtype=np.int32)),
+                               d(np.array(case["row_start"], dtype=np.int32)), vocab, logits=logits.to(device),
+                               temperature=case["temperature"], seeds=d(np.array(case["seeds"], dtype=np.int64)),
+                               steps=d(np.array(case["steps"], dtype=np.int64)))
+    torch.cuda.synchronize()
+    got = [out[s, : nout[s]].tolist() for s in range(len(case["expected"]))]
+    assert got == case["expected"]
