@@ -192,10 +192,11 @@ int ne_qk_norm_rope_kv_write(const void* qkv, int32_t rows, int32_t num_q_heads,
  * (p itself if that is empty) and the bonus samples p of the last row, both by
  * inverse CDF with u_draw.  Uniforms u_i, u_draw come from Philox4x32-10 keyed
  * by seeds[b] at counter (steps[b], j/4), word j%4, j = i (guesses) and 63.
- * Outputs: out_tokens[b, 0..num_out[b]-1] (kept guesses + 1 target token);
- * num_out[b] = kept + 1.  When history is given, the kept tokens and the target
+ * Outputs: out_tokens[b, 0..num_out[b]-1] (kept guesses + 1 target token),
+ * the rest of the row [b, 0..max_drafts] set to -1; num_out[b] = kept + 1.  When history is given, the kept tokens and the target
  * token are appended at history[b, history_len[b]..] and history_len[b] and
- * num_cached[b] (set to history_len_before + kept) are updated.
+ * num_cached[b] (set to history_len_before + kept) are updated; a sequence
+ * whose history_len is 0 is inactive (num_out 0, nothing written).
  */
 int ne_accept(int32_t mode, const void* logits, int64_t ld_logits, const uint64_t* argmax_partials,
               int32_t num_tiles, int32_t vocab, const int32_t* drafts, int32_t max_drafts,
@@ -203,6 +204,24 @@ int ne_accept(int32_t mode, const void* logits, int64_t ld_logits, const uint64_
               float temperature, const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens,
               int32_t* num_out, int32_t* history, int64_t history_stride, int32_t* history_len,
               int32_t* num_cached, void* stream);
+
+/*
+ * Device-side packing of a batched verify step (replaces build_step_inputs,
+ * ne/engine/generation/batch_builder.py:22-65, and the slot arithmetic of
+ * ne/engine/memory/paged_allocator.py:69-79 for the verify step).  Sequence b
+ * owns rows b*R .. b*R+R-1, R = max_drafts + 1: row 0 is the last accepted token
+ * history[b, L-1] at position L-1 (L = history_len[b]), row i <= num_drafts[b]
+ * is guess i-1 at position L-1+i; the remaining rows are padding (token 0,
+ * position 0, scratch_slot).  Writes q_start = b*R, q_len = num_drafts+1 and
+ * ctx_len = L + num_drafts; history_len 0 marks an inactive slot (q_len 0).
+ */
+int ne_prepare_verify_step(const int32_t* history, int64_t history_stride,
+                           const int32_t* history_len, const int32_t* drafts, int32_t max_drafts,
+                           const int32_t* num_drafts, const int32_t* block_tables,
+                           int32_t block_table_stride, int32_t block_size, int32_t scratch_slot,
+                           int32_t num_seqs, int32_t* tokens, int32_t* positions,
+                           int32_t* slot_mapping, int32_t* q_start, int32_t* q_len,
+                           int32_t* ctx_len, void* stream);
 
 /* Plain device copy of `bytes` bytes (16-byte aligned); used to calibrate the
  * hardware byte counters against a kernel of known traffic. */

@@ -86,6 +86,7 @@ __device__ float philox_uniform(uint64_t seed, uint64_t step, int j) {
 }
 
 __device__ __forceinline__ uint64_t key_of(float v, uint32_t idx) {
+  v = v + 0.0f;  // -0 compares equal to +0 (torch.argmax): give both one key
   uint32_t b = __builtin_bit_cast(uint32_t, v);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - idx);
@@ -233,6 +234,12 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  if (p.history != nullptr && p.history_len[b] == 0) {  // inactive sequence slot
+    for (int i = tid; i <= p.max_drafts; i += kThreads)
+      p.out_tokens[(int64_t)b * (p.max_drafts + 1) + i] = -1;
+    if (tid == 0) p.num_out[b] = 0;
+    return;
+  }
   const int g = p.num_drafts[b];
   const int rs0 = p.row_start[b];
   const int32_t* dr = p.drafts + (int64_t)b * p.max_drafts;
@@ -278,8 +285,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
 
   const int kept = s_kept;
   const int fin = s_final;
-  for (int i = tid; i <= kept; i += kThreads)
-    p.out_tokens[(int64_t)b * (p.max_drafts + 1) + i] = (i < kept) ? dr[i] : fin;
+  for (int i = tid; i <= p.max_drafts; i += kThreads)
+    p.out_tokens[(int64_t)b * (p.max_drafts + 1) + i] = (i < kept) ? dr[i] : (i == kept ? fin : -1);
   if (tid == 0) p.num_out[b] = kept + 1;
   if (p.history != nullptr) {
     const int len = p.history_len[b];

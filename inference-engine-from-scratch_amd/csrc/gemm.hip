@@ -47,6 +47,7 @@ __device__ __forceinline__ bf16x8 int8x8_to_bf16x8(uint32_t a, uint32_t b) {
 
 // order-preserving key: larger value wins, then smaller index wins
 __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  v = v + 0.0f;  // -0 compares equal to +0 (torch.argmax): give both one key
   uint32_t b = __builtin_bit_cast(uint32_t, v);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - idx);

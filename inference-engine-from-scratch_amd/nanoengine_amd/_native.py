@@ -92,6 +92,10 @@ SIGNATURES: dict[str, tuple] = {
             _vp,  # stream
         ],
     ),
+    "ne_prepare_verify_step": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
     "ne_copy_bytes": (ctypes.c_int, [_vp, _vp, _sz, _vp]),
 }
 

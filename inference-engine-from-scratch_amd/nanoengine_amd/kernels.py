@@ -424,6 +424,40 @@ def accept(
     return out_tokens, num_out
 
 
+def prepare_verify_step(
+    history: torch.Tensor,
+    history_len: torch.Tensor,
+    drafts: torch.Tensor,
+    num_drafts: torch.Tensor,
+    block_tables: torch.Tensor,
+    block_size: int,
+    scratch_slot: int,
+    tokens: torch.Tensor,
+    positions: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    q_start: torch.Tensor,
+    q_len: torch.Tensor,
+    ctx_len: torch.Tensor,
+) -> None:
+    """Pack a batched verify step on the device: rows, positions, slots, attention metadata."""
+    device = _require_gpu(history, history_len, drafts, num_drafts, block_tables, tokens, positions,
+                          slot_mapping, q_start, q_len, ctx_len)
+    for name, t in (("history", history), ("history_len", history_len), ("drafts", drafts),
+                    ("num_drafts", num_drafts), ("block_tables", block_tables), ("tokens", tokens),
+                    ("positions", positions), ("slot_mapping", slot_mapping), ("q_start", q_start),
+                    ("q_len", q_len), ("ctx_len", ctx_len)):
+        _int32(t, name)
+    num_seqs, max_drafts = drafts.shape
+    _check(tokens.numel() >= num_seqs * (max_drafts + 1), "tokens too small for the padded rows")
+    _native.call(
+        "ne_prepare_verify_step",
+        _ptr(history), history.stride(0), _ptr(history_len), _ptr(drafts), max_drafts, _ptr(num_drafts),
+        _ptr(block_tables), block_tables.stride(0), block_size, scratch_slot, num_seqs,
+        _ptr(tokens), _ptr(positions), _ptr(slot_mapping), _ptr(q_start), _ptr(q_len), _ptr(ctx_len),
+        _stream(device),
+    )
+
+
 def copy_bytes(src: torch.Tensor, dst: torch.Tensor) -> None:
     device = _require_gpu(src, dst)
     nbytes = src.numel() * src.element_size()

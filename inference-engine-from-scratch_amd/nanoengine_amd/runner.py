@@ -1,0 +1,341 @@
+"""Batched speculative verify on the HIP kernels.
+
+The reference verifies one sequence per call (ModelRunner.score_tokens,
+ne/engine/generation/model_runner.py:52-62, driven by
+SpeculativeGenerator._run_speculative_step, ne/engine/speculative/
+speculative_generator.py:70-85).  ``VerifyRunner`` applies the same per-sequence
+semantics to up to ``max_seqs`` sequences at once, with the token histories,
+lengths, block tables and cached counts resident on the device:
+
+  1. n-gram drafting on the device histories (ne_ngram_propose)
+  2. read back the draft counts; reserve KV blocks on the host allocator for
+     L + g tokens per sequence (paged_allocator.py:50-55) and upload new table rows
+  3. pack rows on the device (ne_prepare_verify_step), run the Qwen3 forward,
+     the LM head (argmax partials only when greedy) and the fused acceptance,
+     which appends kept tokens + 1 to the device history and rolls
+     ``num_cached`` back to L + kept
+  4. read back accepted tokens and update the host ``Sequence`` objects
+
+Step 3 has fixed shapes (every slot owns k+1 padded rows), so it can be
+captured once into a HIP graph and replayed.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from nanoengine_amd import kernels
+from nanoengine_amd.interface import (
+    GREEDY_TEMPERATURE,
+    find_finish_reason,
+    num_guesses,
+)
+from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
+from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
+from nanoengine_amd.sequence_state import Sequence
+
+
+@dataclass
+class StepResult:
+    """Tokens emitted for one sequence by one step, with its finish reason if it ended."""
+
+    tokens: list[int]
+    finish_reason: str | None
+    num_guesses: int
+    num_kept: int
+
+
+class VerifyRunner:
+    def __init__(
+        self,
+        model: Qwen3VerifyModel,
+        pool: KVCachePool,
+        allocator: PagedSlotAllocator,
+        max_seqs: int,
+        num_speculative_tokens: int,
+        max_ngram: int,
+        max_model_len: int,
+        stop_token_ids: frozenset[int] = frozenset(),
+        use_graph: bool = False,
+    ) -> None:
+        self.model = model
+        self.pool = pool
+        self.allocator = allocator
+        self.device = model.device
+        self.k = num_speculative_tokens
+        self.R = self.k + 1
+        self.max_seqs = max_seqs
+        self.max_ngram = max_ngram
+        self.stop_token_ids = stop_token_ids
+        self.block_size = allocator.block_size
+        self.capacity = max_model_len + self.R
+        self.max_blocks = math.ceil(self.capacity / self.block_size)
+        self.use_graph = use_graph
+        if self.max_seqs * self.R > model.max_rows:
+            raise ValueError("model activation buffers are smaller than max_seqs * (k + 1) rows")
+        dev = self.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.history = torch.zeros(max_seqs, self.capacity, **i32)
+        self.history_len = torch.zeros(max_seqs, **i32)
+        self.num_cached = torch.zeros(max_seqs, **i32)
+        self.block_tables = torch.zeros(max_seqs, self.max_blocks, **i32)
+        self.num_tokens = torch.zeros(max_seqs, **i32)
+        self.drafts = torch.zeros(max_seqs, self.k, **i32)
+        self.num_drafts = torch.zeros(max_seqs, **i32)
+        self.seeds = torch.zeros(max_seqs, dtype=torch.int64, device=dev)
+        self.steps = torch.zeros(max_seqs, dtype=torch.int64, device=dev)
+        rows = max_seqs * self.R
+        self.tokens = torch.zeros(rows, **i32)
+        self.positions = torch.zeros(rows, **i32)
+        self.slot_mapping = torch.zeros(rows, **i32)
+        self.q_start = torch.zeros(max_seqs, **i32)
+        self.q_len = torch.zeros(max_seqs, **i32)
+        self.ctx_len = torch.zeros(max_seqs, **i32)
+        self.row_start = torch.arange(max_seqs, **i32) * self.R
+        self.out_tokens = torch.zeros(max_seqs, self.R, **i32)
+        self.num_out = torch.zeros(max_seqs, **i32)
+        vocab = model.config.vocab_size
+        self.argmax_partials = torch.zeros(rows, kernels.lm_head_num_tiles(vocab), dtype=torch.int64,
+                                           device=dev)
+        self.logits: torch.Tensor | None = None  # allocated for sampled batches only
+        pin = dict(pin_memory=True)
+        self.h_tables = torch.zeros(max_seqs, self.max_blocks, dtype=torch.int32, **pin)
+        self.h_num_tokens = torch.zeros(max_seqs, dtype=torch.int32, **pin)
+        self.h_steps = torch.zeros(max_seqs, dtype=torch.int64, **pin)
+        self.h_num_drafts = torch.zeros(max_seqs, dtype=torch.int32, **pin)
+        self.h_out = torch.zeros(max_seqs, self.R, dtype=torch.int32, **pin)
+        self.h_num_out = torch.zeros(max_seqs, dtype=torch.int32, **pin)
+        self.slots: list[Sequence | None] = [None] * max_seqs
+        self.temperature: float | None = None
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.graph_temperature: float | None = None
+        self.batch = AttentionBatch(self.positions, self.slot_mapping, self.q_start, self.q_len,
+                                    self.ctx_len, self.block_tables, self.R, self.capacity)
+        # set to a list to record, per verify step, each slot's history, drafts,
+        # emitted tokens and block table (used by the parity tests)
+        self.trace: list | None = None
+
+    # ------------------------------------------------------------------ slots
+    @property
+    def active_slots(self) -> list[int]:
+        return [i for i, s in enumerate(self.slots) if s is not None]
+
+    def free_slots(self) -> list[int]:
+        return [i for i, s in enumerate(self.slots) if s is None]
+
+    def _check_sampling(self, sequence: Sequence) -> None:
+        params = sequence.sampling_params
+        if params.temperature != GREEDY_TEMPERATURE and params.top_p < 1.0:
+            raise NotImplementedError("top_p < 1 is not implemented on the HIP acceptance path")
+        temp = float(params.temperature)
+        if self.temperature is not None and self.active_slots and temp != self.temperature:
+            raise NotImplementedError("one batch verifies with a single temperature")
+        self.temperature = temp
+
+    def add(self, sequences: list[Sequence]) -> list[int]:
+        """Place sequences in free slots, reserve their prompts, prefill them and emit
+        the first token of each (model_runner.py:33-50 + speculative_generator.py:50-53)."""
+        free = self.free_slots()
+        if len(sequences) > len(free):
+            raise ValueError(f"only {len(free)} free sequence slots")
+        for seq in sequences:
+            self._check_sampling(seq)
+            if seq.num_tokens + self.R > self.capacity:
+                raise ValueError(f"prompt of {seq.request_id} exceeds max_model_len")
+        slots = free[: len(sequences)]
+        results = {}
+        # prefill contiguous runs of slots together
+        run: list[tuple[int, Sequence]] = []
+        for slot, seq in zip(slots, sequences, strict=True):
+            if run and slot != run[-1][0] + 1:
+                results.update(self._prefill(run))
+                run = []
+            run.append((slot, seq))
+        if run:
+            results.update(self._prefill(run))
+        return results
+
+    def _prefill(self, run: list[tuple[int, Sequence]]) -> dict[int, StepResult]:
+        dev = self.device
+        s0 = run[0][0]
+        n = len(run)
+        tokens, positions, slots, q_start, q_len = [], [], [], [], []
+        row = 0
+        for slot, seq in run:
+            self.slots[slot] = seq
+            p = seq.num_tokens
+            added = self.allocator.reserve(seq.request_id, p)
+            table = self.allocator.block_table(seq.request_id)
+            self.h_tables[slot].zero_()
+            self.h_tables[slot, : len(table)] = torch.tensor(table, dtype=torch.int32)
+            del added
+            pos = np.arange(p)
+            tokens.append(np.asarray(seq.token_ids, dtype=np.int32))
+            positions.append(pos.astype(np.int32))
+            slots.append(self.allocator.slots_for(seq.request_id, pos).astype(np.int32))
+            q_start.append(row)
+            q_len.append(p)
+            row += p
+            self.history[slot, :p] = torch.tensor(seq.token_ids, dtype=torch.int32)
+            self.history_len[slot] = p
+            self.seeds[slot] = seq.sampling_generator.seed
+            self.steps[slot] = seq.sampling_generator.step
+        if row > self.model.max_rows:
+            raise ValueError(f"prefill of {row} rows exceeds the model's {self.model.max_rows} rows")
+        self.block_tables.copy_(self.h_tables, non_blocking=True)
+        t = lambda a: torch.from_numpy(np.concatenate(a)).to(dev)
+        tok, posn, slot_map = t(tokens), t(positions), t(slots)
+        qs = torch.tensor(q_start, dtype=torch.int32, device=dev)
+        ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+        batch = AttentionBatch(posn, slot_map, qs, ql, ql, self.block_tables[s0 : s0 + n], max(q_len),
+                               max(q_len))
+        hidden = self.model.forward(row, tok, batch, self.pool)
+        last = hidden.index_select(0, (qs + ql - 1).long())
+        greedy = self.temperature == GREEDY_TEMPERATURE
+        logits, partials = self.model.compute_logits(last, logits=not greedy, argmax=greedy)
+        zeros = torch.zeros(n, dtype=torch.int32, device=dev)
+        kernels.accept(
+            self.drafts[s0 : s0 + n], zeros, torch.arange(n, dtype=torch.int32, device=dev),
+            self.model.config.vocab_size, logits=logits, argmax_partials=partials,
+            temperature=self.temperature, seeds=self.seeds[s0 : s0 + n], steps=self.steps[s0 : s0 + n],
+            out_tokens=self.out_tokens[s0 : s0 + n], num_out=self.num_out[s0 : s0 + n],
+            history=self.history[s0 : s0 + n], history_len=self.history_len[s0 : s0 + n],
+            num_cached=self.num_cached[s0 : s0 + n],
+        )
+        self.h_out[s0 : s0 + n].copy_(self.out_tokens[s0 : s0 + n], non_blocking=True)
+        torch.cuda.current_stream(dev).synchronize()
+        results = {}
+        for i, (slot, seq) in enumerate(run):
+            seq.num_cached_tokens = seq.num_tokens
+            seq.sampling_generator.step += 1
+            results[slot] = self._emit(slot, seq, [int(self.h_out[s0 + i, 0])], 0, 0)
+        return results
+
+    # ------------------------------------------------------------- verify step
+    def _device_step(self) -> None:
+        """Fixed-shape part of the verify step: pack, forward, LM head, accept."""
+        kernels.prepare_verify_step(
+            self.history, self.history_len, self.drafts, self.num_drafts, self.block_tables,
+            self.block_size, self.pool.scratch_slot, self.tokens, self.positions, self.slot_mapping,
+            self.q_start, self.q_len, self.ctx_len,
+        )
+        rows = self.max_seqs * self.R
+        hidden = self.model.forward(rows, self.tokens, self.batch, self.pool)
+        greedy = self.temperature == GREEDY_TEMPERATURE
+        if greedy:
+            self.model.compute_logits(hidden, logits=False, argmax=self.argmax_partials)
+            logits = None
+        else:
+            if self.logits is None:
+                self.logits = torch.empty(rows, self.model.config.vocab_size, dtype=torch.bfloat16,
+                                          device=self.device)
+            self.model.compute_logits(hidden, logits=self.logits, argmax=False)
+            logits = self.logits
+        kernels.accept(
+            self.drafts, self.num_drafts, self.row_start, self.model.config.vocab_size, logits=logits,
+            argmax_partials=self.argmax_partials if greedy else None,
+            temperature=self.temperature or 0.0, seeds=self.seeds, steps=self.steps,
+            out_tokens=self.out_tokens, num_out=self.num_out, history=self.history,
+            history_len=self.history_len, num_cached=self.num_cached,
+        )
+
+    def _run_device_step(self) -> None:
+        if not self.use_graph:
+            self._device_step()
+            return
+        if self.graph is None or self.graph_temperature != self.temperature:
+            # this step runs eagerly (which also allocates lazily created buffers and
+            # workspaces); the capture below only records, so nothing runs twice
+            self._device_step()
+            torch.cuda.current_stream(self.device).synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self._device_step()
+            self.graph_temperature = self.temperature
+            return
+        self.graph.replay()
+
+    def step(self) -> dict[int, StepResult]:
+        """One verify step over every active slot; returns what each slot emitted."""
+        active = self.active_slots
+        if not active:
+            return {}
+        for s in range(self.max_seqs):
+            seq = self.slots[s]
+            if seq is None:
+                self.h_num_tokens[s] = 0
+                continue
+            self.h_num_tokens[s] = num_guesses(seq.sampling_params, seq.num_generated_tokens, self.k)
+            self.h_steps[s] = seq.sampling_generator.step
+        self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
+        self.steps.copy_(self.h_steps, non_blocking=True)
+        kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
+                              drafts=self.drafts, num_drafts=self.num_drafts)
+        self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        tables_changed = False
+        for s in active:
+            seq = self.slots[s]
+            g = int(self.h_num_drafts[s])
+            owned = len(self.allocator.block_table(seq.request_id))
+            added = self.allocator.reserve(seq.request_id, seq.num_tokens + g)
+            if added:
+                self.h_tables[s, owned : owned + len(added)] = torch.tensor(added, dtype=torch.int32)
+                tables_changed = True
+        if tables_changed:
+            self.block_tables.copy_(self.h_tables, non_blocking=True)
+        self._run_device_step()
+        self.h_out.copy_(self.out_tokens, non_blocking=True)
+        self.h_num_out.copy_(self.num_out, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        if self.trace is not None:
+            self.trace.append({
+                s: {
+                    "history": list(self.slots[s].token_ids),
+                    "requested": int(self.h_num_tokens[s]),
+                    "drafts": self.drafts[s, : int(self.h_num_drafts[s])].tolist(),
+                    "out": self.h_out[s, : int(self.h_num_out[s])].tolist(),
+                    "table": self.allocator.block_table(self.slots[s].request_id),
+                }
+                for s in active
+            })
+        results = {}
+        for s in active:
+            seq = self.slots[s]
+            n = int(self.h_num_out[s])
+            g = int(self.h_num_drafts[s])
+            kept = n - 1
+            seq.num_cached_tokens = seq.num_tokens + kept
+            seq.sampling_generator.step += 1
+            results[s] = self._emit(s, seq, self.h_out[s, :n].tolist(), g, kept)
+        return results
+
+    def _emit(self, slot: int, seq: Sequence, tokens: list[int], g: int, kept: int) -> StepResult:
+        """Append tokens one by one with the finish checks of speculative_generator.py:54-67."""
+        emitted = []
+        reason = None
+        for token in tokens:
+            seq.token_ids.append(token)
+            emitted.append(token)
+            reason = find_finish_reason(token, seq.num_generated_tokens, seq.sampling_params,
+                                        self.stop_token_ids)
+            if reason is not None:
+                break
+        if reason is not None:
+            self.release(slot)
+        return StepResult(emitted, reason, g, kept)
+
+    def release(self, slot: int) -> None:
+        seq = self.slots[slot]
+        if seq is None:
+            return
+        self.allocator.free(seq.request_id)
+        self.slots[slot] = None
+        self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
+        self.h_tables[slot].zero_()
+        if not self.active_slots:
+            self.temperature = None
