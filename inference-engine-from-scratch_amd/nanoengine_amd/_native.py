@@ -142,10 +142,43 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+class LaunchTimer:
+    """HIP events recorded on the launching stream around every call of one entry point."""
+
+    def __init__(self) -> None:
+        self.pairs: list = []
+
+    def durations_ms(self) -> list[float]:
+        return [start.elapsed_time(stop) for start, stop in self.pairs]
+
+
+_timers: dict[str, LaunchTimer] = {}
+
+
+def set_launch_timer(name: str, timer: LaunchTimer | None) -> None:
+    """Time every launch of ``name`` (events on torch's current stream, which is the
+    stream the wrappers launch on); ``None`` stops timing."""
+    if timer is None:
+        _timers.pop(name, None)
+    else:
+        _timers[name] = timer
+
+
 def call(name: str, *args) -> None:
     """Call an entry point and raise NativeError on a non-zero status."""
     lib = load()
-    status = getattr(lib, name)(*args)
+    timer = _timers.get(name)
+    if timer is not None:
+        import torch
+
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        status = getattr(lib, name)(*args)
+        stop.record()
+        timer.pairs.append((start, stop))
+    else:
+        status = getattr(lib, name)(*args)
     if status != NE_OK:
         message = lib.ne_last_error().decode("utf-8", "replace")
         raise NativeError(name, status, message)

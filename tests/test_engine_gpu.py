@@ -98,8 +98,9 @@ def test_verify_step_logits_match_oracle(norm_ones):
         ref = runner.score_tokens(seq, 1 + len(rec["drafts"])).float()
         got = ours[slot * 5 : slot * 5 + 1 + len(rec["drafts"])]
         # 1e-2 max-abs at the configured N(0, 0.02) scale; with unit norm weights the
-        # logits reach ~4, where one bf16 ulp is 0.03, so the bar scales with them
-        bar = 1e-2 * (float(ref.abs().max()) if norm_ones else 1.0)
+        # logits reach ~3-4, where one bf16 ulp is 0.016-0.03 and both sides round,
+        # so there the bar is 2e-2 of the logit scale
+        bar = 2e-2 * float(ref.abs().max()) if norm_ones else 1e-2
         assert float((got - ref).abs().max()) <= bar
         rel = float((got - ref).norm() / ref.norm())
         assert rel <= 2e-2, f"slot {slot}: relative error {rel:.3e}"
