@@ -130,11 +130,24 @@ int ne_paged_verify_attention(const void* q, int64_t q_token_stride, int64_t q_h
  *   y [m, n_out] bf16 (row stride ldy); n_out = n, or n/2 for NE_EPILOGUE_SWIGLU
  *   where weight rows come in groups of 32 (16 gate rows then 16 up rows) and
  *   y[:, 16*i + j] = bf16(silu(gate) * up) for the pair in group i, row j.
- * Requires k % 64 == 0.
+ * Requires k % 128 == 0 and n % 64 == 0.
  */
 int ne_w8a16_gemm(const void* x, int64_t ldx, const int8_t* w, const void* scale,
                   int32_t scale_dtype, int32_t m, int32_t n, int32_t k, void* y, int64_t ldy,
                   int32_t epilogue, void* stream);
+
+/*
+ * A8 (split over K) - the same product as ne_w8a16_gemm's store epilogue, with K
+ * cut into `splits` equal parts computed by separate work-groups:
+ * partials[s, m, n] = scale[n] * sum_{k in part s} x[m, k] w[n, k], fp32,
+ * contiguous [splits, m, n].  For the short, narrow o_proj / down_proj shapes
+ * (N = hidden), which alone give too few output tiles to fill the GPU;
+ * ne_splitk_add_rmsnorm consumes the partials.  Requires k % (128 * splits) == 0,
+ * n % 64 == 0, 1 <= splits <= 64.
+ */
+int ne_w8a16_gemm_splitk(const void* x, int64_t ldx, const int8_t* w, const void* scale,
+                         int32_t scale_dtype, int32_t m, int32_t n, int32_t k, int32_t splits,
+                         float* partials, void* stream);
 
 /*
  * A8b - bf16 GEMM for the tied LM head: logits[m, n] = bf16(sum_k x[m,k] w[n,k])
@@ -159,6 +172,13 @@ int ne_rmsnorm(const void* x, const void* weight, void* out, int32_t rows, int32
                float eps, void* stream);
 int ne_add_rmsnorm(void* residual, const void* delta, const void* weight, void* out, int32_t rows,
                    int32_t hidden, float eps, void* stream);
+/* ne_add_rmsnorm with delta = bf16(sum_s partials[s, row, :]) taken from the fp32
+ * output of ne_w8a16_gemm_splitk ([splits, rows, hidden], 16-byte aligned); the
+ * projection output is rounded to bf16 before the residual add, as in the
+ * reference's bf16 o_proj / down_proj followed by the residual add
+ * (ne/models/qwen3.py:145-149). */
+int ne_splitk_add_rmsnorm(void* residual, const float* partials, int32_t splits, const void* weight,
+                          void* out, int32_t rows, int32_t hidden, float eps, void* stream);
 int ne_embed_rmsnorm(const int32_t* tokens, const void* embed, const void* weight, void* residual,
                      void* out, int32_t rows, int32_t hidden, float eps, void* stream);
 

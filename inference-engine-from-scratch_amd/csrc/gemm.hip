@@ -4,18 +4,20 @@
 // materialises bf16(int8 * scale) for the whole weight before F.linear, and the
 // tied-embedding LM head (ne/models/qwen3.py:197-203).
 //
-// Each 16x16 MFMA tile computes D = W . X^T (weight rows x token rows) with
-// v_mfma_f32_16x16x32_bf16, so a lane ends up holding four consecutive output
-// columns of one token row (8-byte stores) and the weight operand can be loaded
-// straight from global memory into registers:
-//   lane l, weight subtile: weight row l % 16, k = (l/16)*BK/4 .. +BK/4
-//   lane l, token subtile : token row  l % 16, same k range (read from LDS)
-// int8 weights become bf16 in registers (one SDWA convert per byte; exact) and
-// the per-output-row scale is applied to the fp32 accumulator.  The token tile
-// X[BM x BK] is staged through LDS (double buffered) and shared by the 4 waves
-// of a work-group; wave w owns NW weight subtiles (16 rows each) and all BM
-// token rows.  Work-group ids are mapped so that the M blocks of one weight
-// tile run on the same XCD (shared L2).
+// Shapes here are short and wide: M = query rows of a verify step (64 x 5 =
+// 320), N up to 6144 (151936 for the LM head), K 1024..3072.  A work-group owns
+// a 64 x BN output tile.  K advances in stages of 128: each stage's X and W tiles
+// are copied global -> LDS by the work-group's own DMA loads
+// (global_load_lds_dwordx4, no registers involved) into a ring of S stages, so
+// S - 1 stages are in flight while the MFMAs consume the current one.  The 4
+// waves sit 2 x 2 over the tile and read their MFMA fragments from LDS.
+//
+// Each 16x16 MFMA (v_mfma_f32_16x16x32_bf16) computes D = W . X^T (weight rows x
+// token rows), so a lane ends up holding four consecutive output columns of one
+// token row (8-byte stores).  int8 weights become bf16 in registers after the LDS
+// read (one SDWA convert per byte, exact); the per-row scale is applied to the
+// fp32 sum.  Work-group ids are mapped so that the M blocks of one weight tile run
+// on the same XCD and share its L2.
 #include "ne_common.hpp"
 
 namespace ne {
@@ -24,6 +26,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kGemmWaves = 4;
+constexpr int kBK = 64;  // K slice per ring entry
 
 struct GemmParams {
   const uint16_t* x;
@@ -61,42 +64,6 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// per-lane weight registers for one BK slice of one 16-row subtile
-template <int BK, bool WINT8>
-struct WRegs {
-  static constexpr int kBytes = WINT8 ? BK / 4 : BK / 2;  // 16/8 B int8, 32/16 B bf16
-  static constexpr int kVec = (kBytes + 15) / 16;
-  u32x4 v[kVec];
-};
-
-template <int BK, bool WINT8>
-__device__ __forceinline__ void load_w(const GemmParams& p, int row, int k0, int lane,
-                                       WRegs<BK, WINT8>& R) {
-  const int kk = k0 + (lane >> 4) * (BK / 4);
-  if constexpr (WINT8) {
-    const int8_t* src = (const int8_t*)p.w + (int64_t)row * p.k + kk;
-    if constexpr (BK == 64) {
-      R.v[0] = *(const u32x4*)src;
-    } else {
-      const u32x2 t = *(const u32x2*)src;
-      R.v[0] = u32x4{t[0], t[1], 0, 0};
-    }
-  } else {
-    const u32x4* src = (const u32x4*)((const uint16_t*)p.w + (int64_t)row * p.k + kk);
-#pragma unroll
-    for (int i = 0; i < WRegs<BK, WINT8>::kVec; ++i) R.v[i] = src[i];
-  }
-}
-
-template <int BK, bool WINT8>
-__device__ __forceinline__ bf16x8 w_operand(const WRegs<BK, WINT8>& R, int s) {
-  if constexpr (WINT8) {
-    return int8x8_to_bf16x8(R.v[0][2 * s], R.v[0][2 * s + 1]);
-  } else {
-    return __builtin_bit_cast(bf16x8, R.v[s]);
-  }
-}
-
 template <int SDT>
 __device__ __forceinline__ float scale_at(const void* s, int64_t i) {
   if constexpr (SDT < 0) {
@@ -106,17 +73,135 @@ __device__ __forceinline__ float scale_at(const void* s, int64_t i) {
   }
 }
 
-// EPI: 0 store, 1 swiglu, 2 lm head (optional store + argmax partials)
-template <int MW, int NW, int BK, bool WINT8, int SDT, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
-  constexpr int BM = MW * 16;
-  constexpr int BN = kGemmWaves * NW * 16;
-  constexpr int KS = BK / 32;        // MFMA k-steps per BK slice
-  constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row (bank spread)
-  constexpr int XV = BM * BK / 8;     // 16-byte vectors per X tile
-  constexpr int XV_PER_T = (XV + kThreads - 1) / kThreads;
-  __shared__ __attribute__((aligned(16))) uint16_t s_x[2][BM * LDS_STRIDE];
-  __shared__ uint64_t s_best[kGemmWaves][BM];
+// ---- staged tiles -------------------------------------------------------------
+// A stage holds X[64 rows][BK] bf16 and W[BN rows][BK] (int8 or bf16) in LDS, filled
+// by global_load_lds_dwordx4: every wave-instruction copies 1 KiB of whole 128-byte
+// lines (4 X rows x 256 B, or 8 int8 W rows x 128 B / 4 bf16 W rows x 256 B), the
+// access shape the vector L1 serves at full rate.  Each lane picks its source so
+// that LDS row `row` holds 16-byte chunk c at position c ^ (row % CPR) (CPR = chunks
+// per row), which makes the MFMA fragment reads below bank-conflict free.
+constexpr int kBM = 64;
+constexpr int kArgmaxCols = 64;  // columns per LM-head argmax partial (one wave's share)
+constexpr int kStageK = 128;  // k per stage
+
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+                                   0, 0);
+}
+
+// s_waitcnt vmcnt(n) leaving lgkmcnt/expcnt unconstrained (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BN, bool WINT8>
+struct StageLayout {
+  static constexpr int kXBytes = kBM * kStageK * 2;                     // 16 KiB
+  static constexpr int kWRowBytes = kStageK * (WINT8 ? 1 : 2);          // 128 or 256
+  static constexpr int kWBytes = BN * kWRowBytes;
+  static constexpr int kBytes = kXBytes + kWBytes;
+  static constexpr int kXInstr = kXBytes / 1024 / kGemmWaves;           // per wave
+  static constexpr int kWInstr = kWBytes / 1024 / kGemmWaves;
+  static constexpr int kLoads = kXInstr + kWInstr;                      // per wave per stage
+};
+
+template <int BN, bool WINT8>
+__device__ __forceinline__ void issue_stage(const GemmParams& p, char* stage, int m0, int n0, int k0,
+                                            int wave, int lane) {
+  using L = StageLayout<BN, WINT8>;
+  // X: instruction j of this wave copies rows (wave*kXInstr + j)*4 .. +4, 16 chunks each
+#pragma unroll
+  for (int j = 0; j < L::kXInstr; ++j) {
+    const int blk = wave * L::kXInstr + j;
+    const int row = blk * 4 + (lane >> 4);
+    const int chunk = (lane & 15) ^ (row & 15);
+    const int grow = min(m0 + row, p.m - 1);  // rows past m re-read the last row; never stored
+    lds_dma16(p.x + (int64_t)grow * p.ldx + k0 + chunk * 8, stage + blk * 1024);
+  }
+  char* wst = stage + L::kXBytes;
+#pragma unroll
+  for (int j = 0; j < L::kWInstr; ++j) {
+    const int blk = wave * L::kWInstr + j;
+    if constexpr (WINT8) {  // 8 rows x 8 chunks
+      const int row = blk * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ (row & 7);
+      lds_dma16((const int8_t*)p.w + (int64_t)(n0 + row) * p.k + k0 + chunk * 16, wst + blk * 1024);
+    } else {  // 4 rows x 16 chunks
+      const int row = blk * 4 + (lane >> 4);
+      const int chunk = (lane & 15) ^ (row & 15);
+      lds_dma16((const uint16_t*)p.w + (int64_t)(n0 + row) * p.k + k0 + chunk * 8,
+                wst + blk * 1024);
+    }
+  }
+}
+
+// MFMA k mapping inside a stage: k-step s = 2q + h (q < 2, h < 2); lane group g = l / 16
+// holds logical k = 64 q + 16 g + 8 h + e, e < 8.  For X that is 16-byte chunk 8q + 2g + h
+// of its 256-byte row; for int8 W, bytes 64q + 16g .. +16 cover both h at once.
+template <int BN, bool WINT8, int MS, int NS>
+__device__ __forceinline__ void mma_stage(const char* stage, int wm, int wn, int lane,
+                                          floatx4 (&acc)[MS][NS]) {
+  using L = StageLayout<BN, WINT8>;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const char* xst = stage;
+  const char* wst = stage + L::kXBytes;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    u32x4 wf[NS][2];  // [n subtile][h]
+#pragma unroll
+    for (int ni = 0; ni < NS; ++ni) {
+      const int row = wn * NS * 16 + ni * 16 + r;
+      if constexpr (WINT8) {
+        const int chunk = (4 * q + g) ^ (row & 7);
+        const u32x4 v = *(const u32x4*)(wst + row * L::kWRowBytes + chunk * 16);
+        wf[ni][0] = u32x4{v[0], v[1], 0, 0};
+        wf[ni][1] = u32x4{v[2], v[3], 0, 0};
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int chunk = (8 * q + 2 * g + h) ^ (row & 15);
+          wf[ni][h] = *(const u32x4*)(wst + row * L::kWRowBytes + chunk * 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 a[NS];
+#pragma unroll
+      for (int ni = 0; ni < NS; ++ni) {
+        if constexpr (WINT8) {
+          a[ni] = int8x8_to_bf16x8(wf[ni][h][0], wf[ni][h][1]);
+        } else {
+          a[ni] = __builtin_bit_cast(bf16x8, wf[ni][h]);
+        }
+      }
+#pragma unroll
+      for (int mi = 0; mi < MS; ++mi) {
+        const int row = wm * MS * 16 + mi * 16 + r;
+        const int chunk = (8 * q + 2 * g + h) ^ (row & 15);
+        const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(xst + row * 256 + chunk * 16));
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ni], b, acc[mi][ni], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// EPI: 0 store bf16(acc * scale), 1 swiglu, 2 lm head (optional logits + argmax partials),
+// 3 fp32 partial sums of split `blockIdx` over k (scaled), for a consumer to add.
+// Waves form 2 x 2 over the 64 x BN tile: wave (wm, wn) owns rows 32 wm .. +32 and weight
+// rows BN/2 wn .. +BN/2.  S = LDS stages in flight.
+template <int BN, int S, bool WINT8, int SDT, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p, int k_per_split,
+                                                        float* partial) {
+  using L = StageLayout<BN, WINT8>;
+  constexpr int MS = 2;            // m subtiles per wave
+  constexpr int NS = BN / 32;      // n subtiles per wave
+  extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
@@ -124,143 +209,96 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int tm = jj % p.tiles_m;
   const int tn = (jj / p.tiles_m) * kNumXcd + xcd;
   if (tn >= p.tiles_n) return;
-  const int m0 = tm * BM;
+  const int split = blockIdx.y;
+  const int m0 = tm * kBM;
   const int n0 = tn * BN;
+  const int kbase = split * k_per_split;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  const int wrow0 = n0 + wave * NW * 16;  // first weight row of this wave
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
 
-  floatx4 acc[MW][NW];
+  floatx4 acc[MS][NS];
 #pragma unroll
-  for (int mi = 0; mi < MW; ++mi)
+  for (int mi = 0; mi < MS; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < NW; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int ni = 0; ni < NS; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto load_x = [&](int k0, u32x4(&xr)[XV_PER_T]) {
+  const int kt_n = k_per_split / kStageK;
 #pragma unroll
-    for (int i = 0; i < XV_PER_T; ++i) {
-      const int idx = tid + i * kThreads;
-      const int row = idx / (BK / 8);
-      const int c8 = idx % (BK / 8);
-      u32x4 v = {0, 0, 0, 0};
-      if (idx < XV && m0 + row < p.m)
-        v = *(const u32x4*)(p.x + (int64_t)(m0 + row) * p.ldx + k0 + c8 * 8);
-      xr[i] = v;
-    }
-  };
-  auto store_x = [&](int buf, const u32x4(&xr)[XV_PER_T]) {
-#pragma unroll
-    for (int i = 0; i < XV_PER_T; ++i) {
-      const int idx = tid + i * kThreads;
-      if (idx < XV) {
-        const int row = idx / (BK / 8);
-        const int c8 = idx % (BK / 8);
-        *(u32x4*)&s_x[buf][row * LDS_STRIDE + c8 * 8] = xr[i];
+  for (int s = 0; s < S - 1; ++s)
+    if (s < kt_n) issue_stage<BN, WINT8>(p, smem + s * L::kBytes, m0, n0, kbase + s * kStageK, wave, lane);
+  for (int t = 0; t < kt_n; ++t) {
+    // stages t+1 .. t+S-2 may stay in flight; stage t must have landed
+    const int ahead = min(S - 2, kt_n - 1 - t);
+    if constexpr (S >= 3) {
+      if (ahead >= 1) {
+        if constexpr (S >= 4) {
+          if (ahead >= 2) wait_vmcnt<2 * L::kLoads>();
+          else wait_vmcnt<L::kLoads>();
+        } else {
+          wait_vmcnt<L::kLoads>();
+        }
+      } else {
+        wait_vmcnt<0>();
       }
+    } else {
+      wait_vmcnt<0>();
     }
-  };
-
-  const int n_k = p.k / BK;
-  u32x4 xr[XV_PER_T];
-  WRegs<BK, WINT8> wc[NW], wn[NW];
-  load_x(0, xr);
-#pragma unroll
-  for (int ni = 0; ni < NW; ++ni) load_w<BK, WINT8>(p, wrow0 + ni * 16 + r, 0, lane, wc[ni]);
-  store_x(0, xr);
-  __syncthreads();
-
-  for (int kt = 0; kt < n_k; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < n_k;
-    if (more) {
-      load_x((kt + 1) * BK, xr);
-#pragma unroll
-      for (int ni = 0; ni < NW; ++ni)
-        load_w<BK, WINT8>(p, wrow0 + ni * 16 + r, (kt + 1) * BK, lane, wn[ni]);
-    }
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      bf16x8 a[NW];
-#pragma unroll
-      for (int ni = 0; ni < NW; ++ni) a[ni] = w_operand<BK, WINT8>(wc[ni], s);
-#pragma unroll
-      for (int mi = 0; mi < MW; ++mi) {
-        const bf16x8 b = __builtin_bit_cast(
-            bf16x8, *(const u32x4*)&s_x[buf][(mi * 16 + r) * LDS_STRIDE + g * (BK / 4) + s * 8]);
-#pragma unroll
-        for (int ni = 0; ni < NW; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ni], b, acc[mi][ni], 0, 0, 0);
-      }
-    }
-    if (more) store_x(buf ^ 1, xr);
-    __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int ni = 0; ni < NW; ++ni) wc[ni] = wn[ni];
-    }
+    // the explicit vmcnt wait above covers this wave's DMA; the barrier makes every
+    // wave's stage t visible (a __syncthreads fence would wait for all of them)
+    asm volatile("s_barrier" ::: "memory");
+    const int tn2 = t + S - 1;
+    if (tn2 < kt_n)
+      issue_stage<BN, WINT8>(p, smem + (tn2 % S) * L::kBytes, m0, n0, kbase + tn2 * kStageK, wave, lane);
+    mma_stage<BN, WINT8, MS, NS>(smem + (t % S) * L::kBytes, wm, wn, lane, acc);
   }
 
-  // ---- epilogue: lane holds D[n = 4g + i][m = r] of every (mi, ni) tile ----
-  if constexpr (EPI == 0) {
+  // ---- epilogue: lane holds D[n = 4g + i][m = r] of each (mi, ni) subtile ----
+  const int r = lane & 15;
+  const int g = lane >> 4;
 #pragma unroll
-    for (int ni = 0; ni < NW; ++ni) {
-      const int n = wrow0 + ni * 16 + 4 * g;
-      float sc[4];
+  for (int mi = 0; mi < MS; ++mi) {
+    const int m = m0 + wm * MS * 16 + mi * 16 + r;
+    if constexpr (EPI == 0) {
+      if (m < p.m) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = scale_at<SDT>(p.scale, n + i);
-#pragma unroll
-      for (int mi = 0; mi < MW; ++mi) {
-        const int m = m0 + mi * 16 + r;
-        if (m < p.m) {
+        for (int ni = 0; ni < NS; ++ni) {
+          const int n = n0 + wn * NS * 16 + ni * 16 + 4 * g;
           const floatx4 v = acc[mi][ni];
-          const u32x2 bits = {pack_bf16x2(v[0] * sc[0], v[1] * sc[1]),
-                              pack_bf16x2(v[2] * sc[2], v[3] * sc[3])};
+          const u32x2 bits = {pack_bf16x2(v[0] * scale_at<SDT>(p.scale, n),
+                                          v[1] * scale_at<SDT>(p.scale, n + 1)),
+                              pack_bf16x2(v[2] * scale_at<SDT>(p.scale, n + 2),
+                                          v[3] * scale_at<SDT>(p.scale, n + 3))};
           *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
         }
       }
-    }
-  } else if constexpr (EPI == 1) {
-    static_assert(NW % 2 == 0, "swiglu pairs gate/up subtiles");
+    } else if constexpr (EPI == 1) {
+      static_assert(NS % 2 == 0, "swiglu pairs gate/up subtiles");
+      if (m < p.m) {
 #pragma unroll
-    for (int q = 0; q < NW / 2; ++q) {
-      const int ng = wrow0 + 2 * q * 16 + 4 * g;  // gate rows; up rows are +16
-      const int ncol = (wrow0 + 2 * q * 16) / 2 + 4 * g;
-      float sg[4], su[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sg[i] = scale_at<SDT>(p.scale, ng + i);
-        su[i] = scale_at<SDT>(p.scale, ng + 16 + i);
-      }
-#pragma unroll
-      for (int mi = 0; mi < MW; ++mi) {
-        const int m = m0 + mi * 16 + r;
-        if (m < p.m) {
+        for (int q = 0; q < NS / 2; ++q) {
+          const int ng = n0 + wn * NS * 16 + 2 * q * 16 + 4 * g;  // gate rows; up rows are +16
           float out[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float gate = bf16_round(acc[mi][2 * q][i] * sg[i]);
-            const float up = bf16_round(acc[mi][2 * q + 1][i] * su[i]);
+            const float gate = bf16_round(acc[mi][2 * q][i] * scale_at<SDT>(p.scale, ng + i));
+            const float up = bf16_round(acc[mi][2 * q + 1][i] * scale_at<SDT>(p.scale, ng + 16 + i));
             const float silu = bf16_round(gate / (1.f + __expf(-gate)));
             out[i] = silu * up;
           }
+          const int ncol = (n0 + wn * NS * 16 + 2 * q * 16) / 2 + 4 * g;
           const u32x2 bits = {pack_bf16x2(out[0], out[1]), pack_bf16x2(out[2], out[3])};
           *(u32x2*)(p.y + (int64_t)m * p.ldy + ncol) = bits;
         }
       }
-    }
-  } else {
-    // LM head: optional bf16 logits and per-(row, tile) argmax of bf16 logits
-#pragma unroll
-    for (int mi = 0; mi < MW; ++mi) {
-      const int m = m0 + mi * 16 + r;
+    } else if constexpr (EPI == 2) {
       uint64_t best = 0;
 #pragma unroll
-      for (int ni = 0; ni < NW; ++ni) {
-        const int n = wrow0 + ni * 16 + 4 * g;
+      for (int ni = 0; ni < NS; ++ni) {
+        const int n = n0 + wn * NS * 16 + ni * 16 + 4 * g;
         const floatx4 v = acc[mi][ni];
         const u32x2 bits = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         if (p.y != nullptr && m < p.m) *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
@@ -272,47 +310,267 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       }
       best = max_u64(best, shfl_xor_u64(best, 16));
       best = max_u64(best, shfl_xor_u64(best, 32));
-      if (g == 0) s_best[wave][mi * 16 + r] = best;
-    }
-    if (p.argmax != nullptr) {
-      __syncthreads();
-      for (int row = tid; row < BM; row += kThreads) {
-        const int m = m0 + row;
-        if (m < p.m) {
-          uint64_t b = s_best[0][row];
+      // one partial per (row, 64-column half of the tile)
+      if (p.argmax != nullptr && g == 0 && m < p.m)
+        p.argmax[(int64_t)m * (p.n / kArgmaxCols) + (n0 + wn * NS * 16) / kArgmaxCols] = best;
+    } else {
+      if (m < p.m) {
 #pragma unroll
-          for (int w = 1; w < kGemmWaves; ++w) b = max_u64(b, s_best[w][row]);
-          p.argmax[(int64_t)m * p.tiles_n + tn] = b;
+        for (int ni = 0; ni < NS; ++ni) {
+          const int n = n0 + wn * NS * 16 + ni * 16 + 4 * g;
+          const floatx4 v = acc[mi][ni];
+          const floatx4 sv = {v[0] * scale_at<SDT>(p.scale, n), v[1] * scale_at<SDT>(p.scale, n + 1),
+                              v[2] * scale_at<SDT>(p.scale, n + 2), v[3] * scale_at<SDT>(p.scale, n + 3)};
+          *(floatx4*)(partial + ((int64_t)split * p.m + m) * p.n + n) = sv;
         }
       }
     }
   }
 }
 
-template <int MW, int NW, int BK, bool WINT8, int SDT, int EPI>
-int launch_gemm(GemmParams p, hipStream_t stream, const char* name) {
-  constexpr int BM = MW * 16;
-  constexpr int BN = kGemmWaves * NW * 16;
-  p.tiles_m = ceil_div(p.m, BM);
+template <int BN, int S, bool WINT8, int SDT, int EPI>
+int launch_gemm(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name) {
+  using L = StageLayout<BN, WINT8>;
+  p.tiles_m = ceil_div(p.m, kBM);
   p.tiles_n = p.n / BN;
   const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
-  const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded));
-  hipLaunchKernelGGL((gemm_kernel<MW, NW, BK, WINT8, SDT, EPI>), grid, dim3(kThreads), 0, stream,
-                     p);
+  const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
+  const size_t lds = (size_t)S * L::kBytes;
+  // raise the dynamic LDS limit once per instantiation (thread-safe static init)
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)gemm_kernel<BN, S, WINT8, SDT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+      (int)lds);
+  if (attr != hipSuccess) {
+    set_error("%s: cannot reserve %zu bytes of LDS: %s", name, lds, hipGetErrorString(attr));
+    return NE_ELAUNCH;
+  }
+  hipLaunchKernelGGL((gemm_kernel<BN, S, WINT8, SDT, EPI>), grid, dim3(kThreads), lds, stream, p,
+                     p.k / splits, partial);
+  return check_launch(name);
+}
+
+// ---- W8A16 projections ----------------------------------------------------------
+// Work-group tile: 80 token rows (5 MFMA subtiles) x 16 * NSUB weight rows, sized so
+// that the verify-step shapes give about one work-group per CU (M = 320: QKV
+// N = 4096 and gate|up N = 6144 give 256 tiles; o / down N = 1024 give 64 tiles,
+// split 4 ways over K).  The waves form kKGroups x NSUB/2: wave (kg, nw) runs k-step
+// kg (32 wide) of every 128-wide stage for all 5 token subtiles against weight
+// subtiles 2 nw and 2 nw + 1, so each X fragment read from LDS feeds 2 MFMAs and
+// each weight fragment 5.  The k-groups' partial tiles are summed through LDS at
+// the end, each wave finishing some of the token subtiles.
+constexpr int kPM = 5;  // token subtiles per work-group
+constexpr int kPRows = kPM * 16;
+constexpr int kKGroups = 4;
+constexpr int kProjStages = 3;
+constexpr int kDmaPerWave = 4;  // DMA instructions per issuing wave per stage
+
+template <int NSUB>
+struct ProjLayout {
+  static constexpr int kNW = NSUB / 2;
+  static constexpr int kWaves = kKGroups * kNW;
+  static constexpr int kThreads = kWaves * kWave;
+  static constexpr int kXBytes = kPRows * kStageK * 2;  // 20 KiB
+  static constexpr int kWBytes = NSUB * 16 * kStageK;   // int8 rows of 128 bytes
+  static constexpr int kStage = kXBytes + kWBytes;
+  static constexpr int kXInstr = kXBytes / 1024;
+  static constexpr int kInstr = kXInstr + kWBytes / 1024;
+  static constexpr int kIssuers = kInstr / kDmaPerWave;
+  static_assert(kInstr % kDmaPerWave == 0 && kIssuers <= kWaves, "DMA split");
+  static constexpr int kRedBytes = kKGroups * kNW * kPM * 2 * 1024;
+  static constexpr int kLds = kProjStages * kStage > kRedBytes ? kProjStages * kStage : kRedBytes;
+};
+
+// Copy one 128-wide k stage: X rows m0..m0+79 (rows past m re-read row m-1 and are
+// never stored) and weight rows n0..n0+16*NSUB-1.  Issuing waves copy exactly
+// kDmaPerWave KiB each, so every wave's vmcnt bookkeeping is the same.
+template <int NSUB>
+__device__ __forceinline__ void proj_issue(const GemmParams& p, char* stage, int m0, int n0, int k0,
+                                           int wave, int lane) {
+  using L = ProjLayout<NSUB>;
+  if (wave >= L::kIssuers) return;
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int i = wave * kDmaPerWave + j;
+    if (i < L::kXInstr) {  // 4 rows x 16 chunks of 16 bytes
+      const int row = i * 4 + (lane >> 4);
+      const int chunk = (lane & 15) ^ (row & 15);
+      const int grow = min(m0 + row, p.m - 1);
+      lds_dma16(p.x + (int64_t)grow * p.ldx + k0 + chunk * 8, stage + i * 1024);
+    } else {  // 8 weight rows x 8 chunks
+      const int b = i - L::kXInstr;
+      const int row = b * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ (row & 7);
+      lds_dma16((const int8_t*)p.w + (int64_t)(n0 + row) * p.k + k0 + chunk * 16,
+                stage + L::kXBytes + b * 1024);
+    }
+  }
+}
+
+// k-step kg of a stage.  Lane group g = lane / 16 supplies logical
+// k = 64 (kg / 2) + 16 g + 8 (kg % 2) + e, e < 8: X chunk 8 (kg / 2) + 2 g + kg % 2 of
+// its 256-byte row, weight bytes 16 (4 (kg / 2) + g) + 8 (kg % 2) of its 128-byte row.
+template <int NSUB>
+__device__ __forceinline__ void proj_mma(const char* stage, int kg, int nw, int lane,
+                                         floatx4 (&acc)[kPM][2]) {
+  using L = ProjLayout<NSUB>;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const char* xs = stage;
+  const char* ws = stage + L::kXBytes;
+  bf16x8 a[2];
+#pragma unroll
+  for (int ns = 0; ns < 2; ++ns) {
+    const int row = (2 * nw + ns) * 16 + r;
+    const int chunk = (4 * (kg >> 1) + g) ^ (row & 7);
+    const u32x2 v = *(const u32x2*)(ws + row * 128 + chunk * 16 + (kg & 1) * 8);
+    a[ns] = int8x8_to_bf16x8(v[0], v[1]);
+  }
+#pragma unroll
+  for (int mi = 0; mi < kPM; ++mi) {
+    const int row = mi * 16 + r;
+    const int chunk = (8 * (kg >> 1) + 2 * g + (kg & 1)) ^ (row & 15);
+    const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(xs + row * 256 + chunk * 16));
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns)
+      acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ns], b, acc[mi][ns], 0, 0, 0);
+  }
+}
+
+// EPI 0: y = bf16(acc * scale); 1: SwiGLU of paired gate/up subtiles; 3: fp32 partial
+// sums of K split blockIdx.y, scaled, into partial[split][m][n].
+template <int NSUB, int SDT, int EPI>
+__global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmParams p,
+                                                                         int k_per_split,
+                                                                         float* partial) {
+  using L = ProjLayout<NSUB>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int bid = blockIdx.x;
+  const int xcd = bid % kNumXcd;
+  const int jj = bid / kNumXcd;
+  const int tm = jj % p.tiles_m;
+  const int tn = (jj / p.tiles_m) * kNumXcd + xcd;  // the M tiles of one weight tile share an XCD
+  if (tn >= p.tiles_n) return;
+  const int split = blockIdx.y;
+  const int m0 = tm * kPRows;
+  const int n0 = tn * NSUB * 16;
+  const int kbase = split * k_per_split;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int kg = wave / L::kNW;
+  const int nw = wave % L::kNW;
+
+  floatx4 acc[kPM][2];
+#pragma unroll
+  for (int mi = 0; mi < kPM; ++mi)
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int kt_n = k_per_split / kStageK;
+#pragma unroll
+  for (int s = 0; s < kProjStages - 1; ++s)
+    if (s < kt_n) proj_issue<NSUB>(p, smem + s * L::kStage, m0, n0, kbase + s * kStageK, wave, lane);
+  for (int t = 0; t < kt_n; ++t) {
+    // this wave's copies of stage t are done once at most the next stage's remain
+    if (t + 1 < kt_n) {
+      wait_vmcnt<kDmaPerWave>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    // every wave's stage t is in LDS after the barrier; a __syncthreads fence would
+    // also wait for the stage still in flight
+    asm volatile("s_barrier" ::: "memory");
+    const int tn2 = t + kProjStages - 1;
+    if (tn2 < kt_n)
+      proj_issue<NSUB>(p, smem + (tn2 % kProjStages) * L::kStage, m0, n0, kbase + tn2 * kStageK, wave,
+                       lane);
+    proj_mma<NSUB>(smem + (t % kProjStages) * L::kStage, kg, nw, lane, acc);
+  }
+
+  // ---- sum the k-groups through LDS (the stage ring is free once all waves pass) ----
+  __syncthreads();
+  floatx4* red = (floatx4*)smem;  // [kg][nw][mi][ns][lane]
+#pragma unroll
+  for (int mi = 0; mi < kPM; ++mi)
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * kPM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
+  __syncthreads();
+
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  for (int mi = kg; mi < kPM; mi += kKGroups) {
+    floatx4 v[2];
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) {
+      v[ns] = red[((nw * kPM + mi) * 2 + ns) * kWave + lane];
+#pragma unroll
+      for (int q = 1; q < kKGroups; ++q) v[ns] += red[(((q * L::kNW + nw) * kPM + mi) * 2 + ns) * kWave + lane];
+    }
+    // lane holds D[n = 4 g + i][m = r] of weight subtiles 2 nw + ns
+    const int m = m0 + mi * 16 + r;
+    if (m >= p.m) continue;
+    if constexpr (EPI == 0) {
+#pragma unroll
+      for (int ns = 0; ns < 2; ++ns) {
+        const int n = n0 + (2 * nw + ns) * 16 + 4 * g;
+        const u32x2 bits = {pack_bf16x2(v[ns][0] * scale_at<SDT>(p.scale, n),
+                                        v[ns][1] * scale_at<SDT>(p.scale, n + 1)),
+                            pack_bf16x2(v[ns][2] * scale_at<SDT>(p.scale, n + 2),
+                                        v[ns][3] * scale_at<SDT>(p.scale, n + 3))};
+        *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
+      }
+    } else if constexpr (EPI == 1) {
+      const int ng = n0 + 2 * nw * 16 + 4 * g;  // gate rows; the paired up rows are +16
+      float out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gate = bf16_round(v[0][i] * scale_at<SDT>(p.scale, ng + i));
+        const float up = bf16_round(v[1][i] * scale_at<SDT>(p.scale, ng + 16 + i));
+        const float silu = bf16_round(gate / (1.f + __expf(-gate)));
+        out[i] = silu * up;
+      }
+      const int ncol = (n0 + 2 * nw * 16) / 2 + 4 * g;
+      const u32x2 bits = {pack_bf16x2(out[0], out[1]), pack_bf16x2(out[2], out[3])};
+      *(u32x2*)(p.y + (int64_t)m * p.ldy + ncol) = bits;
+    } else {
+#pragma unroll
+      for (int ns = 0; ns < 2; ++ns) {
+        const int n = n0 + (2 * nw + ns) * 16 + 4 * g;
+        const floatx4 sv = {v[ns][0] * scale_at<SDT>(p.scale, n), v[ns][1] * scale_at<SDT>(p.scale, n + 1),
+                            v[ns][2] * scale_at<SDT>(p.scale, n + 2),
+                            v[ns][3] * scale_at<SDT>(p.scale, n + 3)};
+        *(floatx4*)(partial + ((int64_t)split * p.m + m) * p.n + n) = sv;
+      }
+    }
+  }
+}
+
+template <int NSUB, int SDT, int EPI>
+int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name) {
+  using L = ProjLayout<NSUB>;
+  p.tiles_m = ceil_div(p.m, kPRows);
+  p.tiles_n = p.n / (NSUB * 16);
+  const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
+  const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)proj_kernel<NSUB, SDT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
+  if (attr != hipSuccess) {
+    set_error("%s: cannot reserve %d bytes of LDS: %s", name, L::kLds, hipGetErrorString(attr));
+    return NE_ELAUNCH;
+  }
+  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI>), grid, dim3(L::kThreads), L::kLds, stream, p,
+                     p.k / splits, partial);
   return check_launch(name);
 }
 
 template <int SDT>
-int dispatch_w8a16(GemmParams p, int epilogue, hipStream_t s) {
+int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipStream_t s) {
   if (epilogue == NE_EPILOGUE_SWIGLU) {
-    if (p.m <= 32) return launch_gemm<2, 2, 64, true, SDT, 1>(p, s, "w8a16_swiglu");
-    return launch_gemm<4, 2, 64, true, SDT, 1>(p, s, "w8a16_swiglu");
+    if (p.n % 96 == 0) return launch_proj<6, SDT, 1>(p, 1, nullptr, s, "w8a16_swiglu");
+    return launch_proj<4, SDT, 1>(p, 1, nullptr, s, "w8a16_swiglu");
   }
-  if (p.m <= 32) return launch_gemm<2, 1, 64, true, SDT, 0>(p, s, "w8a16_gemm");
-  return launch_gemm<4, 1, 64, true, SDT, 0>(p, s, "w8a16_gemm");
+  if (partial != nullptr) return launch_proj<4, SDT, 3>(p, splits, partial, s, "w8a16_splitk");
+  return launch_proj<4, SDT, 0>(p, 1, nullptr, s, "w8a16_gemm");
 }
-
-constexpr int kLmHeadBN = kGemmWaves * 16;
 
 }  // namespace
 
@@ -320,22 +578,11 @@ constexpr int kLmHeadBN = kGemmWaves * 16;
 
 using namespace ne;
 
-extern "C" int ne_w8a16_gemm(const void* x, int64_t ldx, const int8_t* w, const void* scale,
-                             int32_t scale_dtype, int32_t m, int32_t n, int32_t k, void* y,
-                             int64_t ldy, int32_t epilogue, void* stream) {
-  NE_CHECK_ARG(m >= 0 && n > 0 && k > 0, "bad gemm shape m=%d n=%d k=%d", m, n, k);
-  if (m == 0) return NE_OK;
-  NE_CHECK_ARG(x && w && scale && y, "null pointer argument");
-  NE_CHECK_ARG(epilogue == NE_EPILOGUE_STORE || epilogue == NE_EPILOGUE_SWIGLU,
-               "unknown epilogue %d", epilogue);
-  NE_CHECK_SUPPORTED(k % 64 == 0, "k must be a multiple of 64 (got %d)", k);
-  const int bn = (epilogue == NE_EPILOGUE_SWIGLU) ? 128 : 64;
-  NE_CHECK_SUPPORTED(n % bn == 0, "n must be a multiple of %d (got %d)", bn, n);
-  NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
-  NE_CHECK_ARG(ldy >= (epilogue == NE_EPILOGUE_SWIGLU ? n / 2 : n) && ldy % 4 == 0,
-               "ldy too small or not a multiple of 4");
-  NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 8) == 0,
-               "x and w must be 16-byte aligned, y 8-byte aligned");
+namespace {
+
+int w8a16_common(const void* x, int64_t ldx, const int8_t* w, const void* scale, int32_t scale_dtype,
+                 int32_t m, int32_t n, int32_t k, void* y, int64_t ldy, int32_t epilogue,
+                 int32_t splits, float* partial, void* stream) {
   GemmParams p{};
   p.x = (const uint16_t*)x;
   p.ldx = ldx;
@@ -349,18 +596,55 @@ extern "C" int ne_w8a16_gemm(const void* x, int64_t ldx, const int8_t* w, const 
   hipStream_t s = (hipStream_t)stream;
   switch (scale_dtype) {
     case NE_DTYPE_BF16:
-      return dispatch_w8a16<NE_DTYPE_BF16>(p, epilogue, s);
+      return dispatch_w8a16<NE_DTYPE_BF16>(p, epilogue, splits, partial, s);
     case NE_DTYPE_FP16:
-      return dispatch_w8a16<NE_DTYPE_FP16>(p, epilogue, s);
+      return dispatch_w8a16<NE_DTYPE_FP16>(p, epilogue, splits, partial, s);
     case NE_DTYPE_FP32:
-      return dispatch_w8a16<NE_DTYPE_FP32>(p, epilogue, s);
+      return dispatch_w8a16<NE_DTYPE_FP32>(p, epilogue, splits, partial, s);
     default:
       set_error("scale_dtype must be bf16, fp16 or fp32");
       return NE_EINVAL;
   }
 }
 
-extern "C" int32_t ne_lm_head_num_tiles(int32_t n) { return n > 0 ? n / kLmHeadBN : 0; }
+}  // namespace
+
+extern "C" int ne_w8a16_gemm(const void* x, int64_t ldx, const int8_t* w, const void* scale,
+                             int32_t scale_dtype, int32_t m, int32_t n, int32_t k, void* y,
+                             int64_t ldy, int32_t epilogue, void* stream) {
+  NE_CHECK_ARG(m >= 0 && n > 0 && k > 0, "bad gemm shape m=%d n=%d k=%d", m, n, k);
+  if (m == 0) return NE_OK;
+  NE_CHECK_ARG(x && w && scale && y, "null pointer argument");
+  NE_CHECK_ARG(epilogue == NE_EPILOGUE_STORE || epilogue == NE_EPILOGUE_SWIGLU,
+               "unknown epilogue %d", epilogue);
+  NE_CHECK_SUPPORTED(k % 128 == 0, "k must be a multiple of 128 (got %d)", k);
+  NE_CHECK_SUPPORTED(n % 64 == 0, "n must be a multiple of 64 (got %d)", n);
+  NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
+  NE_CHECK_ARG(ldy >= (epilogue == NE_EPILOGUE_SWIGLU ? n / 2 : n) && ldy % 4 == 0,
+               "ldy too small or not a multiple of 4");
+  NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 8) == 0,
+               "x and w must be 16-byte aligned, y 8-byte aligned");
+  return w8a16_common(x, ldx, w, scale, scale_dtype, m, n, k, y, ldy, epilogue, 1, nullptr, stream);
+}
+
+extern "C" int ne_w8a16_gemm_splitk(const void* x, int64_t ldx, const int8_t* w, const void* scale,
+                                    int32_t scale_dtype, int32_t m, int32_t n, int32_t k,
+                                    int32_t splits, float* partials, void* stream) {
+  NE_CHECK_ARG(m >= 0 && n > 0 && k > 0, "bad gemm shape m=%d n=%d k=%d", m, n, k);
+  if (m == 0) return NE_OK;
+  NE_CHECK_ARG(x && w && scale && partials, "null pointer argument");
+  NE_CHECK_ARG(splits >= 1 && splits <= 64, "splits must be in [1, 64] (got %d)", splits);
+  NE_CHECK_SUPPORTED(k % (128 * splits) == 0, "k must be a multiple of 128 * splits (k=%d, splits=%d)",
+                     k, splits);
+  NE_CHECK_SUPPORTED(n % 64 == 0, "n must be a multiple of 64 (got %d)", n);
+  NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
+  NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)partials % 16) == 0,
+               "x, w and partials must be 16-byte aligned");
+  return w8a16_common(x, ldx, w, scale, scale_dtype, m, n, k, nullptr, 0, NE_EPILOGUE_STORE, splits,
+                      partials, stream);
+}
+
+extern "C" int32_t ne_lm_head_num_tiles(int32_t n) { return n > 0 ? n / kArgmaxCols : 0; }
 
 extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, int32_t n,
                           int32_t k, void* logits, int64_t ld_logits, uint64_t* argmax_partials,
@@ -369,8 +653,8 @@ extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, 
   if (m == 0) return NE_OK;
   NE_CHECK_ARG(x && w, "null pointer argument");
   NE_CHECK_ARG(logits || argmax_partials, "lm head needs logits and/or argmax_partials");
-  NE_CHECK_SUPPORTED(k % 32 == 0, "k must be a multiple of 32 (got %d)", k);
-  NE_CHECK_SUPPORTED(n % kLmHeadBN == 0, "vocab must be a multiple of %d (got %d)", kLmHeadBN, n);
+  NE_CHECK_SUPPORTED(k % 128 == 0, "k must be a multiple of 128 (got %d)", k);
+  NE_CHECK_SUPPORTED(n % 128 == 0, "vocab must be a multiple of 128 (got %d)", n);
   NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
   NE_CHECK_ARG(!logits || (ld_logits >= n && ld_logits % 4 == 0), "bad ld_logits");
   NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
@@ -387,7 +671,5 @@ extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, 
   p.ldy = ld_logits;
   p.argmax = argmax_partials;
   hipStream_t s = (hipStream_t)stream;
-  if (m <= 64) return launch_gemm<4, 1, 32, false, -1, 2>(p, s, "lm_head");
-  if (m <= 128) return launch_gemm<8, 1, 32, false, -1, 2>(p, s, "lm_head");
-  return launch_gemm<20, 1, 32, false, -1, 2>(p, s, "lm_head");
+  return launch_gemm<128, 3, false, -1, 2>(p, 1, nullptr, s, "lm_head");
 }

@@ -32,13 +32,16 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
 }
 
 // MODE 0: out = norm(x); 1: residual = bf16(residual + delta), out = norm(residual);
-// 2: residual = embed[token], out = norm(residual).  One wave per row.
+// 2: residual = embed[token], out = norm(residual); 3: as 1 with
+// delta = bf16(sum over `splits` fp32 partial rows, split stride rows * hidden).
+// One wave per row.
 template <int MODE>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_t* residual,
                                                       const uint16_t* delta, const int32_t* tokens,
                                                       const uint16_t* embed, const uint16_t* weight,
                                                       uint16_t* out, int rows, int hidden,
-                                                      float eps) {
+                                                      float eps, const float* partials = nullptr,
+                                                      int splits = 0) {
   const int row = blockIdx.x * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
@@ -46,7 +49,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_
   const uint16_t* src;
   if constexpr (MODE == 0) {
     src = x + (int64_t)row * hidden;
-  } else if constexpr (MODE == 1) {
+  } else if constexpr (MODE == 1 || MODE == 3) {
     src = residual + (int64_t)row * hidden;
   } else {
     src = embed + (int64_t)tokens[row] * hidden;
@@ -63,6 +66,20 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_
         unpack8(*(const u32x4*)(delta + (int64_t)row * hidden + ci * 8), d);
 #pragma unroll
         for (int e = 0; e < 8; ++e) h[c][e] = bf16_round(h[c][e] + d[e]);
+      } else if constexpr (MODE == 3) {
+        float d[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < splits; ++sp) {
+          const float* pp = partials + ((int64_t)sp * rows + row) * hidden + ci * 8;
+          const floatx4 lo = *(const floatx4*)pp;
+          const floatx4 hi = *(const floatx4*)(pp + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            d[e] += lo[e];
+            d[e + 4] += hi[e];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[c][e] = bf16_round(h[c][e] + bf16_round(d[e]));
       }
       if constexpr (MODE != 0) *(u32x4*)(residual + (int64_t)row * hidden + ci * 8) = pack8(h[c]);
 #pragma unroll
@@ -214,6 +231,21 @@ extern "C" int ne_add_rmsnorm(void* residual, const void* delta, const void* wei
                      nullptr, (uint16_t*)residual, (const uint16_t*)delta, nullptr, nullptr,
                      (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps);
   return check_launch("add_rmsnorm");
+}
+
+extern "C" int ne_splitk_add_rmsnorm(void* residual, const float* partials, int32_t splits,
+                                     const void* weight, void* out, int32_t rows, int32_t hidden,
+                                     float eps, void* stream) {
+  int rc = check_norm_args(weight, out, rows, hidden);
+  if (rc != NE_OK) return rc;
+  NE_CHECK_ARG(residual && partials, "null residual/partials");
+  NE_CHECK_ARG(splits >= 1 && splits <= 64, "splits must be in [1, 64] (got %d)", splits);
+  NE_CHECK_ARG(((uintptr_t)partials % 16) == 0, "partials must be 16-byte aligned");
+  if (rows == 0) return NE_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel<3>, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
+                     nullptr, (uint16_t*)residual, nullptr, nullptr, nullptr,
+                     (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps, partials, splits);
+  return check_launch("splitk_add_rmsnorm");
 }
 
 extern "C" int ne_embed_rmsnorm(const int32_t* tokens, const void* embed, const void* weight,

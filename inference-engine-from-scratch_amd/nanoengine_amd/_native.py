@@ -66,10 +66,15 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
     ),
+    "ne_w8a16_gemm_splitk": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+    ),
     "ne_lm_head_num_tiles": (_i32, [_i32]),
     "ne_lm_head": (ctypes.c_int, [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _i64, _u64p, _vp]),
     "ne_rmsnorm": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ne_add_rmsnorm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
+    "ne_splitk_add_rmsnorm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ne_embed_rmsnorm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ne_qk_norm_rope_kv_write": (
         ctypes.c_int,

@@ -264,6 +264,50 @@ def w8a16_gemm(
     return out
 
 
+PROJ_TILE_ROWS = 80  # token rows per work-group of the W8A16 kernels
+PROJ_TILE_COLS = 64  # weight rows per work-group of the store / split-K kernels
+TARGET_WORK_GROUPS = 256  # one per CU
+
+
+def splitk_splits(m: int, n: int, k: int, max_splits: int = 4) -> int:
+    """K splits that bring a narrow projection to about one work-group per CU."""
+    tiles = -(-m // PROJ_TILE_ROWS) * (n // PROJ_TILE_COLS)
+    splits = max(1, min(max_splits, TARGET_WORK_GROUPS // max(tiles, 1)))
+    while splits > 1 and k % (128 * splits):
+        splits -= 1
+    return splits
+
+
+def w8a16_gemm_splitk(
+    x: torch.Tensor,
+    weight_int8: torch.Tensor,
+    weight_scale: torch.Tensor,
+    splits: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """fp32 ``[splits, m, n]`` partial products over K parts (scale applied), summed by
+    ``splitk_add_rmsnorm``."""
+    device = _require_gpu(x, weight_int8, weight_scale)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1, "x must be [m, k] bf16")
+    _check(weight_int8.dtype == torch.int8 and weight_int8.dim() == 2, "weight must be [n, k] int8")
+    _contig(weight_int8, "weight_int8")
+    _contig(weight_scale, "weight_scale")
+    m, k = x.shape
+    n = weight_int8.shape[0]
+    _check(weight_int8.shape[1] == k, f"k mismatch: x has {k}, weight {weight_int8.shape[1]}")
+    _check(weight_scale.numel() == n, "one scale per weight row")
+    if out is None:
+        out = torch.empty((splits, m, n), dtype=torch.float32, device=device)
+    _check(out.dtype == torch.float32 and out.is_contiguous() and out.numel() >= splits * m * n,
+           "partials must be contiguous fp32 with room for [splits, m, n]")
+    _native.call(
+        "ne_w8a16_gemm_splitk",
+        _ptr(x), x.stride(0), _ptr(weight_int8), _ptr(weight_scale),
+        dtype_code(weight_scale.dtype), m, n, k, splits, _ptr(out), _stream(device),
+    )
+    return out
+
+
 def lm_head_num_tiles(vocab: int) -> int:
     return int(_native.load().ne_lm_head_num_tiles(vocab))
 
@@ -318,6 +362,20 @@ def add_rmsnorm(residual: torch.Tensor, delta: torch.Tensor, weight: torch.Tenso
     rows, hidden = residual.shape
     _native.call("ne_add_rmsnorm", _ptr(residual), _ptr(delta), _ptr(weight), _ptr(out), rows,
                  hidden, float(eps), _stream(device))
+    return out
+
+
+def splitk_add_rmsnorm(residual: torch.Tensor, partials: torch.Tensor, splits: int, weight: torch.Tensor,
+                       eps: float, out=None) -> torch.Tensor:
+    """``residual += bf16(sum of the split-K partials)`` in place, then RMSNorm."""
+    device = _require_gpu(residual, partials, weight)
+    _contig(residual, "residual")
+    rows, hidden = residual.shape
+    _check(partials.dtype == torch.float32 and partials.is_contiguous()
+           and partials.numel() >= splits * rows * hidden, "partials must be fp32 [splits, rows, hidden]")
+    out = torch.empty_like(residual) if out is None else out
+    _native.call("ne_splitk_add_rmsnorm", _ptr(residual), _ptr(partials), splits, _ptr(weight), _ptr(out),
+                 rows, hidden, float(eps), _stream(device))
     return out
 
 

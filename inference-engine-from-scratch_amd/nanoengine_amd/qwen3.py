@@ -224,6 +224,12 @@ class Qwen3VerifyModel:
         self.inv_freq = (1.0 / (c.rope_theta**exps)).to(device)
         self.workspace = kernels.AttentionWorkspace()
         self.softmax_scale = 1.0 / math.sqrt(c.head_dim)
+        # o_proj / down_proj (N = hidden) split K across work-groups when the rows alone
+        # give too few output tiles; the fp32 partials feed the fused residual add + norm
+        self.o_splits = [kernels.splitk_splits(r, h, q) for r in range(max_rows + 1)]
+        self.down_splits = [kernels.splitk_splits(r, h, c.intermediate_size) for r in range(max_rows + 1)]
+        most = max(max(a * r, b * r) for r, (a, b) in enumerate(zip(self.o_splits, self.down_splits)))
+        self.partials = torch.empty(max(most, 1) * h, dtype=torch.float32, device=device)
 
     def forward(self, rows: int, tokens: torch.Tensor, batch: AttentionBatch, pool) -> torch.Tensor:
         """Hidden states after the final norm for ``rows`` packed query rows; writes this
@@ -249,14 +255,26 @@ class Qwen3VerifyModel:
                 batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start, batch.q_len,
                 batch.max_q_len, batch.max_ctx_len, self.softmax_scale, out=attn, workspace=self.workspace,
             )
-            kernels.w8a16_gemm(attn.view(rows, -1), layer.o_int8, layer.o_scale, out=delta)
-            kernels.add_rmsnorm(res, delta, layer.post_attention_layernorm, eps, out=normed)
+            self._project_add_norm(attn.view(rows, -1), layer.o_int8, layer.o_scale, self.o_splits[rows],
+                                   layer.post_attention_layernorm, res, delta, normed)
             kernels.w8a16_gemm(normed, layer.gate_up_int8, layer.gate_up_scale, epilogue=EPILOGUE_SWIGLU,
                                out=act)
-            kernels.w8a16_gemm(act, layer.down_int8, layer.down_scale, out=delta)
             next_norm = w.layers[i + 1].input_layernorm if i + 1 < len(w.layers) else w.norm
-            kernels.add_rmsnorm(res, delta, next_norm, eps, out=normed)
+            self._project_add_norm(act, layer.down_int8, layer.down_scale, self.down_splits[rows], next_norm,
+                                   res, delta, normed)
         return normed
+
+    def _project_add_norm(self, x, w_int8, w_scale, splits, norm_weight, res, delta, normed) -> None:
+        """residual += bf16(x @ W^T); normed = RMSNorm(residual) (qwen3.py:145-149)."""
+        eps = self.config.rms_norm_eps
+        if splits > 1:
+            rows = x.shape[0]
+            parts = self.partials[: splits * rows * w_int8.shape[0]]
+            kernels.w8a16_gemm_splitk(x, w_int8, w_scale, splits, out=parts)
+            kernels.splitk_add_rmsnorm(res, parts, splits, norm_weight, eps, out=normed)
+        else:
+            kernels.w8a16_gemm(x, w_int8, w_scale, out=delta)
+            kernels.add_rmsnorm(res, delta, norm_weight, eps, out=normed)
 
     def compute_logits(self, hidden: torch.Tensor, logits: bool = True, argmax: bool = False):
         """qwen3.py:197-203 on the bf16 LM-head kernel; optionally only argmax partials."""

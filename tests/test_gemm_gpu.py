@@ -45,6 +45,32 @@ def test_w8a16_matches_int8_linear(device, m, n, k):
     assert rel_err(out, ref_bf16) < TOL
 
 
+@pytest.mark.parametrize("m,n,k,splits", [(320, 1024, 2048, 4), (320, 1024, 3072, 4), (37, 1024, 3072, 3),
+                                          (5, 512, 1024, 2), (160, 1024, 1024, 1)])
+def test_w8a16_splitk_partials(device, m, n, k, splits):
+    """Summed split-K partials equal Int8Linear in fp32 (2e-2 relative), and each part is
+    the product over its own K range."""
+    wq, ws = make_weight(n, k, seed=7 * n + k)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m + k)).to(torch.bfloat16)
+    parts = kernels.w8a16_gemm_splitk(x.to(device), wq.to(device), ws.to(device), splits)
+    torch.cuda.synchronize()
+    parts = parts.cpu()
+    assert parts.shape == (splits, m, n)
+    assert rel_err(parts.sum(0), int8_linear(x.float(), wq, ws.float())) < TOL
+    kp = k // splits
+    for s in range(splits):
+        ref = int8_linear(x[:, s * kp:(s + 1) * kp].float(), wq[:, s * kp:(s + 1) * kp], ws.float())
+        assert rel_err(parts[s], ref) < TOL
+
+
+def test_splitk_choice_targets_one_work_group_per_cu():
+    assert kernels.splitk_splits(320, 1024, 2048) == 4
+    assert kernels.splitk_splits(320, 1024, 3072) == 4
+    assert kernels.splitk_splits(320, 4096, 1024) == 1
+    assert kernels.splitk_splits(4096, 1024, 3072) == 1
+    assert kernels.splitk_splits(80, 1024, 384) == 3  # 3 parts of 128; 4 would not divide k
+
+
 def test_w8a16_fp16_overflow_free(device):
     """int8_quantization.py:41-43: large activations must not overflow (scale is applied in fp32)."""
     wq, ws = make_weight(256, 1024, seed=3)

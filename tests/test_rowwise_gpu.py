@@ -49,6 +49,26 @@ def test_add_rmsnorm_updates_residual(device):
     assert rel_err(out, oracle_norm(new_r, w)) < TOL
 
 
+@pytest.mark.parametrize("splits", [1, 3, 4])
+def test_splitk_add_rmsnorm_equals_add_of_summed_partials(device, splits):
+    """delta = bf16(p[0] + p[1] + ... in order, fp32), then exactly ne_add_rmsnorm."""
+    rows, hidden = 37, 1024
+    parts = torch.randn(splits, rows, hidden) * 0.5
+    r = torch.randn(rows, hidden).to(torch.bfloat16)
+    w = torch.randn(hidden).to(torch.bfloat16)
+    acc = parts[0].numpy().copy()
+    for s in range(1, splits):
+        acc += parts[s].numpy()  # numpy fp32, sequential: the kernel's order
+    delta = torch.from_numpy(acc).to(torch.bfloat16)
+    r1, r2 = r.to(device), r.to(device)
+    want = kernels.add_rmsnorm(r1, delta.to(device), w.to(device), EPS)
+    got = kernels.splitk_add_rmsnorm(r2, parts.to(device), splits, w.to(device), EPS)
+    torch.cuda.synchronize()
+    assert torch.equal(r2.cpu(), r1.cpu())
+    assert torch.equal(got.cpu(), want.cpu())
+    assert torch.equal(r2.cpu(), r + delta)
+
+
 def test_embed_rmsnorm(device):
     emb = (torch.randn(5000, 1024) * 0.02).to(torch.bfloat16)
     w = (torch.randn(1024) * 0.02).to(torch.bfloat16)
