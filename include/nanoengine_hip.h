@@ -100,12 +100,13 @@ int ne_kv_write(const void* vectors, int32_t vec_dtype, int64_t n, int32_t num_h
  *   k/v_cache    [num_slots+1, num_kv_heads, 128] bf16 or int8 (kv_dtype)
  *   k/v_scale    [num_slots+1, num_kv_heads] bf16 or fp16 (int8 cache only)
  *   workspace    ne_paged_attention_workspace_size() bytes.  Bytes 0..3 hold an
- *                error flag (non-zero: a sequence's context exceeded
- *                max_ctx_len), bytes 256.. the per-unit split tickets.  Zero-fill
- *                it before its first use and whenever the shape arguments (and
- *                so its layout) change; every call leaves flag-free tickets at 0.
- * split_len: keys per work-group (multiple of 128, 0 = choose).  head_dim must be
- * 128 and block_size a multiple of 16.
+ *                error flag, set non-zero when a sequence's context exceeded
+ *                max_ctx_len (its keys past the split grid are then dropped); the
+ *                caller clears it.  The rest holds fp32 split partials, written
+ *                and consumed within the call (no state carries between calls).
+ * split_len: keys per work-group (multiple of 128 up to 2048, 0 = choose).  head_dim
+ * must be 128 and block_size a multiple of 16.  One work-group serves every KV head
+ * of a sequence's split; splits are combined by a second kernel on the same stream.
  */
 size_t ne_paged_attention_workspace_size(int32_t num_seqs, int32_t num_q_heads,
                                          int32_t num_kv_heads, int32_t max_q_len,

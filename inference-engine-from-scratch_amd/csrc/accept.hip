@@ -240,7 +240,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
     if (tid == 0) p.num_out[b] = 0;
     return;
   }
-  const int g = p.num_drafts[b];
+  // a draft count beyond max_drafts would index past s_target and the draft row
+  const int g = min(max(p.num_drafts[b], 0), p.max_drafts);
   const int rs0 = p.row_start[b];
   const int32_t* dr = p.drafts + (int64_t)b * p.max_drafts;
 

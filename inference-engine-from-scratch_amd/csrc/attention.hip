@@ -4,19 +4,30 @@
 // (ne/models/attention_context.py:57-109): instead of materialising a padded
 // bf16 copy of every context, K/V 16-token blocks are read in place from the
 // slot pool through the block table, int8 codes are dequantised in registers
-// and both products run on bf16 MFMA (v_mfma_f32_16x16x32_bf16).
+// and both products run on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
 //
 // Work decomposition
 //   unit  = (sequence, KV head, M tile of 16 query rows).  Row r of a unit is
 //           (query head h = r / q_len within the GQA group, query i = r % q_len),
 //           so 2 query heads x 5 queries (k = 4) fill 10 of the 16 MFMA rows.
-//   split = a range of `split_len` keys of one unit; one 256-thread work-group
-//           (4 waves) per (unit, split).  The 4 waves take interleaved 32-key
-//           iterations and are merged through LDS; several splits are merged
-//           by whichever work-group of the unit finishes last (atomic ticket).
-//   Work-group ids are mapped so that every split of a unit lands on the
-//   same XCD (ids are dealt round-robin to the 8 XCDs), keeping the partials
-//   of a unit in one L2.
+//   split = a range of `split_len` keys.  One work-group serves every KV head of
+//           one (sequence, M tile, split): wave w takes KV head w, and all waves
+//           walk the same 16-key tiles together, so each 1 KB (int8) slot of a
+//           block is fetched whole.  Units split per KV head instead read 128-byte
+//           head rows scattered in time, which a load-only probe of the same pool
+//           measured at 3.2 TB/s against 4.7 TB/s for whole slots.  The split's
+//           block-table slots are staged in LDS once; K/V loads are 32-bit lane
+//           offsets on a per-tile buffer resource.
+//   merge = units with more than one split store fp32 partials (reference max,
+//           sum, unnormalised output; real rows only) and a second kernel
+//           combines them.  No fences or atomics order the work-groups: the
+//           kernel boundary does, which on an 8-XCD part with one L2 per XCD is
+//           far cheaper than a device-scope release per work-group.
+//   int8  = codes convert to fp16 exactly with one SDWA op per value and both
+//           products run on fp16 MFMA (Q is bf16, exact in fp16 for |q| < 65504);
+//           the key scale multiplies the scores and the value scale is folded
+//           into P.  bf16 caches use bf16 MFMA directly.
+//   softmax is online with a lazily moved reference max (see compute_iter).
 //
 // Per 32-key iteration a wave computes S^T = K . Q^T as two 16x16 tiles
 // (keys x rows, 4 MFMAs each over the 128 dims) and O^T += V^T . P^T as eight
@@ -41,11 +52,14 @@ namespace {
 constexpr int kHeadDim = 128;
 constexpr int kRows = 16;       // MFMA M/N tile = query rows per unit
 constexpr int kIterKeys = 32;   // keys per wave iteration
-constexpr int kWaves = 4;       // waves per work-group
-constexpr int kThreads = kWaves * kWave;
+constexpr int kTileKeys = 16;   // keys per MFMA tile (never straddles a block)
+constexpr int kMaxSplitLen = 2048;
+constexpr int kMaxTiles = kMaxSplitLen / kTileKeys;
 constexpr float kNegBig = -1e30f;  // finite "minus infinity" for running maxima
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kTargetWorkGroups = 1024;  // ~4 per CU on 256 CUs
+constexpr float kLazyLog2 = 8.f;        // P <= 2^8 between rescales of the output
+constexpr float kLazyMaxVScale = 128.f;  // P * scale <= 2^8 * 128 stays inside fp16
+constexpr int kHeadWaves = 8;           // waves per work-group, one KV head each
 
 struct AttnParams {
   const uint16_t* q;
@@ -60,6 +74,7 @@ struct AttnParams {
   const int32_t* ctx_len;
   const int32_t* q_start;
   const int32_t* q_len;
+  int32_t num_seqs;
   int32_t num_kv_heads;
   int32_t group;
   int32_t mtiles;
@@ -71,10 +86,13 @@ struct AttnParams {
   int64_t o_tok_stride, o_head_stride;
   float* part_o;       // [units][max_splits][16][128]
   float* part_ml;      // [units][max_splits][16][2]
-  uint32_t* counters;  // [units]
   uint32_t* error_flag;
 };
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// K/V registers of one 32-key iteration (two 16-key tiles)
 template <bool INT8>
 struct IterRegs;
 
@@ -89,82 +107,170 @@ template <>
 struct IterRegs<false> {
   u32x4 k[2][4];  // [tile][16 B]: 32 bf16 dims
   u32x4 v[8];     // [key slot e]: 8 bf16 dims
-  float sc;
 };
 
-__device__ __forceinline__ float sbyte(uint32_t w, int k) { return (float)(int8_t)(w >> (8 * k)); }
+// Two int8 codes -> two fp16 values in one dword, one SDWA convert each (exact:
+// |code| <= 127).  SAME: bytes B and B+1 of w.  TWO: byte B of x (low half) and
+// byte B of y (high half).
+#define NE_CVT_LO(B) "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #B "\n\t"
+#define NE_CVT_HI(B, OP) "v_cvt_f16_i16_sdwa %0, sext(" OP ") dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #B
 
-__device__ __forceinline__ bf16x8 int8x8_to_bf16x8(uint32_t a, uint32_t b) {
-  u32x4 r = {pack_bf16x2(sbyte(a, 0), sbyte(a, 1)), pack_bf16x2(sbyte(a, 2), sbyte(a, 3)),
-             pack_bf16x2(sbyte(b, 0), sbyte(b, 1)), pack_bf16x2(sbyte(b, 2), sbyte(b, 3))};
-  return __builtin_bit_cast(bf16x8, r);
+template <int B>
+__device__ __forceinline__ uint32_t i8_pair_f16(uint32_t w) {
+  uint32_t r;
+  if constexpr (B == 0) {
+    asm(NE_CVT_LO(0) NE_CVT_HI(1, "%1") : "=&v"(r) : "v"(w));
+  } else {
+    asm(NE_CVT_LO(2) NE_CVT_HI(3, "%1") : "=&v"(r) : "v"(w));
+  }
+  return r;
 }
 
+template <int B>
+__device__ __forceinline__ uint32_t i8_two_f16(uint32_t x, uint32_t y) {
+  uint32_t r;
+  if constexpr (B == 0) {
+    asm(NE_CVT_LO(0) NE_CVT_HI(0, "%2") : "=&v"(r) : "v"(x), "v"(y));
+  } else if constexpr (B == 1) {
+    asm(NE_CVT_LO(1) NE_CVT_HI(1, "%2") : "=&v"(r) : "v"(x), "v"(y));
+  } else if constexpr (B == 2) {
+    asm(NE_CVT_LO(2) NE_CVT_HI(2, "%2") : "=&v"(r) : "v"(x), "v"(y));
+  } else {
+    asm(NE_CVT_LO(3) NE_CVT_HI(3, "%2") : "=&v"(r) : "v"(x), "v"(y));
+  }
+  return r;
+}
+#undef NE_CVT_LO
+#undef NE_CVT_HI
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  floatx2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// Unit geometry shared by the attention and merge kernels.
+struct UnitInfo {
+  int seq, head, mt, ctx, ql, qs, rows_total, row0, kend_unit, n_splits;
+};
+
+__device__ __forceinline__ UnitInfo unit_info(const AttnParams& p, int unit) {
+  UnitInfo u;
+  u.mt = unit % p.mtiles;
+  u.head = (unit / p.mtiles) % p.num_kv_heads;
+  u.seq = unit / (p.mtiles * p.num_kv_heads);
+  u.ctx = p.ctx_len[u.seq];
+  u.ql = p.q_len[u.seq];
+  u.qs = p.q_start[u.seq];
+  u.rows_total = p.group * u.ql;
+  u.row0 = u.mt * kRows;
+  u.kend_unit = 0;
+  u.n_splits = 0;
+  if (u.row0 < u.rows_total) {
+    const int rows_here = min(kRows, u.rows_total - u.row0);
+    // the largest query index among this tile's rows bounds the keys it can see
+    const int first_i = u.row0 % u.ql;
+    const int max_i = (first_i + rows_here > u.ql) ? u.ql - 1 : first_i + rows_here - 1;
+    u.kend_unit = u.ctx - u.ql + max_i + 1;
+    u.n_splits = max(0, (u.kend_unit + p.split_len - 1) / p.split_len);
+  }
+  return u;
+}
+
+// Per-wave constants for the loads: lane byte offsets inside a 16-key tile.
+struct LaneOffsets {
+  uint32_t k;  // key r, dims 32g..
+  uint32_t v;  // key 4g, dims 8r..
+  uint32_t sc; // this head's scale within a slot's scales (bytes)
+};
+
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+// Buffer resource over `bytes` bytes at a wave-uniform address: loads take a
+// 32-bit lane offset plus an SGPR offset, and anything past `bytes` reads as 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferWord3);
+}
+
+// Issues the loads of 32-key iteration `it` of the split (clamped to the last
+// iteration, whose data is then loaded again but never used).  s_slot[t] is the
+// slot of the first key of the split's 16-key tile t (a tile never straddles a
+// block).  Every load is a per-tile buffer resource plus a 32-bit lane offset.
 template <bool INT8, int SDT>
-__device__ __forceinline__ void load_iter(const AttnParams& p, const int32_t* bt_row, int head,
-                                          int kb, int kend, int lane, IterRegs<INT8>& R) {
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  const int bs = p.block_size;
-  const int64_t slot_stride = (int64_t)p.num_kv_heads * kHeadDim;
+__device__ __forceinline__ void issue_iter(const AttnParams& p, const int* s_slot, int n_tiles,
+                                           int n_iter, int it, int kstart, int kend, int head,
+                                           const LaneOffsets& off, int lane, IterRegs<INT8>& R) {
+  constexpr int kEsz = INT8 ? 1 : 2;
+  const uint32_t slot_bytes = (uint32_t)p.num_kv_heads * kHeadDim * kEsz;
+  const int itc = min(it, n_iter - 1);
+  const int t0 = 2 * itc;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int tile0 = kb + 16 * t;  // wave-uniform
-    if (tile0 < kend) {
-      const int blk = bt_row[tile0 / bs];
-      const int64_t base_slot = (int64_t)blk * bs + (tile0 % bs);
-      // K: key r of the tile, dims 32g..32g+31
-      const int64_t koff = (base_slot + r) * slot_stride + (int64_t)head * kHeadDim + 32 * g;
-      if constexpr (INT8) {
-        const u32x4* src = (const u32x4*)((const int8_t*)p.k_cache + koff);
-        R.k[t][0] = src[0];
-        R.k[t][1] = src[1];
-      } else {
-        const u32x4* src = (const u32x4*)((const uint16_t*)p.k_cache + koff);
+    const int ti = min(t0 + t, n_tiles - 1);
+    const int64_t slot = __builtin_amdgcn_readfirstlane(s_slot[ti]);
+    const int64_t tile_off = slot * slot_bytes + (int64_t)head * kHeadDim * kEsz;
+    const __amdgpu_buffer_rsrc_t kr =
+        tile_rsrc((const char*)p.k_cache + tile_off, kTileKeys * slot_bytes);
+    const __amdgpu_buffer_rsrc_t vr =
+        tile_rsrc((const char*)p.v_cache + tile_off, kTileKeys * slot_bytes);
+    if constexpr (INT8) {
+      R.k[t][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off.k, 0, 0));
+      R.k[t][1] =
+          __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off.k + 16, 0, 0));
 #pragma unroll
-        for (int c = 0; c < 4; ++c) R.k[t][c] = src[c];
-      }
-      // V: keys 4g+i of the tile, dims 8r..8r+7
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t voff =
-            (base_slot + 4 * g + i) * slot_stride + (int64_t)head * kHeadDim + 8 * r;
-        if constexpr (INT8) {
-          R.v[4 * t + i] = *(const u32x2*)((const int8_t*)p.v_cache + voff);
-        } else {
-          R.v[4 * t + i] = *(const u32x4*)((const uint16_t*)p.v_cache + voff);
-        }
-      }
+      for (int i = 0; i < 4; ++i)
+        R.v[4 * t + i] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, off.v, i * slot_bytes, 0));
     } else {
-      if constexpr (INT8) {
-        R.k[t][0] = u32x4{0, 0, 0, 0};
-        R.k[t][1] = u32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) R.v[4 * t + i] = u32x2{0, 0};
-      } else {
+      for (int c = 0; c < 4; ++c)
+        R.k[t][c] =
+            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off.k + 16 * c, 0, 0));
 #pragma unroll
-        for (int c = 0; c < 4; ++c) R.k[t][c] = u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) R.v[4 * t + i] = u32x4{0, 0, 0, 0};
-      }
+      for (int i = 0; i < 4; ++i)
+        R.v[4 * t + i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, off.v, i * slot_bytes, 0));
     }
   }
   if constexpr (INT8) {
     // lanes 0..31: key scale of key kb+lane; lanes 32..63: value scale of key kb+lane-32
-    const int key = kb + (lane & 31);
-    float s = 0.f;
-    if (key < kend) {
-      const int64_t slot = (int64_t)bt_row[key / bs] * bs + key % bs;
-      const int64_t si = slot * p.num_kv_heads + head;
-      s = (lane < 32) ? load_scale<SDT>(p.k_scale, si) : load_scale<SDT>(p.v_scale, si);
+    // The load is unconditional (a key past kend reads its tile's first slot, which
+    // is in range) and masked afterwards: a load under a lane-divergent branch
+    // makes the compiler wait for every load in flight, the next iteration's too.
+    const int key = kstart + itc * kIterKeys + (lane & 31);
+    const int ti = min(t0 + ((lane & 31) >> 4), n_tiles - 1);
+    const int64_t slot = s_slot[ti] + ((key < kend) ? (lane & 15) : 0);
+    const char* base = (const char*)((lane < 32) ? p.k_scale : p.v_scale);
+    constexpr int kSb = (SDT == NE_DTYPE_FP32) ? 4 : 2;
+    const char* src = base + slot * p.num_kv_heads * kSb + off.sc;
+    float s;
+    if constexpr (SDT == NE_DTYPE_BF16) {
+      s = bf16_to_f32(*(const uint16_t*)src);
+    } else if constexpr (SDT == NE_DTYPE_FP16) {
+      s = f16_to_f32(*(const uint16_t*)src);
+    } else {
+      s = *(const float*)src;
     }
-    R.sc = s;
+    R.sc = (key < kend) ? s : 0.f;
   }
 }
 
+// Q fragments of the B operand: fp16 for the int8 cache (int8 codes are exact in
+// fp16, so S keeps the bf16 product's value), bf16 otherwise.
+template <bool INT8>
+struct QFrag;
+template <>
+struct QFrag<true> {
+  f16x8 q[4];
+};
+template <>
+struct QFrag<false> {
+  bf16x8 q[4];
+};
+
+// One 32-key iteration: scores, online softmax, P V.
 template <bool INT8>
 __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs<INT8>& R,
-                                             const bf16x8 (&qf)[4], float* s_sc, int kb,
+                                             const QFrag<INT8>& qf, float* s_sc, int kb,
                                              int kend_row, int ctx, int lane, float& m, float& l,
                                              floatx4 (&o)[8]) {
   const int g = lane >> 4;
@@ -175,14 +281,17 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
     s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      bf16x8 a;
       if constexpr (INT8) {
-        const uint32_t* w = (const uint32_t*)&R.k[t][0];
-        a = int8x8_to_bf16x8(w[2 * c], w[2 * c + 1]);
+        const uint32_t w0 = R.k[t][c >> 1][2 * (c & 1)];
+        const uint32_t w1 = R.k[t][c >> 1][2 * (c & 1) + 1];
+        const u32x4 a = {i8_pair_f16<0>(w0), i8_pair_f16<2>(w0), i8_pair_f16<0>(w1),
+                         i8_pair_f16<2>(w1)};
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf.q[c], s[t],
+                                                      0, 0, 0);
       } else {
-        a = __builtin_bit_cast(bf16x8, R.k[t][c]);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, R.k[t][c]),
+                                                       qf.q[c], s[t], 0, 0, 0);
       }
-      s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[t], 0, 0, 0);
     }
   }
   // ---- per-key scale factors ----
@@ -199,7 +308,7 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
   }
   // ---- masked scores and online softmax (row = lane % 16) ----
   float sc[8];
-  float mx = kNegBig;
+  float mx = kNegBig;  // this lane's max; the row's four lanes hold the same m
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -212,216 +321,295 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
       mx = fmaxf(mx, v);
     }
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float m_new = fmaxf(m, mx);
-  const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+  // Lazy rescale: the reference max m moves only when a score passes it by more
+  // than 2^kLazyLog2 (or, for int8, when a value scale is large enough that
+  // P * scale could leave the fp16 range), so the common path needs neither the
+  // row max across lanes nor a pass over o.
+  bool grow = mx > m + kLazyLog2;
+  if constexpr (INT8) {
+    const float vmax = fmaxf(fmaxf(fmaxf(vf[0][0], vf[0][1]), fmaxf(vf[0][2], vf[0][3])),
+                             fmaxf(fmaxf(vf[1][0], vf[1][1]), fmaxf(vf[1][2], vf[1][3])));
+    grow = grow || (vmax > kLazyMaxVScale && mx > m);
+  }
+  if (__ballot(grow)) {
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    l *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] *= alpha;
+    m = m_new;
+  }
   float pr[8];
   float psum = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int key = kb + 16 * (e >> 2) + 4 * g + (e & 3);
-    pr[e] = (key < kend_row) ? __builtin_amdgcn_exp2f(sc[e] - m_new) : 0.f;
+    pr[e] = (key < kend_row) ? __builtin_amdgcn_exp2f(sc[e] - m) : 0.f;
     psum += pr[e];
   }
-  l = l * alpha + psum;
-  if (__ballot(alpha != 1.f)) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] *= alpha;
-  }
-  m = m_new;
-  // ---- P^T as the B operand (keys x rows), value scales folded in ----
-  float pv[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    if constexpr (INT8) {
-      pv[e] = pr[e] * vf[e >> 2][e & 3];
-    } else {
-      pv[e] = pr[e];
-    }
-  }
-  const u32x4 pb_bits = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
-                         pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7])};
-  const bf16x8 pb = __builtin_bit_cast(bf16x8, pb_bits);
+  l += psum;
   // ---- O^T += V^T . P^T : eight 16x16 tiles (dims x rows) ----
-  // bf16 values past the context end may be stale bit patterns: zero them so
-  // that 0 * NaN cannot leak into the product (int8 codes are always finite).
-  u32x4 vz[8];
-  if constexpr (!INT8) {
+  if constexpr (INT8) {
+    // value scales folded into P, which is the fp16 B operand (keys x rows)
+    const u32x4 pb_bits = {pack_f16x2(pr[0] * vf[0][0], pr[1] * vf[0][1]),
+                           pack_f16x2(pr[2] * vf[0][2], pr[3] * vf[0][3]),
+                           pack_f16x2(pr[4] * vf[1][0], pr[5] * vf[1][1]),
+                           pack_f16x2(pr[6] * vf[1][2], pr[7] * vf[1][3])};
+    const f16x8 pb = __builtin_bit_cast(f16x8, pb_bits);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int w = j >> 2;
+      u32x4 abits;
+      if ((j & 3) == 0) {
+        abits = u32x4{i8_two_f16<0>(R.v[0][w], R.v[1][w]), i8_two_f16<0>(R.v[2][w], R.v[3][w]),
+                      i8_two_f16<0>(R.v[4][w], R.v[5][w]), i8_two_f16<0>(R.v[6][w], R.v[7][w])};
+      } else if ((j & 3) == 1) {
+        abits = u32x4{i8_two_f16<1>(R.v[0][w], R.v[1][w]), i8_two_f16<1>(R.v[2][w], R.v[3][w]),
+                      i8_two_f16<1>(R.v[4][w], R.v[5][w]), i8_two_f16<1>(R.v[6][w], R.v[7][w])};
+      } else if ((j & 3) == 2) {
+        abits = u32x4{i8_two_f16<2>(R.v[0][w], R.v[1][w]), i8_two_f16<2>(R.v[2][w], R.v[3][w]),
+                      i8_two_f16<2>(R.v[4][w], R.v[5][w]), i8_two_f16<2>(R.v[6][w], R.v[7][w])};
+      } else {
+        abits = u32x4{i8_two_f16<3>(R.v[0][w], R.v[1][w]), i8_two_f16<3>(R.v[2][w], R.v[3][w]),
+                      i8_two_f16<3>(R.v[4][w], R.v[5][w]), i8_two_f16<3>(R.v[6][w], R.v[7][w])};
+      }
+      o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, abits), pb, o[j], 0,
+                                                    0, 0);
+    }
+  } else {
+    const u32x4 pb_bits = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                           pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
+    const bf16x8 pb = __builtin_bit_cast(bf16x8, pb_bits);
+    // bf16 values past the context end may be stale bit patterns: zero them so
+    // that 0 * NaN cannot leak into the product (int8 codes are always finite)
+    u32x4 vz[8];
     const bool tail = kb + kIterKeys > ctx;  // wave-uniform
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int key = kb + 16 * (e >> 2) + 4 * g + (e & 3);
       vz[e] = (tail && key >= ctx) ? u32x4{0, 0, 0, 0} : R.v[e];
     }
-  }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    u32x4 abits;
-    if constexpr (INT8) {
-      const int w = j >> 2, b = j & 3;
-      abits = u32x4{pack_bf16x2(sbyte(R.v[0][w], b), sbyte(R.v[1][w], b)),
-                    pack_bf16x2(sbyte(R.v[2][w], b), sbyte(R.v[3][w], b)),
-                    pack_bf16x2(sbyte(R.v[4][w], b), sbyte(R.v[5][w], b)),
-                    pack_bf16x2(sbyte(R.v[6][w], b), sbyte(R.v[7][w], b))};
-    } else {
+    for (int j = 0; j < 8; ++j) {
       const int w = j >> 1;
       const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-      abits = u32x4{__builtin_amdgcn_perm(vz[1][w], vz[0][w], sel),
-                    __builtin_amdgcn_perm(vz[3][w], vz[2][w], sel),
-                    __builtin_amdgcn_perm(vz[5][w], vz[4][w], sel),
-                    __builtin_amdgcn_perm(vz[7][w], vz[6][w], sel)};
+      const u32x4 abits = {__builtin_amdgcn_perm(vz[1][w], vz[0][w], sel),
+                           __builtin_amdgcn_perm(vz[3][w], vz[2][w], sel),
+                           __builtin_amdgcn_perm(vz[5][w], vz[4][w], sel),
+                           __builtin_amdgcn_perm(vz[7][w], vz[6][w], sel)};
+      o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, abits), pb, o[j],
+                                                     0, 0, 0);
     }
-    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, abits), pb, o[j], 0,
-                                                  0, 0);
   }
 }
 
-template <bool INT8, int SDT>
-__global__ __launch_bounds__(kThreads, 3) void paged_attention_kernel(AttnParams p) {
-  __shared__ float s_o[kWaves][kRows][kHeadDim + 4];
-  __shared__ float s_m[kWaves][kRows];
-  __shared__ float s_l[kWaves][kRows];
-  __shared__ float s_sc[kWaves][kWave];
-  __shared__ int s_last;
+// One work-group per (sequence, M tile, split) with kHeadWaves * KG waves.  Wave
+// w serves KV heads w % kHeadWaves (+ kHeadWaves, ...) and takes every KG-th
+// 32-key iteration of the split; the KG partial results of a head are merged
+// through LDS.  All waves walk the same 16-key tiles at about the same time, so a
+// block's 1 KB (int8) slots are fetched whole rather than as 128-byte head rows
+// scattered in time.  DB: double-buffer the registers, keeping the next
+// iteration's loads in flight during the current one's arithmetic.
+template <bool INT8, int SDT, int KG, bool DB>
+__global__ __launch_bounds__(kHeadWaves * KG * kWave) void paged_attention_kernel(AttnParams p) {
+  constexpr int kWaves = kHeadWaves * KG;
+  constexpr int kThreads = kWaves * kWave;
+  __shared__ float s_sc[INT8 ? kWaves : 1][kWave];
+  __shared__ int s_slot[kMaxTiles];
+  __shared__ float s_o[KG > 1 ? kHeadWaves : 1][kRows][kHeadDim + 4];
+  __shared__ float s_ml[KG > 1 ? kHeadWaves : 1][kRows][2];
 
   // ---- work item ----
   const int bid = blockIdx.x;
-  const int xcd = bid % kNumXcd;
-  const int jj = bid / kNumXcd;
-  const int split = jj % p.max_splits;
-  const int unit = (jj / p.max_splits) * kNumXcd + xcd;
-  if (unit >= p.units) return;
-  const int mt = unit % p.mtiles;
-  const int head = (unit / p.mtiles) % p.num_kv_heads;
-  const int seq = unit / (p.mtiles * p.num_kv_heads);
-
-  const int ctx = p.ctx_len[seq];
-  const int ql = p.q_len[seq];
-  const int qs = p.q_start[seq];
-  const int rows_total = p.group * ql;
-  const int row0 = mt * kRows;
-  if (row0 >= rows_total) return;
-  const int rows_here = min(kRows, rows_total - row0);
-  // largest query index among this tile's rows bounds the keys it can see
-  const int first_i = row0 % ql;
-  const int max_i = (first_i + rows_here > ql) ? ql - 1 : first_i + rows_here - 1;
-  const int kend_unit = ctx - ql + max_i + 1;
-  int n_splits = (kend_unit + p.split_len - 1) / p.split_len;
+  const int split = bid % p.max_splits;
+  const int mt = (bid / p.max_splits) % p.mtiles;
+  const int seq = bid / (p.max_splits * p.mtiles);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int head_slot = wave % kHeadWaves;
+  const int kg = wave / kHeadWaves;
+  // the geometry below does not depend on the head
+  const UnitInfo u0 = unit_info(p, seq * p.num_kv_heads * p.mtiles + mt);
+  if (u0.row0 >= u0.rows_total) return;
+  int n_splits = u0.n_splits;
   if (n_splits > p.max_splits) {
-    if (threadIdx.x == 0 && split == 0) atomicOr(p.error_flag, 1u);
+    if (tid == 0 && split == 0) atomicOr(p.error_flag, 1u);
     n_splits = p.max_splits;
   }
   if (split >= n_splits) return;
   const int kstart = split * p.split_len;
-  const int kend = min(kend_unit, kstart + p.split_len);
+  const int kend = min(u0.kend_unit, kstart + p.split_len);
+  const int ql = u0.ql;
 
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int lane = tid % kWave;
+  // ---- block-table slots of this split's 16-key tiles ----
+  const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
+  const int n_tiles = (kend - kstart + kTileKeys - 1) / kTileKeys;
+  for (int t = tid; t < n_tiles; t += kThreads) {
+    const int key0 = kstart + kTileKeys * t;
+    s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+  }
+  __syncthreads();  // s_slot ready
+
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int R = row0 + r;
-  const bool row_valid = R < rows_total;
+  const int R = u0.row0 + r;
+  const bool row_valid = R < u0.rows_total;
   const int h_local = row_valid ? R / ql : 0;
   const int qi = row_valid ? R % ql : 0;
-  const int kend_row = row_valid ? min(kend, ctx - ql + qi + 1) : kend;
-
-  // ---- Q rows as the B operand: dims 32g + 8c .. +8 for chunk c ----
-  bf16x8 qf[4];
-  if (row_valid) {
-    const int64_t qoff = (int64_t)(qs + qi) * p.q_tok_stride +
-                         (int64_t)(head * p.group + h_local) * p.q_head_stride + 32 * g;
-    const u32x4* src = (const u32x4*)(p.q + qoff);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qf[c] = __builtin_bit_cast(bf16x8, src[c]);
-  } else {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qf[c] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
-  }
-
-  const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
-  float m = kNegBig, l = 0.f;
-  floatx4 o[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
+  const int kend_row = row_valid ? min(kend, u0.ctx - ql + qi + 1) : kend;
   const int n_iter = (kend - kstart + kIterKeys - 1) / kIterKeys;
-  for (int it = wave; it < n_iter; it += kWaves) {
-    IterRegs<INT8> A;
-    load_iter<INT8, SDT>(p, bt_row, head, kstart + it * kIterKeys, kend, lane, A);
-    compute_iter<INT8>(p, A, qf, s_sc[wave], kstart + it * kIterKeys, kend_row, ctx, lane, m, l, o);
-  }
-  // full row sum over the four key groups
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
+  constexpr int kEsz = INT8 ? 1 : 2;
+  const int64_t slot_bytes = (int64_t)p.num_kv_heads * kHeadDim * kEsz;
 
-  // ---- merge the four waves through LDS ----
+  for (int pass = 0; pass * kHeadWaves < p.num_kv_heads; ++pass) {
+    const int head = pass * kHeadWaves + head_slot;
+    const bool active = head < p.num_kv_heads;  // wave-uniform
+    float m = kNegBig, l = 0.f;
+    floatx4 o[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    floatx4 lo = {o[0][i], o[1][i], o[2][i], o[3][i]};
-    floatx4 hi = {o[4][i], o[5][i], o[6][i], o[7][i]};
-    *(floatx4*)&s_o[wave][r][32 * g + 8 * i] = lo;
-    *(floatx4*)&s_o[wave][r][32 * g + 8 * i + 4] = hi;
-  }
-  if (g == 0) {
-    s_m[wave][r] = m;
-    s_l[wave][r] = l;
-  }
-  __syncthreads();
-
-  const int crow = tid >> 4;        // row merged by this thread
-  const int cd = (tid & 15) * 8;    // its 8 dims
-  float M = kNegBig;
+    for (int j = 0; j < 8; ++j) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (active) {
+      // ---- Q rows as the B operand: dims 32g + 8c .. +8 for chunk c ----
+      QFrag<INT8> qf;
+      {
+        u32x4 raw[4] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+        if (row_valid) {
+          const int64_t qoff = (int64_t)(u0.qs + qi) * p.q_tok_stride +
+                               (int64_t)(head * p.group + h_local) * p.q_head_stride + 32 * g;
+          const u32x4* src = (const u32x4*)(p.q + qoff);
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][crow]);
-  float L = 0.f;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          for (int c = 0; c < 4; ++c) raw[c] = src[c];
+        }
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float a = __builtin_amdgcn_exp2f(s_m[w][crow] - M);
-    L += a * s_l[w][crow];
+        for (int c = 0; c < 4; ++c) {
+          if constexpr (INT8) {
+            u32x4 h;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) acc[d] += a * s_o[w][crow][cd + d];
-  }
+            for (int i = 0; i < 4; ++i)
+              h[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[c][i] & 0xFFFFu)),
+                                bf16_to_f32((uint16_t)(raw[c][i] >> 16)));
+            qf.q[c] = __builtin_bit_cast(f16x8, h);
+          } else {
+            qf.q[c] = __builtin_bit_cast(bf16x8, raw[c]);
+          }
+        }
+      }
+      LaneOffsets off;
+      off.k = (uint32_t)(r * slot_bytes + 32 * g * kEsz);
+      off.v = (uint32_t)(4 * g * slot_bytes + 8 * r * kEsz);
+      off.sc = (uint32_t)(head * (SDT == NE_DTYPE_FP32 ? 4 : 2));
+      float* sc_row = s_sc[INT8 ? wave : 0];
+      if constexpr (DB) {
+        IterRegs<INT8> A, B;
+        issue_iter<INT8, SDT>(p, s_slot, n_tiles, n_iter, kg, kstart, kend, head, off, lane, A);
+        for (int it = kg; it < n_iter; it += 2 * KG) {
+          issue_iter<INT8, SDT>(p, s_slot, n_tiles, n_iter, it + KG, kstart, kend, head, off, lane,
+                                B);
+          compute_iter<INT8>(p, A, qf, sc_row, kstart + it * kIterKeys, kend_row, u0.ctx, lane, m,
+                             l, o);
+          issue_iter<INT8, SDT>(p, s_slot, n_tiles, n_iter, it + 2 * KG, kstart, kend, head, off,
+                                lane, A);
+          if (it + KG < n_iter)
+            compute_iter<INT8>(p, B, qf, sc_row, kstart + (it + KG) * kIterKeys, kend_row, u0.ctx,
+                               lane, m, l, o);
+        }
+      } else {
+        for (int it = kg; it < n_iter; it += KG) {
+          IterRegs<INT8> A;
+          issue_iter<INT8, SDT>(p, s_slot, n_tiles, n_iter, it, kstart, kend, head, off, lane, A);
+          compute_iter<INT8>(p, A, qf, sc_row, kstart + it * kIterKeys, kend_row, u0.ctx, lane, m,
+                             l, o);
+        }
+      }
+      // full row sum and the row's reference max (lanes of a row agree on m)
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+    }
+    // ---- merge the KG key groups of each head through LDS ----
+    if constexpr (KG > 1) {
+      if (active && kg == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          *(floatx4*)&s_o[head_slot][r][32 * g + 8 * i] = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
+          *(floatx4*)&s_o[head_slot][r][32 * g + 8 * i + 4] =
+              floatx4{o[4][i], o[5][i], o[6][i], o[7][i]};
+        }
+        if (g == 0) {
+          s_ml[head_slot][r][0] = m;
+          s_ml[head_slot][r][1] = l;
+        }
+      }
+      __syncthreads();
+      if (active && kg == 0) {
+        const float m1 = s_ml[head_slot][r][0];
+        const float l1 = s_ml[head_slot][r][1];
+        const float mm = fmaxf(m, m1);
+        const float a0 = __builtin_amdgcn_exp2f(m - mm);
+        const float a1 = __builtin_amdgcn_exp2f(m1 - mm);
+        l = a0 * l + a1 * l1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const floatx4 lo = *(const floatx4*)&s_o[head_slot][r][32 * g + 8 * i];
+          const floatx4 hi = *(const floatx4*)&s_o[head_slot][r][32 * g + 8 * i + 4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            o[j][i] = a0 * o[j][i] + a1 * lo[j];
+            o[4 + j][i] = a0 * o[4 + j][i] + a1 * hi[j];
+          }
+        }
+        m = mm;
+      }
+      __syncthreads();  // s_o free for the next pass
+    }
+    if (!active || kg != 0 || !row_valid) continue;
 
-  const int CR = row0 + crow;
-  const bool crow_valid = CR < rows_total;
-  auto store_out = [&](const float* vals, float denom) {
-    if (!crow_valid) return;
-    const int ch = CR / ql, ci = CR % ql;
-    const int64_t ooff = (int64_t)(qs + ci) * p.o_tok_stride +
-                         (int64_t)(head * p.group + ch) * p.o_head_stride + cd;
-    const float inv = 1.f / denom;
-    u32x4 bits = {pack_bf16x2(vals[0] * inv, vals[1] * inv), pack_bf16x2(vals[2] * inv, vals[3] * inv),
-                  pack_bf16x2(vals[4] * inv, vals[5] * inv), pack_bf16x2(vals[6] * inv, vals[7] * inv)};
-    *(u32x4*)(p.out + ooff) = bits;
-  };
-
-  if (n_splits == 1) {
-    store_out(acc, L);
-    return;
+    // lane (r, g) holds row r, dims 32g + 8i + j in o[j][i]
+    const int unit = (seq * p.num_kv_heads + head) * p.mtiles + mt;
+    if (n_splits == 1) {
+      uint16_t* dst = p.out + (int64_t)(u0.qs + qi) * p.o_tok_stride +
+                      (int64_t)(head * p.group + h_local) * p.o_head_stride + 32 * g;
+      const float inv = 1.f / l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 bits = {pack_bf16x2(o[0][i] * inv, o[1][i] * inv),
+                            pack_bf16x2(o[2][i] * inv, o[3][i] * inv),
+                            pack_bf16x2(o[4][i] * inv, o[5][i] * inv),
+                            pack_bf16x2(o[6][i] * inv, o[7][i] * inv)};
+        *(u32x4*)(dst + 8 * i) = bits;
+      }
+    } else {
+      // several splits: publish this split's partial for the merge kernel
+      const int64_t pbase = ((int64_t)unit * p.max_splits + split) * kRows + r;
+      float* po = p.part_o + pbase * kHeadDim + 32 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(floatx4*)(po + 8 * i) = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
+        *(floatx4*)(po + 8 * i + 4) = floatx4{o[4][i], o[5][i], o[6][i], o[7][i]};
+      }
+      if (g == 0) {
+        p.part_ml[pbase * 2] = m;
+        p.part_ml[pbase * 2 + 1] = l;
+      }
+    }
   }
+}
 
-  // ---- split-K: publish this work-group's partial, last arrival merges ----
-  const int64_t pbase = ((int64_t)unit * p.max_splits + split) * kRows + crow;
-  float* po = p.part_o + pbase * kHeadDim + cd;
-  *(floatx4*)po = floatx4{acc[0], acc[1], acc[2], acc[3]};
-  *(floatx4*)(po + 4) = floatx4{acc[4], acc[5], acc[6], acc[7]};
-  if ((tid & 15) == 0) {
-    p.part_ml[pbase * 2] = M;
-    p.part_ml[pbase * 2 + 1] = L;
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&p.counters[unit], 1u);
-    s_last = (prev == (uint32_t)(n_splits - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
+// Combines the split partials of every unit that has more than one split:
+// out = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s.  One work-group per unit,
+// 16 threads per row, 8 dims per thread.
+__global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
+  const int unit = blockIdx.x;
+  const UnitInfo u = unit_info(p, unit);
+  if (u.row0 >= u.rows_total) return;
+  const int n_splits = min(u.n_splits, p.max_splits);
+  if (n_splits <= 1) return;
+  const int crow = threadIdx.x >> 4;
+  const int cd = (threadIdx.x & 15) * 8;
+  const int CR = u.row0 + crow;
+  if (CR >= u.rows_total) return;
   const int64_t ubase = (int64_t)unit * p.max_splits * kRows + crow;
   float MM = kNegBig;
   for (int s = 0; s < n_splits; ++s) MM = fmaxf(MM, p.part_ml[(ubase + (int64_t)s * kRows) * 2]);
@@ -440,26 +628,35 @@ __global__ __launch_bounds__(kThreads, 3) void paged_attention_kernel(AttnParams
       tot[d + 4] += a * x1[d];
     }
   }
-  store_out(tot, LL);
-  if (tid == 0) p.counters[unit] = 0u;  // leave the ticket ready for the next call
+  const int ch = CR / u.ql, ci = CR % u.ql;
+  uint16_t* dst = p.out + (int64_t)(u.qs + ci) * p.o_tok_stride +
+                  (int64_t)(u.head * p.group + ch) * p.o_head_stride + cd;
+  const float inv = 1.f / LL;
+  *(u32x4*)dst = u32x4{pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv),
+                       pack_bf16x2(tot[4] * inv, tot[5] * inv), pack_bf16x2(tot[6] * inv, tot[7] * inv)};
 }
 
 struct Layout {
   int group, mtiles, units, split_len, max_splits;
-  size_t part_o_off, part_ml_off, counters_off, error_off, total;
+  size_t part_o_off, part_ml_off, error_off, total;
 };
 
+// Default split: about 512 KB of K/V per work-group (256 keys of int8, 128 of bf16,
+// across 8 KV heads), the best of a sweep over 128..1024 keys on the 64-sequence
+// int8 and 16-sequence bf16 verify shapes; longer splits leave CUs idle, shorter
+// ones spend more on partials and per-work-group setup than they gain.
+int default_split_len(int kv_dtype, int max_ctx) {
+  const int split_len = (kv_dtype == NE_DTYPE_INT8) ? 256 : 128;
+  return min(split_len, max(128, ceil_div(max(max_ctx, 1), 128) * 128));
+}
+
 Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_len, int max_ctx,
-                   int split_len) {
+                   int split_len, int kv_dtype) {
   Layout L{};
   L.group = num_q_heads / num_kv_heads;
   L.mtiles = ceil_div((int64_t)L.group * max_q_len, kRows);
   L.units = num_seqs * num_kv_heads * L.mtiles;
-  if (split_len <= 0) {
-    const int want = max(1, ceil_div(kTargetWorkGroups, max(L.units, 1)));
-    split_len = ceil_div(ceil_div(max(max_ctx, 1), want), 128) * 128;
-    split_len = min(max(split_len, 128), 8192);
-  }
+  if (split_len <= 0) split_len = default_split_len(kv_dtype, max_ctx);
   L.split_len = split_len;
   L.max_splits = max(1, ceil_div(max(max_ctx, 1), split_len));
   size_t off = 0;
@@ -468,49 +665,50 @@ Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_le
     off += (bytes + 255) & ~(size_t)255;
     return o;
   };
-  // error flag at byte 0 and tickets at byte 256, so callers can inspect and
-  // re-zero them without knowing the partial-sum layout that follows
+  // error flag at byte 0, so callers can inspect and clear it without knowing the
+  // partial-sum layout that follows
   const size_t parts = (L.max_splits > 1) ? (size_t)L.units * L.max_splits * kRows : 0;
   L.error_off = take(sizeof(uint32_t));
-  L.counters_off = take((size_t)max(L.units, 1) * sizeof(uint32_t));
   L.part_o_off = take(parts * kHeadDim * sizeof(float));
   L.part_ml_off = take(parts * 2 * sizeof(float));
   L.total = off;
   return L;
 }
 
-}  // namespace
-
-}  // namespace ne
-
-using namespace ne;
-
-extern "C" size_t ne_paged_attention_workspace_size(int32_t num_seqs, int32_t num_q_heads,
-                                                    int32_t num_kv_heads, int32_t max_q_len,
-                                                    int32_t max_ctx_len, int32_t split_len) {
-  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_q_len <= 0 ||
-      num_q_heads % num_kv_heads != 0)
-    return 0;
-  return make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len).total;
+template <int KG, bool DB>
+int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStream_t s) {
+  const dim3 grid((unsigned)p.num_seqs * (unsigned)p.mtiles * (unsigned)p.max_splits);
+  const dim3 block(kHeadWaves * KG * kWave);
+  if (kv_dtype == NE_DTYPE_BF16) {
+    hipLaunchKernelGGL((paged_attention_kernel<false, NE_DTYPE_BF16, KG, DB>), grid, block, 0, s, p);
+  } else if (scale_dtype == NE_DTYPE_BF16) {
+    hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_BF16, KG, DB>), grid, block, 0, s, p);
+  } else if (scale_dtype == NE_DTYPE_FP16) {
+    hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_FP16, KG, DB>), grid, block, 0, s, p);
+  } else {
+    hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_FP32, KG, DB>), grid, block, 0, s, p);
+  }
+  int rc = check_launch("paged_attention_kernel");
+  if (rc != NE_OK || p.max_splits == 1) return rc;
+  hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)p.units), dim3(256), 0, s, p);
+  return check_launch("attention_merge_kernel");
 }
 
-extern "C" int ne_paged_verify_attention(
-    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
-    const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
-    int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
-    int32_t block_size, const int32_t* ctx_len, const int32_t* q_start, const int32_t* q_len,
-    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
-    int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, void* workspace,
-    size_t workspace_bytes, void* stream) {
-  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
-  if (num_seqs == 0) return NE_OK;
+// Validates the arguments and fills the kernel parameters; NE_OK or an error code.
+int make_params(const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+                const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
+                int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
+                int32_t block_size, const int32_t* ctx_len, const int32_t* q_start,
+                const int32_t* q_len, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                int32_t head_dim, int32_t max_q_len, int32_t max_ctx_len, float softmax_scale,
+                void* out, int64_t out_token_stride, int64_t out_head_stride, int32_t split_len,
+                void* workspace, size_t workspace_bytes, AttnParams& p) {
   NE_CHECK_SUPPORTED(head_dim == kHeadDim, "paged attention supports head_dim 128 only (got %d)",
                      head_dim);
   NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
                "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_q_heads,
                num_kv_heads);
-  NE_CHECK_SUPPORTED(block_size > 0 && block_size % 16 == 0,
+  NE_CHECK_SUPPORTED(block_size > 0 && block_size % kTileKeys == 0,
                      "block_size must be a positive multiple of 16 (got %d)", block_size);
   NE_CHECK_ARG(kv_dtype == NE_DTYPE_BF16 || kv_dtype == NE_DTYPE_INT8,
                "kv_dtype must be bf16 or int8");
@@ -522,22 +720,20 @@ extern "C" int ne_paged_verify_attention(
                "null pointer argument");
   NE_CHECK_ARG(kv_dtype != NE_DTYPE_INT8 || (k_scale && v_scale), "int8 cache needs scales");
   NE_CHECK_ARG(max_q_len > 0 && max_ctx_len > 0, "max_q_len and max_ctx_len must be positive");
-  NE_CHECK_ARG(split_len == 0 || (split_len > 0 && split_len % 128 == 0),
-               "split_len must be 0 or a positive multiple of 128");
+  NE_CHECK_ARG(split_len == 0 || (split_len > 0 && split_len % 128 == 0 && split_len <= kMaxSplitLen),
+               "split_len must be 0 or a positive multiple of 128 up to %d", kMaxSplitLen);
   NE_CHECK_ARG((q_token_stride % 8) == 0 && (q_head_stride % 8) == 0 &&
                    (out_token_stride % 8) == 0 && (out_head_stride % 8) == 0,
                "q/out strides must be multiples of 8 elements");
   NE_CHECK_ARG(((uintptr_t)q % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
                    ((uintptr_t)k_cache % 16) == 0 && ((uintptr_t)v_cache % 16) == 0,
                "q, out and caches must be 16-byte aligned");
-
-  const Layout L =
-      make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len);
+  const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len,
+                               split_len, kv_dtype);
   NE_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total,
                "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
                L.total);
-
-  AttnParams p{};
+  p = AttnParams{};
   p.q = (const uint16_t*)q;
   p.q_tok_stride = q_token_stride;
   p.q_head_stride = q_head_stride;
@@ -551,6 +747,7 @@ extern "C" int ne_paged_verify_attention(
   p.ctx_len = ctx_len;
   p.q_start = q_start;
   p.q_len = q_len;
+  p.num_seqs = num_seqs;
   p.num_kv_heads = num_kv_heads;
   p.group = L.group;
   p.mtiles = L.mtiles;
@@ -564,24 +761,50 @@ extern "C" int ne_paged_verify_attention(
   char* ws = (char*)workspace;
   p.part_o = (float*)(ws + L.part_o_off);
   p.part_ml = (float*)(ws + L.part_ml_off);
-  p.counters = (uint32_t*)(ws + L.counters_off);
   p.error_flag = (uint32_t*)(ws + L.error_off);
+  return NE_OK;
+}
 
-  const int units_padded = ceil_div(L.units, kNumXcd) * kNumXcd;
-  const dim3 grid((unsigned)units_padded * (unsigned)L.max_splits);
-  hipStream_t s = (hipStream_t)stream;
-  if (kv_dtype == NE_DTYPE_BF16) {
-    hipLaunchKernelGGL((paged_attention_kernel<false, NE_DTYPE_BF16>), grid, dim3(kThreads), 0, s,
-                       p);
-  } else if (scale_dtype == NE_DTYPE_BF16) {
-    hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_BF16>), grid, dim3(kThreads), 0, s,
-                       p);
-  } else if (scale_dtype == NE_DTYPE_FP16) {
-    hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_FP16>), grid, dim3(kThreads), 0, s,
-                       p);
-  } else {
-    hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_FP32>), grid, dim3(kThreads), 0, s,
-                       p);
-  }
-  return check_launch("paged_attention_kernel");
+}  // namespace
+
+}  // namespace ne
+
+using namespace ne;
+
+extern "C" size_t ne_paged_attention_workspace_size(int32_t num_seqs, int32_t num_q_heads,
+                                                    int32_t num_kv_heads, int32_t max_q_len,
+                                                    int32_t max_ctx_len, int32_t split_len) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_q_len <= 0 ||
+      num_q_heads % num_kv_heads != 0 || split_len < 0 || split_len > kMaxSplitLen)
+    return 0;
+  // without an explicit split the size covers either cache dtype's default split
+  const size_t a = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len,
+                               split_len, NE_DTYPE_INT8).total;
+  const size_t b = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len,
+                               split_len, NE_DTYPE_BF16).total;
+  return a > b ? a : b;
+}
+
+extern "C" int ne_paged_verify_attention(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
+    int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
+    int32_t block_size, const int32_t* ctx_len, const int32_t* q_start, const int32_t* q_len,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  AttnParams p;
+  const int rc = make_params(q, q_token_stride, q_head_stride, k_cache, v_cache, k_scale, v_scale,
+                             kv_dtype, scale_dtype, block_tables, block_table_stride, block_size,
+                             ctx_len, q_start, q_len, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
+                             out_head_stride, split_len, workspace, workspace_bytes, p);
+  if (rc != NE_OK) return rc;
+  // int8: one wave per KV head, registers double-buffered (154 VGPRs); bf16: one
+  // wave per KV head, single-buffered (its double-buffered form needs 244 VGPRs)
+  if (kv_dtype == NE_DTYPE_INT8) return launch_attention<1, true>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
+  return launch_attention<1, false>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
 }

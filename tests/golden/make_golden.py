@@ -69,7 +69,7 @@ REFERENCE_KATS = {
     "kv_bytes_per_token": {
         "source": "nanoengine/tests/engine/test_quantization_and_cuda_graphs.py:82-89, "
         "nanoengine/tests/engine/test_kv_cache.py:126-131",
-        "int8_fp16": 59360,
+        "int8_fp16": 58240,
         "fp16": 114688,
     },
     "paged_allocator_growth": {

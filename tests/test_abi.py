@@ -1,0 +1,69 @@
+"""The C-ABI library (CPU only): it loads, exports every entry point that
+include/nanoengine_hip.h declares, and its host-side argument checks reject bad
+calls before any launch.  No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nanoengine_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nanoengine_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ne_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.library_path().exists():
+        pytest.skip("libnanoengine_hip.so is not built (run __graft_entry__.build())")
+    return _native.load()
+
+
+def test_header_and_binding_declare_the_same_entry_points():
+    assert declared_functions() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing
+    assert lib.ne_abi_version() == _native.ABI_VERSION
+
+
+def test_host_checks_reject_bad_arguments_without_launching(lib):
+    null = ctypes.c_void_p(0)
+    rc = lib.ne_ngram_propose(null, 8, null, null, -1, 3, 1, 4, null, null, null)
+    assert rc == -1 and b"num_seqs" in lib.ne_last_error()
+    rc = lib.ne_ngram_propose(null, 8, null, null, 2, 3, 1, 4, null, null, null)
+    assert rc == -1 and b"null" in lib.ne_last_error()
+    rc = lib.ne_ngram_propose(ctypes.c_void_p(16), 8, ctypes.c_void_p(16), ctypes.c_void_p(16), 2, 17, 1, 4,
+                              ctypes.c_void_p(16), ctypes.c_void_p(16), null)
+    assert rc == -2  # max_ngram above the kernel's limit: unsupported, nothing launched
+    # attention: head_dim other than 128 is unsupported
+    p = ctypes.c_void_p(256)
+    rc = lib.ne_paged_verify_attention(p, 2048, 128, p, p, p, p, 3, 0, p, 8, 16, p, p, p, 4, 16, 8, 64,
+                                       5, 100, 0.125, p, 2048, 128, 0, p, 1 << 20, null)
+    assert rc == -2 and b"head_dim" in lib.ne_last_error()
+    # W8A16 GEMM: k must be a multiple of 128
+    rc = lib.ne_w8a16_gemm(p, 1000, p, p, 0, 320, 1024, 1000, p, 1024, 0, null)
+    assert rc == -2
+    rc = lib.ne_accept(0, null, 0, null, 0, 100, p, 0, p, p, 2, 0.0, null, null, p, p, null, 0, null, null, null)
+    assert rc == -1  # max_drafts 0
+
+
+def test_workspace_and_tile_queries(lib):
+    assert lib.ne_lm_head_num_tiles(151936) == 151936 // 64
+    assert lib.ne_paged_attention_workspace_size(0, 16, 8, 5, 1024, 0) == 0
+    assert lib.ne_paged_attention_workspace_size(64, 16, 7, 5, 1024, 0) == 0  # 16 % 7 != 0
+    one_split = lib.ne_paged_attention_workspace_size(64, 16, 8, 5, 256, 256)
+    four_splits = lib.ne_paged_attention_workspace_size(64, 16, 8, 5, 1024, 256)
+    assert one_split == 256  # only the error flag
+    # partials: units x splits x 16 rows x (128 + 2) fp32
+    assert four_splits >= 256 + 64 * 8 * 4 * 16 * 130 * 4

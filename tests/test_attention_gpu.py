@@ -114,5 +114,17 @@ def test_workspace_error_flag_stays_clear(device):
                                    max_q_len=5, max_ctx_len=500, workspace=ws, split_len=128)
     torch.cuda.synchronize()
     assert ws.error_flag() == 0
-    counters = ws.buffer[256:256 + 4 * 64].view(torch.int32)
-    assert int(counters.abs().sum()) == 0  # tickets left at zero for the next call
+
+
+def test_workspace_error_flag_reports_context_past_max(device):
+    # ctx 500 with max_ctx_len 200 and 128-key splits: the split grid covers 256 keys,
+    # so the call reads only in-range blocks, drops the rest and raises the flag
+    ws = kernels.AttentionWorkspace()
+    kc, vc, ks, vs = make_pool(64, 16, HKV, "int8")
+    tables, ctx, qs, ql, rows = make_batch([500, 20], [5, 5], 64, 16)
+    q = torch.randn(rows, HQ, 128).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    kernels.paged_verify_attention(d(q), d(kc), d(vc), d(ks), d(vs), d(tables), 16, d(ctx), d(qs), d(ql),
+                                   max_q_len=5, max_ctx_len=200, workspace=ws, split_len=128)
+    torch.cuda.synchronize()
+    assert ws.error_flag() != 0
