@@ -1,13 +1,13 @@
 #!/usr/bin/env python
 """Benchmark of the speculative-decoding verify step on one MI355X.
 
-Workload (the full-verify-step configuration): Qwen3-0.6B architecture (28
-layers, hidden 1024, 16 Q / 8 KV heads, head_dim 128, MLP 3072, vocab 151936,
-tied embeddings), random-init weights (every parameter N(0, 0.02^2), seed 0, in
-the reference's registration order) cast to bf16 and quantised per output row
-to int8, int8 paged KV (16-token blocks, bf16 scales), 64 sequences whose
-64-token prompts repeat a seeded 16-token motif of ids in [0, 512) four times,
-n-gram (n <= 3) drafting with k = 4, greedy verification, 128 output tokens per
+Workload (the full verify step): Qwen3-0.6B architecture (28 layers, hidden
+1024, 16 Q / 8 KV heads, head_dim 128, MLP 3072, vocab 151936, tied
+embeddings), random-init weights (every parameter N(0, 0.02^2), seed 0, in the
+reference's registration order) cast to bf16 and quantised per output row to
+int8, int8 paged KV (16-token blocks, bf16 scales), 64 sequences whose 64-token
+prompts repeat a seeded 16-token motif of ids in [0, 512) four times, n-gram
+(n <= 3) drafting with k = 4, greedy verification, 128 output tokens per
 sequence.  Synthetic data: no checkpoint or dataset is read.
 
 One step = one batched verify step over the 64 sequences (draft, reserve KV,
@@ -16,24 +16,35 @@ K timed steps bracketed by device synchronisation; ``value`` is accepted tokens
 per second (tokens emitted by the timed steps / elapsed).
 
 Also reported on the same line:
-  roofline      the dominant kernel's algorithmic bytes (or flops) per launch over
-                its average launch time, from HIP events around each launch in
-                the timed region (eager launches; see --graph)
-  attention     the paged verify attention at the kernel-only int8 configuration
-                (64 sequences, context U{128..1024}, 5 queries, fp16 scales,
-                4096-block pool) over 28 distinct layer pools
-  cpu_baseline  the oracle's restatement of the reference CPU path (fp32, batch 1,
-                64-token motif prompt, n-gram k = 4, greedy, 128 tokens,
-                contiguous KV) on this host's cores
+  roofline       the paged verify attention (the kernel the metric's GB/s names)
+                 at the kernel-only int8 configuration: 64 sequences, context
+                 U{128..1024} (seed 1), 5 queries, fp16 scales, a 4096-block pool,
+                 28 distinct layer pools so the last-level cache cannot hold them.
+                 achieved = algorithmic bytes per launch / average launch time from
+                 HIP events on the launching stream; traffic = HBM bytes per launch
+                 from two rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each
+                 scaled by what the counter reads for a 256 MiB copy.
+  gemm           the W8A16 projection GEMMs of the verify step (MFMA roofline)
+  torch_baseline the reference's verify step composed from its own PyTorch ops on
+                 this GPU (dequantise-then-linear, gather + dequant + masked GQA
+                 attention, logits on every row, a per-sequence verify loop with
+                 host syncs), batched over the same 64 sequences
+  cpu_baseline   the oracle's restatement of the reference CPU path (fp32, batch 1,
+                 64-token motif prompt, n-gram k = 4, greedy, 128 tokens,
+                 contiguous KV) on this host's cores
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import math
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -49,6 +60,7 @@ PROMPT_REPEATS = 4
 OUTPUT_TOKENS = 128
 NUM_SEQS = 64
 K_DRAFT = 4
+CALIBRATION_BYTES = 256 << 20
 
 
 def log(msg: str) -> None:
@@ -104,8 +116,7 @@ def run_verify(args, torch):
     log("prefill done")
     for _ in range(args.warmup):
         eng.runner.step()
-    timer_name = {"attention": "ne_paged_verify_attention", "gemm": "ne_w8a16_gemm",
-                  "lm_head": "ne_lm_head"}[args.roofline_kernel]
+    timer_name = "ne_w8a16_gemm"  # the QKV and gate|up projections of every layer
     timer = _native.LaunchTimer() if not args.graph else None
     ctx_per_step, lengths_per_step = [], []
     if timer is not None:
@@ -129,7 +140,7 @@ def run_verify(args, torch):
     roofline = None
     if timer is not None:
         durations = timer.durations_ms()
-        roofline = summarize_roofline(args.roofline_kernel, durations, ctx_per_step, lengths_per_step, cfg)
+        roofline = summarize_roofline("gemm", durations, ctx_per_step, lengths_per_step, cfg)
     active = sum(1 for s in eng.runner.slots if s is not None)
     return {
         "elapsed": elapsed,
@@ -138,6 +149,7 @@ def run_verify(args, torch):
         "roofline": roofline,
         "active_at_end": active,
         "max_new": max_new,
+        "mean_context": sum(sum(c) for c in ctx_per_step) / max(1, sum(len(c) for c in ctx_per_step)),
     }
 
 
@@ -160,12 +172,13 @@ def summarize_roofline(kind, durations_ms, ctx_per_step, lengths_per_step, cfg):
         h, i = cfg.hidden_size, cfg.intermediate_size
         q = cfg.num_attention_heads * cfg.head_dim
         qkv = q + 2 * cfg.num_key_value_heads * cfg.head_dim
-        shapes = [(rows, qkv, h), (rows, h, q), (rows, 2 * i, h), (rows, h, i)]
+        # the timed entry point runs QKV and gate|up (o / down go through the split-K one)
+        shapes = [(rows, qkv, h), (rows, 2 * i, h)]
         flops = sum(2 * m * n * k for m, n, k in shapes) * layers * len(ctx_per_step)
         total_s = sum(durations_ms) * 1e-3
         achieved = flops / total_s / 1e12
         traffic = sum(gemm_traffic(m, n, k) for m, n, k in shapes)
-        return {"kernel": "gemm_kernel<w8a16>", "bound": "mfma", "achieved": round(achieved, 1),
+        return {"kernel": "proj_kernel (W8A16 QKV and gate|up)", "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                 "launches": len(durations_ms), "avg_us": round(1e3 * sum(durations_ms) / len(durations_ms), 2),
                 "hbm_GBps": round(traffic * layers * len(ctx_per_step) / total_s / 1e9, 1)}
@@ -178,65 +191,305 @@ def summarize_roofline(kind, durations_ms, ctx_per_step, lengths_per_step, cfg):
             "avg_us": round(1e3 * sum(durations_ms) / len(durations_ms), 2)}
 
 
+class AttentionWorkload:
+    """Kernel-only int8 verify attention: 64 seqs, ctx U{128..1024} (seed 1), 5 queries,
+    fp16 scales, 4096-block pool, tables from a seeded permutation; `layers` distinct pools."""
+
+    def __init__(self, torch, layers: int = 28):
+        import numpy as np
+
+        from nanoengine_amd import kernels
+
+        dev = torch.device("cuda")
+        blocks, bs, hkv, hq = 4096, 16, 8, 16
+        rng = np.random.default_rng(1)
+        self.ctx = rng.integers(128, 1025, size=NUM_SEQS).astype(np.int32)
+        g = torch.Generator().manual_seed(1)
+        perm = torch.randperm(blocks, generator=g).to(torch.int32)
+        max_blocks = int(math.ceil(self.ctx.max() / bs))
+        tables = torch.zeros(NUM_SEQS, max_blocks, dtype=torch.int32)
+        cur = 0
+        for b, c in enumerate(self.ctx):
+            nb = int(math.ceil(c / bs))
+            tables[b, :nb] = perm[cur : cur + nb]
+            cur += nb
+        slots = blocks * bs + 1
+        self.pools = []
+        for _ in range(layers):
+            kc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
+            vc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
+            ks = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(torch.float16)
+            vs = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(torch.float16)
+            self.pools.append((kc, vc, ks, vs))
+        self.rows = NUM_SEQS * 5
+        self.q = torch.randn(self.rows, hq, 128, device=dev).to(torch.bfloat16)
+        self.out = torch.empty_like(self.q)
+        self.tables = tables.to(dev)
+        self.ctx_d = torch.as_tensor(self.ctx).to(dev)
+        self.q_start = torch.arange(NUM_SEQS, dtype=torch.int32, device=dev) * 5
+        self.q_len = torch.full((NUM_SEQS,), 5, dtype=torch.int32, device=dev)
+        self.ws = kernels.AttentionWorkspace()
+        self.bytes_per_launch = attention_bytes(self.ctx.tolist(), self.rows) + tables.numel() * 4
+        self._kernels = kernels
+
+    def launch(self, pool) -> None:
+        self._kernels.paged_verify_attention(
+            self.q, pool[0], pool[1], pool[2], pool[3], self.tables, 16, self.ctx_d, self.q_start,
+            self.q_len, 5, int(self.ctx.max()), out=self.out, workspace=self.ws)
+
+
 def run_attention_roofline(torch, reps: int = 5):
-    """Kernel-only int8 verify attention (64 seqs, ctx U{128..1024} seed 1, 5 queries, fp16
-    scales, 4096-block pool) over 28 distinct pools so the 256 MB last-level cache cannot
-    hold the working set; HIP events around every launch."""
-    import numpy as np
+    """Average launch time of the attention call over `reps` passes of 28 pools, from HIP
+    events recorded on the launching stream around each call (main + merge kernels)."""
+    from nanoengine_amd import _native
 
-    from nanoengine_amd import _native, kernels
-
-    dev = torch.device("cuda")
-    layers, blocks, bs, hkv, hq = 28, 4096, 16, 8, 16
-    rng = np.random.default_rng(1)
-    ctx = rng.integers(128, 1025, size=NUM_SEQS).astype(np.int32)
-    g = torch.Generator().manual_seed(1)
-    perm = torch.randperm(blocks, generator=g).to(torch.int32)
-    max_blocks = int(math.ceil(ctx.max() / bs))
-    tables = torch.zeros(NUM_SEQS, max_blocks, dtype=torch.int32)
-    cur = 0
-    for b, c in enumerate(ctx):
-        nb = int(math.ceil(c / bs))
-        tables[b, :nb] = perm[cur : cur + nb]
-        cur += nb
-    slots = blocks * bs + 1
-    pools = []
-    for _ in range(layers):
-        kc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
-        vc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
-        ks = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(torch.float16)
-        vs = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(torch.float16)
-        pools.append((kc, vc, ks, vs))
-    rows = NUM_SEQS * 5
-    q = torch.randn(rows, hq, 128, device=dev).to(torch.bfloat16)
-    out = torch.empty_like(q)
-    d = lambda a: torch.as_tensor(a).to(dev)
-    t_d, c_d = tables.to(dev), d(ctx)
-    qs, ql = d(np.arange(NUM_SEQS, dtype=np.int32) * 5), d(np.full(NUM_SEQS, 5, dtype=np.int32))
-    ws = kernels.AttentionWorkspace()
-
-    def launch(p):
-        kernels.paged_verify_attention(q, p[0], p[1], p[2], p[3], t_d, bs, c_d, qs, ql, 5, int(ctx.max()),
-                                       out=out, workspace=ws)
-
-    for p in pools:
-        launch(p)
+    w = AttentionWorkload(torch)
+    for p in w.pools:
+        w.launch(p)
     torch.cuda.synchronize()
     timer = _native.LaunchTimer()
     _native.set_launch_timer("ne_paged_verify_attention", timer)
     for _ in range(reps):
-        for p in pools:
-            launch(p)
+        for p in w.pools:
+            w.launch(p)
     torch.cuda.synchronize()
     _native.set_launch_timer("ne_paged_verify_attention", None)
     dur = timer.durations_ms()
     avg_ms = sum(dur) / len(dur)
-    nbytes = attention_bytes(ctx.tolist(), rows) + tables.numel() * 4
-    achieved = nbytes / (avg_ms * 1e-3) / 1e9
-    return {"workload": "int8 KV, 64 seqs, ctx U{128..1024} seed 1, q=5, fp16 scales",
-            "bytes_per_launch": int(nbytes), "avg_us": round(avg_ms * 1e3, 2),
-            "achieved": round(achieved, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS,
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "launches": len(dur), "sum_ctx": int(ctx.sum())}
+    achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    return {"kernel": "paged_attention_kernel<int8, fp16 scales> + attention_merge_kernel",
+            "workload": "int8 KV, 64 seqs, ctx U{128..1024} seed 1, q=5, fp16 scales, 28 pools",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
+            "bytes_per_launch": int(w.bytes_per_launch), "launches": len(dur),
+            "sum_ctx": int(w.ctx.sum())}
+
+
+def pmc_child(torch) -> int:
+    """What the rocprofv3 --pmc passes profile: one call per pool, then a copy of
+    CALIBRATION_BYTES whose counter reading calibrates the scale."""
+    import ctypes
+
+    from nanoengine_amd import _native
+
+    w = AttentionWorkload(torch)
+    for p in w.pools:
+        w.launch(p)
+    torch.cuda.synchronize()
+    a = torch.empty(CALIBRATION_BYTES, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    _native.call("ne_copy_bytes", ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()), a.numel(),
+                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_child": "done", "launches": len(w.pools)}), flush=True)
+    return 0
+
+
+def measure_traffic() -> dict | None:
+    """HBM bytes per attention call from two rocprofv3 --pmc passes over `--pmc-child`
+    (run before this process touches the GPU).  Each counter is scaled by the reading
+    it gives for the CALIBRATION_BYTES copy (which reads and writes that many bytes)."""
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        log("rocprofv3 not found: traffic not measured")
+        return None
+    per_counter = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
+            cmd = ["timeout", "-s", "KILL", "120", prof, "--pmc", counter, "--output-format", "csv", "-d", tmp,
+                   "-o", "run", "--", sys.executable, str(ROOT / "bench.py"), "--pmc-child"]
+            log(f"pmc pass {counter}")
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            found = list(Path(tmp).rglob("*counter_collection.csv"))
+            if r.returncode != 0 and not found:
+                log(f"pmc pass {counter} failed ({r.returncode}): {r.stderr[-400:]}")
+                return None
+            rows = list(csv.DictReader(open(found[0])))
+        ours = [x for x in rows if x["Kernel_Name"].removeprefix("void ").startswith("ne::")]
+        attn = [float(x["Counter_Value"]) for x in ours if "attention" in x["Kernel_Name"]]
+        calib = [float(x["Counter_Value"]) for x in ours if "copy_kernel" in x["Kernel_Name"]]
+        launches = sum(1 for x in rows if "paged_attention_kernel" in x["Kernel_Name"])
+        if not attn or not calib or not launches:
+            log(f"pmc pass {counter}: kernels not found in the counter output")
+            return None
+        scale = (CALIBRATION_BYTES / 1024.0) / calib[0]  # true KiB per counted KiB
+        per_counter[counter] = {"kib_per_launch": sum(attn) / launches, "scale": scale,
+                                "bytes_per_launch": sum(attn) / launches * scale * 1024.0}
+    return {"fetch_bytes": int(per_counter["FETCH_SIZE"]["bytes_per_launch"]),
+            "write_bytes": int(per_counter["WRITE_SIZE"]["bytes_per_launch"]),
+            "fetch_scale": round(per_counter["FETCH_SIZE"]["scale"], 4),
+            "write_scale": round(per_counter["WRITE_SIZE"]["scale"], 4)}
+
+
+class TorchReferenceStep:
+    """The reference's verify step composed from its own PyTorch ops, batched over the
+    benchmark's 64 sequences, on this GPU with no HIP kernel of this library:
+
+      build_step_inputs      host lists -> token/position/slot/mask tensors each step
+                             (ne/engine/generation/batch_builder.py:22-65,
+                             ne/engine/memory/paged_allocator.py:69-79)
+      Int8Linear.forward     dequantise the whole weight, then F.linear
+                             (ne/models/int8_quantization.py:55-57)
+      RMSNorm, RoPE, QK-norm ne/models/qwen3.py:31-68, 89-115
+      run_cached_attention   quantise + index_copy_ the new K/V, gather the padded
+                             context, dequantise, masked GQA attention
+                             (ne/models/attention_context.py:42-109)
+      compute_logits         every row of the step (ne/models/qwen3.py:197-203)
+      verify_proposal        per sequence, one-hot target and draft, .item() per guess
+                             (ne/engine/speculative/verifier.py:27-60)
+
+    Attention runs SDPA's math path written out (scores, masked softmax, weighted
+    sum) with the key operand made contiguous: torch's bf16 batched matmul with a
+    transposed right operand is not safe on this platform."""
+
+    def __init__(self, torch, state: dict, ctx_len: int, block_size: int = 16):
+        from nanoengine_amd.qwen3 import QWEN3_0_6B, quantize_rows
+
+        self.torch = torch
+        self.F = torch.nn.functional
+        self.c = QWEN3_0_6B
+        dev = torch.device("cuda")
+        bf = torch.bfloat16
+        self.layers = []
+        for i in range(self.c.num_hidden_layers):
+            p = f"model.layers.{i}."
+            lw = {}
+            for name in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                         "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"):
+                q8, s = quantize_rows(state[p + name + ".weight"].to(bf))
+                lw[name] = (q8.to(dev), s.to(dev))
+            for name in ("self_attn.q_norm", "self_attn.k_norm", "input_layernorm", "post_attention_layernorm"):
+                lw[name] = state[p + name + ".weight"].to(bf).to(dev)
+            self.layers.append(lw)
+        self.embed = state["model.embed_tokens.weight"].to(bf).to(dev)
+        self.norm = state["model.norm.weight"].to(bf).to(dev)
+        self.bs = block_size
+        self.ctx_len = ctx_len  # tokens per sequence before the step's guesses
+        blocks_per_seq = math.ceil((ctx_len + K_DRAFT + 1) / block_size)
+        self.num_slots = NUM_SEQS * blocks_per_seq * block_size
+        shape = (self.num_slots + 1, self.c.num_key_value_heads, self.c.head_dim)
+        self.kc = [torch.zeros(shape, dtype=torch.int8, device=dev) for _ in self.layers]
+        self.vc = [torch.zeros(shape, dtype=torch.int8, device=dev) for _ in self.layers]
+        self.ks = [torch.zeros(shape[:2] + (1,), dtype=bf, device=dev) for _ in self.layers]
+        self.vs = [torch.zeros(shape[:2] + (1,), dtype=bf, device=dev) for _ in self.layers]
+        # block tables as the paged allocator leaves them: FIFO blocks per sequence
+        self.tables = [list(range(b * blocks_per_seq, (b + 1) * blocks_per_seq)) for b in range(NUM_SEQS)]
+        g = torch.Generator().manual_seed(5)
+        self.history = [torch.randint(0, 512, (ctx_len,), generator=g).tolist() for _ in range(NUM_SEQS)]
+        self.guesses = [h[-K_DRAFT:] for h in self.history]
+        self.dev = dev
+
+    # ---- reference ops ----
+    def rmsnorm(self, x, w):
+        dt = x.dtype
+        x = x.float()
+        x = x * self.torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.c.rms_norm_eps)
+        return w * x.to(dt)
+
+    def int8_linear(self, x, wq):
+        q8, s = wq
+        return self.F.linear(x, q8.to(x.dtype) * s[:, None])
+
+    def quantize(self, x):
+        s = x.abs().amax(-1, keepdim=True).float().clamp(min=1e-8) / 127
+        return self.torch.round(x.float() / s).clamp(-127, 127).to(self.torch.int8), s.to(x.dtype)
+
+    def rope(self, x, cos, sin):
+        a, b = x.chunk(2, dim=-1)
+        return x * cos + self.torch.cat((-b, a), dim=-1) * sin
+
+    def step(self) -> list[list[int]]:
+        torch, c = self.torch, self.c
+        q_rows = K_DRAFT + 1
+        # build_step_inputs: host lists -> tensors
+        tok_rows, pos_rows = [], []
+        for h, gs in zip(self.history, self.guesses):
+            L = len(h)
+            tok_rows.append([h[-1]] + gs)
+            pos_rows.append(list(range(L - 1, L - 1 + q_rows)))
+        ctx = self.ctx_len + K_DRAFT
+        per_row = math.ceil(ctx / self.bs)
+        tables = torch.tensor([t[:per_row] for t in self.tables], dtype=torch.int64)
+        kpos = torch.arange(ctx)
+        context_slots = (tables[:, kpos // self.bs] * self.bs + kpos % self.bs).to(self.dev)
+        tokens = torch.tensor(tok_rows, device=self.dev)
+        positions = torch.tensor(pos_rows, device=self.dev)
+        slot_mapping = context_slots.gather(1, positions)
+        mask = ((kpos.to(self.dev)[None, None, :] <= positions[:, :, None])
+                & (kpos.to(self.dev)[None, None, :] < ctx)).unsqueeze(1)
+        # forward
+        x = self.embed[tokens]
+        exps = torch.arange(0, c.head_dim, 2, device=self.dev, dtype=torch.float32) / c.head_dim
+        ang = positions.float()[..., None] * (1.0 / (c.rope_theta ** exps))
+        ang = torch.cat((ang, ang), -1).unsqueeze(1)
+        cos, sin = ang.cos().to(x.dtype), ang.sin().to(x.dtype)
+        b, s = tokens.shape
+        nh, nkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        for i, lw in enumerate(self.layers):
+            h = self.rmsnorm(x, lw["input_layernorm"])
+            q = self.rmsnorm(self.int8_linear(h, lw["self_attn.q_proj"]).view(b, s, nh, d),
+                             lw["self_attn.q_norm"]).transpose(1, 2)
+            k = self.rmsnorm(self.int8_linear(h, lw["self_attn.k_proj"]).view(b, s, nkv, d),
+                             lw["self_attn.k_norm"]).transpose(1, 2)
+            v = self.int8_linear(h, lw["self_attn.v_proj"]).view(b, s, nkv, d).transpose(1, 2)
+            q, k = self.rope(q, cos, sin), self.rope(k, cos, sin)
+            target = slot_mapping.reshape(-1)
+            for cache, scales, vec in ((self.kc[i], self.ks[i], k), (self.vc[i], self.vs[i], v)):
+                qv, sv = self.quantize(vec.transpose(1, 2).reshape(-1, nkv, d))
+                cache.index_copy_(0, target, qv)
+                scales.index_copy_(0, target, sv)
+            ck = (self.kc[i][context_slots].to(x.dtype) * self.ks[i][context_slots]).transpose(1, 2)
+            cv = (self.vc[i][context_slots].to(x.dtype) * self.vs[i][context_slots]).transpose(1, 2)
+            ck = ck.repeat_interleave(nh // nkv, dim=1)
+            cv = cv.repeat_interleave(nh // nkv, dim=1).contiguous()
+            scores = torch.matmul(q.contiguous(), ck.transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(d))
+            scores = scores.masked_fill(~mask, float("-inf"))
+            attn = torch.matmul(torch.softmax(scores, dim=-1), cv)
+            x = x + self.int8_linear(attn.transpose(1, 2).reshape(b, s, -1), lw["self_attn.o_proj"])
+            h2 = self.rmsnorm(x, lw["post_attention_layernorm"])
+            mlp = self.F.silu(self.int8_linear(h2, lw["mlp.gate_proj"])) * self.int8_linear(h2, lw["mlp.up_proj"])
+            x = x + self.int8_linear(mlp, lw["mlp.down_proj"])
+        hidden = self.rmsnorm(x, self.norm)
+        logits = self.F.linear(hidden, self.embed)  # [b, k+1, V]
+        # verify_proposal per sequence, greedy, one-hot draft
+        out = []
+        vocab = logits.shape[-1]
+        for bi in range(b):
+            target = self.F.one_hot(torch.argmax(logits[bi], dim=-1), vocab).float()
+            kept = []
+            for j, guess in enumerate(self.guesses[bi]):
+                draft = self.F.one_hot(torch.tensor(guess, device=self.dev), vocab).float()
+                acc = (target[j, guess] / draft[guess].clamp(min=1e-12)).clamp(max=1.0).item()
+                if acc >= 1.0:
+                    kept.append(guess)
+                    continue
+                residual = (target[j] - draft).clamp(min=0.0)
+                if residual.sum() <= 0:
+                    residual = target[j]
+                residual = residual / residual.sum()
+                kept.append(int(torch.argmax(residual).item()))
+                break
+            else:
+                kept.append(int(torch.argmax(target[len(self.guesses[bi])]).item()))
+            out.append(kept)
+        return out
+
+
+def run_torch_baseline(torch, state, ctx_len: int, steps: int = 5, warmup: int = 2):
+    t0 = time.perf_counter()
+    ref = TorchReferenceStep(torch, state, ctx_len)
+    log(f"torch baseline ready {time.perf_counter() - t0:.1f}s")
+    for _ in range(warmup):
+        ref.step()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        ref.step()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - start) / steps
+    return {"verify_step_us": round(step_s * 1e6, 1), "steps": steps, "context_tokens": ctx_len,
+            "workload": f"64 seqs x (1 + {K_DRAFT}) rows, context {ctx_len} + {K_DRAFT} tokens each, int8 W + int8 "
+                        "paged KV, eager PyTorch ops of the reference on this GPU"}
 
 
 def run_cpu_baseline(torch):
@@ -278,28 +531,61 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--temperature", type=float, default=0.0)
     parser.add_argument("--graph", action="store_true", help="replay the fixed-shape step as a HIP graph")
-    parser.add_argument("--roofline-kernel", choices=("attention", "gemm", "lm_head"), default="gemm")
+    parser.add_argument("--only", choices=("all", "verify", "attention", "baseline"), default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-attention", action="store_true")
+    parser.add_argument("--no-torch-baseline", action="store_true")
+    parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
+    parser.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the verify step "
               "shards by sequence with no exchange; run one process per GPU)", file=sys.stderr)
         return 2
+    if args.pmc_child:
+        import torch
+
+        return pmc_child(torch)
+    # counter passes first, as child processes, before this process initialises the GPU
+    traffic = None
+    if args.only in ("all", "attention") and not args.no_traffic:
+        traffic = measure_traffic()
     import torch
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
-    res = run_verify(args, torch)
-    log(f"verify: {res['tokens']} tokens in {res['elapsed']:.3f}s")
-    attention = None if args.no_attention else run_attention_roofline(torch)
-    if attention:
+    res = None
+    if args.only in ("all", "verify"):
+        res = run_verify(args, torch)
+        log(f"verify: {res['tokens']} tokens in {res['elapsed']:.3f}s")
+    attention = None
+    if args.only in ("all", "attention"):
+        attention = run_attention_roofline(torch)
+        attention["traffic"] = None
+        if traffic is not None:
+            attention["traffic"] = traffic["fetch_bytes"] + traffic["write_bytes"]
+            attention["traffic_detail"] = traffic
         log(f"attention: {attention['avg_us']} us, {attention['achieved']} GB/s")
-    cpu = None if args.no_cpu_baseline else run_cpu_baseline(torch)
-    if cpu:
+    torch_base = None
+    if args.only in ("all", "baseline") and not args.no_torch_baseline:
+        from nanoengine_amd.qwen3 import QWEN3_0_6B, random_state_dict
+
+        ctx_len = int(round(res["mean_context"])) if res else PROMPT_MOTIF * PROMPT_REPEATS + 32
+        torch_base = run_torch_baseline(torch, random_state_dict(QWEN3_0_6B, seed=0, std=0.02), ctx_len)
+        log(f"torch baseline: {torch_base['verify_step_us']} us per step")
+    cpu = None
+    if args.only == "all" and not args.no_cpu_baseline:
+        cpu = run_cpu_baseline(torch)
         log(f"cpu baseline: {cpu['value']} tok/s")
+    if res is None:
+        print(json.dumps({"attention": attention, "torch_baseline": torch_base}), flush=True)
+        return 0
     value = res["tokens"] / res["elapsed"]
+    step_us = 1e6 * res["elapsed"] / args.steps
+    if torch_base is not None:
+        torch_base["speedup"] = round(torch_base["verify_step_us"] / step_us, 2)
+        torch_base["accepted_tok_s_at_same_acceptance"] = round(res["tokens"] / args.steps
+                                                                / (torch_base["verify_step_us"] * 1e-6), 1)
     line = {
         "metric": "verify-step us + accepted tok/s (64 seqs, k=4, int8 W+KV); attn HBM GB/s",
         "value": round(value, 1),
@@ -307,7 +593,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(1e3 * res["elapsed"] / args.steps, 4),
+        "ms_per_step": round(step_us / 1e3, 4),
+        "verify_step_us": round(step_us, 1),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -320,8 +607,9 @@ def main() -> int:
                    "global_batch": NUM_SEQS, "seq_len": PROMPT_MOTIF * PROMPT_REPEATS, "parallelism": "single GPU",
                    "hip_graph": bool(args.graph)},
         "accepted_per_step_hist": {str(k): v for k, v in sorted(res["kept_hist"].items())},
-        "roofline": res["roofline"],
-        "attention": attention,
+        "roofline": attention,
+        "gemm": res["roofline"],
+        "torch_baseline": torch_base,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
