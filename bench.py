@@ -11,7 +11,10 @@ prompts repeat a seeded 16-token motif of ids in [0, 512) four times, n-gram
 sequence.  Synthetic data: no checkpoint or dataset is read.
 
 One step = one batched verify step over the 64 sequences (draft, reserve KV,
-forward over 64 x 5 rows, LM head, acceptance, rollback).  W untimed steps, then
+forward over 64 x 5 rows, LM head, acceptance, rollback).  The fixed-shape device
+part of the step (packing, forward, LM head, acceptance) is captured once as a HIP
+graph and replayed, as the reference's NANOENGINE_CUDA_GRAPHS setting does for
+decode; --eager launches it kernel by kernel.  W untimed steps, then
 K timed steps bracketed by device synchronisation; ``value`` is accepted tokens
 per second (tokens emitted by the timed steps / elapsed).
 
@@ -24,7 +27,8 @@ Also reported on the same line:
                  HIP events on the launching stream; traffic = HBM bytes per launch
                  from two rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each
                  scaled by what the counter reads for a 256 MiB copy.
-  gemm           the W8A16 projection GEMMs of the verify step (MFMA roofline)
+  gemm           the W8A16 projection GEMMs of the verify step (MFMA roofline; with
+                 --eager only, since graph replay has no per-launch events)
   torch_baseline the reference's verify step composed from its own PyTorch ops on
                  this GPU (dequantise-then-linear, gather + dequant + masked GQA
                  attention, logits on every row, a per-sequence verify loop with
@@ -530,7 +534,9 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--temperature", type=float, default=0.0)
-    parser.add_argument("--graph", action="store_true", help="replay the fixed-shape step as a HIP graph")
+    parser.add_argument("--eager", dest="graph", action="store_false",
+                        help="launch the step's kernels one by one instead of replaying a HIP graph "
+                             "(per-launch GEMM timing needs this)")
     parser.add_argument("--only", choices=("all", "verify", "attention", "baseline"), default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-torch-baseline", action="store_true")

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 1
+#define NE_ABI_VERSION 2
 
 /* status codes */
 #define NE_OK 0
@@ -174,7 +174,8 @@ int ne_rmsnorm(const void* x, const void* weight, void* out, int32_t rows, int32
 int ne_add_rmsnorm(void* residual, const void* delta, const void* weight, void* out, int32_t rows,
                    int32_t hidden, float eps, void* stream);
 /* ne_add_rmsnorm with delta = bf16(sum_s partials[s, row, :]) taken from the fp32
- * output of ne_w8a16_gemm_splitk ([splits, rows, hidden], 16-byte aligned); the
+ * output of ne_w8a16_gemm_splitk ([splits, rows, hidden], 16-byte aligned, splits
+ * one of 1, 2, 3, 4, 6, 8); the
  * projection output is rounded to bf16 before the residual add, as in the
  * reference's bf16 o_proj / down_proj followed by the residual add
  * (ne/models/qwen3.py:145-149). */
@@ -188,14 +189,18 @@ int ne_embed_rmsnorm(const int32_t* tokens, const void* embed, const void* weigh
  * 47-68, ne/models/attention_context.py:77-94).  qkv [rows, (Hq+2*Hkv)*128] bf16
  * holds q | k | v per row.  q_out [rows, Hq, 128] receives RoPE(q_norm(q)); the
  * key RoPE(k_norm(k)) and value v are written (quantised for an int8 cache) at
- * slot_mapping[row].  inv_freq [64] fp32 holds 1/theta^(2i/128).
+ * slot_mapping[row].  rope_cos_sin [rope_positions][2][64] bf16 holds, per
+ * position p, bf16(cos(p * inv_freq[i])) then bf16(sin(...)), i < 64, with the
+ * fp32 angles of build_rotary_tables (qwen3.py:47-57); dims i and i + 64 share
+ * them.  Positions are clamped to the table.
  */
 int ne_qk_norm_rope_kv_write(const void* qkv, int32_t rows, int32_t num_q_heads,
                              int32_t num_kv_heads, int32_t head_dim, const void* q_norm_weight,
                              const void* k_norm_weight, float eps, const int32_t* positions,
-                             const float* inv_freq, const int32_t* slot_mapping, void* k_cache,
-                             void* v_cache, void* k_scale, void* v_scale, int32_t kv_dtype,
-                             int32_t scale_dtype, void* q_out, void* stream);
+                             const void* rope_cos_sin, int32_t rope_positions,
+                             const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                             void* k_scale, void* v_scale, int32_t kv_dtype, int32_t scale_dtype,
+                             void* q_out, void* stream);
 
 /*
  * A9/A10 - fused acceptance (replaces verify_proposal and the sampling helpers,

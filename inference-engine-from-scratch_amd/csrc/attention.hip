@@ -597,6 +597,213 @@ __global__ __launch_bounds__(kHeadWaves * KG * kWave) void paged_attention_kerne
   }
 }
 
+// ---- DMA-fed variant (int8 cache, 8 KV heads, 2-byte scales) -----------------
+// Same work item and arithmetic as paged_attention_kernel, but each wave (one KV
+// head) streams its head's rows of every 16-key tile, plus all heads' scales of
+// the tile, from HBM straight into its own LDS ring with global_load_lds: no
+// registers hold data in flight, so every wave keeps kDmaRing tiles (18 KB) on
+// the way while it computes, and the loop needs no block barrier.
+constexpr int kDmaRing = 4;                          // 16-key tiles in flight per wave
+constexpr int kRowBytes = kHeadDim;                  // one int8 head row
+constexpr int kTileRows = kTileKeys * kRowBytes;     // 2 KB: one head's K (or V) rows of a tile
+constexpr int kScaleBytes = kTileKeys * kHeadWaves * 2;  // 256 B: a tile's scales, all heads
+constexpr int kDmaSlot = 2 * kTileRows + 2 * kScaleBytes;  // K | V | k-scales | v-scales
+constexpr int kDmaPerTile = 6;                       // 2 K + 2 V (1 KB each) + 2 scale dwords
+constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4 + kHeadWaves * kWave * 4;
+
+__device__ __forceinline__ void lds_dma(const void* src, void* lds, int bytes) {
+  if (bytes == 16) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+  } else {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+  }
+}
+
+// s_waitcnt with only vmcnt (N) or only lgkmcnt (0) constrained (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void dma_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void dma_wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+// Copy tile `t` (clamped to the split's last tile) of head `head` into ring slot
+// `dst`.  K/V rows land as [16 keys][128 B] with 16-byte chunk c of key k stored
+// at chunk position c ^ (k & 7), which makes the fragment reads conflict-free.
+__device__ __forceinline__ void dma_tile(const AttnParams& p, const int* s_slot, int n_tiles, int t,
+                                         int head, int lane, char* dst) {
+  const int ti = min(t, n_tiles - 1);
+  const int64_t slot0 = __builtin_amdgcn_readfirstlane(s_slot[ti]);
+  const int64_t slot_bytes = (int64_t)kHeadWaves * kRowBytes;
+  const char* kbase = (const char*)p.k_cache + slot0 * slot_bytes + head * kRowBytes;
+  const char* vbase = (const char*)p.v_cache + slot0 * slot_bytes + head * kRowBytes;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int key = 8 * j + (lane >> 3);
+    const int chunk = (lane & 7) ^ (key & 7);
+    const int64_t off = key * slot_bytes + chunk * 16;
+    lds_dma(kbase + off, dst + j * 1024, 16);
+    lds_dma(vbase + off, dst + kTileRows + j * 1024, 16);
+  }
+  // scales [slot][8 heads] of 2 bytes: the tile's 16 slots are 256 contiguous bytes
+  lds_dma((const char*)p.k_scale + slot0 * (kHeadWaves * 2) + lane * 4, dst + 2 * kTileRows, 4);
+  lds_dma((const char*)p.v_scale + slot0 * (kHeadWaves * 2) + lane * 4,
+          dst + 2 * kTileRows + kScaleBytes, 4);
+}
+
+// Registers of one 32-key iteration from two ring slots (the layout load_iter gives).
+template <int SDT>
+__device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b, int kb, int kend,
+                                         int head, int lane, IterRegs<true>& R) {
+  const int r = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const char* sl = t ? slot_b : slot_a;
+    R.k[t][0] = *(const u32x4*)(sl + r * kRowBytes + (((2 * g) ^ (r & 7)) * 16));
+    R.k[t][1] = *(const u32x4*)(sl + r * kRowBytes + (((2 * g + 1) ^ (r & 7)) * 16));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 4 * g + i;
+      R.v[4 * t + i] = *(const u32x2*)(sl + kTileRows + key * kRowBytes +
+                                       (((r >> 1) ^ (key & 7)) * 16) + (r & 1) * 8);
+    }
+  }
+  // lanes 0..31: key scale of key kb+lane; lanes 32..63: value scale of key kb+lane-32
+  const int kk = lane & 31;
+  const char* sl = (kk >> 4) ? slot_b : slot_a;
+  const uint16_t raw = *(const uint16_t*)(sl + 2 * kTileRows + (lane >> 5) * kScaleBytes +
+                                          (kk & 15) * (kHeadWaves * 2) + head * 2);
+  const float s = (SDT == NE_DTYPE_BF16) ? bf16_to_f32(raw) : f16_to_f32(raw);
+  R.sc = (kb + kk < kend) ? s : 0.f;
+}
+
+template <int SDT>
+__global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel(AttnParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* s_slot = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot);
+  float* s_sc_all = (float*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4);
+
+  // ---- work item (one sequence's M tile and split; the wave is the KV head) ----
+  const int bid = blockIdx.x;
+  const int split = bid % p.max_splits;
+  const int mt = (bid / p.max_splits) % p.mtiles;
+  const int seq = bid / (p.max_splits * p.mtiles);
+  const int tid = threadIdx.x;
+  const int head = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const UnitInfo u0 = unit_info(p, seq * p.num_kv_heads * p.mtiles + mt);
+  if (u0.row0 >= u0.rows_total) return;
+  int n_splits = u0.n_splits;
+  if (n_splits > p.max_splits) {
+    if (tid == 0 && split == 0) atomicOr(p.error_flag, 1u);
+    n_splits = p.max_splits;
+  }
+  if (split >= n_splits) return;
+  const int kstart = split * p.split_len;
+  const int kend = min(u0.kend_unit, kstart + p.split_len);
+  const int ql = u0.ql;
+
+  const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
+  const int n_tiles = (kend - kstart + kTileKeys - 1) / kTileKeys;
+  for (int t = tid; t < n_tiles; t += kHeadWaves * kWave) {
+    const int key0 = kstart + kTileKeys * t;
+    s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+  }
+  __syncthreads();  // s_slot ready
+
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int R = u0.row0 + r;
+  const bool row_valid = R < u0.rows_total;
+  const int h_local = row_valid ? R / ql : 0;
+  const int qi = row_valid ? R % ql : 0;
+  const int kend_row = row_valid ? min(kend, u0.ctx - ql + qi + 1) : kend;
+
+  // Q first: its registers are then ready without waiting for the ring's copies
+  QFrag<true> qf;
+  {
+    u32x4 raw[4] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+    if (row_valid) {
+      const int64_t qoff = (int64_t)(u0.qs + qi) * p.q_tok_stride +
+                           (int64_t)(head * p.group + h_local) * p.q_head_stride + 32 * g;
+      const u32x4* src = (const u32x4*)(p.q + qoff);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) raw[c] = src[c];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 hv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[c][i] & 0xFFFFu)),
+                           bf16_to_f32((uint16_t)(raw[c][i] >> 16)));
+      qf.q[c] = __builtin_bit_cast(f16x8, hv);
+    }
+  }
+
+  char* ring = smem + head * (kDmaRing * kDmaSlot);
+#pragma unroll
+  for (int j = 0; j < kDmaRing; ++j) dma_tile(p, s_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
+
+  float m = kNegBig, l = 0.f;
+  floatx4 o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float* sc_row = s_sc_all + head * kWave;
+  const int n_iter = (n_tiles + 1) / 2;
+  for (int it = 0; it < n_iter; ++it) {
+    // this wave's DMA of tiles 2it, 2it+1 has landed once at most the two tiles
+    // issued after them are still in flight
+    dma_wait_vmcnt<kDmaPerTile * (kDmaRing - 2)>();
+    const char* sa = ring + ((2 * it) % kDmaRing) * kDmaSlot;
+    const char* sb = ring + ((2 * it + 1) % kDmaRing) * kDmaSlot;
+    const int kb = kstart + it * kIterKeys;
+    IterRegs<true> A;
+    lds_iter<SDT>(sa, sb, kb, kend, head, lane, A);
+    compute_iter<true>(p, A, qf, sc_row, kb, kend_row, u0.ctx, lane, m, l, o);
+    // the two slots are free once their reads have returned: refill them
+    dma_wait_lgkmcnt0();
+    dma_tile(p, s_slot, n_tiles, 2 * it + kDmaRing, head, lane, ring + ((2 * it) % kDmaRing) * kDmaSlot);
+    dma_tile(p, s_slot, n_tiles, 2 * it + 1 + kDmaRing, head, lane,
+             ring + ((2 * it + 1) % kDmaRing) * kDmaSlot);
+  }
+  dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (!row_valid) return;
+
+  // lane (r, g) holds row r, dims 32g + 8i + j in o[j][i]
+  const int unit = (seq * p.num_kv_heads + head) * p.mtiles + mt;
+  if (n_splits == 1) {
+    uint16_t* dst = p.out + (int64_t)(u0.qs + qi) * p.o_tok_stride +
+                    (int64_t)(head * p.group + h_local) * p.o_head_stride + 32 * g;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 bits = {pack_bf16x2(o[0][i] * inv, o[1][i] * inv),
+                          pack_bf16x2(o[2][i] * inv, o[3][i] * inv),
+                          pack_bf16x2(o[4][i] * inv, o[5][i] * inv),
+                          pack_bf16x2(o[6][i] * inv, o[7][i] * inv)};
+      *(u32x4*)(dst + 8 * i) = bits;
+    }
+  } else {
+    const int64_t pbase = ((int64_t)unit * p.max_splits + split) * kRows + r;
+    float* po = p.part_o + pbase * kHeadDim + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(floatx4*)(po + 8 * i) = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
+      *(floatx4*)(po + 8 * i + 4) = floatx4{o[4][i], o[5][i], o[6][i], o[7][i]};
+    }
+    if (g == 0) {
+      p.part_ml[pbase * 2] = m;
+      p.part_ml[pbase * 2 + 1] = l;
+    }
+  }
+}
+
 // Combines the split partials of every unit that has more than one split:
 // out = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s.  One work-group per unit,
 // 16 threads per row, 8 dims per thread.
@@ -689,6 +896,25 @@ int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStre
     hipLaunchKernelGGL((paged_attention_kernel<true, NE_DTYPE_FP32, KG, DB>), grid, block, 0, s, p);
   }
   int rc = check_launch("paged_attention_kernel");
+  if (rc != NE_OK || p.max_splits == 1) return rc;
+  hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)p.units), dim3(256), 0, s, p);
+  return check_launch("attention_merge_kernel");
+}
+
+// The DMA kernel serves int8 caches with 8 KV heads and 2-byte scales; it needs
+// the attribute for more than the default dynamic LDS once per instantiation.
+template <int SDT>
+int launch_attention_dma(const AttnParams& p, hipStream_t s) {
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)paged_attention_dma_kernel<SDT>, hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
+  if (attr != hipSuccess) {
+    set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", kDmaLds,
+              hipGetErrorString(attr));
+    return NE_ELAUNCH;
+  }
+  const dim3 grid((unsigned)p.num_seqs * (unsigned)p.mtiles * (unsigned)p.max_splits);
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT>), grid, dim3(kHeadWaves * kWave), kDmaLds, s, p);
+  int rc = check_launch("paged_attention_dma_kernel");
   if (rc != NE_OK || p.max_splits == 1) return rc;
   hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)p.units), dim3(256), 0, s, p);
   return check_launch("attention_merge_kernel");
@@ -805,6 +1031,13 @@ extern "C" int ne_paged_verify_attention(
   if (rc != NE_OK) return rc;
   // int8: one wave per KV head, registers double-buffered (154 VGPRs); bf16: one
   // wave per KV head, single-buffered (its double-buffered form needs 244 VGPRs)
+  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves &&
+                      scale_dtype != NE_DTYPE_FP32 && ((uintptr_t)k_scale % 4) == 0 &&
+                      ((uintptr_t)v_scale % 4) == 0;
+  if (dma_ok) {
+    return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16>(p, (hipStream_t)stream)
+                                        : launch_attention_dma<NE_DTYPE_FP16>(p, (hipStream_t)stream);
+  }
   if (kv_dtype == NE_DTYPE_INT8) return launch_attention<1, true>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
   return launch_attention<1, false>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
 }

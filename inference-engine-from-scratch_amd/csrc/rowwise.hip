@@ -33,15 +33,17 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
 
 // MODE 0: out = norm(x); 1: residual = bf16(residual + delta), out = norm(residual);
 // 2: residual = embed[token], out = norm(residual); 3: as 1 with
-// delta = bf16(sum over `splits` fp32 partial rows, split stride rows * hidden).
-// One wave per row.
-template <int MODE>
+// delta = bf16(sum over SPLITS fp32 partial rows, split stride rows * hidden).
+// One wave per row.  Every load of a row (input, delta or partials, weight) is
+// issued before the first use, so a wave pays one memory round trip, not one per
+// split: SPLITS is a template parameter for that reason, and so is CPL, the 8-element
+// chunks per lane (hidden <= 512 * CPL), which sizes the register arrays.
+template <int MODE, int SPLITS, int CPL>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_t* residual,
                                                       const uint16_t* delta, const int32_t* tokens,
                                                       const uint16_t* embed, const uint16_t* weight,
                                                       uint16_t* out, int rows, int hidden,
-                                                      float eps, const float* partials = nullptr,
-                                                      int splits = 0) {
+                                                      float eps, const float* partials = nullptr) {
   const int row = blockIdx.x * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
@@ -54,28 +56,45 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_
   } else {
     src = embed + (int64_t)tokens[row] * hidden;
   }
-  float h[kMaxChunksPerLane][8];
-  float ss = 0.f;
+  u32x4 raw[CPL], wraw[CPL], draw[CPL];
+  floatx4 part[CPL][SPLITS > 0 ? SPLITS : 1][2];
 #pragma unroll
-  for (int c = 0; c < kMaxChunksPerLane; ++c) {
+  for (int c = 0; c < CPL; ++c) {
     const int ci = lane + c * kWave;
     if (ci < chunks) {
-      unpack8(*(const u32x4*)(src + ci * 8), h[c]);
+      raw[c] = *(const u32x4*)(src + ci * 8);
+      wraw[c] = *(const u32x4*)(weight + ci * 8);
+      if constexpr (MODE == 1) draw[c] = *(const u32x4*)(delta + (int64_t)row * hidden + ci * 8);
+      if constexpr (MODE == 3) {
+#pragma unroll
+        for (int sp = 0; sp < SPLITS; ++sp) {
+          const float* pp = partials + ((int64_t)sp * rows + row) * hidden + ci * 8;
+          part[c][sp][0] = *(const floatx4*)pp;
+          part[c][sp][1] = *(const floatx4*)(pp + 4);
+        }
+      }
+    }
+  }
+  float h[CPL][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ci = lane + c * kWave;
+    if (ci < chunks) {
+      unpack8(raw[c], h[c]);
       if constexpr (MODE == 1) {
         float d[8];
-        unpack8(*(const u32x4*)(delta + (int64_t)row * hidden + ci * 8), d);
+        unpack8(draw[c], d);
 #pragma unroll
         for (int e = 0; e < 8; ++e) h[c][e] = bf16_round(h[c][e] + d[e]);
       } else if constexpr (MODE == 3) {
         float d[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < splits; ++sp) {
-          const float* pp = partials + ((int64_t)sp * rows + row) * hidden + ci * 8;
-          const floatx4 lo = *(const floatx4*)pp;
-          const floatx4 hi = *(const floatx4*)(pp + 4);
+#pragma unroll
+        for (int sp = 0; sp < SPLITS; ++sp) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            d[e] += lo[e];
-            d[e + 4] += hi[e];
+            d[e] += part[c][sp][0][e];
+            d[e + 4] += part[c][sp][1][e];
           }
         }
 #pragma unroll
@@ -89,11 +108,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)hidden + eps);
 #pragma unroll
-  for (int c = 0; c < kMaxChunksPerLane; ++c) {
+  for (int c = 0; c < CPL; ++c) {
     const int ci = lane + c * kWave;
     if (ci < chunks) {
       float w[8], o[8];
-      unpack8(*(const u32x4*)(weight + ci * 8), w);
+      unpack8(wraw[c], w);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = bf16_round(h[c][e] * inv) * w[e];
       *(u32x4*)(out + (int64_t)row * hidden + ci * 8) = pack8(o);
@@ -123,44 +142,46 @@ __device__ __forceinline__ void write_vector(float a, float b, int lane, int64_t
   }
 }
 
-// One 256-thread work-group per token row; waves walk q heads, then k heads, then v heads.
+// One wave per (token row, head), four heads of a row per work-group: q heads,
+// then k heads, then v heads.  cos/sin come from `rope` ([rope_positions][2][64]
+// bf16: cos, then sin, of position * inv_freq[i]; dims i and i + 64 share them),
+// computed once by the caller exactly as the reference builds its tables.
 template <bool INT8, int SDT>
 __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     const uint16_t* qkv, int hq, int hkv, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
-    float eps, const int32_t* positions, const float* inv_freq, const int32_t* slot_mapping,
-    void* k_cache, void* v_cache, void* k_scale, void* v_scale, uint16_t* q_out) {
-  const int row = blockIdx.x;
-  const int wave = threadIdx.x / kWave;
+    float eps, const int32_t* positions, const uint16_t* rope, int rope_positions,
+    const int32_t* slot_mapping, void* k_cache, void* v_cache, void* k_scale, void* v_scale,
+    uint16_t* q_out) {
+  const int heads = hq + 2 * hkv;
+  const int groups = (heads + 3) / 4;
+  const int row = blockIdx.x / groups;
+  const int h = (blockIdx.x % groups) * 4 + threadIdx.x / kWave;
+  if (h >= heads) return;  // wave-uniform; the kernel has no barrier
   const int lane = threadIdx.x % kWave;
-  const int width = (hq + 2 * hkv) * 128;
-  const uint16_t* src = qkv + (int64_t)row * width;
-  const float pos = (float)positions[row];
+  const uint16_t* v = qkv + (int64_t)row * heads * 128 + h * 128;
+  float a = bf16_to_f32(v[lane]);
+  float b = bf16_to_f32(v[lane + 64]);
   const int64_t slot = slot_mapping[row];
-  // rotary factors for dims lane and lane+64 share one angle
-  float sn, cs;
-  sincosf(pos * inv_freq[lane], &sn, &cs);
-  const float c16 = bf16_round(cs), s16 = bf16_round(sn);
-  for (int h = wave; h < hq + 2 * hkv; h += 4) {
-    const uint16_t* v = src + h * 128;
-    float a = bf16_to_f32(v[lane]);
-    float b = bf16_to_f32(v[lane + 64]);
-    if (h < hq + hkv) {
-      const uint16_t* w = (h < hq) ? q_norm_w : k_norm_w;
-      const float inv = rsqrtf(wave_sum(a * a + b * b) / 128.f + eps);
-      a = bf16_round(bf16_round(a * inv) * bf16_to_f32(w[lane]));
-      b = bf16_round(bf16_round(b * inv) * bf16_to_f32(w[lane + 64]));
-      const float ra = bf16_round(bf16_round(a * c16) + bf16_round(-b * s16));
-      const float rb = bf16_round(bf16_round(b * c16) + bf16_round(a * s16));
-      if (h < hq) {
-        uint16_t* qo = q_out + ((int64_t)row * hq + h) * 128;
-        qo[lane] = f32_to_bf16(ra);
-        qo[lane + 64] = f32_to_bf16(rb);
-      } else {
-        write_vector<INT8, SDT>(ra, rb, lane, slot, h - hq, hkv, k_cache, k_scale);
-      }
+  if (h < hq + hkv) {
+    const uint16_t* w = (h < hq) ? q_norm_w : k_norm_w;
+    const float wa = bf16_to_f32(w[lane]), wb = bf16_to_f32(w[lane + 64]);
+    const int pos = min(max(positions[row], 0), rope_positions - 1);
+    const float c16 = bf16_to_f32(rope[(int64_t)pos * 128 + lane]);
+    const float s16 = bf16_to_f32(rope[(int64_t)pos * 128 + 64 + lane]);
+    const float inv = rsqrtf(wave_sum(a * a + b * b) / 128.f + eps);
+    a = bf16_round(bf16_round(a * inv) * wa);
+    b = bf16_round(bf16_round(b * inv) * wb);
+    const float ra = bf16_round(bf16_round(a * c16) + bf16_round(-b * s16));
+    const float rb = bf16_round(bf16_round(b * c16) + bf16_round(a * s16));
+    if (h < hq) {
+      uint16_t* qo = q_out + ((int64_t)row * hq + h) * 128;
+      qo[lane] = f32_to_bf16(ra);
+      qo[lane + 64] = f32_to_bf16(rb);
     } else {
-      write_vector<INT8, SDT>(a, b, lane, slot, h - hq - hkv, hkv, v_cache, v_scale);
+      write_vector<INT8, SDT>(ra, rb, lane, slot, h - hq, hkv, k_cache, k_scale);
     }
+  } else {
+    write_vector<INT8, SDT>(a, b, lane, slot, h - hq - hkv, hkv, v_cache, v_scale);
   }
 }
 
@@ -200,6 +221,20 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const uint16_t* vectors, 
 
 using namespace ne;
 
+// 8-element chunks per lane for a row of `hidden` elements (one wave per row)
+static int chunks_per_lane(int hidden) { return hidden <= 1024 ? 2 : hidden <= 2048 ? 4 : 8; }
+
+#define NE_NORM_LAUNCH(MODE, SPLITS, ...)                                                     \
+  do {                                                                                         \
+    const int cpl = chunks_per_lane(hidden);                                                   \
+    if (cpl == 2)                                                                              \
+      hipLaunchKernelGGL((rmsnorm_kernel<MODE, SPLITS, 2>), grid, block, 0, s, __VA_ARGS__);   \
+    else if (cpl == 4)                                                                         \
+      hipLaunchKernelGGL((rmsnorm_kernel<MODE, SPLITS, 4>), grid, block, 0, s, __VA_ARGS__);   \
+    else                                                                                       \
+      hipLaunchKernelGGL((rmsnorm_kernel<MODE, SPLITS, 8>), grid, block, 0, s, __VA_ARGS__);   \
+  } while (0)
+
 static int check_norm_args(const void* weight, const void* out, int32_t rows, int32_t hidden) {
   NE_CHECK_ARG(rows >= 0, "rows < 0");
   NE_CHECK_ARG(weight && out, "null pointer argument");
@@ -215,9 +250,10 @@ extern "C" int ne_rmsnorm(const void* x, const void* weight, void* out, int32_t 
   if (rc != NE_OK) return rc;
   NE_CHECK_ARG(x != nullptr, "null x");
   if (rows == 0) return NE_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr,
-                     (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps);
+  const dim3 grid(ceil_div(rows, 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  NE_NORM_LAUNCH(0, 0, (const uint16_t*)x, nullptr, nullptr, nullptr, nullptr,
+                 (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps, nullptr);
   return check_launch("rmsnorm");
 }
 
@@ -227,9 +263,10 @@ extern "C" int ne_add_rmsnorm(void* residual, const void* delta, const void* wei
   if (rc != NE_OK) return rc;
   NE_CHECK_ARG(residual && delta, "null residual/delta");
   if (rows == 0) return NE_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
-                     nullptr, (uint16_t*)residual, (const uint16_t*)delta, nullptr, nullptr,
-                     (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps);
+  const dim3 grid(ceil_div(rows, 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  NE_NORM_LAUNCH(1, 0, nullptr, (uint16_t*)residual, (const uint16_t*)delta, nullptr, nullptr,
+                 (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps, nullptr);
   return check_launch("add_rmsnorm");
 }
 
@@ -239,12 +276,38 @@ extern "C" int ne_splitk_add_rmsnorm(void* residual, const float* partials, int3
   int rc = check_norm_args(weight, out, rows, hidden);
   if (rc != NE_OK) return rc;
   NE_CHECK_ARG(residual && partials, "null residual/partials");
-  NE_CHECK_ARG(splits >= 1 && splits <= 64, "splits must be in [1, 64] (got %d)", splits);
+  NE_CHECK_ARG(splits >= 1, "splits must be >= 1 (got %d)", splits);
   NE_CHECK_ARG(((uintptr_t)partials % 16) == 0, "partials must be 16-byte aligned");
   if (rows == 0) return NE_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel<3>, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
-                     nullptr, (uint16_t*)residual, nullptr, nullptr, nullptr,
-                     (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps, partials, splits);
+  const dim3 grid(ceil_div(rows, 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  // the partials of SPLITS x CPL chunks stay in registers: keep that product small
+  NE_CHECK_SUPPORTED(splits * chunks_per_lane(hidden) <= 16,
+                     "splits x hidden too large for the fused split-K norm (splits=%d, hidden=%d)",
+                     splits, hidden);
+#define NE_SPLITK_NORM(S, C)                                                                  \
+  hipLaunchKernelGGL((rmsnorm_kernel<3, S, C>), grid, block, 0, s, nullptr, (uint16_t*)residual, \
+                     nullptr, nullptr, nullptr, (const uint16_t*)weight, (uint16_t*)out, rows,    \
+                     hidden, eps, partials)
+  const int cpl = chunks_per_lane(hidden);
+  switch (splits * 16 + cpl) {
+    case 1 * 16 + 2: NE_SPLITK_NORM(1, 2); break;
+    case 2 * 16 + 2: NE_SPLITK_NORM(2, 2); break;
+    case 3 * 16 + 2: NE_SPLITK_NORM(3, 2); break;
+    case 4 * 16 + 2: NE_SPLITK_NORM(4, 2); break;
+    case 6 * 16 + 2: NE_SPLITK_NORM(6, 2); break;
+    case 8 * 16 + 2: NE_SPLITK_NORM(8, 2); break;
+    case 1 * 16 + 4: NE_SPLITK_NORM(1, 4); break;
+    case 2 * 16 + 4: NE_SPLITK_NORM(2, 4); break;
+    case 3 * 16 + 4: NE_SPLITK_NORM(3, 4); break;
+    case 4 * 16 + 4: NE_SPLITK_NORM(4, 4); break;
+    case 1 * 16 + 8: NE_SPLITK_NORM(1, 8); break;
+    case 2 * 16 + 8: NE_SPLITK_NORM(2, 8); break;
+    default:
+      set_error("splits must be 1, 2, 3, 4, 6 or 8 (got %d)", splits);
+      return NE_EUNSUPPORTED;
+  }
+#undef NE_SPLITK_NORM
   return check_launch("splitk_add_rmsnorm");
 }
 
@@ -255,9 +318,10 @@ extern "C" int ne_embed_rmsnorm(const int32_t* tokens, const void* embed, const 
   if (rc != NE_OK) return rc;
   NE_CHECK_ARG(tokens && embed && residual, "null tokens/embed/residual");
   if (rows == 0) return NE_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
-                     nullptr, (uint16_t*)residual, nullptr, tokens, (const uint16_t*)embed,
-                     (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps);
+  const dim3 grid(ceil_div(rows, 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  NE_NORM_LAUNCH(2, 0, nullptr, (uint16_t*)residual, nullptr, tokens, (const uint16_t*)embed,
+                 (const uint16_t*)weight, (uint16_t*)out, rows, hidden, eps, nullptr);
   return check_launch("embed_rmsnorm");
 }
 
@@ -265,7 +329,8 @@ extern "C" int ne_qk_norm_rope_kv_write(const void* qkv, int32_t rows, int32_t n
                                         int32_t num_kv_heads, int32_t head_dim,
                                         const void* q_norm_weight, const void* k_norm_weight,
                                         float eps, const int32_t* positions,
-                                        const float* inv_freq, const int32_t* slot_mapping,
+                                        const void* rope_cos_sin, int32_t rope_positions,
+                                        const int32_t* slot_mapping,
                                         void* k_cache, void* v_cache, void* k_scale,
                                         void* v_scale, int32_t kv_dtype, int32_t scale_dtype,
                                         void* q_out, void* stream) {
@@ -273,16 +338,19 @@ extern "C" int ne_qk_norm_rope_kv_write(const void* qkv, int32_t rows, int32_t n
   if (rows == 0) return NE_OK;
   NE_CHECK_SUPPORTED(head_dim == 128, "head_dim must be 128 (got %d)", head_dim);
   NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0, "bad head counts");
-  NE_CHECK_ARG(qkv && q_norm_weight && k_norm_weight && positions && inv_freq && slot_mapping &&
+  NE_CHECK_ARG(qkv && q_norm_weight && k_norm_weight && positions && rope_cos_sin && slot_mapping &&
                    k_cache && v_cache && q_out,
                "null pointer argument");
+  NE_CHECK_ARG(rope_positions > 0, "rope_positions must be positive");
   NE_CHECK_ARG(kv_dtype == NE_DTYPE_BF16 || kv_dtype == NE_DTYPE_INT8,
                "kv_dtype must be bf16 or int8");
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(rows), block(256);
+  const int heads = num_q_heads + 2 * num_kv_heads;
+  const dim3 grid((unsigned)rows * (unsigned)ceil_div(heads, 4)), block(256);
 #define NE_QKR_ARGS                                                                              \
   (const uint16_t*)qkv, num_q_heads, num_kv_heads, (const uint16_t*)q_norm_weight,              \
-      (const uint16_t*)k_norm_weight, eps, positions, inv_freq, slot_mapping, k_cache, v_cache, \
+      (const uint16_t*)k_norm_weight, eps, positions, (const uint16_t*)rope_cos_sin,           \
+      rope_positions, slot_mapping, k_cache, v_cache,                                          \
       k_scale, v_scale, (uint16_t*)q_out
   if (kv_dtype == NE_DTYPE_BF16) {
     hipLaunchKernelGGL((qk_norm_rope_kv_kernel<false, NE_DTYPE_BF16>), grid, block, 0, s,

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -81,7 +81,7 @@ SIGNATURES: dict[str, tuple] = {
         [
             _vp, _i32, _i32, _i32, _i32,  # qkv, rows, heads, kv heads, head dim
             _vp, _vp, _f32,  # norm weights, eps
-            _vp, _vp, _vp,  # positions, inv_freq, slot mapping
+            _vp, _vp, _i32, _vp,  # positions, rope table, its positions, slot mapping
             _vp, _vp, _vp, _vp, _i32, _i32,  # caches, scales, dtypes
             _vp, _vp,  # q_out, stream
         ],

@@ -394,6 +394,16 @@ def embed_rmsnorm(tokens: torch.Tensor, embed: torch.Tensor, weight: torch.Tenso
     return residual, out
 
 
+def rope_table(positions: int, rope_theta: float, head_dim: int = HEAD_DIM) -> torch.Tensor:
+    """[positions, 2, head_dim / 2] bf16 cos | sin on the CPU, built exactly as
+    build_rotary_tables does (ne/models/qwen3.py:47-57): fp32 inverse frequencies,
+    fp32 angles position * inv_freq, cos/sin in fp32, then rounded to bf16."""
+    exps = torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim
+    inv_freq = 1.0 / (rope_theta**exps)
+    angles = torch.arange(positions).float()[:, None] * inv_freq
+    return torch.stack([angles.cos(), angles.sin()], dim=1).to(torch.bfloat16).contiguous()
+
+
 def qk_norm_rope_kv_write(
     qkv: torch.Tensor,
     num_q_heads: int,
@@ -402,7 +412,7 @@ def qk_norm_rope_kv_write(
     k_norm_weight: torch.Tensor,
     eps: float,
     positions: torch.Tensor,
-    inv_freq: torch.Tensor,
+    rope_cos_sin: torch.Tensor,
     slot_mapping: torch.Tensor,
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
@@ -410,12 +420,13 @@ def qk_norm_rope_kv_write(
     v_scale: torch.Tensor | None,
     q_out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    device = _require_gpu(qkv, q_norm_weight, k_norm_weight, positions, inv_freq, slot_mapping,
+    device = _require_gpu(qkv, q_norm_weight, k_norm_weight, positions, rope_cos_sin, slot_mapping,
                           k_cache, v_cache)
     _contig(qkv, "qkv")
     _int32(positions, "positions")
     _int32(slot_mapping, "slot_mapping")
-    _check(inv_freq.dtype == torch.float32 and inv_freq.numel() == HEAD_DIM // 2, "inv_freq [64] fp32")
+    _check(rope_cos_sin.dtype == torch.bfloat16 and rope_cos_sin.dim() == 3 and rope_cos_sin.shape[1:] == (2, 64)
+           and rope_cos_sin.is_contiguous(), "rope_cos_sin must be contiguous [positions, 2, 64] bf16")
     rows = qkv.shape[0]
     _check(qkv.shape[1] == (num_q_heads + 2 * num_kv_heads) * HEAD_DIM, "qkv width mismatch")
     if q_out is None:
@@ -425,7 +436,7 @@ def qk_norm_rope_kv_write(
         "ne_qk_norm_rope_kv_write",
         _ptr(qkv), rows, num_q_heads, num_kv_heads, HEAD_DIM,
         _ptr(q_norm_weight), _ptr(k_norm_weight), float(eps),
-        _ptr(positions), _ptr(inv_freq), _ptr(slot_mapping),
+        _ptr(positions), _ptr(rope_cos_sin), rope_cos_sin.shape[0], _ptr(slot_mapping),
         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
         dtype_code(k_cache.dtype), dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16,
         _ptr(q_out), _stream(device),

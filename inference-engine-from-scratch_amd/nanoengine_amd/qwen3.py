@@ -219,9 +219,11 @@ class Qwen3VerifyModel:
         self.q = torch.empty(max_rows, c.num_attention_heads, c.head_dim, **bf)
         self.attn = torch.empty(max_rows, c.num_attention_heads, c.head_dim, **bf)
         self.act = torch.empty(max_rows, c.intermediate_size, **bf)
-        exps = torch.arange(0, c.head_dim, 2, dtype=torch.float32) / c.head_dim
-        # qwen3.py:51-54, computed once in fp32 on the host as the reference does per step
-        self.inv_freq = (1.0 / (c.rope_theta**exps)).to(device)
+        # cos/sin per position (qwen3.py:47-57), computed once on the host as the
+        # reference computes them per step; grown when a longer position appears
+        self.rope_positions = 0
+        self.rope = None
+        self.ensure_rope(4096)
         self.workspace = kernels.AttentionWorkspace()
         self.softmax_scale = 1.0 / math.sqrt(c.head_dim)
         # o_proj / down_proj (N = hidden) split K across work-groups when the rows alone
@@ -230,6 +232,12 @@ class Qwen3VerifyModel:
         self.down_splits = [kernels.splitk_splits(r, h, c.intermediate_size) for r in range(max_rows + 1)]
         most = max(max(a * r, b * r) for r, (a, b) in enumerate(zip(self.o_splits, self.down_splits)))
         self.partials = torch.empty(max(most, 1) * h, dtype=torch.float32, device=device)
+
+    def ensure_rope(self, positions: int) -> None:
+        """Make the RoPE table cover positions 0 .. positions-1 (before any graph capture)."""
+        if positions > self.rope_positions:
+            self.rope = kernels.rope_table(positions, self.config.rope_theta).to(self.device)
+            self.rope_positions = positions
 
     def forward(self, rows: int, tokens: torch.Tensor, batch: AttentionBatch, pool) -> torch.Tensor:
         """Hidden states after the final norm for ``rows`` packed query rows; writes this
@@ -246,7 +254,7 @@ class Qwen3VerifyModel:
             kernels.w8a16_gemm(normed, layer.qkv_int8, layer.qkv_scale, out=qkv)
             kernels.qk_norm_rope_kv_write(
                 qkv, c.num_attention_heads, c.num_key_value_heads, layer.q_norm, layer.k_norm, eps,
-                batch.positions[:rows], self.inv_freq, batch.slot_mapping[:rows],
+                batch.positions[:rows], self.rope, batch.slot_mapping[:rows],
                 pool.key_caches[i], pool.value_caches[i], pool.key_scale_2d(i), pool.value_scale_2d(i),
                 q_out=q,
             )

@@ -75,6 +75,7 @@ class VerifyRunner:
         self.capacity = max_model_len + self.R
         self.max_blocks = math.ceil(self.capacity / self.block_size)
         self.use_graph = use_graph
+        model.ensure_rope(self.capacity)
         if self.max_seqs * self.R > model.max_rows:
             raise ValueError("model activation buffers are smaller than max_seqs * (k + 1) rows")
         dev = self.device

@@ -1,0 +1,126 @@
+"""Host-side logic of the product package (CPU only): settings, allocator, random
+initialisation order, RoPE table, split choices.  No kernel is launched."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from nanoengine_amd import kernels
+from nanoengine_amd.config import EngineSettings
+from nanoengine_amd.interface import SamplingParams, num_guesses
+from nanoengine_amd.memory import OutOfKVMemoryError, PagedSlotAllocator, count_kv_bytes_per_token
+from nanoengine_amd.qwen3 import Qwen3Config, pair_rows, quantize_rows, random_state_dict
+from oracle import model as om
+from oracle import quant as oq
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+CPU = torch.device("cpu")
+
+
+def test_random_init_matches_the_module_built_reference_order():
+    """Drawing every parameter in registration order after the constructors' own draws
+    gives the same tensors as building the modules (nt/conftest.py:38-43 pattern)."""
+    cfg = Qwen3Config(64, 32, 64, 2, 4, 2, 16, 1e-6, 1e4, True)
+    ours = random_state_dict(cfg, seed=7, std=0.5)
+    ref = om.build_random_model(om.Qwen3Config(64, 32, 64, 2, 4, 2, 16, 1e-6, 1e4, True), seed=7, std=0.5)
+    ref_state = ref.state_dict()
+    assert set(ours) == set(ref_state)
+    for name, t in ours.items():
+        assert torch.equal(t, ref_state[name]), name
+
+
+def test_rope_table_equals_the_reference_tables_bit_for_bit():
+    positions = torch.tensor([[0, 1, 5, 127, 4095, 16999]])
+    cos, sin = om.build_rotary_tables(positions, 128, 1e6, torch.bfloat16)
+    table = kernels.rope_table(17000, 1e6)
+    got = table[positions[0]]
+    assert torch.equal(got[:, 0], cos[0, 0, :, :64]) and torch.equal(got[:, 1], sin[0, 0, :, :64])
+    assert torch.equal(cos[..., :64], cos[..., 64:])  # dims i and i + 64 share the angle
+
+
+def test_weight_quantisation_matches_int8_linear_from_linear():
+    w = torch.randn(48, 64).to(torch.bfloat16)
+    q, s = quantize_rows(w)
+    rq, rs = oq.quantize_linear(w)
+    assert torch.equal(q, rq) and torch.equal(s, rs)
+
+
+def test_gate_up_pairing_interleaves_groups_of_16_rows():
+    gate = torch.arange(32)[:, None].expand(32, 2)
+    up = 100 + torch.arange(32)[:, None].expand(32, 2)
+    paired = pair_rows(gate, up)[:, 0].tolist()
+    assert paired == list(range(16)) + list(range(100, 116)) + list(range(16, 32)) + list(range(116, 132))
+
+
+def test_kv_bytes_per_token_reference_kat():
+    kat = KATS["kv_bytes_per_token"]
+    assert count_kv_bytes_per_token(28, 8, 128, torch.float16, is_int8_cache=True) == kat["int8_fp16"]
+    assert count_kv_bytes_per_token(28, 8, 128, torch.float16) == kat["fp16"]
+
+
+def test_paged_allocator_reference_kat_and_rollback_frees_nothing():
+    kat = KATS["paged_allocator_growth"]
+    alloc = PagedSlotAllocator(kat["num_blocks"], kat["block_size"], CPU)
+    for n in kat["reserve"]:
+        alloc.reserve("r", n)
+    assert alloc.block_table("r") == kat["expected_table"]
+    assert alloc.build_context_slots(["r"], kat["context_length"]).tolist() == kat["expected_slots"]
+    # a shorter reservation (a rollback of rejected guesses) keeps every block
+    alloc.reserve("r", 1)
+    assert alloc.block_table("r") == kat["expected_table"]
+    with pytest.raises(OutOfKVMemoryError):
+        alloc.reserve("r", 100)
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.lists(st.tuples(st.integers(0, 5), st.integers(0, 40), st.booleans()), max_size=40))
+def test_allocator_never_loses_or_shares_a_block(ops):
+    """nt/engine/test_memory_allocators.py:68-89: every block is either free or owned by
+    exactly one request, whatever the sequence of reserves and frees."""
+    alloc = PagedSlotAllocator(16, 4, CPU)
+    for rid, n, free in ops:
+        name = f"r{rid}"
+        if free:
+            alloc.free(name)
+        else:
+            try:
+                alloc.reserve(name, n)
+            except OutOfKVMemoryError:
+                pass
+        owned = [b for i in range(6) for b in alloc.block_table(f"r{i}")]
+        assert len(owned) == len(set(owned))
+        assert len(owned) + alloc.num_free_blocks == 16
+
+
+def test_settings_select_the_hip_path_and_keep_the_reference_checks():
+    ok = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", quantization="int8",
+                        kv_cache_dtype="int8", speculative="ngram", scheduler="continuous")
+    assert ok.hip_verify_path_error() is None
+    assert "dtype" in EngineSettings(device="cuda", kv_cache="paged", quantization="int8",
+                                     speculative="ngram").hip_verify_path_error()
+    with pytest.raises(ValueError):  # ne/config.py:91-97: speculation without a KV cache
+        EngineSettings(speculative="ngram")
+    with pytest.raises(ValueError):  # speculation with the prefix cache stays refused
+        EngineSettings(kv_cache="paged", prefix_cache=True, speculative="ngram")
+    env = {"NANOENGINE_DEVICE": "cuda", "NANOENGINE_KV_CACHE": "paged", "NANOENGINE_CUDA_GRAPHS": "true",
+           "NANOENGINE_NUM_SPECULATIVE_TOKENS": "8"}
+    s = EngineSettings.from_env(env)
+    assert s.device == "cuda" and s.cuda_graphs is True and s.num_speculative_tokens == 8
+
+
+def test_num_guesses_never_passes_the_length_limit():
+    p = SamplingParams(max_new_tokens=128)
+    assert [num_guesses(p, n, 4) for n in (0, 124, 126, 127)] == [4, 3, 1, 0]
+
+
+def test_splitk_split_counts_fill_the_gpu_and_divide_k():
+    for rows in (1, 5, 80, 320, 4096):
+        for k in (2048, 3072):
+            s = kernels.splitk_splits(rows, 1024, k)
+            assert s in (1, 2, 3, 4) and k % (128 * s) == 0

@@ -111,7 +111,7 @@ def test_qk_norm_rope_kv_write(device, kv_dtype):
     kn = (torch.randn(128) * 0.5 + 1).to(torch.bfloat16)
     positions = torch.randint(0, 17000, (rows,), dtype=torch.int32)
     slots = torch.randperm(200)[:rows].to(torch.int32)
-    inv_freq = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    rope = kernels.rope_table(17000, 1e6)
     is_int8 = kv_dtype == "int8"
     cdt = torch.int8 if is_int8 else torch.bfloat16
     kc = torch.zeros(201, hkv, 128, dtype=cdt, device=device)
@@ -120,7 +120,7 @@ def test_qk_norm_rope_kv_write(device, kv_dtype):
     vs = torch.zeros(201, hkv, dtype=torch.bfloat16, device=device) if is_int8 else None
     q_out = kernels.qk_norm_rope_kv_write(
         qkv.to(device), hq, hkv, qn.to(device), kn.to(device), EPS, positions.to(device),
-        inv_freq.to(device), slots.to(device), kc, vc, ks, vs)
+        rope.to(device), slots.to(device), kc, vc, ks, vs)
     torch.cuda.synchronize()
     # oracle: q_norm / k_norm then RoPE in bf16 (qwen3.py:100-104)
     q = qkv[:, : hq * 128].view(1, rows, hq, 128)
