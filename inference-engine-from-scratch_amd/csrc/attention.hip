@@ -84,9 +84,13 @@ struct AttnParams {
   float qk_scale;  // softmax_scale * log2(e)
   uint16_t* out;
   int64_t o_tok_stride, o_head_stride;
-  float* part_o;       // [units][max_splits][16][128]
-  float* part_ml;      // [units][max_splits][16][2]
+  float* part_o;       // [units][max_splits][16][128], or [plan_grid][kv heads][16][128]
+  float* part_ml;      // [units][max_splits][16][2], or [plan_grid][kv heads][16][2]
   uint32_t* error_flag;
+  int32_t* plan;       // DMA kernel: first work-group of each sequence, then the total
+  int32_t plan_w;      // DMA kernel: tiles per split (0: derived from the total work)
+  int32_t plan_grid;   // DMA kernel: work-groups launched
+  int32_t max_ctx;     // the caller's bound on ctx_len
 };
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -609,7 +613,118 @@ constexpr int kTileRows = kTileKeys * kRowBytes;     // 2 KB: one head's K (or V
 constexpr int kScaleBytes = kTileKeys * kHeadWaves * 2;  // 256 B: a tile's scales, all heads
 constexpr int kDmaSlot = 2 * kTileRows + 2 * kScaleBytes;  // K | V | k-scales | v-scales
 constexpr int kDmaPerTile = 6;                       // 2 K + 2 V (1 KB each) + 2 scale dwords
-constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4 + kHeadWaves * kWave * 4;
+constexpr int kPlanInts = 32;                        // LDS ints of the work plan
+constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4 + kHeadWaves * kWave * 4 +
+                        kPlanInts * 4;
+constexpr int kPlanMaxSeqs = 2 * kHeadWaves * kWave;  // two sequences per thread
+constexpr int kPlanMinTiles = 16;                     // no split shorter than 256 keys
+constexpr int kPlanCUs = 256;                         // work-groups the plan aims to fill
+
+// Work plan of the DMA kernel.  Sequence b has tiles_b = ceil(ctx_b / 16) 16-key
+// tiles and gets n_b = ceil(tiles_b / W) splits of near-equal length (split s
+// covers tiles [tiles_b s / n_b, tiles_b (s+1) / n_b)).  W is p.plan_w when the
+// caller fixed the split length, else max(16, ceil(T / (G - B))) for T = sum_b
+// tiles_b, G = p.plan_grid work-groups and B sequences, which keeps sum_b n_b <= G:
+// the longest sequence is spread over as many work-groups as its share of T asks
+// for instead of one per fixed-length split, and no CU waits for a second round
+// of work-groups.  Work-group w serves split w - N_b of the sequence with
+// N_b <= w < N_{b+1} (N = exclusive prefix sum of n).  Every work-group derives
+// the same plan from ctx_len; work-group 0 also stores N (and N_B) for the merge.
+struct PlanItem {
+  int seq, split, n_splits, tiles, ctx, ql, qs;
+};
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+// Called by all threads of the work-group; false when the work-group has no work.
+__device__ bool plan_item(const AttnParams& p, int* s_plan, PlanItem& item) {
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int B = p.num_seqs;
+  int ctx[2], ql[2], qs[2], tiles[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = 2 * tid + k;
+    const bool ok = i < B;
+    ctx[k] = ok ? p.ctx_len[i] : 0;
+    ql[k] = ok ? p.q_len[i] : 0;
+    qs[k] = ok ? p.q_start[i] : 0;
+  }
+  // a context beyond the caller's bound is flagged and clipped to it, so that no
+  // block-table entry past max_ctx is read
+  if (blockIdx.x == 0 && (ctx[0] > p.max_ctx || ctx[1] > p.max_ctx)) atomicOr(p.error_flag, 1u);
+  ctx[0] = min(ctx[0], p.max_ctx);
+  ctx[1] = min(ctx[1], p.max_ctx);
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    tiles[k] = (ql[k] > 0 && ctx[k] > 0) ? (ctx[k] + kTileKeys - 1) / kTileKeys : 0;
+  if (tid == 0) s_plan[16] = -1;
+  const int tsum = wave_sum(tiles[0] + tiles[1]);
+  if (lane == 0) s_plan[wave] = tsum;
+  __syncthreads();
+  int T = 0;
+#pragma unroll
+  for (int w = 0; w < kHeadWaves; ++w) T += s_plan[w];
+  const int G = p.plan_grid;
+  int W = p.plan_w;
+  if (W <= 0) W = max(kPlanMinTiles, (T + (G - B) - 1) / (G - B));
+  if (W > kMaxTiles) {
+    if (tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
+    W = kMaxTiles;
+  }
+  const int n0 = (tiles[0] + W - 1) / W;
+  const int n1 = (tiles[1] + W - 1) / W;
+  const int c = n0 + n1;
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(incl, d);
+    if (lane >= d) incl += y;
+  }
+  if (lane == kWave - 1) s_plan[8 + wave] = incl;
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kHeadWaves; ++w) {
+    const int x = s_plan[8 + w];
+    base += (w < wave) ? x : 0;
+    total += x;
+  }
+  const int N0 = base + incl - c;
+  const int N1 = N0 + n0;
+  if (blockIdx.x == 0) {
+    if (2 * tid < B) p.plan[2 * tid] = N0;
+    if (2 * tid + 1 < B) p.plan[2 * tid + 1] = N1;
+    if (tid == 0) p.plan[B] = total;
+  }
+  if (total > G && tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
+  const int w = blockIdx.x;
+  const int k = (w >= N0 && w < N1) ? 0 : ((w >= N1 && w < N1 + n1) ? 1 : -1);
+  if (k >= 0) {
+    s_plan[16] = 2 * tid + k;
+    s_plan[17] = w - (k ? N1 : N0);
+    s_plan[18] = k ? n1 : n0;
+    s_plan[19] = k ? tiles[1] : tiles[0];
+    s_plan[20] = k ? ctx[1] : ctx[0];
+    s_plan[21] = k ? ql[1] : ql[0];
+    s_plan[22] = k ? qs[1] : qs[0];
+  }
+  __syncthreads();
+  item.seq = s_plan[16];
+  if (item.seq < 0) return false;
+  item.split = s_plan[17];
+  item.n_splits = s_plan[18];
+  item.tiles = s_plan[19];
+  item.ctx = s_plan[20];
+  item.ql = s_plan[21];
+  item.qs = s_plan[22];
+  return true;
+}
 
 __device__ __forceinline__ void lds_dma(const void* src, void* lds, int bytes) {
   if (bytes == 16) {
@@ -685,68 +800,62 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* s_slot = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot);
   float* s_sc_all = (float*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4);
+  int* s_plan = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4 + kHeadWaves * kWave * 4);
 
-  // ---- work item (one sequence's M tile and split; the wave is the KV head) ----
-  const int bid = blockIdx.x;
-  const int split = bid % p.max_splits;
-  const int mt = (bid / p.max_splits) % p.mtiles;
-  const int seq = bid / (p.max_splits * p.mtiles);
+  // ---- work item: one split of one sequence (M tile 0); the wave is the KV head ----
   const int tid = threadIdx.x;
   const int head = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const UnitInfo u0 = unit_info(p, seq * p.num_kv_heads * p.mtiles + mt);
-  if (u0.row0 >= u0.rows_total) return;
-  int n_splits = u0.n_splits;
-  if (n_splits > p.max_splits) {
-    if (tid == 0 && split == 0) atomicOr(p.error_flag, 1u);
-    n_splits = p.max_splits;
-  }
-  if (split >= n_splits) return;
-  const int kstart = split * p.split_len;
-  const int kend = min(u0.kend_unit, kstart + p.split_len);
-  const int ql = u0.ql;
+  PlanItem item;
+  if (!plan_item(p, s_plan, item)) return;
+  const int seq = item.seq;
+  const int n_splits = item.n_splits;
+  const int j0 = (int)((int64_t)item.tiles * item.split / n_splits);
+  const int j1 = (int)((int64_t)item.tiles * (item.split + 1) / n_splits);
+  const int kstart = j0 * kTileKeys;
+  const int kend = min(item.ctx, j1 * kTileKeys);
+  const int n_tiles = j1 - j0;
+  const int ql = item.ql;
+  const int rows_total = p.group * ql;
+  if (rows_total > kRows && tid == 0) atomicOr(p.error_flag, 1u);
 
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const bool row_valid = r < rows_total;
+  const int h_local = row_valid ? r / ql : 0;
+  const int qi = row_valid ? r % ql : 0;
+  const int kend_row = row_valid ? min(kend, item.ctx - ql + qi + 1) : kend;
+
+  // Q and the split's block-table entries are fetched together; Q is converted
+  // only after the ring's first copies are issued, so no wait sits between them
+  u32x4 raw[4] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+  if (row_valid) {
+    const int64_t qoff = (int64_t)(item.qs + qi) * p.q_tok_stride +
+                         (int64_t)(head * p.group + h_local) * p.q_head_stride + 32 * g;
+    const u32x4* src = (const u32x4*)(p.q + qoff);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) raw[c] = src[c];
+  }
   const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
-  const int n_tiles = (kend - kstart + kTileKeys - 1) / kTileKeys;
   for (int t = tid; t < n_tiles; t += kHeadWaves * kWave) {
     const int key0 = kstart + kTileKeys * t;
     s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
   }
   __syncthreads();  // s_slot ready
 
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  const int R = u0.row0 + r;
-  const bool row_valid = R < u0.rows_total;
-  const int h_local = row_valid ? R / ql : 0;
-  const int qi = row_valid ? R % ql : 0;
-  const int kend_row = row_valid ? min(kend, u0.ctx - ql + qi + 1) : kend;
-
-  // Q first: its registers are then ready without waiting for the ring's copies
-  QFrag<true> qf;
-  {
-    u32x4 raw[4] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
-    if (row_valid) {
-      const int64_t qoff = (int64_t)(u0.qs + qi) * p.q_tok_stride +
-                           (int64_t)(head * p.group + h_local) * p.q_head_stride + 32 * g;
-      const u32x4* src = (const u32x4*)(p.q + qoff);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) raw[c] = src[c];
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4 hv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[c][i] & 0xFFFFu)),
-                           bf16_to_f32((uint16_t)(raw[c][i] >> 16)));
-      qf.q[c] = __builtin_bit_cast(f16x8, hv);
-    }
-  }
-
   char* ring = smem + head * (kDmaRing * kDmaSlot);
 #pragma unroll
   for (int j = 0; j < kDmaRing; ++j) dma_tile(p, s_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
+  QFrag<true> qf;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    u32x4 hv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[c][i] & 0xFFFFu)),
+                         bf16_to_f32((uint16_t)(raw[c][i] >> 16)));
+    qf.q[c] = __builtin_bit_cast(f16x8, hv);
+  }
 
   float m = kNegBig, l = 0.f;
   floatx4 o[8];
@@ -763,7 +872,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     const int kb = kstart + it * kIterKeys;
     IterRegs<true> A;
     lds_iter<SDT>(sa, sb, kb, kend, head, lane, A);
-    compute_iter<true>(p, A, qf, sc_row, kb, kend_row, u0.ctx, lane, m, l, o);
+    compute_iter<true>(p, A, qf, sc_row, kb, kend_row, item.ctx, lane, m, l, o);
     // the two slots are free once their reads have returned: refill them
     dma_wait_lgkmcnt0();
     dma_tile(p, s_slot, n_tiles, 2 * it + kDmaRing, head, lane, ring + ((2 * it) % kDmaRing) * kDmaSlot);
@@ -776,9 +885,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   if (!row_valid) return;
 
   // lane (r, g) holds row r, dims 32g + 8i + j in o[j][i]
-  const int unit = (seq * p.num_kv_heads + head) * p.mtiles + mt;
   if (n_splits == 1) {
-    uint16_t* dst = p.out + (int64_t)(u0.qs + qi) * p.o_tok_stride +
+    uint16_t* dst = p.out + (int64_t)(item.qs + qi) * p.o_tok_stride +
                     (int64_t)(head * p.group + h_local) * p.o_head_stride + 32 * g;
     const float inv = 1.f / l;
 #pragma unroll
@@ -790,7 +898,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
       *(u32x4*)(dst + 8 * i) = bits;
     }
   } else {
-    const int64_t pbase = ((int64_t)unit * p.max_splits + split) * kRows + r;
+    // partial slot: this work-group's index, which the plan gives the merge too
+    const int64_t pbase = ((int64_t)blockIdx.x * kHeadWaves + head) * kRows + r;
     float* po = p.part_o + pbase * kHeadDim + 32 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -802,6 +911,48 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
       p.part_ml[pbase * 2 + 1] = l;
     }
   }
+}
+
+// Combines the partials of every sequence the plan split: one work-group per
+// (sequence, KV head), 16 threads per row, 8 dims per thread; partial k of the
+// sequence is work-group N_b + k's.
+__global__ __launch_bounds__(256) void attention_plan_merge_kernel(AttnParams p) {
+  const int seq = blockIdx.x / kHeadWaves;
+  const int head = blockIdx.x % kHeadWaves;
+  const int first = p.plan[seq];
+  const int last = min(p.plan[seq + 1], p.plan_grid);
+  const int n_splits = last - first;
+  if (n_splits <= 1) return;
+  const int ql = p.q_len[seq];
+  const int crow = threadIdx.x >> 4;
+  const int cd = (threadIdx.x & 15) * 8;
+  if (crow >= min(p.group * ql, kRows)) return;
+  float MM = kNegBig;
+  for (int s = 0; s < n_splits; ++s) {
+    const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kRows + crow;
+    MM = fmaxf(MM, p.part_ml[pi * 2]);
+  }
+  float LL = 0.f;
+  float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < n_splits; ++s) {
+    const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kRows + crow;
+    const float a = __builtin_amdgcn_exp2f(p.part_ml[pi * 2] - MM);
+    LL += a * p.part_ml[pi * 2 + 1];
+    const float* src = p.part_o + pi * kHeadDim + cd;
+    const floatx4 x0 = *(const floatx4*)src;
+    const floatx4 x1 = *(const floatx4*)(src + 4);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      tot[d] += a * x0[d];
+      tot[d + 4] += a * x1[d];
+    }
+  }
+  const int ch = crow / ql, ci = crow % ql;
+  uint16_t* dst = p.out + (int64_t)(p.q_start[seq] + ci) * p.o_tok_stride +
+                  (int64_t)(head * p.group + ch) * p.o_head_stride + cd;
+  const float inv = 1.f / LL;
+  *(u32x4*)dst = u32x4{pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv),
+                       pack_bf16x2(tot[4] * inv, tot[5] * inv), pack_bf16x2(tot[6] * inv, tot[7] * inv)};
 }
 
 // Combines the split partials of every unit that has more than one split:
@@ -844,9 +995,25 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
 }
 
 struct Layout {
-  int group, mtiles, units, split_len, max_splits;
-  size_t part_o_off, part_ml_off, error_off, total;
+  int group, mtiles, units, split_len, max_splits, plan_grid, plan_w;
+  size_t part_o_off, part_ml_off, error_off, plan_off, total;
 };
+
+// Work-groups of the DMA kernel's plan: enough that W <= kMaxTiles for any
+// contexts up to max_ctx (G - B >= B ceil(max_ctx / 16) / kMaxTiles) and that G - B
+// >= B; at least one per CU.  With a fixed split length, one per split.
+int plan_grid(int num_seqs, int max_ctx, int split_len) {
+  const int64_t max_tiles = ((int64_t)max(max_ctx, 1) + kTileKeys - 1) / kTileKeys;
+  if (split_len > 0) {
+    const int64_t w = split_len / kTileKeys;
+    return (int)((int64_t)num_seqs * ((max_tiles + w - 1) / w));
+  }
+  const int64_t need = num_seqs + ((int64_t)num_seqs * max_tiles + kMaxTiles - 1) / kMaxTiles;
+  int64_t g = 2 * (int64_t)num_seqs;
+  if (g < kPlanCUs) g = kPlanCUs;
+  if (g < need) g = need;
+  return (int)g;
+}
 
 // Default split: about 512 KB of K/V per work-group (256 keys of int8, 128 of bf16,
 // across 8 KV heads), the best of a sweep over 128..1024 keys on the 64-sequence
@@ -863,6 +1030,7 @@ Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_le
   L.group = num_q_heads / num_kv_heads;
   L.mtiles = ceil_div((int64_t)L.group * max_q_len, kRows);
   L.units = num_seqs * num_kv_heads * L.mtiles;
+  const int fixed_split = split_len > 0 ? split_len : 0;  // 0: the caller left it to us
   if (split_len <= 0) split_len = default_split_len(kv_dtype, max_ctx);
   L.split_len = split_len;
   L.max_splits = max(1, ceil_div(max(max_ctx, 1), split_len));
@@ -874,10 +1042,19 @@ Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_le
   };
   // error flag at byte 0, so callers can inspect and clear it without knowing the
   // partial-sum layout that follows
-  const size_t parts = (L.max_splits > 1) ? (size_t)L.units * L.max_splits * kRows : 0;
+  // the fixed-split kernels index partials by (unit, split); the DMA kernel's plan
+  // by (work-group, KV head) and needs (B + 1) plan entries
+  const bool plan = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && L.mtiles == 1;
+  L.plan_grid = plan ? plan_grid(num_seqs, max_ctx, fixed_split) : 0;
+  L.plan_w = fixed_split / kTileKeys;
+  size_t parts = (L.max_splits > 1) ? (size_t)L.units * L.max_splits * kRows : 0;
+  const int plan_min_w = fixed_split > 0 ? fixed_split / kTileKeys : kPlanMinTiles;
+  const bool plan_splits = ceil_div((int64_t)max(max_ctx, 1), kTileKeys) > plan_min_w;
+  if (plan && plan_splits) parts = max(parts, (size_t)L.plan_grid * kHeadWaves * kRows);
   L.error_off = take(sizeof(uint32_t));
   L.part_o_off = take(parts * kHeadDim * sizeof(float));
   L.part_ml_off = take(parts * 2 * sizeof(float));
+  L.plan_off = take(plan ? ((size_t)num_seqs + 1) * sizeof(int32_t) : 0);
   L.total = off;
   return L;
 }
@@ -912,12 +1089,14 @@ int launch_attention_dma(const AttnParams& p, hipStream_t s) {
               hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  const dim3 grid((unsigned)p.num_seqs * (unsigned)p.mtiles * (unsigned)p.max_splits);
-  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT>), grid, dim3(kHeadWaves * kWave), kDmaLds, s, p);
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT>), dim3((unsigned)p.plan_grid),
+                     dim3(kHeadWaves * kWave), kDmaLds, s, p);
   int rc = check_launch("paged_attention_dma_kernel");
-  if (rc != NE_OK || p.max_splits == 1) return rc;
-  hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)p.units), dim3(256), 0, s, p);
-  return check_launch("attention_merge_kernel");
+  // no sequence is split when every context fits in one split's minimum length
+  const int min_w = p.plan_w > 0 ? p.plan_w : kPlanMinTiles;
+  if (rc != NE_OK || ceil_div(p.max_ctx, kTileKeys) <= min_w) return rc;
+  hipLaunchKernelGGL(attention_plan_merge_kernel, dim3((unsigned)p.num_seqs * kHeadWaves), dim3(256), 0, s, p);
+  return check_launch("attention_plan_merge_kernel");
 }
 
 // Validates the arguments and fills the kernel parameters; NE_OK or an error code.
@@ -988,6 +1167,10 @@ int make_params(const void* q, int64_t q_token_stride, int64_t q_head_stride, co
   p.part_o = (float*)(ws + L.part_o_off);
   p.part_ml = (float*)(ws + L.part_ml_off);
   p.error_flag = (uint32_t*)(ws + L.error_off);
+  p.plan = (int32_t*)(ws + L.plan_off);
+  p.plan_w = L.plan_w;
+  p.plan_grid = L.plan_grid;
+  p.max_ctx = max_ctx_len;
   return NE_OK;
 }
 
@@ -1029,11 +1212,13 @@ extern "C" int ne_paged_verify_attention(
                              max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
                              out_head_stride, split_len, workspace, workspace_bytes, p);
   if (rc != NE_OK) return rc;
-  // int8: one wave per KV head, registers double-buffered (154 VGPRs); bf16: one
-  // wave per KV head, single-buffered (its double-buffered form needs 244 VGPRs)
-  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves &&
-                      scale_dtype != NE_DTYPE_FP32 && ((uintptr_t)k_scale % 4) == 0 &&
-                      ((uintptr_t)v_scale % 4) == 0;
+  // int8 with 8 KV heads, one M tile and 2-byte scales: the DMA kernel on the
+  // balanced plan.  Other int8 shapes: one wave per KV head, registers
+  // double-buffered (154 VGPRs); bf16: single-buffered (double-buffered it needs
+  // 244 VGPRs).  Both on fixed-length splits.
+  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles == 1 &&
+                      num_seqs <= kPlanMaxSeqs && scale_dtype != NE_DTYPE_FP32 &&
+                      ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
   if (dma_ok) {
     return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16>(p, (hipStream_t)stream)
                                         : launch_attention_dma<NE_DTYPE_FP16>(p, (hipStream_t)stream);

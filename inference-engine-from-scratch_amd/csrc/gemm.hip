@@ -458,6 +458,16 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
   const int lane = threadIdx.x % kWave;
   const int kg = wave / L::kNW;
   const int nw = wave % L::kNW;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+
+  // the epilogue's weight-row scales, fetched now so that their latency hides under
+  // the k loop: lane (r, g) stores columns (2 nw + ns) 16 + 4 g + i
+  float sc[2][4];
+#pragma unroll
+  for (int ns = 0; ns < 2; ++ns)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[ns][i] = scale_at<SDT>(p.scale, n0 + (2 * nw + ns) * 16 + 4 * g + i);
 
   floatx4 acc[kPM][2];
 #pragma unroll
@@ -495,8 +505,6 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
     for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * kPM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
   __syncthreads();
 
-  const int r = lane & 15;
-  const int g = lane >> 4;
   for (int mi = kg; mi < kPM; mi += kKGroups) {
     floatx4 v[2];
 #pragma unroll
@@ -512,19 +520,16 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
 #pragma unroll
       for (int ns = 0; ns < 2; ++ns) {
         const int n = n0 + (2 * nw + ns) * 16 + 4 * g;
-        const u32x2 bits = {pack_bf16x2(v[ns][0] * scale_at<SDT>(p.scale, n),
-                                        v[ns][1] * scale_at<SDT>(p.scale, n + 1)),
-                            pack_bf16x2(v[ns][2] * scale_at<SDT>(p.scale, n + 2),
-                                        v[ns][3] * scale_at<SDT>(p.scale, n + 3))};
+        const u32x2 bits = {pack_bf16x2(v[ns][0] * sc[ns][0], v[ns][1] * sc[ns][1]),
+                            pack_bf16x2(v[ns][2] * sc[ns][2], v[ns][3] * sc[ns][3])};
         *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
       }
     } else if constexpr (EPI == 1) {
-      const int ng = n0 + 2 * nw * 16 + 4 * g;  // gate rows; the paired up rows are +16
-      float out[4];
+      float out[4];  // gate rows are subtile 2 nw, the paired up rows subtile 2 nw + 1
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float gate = bf16_round(v[0][i] * scale_at<SDT>(p.scale, ng + i));
-        const float up = bf16_round(v[1][i] * scale_at<SDT>(p.scale, ng + 16 + i));
+        const float gate = bf16_round(v[0][i] * sc[0][i]);
+        const float up = bf16_round(v[1][i] * sc[1][i]);
         const float silu = bf16_round(gate / (1.f + __expf(-gate)));
         out[i] = silu * up;
       }
@@ -535,9 +540,8 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
 #pragma unroll
       for (int ns = 0; ns < 2; ++ns) {
         const int n = n0 + (2 * nw + ns) * 16 + 4 * g;
-        const floatx4 sv = {v[ns][0] * scale_at<SDT>(p.scale, n), v[ns][1] * scale_at<SDT>(p.scale, n + 1),
-                            v[ns][2] * scale_at<SDT>(p.scale, n + 2),
-                            v[ns][3] * scale_at<SDT>(p.scale, n + 3)};
+        const floatx4 sv = {v[ns][0] * sc[ns][0], v[ns][1] * sc[ns][1], v[ns][2] * sc[ns][2],
+                            v[ns][3] * sc[ns][3]};
         *(floatx4*)(partial + ((int64_t)split * p.m + m) * p.n + n) = sv;
       }
     }
@@ -570,6 +574,173 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
   }
   if (partial != nullptr) return launch_proj<4, SDT, 3>(p, splits, partial, s, "w8a16_splitk");
   return launch_proj<4, SDT, 0>(p, 1, nullptr, s, "w8a16_gemm");
+}
+
+// ---- LM head: persistent work-groups over the vocabulary -------------------------
+// logits = X . W^T for X [m, k] bf16 and the tied embedding W [vocab, k] bf16, plus
+// per-(row, 64 columns) argmax partials.  The weight (311 MB for 151936 x 1024) is
+// read from HBM once; what limits a tiled GEMM at m = 320 is the L2 -> CU traffic
+// of X, which every column tile re-reads (about 2.3 GB over 64 x 128 tiles).  So
+// one work-group per CU owns a contiguous range of 64-column groups and walks it in
+// blocks of 256 columns against all rows at once: 8 waves, wave (mw, nw) holding
+// rows 80 mw .. +80 and columns 128 nw .. +128 of the block in 160 accumulators,
+// which cuts the X traffic to one read per 256 columns.  K advances in stages of 64
+// (X 40 KiB + W 32 KiB) copied by DMA into a two-stage LDS ring; each wave places
+// its 9 copy instructions for the next stage between its MFMA groups, so a copy
+// that waits for the memory pipeline does not hold up the multiplies.  Stages run
+// on across blocks.  Rows beyond m re-read row m - 1 and are never stored; more
+// than 320 rows take further passes.
+constexpr int kLmRows = 320;
+constexpr int kLmCols = 256;
+constexpr int kLmWaves = 8;
+constexpr int kLmSK = 64;
+constexpr int kLmRing = 2;
+constexpr int kLmXBytes = kLmRows * kLmSK * 2;   // 40 KiB
+constexpr int kLmWBytes = kLmCols * kLmSK * 2;   // 32 KiB
+constexpr int kLmStage = kLmXBytes + kLmWBytes;
+constexpr int kLmInstr = kLmStage / 1024 / kLmWaves;  // DMA instructions per wave per stage (9)
+static_assert(kLmStage % (1024 * kLmWaves) == 0, "stage split over waves");
+
+struct LmStage {
+  int m0, c0, ccols, k0;
+};
+
+// Copy instruction j of this wave for a stage: 128-byte rows (64 bf16), 8 rows per
+// 1 KiB instruction; row r keeps its 16-byte chunk c at position c ^ (r & 7).
+__device__ __forceinline__ void lm_issue_one(const GemmParams& p, char* stage, const LmStage& st,
+                                             int wave, int j, int lane) {
+  const int i = wave * kLmInstr + j;
+  if (i < kLmXBytes / 1024) {
+    const int row = i * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (row & 7);
+    const int grow = min(st.m0 + row, p.m - 1);
+    lds_dma16(p.x + (int64_t)grow * p.ldx + st.k0 + chunk * 8, stage + i * 1024);
+  } else {
+    const int wrow = (i - kLmXBytes / 1024) * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (wrow & 7);
+    const int crow = st.c0 + min(wrow, st.ccols - 1);  // a short block re-reads its last column
+    lds_dma16((const uint16_t*)p.w + (int64_t)crow * p.k + st.k0 + chunk * 8, stage + i * 1024);
+  }
+}
+
+__device__ __forceinline__ void lm_mma(const GemmParams& p, const char* stage, char* next,
+                                       const LmStage& nst, int mw, int nw, int wave, int lane,
+                                       floatx4 (&acc)[5][8]) {
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const char* xs = stage;
+  const char* ws = stage + kLmXBytes;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {  // two k-steps of 32; lane group g holds k = 32 s + 8 g .. +8
+    bf16x8 b[8];
+#pragma unroll
+    for (int ns = 0; ns < 8; ++ns) {
+      const int row = nw * 128 + ns * 16 + r;
+      b[ns] = __builtin_bit_cast(bf16x8, *(const u32x4*)(ws + row * 128 + (((4 * s + g) ^ (row & 7)) * 16)));
+    }
+#pragma unroll
+    for (int mi = 0; mi < 5; ++mi) {
+      const int row = mw * 80 + mi * 16 + r;
+      const bf16x8 a = __builtin_bit_cast(bf16x8, *(const u32x4*)(xs + row * 128 + (((4 * s + g) ^ (row & 7)) * 16)));
+      const int j = s * 5 + mi;  // copy slot between MFMA groups
+      if (next != nullptr && j < kLmInstr) lm_issue_one(p, next, nst, wave, j, lane);
+#pragma unroll
+      for (int ns = 0; ns < 8; ++ns)
+        acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[ns], a, acc[mi][ns], 0, 0, 0);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int mw = wave & 3;
+  const int nw = wave >> 2;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  // this work-group's 64-column groups [grp0, grp1)
+  const int groups = p.n / kArgmaxCols;
+  const int grp0 = (int)((int64_t)groups * blockIdx.x / gridDim.x);
+  const int grp1 = (int)((int64_t)groups * (blockIdx.x + 1) / gridDim.x);
+  const int nblk = (grp1 - grp0 + 3) / 4;
+  const int kt = p.k / kLmSK;
+  const int mpass = (p.m + kLmRows - 1) / kLmRows;
+  const int total = mpass * nblk * kt;  // stage u = (pass * nblk + block) * kt + t
+  if (total == 0) return;
+  auto stage_of = [&](int u) {
+    const int bi = (u / kt) % nblk;
+    LmStage st;
+    st.m0 = (u / (kt * nblk)) * kLmRows;
+    st.c0 = (grp0 + 4 * bi) * kArgmaxCols;
+    st.ccols = min(4, grp1 - grp0 - 4 * bi) * kArgmaxCols;
+    st.k0 = (u % kt) * kLmSK;
+    return st;
+  };
+
+  floatx4 acc[5][8];
+#pragma unroll
+  for (int mi = 0; mi < 5; ++mi)
+#pragma unroll
+    for (int ns = 0; ns < 8; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  {
+    const LmStage st = stage_of(0);
+    for (int j = 0; j < kLmInstr; ++j) lm_issue_one(p, smem, st, wave, j, lane);
+  }
+  for (int u = 0; u < total; ++u) {
+    wait_vmcnt<0>();                                   // this wave's copies of stage u
+    asm volatile("s_barrier" ::: "memory");           // everyone's; stage u - 1 fully read
+    const bool more = u + 1 < total;
+    const LmStage nst = stage_of(more ? u + 1 : u);
+    lm_mma(p, smem + (u & 1) * kLmStage, more ? smem + ((u + 1) & 1) * kLmStage : nullptr, nst, mw, nw,
+           wave, lane, acc);
+    if (u % kt != kt - 1) continue;
+
+    // ---- block done: logits and argmax partials, then clear the accumulators ----
+    const LmStage st = stage_of(u);
+    const int ngrp = st.ccols / kArgmaxCols;
+#pragma unroll
+    for (int mi = 0; mi < 5; ++mi) {
+      const int m = st.m0 + mw * 80 + mi * 16 + r;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {  // the wave's two 64-column groups
+        const int grp = 2 * nw + q;
+        uint64_t best = 0;
+#pragma unroll
+        for (int nq = 0; nq < 4; ++nq) {
+          const int ns = 4 * q + nq;
+          const int n = st.c0 + nw * 128 + ns * 16 + 4 * g;
+          const floatx4 v = acc[mi][ns];
+          const u32x2 bits = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          if (p.y != nullptr && m < p.m && grp < ngrp) *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float rv = bf16_to_f32((uint16_t)(bits[i >> 1] >> (16 * (i & 1))));
+            best = max_u64(best, argmax_key(rv, (uint32_t)(n + i)));
+          }
+          acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+        best = max_u64(best, shfl_xor_u64(best, 16));
+        best = max_u64(best, shfl_xor_u64(best, 32));
+        if (p.argmax != nullptr && g == 0 && m < p.m && grp < ngrp)
+          p.argmax[(int64_t)m * groups + (st.c0 / kArgmaxCols) + grp] = best;
+      }
+    }
+  }
+}
+
+int launch_lm_head(GemmParams p, hipStream_t stream) {
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)lm_head_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLmRing * kLmStage);
+  if (attr != hipSuccess) {
+    set_error("lm_head: cannot reserve %d bytes of LDS: %s", kLmRing * kLmStage, hipGetErrorString(attr));
+    return NE_ELAUNCH;
+  }
+  const int groups = p.n / kArgmaxCols;
+  const int grid = groups < 256 ? groups : 256;
+  hipLaunchKernelGGL(lm_head_kernel, dim3((unsigned)grid), dim3(kLmWaves * kWave), kLmRing * kLmStage, stream, p);
+  return check_launch("lm_head");
 }
 
 }  // namespace
@@ -671,5 +842,5 @@ extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, 
   p.ldy = ld_logits;
   p.argmax = argmax_partials;
   hipStream_t s = (hipStream_t)stream;
-  return launch_gemm<128, 3, false, -1, 2>(p, 1, nullptr, s, "lm_head");
+  return launch_lm_head(p, s);
 }
