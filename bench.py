@@ -27,8 +27,10 @@ Also reported on the same line:
                  HIP events on the launching stream; traffic = HBM bytes per launch
                  from two rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each
                  scaled by what the counter reads for a 256 MiB copy.
-  gemm           the W8A16 projection GEMMs of the verify step (MFMA roofline; with
-                 --eager only, since graph replay has no per-launch events)
+  gemm           the W8A16 projections (QKV, gate|up with SwiGLU, o and down split-K)
+                 and the LM head at the step's 320 rows, kernel-only: 28 calls with
+                 distinct weights replayed from a HIP graph (no host launch cost);
+                 achieved/frac are MFMA TFLOP/s over QKV + gate|up
   torch_baseline the reference's verify step composed from its own PyTorch ops on
                  this GPU (dequantise-then-linear, gather + dequant + masked GQA
                  attention, logits on every row, a per-sequence verify loop with
@@ -120,11 +122,7 @@ def run_verify(args, torch):
     log("prefill done")
     for _ in range(args.warmup):
         eng.runner.step()
-    timer_name = "ne_w8a16_gemm"  # the QKV and gate|up projections of every layer
-    timer = _native.LaunchTimer() if not args.graph else None
     ctx_per_step, lengths_per_step = [], []
-    if timer is not None:
-        _native.set_launch_timer(timer_name, timer)
     torch.cuda.synchronize()
     start = time.perf_counter()
     tokens = 0
@@ -140,59 +138,15 @@ def run_verify(args, torch):
             kept_hist[r.num_kept] = kept_hist.get(r.num_kept, 0) + 1
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
-    _native.set_launch_timer(timer_name, None)
-    roofline = None
-    if timer is not None:
-        durations = timer.durations_ms()
-        roofline = summarize_roofline("gemm", durations, ctx_per_step, lengths_per_step, cfg)
     active = sum(1 for s in eng.runner.slots if s is not None)
     return {
         "elapsed": elapsed,
         "tokens": tokens,
         "kept_hist": kept_hist,
-        "roofline": roofline,
         "active_at_end": active,
         "max_new": max_new,
         "mean_context": sum(sum(c) for c in ctx_per_step) / max(1, sum(len(c) for c in ctx_per_step)),
     }
-
-
-def summarize_roofline(kind, durations_ms, ctx_per_step, lengths_per_step, cfg):
-    layers = cfg.num_hidden_layers
-    rows = NUM_SEQS * (K_DRAFT + 1)
-    if kind == "attention":
-        # one launch per layer per step; context of sequence b = its length + its guesses (<= k)
-        # query rows read and output rows written: one per real query (1 + guesses)
-        per_step_bytes = [attention_bytes(ctxs, len(ctxs) + sum(ctxs) - sum(lens))
-                          for ctxs, lens in zip(ctx_per_step, lengths_per_step, strict=True)]
-        total_bytes = sum(b * layers for b in per_step_bytes)
-        total_ms = sum(durations_ms)
-        achieved = total_bytes / (total_ms * 1e-3) / 1e9
-        return {"kernel": "paged_attention_kernel<int8>", "bound": "hbm", "achieved": round(achieved, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "launches": len(durations_ms), "avg_us": round(1e3 * total_ms / len(durations_ms), 2),
-                "bytes_per_launch": int(total_bytes / len(durations_ms))}
-    if kind == "gemm":
-        h, i = cfg.hidden_size, cfg.intermediate_size
-        q = cfg.num_attention_heads * cfg.head_dim
-        qkv = q + 2 * cfg.num_key_value_heads * cfg.head_dim
-        # the timed entry point runs QKV and gate|up (o / down go through the split-K one)
-        shapes = [(rows, qkv, h), (rows, 2 * i, h)]
-        flops = sum(2 * m * n * k for m, n, k in shapes) * layers * len(ctx_per_step)
-        total_s = sum(durations_ms) * 1e-3
-        achieved = flops / total_s / 1e12
-        traffic = sum(gemm_traffic(m, n, k) for m, n, k in shapes)
-        return {"kernel": "proj_kernel (W8A16 QKV and gate|up)", "bound": "mfma", "achieved": round(achieved, 1),
-                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                "launches": len(durations_ms), "avg_us": round(1e3 * sum(durations_ms) / len(durations_ms), 2),
-                "hbm_GBps": round(traffic * layers * len(ctx_per_step) / total_s / 1e9, 1)}
-    v, h = cfg.vocab_size, cfg.hidden_size
-    total_s = sum(durations_ms) * 1e-3
-    per_launch = 2 * v * h + 2 * rows * h + rows * (v // 64) * 8
-    achieved = per_launch * len(durations_ms) / total_s / 1e9
-    return {"kernel": "gemm_kernel<lm_head>", "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "launches": len(durations_ms),
-            "avg_us": round(1e3 * sum(durations_ms) / len(durations_ms), 2)}
 
 
 class AttentionWorkload:
@@ -261,12 +215,91 @@ def run_attention_roofline(torch, reps: int = 5):
     dur = timer.durations_ms()
     avg_ms = sum(dur) / len(dur)
     achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
-    return {"kernel": "paged_attention_kernel<int8, fp16 scales> + attention_merge_kernel",
+    return {"kernel": "paged_attention_dma_kernel<fp16 scales> + attention_plan_merge_kernel",
             "workload": "int8 KV, 64 seqs, ctx U{128..1024} seed 1, q=5, fp16 scales, 28 pools",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
             "bytes_per_launch": int(w.bytes_per_launch), "launches": len(dur),
             "sum_ctx": int(w.ctx.sum())}
+
+
+def run_gemm_roofline(torch, layers: int = 28, reps: int = 10):
+    """The W8A16 projections and the LM head of the verify step at M = 64 x 5 = 320 rows,
+    kernel-only: `layers` calls with distinct random weights captured in one HIP graph
+    and replayed `reps` times, so the time is GPU time without host launch cost."""
+    from nanoengine_amd import kernels
+    from nanoengine_amd._native import EPILOGUE_SWIGLU
+    from nanoengine_amd.qwen3 import QWEN3_0_6B as cfg
+
+    dev = torch.device("cuda")
+    m = NUM_SEQS * (K_DRAFT + 1)
+    h, inter = cfg.hidden_size, cfg.intermediate_size
+    qkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+    o_in = cfg.num_attention_heads * cfg.head_dim
+    shapes = [("qkv", qkv, h, 0), ("gate_up_swiglu", 2 * inter, h, 0), ("o_proj_splitk4", h, o_in, 4),
+              ("down_splitk4", h, inter, 4)]
+    out = {}
+    for name, n, k, splits in shapes:
+        ws = [(torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev),
+               (torch.rand(n, device=dev) * 0.01).to(torch.bfloat16)) for _ in range(layers)]
+        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
+        part = torch.empty(max(splits, 1), m, n, dtype=torch.float32, device=dev)
+        y = torch.empty(m, n // 2 if name.startswith("gate") else n, dtype=torch.bfloat16, device=dev)
+
+        def run(w):
+            if splits:
+                kernels.w8a16_gemm_splitk(x, w[0], w[1], splits, out=part)
+            else:
+                kernels.w8a16_gemm(x, w[0], w[1], epilogue=EPILOGUE_SWIGLU if name.startswith("gate") else 0,
+                                   out=y)
+
+        us = _graph_time_us(torch, lambda: [run(w) for w in ws], reps) / layers
+        flops = 2 * m * n * k
+        out[name] = {"m": m, "n": n, "k": k, "splits": splits, "avg_us": round(us, 2),
+                     "TFLOP_s": round(flops / us / 1e6, 1), "mfma_frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                     "weight_GB_s": round(n * k / us / 1e3, 1)}
+        del ws
+    v = cfg.vocab_size
+    embed = (torch.randn(v, h, device=dev) * 0.02).to(torch.bfloat16)
+    hid = (torch.randn(m, h, device=dev) * 0.02).to(torch.bfloat16)
+    parts = torch.empty(m, kernels.lm_head_num_tiles(v), dtype=torch.int64, device=dev)
+    us = _graph_time_us(torch, lambda: kernels.lm_head(hid, embed, logits=False, argmax_partials=parts), reps)
+    out["lm_head_argmax"] = {"m": m, "n": v, "k": h, "avg_us": round(us, 2),
+                             "TFLOP_s": round(2 * m * v * h / us / 1e6, 1),
+                             "mfma_frac": round(2 * m * v * h / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                             "weight_GB_s": round(2 * v * h / us / 1e3, 1),
+                             "hbm_frac": round(2 * v * h / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del embed
+    torch.cuda.empty_cache()
+    qkv_gu = out["qkv"], out["gate_up_swiglu"]
+    flops = sum(2 * e["m"] * e["n"] * e["k"] for e in qkv_gu)
+    us = sum(e["avg_us"] for e in qkv_gu)
+    return {"kernel": "proj_kernel (W8A16) and lm_head_kernel", "bound": "mfma",
+            "achieved": round(flops / us / 1e6, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+            "note": "achieved/frac over the QKV and gate|up projections; per-shape detail below",
+            "shapes": out}
+
+
+def _graph_time_us(torch, body, reps: int) -> float:
+    """Average GPU time of `body` (a fixed sequence of launches) from replays of a HIP
+    graph that holds it, timed with events on the replay stream."""
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        body()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            body()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(st)
+        for _ in range(reps):
+            graph.replay()
+        stop.record(st)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / reps
 
 
 def pmc_child(torch) -> int:
@@ -312,7 +345,9 @@ def measure_traffic() -> dict | None:
         ours = [x for x in rows if x["Kernel_Name"].removeprefix("void ").startswith("ne::")]
         attn = [float(x["Counter_Value"]) for x in ours if "attention" in x["Kernel_Name"]]
         calib = [float(x["Counter_Value"]) for x in ours if "copy_kernel" in x["Kernel_Name"]]
-        launches = sum(1 for x in rows if "paged_attention_kernel" in x["Kernel_Name"])
+        # one main attention kernel per call (the merge kernel, when launched, adds its own
+        # traffic to the same call)
+        launches = sum(1 for x in ours if "paged_attention" in x["Kernel_Name"])
         if not attn or not calib or not launches:
             log(f"pmc pass {counter}: kernels not found in the counter output")
             return None
@@ -535,9 +570,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--temperature", type=float, default=0.0)
     parser.add_argument("--eager", dest="graph", action="store_false",
-                        help="launch the step's kernels one by one instead of replaying a HIP graph "
-                             "(per-launch GEMM timing needs this)")
-    parser.add_argument("--only", choices=("all", "verify", "attention", "baseline"), default="all")
+                        help="launch the step's kernels one by one instead of replaying a HIP graph")
+    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline"), default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-torch-baseline", action="store_true")
     parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
@@ -572,6 +606,10 @@ def main() -> int:
             attention["traffic"] = traffic["fetch_bytes"] + traffic["write_bytes"]
             attention["traffic_detail"] = traffic
         log(f"attention: {attention['avg_us']} us, {attention['achieved']} GB/s")
+    gemm = None
+    if args.only in ("all", "gemm"):
+        gemm = run_gemm_roofline(torch)
+        log(f"gemm: {gemm['achieved']} TFLOP/s over QKV and gate|up")
     torch_base = None
     if args.only in ("all", "baseline") and not args.no_torch_baseline:
         from nanoengine_amd.qwen3 import QWEN3_0_6B, random_state_dict
@@ -584,7 +622,7 @@ def main() -> int:
         cpu = run_cpu_baseline(torch)
         log(f"cpu baseline: {cpu['value']} tok/s")
     if res is None:
-        print(json.dumps({"attention": attention, "torch_baseline": torch_base}), flush=True)
+        print(json.dumps({"attention": attention, "gemm": gemm, "torch_baseline": torch_base}), flush=True)
         return 0
     value = res["tokens"] / res["elapsed"]
     step_us = 1e6 * res["elapsed"] / args.steps
@@ -614,7 +652,7 @@ def main() -> int:
                    "hip_graph": bool(args.graph)},
         "accepted_per_step_hist": {str(k): v for k, v in sorted(res["kept_hist"].items())},
         "roofline": attention,
-        "gemm": res["roofline"],
+        "gemm": gemm,
         "torch_baseline": torch_base,
         "cpu_baseline": cpu,
     }

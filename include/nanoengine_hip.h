@@ -101,12 +101,15 @@ int ne_kv_write(const void* vectors, int32_t vec_dtype, int64_t n, int32_t num_h
  *   k/v_scale    [num_slots+1, num_kv_heads] bf16 or fp16 (int8 cache only)
  *   workspace    ne_paged_attention_workspace_size() bytes.  Bytes 0..3 hold an
  *                error flag, set non-zero when a sequence's context exceeded
- *                max_ctx_len (its keys past the split grid are then dropped); the
- *                caller clears it.  The rest holds fp32 split partials, written
- *                and consumed within the call (no state carries between calls).
- * split_len: keys per work-group (multiple of 128 up to 2048, 0 = choose).  head_dim
- * must be 128 and block_size a multiple of 16.  One work-group serves every KV head
- * of a sequence's split; splits are combined by a second kernel on the same stream.
+ *                max_ctx_len (its keys past max_ctx_len, or past the split grid,
+ *                are then dropped); the caller clears it.  The rest holds the work
+ *                plan and fp32 split partials, written and consumed within the
+ *                call (no state carries between calls).
+ * split_len: most keys per work-group (multiple of 128 up to 2048; 0 = choose: the
+ * int8 / 8-KV-head path then sizes each sequence's splits from the total work, at
+ * least 256 keys each).  head_dim must be 128 and block_size a multiple of 16.  One
+ * work-group serves every KV head of a sequence's split; splits are combined by a
+ * second kernel on the same stream.
  */
 size_t ne_paged_attention_workspace_size(int32_t num_seqs, int32_t num_q_heads,
                                          int32_t num_kv_heads, int32_t max_q_len,

@@ -10,19 +10,21 @@
 //   unit  = (sequence, KV head, M tile of 16 query rows).  Row r of a unit is
 //           (query head h = r / q_len within the GQA group, query i = r % q_len),
 //           so 2 query heads x 5 queries (k = 4) fill 10 of the 16 MFMA rows.
-//   split = a range of `split_len` keys.  One work-group serves every KV head of
-//           one (sequence, M tile, split): wave w takes KV head w, and all waves
+//   split = a range of keys of one sequence.  One work-group serves every KV head
+//           of one (sequence, M tile, split): wave w takes KV head w, and all waves
 //           walk the same 16-key tiles together, so each 1 KB (int8) slot of a
 //           block is fetched whole.  Units split per KV head instead read 128-byte
 //           head rows scattered in time, which a load-only probe of the same pool
 //           measured at 3.2 TB/s against 4.7 TB/s for whole slots.  The split's
-//           block-table slots are staged in LDS once; K/V loads are 32-bit lane
-//           offsets on a per-tile buffer resource.
-//   merge = units with more than one split store fp32 partials (reference max,
-//           sum, unnormalised output; real rows only) and a second kernel
-//           combines them.  No fences or atomics order the work-groups: the
-//           kernel boundary does, which on an 8-XCD part with one L2 per XCD is
-//           far cheaper than a device-scope release per work-group.
+//           block-table slots are staged in LDS once.  The DMA kernel (int8, 8 KV
+//           heads, one M tile) sizes the splits from a work plan that every
+//           work-group derives from the context lengths (plan_item); the register
+//           kernels use fixed `split_len` splits.
+//   merge = splits store fp32 partials (reference max, sum, unnormalised output;
+//           real rows only) and a second kernel combines them.  No fences or
+//           atomics order the work-groups: the kernel boundary does, which on an
+//           8-XCD part with one L2 per XCD is far cheaper than a device-scope
+//           release per work-group.
 //   int8  = codes convert to fp16 exactly with one SDWA op per value and both
 //           products run on fp16 MFMA (Q is bf16, exact in fp16 for |q| < 65504);
 //           the key scale multiplies the scores and the value scale is folded
@@ -915,40 +917,61 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
 
 // Combines the partials of every sequence the plan split: one work-group per
 // (sequence, KV head), 16 threads per row, 8 dims per thread; partial k of the
-// sequence is work-group N_b + k's.
+// sequence is work-group N_b + k's.  A split-length plan gives a sequence at most
+// kMergeBatch partials per pass of loads, so every (m, l, O) of a row is requested
+// at once rather than in a dependent chain.
+constexpr int kMergeBatch = 8;
+
 __global__ __launch_bounds__(256) void attention_plan_merge_kernel(AttnParams p) {
   const int seq = blockIdx.x / kHeadWaves;
   const int head = blockIdx.x % kHeadWaves;
   const int first = p.plan[seq];
   const int last = min(p.plan[seq + 1], p.plan_grid);
+  const int ql = p.q_len[seq];
+  const int qs = p.q_start[seq];
   const int n_splits = last - first;
   if (n_splits <= 1) return;
-  const int ql = p.q_len[seq];
   const int crow = threadIdx.x >> 4;
   const int cd = (threadIdx.x & 15) * 8;
   if (crow >= min(p.group * ql, kRows)) return;
-  float MM = kNegBig;
-  for (int s = 0; s < n_splits; ++s) {
-    const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kRows + crow;
-    MM = fmaxf(MM, p.part_ml[pi * 2]);
-  }
-  float LL = 0.f;
+  float MM = kNegBig, LL = 0.f;
   float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < n_splits; ++s) {
-    const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kRows + crow;
-    const float a = __builtin_amdgcn_exp2f(p.part_ml[pi * 2] - MM);
-    LL += a * p.part_ml[pi * 2 + 1];
-    const float* src = p.part_o + pi * kHeadDim + cd;
-    const floatx4 x0 = *(const floatx4*)src;
-    const floatx4 x1 = *(const floatx4*)(src + 4);
+  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+    float ms[kMergeBatch], ls[kMergeBatch];
+    floatx4 x0[kMergeBatch], x1[kMergeBatch];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      tot[d] += a * x0[d];
-      tot[d + 4] += a * x1[d];
+    for (int j = 0; j < kMergeBatch; ++j) {
+      // a slot past the sequence's last partial re-reads its first one and is ignored
+      const int s = (s0 + j < n_splits) ? s0 + j : s0;
+      const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kRows + crow;
+      const float2 ml = *(const float2*)(p.part_ml + pi * 2);
+      ms[j] = (s0 + j < n_splits) ? ml.x : kNegBig;
+      ls[j] = ml.y;
+      const float* src = p.part_o + pi * kHeadDim + cd;
+      x0[j] = *(const floatx4*)src;
+      x1[j] = *(const floatx4*)(src + 4);
+    }
+    float Mb = MM;
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, ms[j]);
+    const float rescale = __builtin_amdgcn_exp2f(MM - Mb);
+    LL *= rescale;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) tot[d] *= rescale;
+    MM = Mb;
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const float a = (s0 + j < n_splits) ? __builtin_amdgcn_exp2f(ms[j] - MM) : 0.f;
+      LL += a * ls[j];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        tot[d] += a * x0[j][d];
+        tot[d + 4] += a * x1[j][d];
+      }
     }
   }
   const int ch = crow / ql, ci = crow % ql;
-  uint16_t* dst = p.out + (int64_t)(p.q_start[seq] + ci) * p.o_tok_stride +
+  uint16_t* dst = p.out + (int64_t)(qs + ci) * p.o_tok_stride +
                   (int64_t)(head * p.group + ch) * p.o_head_stride + cd;
   const float inv = 1.f / LL;
   *(u32x4*)dst = u32x4{pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv),

@@ -5,28 +5,23 @@
 // tied-embedding LM head (ne/models/qwen3.py:197-203).
 //
 // Shapes here are short and wide: M = query rows of a verify step (64 x 5 =
-// 320), N up to 6144 (151936 for the LM head), K 1024..3072.  A work-group owns
-// a 64 x BN output tile.  K advances in stages of 128: each stage's X and W tiles
-// are copied global -> LDS by the work-group's own DMA loads
-// (global_load_lds_dwordx4, no registers involved) into a ring of S stages, so
-// S - 1 stages are in flight while the MFMAs consume the current one.  The 4
-// waves sit 2 x 2 over the tile and read their MFMA fragments from LDS.
+// 320), N up to 6144 (151936 for the LM head), K 1024..3072.  Both kernels stage
+// X and W tiles in LDS with DMA copies (global_load_lds_dwordx4) so that copies
+// stay in flight while the MFMAs (v_mfma_f32_16x16x32_bf16) consume the previous
+// stage.  Each MFMA computes D = W . X^T (weight rows x token rows), so a lane ends
+// up holding four consecutive output columns of one token row (8-byte stores).
+// int8 weights become bf16 in registers after the LDS read (exact); the per-row
+// scale is applied to the fp32 sum.
 //
-// Each 16x16 MFMA (v_mfma_f32_16x16x32_bf16) computes D = W . X^T (weight rows x
-// token rows), so a lane ends up holding four consecutive output columns of one
-// token row (8-byte stores).  int8 weights become bf16 in registers after the LDS
-// read (one SDWA convert per byte, exact); the per-row scale is applied to the
-// fp32 sum.  Work-group ids are mapped so that the M blocks of one weight tile run
-// on the same XCD and share its L2.
+// At M = 320 every N-tile re-reads X, so what bounds these GEMMs is the L2 -> CU
+// traffic (about 25 B per clock per CU), not HBM or the MFMAs: the tiles are sized
+// to keep that traffic per CU near its minimum for 256 independent tiles, and the
+// LM head keeps all 320 rows resident per work-group to read X once per 256 columns.
 #include "ne_common.hpp"
 
 namespace ne {
 
 namespace {
-
-constexpr int kThreads = 256;
-constexpr int kGemmWaves = 4;
-constexpr int kBK = 64;  // K slice per ring entry
 
 struct GemmParams {
   const uint16_t* x;
@@ -73,16 +68,14 @@ __device__ __forceinline__ float scale_at(const void* s, int64_t i) {
   }
 }
 
-// ---- staged tiles -------------------------------------------------------------
-// A stage holds X[64 rows][BK] bf16 and W[BN rows][BK] (int8 or bf16) in LDS, filled
-// by global_load_lds_dwordx4: every wave-instruction copies 1 KiB of whole 128-byte
-// lines (4 X rows x 256 B, or 8 int8 W rows x 128 B / 4 bf16 W rows x 256 B), the
-// access shape the vector L1 serves at full rate.  Each lane picks its source so
-// that LDS row `row` holds 16-byte chunk c at position c ^ (row % CPR) (CPR = chunks
-// per row), which makes the MFMA fragment reads below bank-conflict free.
-constexpr int kBM = 64;
-constexpr int kArgmaxCols = 64;  // columns per LM-head argmax partial (one wave's share)
-constexpr int kStageK = 128;  // k per stage
+// ---- shared pieces -------------------------------------------------------------
+// Tiles are copied global -> LDS with global_load_lds_dwordx4: every wave-instruction
+// copies 1 KiB of whole 128-byte lines (4 rows of 256 B or 8 rows of 128 B), the access
+// shape the vector L1 serves at full rate.  Each lane picks its source so that LDS row
+// `row` holds 16-byte chunk c at position c ^ (row % chunks-per-row), which makes the
+// MFMA fragment reads bank-conflict free.
+constexpr int kArgmaxCols = 64;  // columns per LM-head argmax partial
+constexpr int kStageK = 128;     // k per stage of the projection kernel
 
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
@@ -94,259 +87,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-template <int BN, bool WINT8>
-struct StageLayout {
-  static constexpr int kXBytes = kBM * kStageK * 2;                     // 16 KiB
-  static constexpr int kWRowBytes = kStageK * (WINT8 ? 1 : 2);          // 128 or 256
-  static constexpr int kWBytes = BN * kWRowBytes;
-  static constexpr int kBytes = kXBytes + kWBytes;
-  static constexpr int kXInstr = kXBytes / 1024 / kGemmWaves;           // per wave
-  static constexpr int kWInstr = kWBytes / 1024 / kGemmWaves;
-  static constexpr int kLoads = kXInstr + kWInstr;                      // per wave per stage
-};
-
-template <int BN, bool WINT8>
-__device__ __forceinline__ void issue_stage(const GemmParams& p, char* stage, int m0, int n0, int k0,
-                                            int wave, int lane) {
-  using L = StageLayout<BN, WINT8>;
-  // X: instruction j of this wave copies rows (wave*kXInstr + j)*4 .. +4, 16 chunks each
-#pragma unroll
-  for (int j = 0; j < L::kXInstr; ++j) {
-    const int blk = wave * L::kXInstr + j;
-    const int row = blk * 4 + (lane >> 4);
-    const int chunk = (lane & 15) ^ (row & 15);
-    const int grow = min(m0 + row, p.m - 1);  // rows past m re-read the last row; never stored
-    lds_dma16(p.x + (int64_t)grow * p.ldx + k0 + chunk * 8, stage + blk * 1024);
-  }
-  char* wst = stage + L::kXBytes;
-#pragma unroll
-  for (int j = 0; j < L::kWInstr; ++j) {
-    const int blk = wave * L::kWInstr + j;
-    if constexpr (WINT8) {  // 8 rows x 8 chunks
-      const int row = blk * 8 + (lane >> 3);
-      const int chunk = (lane & 7) ^ (row & 7);
-      lds_dma16((const int8_t*)p.w + (int64_t)(n0 + row) * p.k + k0 + chunk * 16, wst + blk * 1024);
-    } else {  // 4 rows x 16 chunks
-      const int row = blk * 4 + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 15);
-      lds_dma16((const uint16_t*)p.w + (int64_t)(n0 + row) * p.k + k0 + chunk * 8,
-                wst + blk * 1024);
-    }
-  }
-}
-
-// MFMA k mapping inside a stage: k-step s = 2q + h (q < 2, h < 2); lane group g = l / 16
-// holds logical k = 64 q + 16 g + 8 h + e, e < 8.  For X that is 16-byte chunk 8q + 2g + h
-// of its 256-byte row; for int8 W, bytes 64q + 16g .. +16 cover both h at once.
-template <int BN, bool WINT8, int MS, int NS>
-__device__ __forceinline__ void mma_stage(const char* stage, int wm, int wn, int lane,
-                                          floatx4 (&acc)[MS][NS]) {
-  using L = StageLayout<BN, WINT8>;
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  const char* xst = stage;
-  const char* wst = stage + L::kXBytes;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    u32x4 wf[NS][2];  // [n subtile][h]
-#pragma unroll
-    for (int ni = 0; ni < NS; ++ni) {
-      const int row = wn * NS * 16 + ni * 16 + r;
-      if constexpr (WINT8) {
-        const int chunk = (4 * q + g) ^ (row & 7);
-        const u32x4 v = *(const u32x4*)(wst + row * L::kWRowBytes + chunk * 16);
-        wf[ni][0] = u32x4{v[0], v[1], 0, 0};
-        wf[ni][1] = u32x4{v[2], v[3], 0, 0};
-      } else {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int chunk = (8 * q + 2 * g + h) ^ (row & 15);
-          wf[ni][h] = *(const u32x4*)(wst + row * L::kWRowBytes + chunk * 16);
-        }
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      bf16x8 a[NS];
-#pragma unroll
-      for (int ni = 0; ni < NS; ++ni) {
-        if constexpr (WINT8) {
-          a[ni] = int8x8_to_bf16x8(wf[ni][h][0], wf[ni][h][1]);
-        } else {
-          a[ni] = __builtin_bit_cast(bf16x8, wf[ni][h]);
-        }
-      }
-#pragma unroll
-      for (int mi = 0; mi < MS; ++mi) {
-        const int row = wm * MS * 16 + mi * 16 + r;
-        const int chunk = (8 * q + 2 * g + h) ^ (row & 15);
-        const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(xst + row * 256 + chunk * 16));
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ni], b, acc[mi][ni], 0, 0, 0);
-      }
-    }
-  }
-}
-
-// EPI: 0 store bf16(acc * scale), 1 swiglu, 2 lm head (optional logits + argmax partials),
-// 3 fp32 partial sums of split `blockIdx` over k (scaled), for a consumer to add.
-// Waves form 2 x 2 over the 64 x BN tile: wave (wm, wn) owns rows 32 wm .. +32 and weight
-// rows BN/2 wn .. +BN/2.  S = LDS stages in flight.
-template <int BN, int S, bool WINT8, int SDT, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p, int k_per_split,
-                                                        float* partial) {
-  using L = StageLayout<BN, WINT8>;
-  constexpr int MS = 2;            // m subtiles per wave
-  constexpr int NS = BN / 32;      // n subtiles per wave
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-
-  const int bid = blockIdx.x;
-  const int xcd = bid % kNumXcd;
-  const int jj = bid / kNumXcd;
-  const int tm = jj % p.tiles_m;
-  const int tn = (jj / p.tiles_m) * kNumXcd + xcd;
-  if (tn >= p.tiles_n) return;
-  const int split = blockIdx.y;
-  const int m0 = tm * kBM;
-  const int n0 = tn * BN;
-  const int kbase = split * k_per_split;
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int lane = tid % kWave;
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
-
-  floatx4 acc[MS][NS];
-#pragma unroll
-  for (int mi = 0; mi < MS; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NS; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  const int kt_n = k_per_split / kStageK;
-#pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < kt_n) issue_stage<BN, WINT8>(p, smem + s * L::kBytes, m0, n0, kbase + s * kStageK, wave, lane);
-  for (int t = 0; t < kt_n; ++t) {
-    // stages t+1 .. t+S-2 may stay in flight; stage t must have landed
-    const int ahead = min(S - 2, kt_n - 1 - t);
-    if constexpr (S >= 3) {
-      if (ahead >= 1) {
-        if constexpr (S >= 4) {
-          if (ahead >= 2) wait_vmcnt<2 * L::kLoads>();
-          else wait_vmcnt<L::kLoads>();
-        } else {
-          wait_vmcnt<L::kLoads>();
-        }
-      } else {
-        wait_vmcnt<0>();
-      }
-    } else {
-      wait_vmcnt<0>();
-    }
-    // the explicit vmcnt wait above covers this wave's DMA; the barrier makes every
-    // wave's stage t visible (a __syncthreads fence would wait for all of them)
-    asm volatile("s_barrier" ::: "memory");
-    const int tn2 = t + S - 1;
-    if (tn2 < kt_n)
-      issue_stage<BN, WINT8>(p, smem + (tn2 % S) * L::kBytes, m0, n0, kbase + tn2 * kStageK, wave, lane);
-    mma_stage<BN, WINT8, MS, NS>(smem + (t % S) * L::kBytes, wm, wn, lane, acc);
-  }
-
-  // ---- epilogue: lane holds D[n = 4g + i][m = r] of each (mi, ni) subtile ----
-  const int r = lane & 15;
-  const int g = lane >> 4;
-#pragma unroll
-  for (int mi = 0; mi < MS; ++mi) {
-    const int m = m0 + wm * MS * 16 + mi * 16 + r;
-    if constexpr (EPI == 0) {
-      if (m < p.m) {
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni) {
-          const int n = n0 + wn * NS * 16 + ni * 16 + 4 * g;
-          const floatx4 v = acc[mi][ni];
-          const u32x2 bits = {pack_bf16x2(v[0] * scale_at<SDT>(p.scale, n),
-                                          v[1] * scale_at<SDT>(p.scale, n + 1)),
-                              pack_bf16x2(v[2] * scale_at<SDT>(p.scale, n + 2),
-                                          v[3] * scale_at<SDT>(p.scale, n + 3))};
-          *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
-        }
-      }
-    } else if constexpr (EPI == 1) {
-      static_assert(NS % 2 == 0, "swiglu pairs gate/up subtiles");
-      if (m < p.m) {
-#pragma unroll
-        for (int q = 0; q < NS / 2; ++q) {
-          const int ng = n0 + wn * NS * 16 + 2 * q * 16 + 4 * g;  // gate rows; up rows are +16
-          float out[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float gate = bf16_round(acc[mi][2 * q][i] * scale_at<SDT>(p.scale, ng + i));
-            const float up = bf16_round(acc[mi][2 * q + 1][i] * scale_at<SDT>(p.scale, ng + 16 + i));
-            const float silu = bf16_round(gate / (1.f + __expf(-gate)));
-            out[i] = silu * up;
-          }
-          const int ncol = (n0 + wn * NS * 16 + 2 * q * 16) / 2 + 4 * g;
-          const u32x2 bits = {pack_bf16x2(out[0], out[1]), pack_bf16x2(out[2], out[3])};
-          *(u32x2*)(p.y + (int64_t)m * p.ldy + ncol) = bits;
-        }
-      }
-    } else if constexpr (EPI == 2) {
-      uint64_t best = 0;
-#pragma unroll
-      for (int ni = 0; ni < NS; ++ni) {
-        const int n = n0 + wn * NS * 16 + ni * 16 + 4 * g;
-        const floatx4 v = acc[mi][ni];
-        const u32x2 bits = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        if (p.y != nullptr && m < p.m) *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float rv = bf16_to_f32((uint16_t)(bits[i >> 1] >> (16 * (i & 1))));
-          best = max_u64(best, argmax_key(rv, (uint32_t)(n + i)));
-        }
-      }
-      best = max_u64(best, shfl_xor_u64(best, 16));
-      best = max_u64(best, shfl_xor_u64(best, 32));
-      // one partial per (row, 64-column half of the tile)
-      if (p.argmax != nullptr && g == 0 && m < p.m)
-        p.argmax[(int64_t)m * (p.n / kArgmaxCols) + (n0 + wn * NS * 16) / kArgmaxCols] = best;
-    } else {
-      if (m < p.m) {
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni) {
-          const int n = n0 + wn * NS * 16 + ni * 16 + 4 * g;
-          const floatx4 v = acc[mi][ni];
-          const floatx4 sv = {v[0] * scale_at<SDT>(p.scale, n), v[1] * scale_at<SDT>(p.scale, n + 1),
-                              v[2] * scale_at<SDT>(p.scale, n + 2), v[3] * scale_at<SDT>(p.scale, n + 3)};
-          *(floatx4*)(partial + ((int64_t)split * p.m + m) * p.n + n) = sv;
-        }
-      }
-    }
-  }
-}
-
-template <int BN, int S, bool WINT8, int SDT, int EPI>
-int launch_gemm(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name) {
-  using L = StageLayout<BN, WINT8>;
-  p.tiles_m = ceil_div(p.m, kBM);
-  p.tiles_n = p.n / BN;
-  const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
-  const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
-  const size_t lds = (size_t)S * L::kBytes;
-  // raise the dynamic LDS limit once per instantiation (thread-safe static init)
-  static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)gemm_kernel<BN, S, WINT8, SDT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-      (int)lds);
-  if (attr != hipSuccess) {
-    set_error("%s: cannot reserve %zu bytes of LDS: %s", name, lds, hipGetErrorString(attr));
-    return NE_ELAUNCH;
-  }
-  hipLaunchKernelGGL((gemm_kernel<BN, S, WINT8, SDT, EPI>), grid, dim3(kThreads), lds, stream, p,
-                     p.k / splits, partial);
-  return check_launch(name);
 }
 
 // ---- W8A16 projections ----------------------------------------------------------
