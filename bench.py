@@ -190,36 +190,58 @@ class AttentionWorkload:
         self.bytes_per_launch = attention_bytes(self.ctx.tolist(), self.rows) + tables.numel() * 4
         self._kernels = kernels
 
-    def launch(self, pool) -> None:
+    def plan(self) -> None:
+        """The per-step work plan every layer's planned call reads (same metadata for all pools)."""
+        self._kernels.paged_attention_plan(self.tables, 16, self.ctx_d, self.q_start, self.q_len, 16, 8, 5,
+                                           int(self.ctx.max()), self.ws)
+
+    def launch(self, pool, planned: bool = False) -> None:
         self._kernels.paged_verify_attention(
             self.q, pool[0], pool[1], pool[2], pool[3], self.tables, 16, self.ctx_d, self.q_start,
-            self.q_len, 5, int(self.ctx.max()), out=self.out, workspace=self.ws)
+            self.q_len, 5, int(self.ctx.max()), out=self.out, workspace=self.ws, planned=planned)
 
 
 def run_attention_roofline(torch, reps: int = 5):
-    """Average launch time of the attention call over `reps` passes of 28 pools, from HIP
-    events recorded on the launching stream around each call (main + merge kernels)."""
+    """Average time per attention call over `reps` passes of the 28 pools, from HIP events
+    recorded on the launching stream around each entry point.  A pass is what a verify step
+    does: one plan (ne_paged_attention_plan) and 28 planned calls (main + merge kernels); the
+    plan's time is counted and spread over the pass's calls.  The in-kernel-plan entry point
+    (ne_paged_verify_attention) is timed the same way for comparison."""
     from nanoengine_amd import _native
 
     w = AttentionWorkload(torch)
     for p in w.pools:
         w.launch(p)
+    w.plan()
+    for p in w.pools:
+        w.launch(p, planned=True)
     torch.cuda.synchronize()
-    timer = _native.LaunchTimer()
-    _native.set_launch_timer("ne_paged_verify_attention", timer)
+    timers = {name: _native.LaunchTimer() for name in
+              ("ne_paged_attention_plan", "ne_paged_verify_attention_planned", "ne_paged_verify_attention")}
+    for name, t in timers.items():
+        _native.set_launch_timer(name, t)
+    for _ in range(reps):
+        w.plan()
+        for p in w.pools:
+            w.launch(p, planned=True)
     for _ in range(reps):
         for p in w.pools:
             w.launch(p)
     torch.cuda.synchronize()
-    _native.set_launch_timer("ne_paged_verify_attention", None)
-    dur = timer.durations_ms()
-    avg_ms = sum(dur) / len(dur)
+    for name in timers:
+        _native.set_launch_timer(name, None)
+    plan_ms = sum(timers["ne_paged_attention_plan"].durations_ms())
+    calls = timers["ne_paged_verify_attention_planned"].durations_ms()
+    avg_ms = (plan_ms + sum(calls)) / len(calls)
+    unplanned = timers["ne_paged_verify_attention"].durations_ms()
     achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
-    return {"kernel": "paged_attention_dma_kernel<fp16 scales> + attention_plan_merge_kernel",
+    return {"kernel": "paged_attention_dma_kernel<fp16 scales, planned> + attention_plan_merge_kernel",
             "workload": "int8 KV, 64 seqs, ctx U{128..1024} seed 1, q=5, fp16 scales, 28 pools",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
-            "bytes_per_launch": int(w.bytes_per_launch), "launches": len(dur),
+            "plan_us": round(plan_ms * 1e3 / reps, 2),
+            "unplanned_avg_us": round(1e3 * sum(unplanned) / len(unplanned), 2),
+            "bytes_per_launch": int(w.bytes_per_launch), "launches": len(calls),
             "sum_ctx": int(w.ctx.sum())}
 
 
@@ -310,8 +332,9 @@ def pmc_child(torch) -> int:
     from nanoengine_amd import _native
 
     w = AttentionWorkload(torch)
+    w.plan()
     for p in w.pools:
-        w.launch(p)
+        w.launch(p, planned=True)
     torch.cuda.synchronize()
     a = torch.empty(CALIBRATION_BYTES, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)

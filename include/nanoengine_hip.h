@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 2
+#define NE_ABI_VERSION 3
 
 /* status codes */
 #define NE_OK 0
@@ -124,6 +124,36 @@ int ne_paged_verify_attention(const void* q, int64_t q_token_stride, int64_t q_h
                               int32_t max_ctx_len, float softmax_scale, void* out,
                               int64_t out_token_stride, int64_t out_head_stride, int32_t split_len,
                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * A6 with the work plan computed once per step.  ne_paged_attention_plan writes into
+ * `workspace` the work item of every work-group and the slot of every 16-key tile,
+ * from the same per-step metadata the attention call takes (it replaces the part of
+ * batch_builder.py:22-65 / paged_allocator.py:69-79 that turns block tables into
+ * context slots, once for all layers).  ne_paged_verify_attention_planned then takes
+ * exactly ne_paged_verify_attention's arguments and reads that plan instead of
+ * deriving it, which saves one dependent memory round trip per call.  Valid while
+ * ctx_len, q_start, q_len, block_tables, num_seqs, max_q_len, max_ctx_len and
+ * split_len stay as they were for the plan (a verify step's layers).  Both serve int8
+ * caches with 8 KV heads, 2-byte scales and at most 16 query rows per KV head
+ * (num_q_heads / num_kv_heads * max_q_len <= 16) and return NE_EUNSUPPORTED
+ * otherwise; the workspace size is ne_paged_attention_workspace_size()'s.
+ */
+int ne_paged_attention_plan(const int32_t* block_tables, int32_t block_table_stride,
+                            int32_t block_size, const int32_t* ctx_len, const int32_t* q_start,
+                            const int32_t* q_len, int32_t num_seqs, int32_t num_q_heads,
+                            int32_t num_kv_heads, int32_t max_q_len, int32_t max_ctx_len,
+                            int32_t split_len, void* workspace, size_t workspace_bytes,
+                            void* stream);
+int ne_paged_verify_attention_planned(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
+    int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
+    int32_t block_size, const int32_t* ctx_len, const int32_t* q_start, const int32_t* q_len,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /*
  * A8 - W8A16 projection: y[m, n] = bf16(sum_k x[m, k] * w[n, k] * scale[n])

@@ -93,6 +93,8 @@ struct AttnParams {
   int32_t plan_w;      // DMA kernel: tiles per split (0: derived from the total work)
   int32_t plan_grid;   // DMA kernel: work-groups launched
   int32_t max_ctx;     // the caller's bound on ctx_len
+  int32_t* plan_desc;  // precomputed plan: [plan_grid][8] work items (seq < 0: none)
+  int32_t* plan_slots; // precomputed plan: [plan_grid][kMaxTiles] first slot of each tile
 };
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -642,31 +644,36 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-// Called by all threads of the work-group; false when the work-group has no work.
-__device__ bool plan_item(const AttnParams& p, int* s_plan, PlanItem& item) {
+// The sequences' share of the plan held by thread t: sequences 2t and 2t+1.
+struct PlanScan {
+  int ctx[2], ql[2], qs[2], tiles[2], n[2], first[2];  // first = N_b
+  int total;                                           // sum_b n_b
+};
+
+// Called by all threads of the work-group (two barriers).
+__device__ PlanScan plan_scan(const AttnParams& p, int* s_plan) {
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
   const int B = p.num_seqs;
-  int ctx[2], ql[2], qs[2], tiles[2];
+  PlanScan ps;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int i = 2 * tid + k;
     const bool ok = i < B;
-    ctx[k] = ok ? p.ctx_len[i] : 0;
-    ql[k] = ok ? p.q_len[i] : 0;
-    qs[k] = ok ? p.q_start[i] : 0;
+    ps.ctx[k] = ok ? p.ctx_len[i] : 0;
+    ps.ql[k] = ok ? p.q_len[i] : 0;
+    ps.qs[k] = ok ? p.q_start[i] : 0;
   }
   // a context beyond the caller's bound is flagged and clipped to it, so that no
   // block-table entry past max_ctx is read
-  if (blockIdx.x == 0 && (ctx[0] > p.max_ctx || ctx[1] > p.max_ctx)) atomicOr(p.error_flag, 1u);
-  ctx[0] = min(ctx[0], p.max_ctx);
-  ctx[1] = min(ctx[1], p.max_ctx);
+  if (blockIdx.x == 0 && (ps.ctx[0] > p.max_ctx || ps.ctx[1] > p.max_ctx)) atomicOr(p.error_flag, 1u);
 #pragma unroll
-  for (int k = 0; k < 2; ++k)
-    tiles[k] = (ql[k] > 0 && ctx[k] > 0) ? (ctx[k] + kTileKeys - 1) / kTileKeys : 0;
-  if (tid == 0) s_plan[16] = -1;
-  const int tsum = wave_sum(tiles[0] + tiles[1]);
+  for (int k = 0; k < 2; ++k) {
+    ps.ctx[k] = min(ps.ctx[k], p.max_ctx);
+    ps.tiles[k] = (ps.ql[k] > 0 && ps.ctx[k] > 0) ? (ps.ctx[k] + kTileKeys - 1) / kTileKeys : 0;
+  }
+  const int tsum = wave_sum(ps.tiles[0] + ps.tiles[1]);
   if (lane == 0) s_plan[wave] = tsum;
   __syncthreads();
   int T = 0;
@@ -679,9 +686,9 @@ __device__ bool plan_item(const AttnParams& p, int* s_plan, PlanItem& item) {
     if (tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
     W = kMaxTiles;
   }
-  const int n0 = (tiles[0] + W - 1) / W;
-  const int n1 = (tiles[1] + W - 1) / W;
-  const int c = n0 + n1;
+  ps.n[0] = (ps.tiles[0] + W - 1) / W;
+  ps.n[1] = (ps.tiles[1] + W - 1) / W;
+  const int c = ps.n[0] + ps.n[1];
   int incl = c;
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
@@ -697,24 +704,34 @@ __device__ bool plan_item(const AttnParams& p, int* s_plan, PlanItem& item) {
     base += (w < wave) ? x : 0;
     total += x;
   }
-  const int N0 = base + incl - c;
-  const int N1 = N0 + n0;
+  ps.first[0] = base + incl - c;
+  ps.first[1] = ps.first[0] + ps.n[0];
+  ps.total = total;
   if (blockIdx.x == 0) {
-    if (2 * tid < B) p.plan[2 * tid] = N0;
-    if (2 * tid + 1 < B) p.plan[2 * tid + 1] = N1;
+    if (2 * tid < B) p.plan[2 * tid] = ps.first[0];
+    if (2 * tid + 1 < B) p.plan[2 * tid + 1] = ps.first[1];
     if (tid == 0) p.plan[B] = total;
   }
   if (total > G && tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
+  return ps;
+}
+
+// Called by all threads of the work-group; false when the work-group has no work.
+__device__ bool plan_item(const AttnParams& p, int* s_plan, PlanItem& item) {
+  const int tid = threadIdx.x;
+  if (tid == 0) s_plan[16] = -1;  // ordered before the owner's write by plan_scan's barriers
+  const PlanScan ps = plan_scan(p, s_plan);
   const int w = blockIdx.x;
-  const int k = (w >= N0 && w < N1) ? 0 : ((w >= N1 && w < N1 + n1) ? 1 : -1);
+  const int k = (w >= ps.first[0] && w < ps.first[1]) ? 0
+                : ((w >= ps.first[1] && w < ps.first[1] + ps.n[1]) ? 1 : -1);
   if (k >= 0) {
     s_plan[16] = 2 * tid + k;
-    s_plan[17] = w - (k ? N1 : N0);
-    s_plan[18] = k ? n1 : n0;
-    s_plan[19] = k ? tiles[1] : tiles[0];
-    s_plan[20] = k ? ctx[1] : ctx[0];
-    s_plan[21] = k ? ql[1] : ql[0];
-    s_plan[22] = k ? qs[1] : qs[0];
+    s_plan[17] = w - (k ? ps.first[1] : ps.first[0]);
+    s_plan[18] = k ? ps.n[1] : ps.n[0];
+    s_plan[19] = k ? ps.tiles[1] : ps.tiles[0];
+    s_plan[20] = k ? ps.ctx[1] : ps.ctx[0];
+    s_plan[21] = k ? ps.ql[1] : ps.ql[0];
+    s_plan[22] = k ? ps.qs[1] : ps.qs[0];
   }
   __syncthreads();
   item.seq = s_plan[16];
@@ -726,6 +743,58 @@ __device__ bool plan_item(const AttnParams& p, int* s_plan, PlanItem& item) {
   item.ql = s_plan[21];
   item.qs = s_plan[22];
   return true;
+}
+
+// Precomputed plan (one launch per step, shared by every layer's attention call):
+// work-group b of the plan kernel serves sequence b, writing the work items of its
+// splits and the slot of every 16-key tile, in the layout the planned attention
+// kernel reads.  Work-group 0 also marks the unused items of the grid.
+constexpr int kDescInts = 8;
+
+__global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(AttnParams p) {
+  __shared__ int s_plan[kPlanInts];
+  __shared__ int s_seq[8];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const PlanScan ps = plan_scan(p, s_plan);
+  if (2 * tid == b || 2 * tid + 1 == b) {
+    const int k = (2 * tid == b) ? 0 : 1;
+    s_seq[0] = k ? ps.n[1] : ps.n[0];
+    s_seq[1] = k ? ps.first[1] : ps.first[0];
+    s_seq[2] = k ? ps.tiles[1] : ps.tiles[0];
+    s_seq[3] = k ? ps.ctx[1] : ps.ctx[0];
+    s_seq[4] = k ? ps.ql[1] : ps.ql[0];
+    s_seq[5] = k ? ps.qs[1] : ps.qs[0];
+  }
+  if (b == 0) {  // items past the plan's total have no work
+    for (int w = ps.total + tid; w < p.plan_grid; w += kHeadWaves * kWave) p.plan_desc[(int64_t)w * kDescInts] = -1;
+  }
+  __syncthreads();
+  const int n = s_seq[0], first = s_seq[1], tiles = s_seq[2];
+  for (int s = tid; s < n; s += kHeadWaves * kWave) {
+    const int w = first + s;
+    if (w >= p.plan_grid) break;  // flagged by plan_scan; the item is dropped
+    int32_t* d = p.plan_desc + (int64_t)w * kDescInts;
+    d[0] = b;
+    d[1] = s;
+    d[2] = n;
+    d[3] = tiles;
+    d[4] = s_seq[3];
+    d[5] = s_seq[4];
+    d[6] = s_seq[5];
+    d[7] = 0;
+  }
+  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+  for (int j = tid; j < tiles; j += kHeadWaves * kWave) {
+    // split s holds tiles [tiles s / n, tiles (s + 1) / n); tile j is in the last split
+    // whose start is <= j
+    const int s = (int)(((int64_t)(j + 1) * n - 1) / tiles);
+    const int w = first + s;
+    if (w >= p.plan_grid) continue;
+    const int t = j - (int)((int64_t)tiles * s / n);
+    const int key0 = j * kTileKeys;
+    p.plan_slots[(int64_t)w * kMaxTiles + t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+  }
 }
 
 __device__ __forceinline__ void lds_dma(const void* src, void* lds, int bytes) {
@@ -797,7 +866,9 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
   R.sc = (kb + kk < kend) ? s : 0.f;
 }
 
-template <int SDT>
+// PLANNED: the work item and the split's slots come from attention_plan_kernel's
+// output instead of being derived here (one round trip instead of two).
+template <int SDT, bool PLANNED>
 __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel(AttnParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* s_slot = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot);
@@ -809,7 +880,35 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   const int head = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   PlanItem item;
-  if (!plan_item(p, s_plan, item)) return;
+  if constexpr (PLANNED) {
+    // the split's slots (entries past its tiles are never read) and its work item,
+    // requested together
+    for (int t = tid; t < kMaxTiles; t += kHeadWaves * kWave)
+      s_slot[t] = p.plan_slots[(int64_t)blockIdx.x * kMaxTiles + t];
+    const int32_t* d = p.plan_desc + (int64_t)blockIdx.x * kDescInts;
+    item.seq = d[0];
+    item.split = d[1];
+    item.n_splits = d[2];
+    item.tiles = d[3];
+    item.ctx = d[4];
+    item.ql = d[5];
+    item.qs = d[6];
+    if (item.seq < 0) return;
+    // a work item that this metadata cannot have produced (no plan, or a stale one) is
+    // flagged and skipped rather than followed
+    const int max_tiles = (p.max_ctx + kTileKeys - 1) / kTileKeys;
+    const bool sane = item.seq < p.num_seqs && item.n_splits >= 1 && item.split >= 0 &&
+                      item.split < item.n_splits && item.tiles >= item.n_splits &&
+                      item.tiles <= max_tiles && item.ctx > 0 && item.ctx <= p.max_ctx &&
+                      item.ql > 0 && item.qs >= 0 &&
+                      (item.tiles + item.n_splits - 1) / item.n_splits <= kMaxTiles;
+    if (!sane) {
+      if (tid == 0) atomicOr(p.error_flag, 2u);
+      return;
+    }
+  } else {
+    if (!plan_item(p, s_plan, item)) return;
+  }
   const int seq = item.seq;
   const int n_splits = item.n_splits;
   const int j0 = (int)((int64_t)item.tiles * item.split / n_splits);
@@ -838,10 +937,12 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
 #pragma unroll
     for (int c = 0; c < 4; ++c) raw[c] = src[c];
   }
-  const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
-  for (int t = tid; t < n_tiles; t += kHeadWaves * kWave) {
-    const int key0 = kstart + kTileKeys * t;
-    s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+  if constexpr (!PLANNED) {
+    const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
+    for (int t = tid; t < n_tiles; t += kHeadWaves * kWave) {
+      const int key0 = kstart + kTileKeys * t;
+      s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+    }
   }
   __syncthreads();  // s_slot ready
 
@@ -1019,7 +1120,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
 
 struct Layout {
   int group, mtiles, units, split_len, max_splits, plan_grid, plan_w;
-  size_t part_o_off, part_ml_off, error_off, plan_off, total;
+  size_t part_o_off, part_ml_off, error_off, plan_off, desc_off, slots_off, total;
 };
 
 // Work-groups of the DMA kernel's plan: enough that W <= kMaxTiles for any
@@ -1078,6 +1179,8 @@ Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_le
   L.part_o_off = take(parts * kHeadDim * sizeof(float));
   L.part_ml_off = take(parts * 2 * sizeof(float));
   L.plan_off = take(plan ? ((size_t)num_seqs + 1) * sizeof(int32_t) : 0);
+  L.desc_off = take(plan ? (size_t)L.plan_grid * kDescInts * sizeof(int32_t) : 0);
+  L.slots_off = take(plan ? (size_t)L.plan_grid * kMaxTiles * sizeof(int32_t) : 0);
   L.total = off;
   return L;
 }
@@ -1103,16 +1206,17 @@ int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStre
 
 // The DMA kernel serves int8 caches with 8 KV heads and 2-byte scales; it needs
 // the attribute for more than the default dynamic LDS once per instantiation.
-template <int SDT>
+template <int SDT, bool PLANNED>
 int launch_attention_dma(const AttnParams& p, hipStream_t s) {
   static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)paged_attention_dma_kernel<SDT>, hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
+      (const void*)paged_attention_dma_kernel<SDT, PLANNED>, hipFuncAttributeMaxDynamicSharedMemorySize,
+      kDmaLds);
   if (attr != hipSuccess) {
     set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", kDmaLds,
               hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT>), dim3((unsigned)p.plan_grid),
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED>), dim3((unsigned)p.plan_grid),
                      dim3(kHeadWaves * kWave), kDmaLds, s, p);
   int rc = check_launch("paged_attention_dma_kernel");
   // no sequence is split when every context fits in one split's minimum length
@@ -1191,6 +1295,8 @@ int make_params(const void* q, int64_t q_token_stride, int64_t q_head_stride, co
   p.part_ml = (float*)(ws + L.part_ml_off);
   p.error_flag = (uint32_t*)(ws + L.error_off);
   p.plan = (int32_t*)(ws + L.plan_off);
+  p.plan_desc = (int32_t*)(ws + L.desc_off);
+  p.plan_slots = (int32_t*)(ws + L.slots_off);
   p.plan_w = L.plan_w;
   p.plan_grid = L.plan_grid;
   p.max_ctx = max_ctx_len;
@@ -1243,9 +1349,85 @@ extern "C" int ne_paged_verify_attention(
                       num_seqs <= kPlanMaxSeqs && scale_dtype != NE_DTYPE_FP32 &&
                       ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
   if (dma_ok) {
-    return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16>(p, (hipStream_t)stream)
-                                        : launch_attention_dma<NE_DTYPE_FP16>(p, (hipStream_t)stream);
+    return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, false>(p, (hipStream_t)stream)
+                                        : launch_attention_dma<NE_DTYPE_FP16, false>(p, (hipStream_t)stream);
   }
   if (kv_dtype == NE_DTYPE_INT8) return launch_attention<1, true>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
   return launch_attention<1, false>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
+}
+
+extern "C" int ne_paged_attention_plan(const int32_t* block_tables, int32_t block_table_stride,
+                                       int32_t block_size, const int32_t* ctx_len,
+                                       const int32_t* q_start, const int32_t* q_len, int32_t num_seqs,
+                                       int32_t num_q_heads, int32_t num_kv_heads, int32_t max_q_len,
+                                       int32_t max_ctx_len, int32_t split_len, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
+               "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_q_heads,
+               num_kv_heads);
+  NE_CHECK_SUPPORTED(block_size > 0 && block_size % kTileKeys == 0,
+                     "block_size must be a positive multiple of 16 (got %d)", block_size);
+  NE_CHECK_ARG(block_tables && ctx_len && q_start && q_len, "null pointer argument");
+  NE_CHECK_ARG(max_q_len > 0 && max_ctx_len > 0, "max_q_len and max_ctx_len must be positive");
+  NE_CHECK_ARG(split_len == 0 || (split_len > 0 && split_len % 128 == 0 && split_len <= kMaxSplitLen),
+               "split_len must be 0 or a positive multiple of 128 up to %d", kMaxSplitLen);
+  const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len,
+                               split_len, NE_DTYPE_INT8);
+  NE_CHECK_SUPPORTED(num_kv_heads == kHeadWaves && L.mtiles == 1 && num_seqs <= kPlanMaxSeqs,
+                     "a precomputed plan serves 8 KV heads, at most 16 query rows per KV head "
+                     "and at most %d sequences", kPlanMaxSeqs);
+  NE_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total,
+               "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+  AttnParams p{};
+  p.block_tables = block_tables;
+  p.bt_stride = block_table_stride;
+  p.block_size = block_size;
+  p.ctx_len = ctx_len;
+  p.q_start = q_start;
+  p.q_len = q_len;
+  p.num_seqs = num_seqs;
+  p.num_kv_heads = num_kv_heads;
+  p.group = L.group;
+  p.mtiles = L.mtiles;
+  p.max_ctx = max_ctx_len;
+  p.plan_w = L.plan_w;
+  p.plan_grid = L.plan_grid;
+  char* ws = (char*)workspace;
+  p.error_flag = (uint32_t*)(ws + L.error_off);
+  p.plan = (int32_t*)(ws + L.plan_off);
+  p.plan_desc = (int32_t*)(ws + L.desc_off);
+  p.plan_slots = (int32_t*)(ws + L.slots_off);
+  hipLaunchKernelGGL(attention_plan_kernel, dim3((unsigned)num_seqs), dim3(kHeadWaves * kWave), 0,
+                     (hipStream_t)stream, p);
+  return check_launch("attention_plan_kernel");
+}
+
+extern "C" int ne_paged_verify_attention_planned(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
+    int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
+    int32_t block_size, const int32_t* ctx_len, const int32_t* q_start, const int32_t* q_len,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  AttnParams p;
+  const int rc = make_params(q, q_token_stride, q_head_stride, k_cache, v_cache, k_scale, v_scale,
+                             kv_dtype, scale_dtype, block_tables, block_table_stride, block_size,
+                             ctx_len, q_start, q_len, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
+                             out_head_stride, split_len, workspace, workspace_bytes, p);
+  if (rc != NE_OK) return rc;
+  NE_CHECK_SUPPORTED(kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles == 1 &&
+                         num_seqs <= kPlanMaxSeqs &&
+                         (scale_dtype == NE_DTYPE_BF16 || scale_dtype == NE_DTYPE_FP16) &&
+                         ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0,
+                     "the planned path serves int8 caches with 8 KV heads, 2-byte 4-byte-aligned "
+                     "scales and at most 16 query rows per KV head");
+  return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, true>(p, (hipStream_t)stream)
+                                      : launch_attention_dma<NE_DTYPE_FP16, true>(p, (hipStream_t)stream);
 }

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -62,6 +62,11 @@ SIGNATURES: dict[str, tuple] = {
             _vp, _sz, _vp,  # workspace, bytes, stream
         ],
     ),
+    "ne_paged_verify_attention_planned": (ctypes.c_int, []),  # filled below: same as ne_paged_verify_attention
+    "ne_paged_attention_plan": (
+        ctypes.c_int,
+        [_vp, _i32, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
     "ne_w8a16_gemm": (
         ctypes.c_int,
         [_vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
@@ -103,6 +108,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "ne_copy_bytes": (ctypes.c_int, [_vp, _vp, _sz, _vp]),
 }
+SIGNATURES["ne_paged_verify_attention_planned"] = SIGNATURES["ne_paged_verify_attention"]
 
 
 class NativeError(RuntimeError):

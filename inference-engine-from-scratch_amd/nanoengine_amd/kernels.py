@@ -139,18 +139,24 @@ def kv_write(
 # --------------------------------------------------------------------------- A6
 @dataclass
 class AttentionWorkspace:
-    """Caller-owned scratch for split-K attention; re-zeroed when its layout changes."""
+    """Caller-owned scratch for split-K attention; re-zeroed when its layout changes.
+
+    ``plan_key`` names the metadata the last :func:`paged_attention_plan` call used, so
+    that a planned attention call on other metadata is refused."""
 
     buffer: torch.Tensor | None = None
     layout: tuple | None = None
+    plan_key: tuple | None = None
 
     def get(self, device: torch.device, nbytes: int, layout: tuple) -> torch.Tensor:
         if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
             self.buffer = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
             self.layout = layout
+            self.plan_key = None
         elif self.layout != layout:
             self.buffer.zero_()
             self.layout = layout
+            self.plan_key = None
         return self.buffer
 
     def error_flag(self) -> int:
@@ -183,8 +189,12 @@ def paged_verify_attention(
     out: torch.Tensor | None = None,
     workspace: AttentionWorkspace | None = None,
     split_len: int = 0,
+    planned: bool = False,
 ) -> torch.Tensor:
-    """Paged multi-query attention; ``q``/``out`` are ``[rows, q_heads, 128]`` bf16."""
+    """Paged multi-query attention; ``q``/``out`` are ``[rows, q_heads, 128]`` bf16.
+
+    ``planned=True`` reads the work plan that :func:`paged_attention_plan` wrote into
+    the same ``workspace`` for the same metadata (once per step, shared by the layers)."""
     device = _require_gpu(q, k_cache, v_cache, k_scale, v_scale, block_tables, ctx_len, q_start,
                           q_len)
     _check(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == HEAD_DIM,
@@ -215,11 +225,14 @@ def paged_verify_attention(
         num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len
     )
     _check(nbytes > 0, "bad attention shape")
-    ws = (workspace or default_workspace(device)).get(
-        device, nbytes, (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len)
-    )
+    workspace = workspace or default_workspace(device)
+    ws = workspace.get(device, nbytes, (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len))
+    if planned:
+        _check(workspace.plan_key == _plan_key(block_tables, block_size, ctx_len, q_start, q_len, max_q_len,
+                                               max_ctx_len, split_len),
+               "planned attention needs paged_attention_plan on the same metadata and workspace first")
     _native.call(
-        "ne_paged_verify_attention",
+        "ne_paged_verify_attention_planned" if planned else "ne_paged_verify_attention",
         _ptr(q), q.stride(0), q.stride(1),
         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
         dtype_code(k_cache.dtype), dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16,
@@ -231,6 +244,54 @@ def paged_verify_attention(
         split_len, _ptr(ws), ws.numel(), _stream(device),
     )
     return out
+
+
+def _plan_key(block_tables, block_size, ctx_len, q_start, q_len, max_q_len, max_ctx_len, split_len) -> tuple:
+    return (block_tables.data_ptr(), tuple(block_tables.shape), block_tables.stride(0), block_size,
+            ctx_len.data_ptr(), q_start.data_ptr(), q_len.data_ptr(), ctx_len.shape[0], max_q_len, max_ctx_len,
+            split_len)
+
+
+def paged_attention_plan(
+    block_tables: torch.Tensor,
+    block_size: int,
+    ctx_len: torch.Tensor,
+    q_start: torch.Tensor,
+    q_len: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    max_q_len: int,
+    max_ctx_len: int,
+    workspace: AttentionWorkspace,
+    split_len: int = 0,
+) -> None:
+    """Write the attention work plan for this metadata into ``workspace`` (int8 pools with
+    8 KV heads and at most 16 query rows per KV head)."""
+    device = _require_gpu(block_tables, ctx_len, q_start, q_len)
+    _int32(block_tables, "block_tables")
+    for name, t in (("ctx_len", ctx_len), ("q_start", q_start), ("q_len", q_len)):
+        _int32(t, name)
+    num_seqs = ctx_len.shape[0]
+    nbytes = _native.load().ne_paged_attention_workspace_size(
+        num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len
+    )
+    _check(nbytes > 0, "bad attention shape")
+    ws = workspace.get(device, nbytes, (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len))
+    _native.call(
+        "ne_paged_attention_plan",
+        _ptr(block_tables), block_tables.stride(0), block_size, _ptr(ctx_len), _ptr(q_start), _ptr(q_len),
+        num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len, _ptr(ws), ws.numel(),
+        _stream(device),
+    )
+    workspace.plan_key = _plan_key(block_tables, block_size, ctx_len, q_start, q_len, max_q_len, max_ctx_len,
+                                   split_len)
+
+
+def plan_supported(num_q_heads: int, num_kv_heads: int, max_q_len: int, num_seqs: int, kv_dtype, scale_dtype) -> bool:
+    """Whether :func:`paged_attention_plan` / ``planned=True`` serve this shape."""
+    return (kv_dtype == torch.int8 and scale_dtype in (torch.bfloat16, torch.float16) and num_kv_heads == 8
+            and num_q_heads % num_kv_heads == 0 and (num_q_heads // num_kv_heads) * max_q_len <= 16
+            and num_seqs <= 1024)
 
 
 # --------------------------------------------------------------------------- A8

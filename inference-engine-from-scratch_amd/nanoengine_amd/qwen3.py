@@ -250,6 +250,15 @@ class Qwen3VerifyModel:
         res, normed, delta = self.residual[:rows], self.normed[:rows], self.delta[:rows]
         qkv, q, attn, act = self.qkv[:rows], self.q[:rows], self.attn[:rows], self.act[:rows]
         kernels.embed_rmsnorm(tokens[:rows], w.embed, w.layers[0].input_layernorm, eps, residual=res, out=normed)
+        # the attention work plan depends only on this step's metadata: made once, read by
+        # every layer's attention call
+        planned = kernels.plan_supported(c.num_attention_heads, c.num_key_value_heads, batch.max_q_len,
+                                         batch.ctx_len.shape[0], pool.key_caches[0].dtype,
+                                         pool.key_scale_2d(0).dtype if pool.key_scale_2d(0) is not None else None)
+        if planned:
+            kernels.paged_attention_plan(batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start,
+                                         batch.q_len, c.num_attention_heads, c.num_key_value_heads,
+                                         batch.max_q_len, batch.max_ctx_len, self.workspace)
         for i, layer in enumerate(w.layers):
             kernels.w8a16_gemm(normed, layer.qkv_int8, layer.qkv_scale, out=qkv)
             kernels.qk_norm_rope_kv_write(
@@ -262,6 +271,7 @@ class Qwen3VerifyModel:
                 q, pool.key_caches[i], pool.value_caches[i], pool.key_scale_2d(i), pool.value_scale_2d(i),
                 batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start, batch.q_len,
                 batch.max_q_len, batch.max_ctx_len, self.softmax_scale, out=attn, workspace=self.workspace,
+                planned=planned,
             )
             self._project_add_norm(attn.view(rows, -1), layer.o_int8, layer.o_scale, self.o_splits[rows],
                                    layer.post_attention_layernorm, res, delta, normed)

@@ -128,3 +128,69 @@ def test_workspace_error_flag_reports_context_past_max(device):
                                    max_q_len=5, max_ctx_len=200, workspace=ws, split_len=128)
     torch.cuda.synchronize()
     assert ws.error_flag() != 0
+
+
+@pytest.mark.parametrize("ctx,q_lens,split_len,scale_dtype", [
+    ([5, 17, 40, 129, 300, 1000], [5, 1, 3, 5, 2, 5], 0, torch.bfloat16),
+    ([129, 259, 514, 1000, 2047], [5, 5, 4, 5, 5], 256, torch.float16),
+    ([65, 700, 128, 1500, 16, 900, 256, 1024], [5] * 8, 128, torch.bfloat16),
+])
+def test_planned_matches_unplanned(device, ctx, q_lens, split_len, scale_dtype):
+    """The per-step plan gives the same work items as the in-kernel plan: identical bits."""
+    num_blocks = max(64, sum((c + 15) // 16 for c in ctx) + 8)
+    kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, "int8", scale_dtype, seed=3)
+    tables, ctx_t, qs, ql, rows = make_batch(ctx, q_lens, num_blocks, 16, seed=4)
+    q = torch.randn(rows, HQ, 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    tables_d, ctx_d, qs_d, ql_d = d(tables), d(ctx_t), d(qs), d(ql)
+    args = (d(q), d(kc), d(vc), d(ks), d(vs), tables_d, 16, ctx_d, qs_d, ql_d)
+    ws = kernels.AttentionWorkspace()
+    a = kernels.paged_verify_attention(*args, max_q_len=max(q_lens), max_ctx_len=max(ctx), workspace=ws,
+                                       split_len=split_len)
+    kernels.paged_attention_plan(tables_d, 16, ctx_d, qs_d, ql_d, HQ, HKV, max(q_lens), max(ctx), ws,
+                                 split_len=split_len)
+    b = kernels.paged_verify_attention(*args, max_q_len=max(q_lens), max_ctx_len=max(ctx), workspace=ws,
+                                       split_len=split_len, planned=True)
+    torch.cuda.synchronize()
+    idx = real_rows(qs, ql)
+    assert torch.equal(a.cpu()[idx], b.cpu()[idx])
+    assert ws.error_flag() == 0
+    ref = paged_attention_reference(q, kc, vc, ks, vs, tables, 16, ctx_t, qs, ql, model_dtype=scale_dtype)
+    assert rel_err(b.cpu()[idx], ref[idx]) < TOL
+
+
+def test_planned_path_in_a_captured_graph_replays_like_eager(device):
+    """Plan + planned attention captured in a HIP graph, replayed several times with eager work
+    in between: every replay equals the eager result."""
+    ctx, q_lens = [300, 77, 1000, 513], [5, 5, 5, 5]
+    num_blocks = 128
+    kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, "int8", torch.float16, seed=6)
+    tables, ctx_t, qs, ql, rows = make_batch(ctx, q_lens, num_blocks, 16, seed=7)
+    q = torch.randn(rows, HQ, 128, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    tables, ctx_t, qs, ql, q, kc, vc, ks, vs = map(d, (tables, ctx_t, qs, ql, q, kc, vc, ks, vs))
+    out = torch.empty_like(q)
+    ws = kernels.AttentionWorkspace()
+
+    def body():
+        kernels.paged_attention_plan(tables, 16, ctx_t, qs, ql, HQ, HKV, 5, max(ctx), ws)
+        kernels.paged_verify_attention(q, kc, vc, ks, vs, tables, 16, ctx_t, qs, ql, max_q_len=5,
+                                       max_ctx_len=max(ctx), out=out, workspace=ws, planned=True)
+
+    body()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        body()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            body()
+    idx = real_rows(qs.cpu(), ql.cpu())
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu()[idx], eager.cpu()[idx]), f"replay {i}"
+        _ = (q.float() * 2).sum().item()  # eager work between replays
