@@ -26,7 +26,14 @@ Also reported on the same line:
                  achieved = algorithmic bytes per launch / average launch time from
                  HIP events on the launching stream; traffic = HBM bytes per launch
                  from two rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each
-                 scaled by what the counter reads for a 256 MiB copy.
+                 scaled by what the counter reads for a 256 MiB copy.  The verify step's
+                 sequence is timed: one plan per pass of the 28 pools, then 28 planned
+                 calls; `unplanned_avg_us` times the entry point that plans inside.
+                 Also under roofline: `bf16_config` (16 seqs, ctx U{256..2048}, bf16 KV)
+                 and `long_context_config` (32 seqs sharing a 1024-token prefix, suffixes
+                 U{4096..16384}, 9 queries for k = 8), both kernel-only.
+  sampled        the same verify step with temperature-0.8 rejection sampling on seeded
+                 uniforms (10 timed steps): step time, tok/s, accepted-per-step histogram
   gemm           the W8A16 projections (QKV, gate|up with SwiGLU, o and down split-K)
                  and the LM head at the step's 320 rows, kernel-only: 28 calls with
                  distinct weights replayed from a HIP graph (no host launch cost);
@@ -90,7 +97,8 @@ def gemm_traffic(m, n, k):
     return n * k + 2 * n + 2 * m * k + 2 * m * n
 
 
-def run_verify(args, torch):
+def run_verify(args, torch, temperature: float | None = None, steps: int | None = None,
+               warmup: int | None = None):
     from nanoengine_amd import _native
     from nanoengine_amd.config import EngineSettings
     from nanoengine_amd.interface import GenerationRequest, SamplingParams
@@ -99,7 +107,10 @@ def run_verify(args, torch):
     from nanoengine_amd.sequence_state import Sequence
 
     cfg = QWEN3_0_6B
-    total_steps = args.warmup + args.steps
+    temperature = args.temperature if temperature is None else temperature
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    total_steps = warmup + steps
     # every sequence must still be generating in the last timed step: a step emits at
     # most k + 1 tokens, so 128 tokens last >= 26 steps; longer runs get longer outputs
     max_new = max(OUTPUT_TOKENS, (K_DRAFT + 1) * total_steps + 2)
@@ -114,20 +125,20 @@ def run_verify(args, torch):
     eng = create_verify_engine(cfg, state, settings, max_prefill_rows=NUM_SEQS * PROMPT_MOTIF * PROMPT_REPEATS)
     del state
     log(f"engine ready {time.perf_counter() - t0:.1f}s")
-    params = SamplingParams(max_new_tokens=max_new, temperature=args.temperature, seed=0, ignore_eos=True)
+    params = SamplingParams(max_new_tokens=max_new, temperature=temperature, seed=0, ignore_eos=True)
     prompts = motif_prompts(NUM_SEQS, seed=0)
     seqs = [Sequence.from_request(GenerationRequest(f"s{i}", p, params)) for i, p in enumerate(prompts)]
     eng.runner.add(seqs)
     torch.cuda.synchronize()
     log("prefill done")
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         eng.runner.step()
     ctx_per_step, lengths_per_step = [], []
     torch.cuda.synchronize()
     start = time.perf_counter()
     tokens = 0
     kept_hist: dict[int, int] = {}
-    for _ in range(args.steps):
+    for _ in range(steps):
         lengths = {i: s.num_tokens for i, s in enumerate(eng.runner.slots) if s is not None}
         results = eng.runner.step()
         # context of sequence b in this step = its length before the step + its guesses
@@ -150,55 +161,118 @@ def run_verify(args, torch):
 
 
 class AttentionWorkload:
-    """Kernel-only int8 verify attention: 64 seqs, ctx U{128..1024} (seed 1), 5 queries,
-    fp16 scales, 4096-block pool, tables from a seeded permutation; `layers` distinct pools."""
+    """Kernel-only verify attention over `layers` distinct pools, tables from a seeded
+    permutation of the pool's blocks.
 
-    def __init__(self, torch, layers: int = 28):
+    int8: 64 seqs, ctx U{128..1024} (seed 1), 5 queries, fp16 scales, 4096-block pool.
+    bf16: 16 seqs, ctx U{256..2048} (seed 1), 5 queries, Q/K/V ~ N(0, 1), 4096-block pool.
+    long: 32 seqs sharing a 1024-token prefix (the same 64 blocks at the head of every
+          table), then a suffix of U{4096..16384} tokens (seed 1); 9 queries (k = 8),
+          int8 KV with bf16 scales."""
+
+    def __init__(self, torch, layers: int = 28, kind: str = "int8"):
         import numpy as np
 
         from nanoengine_amd import kernels
 
         dev = torch.device("cuda")
-        blocks, bs, hkv, hq = 4096, 16, 8, 16
+        bs, hkv, hq = 16, 8, 16
         rng = np.random.default_rng(1)
-        self.ctx = rng.integers(128, 1025, size=NUM_SEQS).astype(np.int32)
+        self.kind = kind
+        shared = 0
+        if kind == "int8":
+            self.ctx = rng.integers(128, 1025, size=NUM_SEQS).astype(np.int32)
+            self.ql = 5
+        elif kind == "bf16":
+            self.ctx = rng.integers(256, 2049, size=16).astype(np.int32)
+            self.ql = 5
+        else:
+            shared = 1024
+            self.ctx = (shared + rng.integers(4096, 16385, size=32)).astype(np.int32)
+            self.ql = 9
+        b = len(self.ctx)
+        own = [int(math.ceil((c - shared) / bs)) for c in self.ctx]
+        blocks = max(4096, shared // bs + sum(own) + 1)
         g = torch.Generator().manual_seed(1)
         perm = torch.randperm(blocks, generator=g).to(torch.int32)
         max_blocks = int(math.ceil(self.ctx.max() / bs))
-        tables = torch.zeros(NUM_SEQS, max_blocks, dtype=torch.int32)
-        cur = 0
-        for b, c in enumerate(self.ctx):
-            nb = int(math.ceil(c / bs))
-            tables[b, :nb] = perm[cur : cur + nb]
-            cur += nb
+        tables = torch.zeros(b, max_blocks, dtype=torch.int32)
+        prefix = perm[: shared // bs]
+        cur = shared // bs
+        for i, n in enumerate(own):
+            tables[i, : shared // bs] = prefix
+            tables[i, shared // bs : shared // bs + n] = perm[cur : cur + n]
+            cur += n
         slots = blocks * bs + 1
         self.pools = []
         for _ in range(layers):
-            kc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
-            vc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
-            ks = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(torch.float16)
-            vs = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(torch.float16)
-            self.pools.append((kc, vc, ks, vs))
-        self.rows = NUM_SEQS * 5
+            if kind == "bf16":
+                kc = torch.randn(slots, hkv, 128, device=dev).to(torch.bfloat16)
+                vc = torch.randn(slots, hkv, 128, device=dev).to(torch.bfloat16)
+                self.pools.append((kc, vc, None, None))
+            else:
+                sdt = torch.float16 if kind == "int8" else torch.bfloat16
+                kc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
+                vc = torch.randint(-127, 128, (slots, hkv, 128), dtype=torch.int8, device=dev)
+                ks = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(sdt)
+                vs = (torch.rand(slots, hkv, device=dev) * 0.03 + 0.005).to(sdt)
+                self.pools.append((kc, vc, ks, vs))
+        self.rows = b * self.ql
         self.q = torch.randn(self.rows, hq, 128, device=dev).to(torch.bfloat16)
         self.out = torch.empty_like(self.q)
         self.tables = tables.to(dev)
         self.ctx_d = torch.as_tensor(self.ctx).to(dev)
-        self.q_start = torch.arange(NUM_SEQS, dtype=torch.int32, device=dev) * 5
-        self.q_len = torch.full((NUM_SEQS,), 5, dtype=torch.int32, device=dev)
+        self.q_start = torch.arange(b, dtype=torch.int32, device=dev) * self.ql
+        self.q_len = torch.full((b,), self.ql, dtype=torch.int32, device=dev)
         self.ws = kernels.AttentionWorkspace()
-        self.bytes_per_launch = attention_bytes(self.ctx.tolist(), self.rows) + tables.numel() * 4
+        int8 = kind != "bf16"
+        self.bytes_per_launch = attention_bytes(self.ctx.tolist(), self.rows, int8=int8) + tables.numel() * 4
+        self.plannable = kind == "int8"
         self._kernels = kernels
 
     def plan(self) -> None:
         """The per-step work plan every layer's planned call reads (same metadata for all pools)."""
-        self._kernels.paged_attention_plan(self.tables, 16, self.ctx_d, self.q_start, self.q_len, 16, 8, 5,
+        self._kernels.paged_attention_plan(self.tables, 16, self.ctx_d, self.q_start, self.q_len, 16, 8, self.ql,
                                            int(self.ctx.max()), self.ws)
 
     def launch(self, pool, planned: bool = False) -> None:
         self._kernels.paged_verify_attention(
             self.q, pool[0], pool[1], pool[2], pool[3], self.tables, 16, self.ctx_d, self.q_start,
-            self.q_len, 5, int(self.ctx.max()), out=self.out, workspace=self.ws, planned=planned)
+            self.q_len, self.ql, int(self.ctx.max()), out=self.out, workspace=self.ws, planned=planned)
+
+
+ATTENTION_WORKLOADS = {
+    "bf16": "bf16 KV, 16 seqs, ctx U{256..2048} seed 1, q=5, Q/K/V N(0,1), 4096-block pool",
+    "long": "int8 KV (bf16 scales), 32 seqs sharing a 1024-token prefix + U{4096..16384} suffix seed 1, "
+            "q=9 (k=8)",
+}
+
+
+def run_attention_kernel_only(torch, kind: str, layers: int, reps: int = 3):
+    """Average time per unplanned attention call (HIP events around each call) for the bf16
+    and long-context workloads."""
+    from nanoengine_amd import _native
+
+    w = AttentionWorkload(torch, layers=layers, kind=kind)
+    for p in w.pools:
+        w.launch(p)
+    torch.cuda.synchronize()
+    timer = _native.LaunchTimer()
+    _native.set_launch_timer("ne_paged_verify_attention", timer)
+    for _ in range(reps):
+        for p in w.pools:
+            w.launch(p)
+    torch.cuda.synchronize()
+    _native.set_launch_timer("ne_paged_verify_attention", None)
+    dur = timer.durations_ms()
+    avg_ms = sum(dur) / len(dur)
+    achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    out = {"workload": ATTENTION_WORKLOADS[kind], "achieved": round(achieved, 1), "unit": "GB/s",
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
+           "bytes_per_launch": int(w.bytes_per_launch), "sum_ctx": int(w.ctx.sum()), "launches": len(dur)}
+    del w
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_attention_roofline(torch, reps: int = 5):
@@ -629,6 +703,10 @@ def main() -> int:
             attention["traffic"] = traffic["fetch_bytes"] + traffic["write_bytes"]
             attention["traffic_detail"] = traffic
         log(f"attention: {attention['avg_us']} us, {attention['achieved']} GB/s")
+        attention["bf16_config"] = run_attention_kernel_only(torch, "bf16", layers=28)
+        log(f"attention bf16: {attention['bf16_config']['avg_us']} us")
+        attention["long_context_config"] = run_attention_kernel_only(torch, "long", layers=8)
+        log(f"attention long context: {attention['long_context_config']['avg_us']} us")
     gemm = None
     if args.only in ("all", "gemm"):
         gemm = run_gemm_roofline(torch)
@@ -640,6 +718,15 @@ def main() -> int:
         ctx_len = int(round(res["mean_context"])) if res else PROMPT_MOTIF * PROMPT_REPEATS + 32
         torch_base = run_torch_baseline(torch, random_state_dict(QWEN3_0_6B, seed=0, std=0.02), ctx_len)
         log(f"torch baseline: {torch_base['verify_step_us']} us per step")
+    sampled = None
+    if args.only == "all":
+        # the same step with temperature-0.8 rejection sampling on seeded uniforms
+        s_res = run_verify(args, torch, temperature=0.8, steps=10, warmup=2)
+        s_step_us = 1e6 * s_res["elapsed"] / 10
+        sampled = {"temperature": 0.8, "steps": 10, "verify_step_us": round(s_step_us, 1),
+                   "accepted_tok_s": round(s_res["tokens"] / s_res["elapsed"], 1),
+                   "accepted_per_step_hist": {str(k): v for k, v in sorted(s_res["kept_hist"].items())}}
+        log(f"sampled: {sampled['verify_step_us']} us per step")
     cpu = None
     if args.only == "all" and not args.no_cpu_baseline:
         cpu = run_cpu_baseline(torch)
@@ -676,6 +763,7 @@ def main() -> int:
         "accepted_per_step_hist": {str(k): v for k, v in sorted(res["kept_hist"].items())},
         "roofline": attention,
         "gemm": gemm,
+        "sampled": sampled,
         "torch_baseline": torch_base,
         "cpu_baseline": cpu,
     }

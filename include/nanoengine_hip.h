@@ -135,9 +135,9 @@ int ne_paged_verify_attention(const void* q, int64_t q_token_stride, int64_t q_h
  * deriving it, which saves one dependent memory round trip per call.  Valid while
  * ctx_len, q_start, q_len, block_tables, num_seqs, max_q_len, max_ctx_len and
  * split_len stay as they were for the plan (a verify step's layers).  Both serve int8
- * caches with 8 KV heads, 2-byte scales and at most 16 query rows per KV head
- * (num_q_heads / num_kv_heads * max_q_len <= 16) and return NE_EUNSUPPORTED
- * otherwise; the workspace size is ne_paged_attention_workspace_size()'s.
+ * caches with 8 KV heads, 2-byte scales and at most 32 query rows per KV head
+ * (num_q_heads / num_kv_heads * max_q_len <= 32, i.e. up to k = 15 drafts) and return
+ * NE_EUNSUPPORTED otherwise; the workspace size is ne_paged_attention_workspace_size()'s.
  */
 int ne_paged_attention_plan(const int32_t* block_tables, int32_t block_table_stride,
                             int32_t block_size, const int32_t* ctx_len, const int32_t* q_start,

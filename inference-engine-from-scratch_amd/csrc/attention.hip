@@ -57,6 +57,7 @@ constexpr int kIterKeys = 32;   // keys per wave iteration
 constexpr int kTileKeys = 16;   // keys per MFMA tile (never straddles a block)
 constexpr int kMaxSplitLen = 2048;
 constexpr int kMaxTiles = kMaxSplitLen / kTileKeys;
+constexpr int kPlanMaxTiles = 512;  // tiles per split of the DMA kernel's plan (8192 keys)
 constexpr float kNegBig = -1e30f;  // finite "minus infinity" for running maxima
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.f;        // P <= 2^8 between rescales of the output
@@ -94,7 +95,7 @@ struct AttnParams {
   int32_t plan_grid;   // DMA kernel: work-groups launched
   int32_t max_ctx;     // the caller's bound on ctx_len
   int32_t* plan_desc;  // precomputed plan: [plan_grid][8] work items (seq < 0: none)
-  int32_t* plan_slots; // precomputed plan: [plan_grid][kMaxTiles] first slot of each tile
+  int32_t* plan_slots; // precomputed plan: [plan_grid][kPlanMaxTiles] first slot of each tile
 };
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -117,37 +118,48 @@ struct IterRegs<false> {
   u32x4 v[8];     // [key slot e]: 8 bf16 dims
 };
 
-// Two int8 codes -> two fp16 values in one dword, one SDWA convert each (exact:
-// |code| <= 127).  SAME: bytes B and B+1 of w.  TWO: byte B of x (low half) and
-// byte B of y (high half).
-#define NE_CVT_LO(B) "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #B "\n\t"
-#define NE_CVT_HI(B, OP) "v_cvt_f16_i16_sdwa %0, sext(" OP ") dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #B
+// int8 codes -> fp16 (exact: |code| <= 127), one SDWA convert per value, built as a
+// whole MFMA operand (4 dwords) per asm block.  The compiler sees no instruction
+// inside an asm block, so it cannot insert the wait states CDNA needs between a
+// VALU write of a VGPR and an MFMA reading it (two): every block ends with s_nop 1,
+// which gives them to whichever instruction consumes the result.
+#define NE_CVT_LO(D, S, B) "v_cvt_f16_i16_sdwa " D ", sext(" S ") dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #B "\n\t"
+#define NE_CVT_HI(D, S, B) "v_cvt_f16_i16_sdwa " D ", sext(" S ") dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #B "\n\t"
 
-template <int B>
-__device__ __forceinline__ uint32_t i8_pair_f16(uint32_t w) {
-  uint32_t r;
-  if constexpr (B == 0) {
-    asm(NE_CVT_LO(0) NE_CVT_HI(1, "%1") : "=&v"(r) : "v"(w));
-  } else {
-    asm(NE_CVT_LO(2) NE_CVT_HI(3, "%1") : "=&v"(r) : "v"(w));
-  }
-  return r;
+// K operand: bytes 0..3 of w0 then of w1, in order.
+__device__ __forceinline__ u32x4 i8x8_f16x8(uint32_t w0, uint32_t w1) {
+  uint32_t a, b, c, d;
+  asm(NE_CVT_LO("%0", "%4", 0) NE_CVT_HI("%0", "%4", 1) NE_CVT_LO("%1", "%4", 2) NE_CVT_HI("%1", "%4", 3)
+      NE_CVT_LO("%2", "%5", 0) NE_CVT_HI("%2", "%5", 1) NE_CVT_LO("%3", "%5", 2) NE_CVT_HI("%3", "%5", 3)
+      "s_nop 1"
+      : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+      : "v"(w0), "v"(w1));
+  return u32x4{a, b, c, d};
 }
 
+// V^T operand: byte B of each of the eight key rows x[0..7], in key order.
+#define NE_CVT_COLS(B)                                                                          \
+  asm(NE_CVT_LO("%0", "%4", B) NE_CVT_HI("%0", "%5", B) NE_CVT_LO("%1", "%6", B)               \
+          NE_CVT_HI("%1", "%7", B) NE_CVT_LO("%2", "%8", B) NE_CVT_HI("%2", "%9", B)            \
+              NE_CVT_LO("%3", "%10", B) NE_CVT_HI("%3", "%11", B) "s_nop 1"                     \
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])                                      \
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]))
+
 template <int B>
-__device__ __forceinline__ uint32_t i8_two_f16(uint32_t x, uint32_t y) {
-  uint32_t r;
+__device__ __forceinline__ u32x4 i8_cols_f16x8(const uint32_t (&x)[8]) {
+  uint32_t r[4];
   if constexpr (B == 0) {
-    asm(NE_CVT_LO(0) NE_CVT_HI(0, "%2") : "=&v"(r) : "v"(x), "v"(y));
+    NE_CVT_COLS(0);
   } else if constexpr (B == 1) {
-    asm(NE_CVT_LO(1) NE_CVT_HI(1, "%2") : "=&v"(r) : "v"(x), "v"(y));
+    NE_CVT_COLS(1);
   } else if constexpr (B == 2) {
-    asm(NE_CVT_LO(2) NE_CVT_HI(2, "%2") : "=&v"(r) : "v"(x), "v"(y));
+    NE_CVT_COLS(2);
   } else {
-    asm(NE_CVT_LO(3) NE_CVT_HI(3, "%2") : "=&v"(r) : "v"(x), "v"(y));
+    NE_CVT_COLS(3);
   }
-  return r;
+  return u32x4{r[0], r[1], r[2], r[3]};
 }
+#undef NE_CVT_COLS
 #undef NE_CVT_LO
 #undef NE_CVT_HI
 
@@ -290,10 +302,7 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if constexpr (INT8) {
-        const uint32_t w0 = R.k[t][c >> 1][2 * (c & 1)];
-        const uint32_t w1 = R.k[t][c >> 1][2 * (c & 1) + 1];
-        const u32x4 a = {i8_pair_f16<0>(w0), i8_pair_f16<2>(w0), i8_pair_f16<0>(w1),
-                         i8_pair_f16<2>(w1)};
+        const u32x4 a = i8x8_f16x8(R.k[t][c >> 1][2 * (c & 1)], R.k[t][c >> 1][2 * (c & 1) + 1]);
         s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf.q[c], s[t],
                                                       0, 0, 0);
       } else {
@@ -369,19 +378,17 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int w = j >> 2;
+      const uint32_t col[8] = {R.v[0][w], R.v[1][w], R.v[2][w], R.v[3][w],
+                               R.v[4][w], R.v[5][w], R.v[6][w], R.v[7][w]};
       u32x4 abits;
       if ((j & 3) == 0) {
-        abits = u32x4{i8_two_f16<0>(R.v[0][w], R.v[1][w]), i8_two_f16<0>(R.v[2][w], R.v[3][w]),
-                      i8_two_f16<0>(R.v[4][w], R.v[5][w]), i8_two_f16<0>(R.v[6][w], R.v[7][w])};
+        abits = i8_cols_f16x8<0>(col);
       } else if ((j & 3) == 1) {
-        abits = u32x4{i8_two_f16<1>(R.v[0][w], R.v[1][w]), i8_two_f16<1>(R.v[2][w], R.v[3][w]),
-                      i8_two_f16<1>(R.v[4][w], R.v[5][w]), i8_two_f16<1>(R.v[6][w], R.v[7][w])};
+        abits = i8_cols_f16x8<1>(col);
       } else if ((j & 3) == 2) {
-        abits = u32x4{i8_two_f16<2>(R.v[0][w], R.v[1][w]), i8_two_f16<2>(R.v[2][w], R.v[3][w]),
-                      i8_two_f16<2>(R.v[4][w], R.v[5][w]), i8_two_f16<2>(R.v[6][w], R.v[7][w])};
+        abits = i8_cols_f16x8<2>(col);
       } else {
-        abits = u32x4{i8_two_f16<3>(R.v[0][w], R.v[1][w]), i8_two_f16<3>(R.v[2][w], R.v[3][w]),
-                      i8_two_f16<3>(R.v[4][w], R.v[5][w]), i8_two_f16<3>(R.v[6][w], R.v[7][w])};
+        abits = i8_cols_f16x8<3>(col);
       }
       o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, abits), pb, o[j], 0,
                                                     0, 0);
@@ -410,6 +417,106 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
       o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, abits), pb, o[j],
                                                      0, 0, 0);
     }
+  }
+}
+
+// compute_iter for an int8 cache with MT row tiles of 16 (MT * 16 query rows per KV
+// head) in one wave: each K chunk and each V column block is converted once and
+// feeds every row tile's MFMAs, so with k = 8 drafts (18 rows per KV head) K/V are
+// read and converted once instead of once per row tile.
+template <int MT>
+__device__ __forceinline__ void compute_iter_mt(const AttnParams& p, const IterRegs<true>& R,
+                                                const QFrag<true> (&qf)[MT], float* s_sc, int kb,
+                                                const int (&kend_row)[MT], int lane, float (&m)[MT],
+                                                float (&l)[MT], floatx4 (&o)[MT][8]) {
+  const int g = lane >> 4;
+  // ---- S^T = K . Q^T per row tile: two 16x16 tiles (keys x rows) each ----
+  floatx4 s[MT][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) s[mt][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 a = i8x8_f16x8(R.k[t][c >> 1][2 * (c & 1)], R.k[t][c >> 1][2 * (c & 1) + 1]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        s[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf[mt].q[c],
+                                                          s[mt][t], 0, 0, 0);
+    }
+  }
+  // ---- per-key scale factors (lanes 0..31 key scales, 32..63 value scales) ----
+  s_sc[lane] = R.sc;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const floatx4 kf0 = *(const floatx4*)&s_sc[4 * g];
+  const floatx4 kf1 = *(const floatx4*)&s_sc[16 + 4 * g];
+  const floatx4 vf0 = *(const floatx4*)&s_sc[32 + 4 * g];
+  const floatx4 vf1 = *(const floatx4*)&s_sc[48 + 4 * g];
+  const float vmax = fmaxf(fmaxf(fmaxf(vf0[0], vf0[1]), fmaxf(vf0[2], vf0[3])),
+                           fmaxf(fmaxf(vf1[0], vf1[1]), fmaxf(vf1[2], vf1[3])));
+  // ---- masked scores, lazy online softmax and P per row tile ----
+  f16x8 pb[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    float sc[8];
+    float mx = kNegBig;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + 16 * t + 4 * g + i;
+        float v = s[mt][t][i] * p.qk_scale * (t ? kf1[i] : kf0[i]);
+        v = (key < kend_row[mt]) ? v : kNegBig;
+        sc[4 * t + i] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+    const bool grow = (mx > m[mt] + kLazyLog2) || (vmax > kLazyMaxVScale && mx > m[mt]);
+    if (__ballot(grow)) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m[mt], mx);
+      const float alpha = __builtin_amdgcn_exp2f(m[mt] - m_new);
+      l[mt] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[mt][j] *= alpha;
+      m[mt] = m_new;
+    }
+    float pr[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = kb + 16 * (e >> 2) + 4 * g + (e & 3);
+      pr[e] = (key < kend_row[mt]) ? __builtin_amdgcn_exp2f(sc[e] - m[mt]) : 0.f;
+      psum += pr[e];
+    }
+    l[mt] += psum;
+    const u32x4 pb_bits = {pack_f16x2(pr[0] * vf0[0], pr[1] * vf0[1]), pack_f16x2(pr[2] * vf0[2], pr[3] * vf0[3]),
+                           pack_f16x2(pr[4] * vf1[0], pr[5] * vf1[1]), pack_f16x2(pr[6] * vf1[2], pr[7] * vf1[3])};
+    pb[mt] = __builtin_bit_cast(f16x8, pb_bits);
+  }
+  // ---- O^T += V^T . P^T: eight 16x16 tiles (dims x rows) per row tile ----
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = j >> 2;
+    const uint32_t col[8] = {R.v[0][w], R.v[1][w], R.v[2][w], R.v[3][w],
+                             R.v[4][w], R.v[5][w], R.v[6][w], R.v[7][w]};
+    u32x4 abits;
+    if ((j & 3) == 0) {
+      abits = i8_cols_f16x8<0>(col);
+    } else if ((j & 3) == 1) {
+      abits = i8_cols_f16x8<1>(col);
+    } else if ((j & 3) == 2) {
+      abits = i8_cols_f16x8<2>(col);
+    } else {
+      abits = i8_cols_f16x8<3>(col);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      o[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, abits), pb[mt], o[mt][j],
+                                                        0, 0, 0);
   }
 }
 
@@ -618,7 +725,9 @@ constexpr int kScaleBytes = kTileKeys * kHeadWaves * 2;  // 256 B: a tile's scal
 constexpr int kDmaSlot = 2 * kTileRows + 2 * kScaleBytes;  // K | V | k-scales | v-scales
 constexpr int kDmaPerTile = 6;                       // 2 K + 2 V (1 KB each) + 2 scale dwords
 constexpr int kPlanInts = 32;                        // LDS ints of the work plan
-constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4 + kHeadWaves * kWave * 4 +
+constexpr int kMaxRowTiles = 2;                      // row tiles per KV head in one wave
+constexpr int kPartRows = kRows * kMaxRowTiles;      // rows per (work-group, KV head) partial
+constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4 + kHeadWaves * kWave * 4 +
                         kPlanInts * 4;
 constexpr int kPlanMaxSeqs = 2 * kHeadWaves * kWave;  // two sequences per thread
 constexpr int kPlanMinTiles = 16;                     // no split shorter than 256 keys
@@ -682,9 +791,9 @@ __device__ PlanScan plan_scan(const AttnParams& p, int* s_plan) {
   const int G = p.plan_grid;
   int W = p.plan_w;
   if (W <= 0) W = max(kPlanMinTiles, (T + (G - B) - 1) / (G - B));
-  if (W > kMaxTiles) {
+  if (W > kPlanMaxTiles) {
     if (tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
-    W = kMaxTiles;
+    W = kPlanMaxTiles;
   }
   ps.n[0] = (ps.tiles[0] + W - 1) / W;
   ps.n[1] = (ps.tiles[1] + W - 1) / W;
@@ -793,7 +902,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
     if (w >= p.plan_grid) continue;
     const int t = j - (int)((int64_t)tiles * s / n);
     const int key0 = j * kTileKeys;
-    p.plan_slots[(int64_t)w * kMaxTiles + t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+    p.plan_slots[(int64_t)w * kPlanMaxTiles + t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
   }
 }
 
@@ -868,12 +977,13 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
 
 // PLANNED: the work item and the split's slots come from attention_plan_kernel's
 // output instead of being derived here (one round trip instead of two).
-template <int SDT, bool PLANNED>
+// MT: row tiles of 16 per KV head handled by each wave (1, or 2 for up to 32 rows).
+template <int SDT, bool PLANNED, int MT>
 __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel(AttnParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* s_slot = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot);
-  float* s_sc_all = (float*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4);
-  int* s_plan = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kMaxTiles * 4 + kHeadWaves * kWave * 4);
+  float* s_sc_all = (float*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4);
+  int* s_plan = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4 + kHeadWaves * kWave * 4);
 
   // ---- work item: one split of one sequence (M tile 0); the wave is the KV head ----
   const int tid = threadIdx.x;
@@ -883,8 +993,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   if constexpr (PLANNED) {
     // the split's slots (entries past its tiles are never read) and its work item,
     // requested together
-    for (int t = tid; t < kMaxTiles; t += kHeadWaves * kWave)
-      s_slot[t] = p.plan_slots[(int64_t)blockIdx.x * kMaxTiles + t];
+    for (int t = tid; t < kPlanMaxTiles; t += kHeadWaves * kWave)
+      s_slot[t] = p.plan_slots[(int64_t)blockIdx.x * kPlanMaxTiles + t];
     const int32_t* d = p.plan_desc + (int64_t)blockIdx.x * kDescInts;
     item.seq = d[0];
     item.split = d[1];
@@ -901,7 +1011,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
                       item.split < item.n_splits && item.tiles >= item.n_splits &&
                       item.tiles <= max_tiles && item.ctx > 0 && item.ctx <= p.max_ctx &&
                       item.ql > 0 && item.qs >= 0 &&
-                      (item.tiles + item.n_splits - 1) / item.n_splits <= kMaxTiles;
+                      (item.tiles + item.n_splits - 1) / item.n_splits <= kPlanMaxTiles;
     if (!sane) {
       if (tid == 0) atomicOr(p.error_flag, 2u);
       return;
@@ -918,24 +1028,36 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   const int n_tiles = j1 - j0;
   const int ql = item.ql;
   const int rows_total = p.group * ql;
-  if (rows_total > kRows && tid == 0) atomicOr(p.error_flag, 1u);
+  if (rows_total > MT * kRows && tid == 0) atomicOr(p.error_flag, 1u);
 
+  // lane (r, g) owns row mt * 16 + r of row tile mt
   const int r = lane & 15;
   const int g = lane >> 4;
-  const bool row_valid = r < rows_total;
-  const int h_local = row_valid ? r / ql : 0;
-  const int qi = row_valid ? r % ql : 0;
-  const int kend_row = row_valid ? min(kend, item.ctx - ql + qi + 1) : kend;
+  bool row_valid[MT];
+  int h_local[MT], qi[MT], kend_row[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int R = mt * kRows + r;
+    row_valid[mt] = R < rows_total;
+    h_local[mt] = row_valid[mt] ? R / ql : 0;
+    qi[mt] = row_valid[mt] ? R % ql : 0;
+    kend_row[mt] = row_valid[mt] ? min(kend, item.ctx - ql + qi[mt] + 1) : kend;
+  }
 
   // Q and the split's block-table entries are fetched together; Q is converted
   // only after the ring's first copies are issued, so no wait sits between them
-  u32x4 raw[4] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
-  if (row_valid) {
-    const int64_t qoff = (int64_t)(item.qs + qi) * p.q_tok_stride +
-                         (int64_t)(head * p.group + h_local) * p.q_head_stride + 32 * g;
-    const u32x4* src = (const u32x4*)(p.q + qoff);
+  u32x4 raw[MT][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) raw[c] = src[c];
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) raw[mt][c] = u32x4{0, 0, 0, 0};
+    if (row_valid[mt]) {
+      const int64_t qoff = (int64_t)(item.qs + qi[mt]) * p.q_tok_stride +
+                           (int64_t)(head * p.group + h_local[mt]) * p.q_head_stride + 32 * g;
+      const u32x4* src = (const u32x4*)(p.q + qoff);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) raw[mt][c] = src[c];
+    }
   }
   if constexpr (!PLANNED) {
     const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
@@ -949,21 +1071,29 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   char* ring = smem + head * (kDmaRing * kDmaSlot);
 #pragma unroll
   for (int j = 0; j < kDmaRing; ++j) dma_tile(p, s_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
-  QFrag<true> qf;
+  QFrag<true> qf[MT];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    u32x4 hv;
+  for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[c][i] & 0xFFFFu)),
-                         bf16_to_f32((uint16_t)(raw[c][i] >> 16)));
-    qf.q[c] = __builtin_bit_cast(f16x8, hv);
+    for (int c = 0; c < 4; ++c) {
+      u32x4 hv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[mt][c][i] & 0xFFFFu)),
+                           bf16_to_f32((uint16_t)(raw[mt][c][i] >> 16)));
+      qf[mt].q[c] = __builtin_bit_cast(f16x8, hv);
+    }
   }
 
-  float m = kNegBig, l = 0.f;
-  floatx4 o[8];
+  float m[MT], l[MT];
+  floatx4 o[MT][8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt) {
+    m[mt] = kNegBig;
+    l[mt] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
   float* sc_row = s_sc_all + head * kWave;
   const int n_iter = (n_tiles + 1) / 2;
   for (int it = 0; it < n_iter; ++it) {
@@ -975,7 +1105,11 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     const int kb = kstart + it * kIterKeys;
     IterRegs<true> A;
     lds_iter<SDT>(sa, sb, kb, kend, head, lane, A);
-    compute_iter<true>(p, A, qf, sc_row, kb, kend_row, item.ctx, lane, m, l, o);
+    if constexpr (MT == 1) {
+      compute_iter<true>(p, A, qf[0], sc_row, kb, kend_row[0], item.ctx, lane, m[0], l[0], o[0]);
+    } else {
+      compute_iter_mt<MT>(p, A, qf, sc_row, kb, kend_row, lane, m, l, o);
+    }
     // the two slots are free once their reads have returned: refill them
     dma_wait_lgkmcnt0();
     dma_tile(p, s_slot, n_tiles, 2 * it + kDmaRing, head, lane, ring + ((2 * it) % kDmaRing) * kDmaSlot);
@@ -983,35 +1117,39 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
              ring + ((2 * it + 1) % kDmaRing) * kDmaSlot);
   }
   dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (!row_valid) return;
 
-  // lane (r, g) holds row r, dims 32g + 8i + j in o[j][i]
-  if (n_splits == 1) {
-    uint16_t* dst = p.out + (int64_t)(item.qs + qi) * p.o_tok_stride +
-                    (int64_t)(head * p.group + h_local) * p.o_head_stride + 32 * g;
-    const float inv = 1.f / l;
+  // lane (r, g) holds row r of tile mt, dims 32g + 8i + j in o[mt][j][i]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 bits = {pack_bf16x2(o[0][i] * inv, o[1][i] * inv),
-                          pack_bf16x2(o[2][i] * inv, o[3][i] * inv),
-                          pack_bf16x2(o[4][i] * inv, o[5][i] * inv),
-                          pack_bf16x2(o[6][i] * inv, o[7][i] * inv)};
-      *(u32x4*)(dst + 8 * i) = bits;
-    }
-  } else {
-    // partial slot: this work-group's index, which the plan gives the merge too
-    const int64_t pbase = ((int64_t)blockIdx.x * kHeadWaves + head) * kRows + r;
-    float* po = p.part_o + pbase * kHeadDim + 32 * g;
+  for (int mt = 0; mt < MT; ++mt) {
+    float lt = l[mt];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    if (!row_valid[mt]) continue;
+    if (n_splits == 1) {
+      uint16_t* dst = p.out + (int64_t)(item.qs + qi[mt]) * p.o_tok_stride +
+                      (int64_t)(head * p.group + h_local[mt]) * p.o_head_stride + 32 * g;
+      const float inv = 1.f / lt;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(floatx4*)(po + 8 * i) = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
-      *(floatx4*)(po + 8 * i + 4) = floatx4{o[4][i], o[5][i], o[6][i], o[7][i]};
-    }
-    if (g == 0) {
-      p.part_ml[pbase * 2] = m;
-      p.part_ml[pbase * 2 + 1] = l;
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 bits = {pack_bf16x2(o[mt][0][i] * inv, o[mt][1][i] * inv),
+                            pack_bf16x2(o[mt][2][i] * inv, o[mt][3][i] * inv),
+                            pack_bf16x2(o[mt][4][i] * inv, o[mt][5][i] * inv),
+                            pack_bf16x2(o[mt][6][i] * inv, o[mt][7][i] * inv)};
+        *(u32x4*)(dst + 8 * i) = bits;
+      }
+    } else {
+      // partial slot: this work-group's index, which the plan gives the merge too
+      const int64_t pbase = ((int64_t)blockIdx.x * kHeadWaves + head) * kPartRows + mt * kRows + r;
+      float* po = p.part_o + pbase * kHeadDim + 32 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(floatx4*)(po + 8 * i) = floatx4{o[mt][0][i], o[mt][1][i], o[mt][2][i], o[mt][3][i]};
+        *(floatx4*)(po + 8 * i + 4) = floatx4{o[mt][4][i], o[mt][5][i], o[mt][6][i], o[mt][7][i]};
+      }
+      if (g == 0) {
+        p.part_ml[pbase * 2] = m[mt];
+        p.part_ml[pbase * 2 + 1] = lt;
+      }
     }
   }
 }
@@ -1023,7 +1161,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
 // at once rather than in a dependent chain.
 constexpr int kMergeBatch = 8;
 
-__global__ __launch_bounds__(256) void attention_plan_merge_kernel(AttnParams p) {
+__global__ __launch_bounds__(kPartRows * 16) void attention_plan_merge_kernel(AttnParams p) {
   const int seq = blockIdx.x / kHeadWaves;
   const int head = blockIdx.x % kHeadWaves;
   const int first = p.plan[seq];
@@ -1034,7 +1172,7 @@ __global__ __launch_bounds__(256) void attention_plan_merge_kernel(AttnParams p)
   if (n_splits <= 1) return;
   const int crow = threadIdx.x >> 4;
   const int cd = (threadIdx.x & 15) * 8;
-  if (crow >= min(p.group * ql, kRows)) return;
+  if (crow >= min(p.group * ql, kPartRows)) return;
   float MM = kNegBig, LL = 0.f;
   float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
@@ -1044,7 +1182,7 @@ __global__ __launch_bounds__(256) void attention_plan_merge_kernel(AttnParams p)
     for (int j = 0; j < kMergeBatch; ++j) {
       // a slot past the sequence's last partial re-reads its first one and is ignored
       const int s = (s0 + j < n_splits) ? s0 + j : s0;
-      const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kRows + crow;
+      const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kPartRows + crow;
       const float2 ml = *(const float2*)(p.part_ml + pi * 2);
       ms[j] = (s0 + j < n_splits) ? ml.x : kNegBig;
       ls[j] = ml.y;
@@ -1123,8 +1261,8 @@ struct Layout {
   size_t part_o_off, part_ml_off, error_off, plan_off, desc_off, slots_off, total;
 };
 
-// Work-groups of the DMA kernel's plan: enough that W <= kMaxTiles for any
-// contexts up to max_ctx (G - B >= B ceil(max_ctx / 16) / kMaxTiles) and that G - B
+// Work-groups of the DMA kernel's plan: enough that W <= kPlanMaxTiles for any
+// contexts up to max_ctx (G - B >= B ceil(max_ctx / 16) / kPlanMaxTiles) and that G - B
 // >= B; at least one per CU.  With a fixed split length, one per split.
 int plan_grid(int num_seqs, int max_ctx, int split_len) {
   const int64_t max_tiles = ((int64_t)max(max_ctx, 1) + kTileKeys - 1) / kTileKeys;
@@ -1132,7 +1270,7 @@ int plan_grid(int num_seqs, int max_ctx, int split_len) {
     const int64_t w = split_len / kTileKeys;
     return (int)((int64_t)num_seqs * ((max_tiles + w - 1) / w));
   }
-  const int64_t need = num_seqs + ((int64_t)num_seqs * max_tiles + kMaxTiles - 1) / kMaxTiles;
+  const int64_t need = num_seqs + ((int64_t)num_seqs * max_tiles + kPlanMaxTiles - 1) / kPlanMaxTiles;
   int64_t g = 2 * (int64_t)num_seqs;
   if (g < kPlanCUs) g = kPlanCUs;
   if (g < need) g = need;
@@ -1168,19 +1306,19 @@ Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_le
   // partial-sum layout that follows
   // the fixed-split kernels index partials by (unit, split); the DMA kernel's plan
   // by (work-group, KV head) and needs (B + 1) plan entries
-  const bool plan = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && L.mtiles == 1;
+  const bool plan = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && L.mtiles <= kMaxRowTiles;
   L.plan_grid = plan ? plan_grid(num_seqs, max_ctx, fixed_split) : 0;
   L.plan_w = fixed_split / kTileKeys;
   size_t parts = (L.max_splits > 1) ? (size_t)L.units * L.max_splits * kRows : 0;
   const int plan_min_w = fixed_split > 0 ? fixed_split / kTileKeys : kPlanMinTiles;
   const bool plan_splits = ceil_div((int64_t)max(max_ctx, 1), kTileKeys) > plan_min_w;
-  if (plan && plan_splits) parts = max(parts, (size_t)L.plan_grid * kHeadWaves * kRows);
+  if (plan && plan_splits) parts = max(parts, (size_t)L.plan_grid * kHeadWaves * kPartRows);
   L.error_off = take(sizeof(uint32_t));
   L.part_o_off = take(parts * kHeadDim * sizeof(float));
   L.part_ml_off = take(parts * 2 * sizeof(float));
   L.plan_off = take(plan ? ((size_t)num_seqs + 1) * sizeof(int32_t) : 0);
   L.desc_off = take(plan ? (size_t)L.plan_grid * kDescInts * sizeof(int32_t) : 0);
-  L.slots_off = take(plan ? (size_t)L.plan_grid * kMaxTiles * sizeof(int32_t) : 0);
+  L.slots_off = take(plan ? (size_t)L.plan_grid * kPlanMaxTiles * sizeof(int32_t) : 0);
   L.total = off;
   return L;
 }
@@ -1206,24 +1344,31 @@ int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStre
 
 // The DMA kernel serves int8 caches with 8 KV heads and 2-byte scales; it needs
 // the attribute for more than the default dynamic LDS once per instantiation.
-template <int SDT, bool PLANNED>
-int launch_attention_dma(const AttnParams& p, hipStream_t s) {
+template <int SDT, bool PLANNED, int MT>
+int launch_attention_dma_mt(const AttnParams& p, hipStream_t s) {
   static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)paged_attention_dma_kernel<SDT, PLANNED>, hipFuncAttributeMaxDynamicSharedMemorySize,
+      (const void*)paged_attention_dma_kernel<SDT, PLANNED, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
       kDmaLds);
   if (attr != hipSuccess) {
     set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", kDmaLds,
               hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED>), dim3((unsigned)p.plan_grid),
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT>), dim3((unsigned)p.plan_grid),
                      dim3(kHeadWaves * kWave), kDmaLds, s, p);
   int rc = check_launch("paged_attention_dma_kernel");
   // no sequence is split when every context fits in one split's minimum length
   const int min_w = p.plan_w > 0 ? p.plan_w : kPlanMinTiles;
   if (rc != NE_OK || ceil_div(p.max_ctx, kTileKeys) <= min_w) return rc;
-  hipLaunchKernelGGL(attention_plan_merge_kernel, dim3((unsigned)p.num_seqs * kHeadWaves), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(attention_plan_merge_kernel, dim3((unsigned)p.num_seqs * kHeadWaves),
+                     dim3(kPartRows * 16), 0, s, p);
   return check_launch("attention_plan_merge_kernel");
+}
+
+template <int SDT, bool PLANNED>
+int launch_attention_dma(const AttnParams& p, hipStream_t s) {
+  return p.mtiles == 1 ? launch_attention_dma_mt<SDT, PLANNED, 1>(p, s)
+                       : launch_attention_dma_mt<SDT, PLANNED, 2>(p, s);
 }
 
 // Validates the arguments and fills the kernel parameters; NE_OK or an error code.
@@ -1345,7 +1490,7 @@ extern "C" int ne_paged_verify_attention(
   // balanced plan.  Other int8 shapes: one wave per KV head, registers
   // double-buffered (154 VGPRs); bf16: single-buffered (double-buffered it needs
   // 244 VGPRs).  Both on fixed-length splits.
-  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles == 1 &&
+  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles <= kMaxRowTiles &&
                       num_seqs <= kPlanMaxSeqs && scale_dtype != NE_DTYPE_FP32 &&
                       ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
   if (dma_ok) {
@@ -1375,9 +1520,9 @@ extern "C" int ne_paged_attention_plan(const int32_t* block_tables, int32_t bloc
                "split_len must be 0 or a positive multiple of 128 up to %d", kMaxSplitLen);
   const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len,
                                split_len, NE_DTYPE_INT8);
-  NE_CHECK_SUPPORTED(num_kv_heads == kHeadWaves && L.mtiles == 1 && num_seqs <= kPlanMaxSeqs,
-                     "a precomputed plan serves 8 KV heads, at most 16 query rows per KV head "
-                     "and at most %d sequences", kPlanMaxSeqs);
+  NE_CHECK_SUPPORTED(num_kv_heads == kHeadWaves && L.mtiles <= kMaxRowTiles && num_seqs <= kPlanMaxSeqs,
+                     "a precomputed plan serves 8 KV heads, at most %d query rows per KV head "
+                     "and at most %d sequences", kMaxRowTiles * kRows, kPlanMaxSeqs);
   NE_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total,
                "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
   AttnParams p{};
@@ -1422,12 +1567,12 @@ extern "C" int ne_paged_verify_attention_planned(
                              max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
                              out_head_stride, split_len, workspace, workspace_bytes, p);
   if (rc != NE_OK) return rc;
-  NE_CHECK_SUPPORTED(kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles == 1 &&
+  NE_CHECK_SUPPORTED(kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles <= kMaxRowTiles &&
                          num_seqs <= kPlanMaxSeqs &&
                          (scale_dtype == NE_DTYPE_BF16 || scale_dtype == NE_DTYPE_FP16) &&
                          ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0,
                      "the planned path serves int8 caches with 8 KV heads, 2-byte 4-byte-aligned "
-                     "scales and at most 16 query rows per KV head");
+                     "scales and at most 32 query rows per KV head");
   return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, true>(p, (hipStream_t)stream)
                                       : launch_attention_dma<NE_DTYPE_FP16, true>(p, (hipStream_t)stream);
 }

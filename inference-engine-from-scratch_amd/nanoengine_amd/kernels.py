@@ -266,7 +266,7 @@ def paged_attention_plan(
     split_len: int = 0,
 ) -> None:
     """Write the attention work plan for this metadata into ``workspace`` (int8 pools with
-    8 KV heads and at most 16 query rows per KV head)."""
+    8 KV heads and at most 32 query rows per KV head)."""
     device = _require_gpu(block_tables, ctx_len, q_start, q_len)
     _int32(block_tables, "block_tables")
     for name, t in (("ctx_len", ctx_len), ("q_start", q_start), ("q_len", q_len)):
@@ -290,7 +290,7 @@ def paged_attention_plan(
 def plan_supported(num_q_heads: int, num_kv_heads: int, max_q_len: int, num_seqs: int, kv_dtype, scale_dtype) -> bool:
     """Whether :func:`paged_attention_plan` / ``planned=True`` serve this shape."""
     return (kv_dtype == torch.int8 and scale_dtype in (torch.bfloat16, torch.float16) and num_kv_heads == 8
-            and num_q_heads % num_kv_heads == 0 and (num_q_heads // num_kv_heads) * max_q_len <= 16
+            and num_q_heads % num_kv_heads == 0 and (num_q_heads // num_kv_heads) * max_q_len <= 32
             and num_seqs <= 1024)
 
 

@@ -65,14 +65,14 @@ def test_workspace_and_tile_queries(lib):
     one_split = lib.ne_paged_attention_workspace_size(64, 16, 8, 5, 256, 256)
     four_splits = lib.ne_paged_attention_workspace_size(64, 16, 8, 5, 1024, 256)
     # no partial sums: the error flag, the int8 work plan's 65 prefix entries, and the
-    # precomputed plan's 64 work items (8 ints) and slot lists (128 ints)
-    assert one_split == 256 + 512 + 64 * 8 * 4 + 64 * 128 * 4
+    # precomputed plan's 64 work items (8 ints) and slot lists (512 ints)
+    assert one_split == 256 + 512 + 64 * 8 * 4 + 64 * 512 * 4
     # partials: units x splits x 16 rows x (128 + 2) fp32
     assert four_splits >= 256 + 64 * 8 * 4 * 16 * 130 * 4
 
 
 def test_plan_entry_points_refuse_shapes_off_the_planned_path(lib):
-    """The precomputed plan serves 8 KV heads and <= 16 query rows per KV head (int8 with
+    """The precomputed plan serves 8 KV heads and <= 32 query rows per KV head (int8 with
     2-byte scales for the attention call); anything else is refused before a launch."""
     p = ctypes.c_void_p(256)
     null = ctypes.c_void_p(0)
@@ -80,8 +80,8 @@ def test_plan_entry_points_refuse_shapes_off_the_planned_path(lib):
     # 4 KV heads
     rc = lib.ne_paged_attention_plan(p, 64, 16, p, p, p, 8, 16, 4, 5, 1024, 0, p, ws, null)
     assert rc == -2 and b"8 KV heads" in lib.ne_last_error()
-    # 2 q heads per KV head x 9 queries = 18 rows per KV head
-    rc = lib.ne_paged_attention_plan(p, 64, 16, p, p, p, 8, 16, 8, 9, 1024, 0, p, ws, null)
+    # 2 q heads per KV head x 17 queries = 34 rows per KV head
+    rc = lib.ne_paged_attention_plan(p, 64, 16, p, p, p, 8, 16, 8, 17, 1024, 0, p, ws, null)
     assert rc == -2
     # bf16 cache on the planned attention call
     rc = lib.ne_paged_verify_attention_planned(p, 2048, 128, p, p, null, null, 0, 0, p, 64, 16, p, p, p,

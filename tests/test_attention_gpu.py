@@ -134,6 +134,7 @@ def test_workspace_error_flag_reports_context_past_max(device):
     ([5, 17, 40, 129, 300, 1000], [5, 1, 3, 5, 2, 5], 0, torch.bfloat16),
     ([129, 259, 514, 1000, 2047], [5, 5, 4, 5, 5], 256, torch.float16),
     ([65, 700, 128, 1500, 16, 900, 256, 1024], [5] * 8, 128, torch.bfloat16),
+    ([300, 1500, 2100, 40, 9], [9, 9, 7, 9, 9], 0, torch.float16),  # k = 8: two row tiles per KV head
 ])
 def test_planned_matches_unplanned(device, ctx, q_lens, split_len, scale_dtype):
     """The per-step plan gives the same work items as the in-kernel plan: identical bits."""
@@ -194,3 +195,31 @@ def test_planned_path_in_a_captured_graph_replays_like_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(out.cpu()[idx], eager.cpu()[idx]), f"replay {i}"
         _ = (q.float() * 2).sum().item()  # eager work between replays
+
+
+@pytest.mark.parametrize("split_len", [0, 128])
+def test_k8_long_contexts_with_a_shared_prefix(device, split_len):
+    """k = 8 (9 queries, 18 rows per KV head) over long contexts whose first 64 blocks are the
+    same physical blocks in every table (a shared prefix), int8 with bf16 scales."""
+    bs, shared = 16, 1024
+    ctx = [shared + 300, shared + 2500, shared + 17, shared + 1200]
+    own = [(c - shared + bs - 1) // bs for c in ctx]
+    num_blocks = shared // bs + sum(own) + 8
+    kc, vc, ks, vs = make_pool(num_blocks, bs, HKV, "int8", torch.bfloat16, seed=11)
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(12)).to(torch.int32)
+    tables = torch.zeros(len(ctx), max((c + bs - 1) // bs for c in ctx), dtype=torch.int32)
+    cur = shared // bs
+    for i, n in enumerate(own):
+        tables[i, : shared // bs] = perm[: shared // bs]
+        tables[i, shared // bs : shared // bs + n] = perm[cur : cur + n]
+        cur += n
+    ql = torch.full((len(ctx),), 9, dtype=torch.int32)
+    qs = torch.arange(len(ctx), dtype=torch.int32) * 9
+    ctx_t = torch.tensor(ctx, dtype=torch.int32)
+    q = torch.randn(9 * len(ctx), HQ, 128, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
+    ref = paged_attention_reference(q, kc, vc, ks, vs, tables, bs, ctx_t, qs, ql, model_dtype=torch.bfloat16)
+    d = lambda t: t.to(device)
+    out = kernels.paged_verify_attention(d(q), d(kc), d(vc), d(ks), d(vs), d(tables), bs, d(ctx_t), d(qs), d(ql),
+                                         max_q_len=9, max_ctx_len=max(ctx), split_len=split_len)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu(), ref) < TOL
