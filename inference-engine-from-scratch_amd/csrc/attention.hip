@@ -1019,6 +1019,15 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   } else {
     if (!plan_item(p, s_plan, item)) return;
   }
+  // the item is the same for the whole work-group: keep it in scalar registers, so
+  // that the loop and its waits are compiled as uniform
+  item.seq = __builtin_amdgcn_readfirstlane(item.seq);
+  item.split = __builtin_amdgcn_readfirstlane(item.split);
+  item.n_splits = __builtin_amdgcn_readfirstlane(item.n_splits);
+  item.tiles = __builtin_amdgcn_readfirstlane(item.tiles);
+  item.ctx = __builtin_amdgcn_readfirstlane(item.ctx);
+  item.ql = __builtin_amdgcn_readfirstlane(item.ql);
+  item.qs = __builtin_amdgcn_readfirstlane(item.qs);
   const int seq = item.seq;
   const int n_splits = item.n_splits;
   const int j0 = (int)((int64_t)item.tiles * item.split / n_splits);
@@ -1046,18 +1055,17 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
 
   // Q and the split's block-table entries are fetched together; Q is converted
   // only after the ring's first copies are issued, so no wait sits between them
+  // The loads are unconditional (an invalid row re-reads the sequence's first row
+  // and is zeroed after): a load under a lane-divergent branch makes the compiler
+  // wait for every memory operation in flight, the ring's first copies included.
   u32x4 raw[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    const int64_t qoff = (int64_t)(item.qs + qi[mt]) * p.q_tok_stride +
+                         (int64_t)(head * p.group + h_local[mt]) * p.q_head_stride + 32 * g;
+    const u32x4* src = (const u32x4*)(p.q + qoff);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) raw[mt][c] = u32x4{0, 0, 0, 0};
-    if (row_valid[mt]) {
-      const int64_t qoff = (int64_t)(item.qs + qi[mt]) * p.q_tok_stride +
-                           (int64_t)(head * p.group + h_local[mt]) * p.q_head_stride + 32 * g;
-      const u32x4* src = (const u32x4*)(p.q + qoff);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) raw[mt][c] = src[c];
-    }
+    for (int c = 0; c < 4; ++c) raw[mt][c] = src[c];
   }
   if constexpr (!PLANNED) {
     const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
@@ -1071,6 +1079,9 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   char* ring = smem + head * (kDmaRing * kDmaSlot);
 #pragma unroll
   for (int j = 0; j < kDmaRing; ++j) dma_tile(p, s_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
+  // Q was issued before the ring's copies: wait for it alone (the compiler's own wait
+  // would also drain the copies, since it does not order them after the Q loads)
+  dma_wait_vmcnt<kDmaPerTile * kDmaRing>();
   QFrag<true> qf[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -1078,9 +1089,10 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     for (int c = 0; c < 4; ++c) {
       u32x4 hv;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(raw[mt][c][i] & 0xFFFFu)),
-                           bf16_to_f32((uint16_t)(raw[mt][c][i] >> 16)));
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = row_valid[mt] ? raw[mt][c][i] : 0u;
+        hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(w & 0xFFFFu)), bf16_to_f32((uint16_t)(w >> 16)));
+      }
       qf[mt].q[c] = __builtin_bit_cast(f16x8, hv);
     }
   }
