@@ -1,11 +1,16 @@
 """Engine settings from ``NANOENGINE_*`` variables (ne/config.py:23-108, ne/constants.py:6-7).
 
 Same field names, defaults and cross-field checks as the reference's
-EngineSettings, restated without pydantic-settings.  One deliberate widening:
-the reference refuses speculation with a batched scheduler (ne/config.py:91-97)
-because its verify step handles one sequence; the HIP path verifies a whole
-batch per step, so ``scheduler=static|continuous`` with ``speculative=ngram`` is
-accepted here.  Speculation with the prefix cache stays refused.
+EngineSettings, restated without pydantic-settings.  Two deliberate widenings of
+ne/config.py:91-97:
+
+* the reference refuses speculation with a batched scheduler because its verify
+  step handles one sequence; the HIP path verifies a whole batch per step, so
+  ``scheduler=static|continuous`` with ``speculative=ngram`` is accepted;
+* the reference refuses speculation with the prefix cache because its verify
+  step registers blocks while the guesses are still part of the sequence
+  (model_runner.py:60-61); the HIP runner registers only verified blocks after
+  acceptance, so ``prefix_cache=true`` with ``speculative=ngram`` is accepted.
 """
 
 from __future__ import annotations
@@ -87,7 +92,7 @@ class EngineSettings:
         return self.served_model_name or self.model_id
 
     def _check_combinations(self) -> None:
-        """ne/config.py:81-98, with batched speculation allowed (see module docstring)."""
+        """ne/config.py:81-98, with batched and prefix-cached speculation allowed (see module docstring)."""
         if self.is_batched and self.kv_cache == "none":
             raise ValueError(f"scheduler={self.scheduler} needs kv_cache=contiguous or paged")
         if self.prefix_cache and self.kv_cache != "paged":
@@ -96,8 +101,10 @@ class EngineSettings:
             raise ValueError("chunked_prefill needs scheduler=continuous")
         if self.kv_cache == "none" and (self.kv_cache_dtype == "int8" or self.cuda_graphs):
             raise ValueError("kv_cache_dtype=int8 and cuda_graphs need a KV cache")
-        if self.speculative != "none" and (self.kv_cache == "none" or self.prefix_cache):
-            raise ValueError("speculative decoding needs a KV cache and no prefix cache")
+        if self.speculative != "none" and self.kv_cache == "none":
+            raise ValueError("speculative decoding needs a KV cache")
+        if self.speculative == "draft" and self.prefix_cache:
+            raise ValueError("draft-model speculation does not support the prefix cache")
 
     @classmethod
     def from_env(cls, environ: dict[str, str] | None = None) -> "EngineSettings":

@@ -1,7 +1,8 @@
-"""KV memory: the slot pool and the paged allocator.
+"""KV memory: the slot pool, the paged allocator and the prefix cache.
 
 Host-side counterparts of ne/engine/memory/kv_cache_pool.py:11-69,
-block_allocator.py:8-33, paged_allocator.py:16-79 and slot_allocator.py:10-38.
+block_allocator.py:8-33, paged_allocator.py:16-79, slot_allocator.py:10-38 and
+prefix_cache.py:21-158.
 The pool keeps the reference layout so the kernels read it in place: per layer
 ``[num_slots + 1, kv_heads, head_dim]`` (int8 or model dtype) plus, for an int8
 cache, scales ``[num_slots + 1, kv_heads, 1]`` in the model dtype; the last slot
@@ -11,7 +12,7 @@ is the scratch slot that padded rows write to.
 from __future__ import annotations
 
 import math
-from collections import deque
+from collections import OrderedDict, deque
 
 import numpy as np
 import torch
@@ -89,11 +90,17 @@ class BlockAllocator:
         self._free.append(block)
 
 
+def _request_id(sequence) -> str:
+    """The allocators take a ``Sequence`` (as the reference's do) or its request id."""
+    return sequence if isinstance(sequence, str) else sequence.request_id
+
+
 class PagedSlotAllocator:
     """Block tables per request (paged_allocator.py:21-79).
 
     Rollback of rejected guesses frees nothing: blocks reserved for them stay in
-    the table and are overwritten later, as in the reference.
+    the table and are overwritten later, as in the reference.  Every method takes
+    a ``Sequence`` or its request id.
     """
 
     def __init__(self, num_blocks: int, block_size: int, device: torch.device) -> None:
@@ -118,44 +125,226 @@ class PagedSlotAllocator:
     def num_prefix_hit_tokens(self) -> int:
         return 0
 
-    def block_table(self, request_id: str) -> list[int]:
-        return list(self._tables.get(request_id, []))
+    def block_table(self, sequence) -> list[int]:
+        return list(self._tables.get(_request_id(sequence), []))
 
-    def count_missing_blocks(self, request_id: str, num_tokens: int) -> int:
-        owned = len(self._tables.get(request_id, []))
+    def count_missing_blocks(self, sequence, num_tokens: int) -> int:
+        owned = len(self._tables.get(_request_id(sequence), []))
         return max(0, math.ceil(num_tokens / self.block_size) - owned)
 
-    def can_reserve(self, request_id: str, num_tokens: int) -> bool:
-        return self.count_missing_blocks(request_id, num_tokens) <= self._blocks.num_free_blocks
+    def can_reserve(self, sequence, num_tokens: int) -> bool:
+        return self.count_missing_blocks(sequence, num_tokens) <= self._blocks.num_free_blocks
 
-    def reserve(self, request_id: str, num_tokens: int) -> list[int]:
-        """Grow the table to hold ``num_tokens``; returns the newly added blocks."""
-        if not self.can_reserve(request_id, num_tokens):
-            raise OutOfKVMemoryError(f"no blocks for {num_tokens} tokens of {request_id}")
-        table = self._tables.setdefault(request_id, [])
-        added = [self._blocks.allocate() for _ in range(self.count_missing_blocks(request_id, num_tokens))]
+    def reserve(self, sequence, num_tokens: int) -> list[int]:
+        """Grow the table to hold ``num_tokens``; returns the newly allocated blocks."""
+        rid = _request_id(sequence)
+        if self.count_missing_blocks(rid, num_tokens) > self._blocks.num_free_blocks:
+            raise OutOfKVMemoryError(f"no blocks for {num_tokens} tokens of {rid}")
+        table = self._tables.setdefault(rid, [])
+        added = [self._blocks.allocate() for _ in range(self.count_missing_blocks(rid, num_tokens))]
         table.extend(added)
         return added
 
-    def free(self, request_id: str) -> None:
-        for block in self._tables.pop(request_id, []):
+    def free(self, sequence) -> None:
+        for block in self._tables.pop(_request_id(sequence), []):
             self._blocks.free(block)
 
-    def on_tokens_cached(self, request_id: str) -> None:
+    def on_tokens_cached(self, sequence) -> None:
         """Called after a step wrote more of a sequence into the cache (no-op without a prefix cache)."""
 
-    def slots_for(self, request_id: str, positions: np.ndarray) -> np.ndarray:
-        table = np.asarray(self._tables[request_id], dtype=np.int64)
+    def first_writable_position(self, sequence) -> int:
+        """Positions below this one sit in blocks other requests may read (none here)."""
+        return 0
+
+    def slots_for(self, sequence, positions: np.ndarray) -> np.ndarray:
+        table = np.asarray(self._tables[_request_id(sequence)], dtype=np.int64)
         return table[positions // self.block_size] * self.block_size + positions % self.block_size
 
-    def build_context_slots(self, request_ids: list[str], context_length: int) -> torch.Tensor:
+    def build_context_slots(self, sequences: list, context_length: int) -> torch.Tensor:
         """paged_allocator.py:69-79 (kept for API parity; the kernels read block tables)."""
         per_row = math.ceil(context_length / self.block_size)
+        request_ids = [_request_id(x) for x in sequences]
         rows = [(self._tables[r][:per_row] + [0] * per_row)[:per_row] for r in request_ids]
         tables = torch.tensor(rows, dtype=torch.int64)
         positions = torch.arange(context_length)
         slots = tables[:, positions // self.block_size] * self.block_size + positions % self.block_size
         return slots.to(self._device)
+
+
+ROOT_PARENT_HASH = 0
+
+
+def build_block_keys(token_ids, block_size: int, num_blocks: int) -> list[tuple[int, tuple[int, ...]]]:
+    """Keys of the first ``num_blocks`` full blocks (prefix_cache.py:25-34).
+
+    A key is (hash of the previous block's key, this block's tokens), so equal keys
+    mean equal whole prefixes, not only equal 16-token windows.  Python's hash of a
+    tuple of ints is deterministic, so keys agree across processes and with the
+    reference's."""
+    keys = []
+    parent = ROOT_PARENT_HASH
+    for start in range(0, num_blocks * block_size, block_size):
+        key = (parent, tuple(token_ids[start:start + block_size]))
+        keys.append(key)
+        parent = hash(key)
+    return keys
+
+
+class CachingBlockPool:
+    """Reference-counted blocks whose content outlives their last owner (prefix_cache.py:37-97).
+
+    A block with no owner is either empty (never registered) or cached (registered
+    under a key, still holding that prefix's keys/values).  ``allocate`` takes an
+    empty block first, then evicts the least recently freed cached block; ``share``
+    takes one more reference to a cached block, reviving it if it was free."""
+
+    def __init__(self, num_blocks: int) -> None:
+        self.num_blocks = num_blocks
+        self._refs = np.zeros(num_blocks, dtype=np.int64)
+        self._empty: deque[int] = deque(range(num_blocks))
+        self._cached_free: OrderedDict[int, None] = OrderedDict()  # least recently freed first
+        self._block_of: dict = {}
+        self._key_of: dict[int, tuple] = {}
+
+    @property
+    def num_free_blocks(self) -> int:
+        return len(self._empty) + len(self._cached_free)
+
+    @property
+    def num_used_blocks(self) -> int:
+        return self.num_blocks - self.num_free_blocks
+
+    def reference_count(self, block: int) -> int:
+        return int(self._refs[block])
+
+    def is_free(self, block: int) -> bool:
+        return self._refs[block] == 0
+
+    def is_registered(self, block: int) -> bool:
+        return block in self._key_of
+
+    def allocate(self) -> int:
+        if self._empty:
+            block = self._empty.popleft()
+        elif self._cached_free:
+            block = next(iter(self._cached_free))
+            del self._cached_free[block]
+            del self._block_of[self._key_of.pop(block)]
+        else:
+            raise OutOfKVMemoryError("no free KV blocks")
+        self._refs[block] = 1
+        return block
+
+    def free(self, block: int) -> None:
+        if self._refs[block] <= 0:
+            raise ValueError(f"block {block} is not allocated")
+        self._refs[block] -= 1
+        if self._refs[block] == 0:
+            if block in self._key_of:
+                self._cached_free[block] = None
+            else:
+                self._empty.append(block)
+
+    def find(self, key) -> int | None:
+        return self._block_of.get(key)
+
+    def share(self, block: int) -> None:
+        if self._refs[block] == 0:
+            self._cached_free.pop(block)
+        self._refs[block] += 1
+
+    def register(self, block: int, key) -> None:
+        """Record that ``block`` holds ``key``'s prefix; an existing key or block keeps its entry."""
+        if key not in self._block_of and block not in self._key_of:
+            self._block_of[key] = block
+            self._key_of[block] = key
+
+
+class PrefixCachingSlotAllocator(PagedSlotAllocator):
+    """Paged allocator that shares full prompt blocks between requests (prefix_cache.py:100-158).
+
+    Speculation-safe by its call sites, not by extra state: a block is registered only
+    from ``on_tokens_cached(sequence)``, which keys blocks by ``sequence.token_ids`` and
+    counts ``sequence.num_cached_tokens``.  The verify runner calls it after acceptance,
+    when ``token_ids`` holds verified tokens only and ``num_cached_tokens`` counts the
+    positions whose keys/values belong to them (the reference calls it from
+    score_tokens while the guesses are still appended, model_runner.py:60-61, which
+    would register blocks keyed by rejected guesses).  Registered blocks end below
+    ``num_cached_tokens`` and a step only writes at ``num_cached_tokens`` and later, so
+    no step - a rejected guess included - ever writes into a block another request
+    can read.  ``first_writable_position`` exposes that bound for the runner to check.
+    """
+
+    def __init__(self, num_blocks: int, block_size: int, device: torch.device) -> None:
+        super().__init__(num_blocks, block_size, device)
+        self._blocks = CachingBlockPool(num_blocks)
+        self._num_registered: dict[str, int] = {}
+        self._hit_tokens = 0
+
+    @property
+    def num_prefix_hit_tokens(self) -> int:
+        return self._hit_tokens
+
+    @property
+    def pool(self) -> CachingBlockPool:
+        return self._blocks
+
+    def find_cached_blocks(self, sequence) -> list[int]:
+        """Cached blocks that match the start of ``sequence``; the last token is always
+        left to compute, since its logits are needed (prefix_cache.py:111-120)."""
+        usable = (sequence.num_tokens - 1) // self.block_size
+        found = []
+        for key in build_block_keys(sequence.token_ids, self.block_size, usable):
+            block = self._blocks.find(key)
+            if block is None:
+                break
+            found.append(block)
+        return found
+
+    def can_reserve(self, sequence, num_tokens: int) -> bool:
+        rid = _request_id(sequence)
+        if rid in self._tables or isinstance(sequence, str):
+            return super().can_reserve(rid, num_tokens)
+        cached = self.find_cached_blocks(sequence)
+        revived = sum(1 for b in cached if self._blocks.is_free(b))
+        return math.ceil(num_tokens / self.block_size) - len(cached) <= self._blocks.num_free_blocks - revived
+
+    def reserve(self, sequence, num_tokens: int) -> list[int]:
+        """A new sequence first takes its cached prefix (setting ``num_cached_tokens``),
+        then gets fresh blocks for the rest (prefix_cache.py:130-142).  Returns the
+        freshly allocated blocks; shared ones are in ``block_table``."""
+        rid = _request_id(sequence)
+        if rid not in self._tables and not isinstance(sequence, str):
+            if not self.can_reserve(sequence, num_tokens):
+                raise OutOfKVMemoryError(f"no blocks for {rid}")
+            cached = self.find_cached_blocks(sequence)
+            for block in cached:
+                self._blocks.share(block)
+            self._tables[rid] = list(cached)
+            self._num_registered[rid] = len(cached)
+            sequence.num_cached_tokens = len(cached) * self.block_size
+            self._hit_tokens += sequence.num_cached_tokens
+        return super().reserve(rid, num_tokens)
+
+    def on_tokens_cached(self, sequence) -> None:
+        """Register the blocks that became full since the last call (prefix_cache.py:144-154)."""
+        rid = sequence.request_id
+        table = self._tables.get(rid, [])
+        done = self._num_registered.get(rid, 0)
+        full = min(sequence.num_cached_tokens // self.block_size, len(table), sequence.num_tokens // self.block_size)
+        if full <= done:
+            return
+        keys = build_block_keys(sequence.token_ids, self.block_size, full)
+        for i in range(done, full):
+            self._blocks.register(table[i], keys[i])
+        self._num_registered[rid] = full
+
+    def first_writable_position(self, sequence) -> int:
+        return self._num_registered.get(_request_id(sequence), 0) * self.block_size
+
+    def free(self, sequence) -> None:
+        super().free(sequence)
+        self._num_registered.pop(_request_id(sequence), None)
 
 
 def slots_for_budget(num_layers: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype,

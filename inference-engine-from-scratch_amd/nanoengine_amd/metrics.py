@@ -1,4 +1,5 @@
-"""Speculative-decoding counters (ne/engine/metrics.py:66-75) in a per-engine registry.
+"""Speculative-decoding counters (ne/engine/metrics.py:66-75) and the prefix-cache
+hit gauge (metrics.py:61-65) in a per-engine registry.
 
 Uses prometheus_client when it is importable, with the same metric names; the
 benchmark definitions (ne/benchmarks/speculative.py:104-114) are
@@ -8,10 +9,11 @@ acceptance = accepted / proposed and tokens per target pass = tokens / (tokens -
 from __future__ import annotations
 
 try:
-    from prometheus_client import CollectorRegistry, Counter
+    from prometheus_client import CollectorRegistry, Counter, Gauge
 except ImportError:  # pragma: no cover - the image ships prometheus_client
     CollectorRegistry = None
     Counter = None
+    Gauge = None
 
 
 class _PlainCounter:
@@ -20,6 +22,9 @@ class _PlainCounter:
 
     def inc(self, amount: float = 1.0) -> None:
         self.value += amount
+
+    def set(self, value: float) -> None:
+        self.value = value
 
 
 class EngineMetrics:
@@ -33,10 +38,15 @@ class EngineMetrics:
                 "nanoengine_speculative_accepted_tokens",
                 "Guessed tokens the target model kept; accepted / proposed is the acceptance rate",
                 registry=self.registry)
+            self.prefix_cache_hit_tokens = Gauge(
+                "nanoengine_prefix_cache_hit_tokens",
+                "Prompt tokens taken from the prefix cache instead of computed, since start",
+                registry=self.registry)
         else:
             self.registry = None
             self.speculative_proposed_tokens = _PlainCounter()
             self.speculative_accepted_tokens = _PlainCounter()
+            self.prefix_cache_hit_tokens = _PlainCounter()
 
     def _value(self, counter, name: str) -> float:
         if self.registry is not None:
@@ -50,6 +60,10 @@ class EngineMetrics:
     @property
     def accepted(self) -> float:
         return self._value(self.speculative_accepted_tokens, "nanoengine_speculative_accepted_tokens_total")
+
+    @property
+    def prefix_hit_tokens(self) -> float:
+        return self._value(self.prefix_cache_hit_tokens, "nanoengine_prefix_cache_hit_tokens")
 
 
 def acceptance_rate(proposed: float, accepted: float) -> float:

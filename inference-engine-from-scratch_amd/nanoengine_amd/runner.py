@@ -14,10 +14,17 @@ lengths, block tables and cached counts resident on the device:
      the LM head (argmax partials only when greedy) and the fused acceptance,
      which appends kept tokens + 1 to the device history and rolls
      ``num_cached`` back to L + kept
-  4. read back accepted tokens and update the host ``Sequence`` objects
+  4. read back accepted tokens and update the host ``Sequence`` objects; only
+     then, with the guesses gone and ``num_cached_tokens`` = L + kept, tell the
+     allocator which tokens are cached (a prefix cache registers verified full
+     blocks only)
 
 Step 3 has fixed shapes (every slot owns k+1 padded rows), so it can be
 captured once into a HIP graph and replayed.
+
+With a prefix-caching allocator, a new sequence takes the cached blocks of its
+prompt's start and its prefill computes only the remaining rows (queries at
+positions c..p-1 over a context of p keys).
 """
 
 from __future__ import annotations
@@ -166,21 +173,26 @@ class VerifyRunner:
         n = len(run)
         tokens, positions, slots, q_start, q_len = [], [], [], [], []
         row = 0
+        ctx_len = []
         for slot, seq in run:
             self.slots[slot] = seq
             p = seq.num_tokens
-            added = self.allocator.reserve(seq.request_id, p)
-            table = self.allocator.block_table(seq.request_id)
+            seq.num_cached_tokens = 0
+            self.allocator.reserve(seq, p)  # a prefix cache sets num_cached_tokens to its hit
+            c = seq.num_cached_tokens
+            table = self.allocator.block_table(seq)
             self.h_tables[slot].zero_()
             self.h_tables[slot, : len(table)] = torch.tensor(table, dtype=torch.int32)
-            del added
-            pos = np.arange(p)
-            tokens.append(np.asarray(seq.token_ids, dtype=np.int32))
+            pos = np.arange(c, p)
+            if c < self.allocator.first_writable_position(seq):
+                raise RuntimeError(f"prefill of {seq.request_id} would write into a shared block")
+            tokens.append(np.asarray(seq.token_ids[c:], dtype=np.int32))
             positions.append(pos.astype(np.int32))
-            slots.append(self.allocator.slots_for(seq.request_id, pos).astype(np.int32))
+            slots.append(self.allocator.slots_for(seq, pos).astype(np.int32))
             q_start.append(row)
-            q_len.append(p)
-            row += p
+            q_len.append(p - c)
+            ctx_len.append(p)
+            row += p - c
             self.history[slot, :p] = torch.tensor(seq.token_ids, dtype=torch.int32)
             self.history_len[slot] = p
             self.seeds[slot] = seq.sampling_generator.seed
@@ -192,8 +204,9 @@ class VerifyRunner:
         tok, posn, slot_map = t(tokens), t(positions), t(slots)
         qs = torch.tensor(q_start, dtype=torch.int32, device=dev)
         ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
-        batch = AttentionBatch(posn, slot_map, qs, ql, ql, self.block_tables[s0 : s0 + n], max(q_len),
-                               max(q_len))
+        cl = torch.tensor(ctx_len, dtype=torch.int32, device=dev)
+        batch = AttentionBatch(posn, slot_map, qs, ql, cl, self.block_tables[s0 : s0 + n], max(q_len),
+                               max(ctx_len))
         hidden = self.model.forward(row, tok, batch, self.pool)
         last = hidden.index_select(0, (qs + ql - 1).long())
         greedy = self.temperature == GREEDY_TEMPERATURE
@@ -212,6 +225,7 @@ class VerifyRunner:
         results = {}
         for i, (slot, seq) in enumerate(run):
             seq.num_cached_tokens = seq.num_tokens
+            self.allocator.on_tokens_cached(seq)  # the whole prompt is verified and cached
             seq.sampling_generator.step += 1
             results[slot] = self._emit(slot, seq, [int(self.h_out[s0 + i, 0])], 0, 0)
         return results
@@ -282,8 +296,12 @@ class VerifyRunner:
         for s in active:
             seq = self.slots[s]
             g = int(self.h_num_drafts[s])
-            owned = len(self.allocator.block_table(seq.request_id))
-            added = self.allocator.reserve(seq.request_id, seq.num_tokens + g)
+            # rows write positions L-1 .. L-1+g; every block below the allocator's
+            # bound may be read by other requests and must never be written
+            if seq.num_tokens - 1 < self.allocator.first_writable_position(seq):
+                raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
+            owned = len(self.allocator.block_table(seq))
+            added = self.allocator.reserve(seq, seq.num_tokens + g)
             if added:
                 self.h_tables[s, owned : owned + len(added)] = torch.tensor(added, dtype=torch.int32)
                 tables_changed = True
@@ -300,7 +318,7 @@ class VerifyRunner:
                     "requested": int(self.h_num_tokens[s]),
                     "drafts": self.drafts[s, : int(self.h_num_drafts[s])].tolist(),
                     "out": self.h_out[s, : int(self.h_num_out[s])].tolist(),
-                    "table": self.allocator.block_table(self.slots[s].request_id),
+                    "table": self.allocator.block_table(self.slots[s]),
                 }
                 for s in active
             })
@@ -310,13 +328,19 @@ class VerifyRunner:
             n = int(self.h_num_out[s])
             g = int(self.h_num_drafts[s])
             kept = n - 1
-            seq.num_cached_tokens = seq.num_tokens + kept
+            cached = seq.num_tokens + kept  # L-1 .. L-1+kept now hold the kept tokens
             seq.sampling_generator.step += 1
-            results[s] = self._emit(s, seq, self.h_out[s, :n].tolist(), g, kept)
+            results[s] = self._emit(s, seq, self.h_out[s, :n].tolist(), g, kept, cached)
         return results
 
-    def _emit(self, slot: int, seq: Sequence, tokens: list[int], g: int, kept: int) -> StepResult:
-        """Append tokens one by one with the finish checks of speculative_generator.py:54-67."""
+    def _emit(self, slot: int, seq: Sequence, tokens: list[int], g: int, kept: int,
+              cached: int | None = None) -> StepResult:
+        """Append tokens one by one with the finish checks of speculative_generator.py:54-67.
+
+        ``cached`` (verify steps) is the number of positions whose keys/values now hold
+        verified tokens; it is recorded, clipped to the tokens actually kept when a stop
+        ends the sequence early, and reported to the allocator before a finished
+        sequence is released, so its verified blocks stay reusable."""
         emitted = []
         reason = None
         for token in tokens:
@@ -326,6 +350,9 @@ class VerifyRunner:
                                         self.stop_token_ids)
             if reason is not None:
                 break
+        if cached is not None:
+            seq.num_cached_tokens = min(cached, seq.num_tokens)
+            self.allocator.on_tokens_cached(seq)
         if reason is not None:
             self.release(slot)
         return StepResult(emitted, reason, g, kept)
@@ -334,7 +361,7 @@ class VerifyRunner:
         seq = self.slots[slot]
         if seq is None:
             return
-        self.allocator.free(seq.request_id)
+        self.allocator.free(seq)
         self.slots[slot] = None
         self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
         self.h_tables[slot].zero_()

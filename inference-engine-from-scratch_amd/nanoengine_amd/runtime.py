@@ -9,7 +9,7 @@ from dataclasses import dataclass
 import torch
 
 from nanoengine_amd.config import TORCH_DTYPES, EngineSettings
-from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator, slots_for_budget
+from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator, PrefixCachingSlotAllocator, slots_for_budget
 from nanoengine_amd.metrics import EngineMetrics
 from nanoengine_amd.qwen3 import Qwen3Config, Qwen3VerifyModel, Qwen3Weights
 from nanoengine_amd.runner import VerifyRunner
@@ -50,7 +50,8 @@ def create_verify_engine(config: Qwen3Config, state_dict: dict[str, torch.Tensor
             f"kv_cache_memory_mb={settings.kv_cache_memory_mb} holds fewer tokens than "
             f"max_model_len={settings.max_model_len}; raise the budget"
         )
-    allocator = PagedSlotAllocator(num_blocks, settings.kv_block_size, device)
+    allocator_type = PrefixCachingSlotAllocator if settings.prefix_cache else PagedSlotAllocator  # runtime.py:93-94
+    allocator = allocator_type(num_blocks, settings.kv_block_size, device)
     pool = KVCachePool(config.num_hidden_layers, config.num_key_value_heads, config.head_dim,
                        num_blocks * settings.kv_block_size, device, dtype, settings.is_int8_kv_cache,
                        settings.kv_block_size)

@@ -138,6 +138,8 @@ class BatchedSpeculativeGenerator:
                 for (req, _), slot in zip(batch, sorted(results), strict=True):
                     slot_request[slot] = req
                 self._record(results, slot_request, events)
+                if self._metrics is not None:  # batch_engine_loop.py:176
+                    self._metrics.prefix_cache_hit_tokens.set(self._runner.allocator.num_prefix_hit_tokens)
                 continue
             results = self._runner.step()
             for result in results.values():

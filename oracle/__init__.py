@@ -12,6 +12,9 @@ numpy, C (``csrc/accept_oracle.c``) or torch on the CPU:
   ngram.py      NgramProposer.propose             ne/engine/speculative/proposers.py:39-57
   paging.py     block / paged / contiguous slot   ne/engine/memory/*.py, batch_builder.py
                 allocators, step inputs, masks
+  prefix_cache.py  hash-chained block keys,       ne/engine/memory/prefix_cache.py:21-158
+                refcounted LRU block pool, prefix
+                caching slot allocator
   quant.py      quantize_vectors, Int8Linear      ne/models/int8_quantization.py:30-73
   attention.py  cached GQA attention              ne/models/attention_context.py:32-109
   model.py      Qwen3 forward, logits, init       ne/models/qwen3.py:13-203

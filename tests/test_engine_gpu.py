@@ -176,3 +176,122 @@ def test_stop_token_ends_a_request_early():
         GenerationRequest("b", prompt, SamplingParams(max_new_tokens=12))))
     assert events[-1].finish_reason == "stop" and events[-1].token_id == stop
     assert len(events) == tokens.index(stop) + 1
+
+
+# ------------------------------------------------------------------ prefix cache
+def prefix_engine(state, num_seqs, graphs=False):
+    settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                              quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                              num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=num_seqs,
+                              max_model_len=256, kv_cache_memory_mb=64, cuda_graphs=graphs,
+                              prefix_cache=True)
+    return create_verify_engine(CFG, state, settings, max_prefill_rows=64 * num_seqs)
+
+
+def shared_prefix_prompts(n, seed):
+    """A 48-token shared start (three 16-token blocks, motif-repeating so drafts are
+    accepted) followed by a distinct suffix per prompt."""
+    g = torch.Generator().manual_seed(seed)
+    motif = torch.randint(0, 512, (16,), generator=g).tolist()
+    prompts = []
+    for i in range(n):
+        suffix = torch.randint(0, 512, (5 + 3 * i,), generator=g).tolist()
+        prompts.append(motif * 3 + suffix + motif[:8])
+    return prompts
+
+
+def pool_bytes(pool, slots):
+    idx = torch.tensor(slots, dtype=torch.long, device=pool.key_caches[0].device)
+    parts = []
+    for i in range(len(pool.key_caches)):
+        for t in (pool.key_caches[i], pool.value_caches[i], pool.key_scales[i], pool.value_scales[i]):
+            parts.append(t.index_select(0, idx).view(torch.uint8).reshape(-1).cpu())
+    return torch.cat(parts)
+
+
+def test_prefix_hit_verify_logits_match_a_full_prefill_on_the_oracle():
+    """Sequences that take 48 cached tokens prefill only their suffix (queries at
+    positions 48..p-1 over p keys); their verify-step logits must equal, to the same
+    bar as without the cache, the oracle's logits after a full prefill."""
+    state = make_state(norm_ones=False)
+    prompts = shared_prefix_prompts(4, seed=11)
+    eng = prefix_engine(state, 4)
+    params = SamplingParams(max_new_tokens=32, temperature=0.8, seed=1, ignore_eos=True)
+    seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts)]
+    eng.runner.add(seqs[:1])  # registers the shared blocks
+    eng.runner.add(seqs[1:])
+    assert eng.allocator.num_prefix_hit_tokens == 3 * 48
+    warm_table = eng.allocator.block_table(seqs[0])
+    for seq in seqs[1:]:
+        assert eng.allocator.block_table(seq)[:3] == warm_table[:3]
+    eng.runner.trace = []
+    eng.runner.step()
+    torch.cuda.synchronize()
+    ours = eng.runner.logits.float().cpu()
+    step = eng.runner.trace[0]
+    ref_model = oracle_model(state, torch.bfloat16)
+    pool = om.KVCachePool(OCFG, 64 * 16, torch.bfloat16, is_int8=True)
+    runner = OracleRunner(ref_model, pool, OraclePaged(64, 16))
+    for slot, rec in step.items():
+        seq = OracleSequence(f"o{slot}", list(prompts[slot]), 64, 32)
+        runner.allocator.reserve(seq.request_id, len(seq.token_ids))
+        runner.run_step([seq])
+        seq.token_ids = list(rec["history"]) + rec["drafts"]
+        runner.allocator.reserve(seq.request_id, len(seq.token_ids))
+        ref = runner.score_tokens(seq, 1 + len(rec["drafts"])).float()
+        got = ours[slot * 5 : slot * 5 + 1 + len(rec["drafts"])]
+        assert float((got - ref).abs().max()) <= 1e-2, f"slot {slot}"
+        rel = float((got - ref).norm() / ref.norm())
+        assert rel <= 2e-2, f"slot {slot}: relative error {rel:.3e}"
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_prefix_cached_speculation_keeps_shared_blocks_and_matches_oracle(graphs):
+    """Greedy speculation over shared prefix blocks: the shared blocks' bytes (keys,
+    values and scales of every layer) never change while the sharers verify, accept
+    and roll back; every emitted token equals the fp32 oracle's argmax where its
+    top-2 margin is clear; later requests reuse blocks that finished requests
+    registered from verified tokens only."""
+    state = make_state(norm_ones=True)
+    prompts = shared_prefix_prompts(5, seed=4)
+    eng = prefix_engine(state, 5, graphs=graphs)
+    params = SamplingParams(max_new_tokens=40, ignore_eos=True)
+    seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts)]
+    emitted = {i: [] for i in range(5)}
+    for slot, res in eng.runner.add(seqs[:1]).items():
+        emitted[slot] += res.tokens
+    shared = eng.allocator.block_table(seqs[0])[:3]
+    slots = [b * 16 + o for b in shared for o in range(16)]
+    before = pool_bytes(eng.pool, slots)
+    for slot, res in eng.runner.add(seqs[1:]).items():
+        emitted[slot] += res.tokens
+    assert eng.allocator.num_prefix_hit_tokens == 4 * 48
+    assert all(eng.allocator.pool.reference_count(b) == 5 for b in shared)
+    while eng.runner.active_slots:
+        for slot, res in eng.runner.step().items():
+            emitted[slot] += res.tokens
+    assert torch.equal(pool_bytes(eng.pool, slots), before), "a shared block was written"
+    ref32 = om.Qwen3ForCausalLM(OCFG)
+    ref32.load_state_dict(state)
+    ref32 = ref32.eval()
+    om.quantize_linear_layers(ref32)
+    checked = 0
+    for i in range(5):
+        toks = emitted[i]
+        assert len(toks) == 40
+        with torch.inference_mode():
+            logits = ref32.compute_logits(ref32(torch.tensor([prompts[i] + toks])))[0]
+        scale = float(logits.abs().max())
+        for j, tok in enumerate(toks):
+            row = logits[len(prompts[i]) - 1 + j]
+            top2 = torch.topk(row, 2)
+            if float(top2.values[0] - top2.values[1]) > 2e-2 * scale:
+                assert tok == int(top2.indices[0]), f"seq {i} token {j}"
+                checked += 1
+    assert checked > 0
+    # a request repeating a finished sequence's verified history reuses its blocks
+    history = prompts[2] + emitted[2]
+    again = Sequence.from_request(GenerationRequest("again", history, SamplingParams(max_new_tokens=2)))
+    hits = eng.allocator.num_prefix_hit_tokens
+    eng.runner.add([again])
+    assert eng.allocator.num_prefix_hit_tokens - hits == ((len(history) - 1) // 16) * 16

@@ -106,8 +106,13 @@ def test_settings_select_the_hip_path_and_keep_the_reference_checks():
                                      speculative="ngram").hip_verify_path_error()
     with pytest.raises(ValueError):  # ne/config.py:91-97: speculation without a KV cache
         EngineSettings(speculative="ngram")
-    with pytest.raises(ValueError):  # speculation with the prefix cache stays refused
-        EngineSettings(kv_cache="paged", prefix_cache=True, speculative="ngram")
+    # prefix-cached speculation is accepted (only verified blocks are registered);
+    # the draft-model path keeps the reference's refusal
+    assert EngineSettings(kv_cache="paged", prefix_cache=True, speculative="ngram").prefix_cache
+    with pytest.raises(ValueError):
+        EngineSettings(kv_cache="paged", prefix_cache=True, speculative="draft")
+    with pytest.raises(ValueError):  # ne/config.py:85-86
+        EngineSettings(kv_cache="contiguous", prefix_cache=True)
     env = {"NANOENGINE_DEVICE": "cuda", "NANOENGINE_KV_CACHE": "paged", "NANOENGINE_CUDA_GRAPHS": "true",
            "NANOENGINE_NUM_SPECULATIVE_TOKENS": "8"}
     s = EngineSettings.from_env(env)
