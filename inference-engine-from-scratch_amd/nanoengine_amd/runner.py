@@ -30,6 +30,7 @@ positions c..p-1 over a context of p keys).
 from __future__ import annotations
 
 import math
+from collections import deque
 from dataclasses import dataclass
 
 import numpy as np
@@ -168,58 +169,45 @@ class VerifyRunner:
         return results
 
     def _prefill(self, run: list[tuple[int, Sequence]]) -> dict[int, StepResult]:
+        """Reserve and prefill a run of consecutive slots, then emit each first token.
+
+        The uncached rows of the run are packed in slot order into forwards of at most
+        ``model.max_rows`` rows; a prompt longer than the room left is cut into chunks
+        (as the reference's chunked prefill does), each chunk's queries attending to
+        every key before them (queries at positions a..e-1 over e keys)."""
         dev = self.device
         s0 = run[0][0]
         n = len(run)
-        tokens, positions, slots, q_start, q_len = [], [], [], [], []
-        row = 0
-        ctx_len = []
+        pending: deque[list] = deque()
         for slot, seq in run:
             self.slots[slot] = seq
             p = seq.num_tokens
             seq.num_cached_tokens = 0
             self.allocator.reserve(seq, p)  # a prefix cache sets num_cached_tokens to its hit
             c = seq.num_cached_tokens
+            if c < self.allocator.first_writable_position(seq):
+                raise RuntimeError(f"prefill of {seq.request_id} would write into a shared block")
             table = self.allocator.block_table(seq)
             self.h_tables[slot].zero_()
             self.h_tables[slot, : len(table)] = torch.tensor(table, dtype=torch.int32)
-            pos = np.arange(c, p)
-            if c < self.allocator.first_writable_position(seq):
-                raise RuntimeError(f"prefill of {seq.request_id} would write into a shared block")
-            tokens.append(np.asarray(seq.token_ids[c:], dtype=np.int32))
-            positions.append(pos.astype(np.int32))
-            slots.append(self.allocator.slots_for(seq, pos).astype(np.int32))
-            q_start.append(row)
-            q_len.append(p - c)
-            ctx_len.append(p)
-            row += p - c
             self.history[slot, :p] = torch.tensor(seq.token_ids, dtype=torch.int32)
             self.history_len[slot] = p
             self.seeds[slot] = seq.sampling_generator.seed
             self.steps[slot] = seq.sampling_generator.step
-        if row > self.model.max_rows:
-            raise ValueError(f"prefill of {row} rows exceeds the model's {self.model.max_rows} rows")
+            pending.append([slot, seq, c, p])
         self.block_tables.copy_(self.h_tables, non_blocking=True)
-        t = lambda a: torch.from_numpy(np.concatenate(a)).to(dev)
-        tok, posn, slot_map = t(tokens), t(positions), t(slots)
-        qs = torch.tensor(q_start, dtype=torch.int32, device=dev)
-        ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
-        cl = torch.tensor(ctx_len, dtype=torch.int32, device=dev)
-        batch = AttentionBatch(posn, slot_map, qs, ql, cl, self.block_tables[s0 : s0 + n], max(q_len),
-                               max(ctx_len))
-        hidden = self.model.forward(row, tok, batch, self.pool)
-        last = hidden.index_select(0, (qs + ql - 1).long())
-        greedy = self.temperature == GREEDY_TEMPERATURE
-        logits, partials = self.model.compute_logits(last, logits=not greedy, argmax=greedy)
-        zeros = torch.zeros(n, dtype=torch.int32, device=dev)
-        kernels.accept(
-            self.drafts[s0 : s0 + n], zeros, torch.arange(n, dtype=torch.int32, device=dev),
-            self.model.config.vocab_size, logits=logits, argmax_partials=partials,
-            temperature=self.temperature, seeds=self.seeds[s0 : s0 + n], steps=self.steps[s0 : s0 + n],
-            out_tokens=self.out_tokens[s0 : s0 + n], num_out=self.num_out[s0 : s0 + n],
-            history=self.history[s0 : s0 + n], history_len=self.history_len[s0 : s0 + n],
-            num_cached=self.num_cached[s0 : s0 + n],
-        )
+        while pending:
+            pieces, room = [], self.model.max_rows
+            while pending and room > 0:
+                slot, seq, a, p = pending[0]
+                e = min(p, a + room)
+                pieces.append((slot, seq, a, e, p))
+                room -= e - a
+                if e < p:
+                    pending[0][2] = e
+                    break
+                pending.popleft()
+            self._prefill_forward(pieces)
         self.h_out[s0 : s0 + n].copy_(self.out_tokens[s0 : s0 + n], non_blocking=True)
         torch.cuda.current_stream(dev).synchronize()
         results = {}
@@ -229,6 +217,46 @@ class VerifyRunner:
             seq.sampling_generator.step += 1
             results[slot] = self._emit(slot, seq, [int(self.h_out[s0 + i, 0])], 0, 0)
         return results
+
+    def _prefill_forward(self, pieces: list[tuple[int, Sequence, int, int, int]]) -> None:
+        """One forward over (slot, seq, a, e, p) pieces of consecutive slots; the pieces
+        that end their prompt (e == p, a leading run of them) get their first token."""
+        dev = self.device
+        tokens, positions, slots, q_start, q_len, ctx_len = [], [], [], [], [], []
+        row = 0
+        for slot, seq, a, e, p in pieces:
+            pos = np.arange(a, e)
+            tokens.append(np.asarray(seq.token_ids[a:e], dtype=np.int32))
+            positions.append(pos.astype(np.int32))
+            slots.append(self.allocator.slots_for(seq, pos).astype(np.int32))
+            q_start.append(row)
+            q_len.append(e - a)
+            ctx_len.append(e)
+            row += e - a
+        t = lambda x: torch.from_numpy(np.concatenate(x)).to(dev)
+        tok, posn, slot_map = t(tokens), t(positions), t(slots)
+        qs = torch.tensor(q_start, dtype=torch.int32, device=dev)
+        ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+        cl = torch.tensor(ctx_len, dtype=torch.int32, device=dev)
+        s0 = pieces[0][0]
+        batch = AttentionBatch(posn, slot_map, qs, ql, cl, self.block_tables[s0 : s0 + len(pieces)], max(q_len),
+                               max(ctx_len))
+        hidden = self.model.forward(row, tok, batch, self.pool)
+        nf = sum(1 for piece in pieces if piece[3] == piece[4])
+        if nf == 0:
+            return
+        last = hidden.index_select(0, (qs[:nf] + ql[:nf] - 1).long())
+        greedy = self.temperature == GREEDY_TEMPERATURE
+        logits, partials = self.model.compute_logits(last, logits=not greedy, argmax=greedy)
+        zeros = torch.zeros(nf, dtype=torch.int32, device=dev)
+        sl = slice(s0, s0 + nf)
+        kernels.accept(
+            self.drafts[sl], zeros, torch.arange(nf, dtype=torch.int32, device=dev),
+            self.model.config.vocab_size, logits=logits, argmax_partials=partials,
+            temperature=self.temperature, seeds=self.seeds[sl], steps=self.steps[sl],
+            out_tokens=self.out_tokens[sl], num_out=self.num_out[sl], history=self.history[sl],
+            history_len=self.history_len[sl], num_cached=self.num_cached[sl],
+        )
 
     # ------------------------------------------------------------- verify step
     def _device_step(self) -> None:

@@ -64,20 +64,24 @@ def oracle_model(state, dtype):
     return model
 
 
-def engine_for(state, num_seqs, kv_int8=True, graphs=False):
+def engine_for(state, num_seqs, kv_int8=True, graphs=False, prefill_rows=None):
     settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
                               quantization="int8", kv_cache_dtype="int8" if kv_int8 else "auto",
                               speculative="ngram", num_speculative_tokens=4, ngram_max_size=3,
                               max_num_seqs=num_seqs, max_model_len=256, kv_cache_memory_mb=64,
                               cuda_graphs=graphs)
-    return create_verify_engine(CFG, state, settings, max_prefill_rows=64 * num_seqs)
+    return create_verify_engine(CFG, state, settings, max_prefill_rows=prefill_rows or 64 * num_seqs)
 
 
-@pytest.mark.parametrize("norm_ones", [False, True])
-def test_verify_step_logits_match_oracle(norm_ones):
+@pytest.mark.parametrize("norm_ones,prefill_rows", [(False, None), (True, None), (False, 24)],
+                         ids=["small-norms", "unit-norms", "chunked-prefill-24-rows"])
+def test_verify_step_logits_match_oracle(norm_ones, prefill_rows):
+    """prefill_rows=24: the 64-token prompts prefill in forwards of at most 24 rows
+    (chunks over 24, 48 and 64 keys, cut across sequence boundaries)."""
     state = make_state(norm_ones)
     prompts = motif_prompts(4)
-    eng = engine_for(state, 4)
+    eng = engine_for(state, 4, prefill_rows=prefill_rows)
+    assert prefill_rows is None or eng.model.max_rows == prefill_rows
     params = SamplingParams(max_new_tokens=32, temperature=0.8, seed=1, ignore_eos=True)
     seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts)]
     eng.runner.add(seqs)
