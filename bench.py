@@ -34,6 +34,10 @@ Also reported on the same line:
                  U{4096..16384}, 9 queries for k = 8), both kernel-only.
   sampled        the same verify step with temperature-0.8 rejection sampling on seeded
                  uniforms (10 timed steps): step time, tok/s, accepted-per-step histogram
+  long_context_verify
+                 the full verify step for 32 sequences sharing a 1024-token prefix
+                 (served from the prefix cache) with U{4096..16384}-token suffixes,
+                 k = 8, greedy (10 timed steps after 2 warm-up steps; prefill untimed)
   gemm           the W8A16 projections (QKV, gate|up with SwiGLU, o and down split-K)
                  and the LM head at the step's 320 rows, kernel-only: 28 calls with
                  distinct weights replayed from a HIP graph (no host launch cost);
@@ -158,6 +162,98 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
         "max_new": max_new,
         "mean_context": sum(sum(c) for c in ctx_per_step) / max(1, sum(len(c) for c in ctx_per_step)),
     }
+
+
+LONG_SEQS = 32
+LONG_PREFIX = 1024
+LONG_K = 8
+LONG_PREFILL_ROWS = 8192
+
+
+def long_prompts(seed: int = 1) -> list[list[int]]:
+    """32 prompts: a shared 1024-token prefix (a seeded 16-token motif repeated) and a
+    suffix of U{4096..16384} tokens (the same length draw as the kernel-only long
+    attention workload) repeating each prompt's own motif; ids in [0, 512)."""
+    import numpy as np
+    import torch
+
+    lengths = np.random.default_rng(seed).integers(4096, 16385, size=LONG_SEQS)
+    g = torch.Generator().manual_seed(seed)
+    prefix = torch.randint(0, 512, (PROMPT_MOTIF,), generator=g).tolist() * (LONG_PREFIX // PROMPT_MOTIF)
+    prompts = []
+    for n in lengths:
+        motif = torch.randint(0, 512, (PROMPT_MOTIF,), generator=g).tolist()
+        prompts.append(prefix + (motif * (int(n) // PROMPT_MOTIF + 1))[: int(n)])
+    return prompts
+
+
+def run_verify_long(args, torch, steps: int = 10, warmup: int = 2):
+    """The full verify step at long context with a shared prefix (k = 8, greedy): the
+    first request prefills and registers the 1024-token prefix; the other 31 take its
+    64 blocks from the prefix cache and prefill only their suffixes (chunks of 8192
+    rows).  Timed like the main leg (HIP graph replay unless --eager)."""
+    from nanoengine_amd.config import EngineSettings
+    from nanoengine_amd.interface import GenerationRequest, SamplingParams
+    from nanoengine_amd.qwen3 import QWEN3_0_6B, random_state_dict
+    from nanoengine_amd.runtime import create_verify_engine
+    from nanoengine_amd.sequence_state import Sequence
+
+    cfg = QWEN3_0_6B
+    prompts = long_prompts()
+    max_new = (LONG_K + 1) * (steps + warmup) + 2
+    max_len = max(len(p) for p in prompts) + max_new + LONG_K + 1
+    tokens_needed = LONG_PREFIX + sum(len(p) - LONG_PREFIX for p in prompts) + LONG_SEQS * (max_new + 2 * 16 + LONG_K)
+    per_token = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * (cfg.head_dim + 2)
+    state = random_state_dict(cfg, seed=0, std=0.02)
+    settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                              quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                              num_speculative_tokens=LONG_K, ngram_max_size=3, max_num_seqs=LONG_SEQS,
+                              max_model_len=max_len, prefix_cache=True, cuda_graphs=args.graph,
+                              kv_cache_memory_mb=int(math.ceil(tokens_needed * per_token / 2**20)) + 64)
+    eng = create_verify_engine(cfg, state, settings, max_prefill_rows=LONG_PREFILL_ROWS)
+    del state
+    params = SamplingParams(max_new_tokens=max_new, seed=0, ignore_eos=True)
+    seqs = [Sequence.from_request(GenerationRequest(f"l{i}", p, params)) for i, p in enumerate(prompts)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.runner.add(seqs[:1])
+    eng.runner.add(seqs[1:])
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"long prefill {prefill_s:.1f}s, prefix hits {eng.allocator.num_prefix_hit_tokens} tokens")
+    for _ in range(warmup):
+        eng.runner.step()
+    torch.cuda.synchronize()
+    ctx = []
+    tokens = 0
+    kept_hist: dict[int, int] = {}
+    start = time.perf_counter()
+    for _ in range(steps):
+        lengths = {i: s.num_tokens for i, s in enumerate(eng.runner.slots) if s is not None}
+        results = eng.runner.step()
+        ctx += [lengths[i] + results[i].num_guesses for i in lengths]
+        for r in results.values():
+            tokens += len(r.tokens)
+            kept_hist[r.num_kept] = kept_hist.get(r.num_kept, 0) + 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    out = {
+        "workload": "full verify step, Qwen3-0.6B architecture, 32 seqs sharing a 1024-token prefix "
+                    "(prefix cache) + U{4096..16384}-token suffixes (seed 1), n-gram k=8, greedy, "
+                    "int8 W + int8 paged KV",
+        "steps": steps, "warmup": warmup,
+        "verify_step_us": round(1e6 * elapsed / steps, 1),
+        "accepted_tok_s": round(tokens / elapsed, 1),
+        "mean_context": round(sum(ctx) / max(len(ctx), 1), 1),
+        "prefix_hit_tokens": eng.allocator.num_prefix_hit_tokens,
+        "prefill_s": round(prefill_s, 2),
+        "active_at_end": sum(1 for s in eng.runner.slots if s is not None),
+        "accepted_per_step_hist": {str(k): v for k, v in sorted(kept_hist.items())},
+        "hip_graph": bool(args.graph),
+    }
+    del eng
+    torch.cuda.empty_cache()
+    return out
 
 
 class AttentionWorkload:
@@ -668,7 +764,8 @@ def main() -> int:
     parser.add_argument("--temperature", type=float, default=0.0)
     parser.add_argument("--eager", dest="graph", action="store_false",
                         help="launch the step's kernels one by one instead of replaying a HIP graph")
-    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline"), default="all")
+    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline", "long"),
+                        default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-torch-baseline", action="store_true")
     parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
@@ -727,12 +824,17 @@ def main() -> int:
                    "accepted_tok_s": round(s_res["tokens"] / s_res["elapsed"], 1),
                    "accepted_per_step_hist": {str(k): v for k, v in sorted(s_res["kept_hist"].items())}}
         log(f"sampled: {sampled['verify_step_us']} us per step")
+    long_verify = None
+    if args.only in ("all", "long"):
+        long_verify = run_verify_long(args, torch)
+        log(f"long-context verify: {long_verify['verify_step_us']} us per step")
     cpu = None
     if args.only == "all" and not args.no_cpu_baseline:
         cpu = run_cpu_baseline(torch)
         log(f"cpu baseline: {cpu['value']} tok/s")
     if res is None:
-        print(json.dumps({"attention": attention, "gemm": gemm, "torch_baseline": torch_base}), flush=True)
+        print(json.dumps({"attention": attention, "gemm": gemm, "torch_baseline": torch_base,
+                          "long_context_verify": long_verify}), flush=True)
         return 0
     value = res["tokens"] / res["elapsed"]
     step_us = 1e6 * res["elapsed"] / args.steps
@@ -764,6 +866,7 @@ def main() -> int:
         "roofline": attention,
         "gemm": gemm,
         "sampled": sampled,
+        "long_context_verify": long_verify,
         "torch_baseline": torch_base,
         "cpu_baseline": cpu,
     }
