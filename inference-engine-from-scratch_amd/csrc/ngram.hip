@@ -2,11 +2,13 @@
 //
 // Restates NgramProposer.propose (ne/engine/speculative/proposers.py:44-57) for a
 // batch: one 256-thread work-group per sequence.  For n = max_ngram..min_ngram
-// (skipping n >= len) the work-group tests every start position in parallel
-// and keeps the largest start whose window equals the last n tokens -- the
-// reference scans starts from len-n-1 downward and returns the first match,
-// which is the same window.  The guesses are the tokens that followed it,
-// clipped to the history, so they are never empty.
+// (skipping n >= len) the work-group tests start positions from len-n-1 downward,
+// 1024 at a time (4 per thread), and stops after the first chunk holding a start
+// whose window equals the last n tokens, keeping the largest such start -- the
+// reference scans starts from len-n-1 downward and returns the first match, which
+// is the same window.  A recent match (the common case in long histories) costs one
+// chunk instead of a scan of the whole history.  The guesses are the tokens that
+// followed it, clipped to the history, so they are never empty.
 #include "ne_common.hpp"
 
 namespace ne {
@@ -14,6 +16,8 @@ namespace ne {
 namespace {
 
 constexpr int kMaxNgram = 16;
+constexpr int kScanPerThread = 4;
+constexpr int kScanChunk = 256 * kScanPerThread;
 
 __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int64_t stride,
                                                     const int32_t* history_len,
@@ -35,22 +39,31 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
     int suffix[kMaxNgram];
 #pragma unroll
     for (int i = 0; i < kMaxNgram; ++i) suffix[i] = (i < n) ? h[len - n + i] : 0;
-    int best = -1;
-    for (int start = tid; start <= len - n - 1; start += 256) {
-      bool eq = true;
+    int top = -1;
+    for (int hi = len - n - 1; hi >= 0 && top < 0; hi -= kScanChunk) {
+      // thread tid tests starts hi - tid, hi - tid - 256, ...: its first hit is its
+      // largest, and the owner of the chunk's largest hit has no larger one
+      int best = -1;
 #pragma unroll
-      for (int i = 0; i < kMaxNgram; ++i)
-        if (i < n) eq = eq && (h[start + i] == suffix[i]);
-      if (eq) best = start;  // starts grow with the loop, so the last hit is the largest
+      for (int j = 0; j < kScanPerThread; ++j) {
+        const int start = hi - j * 256 - tid;
+        if (start >= 0 && best < 0) {
+          bool eq = true;
+#pragma unroll
+          for (int i = 0; i < kMaxNgram; ++i)
+            if (i < n) eq = eq && (h[start + i] == suffix[i]);
+          if (eq) best = start;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) best = max(best, __shfl_xor(best, o));
+      if (tid % kWave == 0) s_best[tid / kWave] = best;
+      __syncthreads();
+      top = s_best[0];
+#pragma unroll
+      for (int w = 1; w < 256 / kWave; ++w) top = max(top, s_best[w]);
+      __syncthreads();
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) best = max(best, __shfl_xor(best, o));
-    if (tid % kWave == 0) s_best[tid / kWave] = best;
-    __syncthreads();
-    int top = s_best[0];
-#pragma unroll
-    for (int w = 1; w < 256 / kWave; ++w) top = max(top, s_best[w]);
-    __syncthreads();
     if (top >= 0) {
       const int follow = top + n;
       const int count = min(want, len - follow);

@@ -128,6 +128,9 @@ class PagedSlotAllocator:
     def block_table(self, sequence) -> list[int]:
         return list(self._tables.get(_request_id(sequence), []))
 
+    def num_blocks_of(self, sequence) -> int:
+        return len(self._tables.get(_request_id(sequence), ()))
+
     def count_missing_blocks(self, sequence, num_tokens: int) -> int:
         owned = len(self._tables.get(_request_id(sequence), []))
         return max(0, math.ceil(num_tokens / self.block_size) - owned)
@@ -174,16 +177,18 @@ class PagedSlotAllocator:
 ROOT_PARENT_HASH = 0
 
 
-def build_block_keys(token_ids, block_size: int, num_blocks: int) -> list[tuple[int, tuple[int, ...]]]:
-    """Keys of the first ``num_blocks`` full blocks (prefix_cache.py:25-34).
+def build_block_keys(token_ids, block_size: int, num_blocks: int, first: int = 0,
+                     parent: int = ROOT_PARENT_HASH) -> list[tuple[int, tuple[int, ...]]]:
+    """Keys of full blocks ``first`` .. ``num_blocks``-1 (prefix_cache.py:25-34).
 
     A key is (hash of the previous block's key, this block's tokens), so equal keys
-    mean equal whole prefixes, not only equal 16-token windows.  Python's hash of a
-    tuple of ints is deterministic, so keys agree across processes and with the
-    reference's."""
+    mean equal whole prefixes, not only equal 16-token windows.  ``parent`` is the
+    hash of block ``first``-1's key (the root value for ``first`` 0), so a caller
+    that remembers it extends a chain without rehashing the blocks before.  Python's
+    hash of a tuple of ints is deterministic, so keys agree across processes and
+    with the reference's."""
     keys = []
-    parent = ROOT_PARENT_HASH
-    for start in range(0, num_blocks * block_size, block_size):
+    for start in range(first * block_size, num_blocks * block_size, block_size):
         key = (parent, tuple(token_ids[start:start + block_size]))
         keys.append(key)
         parent = hash(key)
@@ -279,6 +284,9 @@ class PrefixCachingSlotAllocator(PagedSlotAllocator):
         super().__init__(num_blocks, block_size, device)
         self._blocks = CachingBlockPool(num_blocks)
         self._num_registered: dict[str, int] = {}
+        # hash of the last registered block's key per request: verified tokens never
+        # change, so registration extends the chain instead of rehashing a long history
+        self._chain: dict[str, int] = {}
         self._hit_tokens = 0
 
     @property
@@ -292,14 +300,18 @@ class PrefixCachingSlotAllocator(PagedSlotAllocator):
     def find_cached_blocks(self, sequence) -> list[int]:
         """Cached blocks that match the start of ``sequence``; the last token is always
         left to compute, since its logits are needed (prefix_cache.py:111-120)."""
+        return self._find_cached(sequence)[0]
+
+    def _find_cached(self, sequence) -> tuple[list[int], int]:
         usable = (sequence.num_tokens - 1) // self.block_size
-        found = []
+        found, parent = [], ROOT_PARENT_HASH
         for key in build_block_keys(sequence.token_ids, self.block_size, usable):
             block = self._blocks.find(key)
             if block is None:
                 break
             found.append(block)
-        return found
+            parent = hash(key)
+        return found, parent
 
     def can_reserve(self, sequence, num_tokens: int) -> bool:
         rid = _request_id(sequence)
@@ -317,11 +329,12 @@ class PrefixCachingSlotAllocator(PagedSlotAllocator):
         if rid not in self._tables and not isinstance(sequence, str):
             if not self.can_reserve(sequence, num_tokens):
                 raise OutOfKVMemoryError(f"no blocks for {rid}")
-            cached = self.find_cached_blocks(sequence)
+            cached, parent = self._find_cached(sequence)
             for block in cached:
                 self._blocks.share(block)
             self._tables[rid] = list(cached)
             self._num_registered[rid] = len(cached)
+            self._chain[rid] = parent
             sequence.num_cached_tokens = len(cached) * self.block_size
             self._hit_tokens += sequence.num_cached_tokens
         return super().reserve(rid, num_tokens)
@@ -334,10 +347,12 @@ class PrefixCachingSlotAllocator(PagedSlotAllocator):
         full = min(sequence.num_cached_tokens // self.block_size, len(table), sequence.num_tokens // self.block_size)
         if full <= done:
             return
-        keys = build_block_keys(sequence.token_ids, self.block_size, full)
-        for i in range(done, full):
-            self._blocks.register(table[i], keys[i])
+        keys = build_block_keys(sequence.token_ids, self.block_size, full, done,
+                                self._chain.get(rid, ROOT_PARENT_HASH))
+        for i, key in enumerate(keys, start=done):
+            self._blocks.register(table[i], key)
         self._num_registered[rid] = full
+        self._chain[rid] = hash(keys[-1])
 
     def first_writable_position(self, sequence) -> int:
         return self._num_registered.get(_request_id(sequence), 0) * self.block_size
@@ -345,6 +360,7 @@ class PrefixCachingSlotAllocator(PagedSlotAllocator):
     def free(self, sequence) -> None:
         super().free(sequence)
         self._num_registered.pop(_request_id(sequence), None)
+        self._chain.pop(_request_id(sequence), None)
 
 
 def slots_for_budget(num_layers: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype,

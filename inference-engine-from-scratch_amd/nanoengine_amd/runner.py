@@ -328,7 +328,7 @@ class VerifyRunner:
             # bound may be read by other requests and must never be written
             if seq.num_tokens - 1 < self.allocator.first_writable_position(seq):
                 raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
-            owned = len(self.allocator.block_table(seq))
+            owned = self.allocator.num_blocks_of(seq)
             added = self.allocator.reserve(seq, seq.num_tokens + g)
             if added:
                 self.h_tables[s, owned : owned + len(added)] = torch.tensor(added, dtype=torch.int32)

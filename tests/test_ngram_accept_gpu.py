@@ -61,6 +61,26 @@ def test_ngram_long_history_k8(device):
     assert got == want
 
 
+def test_ngram_match_found_deep_in_the_history(device):
+    """Distinct tokens with one planted earlier occurrence of the last n tokens, at
+    depths on both sides of the kernel's 1024-start chunk edges, at start 0, only for
+    n = 2 or n = 1, twice (the later copy wins) or nowhere."""
+    L = 5000
+    base = list(range(10000, 10000 + L))
+    cases = []
+    for p in (0, 1, L - 1030, L - 1027, L - 1026, L - 1025, L - 2051, L - 2050, L - 8, 2500):
+        cases.append(base + base[p:p + 3])  # last trigram occurs at start p
+    cases.append(base + [base[2000], base[2001], 7])  # only the last token (7) is new: no match
+    cases.append(base + [3, base[1200], base[1201]])  # n = 2 only, deep
+    cases.append(base + [3, 4, base[40]])  # n = 1 only, near the start
+    cases.append(base[:3000] + [5, 6, 9] + base[3000:] + [5, 6, 9])  # one copy, mid-history
+    cases.append([5, 6, 9] + base + [5, 6, 9] + base[:100] + [5, 6, 9])  # two copies: the later wins
+    got = run_ngram(device, cases, [8] * len(cases), max_drafts=8)
+    want = [oracle_ngram.propose(h, 8, 3) for h in cases]
+    assert got == want
+    assert all(w for w in want[:10]) and want[10] == []
+
+
 def bf16_logits(rows, vocab, rng, scale=1.0):
     return torch.tensor(rng.standard_normal((rows, vocab)) * scale, dtype=torch.float32).to(torch.bfloat16)
 

@@ -95,6 +95,14 @@ def test_block_keys_include_the_whole_prefix(impl):
     assert impl.keys([1, 2, 3], BLOCK, 0) == []
 
 
+def test_extending_a_key_chain_equals_rebuilding_it():
+    toks = list(range(100, 161))
+    full = op.build_block_keys(toks, BLOCK, 15)
+    for first in (0, 1, 7, 14, 15):
+        parent = hash(full[first - 1]) if first else 0
+        assert pm.build_block_keys(toks, BLOCK, 15, first, parent) == full[first:]
+
+
 @pytest.mark.parametrize("impl", IMPLS, ids=lambda i: i.name)
 def test_pool_reuses_empty_blocks_first_then_evicts_the_oldest_cached(impl):
     """test_prefix_and_chunked_prefill.py:55-76."""
