@@ -730,14 +730,18 @@ constexpr int kPartRows = kRows * kMaxRowTiles;      // rows per (work-group, KV
 constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4 + kHeadWaves * kWave * 4 +
                         kPlanInts * 4;
 constexpr int kPlanMaxSeqs = 2 * kHeadWaves * kWave;  // two sequences per thread
-constexpr int kPlanMinTiles = 16;                     // no split shorter than 256 keys
+constexpr int kPlanMinTiles = 16;                     // contexts up to 256 keys are never split
+constexpr int kPlanFloorTiles = 4;                    // no split shorter than 64 keys
 constexpr int kPlanCUs = 256;                         // work-groups the plan aims to fill
 
 // Work plan of the DMA kernel.  Sequence b has tiles_b = ceil(ctx_b / 16) 16-key
 // tiles and gets n_b = ceil(tiles_b / W) splits of near-equal length (split s
 // covers tiles [tiles_b s / n_b, tiles_b (s+1) / n_b)).  W is p.plan_w when the
-// caller fixed the split length, else max(16, ceil(T / (G - B))) for T = sum_b
-// tiles_b, G = p.plan_grid work-groups and B sequences, which keeps sum_b n_b <= G:
+// caller fixed the split length; else 16 when every context fits in 16 tiles (one
+// split per sequence, so no partials and no merge kernel); else
+// max(4, ceil(T / (G - B))) for T = sum_b tiles_b, G = p.plan_grid work-groups and
+// B sequences -- splitting is paid for already, so W only balances the longest
+// split against the mean.  Both keep sum_b n_b <= G:
 // the longest sequence is spread over as many work-groups as its share of T asks
 // for instead of one per fixed-length split, and no CU waits for a second round
 // of work-groups.  Work-group w serves split w - N_b of the sequence with
@@ -790,7 +794,10 @@ __device__ PlanScan plan_scan(const AttnParams& p, int* s_plan) {
   for (int w = 0; w < kHeadWaves; ++w) T += s_plan[w];
   const int G = p.plan_grid;
   int W = p.plan_w;
-  if (W <= 0) W = max(kPlanMinTiles, (T + (G - B) - 1) / (G - B));
+  if (W <= 0)
+    W = (p.max_ctx + kTileKeys - 1) / kTileKeys <= kPlanMinTiles
+            ? kPlanMinTiles
+            : max(kPlanFloorTiles, (T + (G - B) - 1) / (G - B));
   if (W > kPlanMaxTiles) {
     if (tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
     W = kPlanMaxTiles;
