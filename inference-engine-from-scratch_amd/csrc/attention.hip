@@ -913,6 +913,10 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
   }
 }
 
+// int32 read through the scalar cache: loads of a wave-uniform address in the constant
+// address space compile to s_load (data written by an earlier kernel only)
+using ConstI32 = __attribute__((address_space(4))) const int32_t;
+
 __device__ __forceinline__ void lds_dma(const void* src, void* lds, int bytes) {
   if (bytes == 16) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -997,12 +1001,17 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   const int head = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   PlanItem item;
+  int32_t planned_slot = 0;
   if constexpr (PLANNED) {
-    // the split's slots (entries past its tiles are never read) and its work item,
-    // requested together
-    for (int t = tid; t < kPlanMaxTiles; t += kHeadWaves * kWave)
-      s_slot[t] = p.plan_slots[(int64_t)blockIdx.x * kPlanMaxTiles + t];
-    const int32_t* d = p.plan_desc + (int64_t)blockIdx.x * kDescInts;
+    // The split's slot list (one dword per thread; entries past its tiles are never
+    // read) and the work item (through the scalar cache) are requested together, and
+    // the slot is stored to LDS only after the Q loads are issued, so that a single
+    // round trip precedes the first K/V copy.  The compiler barriers keep the load
+    // first and the store last.
+    static_assert(kPlanMaxTiles == kHeadWaves * kWave, "one slot per thread");
+    const int32_t my_slot = p.plan_slots[(int64_t)blockIdx.x * kPlanMaxTiles + tid];
+    __asm__ __volatile__("" ::: "memory");
+    const ConstI32* d = (const ConstI32*)(p.plan_desc + (int64_t)blockIdx.x * kDescInts);
     item.seq = d[0];
     item.split = d[1];
     item.n_splits = d[2];
@@ -1010,7 +1019,6 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     item.ctx = d[4];
     item.ql = d[5];
     item.qs = d[6];
-    if (item.seq < 0) return;
     // a work item that this metadata cannot have produced (no plan, or a stale one) is
     // flagged and skipped rather than followed
     const int max_tiles = (p.max_ctx + kTileKeys - 1) / kTileKeys;
@@ -1019,10 +1027,11 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
                       item.tiles <= max_tiles && item.ctx > 0 && item.ctx <= p.max_ctx &&
                       item.ql > 0 && item.qs >= 0 &&
                       (item.tiles + item.n_splits - 1) / item.n_splits <= kPlanMaxTiles;
-    if (!sane) {
-      if (tid == 0) atomicOr(p.error_flag, 2u);
+    if (item.seq < 0 || !sane) {
+      if (item.seq >= 0 && tid == 0) atomicOr(p.error_flag, 2u);
       return;
     }
+    planned_slot = my_slot;
   } else {
     if (!plan_item(p, s_plan, item)) return;
   }
@@ -1080,6 +1089,9 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
       const int key0 = kstart + kTileKeys * t;
       s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
     }
+  } else {
+    __asm__ __volatile__("" ::: "memory");
+    s_slot[tid] = planned_slot;  // waits for the slot load alone: the Q loads are younger
   }
   __syncthreads();  // s_slot ready
 
@@ -1183,10 +1195,11 @@ constexpr int kMergeBatch = 8;
 __global__ __launch_bounds__(kPartRows * 16) void attention_plan_merge_kernel(AttnParams p) {
   const int seq = blockIdx.x / kHeadWaves;
   const int head = blockIdx.x % kHeadWaves;
-  const int first = p.plan[seq];
-  const int last = min(p.plan[seq + 1], p.plan_grid);
-  const int ql = p.q_len[seq];
-  const int qs = p.q_start[seq];
+  // the sequence's plan entries and rows through the scalar cache (written by earlier kernels)
+  const int first = ((const ConstI32*)p.plan)[seq];
+  const int last = min(((const ConstI32*)p.plan)[seq + 1], p.plan_grid);
+  const int ql = ((const ConstI32*)p.q_len)[seq];
+  const int qs = ((const ConstI32*)p.q_start)[seq];
   const int n_splits = last - first;
   if (n_splits <= 1) return;
   const int crow = threadIdx.x >> 4;
