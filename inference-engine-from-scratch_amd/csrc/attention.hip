@@ -749,7 +749,14 @@ constexpr int kPlanCUs = 256;                         // work-groups the plan ai
 // the same plan from ctx_len; work-group 0 also stores N (and N_B) for the merge.
 struct PlanItem {
   int seq, split, n_splits, tiles, ctx, ql, qs;
+  int j0, j1;  // the split's tiles [j0, j1) (precomputed plan only)
 };
+
+// R / d for 0 <= R < 64 and 1 <= d <= 64 without an integer division: (R + 0.5) / d
+// lies at least 0.5 / d from an integer, far beyond the float reciprocal's error.
+__device__ __forceinline__ int small_div(int R, int d) {
+  return (int)(((float)R + 0.5f) * __builtin_amdgcn_rcpf((float)d));
+}
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -894,11 +901,11 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
     d[0] = b;
     d[1] = s;
     d[2] = n;
-    d[3] = tiles;
+    d[3] = (int)((int64_t)tiles * s / n);  // the split's tiles [d[3], d[7])
     d[4] = s_seq[3];
     d[5] = s_seq[4];
     d[6] = s_seq[5];
-    d[7] = 0;
+    d[7] = (int)((int64_t)tiles * (s + 1) / n);
   }
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   for (int j = tid; j < tiles; j += kHeadWaves * kWave) {
@@ -1015,18 +1022,17 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     item.seq = d[0];
     item.split = d[1];
     item.n_splits = d[2];
-    item.tiles = d[3];
+    item.j0 = d[3];
     item.ctx = d[4];
     item.ql = d[5];
     item.qs = d[6];
+    item.j1 = d[7];
     // a work item that this metadata cannot have produced (no plan, or a stale one) is
     // flagged and skipped rather than followed
-    const int max_tiles = (p.max_ctx + kTileKeys - 1) / kTileKeys;
     const bool sane = item.seq < p.num_seqs && item.n_splits >= 1 && item.split >= 0 &&
-                      item.split < item.n_splits && item.tiles >= item.n_splits &&
-                      item.tiles <= max_tiles && item.ctx > 0 && item.ctx <= p.max_ctx &&
-                      item.ql > 0 && item.qs >= 0 &&
-                      (item.tiles + item.n_splits - 1) / item.n_splits <= kPlanMaxTiles;
+                      item.split < item.n_splits && item.ctx > 0 && item.ctx <= p.max_ctx &&
+                      item.j0 >= 0 && item.j0 < item.j1 && item.j1 - item.j0 <= kPlanMaxTiles &&
+                      (item.j1 - 1) * kTileKeys < item.ctx && item.ql > 0 && item.qs >= 0;
     if (item.seq < 0 || !sane) {
       if (item.seq >= 0 && tid == 0) atomicOr(p.error_flag, 2u);
       return;
@@ -1040,14 +1046,20 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   item.seq = __builtin_amdgcn_readfirstlane(item.seq);
   item.split = __builtin_amdgcn_readfirstlane(item.split);
   item.n_splits = __builtin_amdgcn_readfirstlane(item.n_splits);
-  item.tiles = __builtin_amdgcn_readfirstlane(item.tiles);
   item.ctx = __builtin_amdgcn_readfirstlane(item.ctx);
   item.ql = __builtin_amdgcn_readfirstlane(item.ql);
   item.qs = __builtin_amdgcn_readfirstlane(item.qs);
   const int seq = item.seq;
   const int n_splits = item.n_splits;
-  const int j0 = (int)((int64_t)item.tiles * item.split / n_splits);
-  const int j1 = (int)((int64_t)item.tiles * (item.split + 1) / n_splits);
+  int j0, j1;
+  if constexpr (PLANNED) {
+    j0 = item.j0;
+    j1 = item.j1;
+  } else {
+    item.tiles = __builtin_amdgcn_readfirstlane(item.tiles);
+    j0 = (int)((int64_t)item.tiles * item.split / n_splits);
+    j1 = (int)((int64_t)item.tiles * (item.split + 1) / n_splits);
+  }
   const int kstart = j0 * kTileKeys;
   const int kend = min(item.ctx, j1 * kTileKeys);
   const int n_tiles = j1 - j0;
@@ -1064,8 +1076,9 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   for (int mt = 0; mt < MT; ++mt) {
     const int R = mt * kRows + r;
     row_valid[mt] = R < rows_total;
-    h_local[mt] = row_valid[mt] ? R / ql : 0;
-    qi[mt] = row_valid[mt] ? R % ql : 0;
+    const int hq = small_div(R, ql);  // R < 32
+    h_local[mt] = row_valid[mt] ? hq : 0;
+    qi[mt] = row_valid[mt] ? R - hq * ql : 0;
     kend_row[mt] = row_valid[mt] ? min(kend, item.ctx - ql + qi[mt] + 1) : kend;
   }
 
