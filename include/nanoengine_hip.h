@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 3
+#define NE_ABI_VERSION 4
 
 /* status codes */
 #define NE_OK 0
@@ -234,6 +234,26 @@ int ne_qk_norm_rope_kv_write(const void* qkv, int32_t rows, int32_t num_q_heads,
                              const int32_t* slot_mapping, void* k_cache, void* v_cache,
                              void* k_scale, void* v_scale, int32_t kv_dtype, int32_t scale_dtype,
                              void* q_out, void* stream);
+
+/*
+ * A8 + A7 fused for the QKV projection: the W8A16 product of ne_w8a16_gemm (store
+ * epilogue) over the concatenated q | k | v weight ([(Hq+2*Hkv)*128, k] int8,
+ * per-row scales), each 128-wide head of every row then taken exactly as
+ * ne_qk_norm_rope_kv_write takes it (the same bits), without writing the qkv
+ * product to memory.  Replaces Int8Linear.forward of q_proj/k_proj/v_proj
+ * (ne/models/int8_quantization.py:55-57, ne/models/qwen3.py:95-98) followed by
+ * qwen3.py:100-104 and write_to_cache (ne/models/attention_context.py:42-54).
+ * kv_dtype NE_DTYPE_INT8 (scales bf16 or fp16) or NE_DTYPE_BF16; k % 128 == 0;
+ * x and w 16-byte aligned.
+ */
+int ne_w8a16_qkv_norm_rope_kv(const void* x, int64_t ldx, const int8_t* w, const void* scale,
+                              int32_t scale_dtype, int32_t m, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t k, const void* q_norm_weight,
+                              const void* k_norm_weight, float eps, const int32_t* positions,
+                              const void* rope_cos_sin, int32_t rope_positions,
+                              const int32_t* slot_mapping, int32_t kv_dtype, void* k_cache,
+                              void* v_cache, void* k_scale, void* v_scale, int32_t kv_scale_dtype,
+                              void* q_out, void* stream);
 
 /*
  * A9/A10 - fused acceptance (replaces verify_proposal and the sampling helpers,

@@ -920,10 +920,6 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
   }
 }
 
-// int32 read through the scalar cache: loads of a wave-uniform address in the constant
-// address space compile to s_load (data written by an earlier kernel only)
-using ConstI32 = __attribute__((address_space(4))) const int32_t;
-
 __device__ __forceinline__ void lds_dma(const void* src, void* lds, int bytes) {
   if (bytes == 16) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);

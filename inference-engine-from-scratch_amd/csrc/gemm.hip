@@ -18,6 +18,7 @@
 // to keep that traffic per CU near its minimum for 256 independent tiles, and the
 // LM head keeps all 320 rows resident per work-group to read X once per 256 columns.
 #include "ne_common.hpp"
+#include "qk_rope_kv.hpp"
 
 namespace ne {
 
@@ -98,35 +99,35 @@ __device__ __forceinline__ void wait_vmcnt() {
 // subtiles 2 nw and 2 nw + 1, so each X fragment read from LDS feeds 2 MFMAs and
 // each weight fragment 5.  The k-groups' partial tiles are summed through LDS at
 // the end, each wave finishing some of the token subtiles.
-constexpr int kPM = 5;  // token subtiles per work-group
-constexpr int kPRows = kPM * 16;
+constexpr int kPM = 5;  // token subtiles per work-group (the fused QKV epilogue uses 3)
 constexpr int kKGroups = 4;
 constexpr int kProjStages = 3;
 constexpr int kDmaPerWave = 4;  // DMA instructions per issuing wave per stage
 
-template <int NSUB>
+template <int NSUB, int PM = kPM>
 struct ProjLayout {
+  static constexpr int kPRows = PM * 16;
   static constexpr int kNW = NSUB / 2;
   static constexpr int kWaves = kKGroups * kNW;
   static constexpr int kThreads = kWaves * kWave;
-  static constexpr int kXBytes = kPRows * kStageK * 2;  // 20 KiB
+  static constexpr int kXBytes = kPRows * kStageK * 2;  // 20 KiB at 5 subtiles
   static constexpr int kWBytes = NSUB * 16 * kStageK;   // int8 rows of 128 bytes
   static constexpr int kStage = kXBytes + kWBytes;
   static constexpr int kXInstr = kXBytes / 1024;
   static constexpr int kInstr = kXInstr + kWBytes / 1024;
   static constexpr int kIssuers = kInstr / kDmaPerWave;
   static_assert(kInstr % kDmaPerWave == 0 && kIssuers <= kWaves, "DMA split");
-  static constexpr int kRedBytes = kKGroups * kNW * kPM * 2 * 1024;
+  static constexpr int kRedBytes = kKGroups * kNW * PM * 2 * 1024;
   static constexpr int kLds = kProjStages * kStage > kRedBytes ? kProjStages * kStage : kRedBytes;
 };
 
 // Copy one 128-wide k stage: X rows m0..m0+79 (rows past m re-read row m-1 and are
 // never stored) and weight rows n0..n0+16*NSUB-1.  Issuing waves copy exactly
 // kDmaPerWave KiB each, so every wave's vmcnt bookkeeping is the same.
-template <int NSUB>
+template <int NSUB, int PM>
 __device__ __forceinline__ void proj_issue(const GemmParams& p, char* stage, int m0, int n0, int k0,
                                            int wave, int lane) {
-  using L = ProjLayout<NSUB>;
+  using L = ProjLayout<NSUB, PM>;
   if (wave >= L::kIssuers) return;
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
@@ -149,10 +150,10 @@ __device__ __forceinline__ void proj_issue(const GemmParams& p, char* stage, int
 // k-step kg of a stage.  Lane group g = lane / 16 supplies logical
 // k = 64 (kg / 2) + 16 g + 8 (kg % 2) + e, e < 8: X chunk 8 (kg / 2) + 2 g + kg % 2 of
 // its 256-byte row, weight bytes 16 (4 (kg / 2) + g) + 8 (kg % 2) of its 128-byte row.
-template <int NSUB>
+template <int NSUB, int PM>
 __device__ __forceinline__ void proj_mma(const char* stage, int kg, int nw, int lane,
-                                         floatx4 (&acc)[kPM][2]) {
-  using L = ProjLayout<NSUB>;
+                                         floatx4 (&acc)[PM][2]) {
+  using L = ProjLayout<NSUB, PM>;
   const int r = lane & 15;
   const int g = lane >> 4;
   const char* xs = stage;
@@ -166,7 +167,7 @@ __device__ __forceinline__ void proj_mma(const char* stage, int kg, int nw, int 
     a[ns] = int8x8_to_bf16x8(v[0], v[1]);
   }
 #pragma unroll
-  for (int mi = 0; mi < kPM; ++mi) {
+  for (int mi = 0; mi < PM; ++mi) {
     const int row = mi * 16 + r;
     const int chunk = (8 * (kg >> 1) + 2 * g + (kg & 1)) ^ (row & 15);
     const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(xs + row * 256 + chunk * 16));
@@ -177,12 +178,18 @@ __device__ __forceinline__ void proj_mma(const char* stage, int kg, int nw, int 
 }
 
 // EPI 0: y = bf16(acc * scale); 1: SwiGLU of paired gate/up subtiles; 3: fp32 partial
-// sums of K split blockIdx.y, scaled, into partial[split][m][n].
-template <int NSUB, int SDT, int EPI>
-__global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmParams p,
+// sums of K split blockIdx.y, scaled, into partial[split][m][n]; 4: the QKV projection
+// with one 128-column head per tile (NSUB 8), each head vector of the bf16 result taken
+// through QK-norm + RoPE into q_out or quantised into the KV cache (qk_rope_kv.hpp) --
+// the bits the GEMM with EPI 0 followed by the row kernel produce, without the qkv round
+// trip through memory.  KV (EPI 4): 1 bf16 cache, 2 int8 + bf16 scales, 3 int8 + fp16.
+template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM>
+__global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(GemmParams p,
                                                                          int k_per_split,
-                                                                         float* partial) {
-  using L = ProjLayout<NSUB>;
+                                                                         float* partial,
+                                                                         QkvRopeArgs qa) {
+  using L = ProjLayout<NSUB, PM>;
+  constexpr int kPRows = L::kPRows;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
@@ -209,16 +216,35 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[ns][i] = scale_at<SDT>(p.scale, n0 + (2 * nw + ns) * 16 + 4 * g + i);
 
-  floatx4 acc[kPM][2];
+  // EPI 4: wave w finishes rows w, w + kWaves, ... of the tile (head tn).  Their slots
+  // and positions (scalar loads) and the head's norm weights are requested now and
+  // used only in the epilogue, so no wait for them precedes the k loop; the RoPE
+  // values, which need the positions, are requested right after the k loop.
+  constexpr int kEpiRows = (kPRows + L::kWaves - 1) / L::kWaves;
+  int e_slot[kEpiRows], e_pos[kEpiRows];
+  uint16_t e_w[2] = {0, 0};
+  if constexpr (EPI == 4) {
+    const uint16_t* w = (tn < qa.hq) ? qa.q_norm_w : qa.k_norm_w;  // v heads do not use it
+    e_w[0] = w[lane];
+    e_w[1] = w[lane + 64];
 #pragma unroll
-  for (int mi = 0; mi < kPM; ++mi)
+    for (int i = 0; i < kEpiRows; ++i) {
+      const int m = min(m0 + wave + L::kWaves * i, p.m - 1);
+      e_slot[i] = ((const ConstI32*)qa.slot_mapping)[m];
+      e_pos[i] = ((const ConstI32*)qa.positions)[m];
+    }
+  }
+
+  floatx4 acc[PM][2];
+#pragma unroll
+  for (int mi = 0; mi < PM; ++mi)
 #pragma unroll
     for (int ns = 0; ns < 2; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int kt_n = k_per_split / kStageK;
 #pragma unroll
   for (int s = 0; s < kProjStages - 1; ++s)
-    if (s < kt_n) proj_issue<NSUB>(p, smem + s * L::kStage, m0, n0, kbase + s * kStageK, wave, lane);
+    if (s < kt_n) proj_issue<NSUB, PM>(p, smem + s * L::kStage, m0, n0, kbase + s * kStageK, wave, lane);
   for (int t = 0; t < kt_n; ++t) {
     // this wave's copies of stage t are done once at most the next stage's remain
     if (t + 1 < kt_n) {
@@ -231,27 +257,94 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
     asm volatile("s_barrier" ::: "memory");
     const int tn2 = t + kProjStages - 1;
     if (tn2 < kt_n)
-      proj_issue<NSUB>(p, smem + (tn2 % kProjStages) * L::kStage, m0, n0, kbase + tn2 * kStageK, wave,
+      proj_issue<NSUB, PM>(p, smem + (tn2 % kProjStages) * L::kStage, m0, n0, kbase + tn2 * kStageK, wave,
                        lane);
-    proj_mma<NSUB>(smem + (t % kProjStages) * L::kStage, kg, nw, lane, acc);
+    proj_mma<NSUB, PM>(smem + (t % kProjStages) * L::kStage, kg, nw, lane, acc);
+  }
+
+  // EPI 4: the rows' cos / sin, in flight while the k-groups are summed
+  uint16_t e_rc[kEpiRows], e_rs[kEpiRows];
+  if constexpr (EPI == 4) {
+    // the loads issued before the k loop are long done: take their values now, so that
+    // the compiler's wait for them does not land after the loads below
+    __asm__ __volatile__("" ::"v"(sc[0][0]), "v"(sc[0][1]), "v"(sc[0][2]), "v"(sc[0][3]), "v"(sc[1][0]),
+                         "v"(sc[1][1]), "v"(sc[1][2]), "v"(sc[1][3]), "v"(e_w[0]), "v"(e_w[1]));
+#pragma unroll
+    for (int i = 0; i < kEpiRows; ++i) {
+      const int64_t pos = min(max(e_pos[i], 0), qa.rope_positions - 1);
+      e_rc[i] = qa.rope[pos * 128 + lane];
+      e_rs[i] = qa.rope[pos * 128 + 64 + lane];
+    }
   }
 
   // ---- sum the k-groups through LDS (the stage ring is free once all waves pass) ----
-  __syncthreads();
+  lds_barrier();
   floatx4* red = (floatx4*)smem;  // [kg][nw][mi][ns][lane]
 #pragma unroll
-  for (int mi = 0; mi < kPM; ++mi)
+  for (int mi = 0; mi < PM; ++mi)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * kPM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
-  __syncthreads();
+    for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
+  lds_barrier();
 
-  for (int mi = kg; mi < kPM; mi += kKGroups) {
+  if constexpr (EPI == 4) {
+    static_assert(NSUB == 8 && PM <= 2 * kKGroups, "one head per tile, two row subtiles per wave");
+    constexpr bool kInt8 = KV >= 2;
+    constexpr int kKvSdt = KV == 3 ? NE_DTYPE_FP16 : NE_DTYPE_BF16;
+    u32x2 bits[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int mi = kg + t * kKGroups;
+      if (mi < PM) {
+#pragma unroll
+        for (int ns = 0; ns < 2; ++ns) {
+          floatx4 v = red[((nw * PM + mi) * 2 + ns) * kWave + lane];
+#pragma unroll
+          for (int q = 1; q < kKGroups; ++q) v += red[(((q * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane];
+          bits[t][ns] = u32x2{pack_bf16x2(v[0] * sc[ns][0], v[1] * sc[ns][1]),
+                              pack_bf16x2(v[2] * sc[ns][2], v[3] * sc[ns][3])};
+        }
+      }
+    }
+    lds_barrier();  // the reduction buffer is read: reuse it for the bf16 tile [80][128]
+    uint16_t* tile = (uint16_t*)smem;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int mi = kg + t * kKGroups;
+      if (mi < PM) {
+#pragma unroll
+        for (int ns = 0; ns < 2; ++ns)
+          *(u32x2*)(tile + (mi * 16 + r) * 128 + (2 * nw + ns) * 16 + 4 * g) = bits[t][ns];
+      }
+    }
+    lds_barrier();
+    // this wave's rows all at once, so that their reductions overlap
+    int rows_e[kEpiRows];
+    bool valid_e[kEpiRows];
+    float a_e[kEpiRows], b_e[kEpiRows], c_e[kEpiRows], s_e[kEpiRows];
+    int64_t slot_e[kEpiRows];
+#pragma unroll
+    for (int i = 0; i < kEpiRows; ++i) {
+      const int rr = min(wave + L::kWaves * i, kPRows - 1);
+      rows_e[i] = m0 + rr;
+      valid_e[i] = wave + L::kWaves * i < kPRows && m0 + rr < p.m;
+      a_e[i] = bf16_to_f32(tile[rr * 128 + lane]);
+      b_e[i] = bf16_to_f32(tile[rr * 128 + 64 + lane]);
+      c_e[i] = bf16_to_f32(e_rc[i]);
+      s_e[i] = bf16_to_f32(e_rs[i]);
+      slot_e[i] = e_slot[i];
+    }
+    qk_norm_rope_kv_vectors<kInt8, kKvSdt, kEpiRows>(qa, rows_e, valid_e, tn, lane, a_e, b_e, slot_e,
+                                                     bf16_to_f32(e_w[0]), bf16_to_f32(e_w[1]), c_e, s_e);
+    return;
+  }
+
+  for (int mi = kg; mi < PM; mi += kKGroups) {
     floatx4 v[2];
 #pragma unroll
     for (int ns = 0; ns < 2; ++ns) {
-      v[ns] = red[((nw * kPM + mi) * 2 + ns) * kWave + lane];
+      v[ns] = red[((nw * PM + mi) * 2 + ns) * kWave + lane];
 #pragma unroll
-      for (int q = 1; q < kKGroups; ++q) v[ns] += red[(((q * L::kNW + nw) * kPM + mi) * 2 + ns) * kWave + lane];
+      for (int q = 1; q < kKGroups; ++q) v[ns] += red[(((q * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane];
     }
     // lane holds D[n = 4 g + i][m = r] of weight subtiles 2 nw + ns
     const int m = m0 + mi * 16 + r;
@@ -288,22 +381,33 @@ __global__ __launch_bounds__(ProjLayout<NSUB>::kThreads) void proj_kernel(GemmPa
   }
 }
 
-template <int NSUB, int SDT, int EPI>
-int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name) {
-  using L = ProjLayout<NSUB>;
-  p.tiles_m = ceil_div(p.m, kPRows);
+template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM>
+int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
+                const QkvRopeArgs& qa = QkvRopeArgs{}) {
+  using L = ProjLayout<NSUB, PM>;
+  p.tiles_m = ceil_div(p.m, L::kPRows);
   p.tiles_n = p.n / (NSUB * 16);
   const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
   const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
   static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)proj_kernel<NSUB, SDT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
+      (const void*)proj_kernel<NSUB, SDT, EPI, KV, PM>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
   if (attr != hipSuccess) {
     set_error("%s: cannot reserve %d bytes of LDS: %s", name, L::kLds, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI>), grid, dim3(L::kThreads), L::kLds, stream, p,
-                     p.k / splits, partial);
+  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI, KV, PM>), grid, dim3(L::kThreads), L::kLds, stream, p,
+                     p.k / splits, partial, qa);
   return check_launch(name);
+}
+
+template <int SDT>
+int dispatch_qkv_fused(GemmParams p, const QkvRopeArgs& qa, int kv_mode, hipStream_t s) {
+  switch (kv_mode) {
+    // 48-row tiles: 7 x 32 = 224 work-groups for 320 rows, 3 rows per wave in the epilogue
+    case 1: return launch_proj<8, SDT, 4, 1, 3>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
+    case 2: return launch_proj<8, SDT, 4, 2, 3>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
+    default: return launch_proj<8, SDT, 4, 3, 3>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
+  }
 }
 
 template <int SDT>
@@ -553,6 +657,55 @@ extern "C" int ne_w8a16_gemm_splitk(const void* x, int64_t ldx, const int8_t* w,
                "x, w and partials must be 16-byte aligned");
   return w8a16_common(x, ldx, w, scale, scale_dtype, m, n, k, nullptr, 0, NE_EPILOGUE_STORE, splits,
                       partials, stream);
+}
+
+extern "C" int ne_w8a16_qkv_norm_rope_kv(
+    const void* x, int64_t ldx, const int8_t* w, const void* scale, int32_t scale_dtype, int32_t m,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t k, const void* q_norm_w, const void* k_norm_w,
+    float eps, const int32_t* positions, const void* rope, int32_t rope_positions,
+    const int32_t* slot_mapping, int32_t kv_dtype, void* k_cache, void* v_cache, void* k_scale,
+    void* v_scale, int32_t kv_scale_dtype, void* q_out, void* stream) {
+  NE_CHECK_ARG(m >= 0 && num_q_heads > 0 && num_kv_heads > 0 && k > 0, "bad shape");
+  if (m == 0) return NE_OK;
+  NE_CHECK_ARG(x && w && scale && q_norm_w && k_norm_w && positions && rope && slot_mapping && k_cache &&
+                   v_cache && q_out,
+               "null pointer argument");
+  NE_CHECK_ARG(rope_positions > 0, "rope_positions must be > 0");
+  NE_CHECK_SUPPORTED(k % 128 == 0, "k must be a multiple of 128 (got %d)", k);
+  NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
+  NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0, "x and w must be 16-byte aligned");
+  int kv_mode = 0;
+  if (kv_dtype == NE_DTYPE_BF16) {
+    kv_mode = 1;
+  } else if (kv_dtype == NE_DTYPE_INT8) {
+    NE_CHECK_ARG(k_scale && v_scale, "an int8 cache needs k_scale and v_scale");
+    NE_CHECK_SUPPORTED(kv_scale_dtype == NE_DTYPE_BF16 || kv_scale_dtype == NE_DTYPE_FP16,
+                       "fused KV write supports bf16 or fp16 scales");
+    kv_mode = kv_scale_dtype == NE_DTYPE_BF16 ? 2 : 3;
+  } else {
+    set_error("kv_dtype must be int8 or bf16");
+    return NE_EINVAL;
+  }
+  GemmParams p{};
+  p.x = (const uint16_t*)x;
+  p.ldx = ldx;
+  p.w = w;
+  p.scale = scale;
+  p.m = m;
+  p.n = (num_q_heads + 2 * num_kv_heads) * 128;
+  p.k = k;
+  const QkvRopeArgs qa{num_q_heads, num_kv_heads, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w,
+                       eps, positions, (const uint16_t*)rope, rope_positions, slot_mapping,
+                       k_cache, v_cache, k_scale, v_scale, (uint16_t*)q_out};
+  hipStream_t s = (hipStream_t)stream;
+  switch (scale_dtype) {
+    case NE_DTYPE_BF16: return dispatch_qkv_fused<NE_DTYPE_BF16>(p, qa, kv_mode, s);
+    case NE_DTYPE_FP16: return dispatch_qkv_fused<NE_DTYPE_FP16>(p, qa, kv_mode, s);
+    case NE_DTYPE_FP32: return dispatch_qkv_fused<NE_DTYPE_FP32>(p, qa, kv_mode, s);
+    default:
+      set_error("scale_dtype must be bf16, fp16 or fp32");
+      return NE_EINVAL;
+  }
 }
 
 extern "C" int32_t ne_lm_head_num_tiles(int32_t n) { return n > 0 ? n / kArgmaxCols : 0; }

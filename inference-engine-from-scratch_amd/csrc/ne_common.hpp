@@ -20,6 +20,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
+// int32 read through the scalar cache: loads of a wave-uniform address in the constant
+// address space compile to s_load (data written by an earlier kernel only)
+using ConstI32 = __attribute__((address_space(4))) const int32_t;
+
 constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, work-groups dispatched round-robin
 
 // ---- error state (per calling thread) ------------------------------------
@@ -90,6 +94,13 @@ __device__ __forceinline__ void store_scale(void* p, int64_t i, float v) {
   } else {
     ((float*)p)[i] = v;
   }
+}
+
+// Work-group barrier ordering LDS accesses only: waits for this wave's LDS operations,
+// not for its global loads in flight (a __syncthreads fence would wait for those too).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0), vmcnt / expcnt left alone
+  __asm__ __volatile__("s_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -11,6 +11,7 @@
 //   int8 KV (ne/models/int8_quantization.py:30-34): s = max(amax, 1e-8)/127 in fp32,
 //            code = rint(fp32(x)/s) clamped to +-127, stored scale = s in the scale dtype
 #include "ne_common.hpp"
+#include "qk_rope_kv.hpp"
 
 namespace ne {
 
@@ -120,28 +121,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_
   }
 }
 
-// Quantise (int8 cache) or copy one 128-vector held as lane / lane+64 values.
-template <bool INT8, int SDT>
-__device__ __forceinline__ void write_vector(float a, float b, int lane, int64_t slot, int head,
-                                             int num_heads, void* cache, void* scales) {
-  const int64_t base = (slot * num_heads + head) * 128;
-  if constexpr (INT8) {
-    float amax = fmaxf(fabsf(a), fabsf(b));
-    amax = wave_max(amax);
-    const float s = fmaxf(amax, 1e-8f) / 127.f;
-    const float qa = fminf(fmaxf(rintf(a / s), -127.f), 127.f);
-    const float qb = fminf(fmaxf(rintf(b / s), -127.f), 127.f);
-    int8_t* c = (int8_t*)cache + base;
-    c[lane] = (int8_t)(int)qa;
-    c[lane + 64] = (int8_t)(int)qb;
-    if (lane == 0) store_scale<SDT>(scales, slot * num_heads + head, s);
-  } else {
-    uint16_t* c = (uint16_t*)cache + base;
-    c[lane] = f32_to_bf16(a);
-    c[lane + 64] = f32_to_bf16(b);
-  }
-}
-
 // One wave per (token row, head), four heads of a row per work-group: q heads,
 // then k heads, then v heads.  cos/sin come from `rope` ([rope_positions][2][64]
 // bf16: cos, then sin, of position * inv_freq[i]; dims i and i + 64 share them),
@@ -159,30 +138,26 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
   if (h >= heads) return;  // wave-uniform; the kernel has no barrier
   const int lane = threadIdx.x % kWave;
   const uint16_t* v = qkv + (int64_t)row * heads * 128 + h * 128;
-  float a = bf16_to_f32(v[lane]);
-  float b = bf16_to_f32(v[lane + 64]);
+  const float a = bf16_to_f32(v[lane]);
+  const float b = bf16_to_f32(v[lane + 64]);
   const int64_t slot = slot_mapping[row];
+  float wa = 0.f, wb = 0.f, c16 = 0.f, s16 = 0.f;
   if (h < hq + hkv) {
     const uint16_t* w = (h < hq) ? q_norm_w : k_norm_w;
-    const float wa = bf16_to_f32(w[lane]), wb = bf16_to_f32(w[lane + 64]);
+    wa = bf16_to_f32(w[lane]);
+    wb = bf16_to_f32(w[lane + 64]);
     const int pos = min(max(positions[row], 0), rope_positions - 1);
-    const float c16 = bf16_to_f32(rope[(int64_t)pos * 128 + lane]);
-    const float s16 = bf16_to_f32(rope[(int64_t)pos * 128 + 64 + lane]);
-    const float inv = rsqrtf(wave_sum(a * a + b * b) / 128.f + eps);
-    a = bf16_round(bf16_round(a * inv) * wa);
-    b = bf16_round(bf16_round(b * inv) * wb);
-    const float ra = bf16_round(bf16_round(a * c16) + bf16_round(-b * s16));
-    const float rb = bf16_round(bf16_round(b * c16) + bf16_round(a * s16));
-    if (h < hq) {
-      uint16_t* qo = q_out + ((int64_t)row * hq + h) * 128;
-      qo[lane] = f32_to_bf16(ra);
-      qo[lane + 64] = f32_to_bf16(rb);
-    } else {
-      write_vector<INT8, SDT>(ra, rb, lane, slot, h - hq, hkv, k_cache, k_scale);
-    }
-  } else {
-    write_vector<INT8, SDT>(a, b, lane, slot, h - hq - hkv, hkv, v_cache, v_scale);
+    c16 = bf16_to_f32(rope[(int64_t)pos * 128 + lane]);
+    s16 = bf16_to_f32(rope[(int64_t)pos * 128 + 64 + lane]);
   }
+  const QkvRopeArgs q{hq, hkv, q_norm_w, k_norm_w, eps, positions, rope, rope_positions, slot_mapping,
+                      k_cache, v_cache, k_scale, v_scale, q_out};
+  const int rows1[1] = {row};
+  const bool valid1[1] = {true};
+  float av[1] = {a}, bv[1] = {b};
+  const int64_t sv[1] = {slot};
+  const float cv[1] = {c16}, sn[1] = {s16};
+  qk_norm_rope_kv_vectors<INT8, SDT, 1>(q, rows1, valid1, h, lane, av, bv, sv, wa, wb, cv, sn);
 }
 
 // Standalone A7: vectors [n, heads, 128] -> cache at slot_mapping, one wave per vector.

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -88,6 +88,16 @@ SIGNATURES: dict[str, tuple] = {
             _vp, _vp, _f32,  # norm weights, eps
             _vp, _vp, _i32, _vp,  # positions, rope table, its positions, slot mapping
             _vp, _vp, _vp, _vp, _i32, _i32,  # caches, scales, dtypes
+            _vp, _vp,  # q_out, stream
+        ],
+    ),
+    "ne_w8a16_qkv_norm_rope_kv": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32,  # x, ldx, w, scale, dtype, m, hq, hkv, k
+            _vp, _vp, _f32,  # norm weights, eps
+            _vp, _vp, _i32, _vp,  # positions, rope table, its positions, slot mapping
+            _i32, _vp, _vp, _vp, _vp, _i32,  # kv dtype, caches, scales, scale dtype
             _vp, _vp,  # q_out, stream
         ],
     ),

@@ -505,6 +505,59 @@ def qk_norm_rope_kv_write(
     return q_out
 
 
+def w8a16_qkv_norm_rope_kv(
+    x: torch.Tensor,
+    w_int8: torch.Tensor,
+    w_scale: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    eps: float,
+    positions: torch.Tensor,
+    rope_cos_sin: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    q_out: torch.Tensor,
+) -> torch.Tensor:
+    """The QKV projection with QK-norm, RoPE and the KV write fused into its epilogue:
+    the same bits as :func:`w8a16_gemm` followed by :func:`qk_norm_rope_kv_write`."""
+    device = _require_gpu(x, w_int8, w_scale, q_norm_weight, k_norm_weight, positions, rope_cos_sin,
+                          slot_mapping, k_cache, v_cache, q_out)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1, "x must be [m, k] bf16")
+    _check(w_int8.dtype == torch.int8 and w_int8.is_contiguous(), "w must be contiguous int8")
+    _int32(positions, "positions")
+    _int32(slot_mapping, "slot_mapping")
+    _check(rope_cos_sin.dtype == torch.bfloat16 and rope_cos_sin.dim() == 3 and rope_cos_sin.shape[1:] == (2, 64)
+           and rope_cos_sin.is_contiguous(), "rope_cos_sin must be contiguous [positions, 2, 64] bf16")
+    rows, kdim = x.shape
+    _check(w_int8.shape == ((num_q_heads + 2 * num_kv_heads) * HEAD_DIM, kdim), "w shape mismatch")
+    _check(q_out.shape == (rows, num_q_heads, HEAD_DIM) and q_out.dtype == torch.bfloat16 and q_out.is_contiguous(),
+           "q_out must be contiguous [rows, q_heads, 128] bf16")
+    is_int8 = k_cache.dtype == torch.int8
+    _native.call(
+        "ne_w8a16_qkv_norm_rope_kv",
+        _ptr(x), x.stride(0), _ptr(w_int8), _ptr(w_scale), dtype_code(w_scale.dtype), rows,
+        num_q_heads, num_kv_heads, kdim,
+        _ptr(q_norm_weight), _ptr(k_norm_weight), float(eps),
+        _ptr(positions), _ptr(rope_cos_sin), rope_cos_sin.shape[0], _ptr(slot_mapping),
+        dtype_code(k_cache.dtype), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16,
+        _ptr(q_out), _stream(device),
+    )
+    return q_out
+
+
+def qkv_fusion_supported(k_cache: torch.Tensor, k_scale: torch.Tensor | None) -> bool:
+    """Whether :func:`w8a16_qkv_norm_rope_kv` takes this cache (bf16, or int8 with bf16/fp16 scales)."""
+    if k_cache.dtype == torch.bfloat16:
+        return True
+    return k_cache.dtype == torch.int8 and k_scale is not None and k_scale.dtype in (torch.bfloat16, torch.float16)
+
+
 # ------------------------------------------------------------------------ A9/A10
 def accept(
     drafts: torch.Tensor,

@@ -225,6 +225,9 @@ class Qwen3VerifyModel:
         self.rope = None
         self.ensure_rope(4096)
         self.workspace = kernels.AttentionWorkspace()
+        # QKV projection with QK-norm, RoPE and the KV write in its epilogue; False
+        # runs the GEMM and the row kernel separately (the same bits, one more launch)
+        self.fuse_qkv = True
         self.softmax_scale = 1.0 / math.sqrt(c.head_dim)
         # o_proj / down_proj (N = hidden) split K across work-groups when the rows alone
         # give too few output tiles; the fp32 partials feed the fused residual add + norm
@@ -259,14 +262,23 @@ class Qwen3VerifyModel:
             kernels.paged_attention_plan(batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start,
                                          batch.q_len, c.num_attention_heads, c.num_key_value_heads,
                                          batch.max_q_len, batch.max_ctx_len, self.workspace)
+        fuse = self.fuse_qkv and kernels.qkv_fusion_supported(pool.key_caches[0], pool.key_scale_2d(0))
         for i, layer in enumerate(w.layers):
-            kernels.w8a16_gemm(normed, layer.qkv_int8, layer.qkv_scale, out=qkv)
-            kernels.qk_norm_rope_kv_write(
-                qkv, c.num_attention_heads, c.num_key_value_heads, layer.q_norm, layer.k_norm, eps,
-                batch.positions[:rows], self.rope, batch.slot_mapping[:rows],
-                pool.key_caches[i], pool.value_caches[i], pool.key_scale_2d(i), pool.value_scale_2d(i),
-                q_out=q,
-            )
+            if fuse:  # QK-norm + RoPE + KV write in the QKV GEMM's epilogue (same bits)
+                kernels.w8a16_qkv_norm_rope_kv(
+                    normed, layer.qkv_int8, layer.qkv_scale, c.num_attention_heads, c.num_key_value_heads,
+                    layer.q_norm, layer.k_norm, eps, batch.positions[:rows], self.rope,
+                    batch.slot_mapping[:rows], pool.key_caches[i], pool.value_caches[i],
+                    pool.key_scale_2d(i), pool.value_scale_2d(i), q_out=q,
+                )
+            else:
+                kernels.w8a16_gemm(normed, layer.qkv_int8, layer.qkv_scale, out=qkv)
+                kernels.qk_norm_rope_kv_write(
+                    qkv, c.num_attention_heads, c.num_key_value_heads, layer.q_norm, layer.k_norm, eps,
+                    batch.positions[:rows], self.rope, batch.slot_mapping[:rows],
+                    pool.key_caches[i], pool.value_caches[i], pool.key_scale_2d(i), pool.value_scale_2d(i),
+                    q_out=q,
+                )
             kernels.paged_verify_attention(
                 q, pool.key_caches[i], pool.value_caches[i], pool.key_scale_2d(i), pool.value_scale_2d(i),
                 batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start, batch.q_len,

@@ -132,3 +132,46 @@ def test_lm_head_argmax_only_matches_logits_path(device):
     _, p2 = kernels.lm_head(hidden, embed, logits=False, argmax_partials=True)
     torch.cuda.synchronize()
     assert torch.equal(p1, p2)
+
+
+@pytest.mark.parametrize("kv", ["int8-bf16-scales", "int8-fp16-scales", "bf16"])
+@pytest.mark.parametrize("m", [320, 37, 1])
+def test_fused_qkv_epilogue_equals_gemm_then_row_kernel(device, kv, m):
+    """ne_w8a16_qkv_norm_rope_kv writes the same bits (q_out, cache codes, scales) as
+    ne_w8a16_gemm followed by ne_qk_norm_rope_kv_write; the latter is checked against
+    the oracle in test_rowwise_gpu.py and the GEMM above."""
+    hq, hkv, k = 16, 8, 1024
+    g = torch.Generator().manual_seed(1000 + m)
+    wq, ws = make_weight((hq + 2 * hkv) * 128, k, seed=7)
+    wq, ws = wq.to(device), ws.to(device)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(device)
+    q_norm = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(device)
+    k_norm = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(device)
+    positions = torch.randint(0, 3000, (m,), generator=g, dtype=torch.int32).to(device)
+    rope = kernels.rope_table(4096, 1e6).to(device)
+    num_slots = 2048
+    slots = torch.randperm(num_slots, generator=g)[:m].to(torch.int32).to(device)
+
+    def pool():
+        if kv == "bf16":
+            return (torch.zeros(num_slots, hkv, 128, dtype=torch.bfloat16, device=device),
+                    torch.zeros(num_slots, hkv, 128, dtype=torch.bfloat16, device=device), None, None)
+        sdt = torch.bfloat16 if kv == "int8-bf16-scales" else torch.float16
+        return (torch.zeros(num_slots, hkv, 128, dtype=torch.int8, device=device),
+                torch.zeros(num_slots, hkv, 128, dtype=torch.int8, device=device),
+                torch.zeros(num_slots, hkv, dtype=sdt, device=device),
+                torch.zeros(num_slots, hkv, dtype=sdt, device=device))
+
+    a, b = pool(), pool()
+    qkv = kernels.w8a16_gemm(x, wq, ws)
+    q_ref = kernels.qk_norm_rope_kv_write(qkv, hq, hkv, q_norm, k_norm, 1e-6, positions, rope, slots, *a)
+    q_out = torch.empty(m, hq, 128, dtype=torch.bfloat16, device=device)
+    assert kernels.qkv_fusion_supported(b[0], b[2])
+    kernels.w8a16_qkv_norm_rope_kv(x, wq, ws, hq, hkv, q_norm, k_norm, 1e-6, positions, rope, slots, *b,
+                                   q_out=q_out)
+    torch.cuda.synchronize()
+    assert torch.equal(q_out.view(torch.int16), q_ref.view(torch.int16))
+    for ta, tb in zip(a, b):
+        if ta is not None:
+            assert torch.equal(ta.view(torch.uint8), tb.view(torch.uint8))
+    assert int(a[0].view(torch.uint8).ne(0).sum()) > 0  # something was written
