@@ -992,16 +992,26 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
 // PLANNED: the work item and the split's slots come from attention_plan_kernel's
 // output instead of being derived here (one round trip instead of two).
 // MT: row tiles of 16 per KV head handled by each wave (1, or 2 for up to 32 rows).
-template <int SDT, bool PLANNED, int MT>
+// KS: waves per KV head.  KS = 1: the 8 waves are the 8 KV heads of one work item.
+// KS > 1 (planned, one row tile, items of whole sequences): KS work-groups share an
+// item, each taking 8 / KS heads, and a head's KS waves take consecutive parts of the
+// item's tiles, their (m, l, O) merged through LDS before the store -- so that short
+// contexts fill KS times as many CUs without a merge kernel.
+template <int SDT, bool PLANNED, int MT, int KS = 1>
 __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel(AttnParams p) {
+  static_assert(KS == 1 || (PLANNED && MT == 1 && kHeadWaves % KS == 0), "head split: planned, one row tile");
+  constexpr int HG = kHeadWaves / KS;  // KV heads per work-group
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int* s_slot = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot);
   float* s_sc_all = (float*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4);
   int* s_plan = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4 + kHeadWaves * kWave * 4);
 
-  // ---- work item: one split of one sequence (M tile 0); the wave is the KV head ----
+  // ---- work item: one split of one sequence (M tile 0); wave -> (KV head, part) ----
   const int tid = threadIdx.x;
-  const int head = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int widx = (KS == 1) ? (int)blockIdx.x : (int)blockIdx.x / KS;  // work item
+  const int head = (KS == 1) ? wave : ((int)blockIdx.x % KS) * HG + wave % HG;
+  const int ks = wave / HG;  // this wave's part of the item's tiles
   const int lane = tid % kWave;
   PlanItem item;
   int32_t planned_slot = 0;
@@ -1012,9 +1022,9 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     // round trip precedes the first K/V copy.  The compiler barriers keep the load
     // first and the store last.
     static_assert(kPlanMaxTiles == kHeadWaves * kWave, "one slot per thread");
-    const int32_t my_slot = p.plan_slots[(int64_t)blockIdx.x * kPlanMaxTiles + tid];
+    const int32_t my_slot = p.plan_slots[(int64_t)widx * kPlanMaxTiles + tid];
     __asm__ __volatile__("" ::: "memory");
-    const ConstI32* d = (const ConstI32*)(p.plan_desc + (int64_t)blockIdx.x * kDescInts);
+    const ConstI32* d = (const ConstI32*)(p.plan_desc + (int64_t)widx * kDescInts);
     item.seq = d[0];
     item.split = d[1];
     item.n_splits = d[2];
@@ -1056,9 +1066,12 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     j0 = (int)((int64_t)item.tiles * item.split / n_splits);
     j1 = (int)((int64_t)item.tiles * (item.split + 1) / n_splits);
   }
-  const int kstart = j0 * kTileKeys;
-  const int kend = min(item.ctx, j1 * kTileKeys);
-  const int n_tiles = j1 - j0;
+  // this wave's tiles: part ks of KS of the item's [j0, j1)
+  const int jw0 = j0 + (j1 - j0) * ks / KS;
+  const int jw1 = j0 + (j1 - j0) * (ks + 1) / KS;
+  const int kstart = jw0 * kTileKeys;
+  const int kend = min(item.ctx, jw1 * kTileKeys);
+  const int n_tiles = jw1 - jw0;
   const int ql = item.ql;
   const int rows_total = p.group * ql;
   if (rows_total > MT * kRows && tid == 0) atomicOr(p.error_flag, 1u);
@@ -1104,12 +1117,17 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   }
   __syncthreads();  // s_slot ready
 
-  char* ring = smem + head * (kDmaRing * kDmaSlot);
+  char* ring = smem + wave * (kDmaRing * kDmaSlot);
+  const int* w_slot = s_slot + (jw0 - j0);  // this wave's tiles in the item's slot list
+  if (n_tiles > 0) {
 #pragma unroll
-  for (int j = 0; j < kDmaRing; ++j) dma_tile(p, s_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
-  // Q was issued before the ring's copies: wait for it alone (the compiler's own wait
-  // would also drain the copies, since it does not order them after the Q loads)
-  dma_wait_vmcnt<kDmaPerTile * kDmaRing>();
+    for (int j = 0; j < kDmaRing; ++j) dma_tile(p, w_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
+    // Q was issued before the ring's copies: wait for it alone (the compiler's own wait
+    // would also drain the copies, since it does not order them after the Q loads)
+    dma_wait_vmcnt<kDmaPerTile * kDmaRing>();
+  } else {
+    dma_wait_vmcnt<0>();  // a wave with no tiles of the item (KS > 1) only loads Q
+  }
   QFrag<true> qf[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -1134,7 +1152,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  float* sc_row = s_sc_all + head * kWave;
+  float* sc_row = s_sc_all + wave * kWave;
   const int n_iter = (n_tiles + 1) / 2;
   for (int it = 0; it < n_iter; ++it) {
     // this wave's DMA of tiles 2it, 2it+1 has landed once at most the two tiles
@@ -1152,18 +1170,54 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     }
     // the two slots are free once their reads have returned: refill them
     dma_wait_lgkmcnt0();
-    dma_tile(p, s_slot, n_tiles, 2 * it + kDmaRing, head, lane, ring + ((2 * it) % kDmaRing) * kDmaSlot);
-    dma_tile(p, s_slot, n_tiles, 2 * it + 1 + kDmaRing, head, lane,
+    dma_tile(p, w_slot, n_tiles, 2 * it + kDmaRing, head, lane, ring + ((2 * it) % kDmaRing) * kDmaSlot);
+    dma_tile(p, w_slot, n_tiles, 2 * it + 1 + kDmaRing, head, lane,
              ring + ((2 * it + 1) % kDmaRing) * kDmaSlot);
   }
   dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
+
+  if constexpr (KS > 1) {
+    // the KS waves of a head combine their states (the rings are free once every wave
+    // is past its loop): out = sum_k 2^(m_k - M) O_k / sum_k 2^(m_k - M) l_k
+    float lt = l[0];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    lds_barrier();
+    floatx4* s_o = (floatx4*)smem;                   // [wave][8][lane]
+    float2* s_ml = (float2*)(smem + kHeadWaves * 8 * kWave * 16);  // [wave][lane]
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_o[(wave * 8 + j) * kWave + lane] = o[0][j];
+    s_ml[wave * kWave + lane] = float2{m[0], lt};
+    lds_barrier();
+    if (ks != 0) return;
+    float M = m[0];
+#pragma unroll
+    for (int k = 1; k < KS; ++k) M = fmaxf(M, s_ml[(k * HG + wave) * kWave + lane].x);
+    const float a0 = __builtin_amdgcn_exp2f(m[0] - M);
+    lt *= a0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[0][j] *= a0;
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const int w = k * HG + wave;
+      const float2 ml = s_ml[w * kWave + lane];
+      const float a = __builtin_amdgcn_exp2f(ml.x - M);
+      lt += a * ml.y;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[0][j] += a * s_o[(w * 8 + j) * kWave + lane];
+    }
+    m[0] = M;
+    l[0] = lt;
+  }
 
   // lane (r, g) holds row r of tile mt, dims 32g + 8i + j in o[mt][j][i]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     float lt = l[mt];
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
+    if constexpr (KS == 1) {
+      lt += __shfl_xor(lt, 16);
+      lt += __shfl_xor(lt, 32);
+    }
     if (!row_valid[mt]) continue;
     if (n_splits == 1) {
       uint16_t* dst = p.out + (int64_t)(item.qs + qi[mt]) * p.o_tok_stride +
@@ -1178,8 +1232,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
         *(u32x4*)(dst + 8 * i) = bits;
       }
     } else {
-      // partial slot: this work-group's index, which the plan gives the merge too
-      const int64_t pbase = ((int64_t)blockIdx.x * kHeadWaves + head) * kPartRows + mt * kRows + r;
+      // partial slot: this work item's index, which the plan gives the merge too
+      const int64_t pbase = ((int64_t)widx * kHeadWaves + head) * kPartRows + mt * kRows + r;
       float* po = p.part_o + pbase * kHeadDim + 32 * g;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1385,22 +1439,39 @@ int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStre
 
 // The DMA kernel serves int8 caches with 8 KV heads and 2-byte scales; it needs
 // the attribute for more than the default dynamic LDS once per instantiation.
-template <int SDT, bool PLANNED, int MT>
-int launch_attention_dma_mt(const AttnParams& p, hipStream_t s) {
+template <int SDT, bool PLANNED, int MT, int KS = 1>
+int launch_attention_dma_ks(const AttnParams& p, unsigned grid, hipStream_t s) {
   static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)paged_attention_dma_kernel<SDT, PLANNED, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+      (const void*)paged_attention_dma_kernel<SDT, PLANNED, MT, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
       kDmaLds);
   if (attr != hipSuccess) {
     set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", kDmaLds,
               hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT>), dim3((unsigned)p.plan_grid),
-                     dim3(kHeadWaves * kWave), kDmaLds, s, p);
-  int rc = check_launch("paged_attention_dma_kernel");
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT, KS>), dim3(grid), dim3(kHeadWaves * kWave),
+                     kDmaLds, s, p);
+  return check_launch("paged_attention_dma_kernel");
+}
+
+template <int SDT, bool PLANNED, int MT>
+int launch_attention_dma_mt(const AttnParams& p, hipStream_t s) {
   // no sequence is split when every context fits in one split's minimum length
   const int min_w = p.plan_w > 0 ? p.plan_w : kPlanMinTiles;
-  if (rc != NE_OK || ceil_div(p.max_ctx, kTileKeys) <= min_w) return rc;
+  const bool no_splits = ceil_div(p.max_ctx, kTileKeys) <= min_w;
+  int rc;
+  if constexpr (PLANNED && MT == 1) {
+    // whole-sequence items: 4 (or 2) work-groups per sequence, each over 2 (or 4) KV
+    // heads, while that still fits one work-group per CU
+    if (no_splits && p.plan_w == 0 && p.num_seqs * 4 <= kPlanCUs) {
+      return launch_attention_dma_ks<SDT, PLANNED, MT, 4>(p, (unsigned)p.num_seqs * 4, s);
+    }
+    if (no_splits && p.plan_w == 0 && p.num_seqs * 2 <= kPlanCUs) {
+      return launch_attention_dma_ks<SDT, PLANNED, MT, 2>(p, (unsigned)p.num_seqs * 2, s);
+    }
+  }
+  rc = launch_attention_dma_ks<SDT, PLANNED, MT>(p, (unsigned)p.plan_grid, s);
+  if (rc != NE_OK || no_splits) return rc;
   hipLaunchKernelGGL(attention_plan_merge_kernel, dim3((unsigned)p.num_seqs * kHeadWaves),
                      dim3(kPartRows * 16), 0, s, p);
   return check_launch("attention_plan_merge_kernel");

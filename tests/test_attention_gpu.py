@@ -223,3 +223,33 @@ def test_k8_long_contexts_with_a_shared_prefix(device, split_len):
                                          max_q_len=9, max_ctx_len=max(ctx), split_len=split_len)
     torch.cuda.synchronize()
     assert rel_err(out.cpu(), ref) < TOL
+
+
+@pytest.mark.parametrize("num_seqs", [64, 100, 200])
+def test_head_split_planned_path_for_short_contexts(device, num_seqs):
+    """Contexts of at most 256 keys (the verify step's): the planned kernel gives 4 (64
+    sequences) or 2 (100) work-groups per sequence, each over 2 or 4 KV heads, a head's
+    waves taking consecutive parts of its tiles and merging through LDS; 200 sequences
+    keep one work-group each.  Contexts of 1..17 keys leave some waves without tiles."""
+    rng = np.random.default_rng(num_seqs)
+    ctx = [int(c) for c in rng.integers(1, 257, size=num_seqs)]
+    ctx[:6] = [1, 2, 15, 16, 17, 256]
+    q_lens = [int(min(c, 5)) for c in ctx]
+    num_blocks = sum((c + 15) // 16 for c in ctx) + 8
+    kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, "int8", torch.bfloat16, seed=11)
+    tables, ctx_t, qs, ql, rows = make_batch(ctx, q_lens, num_blocks, 16, seed=12)
+    q = torch.randn(rows, HQ, 128, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    tables_d, ctx_d, qs_d, ql_d = d(tables), d(ctx_t), d(qs), d(ql)
+    args = (d(q), d(kc), d(vc), d(ks), d(vs), tables_d, 16, ctx_d, qs_d, ql_d)
+    ws = kernels.AttentionWorkspace()
+    a = kernels.paged_verify_attention(*args, max_q_len=5, max_ctx_len=max(ctx), workspace=ws)
+    kernels.paged_attention_plan(tables_d, 16, ctx_d, qs_d, ql_d, HQ, HKV, 5, max(ctx), ws)
+    b = kernels.paged_verify_attention(*args, max_q_len=5, max_ctx_len=max(ctx), workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    idx = real_rows(qs, ql)
+    ref = paged_attention_reference(q, kc, vc, ks, vs, tables, 16, ctx_t, qs, ql, model_dtype=torch.bfloat16)
+    assert rel_err(b.cpu()[idx], ref[idx]) < TOL
+    # the same values as one wave per head, up to the order of the fp32 sums (bf16 output)
+    assert float((b.cpu()[idx].float() - a.cpu()[idx].float()).abs().max()) <= 2e-2 * float(a.cpu()[idx].float().abs().max())
