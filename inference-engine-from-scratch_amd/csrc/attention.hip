@@ -92,6 +92,7 @@ struct AttnParams {
   uint32_t* error_flag;
   int32_t* plan;       // DMA kernel: first work-group of each sequence, then the total
   int32_t plan_w;      // DMA kernel: tiles per split (0: derived from the total work)
+  int32_t plan_whole;  // planned path: one work item per sequence (head-split kernel)
   int32_t plan_grid;   // DMA kernel: work-groups launched
   int32_t max_ctx;     // the caller's bound on ctx_len
   int32_t* plan_desc;  // precomputed plan: [plan_grid][8] work items (seq < 0: none)
@@ -733,6 +734,17 @@ constexpr int kPlanMaxSeqs = 2 * kHeadWaves * kWave;  // two sequences per threa
 constexpr int kPlanMinTiles = 16;                     // contexts up to 256 keys are never split
 constexpr int kPlanFloorTiles = 4;                    // no split shorter than 64 keys
 constexpr int kPlanCUs = 256;                         // work-groups the plan aims to fill
+constexpr int kWholeMaxTiles = 64;                    // longest context of a whole-sequence plan
+
+// Waves per KV head (4 or 2) when the precomputed plan gives every sequence one
+// whole work item, served by that many work-groups (one per CU at most): no split
+// partials and no merge kernel.  0 when the split plan serves the shape better.
+int whole_plan_ks(int num_seqs, int max_ctx, int split_len, int mtiles) {
+  if (split_len != 0 || mtiles != 1 || (max_ctx + kTileKeys - 1) / kTileKeys > kWholeMaxTiles) return 0;
+  if (num_seqs * 4 <= kPlanCUs) return 4;
+  if (num_seqs * 2 <= kPlanCUs) return 2;
+  return 0;
+}
 
 // Work plan of the DMA kernel.  Sequence b has tiles_b = ceil(ctx_b / 16) 16-key
 // tiles and gets n_b = ceil(tiles_b / W) splits of near-equal length (split s
@@ -801,10 +813,13 @@ __device__ PlanScan plan_scan(const AttnParams& p, int* s_plan) {
   for (int w = 0; w < kHeadWaves; ++w) T += s_plan[w];
   const int G = p.plan_grid;
   int W = p.plan_w;
-  if (W <= 0)
-    W = (p.max_ctx + kTileKeys - 1) / kTileKeys <= kPlanMinTiles
-            ? kPlanMinTiles
-            : max(kPlanFloorTiles, (T + (G - B) - 1) / (G - B));
+  const int max_tiles = (p.max_ctx + kTileKeys - 1) / kTileKeys;
+  if (W <= 0) {
+    if (p.plan_whole)
+      W = max(max_tiles, 1);  // every sequence in one item
+    else
+      W = max_tiles <= kPlanMinTiles ? kPlanMinTiles : max(kPlanFloorTiles, (T + (G - B) - 1) / (G - B));
+  }
   if (W > kPlanMaxTiles) {
     if (tid == 0 && blockIdx.x == 0) atomicOr(p.error_flag, 1u);
     W = kPlanMaxTiles;
@@ -1456,21 +1471,19 @@ int launch_attention_dma_ks(const AttnParams& p, unsigned grid, hipStream_t s) {
 
 template <int SDT, bool PLANNED, int MT>
 int launch_attention_dma_mt(const AttnParams& p, hipStream_t s) {
-  // no sequence is split when every context fits in one split's minimum length
-  const int min_w = p.plan_w > 0 ? p.plan_w : kPlanMinTiles;
-  const bool no_splits = ceil_div(p.max_ctx, kTileKeys) <= min_w;
-  int rc;
   if constexpr (PLANNED && MT == 1) {
     // whole-sequence items: 4 (or 2) work-groups per sequence, each over 2 (or 4) KV
-    // heads, while that still fits one work-group per CU
-    if (no_splits && p.plan_w == 0 && p.num_seqs * 4 <= kPlanCUs) {
-      return launch_attention_dma_ks<SDT, PLANNED, MT, 4>(p, (unsigned)p.num_seqs * 4, s);
-    }
-    if (no_splits && p.plan_w == 0 && p.num_seqs * 2 <= kPlanCUs) {
+    // heads, the waves of a head over consecutive parts of its tiles
+    if (p.plan_whole) {
+      if (whole_plan_ks(p.num_seqs, p.max_ctx, 0, 1) == 4)
+        return launch_attention_dma_ks<SDT, PLANNED, MT, 4>(p, (unsigned)p.num_seqs * 4, s);
       return launch_attention_dma_ks<SDT, PLANNED, MT, 2>(p, (unsigned)p.num_seqs * 2, s);
     }
   }
-  rc = launch_attention_dma_ks<SDT, PLANNED, MT>(p, (unsigned)p.plan_grid, s);
+  // no sequence is split when every context fits in one split's minimum length
+  const int min_w = p.plan_w > 0 ? p.plan_w : kPlanMinTiles;
+  const bool no_splits = ceil_div(p.max_ctx, kTileKeys) <= min_w;
+  const int rc = launch_attention_dma_ks<SDT, PLANNED, MT>(p, (unsigned)p.plan_grid, s);
   if (rc != NE_OK || no_splits) return rc;
   hipLaunchKernelGGL(attention_plan_merge_kernel, dim3((unsigned)p.num_seqs * kHeadWaves),
                      dim3(kPartRows * 16), 0, s, p);
@@ -1556,6 +1569,7 @@ int make_params(const void* q, int64_t q_token_stride, int64_t q_head_stride, co
   p.plan_slots = (int32_t*)(ws + L.slots_off);
   p.plan_w = L.plan_w;
   p.plan_grid = L.plan_grid;
+  p.plan_whole = 0;  // the planned entry point decides
   p.max_ctx = max_ctx_len;
   return NE_OK;
 }
@@ -1651,6 +1665,7 @@ extern "C" int ne_paged_attention_plan(const int32_t* block_tables, int32_t bloc
   p.max_ctx = max_ctx_len;
   p.plan_w = L.plan_w;
   p.plan_grid = L.plan_grid;
+  p.plan_whole = whole_plan_ks(num_seqs, max_ctx_len, split_len, L.mtiles) > 0;
   char* ws = (char*)workspace;
   p.error_flag = (uint32_t*)(ws + L.error_off);
   p.plan = (int32_t*)(ws + L.plan_off);
@@ -1685,6 +1700,8 @@ extern "C" int ne_paged_verify_attention_planned(
                          ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0,
                      "the planned path serves int8 caches with 8 KV heads, 2-byte 4-byte-aligned "
                      "scales and at most 32 query rows per KV head");
+  // the same choice as ne_paged_attention_plan made from the same metadata
+  p.plan_whole = whole_plan_ks(num_seqs, max_ctx_len, split_len, p.mtiles) > 0;
   return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, true>(p, (hipStream_t)stream)
                                       : launch_attention_dma<NE_DTYPE_FP16, true>(p, (hipStream_t)stream);
 }

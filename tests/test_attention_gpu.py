@@ -137,7 +137,9 @@ def test_workspace_error_flag_reports_context_past_max(device):
     ([300, 1500, 2100, 40, 9], [9, 9, 7, 9, 9], 0, torch.float16),  # k = 8: two row tiles per KV head
 ])
 def test_planned_matches_unplanned(device, ctx, q_lens, split_len, scale_dtype):
-    """The per-step plan gives the same work items as the in-kernel plan: identical bits."""
+    """The per-step plan gives the same work items as the in-kernel plan: identical bits.
+    Where the plan makes whole-sequence items instead (at most 64 tiles of context, no
+    fixed split, one row tile, few sequences), the values agree up to the fp32 order."""
     num_blocks = max(64, sum((c + 15) // 16 for c in ctx) + 8)
     kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, "int8", scale_dtype, seed=3)
     tables, ctx_t, qs, ql, rows = make_batch(ctx, q_lens, num_blocks, 16, seed=4)
@@ -154,7 +156,12 @@ def test_planned_matches_unplanned(device, ctx, q_lens, split_len, scale_dtype):
                                        split_len=split_len, planned=True)
     torch.cuda.synchronize()
     idx = real_rows(qs, ql)
-    assert torch.equal(a.cpu()[idx], b.cpu()[idx])
+    whole = split_len == 0 and max(q_lens) * HQ // HKV <= 16 and (max(ctx) + 15) // 16 <= 64
+    if whole:
+        diff = float((a.cpu()[idx].float() - b.cpu()[idx].float()).abs().max())
+        assert diff <= 2e-2 * float(a.cpu()[idx].float().abs().max())
+    else:
+        assert torch.equal(a.cpu()[idx], b.cpu()[idx])
     assert ws.error_flag() == 0
     ref = paged_attention_reference(q, kc, vc, ks, vs, tables, 16, ctx_t, qs, ql, model_dtype=scale_dtype)
     assert rel_err(b.cpu()[idx], ref[idx]) < TOL
@@ -225,15 +232,17 @@ def test_k8_long_contexts_with_a_shared_prefix(device, split_len):
     assert rel_err(out.cpu(), ref) < TOL
 
 
-@pytest.mark.parametrize("num_seqs", [64, 100, 200])
-def test_head_split_planned_path_for_short_contexts(device, num_seqs):
-    """Contexts of at most 256 keys (the verify step's): the planned kernel gives 4 (64
-    sequences) or 2 (100) work-groups per sequence, each over 2 or 4 KV heads, a head's
-    waves taking consecutive parts of its tiles and merging through LDS; 200 sequences
-    keep one work-group each.  Contexts of 1..17 keys leave some waves without tiles."""
-    rng = np.random.default_rng(num_seqs)
-    ctx = [int(c) for c in rng.integers(1, 257, size=num_seqs)]
-    ctx[:6] = [1, 2, 15, 16, 17, 256]
+@pytest.mark.parametrize("num_seqs,max_ctx", [(64, 256), (100, 256), (200, 256), (64, 1024), (128, 1024),
+                                              (64, 1025)])
+def test_head_split_planned_path(device, num_seqs, max_ctx):
+    """Contexts of at most 1024 keys: the planned kernel gives every sequence one item
+    served by 4 (64 sequences) or 2 (100, 128) work-groups, each over 2 or 4 KV heads, a
+    head's waves taking consecutive parts of its tiles and merging through LDS; 200
+    sequences, or a 1025-key context, keep the split plan.  Contexts of 1..17 keys leave
+    some waves without tiles."""
+    rng = np.random.default_rng(num_seqs + max_ctx)
+    ctx = [int(c) for c in rng.integers(1, max_ctx + 1, size=num_seqs)]
+    ctx[:6] = [1, 2, 15, 16, 17, max_ctx]
     q_lens = [int(min(c, 5)) for c in ctx]
     num_blocks = sum((c + 15) // 16 for c in ctx) + 8
     kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, "int8", torch.bfloat16, seed=11)
