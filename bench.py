@@ -374,7 +374,8 @@ def run_attention_kernel_only(torch, kind: str, layers: int, reps: int = 3):
 def run_attention_roofline(torch, reps: int = 5):
     """Average time per attention call over `reps` passes of the 28 pools, from HIP events
     recorded on the launching stream around each entry point.  A pass is what a verify step
-    does: one plan (ne_paged_attention_plan) and 28 planned calls (main + merge kernels); the
+    does: one plan (ne_paged_attention_plan) and 28 planned calls (the main kernel, plus the
+    merge kernel when the plan splits sequences); the
     plan's time is counted and spread over the pass's calls.  The in-kernel-plan entry point
     (ne_paged_verify_attention) is timed the same way for comparison."""
     from nanoengine_amd import _native
@@ -405,7 +406,8 @@ def run_attention_roofline(torch, reps: int = 5):
     avg_ms = (plan_ms + sum(calls)) / len(calls)
     unplanned = timers["ne_paged_verify_attention"].durations_ms()
     achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
-    return {"kernel": "paged_attention_dma_kernel<fp16 scales, planned> + attention_plan_merge_kernel",
+    return {"kernel": "paged_attention_dma_kernel<fp16 scales, planned> (whole-sequence items, 4 work-groups "
+                      "per sequence, no merge kernel at this shape)",
             "workload": "int8 KV, 64 seqs, ctx U{128..1024} seed 1, q=5, fp16 scales, 28 pools",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
