@@ -118,6 +118,14 @@ class VerifyRunner:
         self.h_num_drafts = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         self.h_out = torch.zeros(max_seqs, self.R, dtype=torch.int32, **pin)
         self.h_num_out = torch.zeros(max_seqs, dtype=torch.int32, **pin)
+        # numpy views of the pinned buffers: the per-step host work indexes them per
+        # sequence, which costs ~1 us through torch and ~0.1 us through numpy
+        self.np_tables = self.h_tables.numpy()
+        self.np_num_tokens = self.h_num_tokens.numpy()
+        self.np_steps = self.h_steps.numpy()
+        self.np_num_drafts = self.h_num_drafts.numpy()
+        self.np_out = self.h_out.numpy()
+        self.np_num_out = self.h_num_out.numpy()
         self.slots: list[Sequence | None] = [None] * max_seqs
         self.temperature: float | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
@@ -307,13 +315,13 @@ class VerifyRunner:
         active = self.active_slots
         if not active:
             return {}
-        for s in range(self.max_seqs):
-            seq = self.slots[s]
-            if seq is None:
-                self.h_num_tokens[s] = 0
-                continue
-            self.h_num_tokens[s] = num_guesses(seq.sampling_params, seq.num_generated_tokens, self.k)
-            self.h_steps[s] = seq.sampling_generator.step
+        slots = self.slots
+        np_num_tokens, np_steps = self.np_num_tokens, self.np_steps
+        np_num_tokens[:] = 0
+        for s in active:
+            seq = slots[s]
+            np_num_tokens[s] = num_guesses(seq.sampling_params, seq.num_generated_tokens, self.k)
+            np_steps[s] = seq.sampling_generator.step
         self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
         self.steps.copy_(self.h_steps, non_blocking=True)
         kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
@@ -321,17 +329,18 @@ class VerifyRunner:
         self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
         tables_changed = False
+        np_num_drafts, allocator, bs = self.np_num_drafts, self.allocator, self.block_size
         for s in active:
-            seq = self.slots[s]
-            g = int(self.h_num_drafts[s])
+            seq = slots[s]
+            need = seq.num_tokens + int(np_num_drafts[s])
             # rows write positions L-1 .. L-1+g; every block below the allocator's
             # bound may be read by other requests and must never be written
-            if seq.num_tokens - 1 < self.allocator.first_writable_position(seq):
+            if seq.num_tokens - 1 < allocator.first_writable_position(seq):
                 raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
-            owned = self.allocator.num_blocks_of(seq)
-            added = self.allocator.reserve(seq, seq.num_tokens + g)
-            if added:
-                self.h_tables[s, owned : owned + len(added)] = torch.tensor(added, dtype=torch.int32)
+            owned = allocator.num_blocks_of(seq)
+            if need > owned * bs:  # (paged_allocator.py:50-55 adds blocks only then)
+                added = allocator.reserve(seq, need)
+                self.np_tables[s, owned : owned + len(added)] = added
                 tables_changed = True
         if tables_changed:
             self.block_tables.copy_(self.h_tables, non_blocking=True)
@@ -351,14 +360,15 @@ class VerifyRunner:
                 for s in active
             })
         results = {}
+        np_out, np_num_out = self.np_out, self.np_num_out
         for s in active:
-            seq = self.slots[s]
-            n = int(self.h_num_out[s])
-            g = int(self.h_num_drafts[s])
+            seq = slots[s]
+            n = int(np_num_out[s])
+            g = int(np_num_drafts[s])
             kept = n - 1
             cached = seq.num_tokens + kept  # L-1 .. L-1+kept now hold the kept tokens
             seq.sampling_generator.step += 1
-            results[s] = self._emit(s, seq, self.h_out[s, :n].tolist(), g, kept, cached)
+            results[s] = self._emit(s, seq, np_out[s, :n].tolist(), g, kept, cached)
         return results
 
     def _emit(self, slot: int, seq: Sequence, tokens: list[int], g: int, kept: int,
