@@ -379,15 +379,21 @@ class VerifyRunner:
         verified tokens; it is recorded, clipped to the tokens actually kept when a stop
         ends the sequence early, and reported to the allocator before a finished
         sequence is released, so its verified blocks stay reusable."""
-        emitted = []
+        params = seq.sampling_params
         reason = None
-        for token in tokens:
-            seq.token_ids.append(token)
-            emitted.append(token)
-            reason = find_finish_reason(token, seq.num_generated_tokens, seq.sampling_params,
-                                        self.stop_token_ids)
-            if reason is not None:
-                break
+        stops = () if params.ignore_eos else self.stop_token_ids
+        if seq.num_generated_tokens + len(tokens) < params.max_new_tokens and not any(t in stops for t in tokens):
+            # no token can end the sequence: the checks below would all pass
+            seq.token_ids.extend(tokens)
+            emitted = tokens
+        else:
+            emitted = []
+            for token in tokens:
+                seq.token_ids.append(token)
+                emitted.append(token)
+                reason = find_finish_reason(token, seq.num_generated_tokens, params, self.stop_token_ids)
+                if reason is not None:
+                    break
         if cached is not None:
             seq.num_cached_tokens = min(cached, seq.num_tokens)
             self.allocator.on_tokens_cached(seq)
