@@ -40,7 +40,6 @@ from nanoengine_amd import kernels
 from nanoengine_amd.interface import (
     GREEDY_TEMPERATURE,
     find_finish_reason,
-    num_guesses,
 )
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
 from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
@@ -73,6 +72,8 @@ class VerifyRunner:
         self.model = model
         self.pool = pool
         self.allocator = allocator
+        # the shared-block guard only has something to check with a prefix cache
+        self._guard_shared = type(allocator).first_writable_position is not PagedSlotAllocator.first_writable_position
         self.device = model.device
         self.k = num_speculative_tokens
         self.R = self.k + 1
@@ -126,6 +127,14 @@ class VerifyRunner:
         self.np_num_drafts = self.h_num_drafts.numpy()
         self.np_out = self.h_out.numpy()
         self.np_num_out = self.h_num_out.numpy()
+        # per-slot host state mirrored from the Sequence objects, so that a step's counts
+        # and block checks are array operations: active, length L, generated tokens,
+        # length limit, blocks owned
+        self.np_active = np.zeros(max_seqs, dtype=bool)
+        self.np_len = np.zeros(max_seqs, dtype=np.int64)
+        self.np_gen = np.zeros(max_seqs, dtype=np.int64)
+        self.np_max_new = np.zeros(max_seqs, dtype=np.int64)
+        self.np_owned = np.zeros(max_seqs, dtype=np.int64)
         self.slots: list[Sequence | None] = [None] * max_seqs
         self.temperature: float | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
@@ -223,7 +232,13 @@ class VerifyRunner:
             seq.num_cached_tokens = seq.num_tokens
             self.allocator.on_tokens_cached(seq)  # the whole prompt is verified and cached
             seq.sampling_generator.step += 1
+            self.np_active[slot] = True
+            self.np_max_new[slot] = seq.sampling_params.max_new_tokens
+            self.np_owned[slot] = self.allocator.num_blocks_of(seq)
+            self.np_steps[slot] = seq.sampling_generator.step
             results[slot] = self._emit(slot, seq, [int(self.h_out[s0 + i, 0])], 0, 0)
+            self.np_len[slot] = seq.num_tokens
+            self.np_gen[slot] = seq.num_generated_tokens
         return results
 
     def _prefill_forward(self, pieces: list[tuple[int, Sequence, int, int, int]]) -> None:
@@ -316,32 +331,32 @@ class VerifyRunner:
         if not active:
             return {}
         slots = self.slots
-        np_num_tokens, np_steps = self.np_num_tokens, self.np_steps
-        np_num_tokens[:] = 0
-        for s in active:
-            seq = slots[s]
-            np_num_tokens[s] = num_guesses(seq.sampling_params, seq.num_generated_tokens, self.k)
-            np_steps[s] = seq.sampling_generator.step
+        act = self.np_active.copy()
+        # num_guesses for every slot at once (speculative_generator.py:71-72)
+        counts = np.clip(np.minimum(self.k, self.np_max_new - self.np_gen - 1), 0, None)
+        self.np_num_tokens[:] = np.where(act, counts, 0)
         self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
         self.steps.copy_(self.h_steps, non_blocking=True)
         kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
                               drafts=self.drafts, num_drafts=self.num_drafts)
         self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
-        tables_changed = False
         np_num_drafts, allocator, bs = self.np_num_drafts, self.allocator, self.block_size
-        for s in active:
-            seq = slots[s]
-            need = seq.num_tokens + int(np_num_drafts[s])
+        if self._guard_shared:
             # rows write positions L-1 .. L-1+g; every block below the allocator's
             # bound may be read by other requests and must never be written
-            if seq.num_tokens - 1 < allocator.first_writable_position(seq):
-                raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
-            owned = allocator.num_blocks_of(seq)
-            if need > owned * bs:  # (paged_allocator.py:50-55 adds blocks only then)
-                added = allocator.reserve(seq, need)
-                self.np_tables[s, owned : owned + len(added)] = added
-                tables_changed = True
+            for s in active:
+                seq = slots[s]
+                if seq.num_tokens - 1 < allocator.first_writable_position(seq):
+                    raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
+        need = self.np_len + np_num_drafts
+        grow = np.nonzero(act & (need > self.np_owned * bs))[0]  # (paged_allocator.py:50-55)
+        for s in grow.tolist():
+            owned = int(self.np_owned[s])
+            added = allocator.reserve(slots[s], int(need[s]))
+            self.np_tables[s, owned : owned + len(added)] = added
+            self.np_owned[s] = owned + len(added)
+        tables_changed = len(grow) > 0
         if tables_changed:
             self.block_tables.copy_(self.h_tables, non_blocking=True)
         self._run_device_step()
@@ -361,6 +376,11 @@ class VerifyRunner:
             })
         results = {}
         np_out, np_num_out = self.np_out, self.np_num_out
+        # the mirrors advance by the emitted counts (a slot that finishes is released)
+        emitted = np.where(act, np_num_out, 0)
+        self.np_len += emitted
+        self.np_gen += emitted
+        self.np_steps[act] += 1
         for s in active:
             seq = slots[s]
             n = int(np_num_out[s])
@@ -407,6 +427,8 @@ class VerifyRunner:
             return
         self.allocator.free(seq)
         self.slots[slot] = None
+        self.np_active[slot] = False
+        self.np_owned[slot] = 0
         self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
         self.h_tables[slot].zero_()
         if not self.active_slots:
