@@ -1,14 +1,17 @@
 // n-gram prompt-lookup drafting on the device token history (gfx950).
 //
 // Restates NgramProposer.propose (ne/engine/speculative/proposers.py:44-57) for a
-// batch: one 256-thread work-group per sequence.  For n = max_ngram..min_ngram
-// (skipping n >= len) the work-group tests start positions from len-n-1 downward,
-// 1024 at a time (4 per thread), and stops after the first chunk holding a start
-// whose window equals the last n tokens, keeping the largest such start -- the
-// reference scans starts from len-n-1 downward and returns the first match, which
-// is the same window.  A recent match (the common case in long histories) costs one
-// chunk instead of a scan of the whole history.  The guesses are the tokens that
-// followed it, clipped to the history, so they are never empty.
+// batch: one 256-thread work-group per sequence.  For each n (max_ngram down to
+// min_ngram, skipping n >= len) the reference scans starts from len-n-1 downward and
+// returns the first window equal to the last n tokens.  A window of length n starting
+// at s ends at e = s + n - 1 <= len - 2, and it matches exactly when the tokens ending
+// at e and those ending at len - 1 agree on their last n; so one pass over end
+// positions e = len - 2, len - 3, ..., computing that agreement length c(e) (up to
+// max_ngram), finds for every n the largest matching e at once.  The pass runs 1024
+// ends at a time (4 per thread) and stops after the first chunk holding a max_ngram
+// match, which is the common case in long histories; without one, the same pass has
+// already found the smaller n's answers.  The guesses are the tokens that followed
+// the window, clipped to the history, so they are never empty.
 #include "ne_common.hpp"
 
 namespace ne {
@@ -24,55 +27,86 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
                                                     const int32_t* num_tokens, int max_ngram,
                                                     int min_ngram, int max_drafts, int32_t* drafts,
                                                     int32_t* num_drafts) {
-  __shared__ int s_best[256 / kWave];
+  __shared__ int s_best[kMaxNgram][256 / kWave];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int32_t* h = history + (int64_t)b * stride;
   const int len = history_len[b];
   const int want = min(num_tokens[b], max_drafts);
-  if (want <= 0) {
+  const int nmax = min(max_ngram, len - 1);  // n < len
+  if (want <= 0 || nmax < min_ngram) {
     if (tid == 0) num_drafts[b] = 0;
     return;
   }
-  for (int n = max_ngram; n >= min_ngram; --n) {
-    if (len <= n) continue;
-    int suffix[kMaxNgram];
+  int suffix[kMaxNgram];  // the history read backwards from its last token
 #pragma unroll
-    for (int i = 0; i < kMaxNgram; ++i) suffix[i] = (i < n) ? h[len - n + i] : 0;
-    int top = -1;
-    for (int hi = len - n - 1; hi >= 0 && top < 0; hi -= kScanChunk) {
-      // thread tid tests starts hi - tid, hi - tid - 256, ...: its first hit is its
-      // largest, and the owner of the chunk's largest hit has no larger one
-      int best = -1;
+  for (int i = 0; i < kMaxNgram; ++i) suffix[i] = (i < nmax) ? h[len - 1 - i] : 0;
+  int found[kMaxNgram];  // found[n - 1]: the largest end e of an n-window match so far
 #pragma unroll
-      for (int j = 0; j < kScanPerThread; ++j) {
-        const int start = hi - j * 256 - tid;
-        if (start >= 0 && best < 0) {
-          bool eq = true;
+  for (int i = 0; i < kMaxNgram; ++i) found[i] = -1;
+  for (int hi = len - 2; hi >= 0; hi -= kScanChunk) {
+    // thread tid tests ends hi - tid, hi - tid - 256, ...: its first hit for each n is
+    // its largest, and the owner of the chunk's largest hit has no larger one
+    int best[kMaxNgram];
 #pragma unroll
-          for (int i = 0; i < kMaxNgram; ++i)
-            if (i < n) eq = eq && (h[start + i] == suffix[i]);
-          if (eq) best = start;
+    for (int i = 0; i < kMaxNgram; ++i) best[i] = -1;
+#pragma unroll
+    for (int j = 0; j < kScanPerThread; ++j) {
+      const int e = hi - j * 256 - tid;
+      if (e >= 0) {
+        int c = 0;  // tokens ending at e that equal those ending at len - 1
+        bool same = true;
+#pragma unroll
+        for (int i = 0; i < kMaxNgram; ++i) {
+          if (same && i < nmax && e - i >= 0 && h[e - i] == suffix[i]) {
+            ++c;
+          } else {
+            same = false;
+          }
         }
+#pragma unroll
+        for (int i = 0; i < kMaxNgram; ++i)
+          if (i < c && best[i] < 0) best[i] = e;
       }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) best = max(best, __shfl_xor(best, o));
-      if (tid % kWave == 0) s_best[tid / kWave] = best;
-      __syncthreads();
-      top = s_best[0];
-#pragma unroll
-      for (int w = 1; w < 256 / kWave; ++w) top = max(top, s_best[w]);
-      __syncthreads();
     }
-    if (top >= 0) {
-      const int follow = top + n;
-      const int count = min(want, len - follow);
-      for (int i = tid; i < count; i += 256) drafts[(int64_t)b * max_drafts + i] = h[follow + i];
-      if (tid == 0) num_drafts[b] = count;
-      return;
+#pragma unroll
+    for (int i = 0; i < kMaxNgram; ++i) {
+      if (i + 1 >= min_ngram && i < nmax) {  // uniform
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) best[i] = max(best[i], __shfl_xor(best[i], o));
+        if (tid % kWave == 0) s_best[i][tid / kWave] = best[i];
+      }
     }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMaxNgram; ++i) {
+      if (i + 1 >= min_ngram && i < nmax) {
+        int top = s_best[i][0];
+#pragma unroll
+        for (int w = 1; w < 256 / kWave; ++w) top = max(top, s_best[i][w]);
+        if (found[i] < 0) found[i] = top;
+      }
+    }
+    __syncthreads();
+    bool done = false;
+#pragma unroll
+    for (int i = 0; i < kMaxNgram; ++i)
+      if (i == nmax - 1) done = found[i] >= 0;
+    if (done) break;  // uniform: the largest n has its answer
   }
-  if (tid == 0) num_drafts[b] = 0;
+  // the largest n with a match
+  int e = -1;
+#pragma unroll
+  for (int i = 0; i < kMaxNgram; ++i)
+    if (i + 1 >= min_ngram && i < nmax && found[i] >= 0) e = found[i];
+  if (e < 0) {
+    if (tid == 0) num_drafts[b] = 0;
+    return;
+  }
+  const int follow = e + 1;
+  const int count = min(want, len - follow);
+  for (int i = tid; i < count; i += 256) drafts[(int64_t)b * max_drafts + i] = h[follow + i];
+  if (tid == 0) num_drafts[b] = count;
 }
 
 }  // namespace
