@@ -45,6 +45,8 @@
 // The MFMA contraction index is permuted consistently on both operands (dim
 // 32g + 8c + e for slot 8g+e of chunk c; key 16(e/4) + 4g + e%4 for slot 8g+e),
 // which is legal because a dot product does not depend on summation order.
+#include <type_traits>
+
 #include "ne_common.hpp"
 
 namespace ne {
@@ -421,29 +423,106 @@ __device__ __forceinline__ void compute_iter(const AttnParams& p, const IterRegs
   }
 }
 
-// compute_iter for an int8 cache with MT row tiles of 16 (MT * 16 query rows per KV
-// head) in one wave: each K chunk and each V column block is converted once and
-// feeds every row tile's MFMAs, so with k = 8 drafts (18 rows per KV head) K/V are
-// read and converted once instead of once per row tile.
-template <int MT>
-__device__ __forceinline__ void compute_iter_mt(const AttnParams& p, const IterRegs<true>& R,
-                                                const QFrag<true> (&qf)[MT], float* s_sc, int kb,
-                                                const int (&kend_row)[MT], int lane, float (&m)[MT],
-                                                float (&l)[MT], floatx4 (&o)[MT][8]) {
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Q of one row tile for the DMA kernel's int8 product: q ~= s * (256 * hi + lo) with
+// s = absmax(row) / 32512, hi in [-127, 127] and lo in [-128, 127].  The scores then run
+// on the int8 MFMA straight from the cache's codes (no conversion of K), and the
+// two-plane code keeps 15 bits of each row: the error, at most absmax / 65024 per
+// element, is far below the bf16 rounding of Q itself.
+struct QFragI8 {
+  u32x4 hi[2];  // chunk c: 16 codes of dims 32g + 16c + 0..15 of this lane's row
+  u32x4 lo[2];
+  float c;      // qk_scale * s for this lane's row (NaN when the row is not finite)
+};
+
+constexpr float kQCodeMax = 32512.f;  // 127 * 256: hi = round(code / 256) stays in int8
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// Maximum of v over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lanes of a row), by
+// the gfx950 row and half-wave swaps (no LDS round trip).
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(b[0], b[1]);
+}
+
+// raw: this lane's 32 bf16 dims of its row (dims 32g + 8c + 2i, +1 in raw[c][i]).
+// The code of x is round(x / s) for s = absmax / 32512, taken as the low bits of
+// fma(x, 1 / s, 1.5 * 2^23 + 128) (exact integer rounding below 2^22): byte 1 of those
+// bits is hi = (code + 128) >> 8 and byte 0, with its top bit flipped, is the low byte
+// of lo = code - 256 hi.
+__device__ __forceinline__ void quantize_q_row(const u32x4 (&raw)[4], bool valid, float qk_scale,
+                                               QFragI8& f) {
+  uint32_t w[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[4 * c + i] = valid ? raw[c][i] : 0u;
+  }
+  // row absmax from the bf16 magnitudes (packed 16-bit maxima); a magnitude from
+  // 0x7F80 up is an infinity or NaN
+  u16x2 mh = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    mh = __builtin_elementwise_max(mh, __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu));
+  const uint32_t mag = row_max_u32(max((uint32_t)mh[0], (uint32_t)mh[1]));
+  const float amax = __uint_as_float(mag << 16);
+  const float s = amax * (1.f / kQCodeMax);
+  const float inv = mag != 0u ? __builtin_amdgcn_rcpf(s) : 0.f;
+  constexpr float kMagic = 12583040.f;  // 1.5 * 2^23 + 128
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      // dims 16c + 4d + b: bf16 pairs w[8c + 2d] (b = 0, 1) and w[8c + 2d + 1] (b = 2, 3)
+      const uint32_t w0 = w[8 * c + 2 * d], w1 = w[8 * c + 2 * d + 1];
+      const uint32_t g0 = __float_as_uint(__builtin_fmaf(__uint_as_float(w0 << 16), inv, kMagic));
+      const uint32_t g1 = __float_as_uint(__builtin_fmaf(__uint_as_float(w0 & 0xFFFF0000u), inv, kMagic));
+      const uint32_t g2 = __float_as_uint(__builtin_fmaf(__uint_as_float(w1 << 16), inv, kMagic));
+      const uint32_t g3 = __float_as_uint(__builtin_fmaf(__uint_as_float(w1 & 0xFFFF0000u), inv, kMagic));
+      const uint32_t p01 = __builtin_amdgcn_perm(g1, g0, 0x04000501u);  // hi0 hi1 lo0 lo1
+      const uint32_t p23 = __builtin_amdgcn_perm(g3, g2, 0x04000501u);  // hi2 hi3 lo2 lo3
+      f.hi[c][d] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+      f.lo[c][d] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+    }
+  }
+  f.c = mag < 0x7F80u ? qk_scale * s : __builtin_nanf("");
+}
+
+// One 32-key iteration of the DMA kernel over MT row tiles of 16 query rows:
+// S^T = K . Q^T on the int8 MFMA (K codes as they sit in LDS, Q in two int8 planes),
+// the lazy online softmax, and O^T += V^T . P^T on the fp16 MFMA with the value
+// scales folded into P.  Each K chunk and V column block feeds every row tile.
+// MASK = false: every key of the iteration is visible to every row (no causal or
+// context-end masking needed).
+template <int MT, bool MASK>
+__device__ __forceinline__ void compute_iter_q8(const IterRegs<true>& R, const QFragI8 (&qf)[MT],
+                                                float* s_sc, int kb, const int (&kend_row)[MT],
+                                                int lane, float (&m)[MT], float (&l)[MT],
+                                                floatx4 (&o)[MT][8]) {
   const int g = lane >> 4;
-  // ---- S^T = K . Q^T per row tile: two 16x16 tiles (keys x rows) each ----
-  floatx4 s[MT][2];
+  // ---- integer scores: 256 * (K . Qhi) + K . Qlo, exact in int32 ----
+  i32x4 shi[MT][2], slo[MT][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) s[mt][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) {
+      shi[mt][t] = i32x4{0, 0, 0, 0};
+      slo[mt][t] = i32x4{0, 0, 0, 0};
+    }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4 a = i8x8_f16x8(R.k[t][c >> 1][2 * (c & 1)], R.k[t][c >> 1][2 * (c & 1) + 1]);
+    for (int c = 0; c < 2; ++c) {
+      const i32x4 a = __builtin_bit_cast(i32x4, R.k[t][c]);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        s[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf[mt].q[c],
-                                                          s[mt][t], 0, 0, 0);
+      for (int mt = 0; mt < MT; ++mt) {
+        shi[mt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, __builtin_bit_cast(i32x4, qf[mt].hi[c]),
+                                                           shi[mt][t], 0, 0, 0);
+        slo[mt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, __builtin_bit_cast(i32x4, qf[mt].lo[c]),
+                                                           slo[mt][t], 0, 0, 0);
+      }
     }
   }
   // ---- per-key scale factors (lanes 0..31 key scales, 32..63 value scales) ----
@@ -457,23 +536,25 @@ __device__ __forceinline__ void compute_iter_mt(const AttnParams& p, const IterR
   const floatx4 vf1 = *(const floatx4*)&s_sc[48 + 4 * g];
   const float vmax = fmaxf(fmaxf(fmaxf(vf0[0], vf0[1]), fmaxf(vf0[2], vf0[3])),
                            fmaxf(fmaxf(vf1[0], vf1[1]), fmaxf(vf1[2], vf1[3])));
-  // ---- masked scores, lazy online softmax and P per row tile ----
+  // ---- scores up to the row factor c (score = c * sc), lazy online softmax, P ----
   f16x8 pb[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    const float c = qf[mt].c;
     float sc[8];
     float mx = kNegBig;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = kb + 16 * t + 4 * g + i;
-        float v = s[mt][t][i] * p.qk_scale * (t ? kf1[i] : kf0[i]);
-        v = (key < kend_row[mt]) ? v : kNegBig;
+        const int si = (shi[mt][t][i] << 8) + slo[mt][t][i];
+        float v = (float)si * (t ? kf1[i] : kf0[i]);
+        if constexpr (MASK) v = (kb + 16 * t + 4 * g + i < kend_row[mt]) ? v : kNegBig;
         sc[4 * t + i] = v;
         mx = fmaxf(mx, v);
       }
     }
+    mx *= c;
     const bool grow = (mx > m[mt] + kLazyLog2) || (vmax > kLazyMaxVScale && mx > m[mt]);
     if (__ballot(grow)) {
       mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -489,8 +570,8 @@ __device__ __forceinline__ void compute_iter_mt(const AttnParams& p, const IterR
     float psum = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int key = kb + 16 * (e >> 2) + 4 * g + (e & 3);
-      pr[e] = (key < kend_row[mt]) ? __builtin_amdgcn_exp2f(sc[e] - m[mt]) : 0.f;
+      pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c, -m[mt]));
+      if constexpr (MASK) pr[e] = (kb + 16 * (e >> 2) + 4 * g + (e & 3) < kend_row[mt]) ? pr[e] : 0.f;
       psum += pr[e];
     }
     l[mt] += psum;
@@ -714,11 +795,13 @@ __global__ __launch_bounds__(kHeadWaves * KG * kWave) void paged_attention_kerne
 }
 
 // ---- DMA-fed variant (int8 cache, 8 KV heads, 2-byte scales) -----------------
-// Same work item and arithmetic as paged_attention_kernel, but each wave (one KV
-// head) streams its head's rows of every 16-key tile, plus all heads' scales of
-// the tile, from HBM straight into its own LDS ring with global_load_lds: no
-// registers hold data in flight, so every wave keeps kDmaRing tiles (18 KB) on
-// the way while it computes, and the loop needs no block barrier.
+// Same work item as paged_attention_kernel, but each wave (one KV head) streams its
+// head's rows of every 16-key tile, plus all heads' scales of the tile, from HBM
+// straight into its own LDS ring with global_load_lds: no registers hold data in
+// flight, so every wave keeps kDmaRing tiles (18 KB) on the way while it computes,
+// and the loop needs no block barrier.  The scores run on the int8 MFMA with the K
+// codes as they sit in LDS and Q in two int8 planes (quantize_q_row); P V stays on
+// the fp16 MFMA.
 constexpr int kDmaRing = 4;                          // 16-key tiles in flight per wave
 constexpr int kRowBytes = kHeadDim;                  // one int8 head row
 constexpr int kTileRows = kTileKeys * kRowBytes;     // 2 KB: one head's K (or V) rows of a tile
@@ -728,9 +811,28 @@ constexpr int kDmaPerTile = 6;                       // 2 K + 2 V (1 KB each) + 
 constexpr int kPlanInts = 32;                        // LDS ints of the work plan
 constexpr int kMaxRowTiles = 2;                      // row tiles per KV head in one wave
 constexpr int kPartRows = kRows * kMaxRowTiles;      // rows per (work-group, KV head) partial
-constexpr int kDmaLds = kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4 + kHeadWaves * kWave * 4 +
-                        kPlanInts * 4;
 constexpr int kPlanMaxSeqs = 2 * kHeadWaves * kWave;  // two sequences per thread
+
+// Work-group shape of the DMA kernel by KS, the waves per KV head: waves per
+// work-group, KV heads per work-group, work-groups per work item, ring tiles per wave
+// and the dynamic LDS layout (rings, slot list, per-wave scales, plan).
+template <int KS>
+struct DmaShape {
+  static constexpr int waves = kHeadWaves;
+  static constexpr int heads = waves / KS;               // KV heads per work-group
+  static constexpr int groups = kHeadWaves / heads;      // work-groups per work item
+  static constexpr int ring = kDmaRing;                  // tiles in flight per wave
+  // tiles issued before the first iteration; the rest of the ring follows once the
+  // first two have landed, which keeps the launch's opening burst of copies (and the
+  // queueing delay every wave's first tiles see behind it) at half the ring
+  static constexpr int first = 2;
+  static constexpr int slot_off = waves * ring * kDmaSlot;
+  static constexpr int sc_off = slot_off + kPlanMaxTiles * 4;
+  static constexpr int plan_off = sc_off + waves * kWave * 4;
+  static constexpr int lds = plan_off + kPlanInts * 4;
+  static_assert(waves % KS == 0 && kHeadWaves % heads == 0, "whole heads per work-group");
+  static_assert(lds <= 160 * 1024, "LDS of one CU");
+};
 constexpr int kPlanMinTiles = 16;                     // contexts up to 256 keys are never split
 constexpr int kPlanFloorTiles = 4;                    // no split shorter than 64 keys
 constexpr int kPlanCUs = 256;                         // work-groups the plan aims to fill
@@ -953,32 +1055,52 @@ __device__ __forceinline__ void dma_wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
 
-// Copy tile `t` (clamped to the split's last tile) of head `head` into ring slot
-// `dst`.  K/V rows land as [16 keys][128 B] with 16-byte chunk c of key k stored
-// at chunk position c ^ (k & 7), which makes the fragment reads conflict-free.
+// Per-lane byte offsets of a tile copy: K/V rows land as [16 keys][128 B] with 16-byte
+// chunk c of key k stored at chunk position c ^ (k & 7), which makes the fragment reads
+// conflict-free.  The offsets are 32-bit and the tile's base is wave-uniform, so every
+// copy is a scalar base plus a fixed lane offset (no 64-bit address arithmetic).
+struct DmaLane {
+  uint32_t kv[2];  // copy j: key 8j + lane / 8, chunk (lane % 8) ^ (key % 8)
+  uint32_t sc;     // the lane's dword of a tile's 256 scale bytes
+};
+
+__device__ __forceinline__ DmaLane dma_lane(int lane) {
+  constexpr uint32_t slot_bytes = kHeadWaves * kRowBytes;
+  DmaLane d;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int key = 8 * j + (lane >> 3);
+    const int chunk = (lane & 7) ^ (key & 7);
+    d.kv[j] = (uint32_t)key * slot_bytes + (uint32_t)chunk * 16u;
+  }
+  d.sc = (uint32_t)lane * 4u;
+  return d;
+}
+
+// Copy tile `t` (clamped to the split's last tile) of head `head` into ring slot `dst`.
 __device__ __forceinline__ void dma_tile(const AttnParams& p, const int* s_slot, int n_tiles, int t,
-                                         int head, int lane, char* dst) {
+                                         int head, const DmaLane& dl, char* dst) {
   const int ti = min(t, n_tiles - 1);
   const int64_t slot0 = __builtin_amdgcn_readfirstlane(s_slot[ti]);
   const int64_t slot_bytes = (int64_t)kHeadWaves * kRowBytes;
   const char* kbase = (const char*)p.k_cache + slot0 * slot_bytes + head * kRowBytes;
   const char* vbase = (const char*)p.v_cache + slot0 * slot_bytes + head * kRowBytes;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int key = 8 * j + (lane >> 3);
-    const int chunk = (lane & 7) ^ (key & 7);
-    const int64_t off = key * slot_bytes + chunk * 16;
-    lds_dma(kbase + off, dst + j * 1024, 16);
-    lds_dma(vbase + off, dst + kTileRows + j * 1024, 16);
-  }
+  // the offsets pass through an empty asm so that each address is formed here from the
+  // 32-bit value (scalar base + lane offset) rather than from a hoisted 64-bit copy
+  uint32_t kv0 = dl.kv[0], kv1 = dl.kv[1], sc = dl.sc;
+  __asm__("" : "+v"(kv0), "+v"(kv1), "+v"(sc));
+  lds_dma(kbase + kv0, dst, 16);
+  lds_dma(vbase + kv0, dst + kTileRows, 16);
+  lds_dma(kbase + kv1, dst + 1024, 16);
+  lds_dma(vbase + kv1, dst + kTileRows + 1024, 16);
   // scales [slot][8 heads] of 2 bytes: the tile's 16 slots are 256 contiguous bytes
-  lds_dma((const char*)p.k_scale + slot0 * (kHeadWaves * 2) + lane * 4, dst + 2 * kTileRows, 4);
-  lds_dma((const char*)p.v_scale + slot0 * (kHeadWaves * 2) + lane * 4,
-          dst + 2 * kTileRows + kScaleBytes, 4);
+  lds_dma((const char*)p.k_scale + slot0 * (kHeadWaves * 2) + sc, dst + 2 * kTileRows, 4);
+  lds_dma((const char*)p.v_scale + slot0 * (kHeadWaves * 2) + sc, dst + 2 * kTileRows + kScaleBytes, 4);
 }
 
 // Registers of one 32-key iteration from two ring slots (the layout load_iter gives).
-template <int SDT>
+// MASK = false: every key of the iteration is below kend, so no scale is zeroed.
+template <int SDT, bool MASK>
 __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b, int kb, int kend,
                                          int head, int lane, IterRegs<true>& R) {
   const int r = lane & 15;
@@ -1001,7 +1123,7 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
   const uint16_t raw = *(const uint16_t*)(sl + 2 * kTileRows + (lane >> 5) * kScaleBytes +
                                           (kk & 15) * (kHeadWaves * 2) + head * 2);
   const float s = (SDT == NE_DTYPE_BF16) ? bf16_to_f32(raw) : f16_to_f32(raw);
-  R.sc = (kb + kk < kend) ? s : 0.f;
+  R.sc = (!MASK || kb + kk < kend) ? s : 0.f;
 }
 
 // PLANNED: the work item and the split's slots come from attention_plan_kernel's
@@ -1013,19 +1135,23 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
 // item's tiles, their (m, l, O) merged through LDS before the store -- so that short
 // contexts fill KS times as many CUs without a merge kernel.
 template <int SDT, bool PLANNED, int MT, int KS = 1>
-__global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel(AttnParams p) {
-  static_assert(KS == 1 || (PLANNED && MT == 1 && kHeadWaves % KS == 0), "head split: planned, one row tile");
-  constexpr int HG = kHeadWaves / KS;  // KV heads per work-group
+__global__ __launch_bounds__(DmaShape<KS>::waves * kWave) void paged_attention_dma_kernel(AttnParams p) {
+  static_assert(KS == 1 || (PLANNED && MT == 1), "head split: planned, one row tile");
+  using Shape = DmaShape<KS>;
+  constexpr int HG = Shape::heads;  // KV heads per work-group
+  constexpr int RING = Shape::ring;
+  constexpr int FIRST = Shape::first;
+  constexpr int kThreads = Shape::waves * kWave;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  int* s_slot = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot);
-  float* s_sc_all = (float*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4);
-  int* s_plan = (int*)(smem + kHeadWaves * kDmaRing * kDmaSlot + kPlanMaxTiles * 4 + kHeadWaves * kWave * 4);
+  int* s_slot = (int*)(smem + Shape::slot_off);
+  float* s_sc_all = (float*)(smem + Shape::sc_off);
+  int* s_plan = (int*)(smem + Shape::plan_off);
 
   // ---- work item: one split of one sequence (M tile 0); wave -> (KV head, part) ----
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int widx = (KS == 1) ? (int)blockIdx.x : (int)blockIdx.x / KS;  // work item
-  const int head = (KS == 1) ? wave : ((int)blockIdx.x % KS) * HG + wave % HG;
+  const int widx = (int)blockIdx.x / Shape::groups;  // work item
+  const int head = ((int)blockIdx.x % Shape::groups) * HG + wave % HG;
   const int ks = wave / HG;  // this wave's part of the item's tiles
   const int lane = tid % kWave;
   PlanItem item;
@@ -1036,7 +1162,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     // the slot is stored to LDS only after the Q loads are issued, so that a single
     // round trip precedes the first K/V copy.  The compiler barriers keep the load
     // first and the store last.
-    static_assert(kPlanMaxTiles == kHeadWaves * kWave, "one slot per thread");
+    static_assert(kPlanMaxTiles == kThreads, "one slot per thread");
     const int32_t my_slot = p.plan_slots[(int64_t)widx * kPlanMaxTiles + tid];
     __asm__ __volatile__("" ::: "memory");
     const ConstI32* d = (const ConstI32*)(p.plan_desc + (int64_t)widx * kDescInts);
@@ -1122,7 +1248,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   }
   if constexpr (!PLANNED) {
     const int32_t* bt_row = p.block_tables + (int64_t)seq * p.bt_stride;
-    for (int t = tid; t < n_tiles; t += kHeadWaves * kWave) {
+    for (int t = tid; t < n_tiles; t += kThreads) {
       const int key0 = kstart + kTileKeys * t;
       s_slot[t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
     }
@@ -1132,31 +1258,21 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   }
   __syncthreads();  // s_slot ready
 
-  char* ring = smem + wave * (kDmaRing * kDmaSlot);
+  char* ring = smem + wave * (RING * kDmaSlot);
   const int* w_slot = s_slot + (jw0 - j0);  // this wave's tiles in the item's slot list
+  const DmaLane dl = dma_lane(lane);
   if (n_tiles > 0) {
 #pragma unroll
-    for (int j = 0; j < kDmaRing; ++j) dma_tile(p, w_slot, n_tiles, j, head, lane, ring + j * kDmaSlot);
+    for (int j = 0; j < FIRST; ++j) dma_tile(p, w_slot, n_tiles, j, head, dl, ring + j * kDmaSlot);
     // Q was issued before the ring's copies: wait for it alone (the compiler's own wait
     // would also drain the copies, since it does not order them after the Q loads)
-    dma_wait_vmcnt<kDmaPerTile * kDmaRing>();
+    dma_wait_vmcnt<kDmaPerTile * FIRST>();
   } else {
     dma_wait_vmcnt<0>();  // a wave with no tiles of the item (KS > 1) only loads Q
   }
-  QFrag<true> qf[MT];
+  QFragI8 qf[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4 hv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t w = row_valid[mt] ? raw[mt][c][i] : 0u;
-        hv[i] = pack_f16x2(bf16_to_f32((uint16_t)(w & 0xFFFFu)), bf16_to_f32((uint16_t)(w >> 16)));
-      }
-      qf[mt].q[c] = __builtin_bit_cast(f16x8, hv);
-    }
-  }
+  for (int mt = 0; mt < MT; ++mt) quantize_q_row(raw[mt], row_valid[mt], p.qk_scale, qf[mt]);
 
   float m[MT], l[MT];
   floatx4 o[MT][8];
@@ -1169,26 +1285,44 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
   }
   float* sc_row = s_sc_all + wave * kWave;
   const int n_iter = (n_tiles + 1) / 2;
-  for (int it = 0; it < n_iter; ++it) {
+  // iterations whose 32 keys every row sees (below the context end and the causal
+  // limit of the first query) need no masking
+  const int kfull = min(kend, item.ctx - ql + 1);
+  const int n_full = min(n_iter, max(0, (kfull - kstart) / kIterKeys));
+  auto iteration = [&](int it, auto mask, auto first) {
+    constexpr bool kMask = decltype(mask)::value;
+    constexpr bool kFirst = decltype(first)::value;
     // this wave's DMA of tiles 2it, 2it+1 has landed once at most the two tiles
-    // issued after them are still in flight
-    dma_wait_vmcnt<kDmaPerTile * (kDmaRing - 2)>();
-    const char* sa = ring + ((2 * it) % kDmaRing) * kDmaSlot;
-    const char* sb = ring + ((2 * it + 1) % kDmaRing) * kDmaSlot;
+    // issued after them are still in flight (none before the first iteration)
+    dma_wait_vmcnt<kFirst ? kDmaPerTile * (FIRST - 2) : kDmaPerTile * (RING - 2)>();
+    const char* sa = ring + ((2 * it) % RING) * kDmaSlot;
+    const char* sb = ring + ((2 * it + 1) % RING) * kDmaSlot;
     const int kb = kstart + it * kIterKeys;
     IterRegs<true> A;
-    lds_iter<SDT>(sa, sb, kb, kend, head, lane, A);
-    if constexpr (MT == 1) {
-      compute_iter<true>(p, A, qf[0], sc_row, kb, kend_row[0], item.ctx, lane, m[0], l[0], o[0]);
-    } else {
-      compute_iter_mt<MT>(p, A, qf, sc_row, kb, kend_row, lane, m, l, o);
-    }
-    // the two slots are free once their reads have returned: refill them
+    lds_iter<SDT, kMask>(sa, sb, kb, kend, head, lane, A);
+    // the two slots are free once their reads have returned: refill them before the
+    // arithmetic, so that each copy has two iterations to land
     dma_wait_lgkmcnt0();
-    dma_tile(p, w_slot, n_tiles, 2 * it + kDmaRing, head, lane, ring + ((2 * it) % kDmaRing) * kDmaSlot);
-    dma_tile(p, w_slot, n_tiles, 2 * it + 1 + kDmaRing, head, lane,
-             ring + ((2 * it + 1) % kDmaRing) * kDmaSlot);
+    if constexpr (kFirst) {
+#pragma unroll
+      for (int j = FIRST; j < RING; ++j) dma_tile(p, w_slot, n_tiles, j, head, dl, ring + j * kDmaSlot);
+    }
+    dma_tile(p, w_slot, n_tiles, 2 * it + RING, head, dl, ring + ((2 * it) % RING) * kDmaSlot);
+    dma_tile(p, w_slot, n_tiles, 2 * it + 1 + RING, head, dl, ring + ((2 * it + 1) % RING) * kDmaSlot);
+    compute_iter_q8<MT, kMask>(A, qf, sc_row, kb, kend_row, lane, m, l, o);
+  };
+  int it = 0;
+  if (n_iter > 0) {
+    // the first iteration also issues the ring's remaining tiles
+    if (n_full > 0) {
+      iteration(0, std::false_type{}, std::true_type{});
+    } else {
+      iteration(0, std::true_type{}, std::true_type{});
+    }
+    it = 1;
   }
+  for (; it < n_full; ++it) iteration(it, std::false_type{}, std::false_type{});
+  for (; it < n_iter; ++it) iteration(it, std::true_type{}, std::false_type{});
   dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
 
   if constexpr (KS > 1) {
@@ -1199,7 +1333,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void paged_attention_dma_kernel
     lt += __shfl_xor(lt, 32);
     lds_barrier();
     floatx4* s_o = (floatx4*)smem;                   // [wave][8][lane]
-    float2* s_ml = (float2*)(smem + kHeadWaves * 8 * kWave * 16);  // [wave][lane]
+    float2* s_ml = (float2*)(smem + Shape::waves * 8 * kWave * 16);  // [wave][lane]
+    static_assert(Shape::waves * kWave * (8 * 16 + 8) <= Shape::slot_off, "the merge fits in the rings");
 #pragma unroll
     for (int j = 0; j < 8; ++j) s_o[(wave * 8 + j) * kWave + lane] = o[0][j];
     s_ml[wave * kWave + lane] = float2{m[0], lt};
@@ -1456,16 +1591,16 @@ int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStre
 // the attribute for more than the default dynamic LDS once per instantiation.
 template <int SDT, bool PLANNED, int MT, int KS = 1>
 int launch_attention_dma_ks(const AttnParams& p, unsigned grid, hipStream_t s) {
+  constexpr int lds = DmaShape<KS>::lds;
   static const hipError_t attr = hipFuncSetAttribute(
       (const void*)paged_attention_dma_kernel<SDT, PLANNED, MT, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
-      kDmaLds);
+      lds);
   if (attr != hipSuccess) {
-    set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", kDmaLds,
-              hipGetErrorString(attr));
+    set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", lds, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT, KS>), dim3(grid), dim3(kHeadWaves * kWave),
-                     kDmaLds, s, p);
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT, KS>), dim3(grid),
+                     dim3(DmaShape<KS>::waves * kWave), lds, s, p);
   return check_launch("paged_attention_dma_kernel");
 }
 
@@ -1476,8 +1611,8 @@ int launch_attention_dma_mt(const AttnParams& p, hipStream_t s) {
     // heads, the waves of a head over consecutive parts of its tiles
     if (p.plan_whole) {
       if (whole_plan_ks(p.num_seqs, p.max_ctx, 0, 1) == 4)
-        return launch_attention_dma_ks<SDT, PLANNED, MT, 4>(p, (unsigned)p.num_seqs * 4, s);
-      return launch_attention_dma_ks<SDT, PLANNED, MT, 2>(p, (unsigned)p.num_seqs * 2, s);
+        return launch_attention_dma_ks<SDT, PLANNED, MT, 4>(p, (unsigned)p.num_seqs * DmaShape<4>::groups, s);
+      return launch_attention_dma_ks<SDT, PLANNED, MT, 2>(p, (unsigned)p.num_seqs * DmaShape<2>::groups, s);
     }
   }
   // no sequence is split when every context fits in one split's minimum length
