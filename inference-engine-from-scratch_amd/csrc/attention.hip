@@ -1398,40 +1398,30 @@ __global__ __launch_bounds__(DmaShape<KS>::waves * kWave) void paged_attention_d
   }
 }
 
-// Combines the partials of every sequence the plan split: one work-group per
-// (sequence, KV head), 16 threads per row, 8 dims per thread; partial k of the
-// sequence is work-group N_b + k's.  A split-length plan gives a sequence at most
-// kMergeBatch partials per pass of loads, so every (m, l, O) of a row is requested
-// at once rather than in a dependent chain.
+// Partials of a row requested together by the merge kernels: a split-length plan gives
+// a sequence at most kMergeBatch partials per pass of loads, so every (m, l, O) of a row
+// is requested at once rather than in a dependent chain.
 constexpr int kMergeBatch = 8;
 
-__global__ __launch_bounds__(kPartRows * 16) void attention_plan_merge_kernel(AttnParams p) {
-  const int seq = blockIdx.x / kHeadWaves;
-  const int head = blockIdx.x % kHeadWaves;
-  // the sequence's plan entries and rows through the scalar cache (written by earlier kernels)
-  const int first = ((const ConstI32*)p.plan)[seq];
-  const int last = min(((const ConstI32*)p.plan)[seq + 1], p.plan_grid);
-  const int ql = ((const ConstI32*)p.q_len)[seq];
-  const int qs = ((const ConstI32*)p.q_start)[seq];
-  const int n_splits = last - first;
-  if (n_splits <= 1) return;
-  const int crow = threadIdx.x >> 4;
-  const int cd = (threadIdx.x & 15) * 8;
-  if (crow >= min(p.group * ql, kPartRows)) return;
+// Merges n partial states (m, l, O) of one query row: out = sum_s 2^(m_s - M) O_s /
+// sum_s 2^(m_s - M) l_s over dims cd..cd+7.  pi(s) is the row of partial s in part_ml /
+// part_o; the partials of a batch of kMergeBatch are all requested before any is used
+// (a slot past the last partial re-reads partial s0 and is ignored).
+template <typename PartIndex>
+__device__ __forceinline__ void merge_partials(const AttnParams& p, int n, int cd, PartIndex pi,
+                                               uint16_t* dst) {
   float MM = kNegBig, LL = 0.f;
   float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+  for (int s0 = 0; s0 < n; s0 += kMergeBatch) {
     float ms[kMergeBatch], ls[kMergeBatch];
     floatx4 x0[kMergeBatch], x1[kMergeBatch];
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) {
-      // a slot past the sequence's last partial re-reads its first one and is ignored
-      const int s = (s0 + j < n_splits) ? s0 + j : s0;
-      const int64_t pi = ((int64_t)(first + s) * kHeadWaves + head) * kPartRows + crow;
-      const float2 ml = *(const float2*)(p.part_ml + pi * 2);
-      ms[j] = (s0 + j < n_splits) ? ml.x : kNegBig;
+      const int64_t r = pi((s0 + j < n) ? s0 + j : s0);
+      const float2 ml = *(const float2*)(p.part_ml + r * 2);
+      ms[j] = (s0 + j < n) ? ml.x : kNegBig;
       ls[j] = ml.y;
-      const float* src = p.part_o + pi * kHeadDim + cd;
+      const float* src = p.part_o + r * kHeadDim + cd;
       x0[j] = *(const floatx4*)src;
       x1[j] = *(const floatx4*)(src + 4);
     }
@@ -1445,7 +1435,7 @@ __global__ __launch_bounds__(kPartRows * 16) void attention_plan_merge_kernel(At
     MM = Mb;
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) {
-      const float a = (s0 + j < n_splits) ? __builtin_amdgcn_exp2f(ms[j] - MM) : 0.f;
+      const float a = (s0 + j < n) ? __builtin_amdgcn_exp2f(ms[j] - MM) : 0.f;
       LL += a * ls[j];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
@@ -1454,17 +1444,37 @@ __global__ __launch_bounds__(kPartRows * 16) void attention_plan_merge_kernel(At
       }
     }
   }
-  const int ch = crow / ql, ci = crow % ql;
-  uint16_t* dst = p.out + (int64_t)(qs + ci) * p.o_tok_stride +
-                  (int64_t)(head * p.group + ch) * p.o_head_stride + cd;
   const float inv = 1.f / LL;
   *(u32x4*)dst = u32x4{pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv),
                        pack_bf16x2(tot[4] * inv, tot[5] * inv), pack_bf16x2(tot[6] * inv, tot[7] * inv)};
 }
 
-// Combines the split partials of every unit that has more than one split:
-// out = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s.  One work-group per unit,
-// 16 threads per row, 8 dims per thread.
+// Combines the partials of every sequence the plan split: one work-group per
+// (sequence, KV head), 16 threads per row, 8 dims per thread; partial k of the
+// sequence is work-group N_b + k's.
+__global__ __launch_bounds__(kPartRows * 16) void attention_plan_merge_kernel(AttnParams p) {
+  const int seq = blockIdx.x / kHeadWaves;
+  const int head = blockIdx.x % kHeadWaves;
+  // the sequence's plan entries and rows through the scalar cache (written by earlier kernels)
+  const int first = ((const ConstI32*)p.plan)[seq];
+  const int last = min(((const ConstI32*)p.plan)[seq + 1], p.plan_grid);
+  const int ql = ((const ConstI32*)p.q_len)[seq];
+  const int qs = ((const ConstI32*)p.q_start)[seq];
+  const int n_splits = last - first;
+  if (n_splits <= 1) return;
+  const int crow = threadIdx.x >> 4;
+  const int cd = (threadIdx.x & 15) * 8;
+  if (crow >= min(p.group * ql, kPartRows)) return;
+  const int ch = crow / ql, ci = crow % ql;
+  uint16_t* dst = p.out + (int64_t)(qs + ci) * p.o_tok_stride +
+                  (int64_t)(head * p.group + ch) * p.o_head_stride + cd;
+  merge_partials(p, n_splits, cd,
+                 [&](int s) { return ((int64_t)(first + s) * kHeadWaves + head) * kPartRows + crow; }, dst);
+}
+
+// Combines the split partials of every unit that has more than one split (the
+// fixed-split kernels' layout): one work-group per unit, 16 threads per row, 8 dims
+// per thread.
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   const int unit = blockIdx.x;
   const UnitInfo u = unit_info(p, unit);
@@ -1476,29 +1486,10 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   const int CR = u.row0 + crow;
   if (CR >= u.rows_total) return;
   const int64_t ubase = (int64_t)unit * p.max_splits * kRows + crow;
-  float MM = kNegBig;
-  for (int s = 0; s < n_splits; ++s) MM = fmaxf(MM, p.part_ml[(ubase + (int64_t)s * kRows) * 2]);
-  float LL = 0.f;
-  float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < n_splits; ++s) {
-    const int64_t pi = ubase + (int64_t)s * kRows;
-    const float a = __builtin_amdgcn_exp2f(p.part_ml[pi * 2] - MM);
-    LL += a * p.part_ml[pi * 2 + 1];
-    const float* src = p.part_o + pi * kHeadDim + cd;
-    const floatx4 x0 = *(const floatx4*)src;
-    const floatx4 x1 = *(const floatx4*)(src + 4);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      tot[d] += a * x0[d];
-      tot[d + 4] += a * x1[d];
-    }
-  }
   const int ch = CR / u.ql, ci = CR % u.ql;
   uint16_t* dst = p.out + (int64_t)(u.qs + ci) * p.o_tok_stride +
                   (int64_t)(u.head * p.group + ch) * p.o_head_stride + cd;
-  const float inv = 1.f / LL;
-  *(u32x4*)dst = u32x4{pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv),
-                       pack_bf16x2(tot[4] * inv, tot[5] * inv), pack_bf16x2(tot[6] * inv, tot[7] * inv)};
+  merge_partials(p, n_splits, cd, [&](int s) { return ubase + (int64_t)s * kRows; }, dst);
 }
 
 struct Layout {
