@@ -144,8 +144,8 @@ class EngineSettings:
             return "kv_cache must be paged"
         if self.quantization != "int8":
             return "quantization must be int8 (W8A16 projections)"
-        if self.speculative != "ngram":
-            return "speculative must be ngram"
+        if self.speculative not in ("ngram", "draft"):
+            return "speculative must be ngram or draft"
         if self.kv_block_size % 16 != 0:
             return "kv_block_size must be a multiple of 16"
         return None

@@ -1,0 +1,177 @@
+"""Draft-model proposer for the batched verify step on the HIP kernels.
+
+The reference's ``DraftModelProposer`` (ne/engine/speculative/proposers.py:63-106)
+runs a small model of the target's family ``num_tokens`` steps ahead of one
+request, with its own KV cache (a one-sequence pool, ne/engine/runtime.py:116-129):
+
+  * ``_sync_draft`` makes the draft's tokens equal the target's and keeps its
+    cache only for their common prefix (``num_cached = min(num_cached, common)``);
+  * every step reserves the draft's slots, scores its uncached tokens
+    (``ModelRunner.score_tokens``), and takes the last row's greedy token as the
+    next guess (the first step catches up on the tokens the target emitted).
+
+``DraftModelProposer`` here does the same for every slot of a ``VerifyRunner`` at
+once: one forward of the draft model per guess position covers all slots that
+still need guesses (their uncached tokens packed as rows, chunked to the model's
+row capacity), on the same W8A16 projection, paged attention and LM-head kernels
+as the target, over its own paged pool and allocator.  The next token of each
+slot is the LM head's argmax reduced by the acceptance kernel with no drafts.
+
+Only greedy guesses are made: the reference's sampled draft also hands its
+distributions to the verifier (``Proposal.probabilities``), which the fused
+acceptance kernel does not take, so a sampled request is refused up front.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from nanoengine_amd import kernels
+from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
+from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
+from nanoengine_amd.sequence_state import Sequence
+
+
+class DraftModelProposer:
+    """Greedy draft-model guesses for the slots of a batched verify step."""
+
+    def __init__(self, model: Qwen3VerifyModel, pool: KVCachePool, allocator: PagedSlotAllocator,
+                 max_seqs: int, max_tokens: int, device: torch.device) -> None:
+        self.model = model
+        self.pool = pool
+        self.allocator = allocator
+        self.device = device
+        self.block_size = allocator.block_size
+        self.max_blocks = math.ceil(max_tokens / self.block_size)
+        self.max_seqs = max_seqs
+        # per slot: the draft's own Sequence (its tokens and cached count) and block table
+        self.drafts: dict[int, Sequence] = {}
+        self.tables = np.zeros((max_seqs, self.max_blocks), dtype=np.int32)
+        self.owned = np.zeros(max_seqs, dtype=np.int64)
+        i32 = dict(dtype=torch.int32, device=device)
+        self.out_tokens = torch.zeros((max_seqs, 2), **i32)
+        self.num_out = torch.zeros(max_seqs, **i32)
+        self.no_drafts = torch.zeros((max_seqs, 1), **i32)
+        self.zero_counts = torch.zeros(max_seqs, **i32)
+        self.last_rows = torch.arange(max_seqs, **i32)
+        self.h_out = torch.zeros((max_seqs, 2), dtype=torch.int32, pin_memory=True)
+        self.forwards = 0  # draft forwards run (a count for tests and benchmarks)
+
+    # ------------------------------------------------------------------ state
+    def _sync(self, slot: int, sequence: Sequence) -> Sequence:
+        """proposers.py:95-106: the draft takes the target's tokens, keeping its cache for
+        their common prefix."""
+        draft = self.drafts.get(slot)
+        if draft is None:
+            draft = Sequence.from_request(sequence.request)
+            self.drafts[slot] = draft
+        common = 0
+        for draft_token, target_token in zip(draft.token_ids, sequence.token_ids):
+            if draft_token != target_token:
+                break
+            common += 1
+        draft.token_ids = list(sequence.token_ids)
+        draft.num_cached_tokens = min(draft.num_cached_tokens, common)
+        return draft
+
+    def _reserve(self, slot: int, draft: Sequence, num_tokens: int) -> None:
+        added = self.allocator.reserve(draft, num_tokens)
+        if added:
+            owned = int(self.owned[slot])
+            if owned + len(added) > self.max_blocks:
+                raise ValueError(f"draft of slot {slot} needs more than {self.max_blocks} blocks")
+            self.tables[slot, owned : owned + len(added)] = added
+            self.owned[slot] = owned + len(added)
+
+    def release(self, slot: int) -> None:
+        """proposers.py:90-93: the request finished; free the draft's blocks."""
+        draft = self.drafts.pop(slot, None)
+        if draft is not None:
+            self.allocator.free(draft)
+        self.owned[slot] = 0
+
+    # -------------------------------------------------------------- proposals
+    def propose(self, sequences: dict[int, Sequence], counts: dict[int, int]) -> dict[int, list[int]]:
+        """``counts[slot]`` greedy guesses for each slot (proposers.py:70-88)."""
+        want = {s: n for s, n in counts.items() if n > 0}
+        guesses: dict[int, list[int]] = {s: [] for s in want}
+        for s in want:
+            self._sync(s, sequences[s])
+        while True:
+            live = [s for s in sorted(want) if len(guesses[s]) < want[s]]
+            if not live:
+                break
+            for s, token in self._next_tokens(live).items():
+                self.drafts[s].token_ids.append(token)
+                guesses[s].append(token)
+        return guesses
+
+    def _next_tokens(self, live: list[int]) -> dict[int, int]:
+        """Score every live draft's uncached tokens; return each one's greedy next token."""
+        work = []  # (slot, draft, start, end): rows start..end-1, context end
+        for s in live:
+            draft = self.drafts[s]
+            self._reserve(s, draft, draft.num_tokens)
+            work.append([s, draft, draft.num_cached_tokens, draft.num_tokens])
+        cap = self.model.max_rows
+        done: list[int] = []  # slots whose last row has been scored, in output order
+        while work:
+            pieces, rows = [], 0
+            while work and rows < cap:
+                s, draft, a, e = work[0]
+                n = min(e - a, cap - rows)
+                pieces.append((s, draft, a, a + n, e))
+                rows += n
+                if a + n == e:
+                    work.pop(0)
+                else:
+                    work[0][2] = a + n
+            self._forward(pieces, rows, done)
+        torch.cuda.current_stream(self.device).synchronize()
+        self.h_out.copy_(self.out_tokens)
+        return {s: int(self.h_out[i, 0]) for i, s in enumerate(done)}
+
+    def _forward(self, pieces, rows: int, done: list[int]) -> None:
+        """One draft forward over packed pieces; the pieces that reach their draft's last
+        token get their greedy next token in out_tokens[len(done) ...]."""
+        dev = self.device
+        tokens, positions, slot_map, q_start, q_len, ctx_len, tables = [], [], [], [], [], [], []
+        row = 0
+        for s, draft, a, b, e in pieces:
+            pos = np.arange(a, b)
+            tokens.append(np.asarray(draft.token_ids[a:b], dtype=np.int32))
+            positions.append(pos.astype(np.int32))
+            slot_map.append(self.allocator.slots_for(draft, pos).astype(np.int32))
+            q_start.append(row)
+            q_len.append(b - a)
+            ctx_len.append(b)
+            tables.append(self.tables[s])
+            row += b - a
+        up = lambda x: torch.from_numpy(np.ascontiguousarray(np.concatenate(x))).to(dev)
+        tok, posn, slots = up(tokens), up(positions), up(slot_map)
+        qs = torch.tensor(q_start, dtype=torch.int32, device=dev)
+        ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+        cl = torch.tensor(ctx_len, dtype=torch.int32, device=dev)
+        bt = torch.from_numpy(np.stack(tables)).to(dev)
+        batch = AttentionBatch(posn, slots, qs, ql, cl, bt, max(q_len), max(ctx_len))
+        self.model.ensure_rope(max(ctx_len))
+        hidden = self.model.forward(rows, tok, batch, self.pool)
+        self.forwards += 1
+        for s, draft, a, b, e in pieces:
+            draft.num_cached_tokens = b
+        ends = [i for i, (s, draft, a, b, e) in enumerate(pieces) if b == e]
+        if not ends:
+            return
+        last_rows = torch.tensor([q_start[i] + q_len[i] - 1 for i in ends], dtype=torch.long, device=dev)
+        last = hidden.index_select(0, last_rows)
+        _, partials = self.model.compute_logits(last, logits=False, argmax=True)
+        n, o = len(ends), len(done)
+        kernels.accept(
+            self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], self.model.config.vocab_size,
+            argmax_partials=partials, temperature=0.0, out_tokens=self.out_tokens[o : o + n],
+            num_out=self.num_out[o : o + n],
+        )
+        done.extend(pieces[i][0] for i in ends)

@@ -7,7 +7,8 @@ speculative_generator.py:70-85).  ``VerifyRunner`` applies the same per-sequence
 semantics to up to ``max_seqs`` sequences at once, with the token histories,
 lengths, block tables and cached counts resident on the device:
 
-  1. n-gram drafting on the device histories (ne_ngram_propose)
+  1. n-gram drafting on the device histories (ne_ngram_propose), or a draft
+     model's greedy guesses (``DraftModelProposer``, nanoengine_amd/draft.py)
   2. read back the draft counts; reserve KV blocks on the host allocator for
      L + g tokens per sequence (paged_allocator.py:50-55) and upload new table rows
   3. pack rows on the device (ne_prepare_verify_step), run the Qwen3 forward,
@@ -31,6 +32,7 @@ from __future__ import annotations
 
 import math
 from collections import deque
+from typing import TYPE_CHECKING
 from dataclasses import dataclass
 
 import numpy as np
@@ -44,6 +46,9 @@ from nanoengine_amd.interface import (
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
 from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
 from nanoengine_amd.sequence_state import Sequence
+
+if TYPE_CHECKING:
+    from nanoengine_amd.draft import DraftModelProposer
 
 
 @dataclass
@@ -68,8 +73,11 @@ class VerifyRunner:
         max_model_len: int,
         stop_token_ids: frozenset[int] = frozenset(),
         use_graph: bool = False,
+        proposer: "DraftModelProposer | None" = None,
     ) -> None:
         self.model = model
+        # None: n-gram drafting on the device histories; else a draft model's greedy guesses
+        self.proposer = proposer
         self.pool = pool
         self.allocator = allocator
         # the shared-block guard only has something to check with a prefix cache
@@ -118,6 +126,7 @@ class VerifyRunner:
         self.h_steps = torch.zeros(max_seqs, dtype=torch.int64, **pin)
         self.h_num_drafts = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         self.h_out = torch.zeros(max_seqs, self.R, dtype=torch.int32, **pin)
+        self.h_drafts = torch.zeros(max_seqs, self.k, dtype=torch.int32, **pin)
         self.h_num_out = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         # numpy views of the pinned buffers: the per-step host work indexes them per
         # sequence, which costs ~1 us through torch and ~0.1 us through numpy
@@ -158,6 +167,9 @@ class VerifyRunner:
         if params.temperature != GREEDY_TEMPERATURE and params.top_p < 1.0:
             raise NotImplementedError("top_p < 1 is not implemented on the HIP acceptance path")
         temp = float(params.temperature)
+        if self.proposer is not None and temp != GREEDY_TEMPERATURE:
+            raise NotImplementedError("draft-model speculation verifies greedy requests only (the acceptance "
+                                      "kernel takes deterministic guesses, not draft distributions)")
         if self.temperature is not None and self.active_slots and temp != self.temperature:
             raise NotImplementedError("one batch verifies with a single temperature")
         self.temperature = temp
@@ -337,10 +349,21 @@ class VerifyRunner:
         self.np_num_tokens[:] = np.where(act, counts, 0)
         self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
         self.steps.copy_(self.h_steps, non_blocking=True)
-        kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
-                              drafts=self.drafts, num_drafts=self.num_drafts)
-        self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
-        torch.cuda.current_stream(self.device).synchronize()
+        if self.proposer is None:
+            kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
+                                  drafts=self.drafts, num_drafts=self.num_drafts)
+            self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
+            torch.cuda.current_stream(self.device).synchronize()
+        else:
+            guesses = self.proposer.propose({s: slots[s] for s in active},
+                                            {s: int(self.np_num_tokens[s]) for s in active})
+            self.np_num_drafts[:] = 0
+            np_drafts = self.h_drafts.numpy()
+            for s, g in guesses.items():
+                np_drafts[s, : len(g)] = g
+                self.np_num_drafts[s] = len(g)
+            self.drafts.copy_(self.h_drafts, non_blocking=True)
+            self.num_drafts.copy_(self.h_num_drafts, non_blocking=True)
         np_num_drafts, allocator, bs = self.np_num_drafts, self.allocator, self.block_size
         if self._guard_shared:
             # rows write positions L-1 .. L-1+g; every block below the allocator's
@@ -426,6 +449,8 @@ class VerifyRunner:
         if seq is None:
             return
         self.allocator.free(seq)
+        if self.proposer is not None:
+            self.proposer.release(slot)
         self.slots[slot] = None
         self.np_active[slot] = False
         self.np_owned[slot] = 0

@@ -4,11 +4,13 @@ speculative generator)."""
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import torch
 
 from nanoengine_amd.config import TORCH_DTYPES, EngineSettings
+from nanoengine_amd.draft import DraftModelProposer
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator, PrefixCachingSlotAllocator, slots_for_budget
 from nanoengine_amd.metrics import EngineMetrics
 from nanoengine_amd.qwen3 import Qwen3Config, Qwen3VerifyModel, Qwen3Weights
@@ -34,9 +36,13 @@ class VerifyEngine:
 
 def create_verify_engine(config: Qwen3Config, state_dict: dict[str, torch.Tensor], settings: EngineSettings,
                          stop_token_ids: frozenset[int] = frozenset(), max_prefill_rows: int | None = None,
-                         ) -> VerifyEngine:
+                         draft_config: Qwen3Config | None = None,
+                         draft_state_dict: dict[str, torch.Tensor] | None = None) -> VerifyEngine:
     """Pool sized from ``kv_cache_memory_mb`` (runtime.py:81-95), int8 weights
-    (runtime.py:140-141), one VerifyRunner with ``max_num_seqs`` slots."""
+    (runtime.py:140-141), one VerifyRunner with ``max_num_seqs`` slots.  With
+    ``speculative="draft"`` the draft model (``draft_config`` / ``draft_state_dict``, the
+    weights ``draft_model_id`` names) gets its own paged pool with room for every slot's
+    full length and a ``DraftModelProposer`` (runtime.py:116-129)."""
     problem = settings.hip_verify_path_error()
     if problem is not None:
         raise ValueError(f"the HIP verify path needs other settings: {problem}")
@@ -59,7 +65,22 @@ def create_verify_engine(config: Qwen3Config, state_dict: dict[str, torch.Tensor
     max_seqs = settings.max_num_seqs if settings.is_batched else 1
     rows = max(max_seqs * (settings.num_speculative_tokens + 1), max_prefill_rows or settings.max_prefill_tokens)
     model = Qwen3VerifyModel(weights, rows, device)
+    proposer = None
+    if settings.speculative == "draft":
+        if draft_config is None or draft_state_dict is None:
+            raise ValueError("speculative='draft' needs the draft model's config and weights")
+        if draft_config.vocab_size != config.vocab_size:
+            raise ValueError("the draft model must share the target's vocabulary")
+        tokens = settings.max_model_len + settings.num_speculative_tokens + 1
+        draft_blocks = max_seqs * math.ceil(tokens / settings.kv_block_size)
+        draft_pool = KVCachePool(draft_config.num_hidden_layers, draft_config.num_key_value_heads,
+                                 draft_config.head_dim, draft_blocks * settings.kv_block_size, device, dtype,
+                                 settings.is_int8_kv_cache, settings.kv_block_size)
+        draft_weights = Qwen3Weights.from_state_dict(draft_config, draft_state_dict, device, dtype)
+        draft_model = Qwen3VerifyModel(draft_weights, rows, device)
+        draft_allocator = PagedSlotAllocator(draft_blocks, settings.kv_block_size, device)
+        proposer = DraftModelProposer(draft_model, draft_pool, draft_allocator, max_seqs, tokens, device)
     runner = VerifyRunner(model, pool, allocator, max_seqs, settings.num_speculative_tokens,
                           settings.ngram_max_size, settings.max_model_len, stop_token_ids,
-                          use_graph=settings.cuda_graphs)
+                          use_graph=settings.cuda_graphs, proposer=proposer)
     return VerifyEngine(settings, model, pool, allocator, runner, EngineMetrics())

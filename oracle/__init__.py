@@ -10,6 +10,8 @@ reference tree, ``ne/`` = ``nanoengine/src/nanoengine/``) in plain Python,
 numpy, C (``csrc/accept_oracle.c``) or torch on the CPU:
 
   ngram.py      NgramProposer.propose             ne/engine/speculative/proposers.py:39-57
+  draft.py      DraftModelProposer.propose        ne/engine/speculative/proposers.py:63-106
+                (greedy guesses)
   paging.py     block / paged / contiguous slot   ne/engine/memory/*.py, batch_builder.py
                 allocators, step inputs, masks
   prefix_cache.py  hash-chained block keys,       ne/engine/memory/prefix_cache.py:21-158

@@ -369,3 +369,28 @@ def test_speculative_output_equals_the_target_alone(kv_int8):
         runner2.allocator.reserve("t", len(seq2.token_ids))
     assert spec == plain
     assert 0 <= stats.accepted <= stats.proposed and stats.proposed > 0
+
+
+def test_draft_proposals_equal_a_cached_greedy_decode():
+    """oracle.draft.propose (full forwards) against the oracle's cached ModelRunner path
+    (paged KV, one scored token per step) on the same tiny draft model; a shorter
+    proposal is a prefix of a longer one (proposers.py:70-88 appends each guess)."""
+    from oracle import draft as odr
+
+    cfg = om.Qwen3Config(97, 64, 128, 2, 4, 2, 16, 1e-6, 1e4, True)
+    model = om.build_random_model(cfg, seed=11, std=0.3)
+    prompt = [5, 17, 3, 88, 41, 5, 17, 3]
+    guesses = odr.propose(model, prompt, 6)
+    assert odr.propose(model, prompt, 3) == guesses[:3]
+    runner = ov.ModelRunner(model, om.KVCachePool(cfg, 64, torch.float32), opg.PagedSlotAllocator(4, 16))
+    seq = ov.Sequence("d", list(prompt), len(prompt), 6)
+    decoded = []
+    for _ in range(6):
+        runner.allocator.reserve(seq.request_id, len(seq.token_ids))
+        token = runner.run_step([seq])[0]
+        seq.token_ids.append(token)
+        decoded.append(token)
+    assert decoded == guesses
+    rows = odr.draft_logits(model, prompt, guesses)
+    assert rows.shape == (6, 97)
+    assert [int(r.argmax()) for r in rows] == guesses
