@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 4
+#define NE_ABI_VERSION 5
 
 /* status codes */
 #define NE_OK 0
@@ -271,6 +271,12 @@ int ne_w8a16_qkv_norm_rope_kv(const void* x, int64_t ldx, const int8_t* w, const
  * (p itself if that is empty) and the bonus samples p of the last row, both by
  * inverse CDF with u_draw.  Uniforms u_i, u_draw come from Philox4x32-10 keyed
  * by seeds[b] at counter (steps[b], j/4), word j%4, j = i (guesses) and 63.
+ * With draft_logits (sampled only; guesses drawn by a draft model): the draft's
+ * logits for guess i of sequence b are row draft_row_start[b] + i (stride
+ * ld_draft); q = its softmax under the same contract; guess i is kept iff
+ * a = min(p/max(q,1e-12), 1) >= 1 or (a > 0 and u_i < a), and a rejection draws
+ * from max(p - q, 0) (p when that is empty), verifier.py:36-56.  Null: the
+ * guesses are deterministic (one-hot q), as above.
  * Outputs: out_tokens[b, 0..num_out[b]-1] (kept guesses + 1 target token),
  * the rest of the row [b, 0..max_drafts] set to -1; num_out[b] = kept + 1.  When history is given, the kept tokens and the target
  * token are appended at history[b, history_len[b]..] and history_len[b] and
@@ -282,7 +288,8 @@ int ne_accept(int32_t mode, const void* logits, int64_t ld_logits, const uint64_
               const int32_t* num_drafts, const int32_t* row_start, int32_t num_seqs,
               float temperature, const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens,
               int32_t* num_out, int32_t* history, int64_t history_stride, int32_t* history_len,
-              int32_t* num_cached, void* stream);
+              int32_t* num_cached, const void* draft_logits, int64_t ld_draft,
+              const int32_t* draft_row_start, void* stream);
 
 /*
  * Device-side packing of a batched verify step (replaces build_step_inputs,

@@ -29,6 +29,13 @@
 //   uniforms: Philox4x32-10 (Salmon et al., SC'11), key = seed, counter =
 //          (step lo, step hi, j / 4, 0), word j % 4, u = (word >> 8) * 2^-24;
 //          j = i for guess i, j = 63 for the draw.
+//   with draft rows (a draft model's logits for each guess, the same T): f_j and
+//          Zq as e_j and Z over the draft row; p = e_g / Z, q = max(f_g / Zq, 1e-12),
+//          a = min(p / q, 1); guess i is kept iff a >= 1 or (a > 0 and u_i < a)
+//          (verifier.py:44-51).  At the first rejection the draw is from the
+//          residual r_j = max(e_j / Z - f_j / Zq, 0) (each term one fp32 op), chunk
+//          sums and total as above, falling back to e when the total is not > 0
+//          (verifier.py:52-56).
 // FP contraction is disabled in this file's arithmetic on that path so that
 // every operation is a single IEEE-rounded fp32 op, as in the C oracle.
 #include "ne_common.hpp"
@@ -137,6 +144,9 @@ struct AcceptParams {
   int64_t hist_stride;
   int32_t* history_len;
   int32_t* num_cached;
+  const uint16_t* draft_logits;  // sampled mode: the draft's row per guess, or null (one-hot)
+  int64_t dld;
+  const int32_t* draft_row_start;
 };
 
 __device__ __forceinline__ float logit_at(const AcceptParams& p, int row, int j) {
@@ -163,16 +173,22 @@ struct RowSums {
   float Z;   // total of chunk sums
 };
 
-__device__ RowSums row_sums(const AcceptParams& p, int row, float* s_chunk, float* s_redf) {
+__device__ __forceinline__ float logit_of(const uint16_t* base, int64_t ld, int row, int j) {
+  return bf16_to_f32(base[(int64_t)row * ld + j]);
+}
+
+// over the target's logits (base = p.logits) or the draft's (base = p.draft_logits)
+__device__ RowSums row_sums(const AcceptParams& p, const uint16_t* base, int64_t ld, int row, float* s_chunk,
+                            float* s_redf) {
   const int V = p.vocab;
   const int CH = (V + kChunks - 1) / kChunks;
   float m = -INFINITY;
-  for (int j = threadIdx.x; j < V; j += kThreads) m = fmaxf(m, logit_at(p, row, j) / p.temperature);
+  for (int j = threadIdx.x; j < V; j += kThreads) m = fmaxf(m, logit_of(base, ld, row, j) / p.temperature);
   const float mx = block_max_f32(m, s_redf);
   const int c = threadIdx.x;
   float s = 0.f;
   const int lo = c * CH, hi = min(lo + CH, V);
-  for (int j = lo; j < hi; ++j) s = s + cephes_exp(logit_at(p, row, j) / p.temperature - mx);
+  for (int j = lo; j < hi; ++j) s = s + cephes_exp(logit_of(base, ld, row, j) / p.temperature - mx);
   s_chunk[c] = s;
   __syncthreads();
   float Z = 0.f;
@@ -225,10 +241,71 @@ __device__ int draw_row(const AcceptParams& p, int row, const RowSums& rs, int x
   return 0;
 }
 
+// residual draw: r_j = max(e_j / Z - f_j / Zq, 0) over the target row `row` (sums rs)
+// and the draft row `drow` (sums rq); every thread sums its chunk, thread 0 scans.
+// Falls back to the target row (no exclusion) when the residual total is not > 0.
+__device__ int draw_residual(const AcceptParams& p, int row, const RowSums& rs, int drow, const RowSums& rq,
+                             float u, float* s_chunk, float* s_rchunk) {
+  const int V = p.vocab;
+  const int CH = (V + kChunks - 1) / kChunks;
+  const float T = p.temperature;
+  auto r_at = [&](int j) -> float {
+    const float pj = cephes_exp(logit_at(p, row, j) / T - rs.mx) / rs.Z;
+    const float qj = cephes_exp(logit_of(p.draft_logits, p.dld, drow, j) / T - rq.mx) / rq.Z;
+    const float r = pj - qj;
+    return r > 0.f ? r : 0.f;
+  };
+  {
+    const int c = threadIdx.x;
+    float sr = 0.f;
+    const int lo = c * CH, hi = min(lo + CH, V);
+    for (int j = lo; j < hi; ++j) sr = sr + r_at(j);
+    s_rchunk[c] = sr;
+  }
+  __syncthreads();
+  int res = 0;
+  if (threadIdx.x == 0) {
+    float R = 0.f;
+    for (int c = 0; c < kChunks; ++c) R = R + s_rchunk[c];
+    if (!(R > 0.f)) {
+      res = draw_row(p, row, rs, -1, u, s_chunk);
+    } else {
+      const float t = u * R;
+      float prefix = 0.f;
+      res = -1;
+      for (int c = 0; c < kChunks && res < 0; ++c) {
+        const float rc = s_rchunk[c];
+        if (prefix + rc > t) {
+          float q = 0.f;
+          const int lo = c * CH, hi = min(lo + CH, V);
+          for (int j = lo; j < hi; ++j) {
+            q = q + r_at(j);
+            if (prefix + q > t) {
+              res = j;
+              break;
+            }
+          }
+        }
+        prefix = prefix + rc;
+      }
+      if (res < 0) {
+        for (int j = V - 1; j >= 0; --j)
+          if (r_at(j) > 0.f) {
+            res = j;
+            break;
+          }
+        if (res < 0) res = 0;
+      }
+    }
+  }
+  return res;
+}
+
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
   __shared__ uint64_t s_red[kThreads / kWave];
   __shared__ float s_redf[kThreads / kWave];
   __shared__ float s_chunk[kChunks];
+  __shared__ float s_qchunk[kChunks];
   __shared__ int s_target[kMaxRows];
   __shared__ int s_kept, s_final;
 
@@ -262,22 +339,37 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
     const uint64_t seed = p.seeds[b], step = p.steps[b];
     int kept = 0;
     bool done = false;
+    const int dr0 = p.draft_logits != nullptr ? p.draft_row_start[b] : 0;
     for (int i = 0; i < g && !done; ++i) {
-      const RowSums rs = row_sums(p, rs0 + i, s_chunk, s_redf);
+      const RowSums rs = row_sums(p, p.logits, p.ld, rs0 + i, s_chunk, s_redf);
       const int guess = dr[i];
       const float pg = cephes_exp(logit_at(p, rs0 + i, guess) / p.temperature - rs.mx) / rs.Z;
       const float u = philox_uniform(seed, step, i);
-      if (pg >= 1.f || (pg > 0.f && u < pg)) {
-        ++kept;
-        continue;
-      }
-      if (tid == 0) {
-        s_final = draw_row(p, rs0 + i, rs, guess, philox_uniform(seed, step, 63), s_chunk);
+      if (p.draft_logits == nullptr) {
+        if (pg >= 1.f || (pg > 0.f && u < pg)) {
+          ++kept;
+          continue;
+        }
+        if (tid == 0) {
+          s_final = draw_row(p, rs0 + i, rs, guess, philox_uniform(seed, step, 63), s_chunk);
+        }
+      } else {
+        const RowSums rq = row_sums(p, p.draft_logits, p.dld, dr0 + i, s_qchunk, s_redf);
+        const float qg = fmaxf(
+            cephes_exp(logit_of(p.draft_logits, p.dld, dr0 + i, guess) / p.temperature - rq.mx) / rq.Z, 1e-12f);
+        const float a = fminf(pg / qg, 1.f);
+        if (a >= 1.f || (a > 0.f && u < a)) {
+          ++kept;
+          continue;
+        }
+        const int t = draw_residual(p, rs0 + i, rs, dr0 + i, rq, philox_uniform(seed, step, 63), s_chunk,
+                                    s_qchunk);
+        if (tid == 0) s_final = t;
       }
       done = true;
     }
     if (!done) {
-      const RowSums rs = row_sums(p, rs0 + g, s_chunk, s_redf);
+      const RowSums rs = row_sums(p, p.logits, p.ld, rs0 + g, s_chunk, s_redf);
       if (tid == 0) s_final = draw_row(p, rs0 + g, rs, -1, philox_uniform(seed, step, 63), s_chunk);
     }
     if (tid == 0) s_kept = kept;
@@ -313,7 +405,8 @@ extern "C" int ne_accept(int32_t mode, const void* logits, int64_t ld_logits,
                          const int32_t* row_start, int32_t num_seqs, float temperature,
                          const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens,
                          int32_t* num_out, int32_t* history, int64_t history_stride,
-                         int32_t* history_len, int32_t* num_cached, void* stream) {
+                         int32_t* history_len, int32_t* num_cached, const void* draft_logits,
+                         int64_t ld_draft, const int32_t* draft_row_start, void* stream) {
   NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
   if (num_seqs == 0) return NE_OK;
   NE_CHECK_ARG(mode == NE_ACCEPT_GREEDY || mode == NE_ACCEPT_SAMPLED, "unknown mode %d", mode);
@@ -331,6 +424,8 @@ extern "C" int ne_accept(int32_t mode, const void* logits, int64_t ld_logits,
   }
   NE_CHECK_ARG(!logits || ld_logits >= vocab, "ld_logits < vocab");
   NE_CHECK_ARG(!history || (history_len && history_stride > 0), "history needs history_len");
+  NE_CHECK_ARG(!draft_logits || (mode == NE_ACCEPT_SAMPLED && draft_row_start && ld_draft >= vocab),
+               "draft rows need sampled mode, draft_row_start and ld_draft >= vocab");
   AcceptParams p{};
   p.mode = mode;
   p.logits = (const uint16_t*)logits;
@@ -351,6 +446,9 @@ extern "C" int ne_accept(int32_t mode, const void* logits, int64_t ld_logits,
   p.hist_stride = history_stride;
   p.history_len = history_len;
   p.num_cached = num_cached;
+  p.draft_logits = (const uint16_t*)draft_logits;
+  p.dld = ld_draft;
+  p.draft_row_start = draft_row_start;
   hipLaunchKernelGGL(accept_kernel, dim3(num_seqs), dim3(kThreads), 0, (hipStream_t)stream, p);
   return check_launch("accept");
 }

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -109,6 +109,7 @@ SIGNATURES: dict[str, tuple] = {
             _f32, _u64p, _u64p,  # temperature, seeds, steps
             _vp, _vp,  # out tokens, num out
             _vp, _i64, _vp, _vp,  # history, stride, history len, num cached
+            _vp, _i64, _vp,  # draft logits, ld, draft row start
             _vp,  # stream
         ],
     ),

@@ -7,19 +7,21 @@ request, with its own KV cache (a one-sequence pool, ne/engine/runtime.py:116-12
   * ``_sync_draft`` makes the draft's tokens equal the target's and keeps its
     cache only for their common prefix (``num_cached = min(num_cached, common)``);
   * every step reserves the draft's slots, scores its uncached tokens
-    (``ModelRunner.score_tokens``), and takes the last row's greedy token as the
-    next guess (the first step catches up on the tokens the target emitted).
+    (``ModelRunner.score_tokens``), and takes the last row's token as the next
+    guess, greedy or sampled (the first step catches up on the tokens the target
+    emitted), keeping the distribution it was drawn from for the verifier.
 
 ``DraftModelProposer`` here does the same for every slot of a ``VerifyRunner`` at
 once: one forward of the draft model per guess position covers all slots that
 still need guesses (their uncached tokens packed as rows, chunked to the model's
 row capacity), on the same W8A16 projection, paged attention and LM-head kernels
 as the target, over its own paged pool and allocator.  The next token of each
-slot is the LM head's argmax reduced by the acceptance kernel with no drafts.
-
-Only greedy guesses are made: the reference's sampled draft also hands its
-distributions to the verifier (``Proposal.probabilities``), which the fused
-acceptance kernel does not take, so a sampled request is refused up front.
+slot comes from the acceptance kernel run with no drafts: the argmax of the LM head's
+partials when greedy; when sampled, an inverse-CDF draw from the draft row's softmax
+under the acceptance kernel's explicit-uniform contract, with the uniform of guess j at
+verify step s taken at counter step s + (j + 1) * 2^48 (apart from the verifier's own
+uniforms at step s).  The sampled draft's logits stay in ``logits``, row slot * k + j,
+where the verify step's acceptance reads them as the draft distributions.
 """
 
 from __future__ import annotations
@@ -36,10 +38,10 @@ from nanoengine_amd.sequence_state import Sequence
 
 
 class DraftModelProposer:
-    """Greedy draft-model guesses for the slots of a batched verify step."""
+    """Draft-model guesses for the slots of a batched verify step."""
 
     def __init__(self, model: Qwen3VerifyModel, pool: KVCachePool, allocator: PagedSlotAllocator,
-                 max_seqs: int, max_tokens: int, device: torch.device) -> None:
+                 max_seqs: int, max_tokens: int, device: torch.device, k: int = 1) -> None:
         self.model = model
         self.pool = pool
         self.allocator = allocator
@@ -59,6 +61,14 @@ class DraftModelProposer:
         self.last_rows = torch.arange(max_seqs, **i32)
         self.h_out = torch.zeros((max_seqs, 2), dtype=torch.int32, pin_memory=True)
         self.forwards = 0  # draft forwards run (a count for tests and benchmarks)
+        self.k = k
+        # sampled proposals: the draft's logits per (slot, guess), read by the verifier
+        self.logits: torch.Tensor | None = None
+        self.row_start = torch.arange(max_seqs, **i32) * k
+        self.temperature = 0.0
+        self.seeds: torch.Tensor | None = None
+        self.steps: np.ndarray | None = None
+        self.target_len: dict[int, int] = {}  # this proposal's target length per slot
 
     # ------------------------------------------------------------------ state
     def _sync(self, slot: int, sequence: Sequence) -> Sequence:
@@ -94,12 +104,26 @@ class DraftModelProposer:
         self.owned[slot] = 0
 
     # -------------------------------------------------------------- proposals
-    def propose(self, sequences: dict[int, Sequence], counts: dict[int, int]) -> dict[int, list[int]]:
-        """``counts[slot]`` greedy guesses for each slot (proposers.py:70-88)."""
+    def propose(self, sequences: dict[int, Sequence], counts: dict[int, int], temperature: float = 0.0,
+                seeds: torch.Tensor | None = None, steps: np.ndarray | None = None) -> dict[int, list[int]]:
+        """``counts[slot]`` guesses for each slot (proposers.py:70-88): greedy, or sampled at
+        ``temperature`` with the slots' ``seeds`` (device int64) at verify ``steps`` (host)."""
+        self.temperature = float(temperature)
+        if self.temperature > 0.0:
+            if seeds is None or steps is None:
+                raise ValueError("sampled draft proposals need seeds and steps")
+            if self.logits is None:
+                self.logits = torch.zeros((self.max_seqs * self.k, self.model.config.vocab_size),
+                                          dtype=torch.bfloat16, device=self.device)
+            self.seeds, self.steps = seeds, steps
         want = {s: n for s, n in counts.items() if n > 0}
+        if want and max(want.values()) > self.k:
+            raise ValueError(f"at most {self.k} guesses per slot")
         guesses: dict[int, list[int]] = {s: [] for s in want}
+        self.target_len = {}
         for s in want:
             self._sync(s, sequences[s])
+            self.target_len[s] = sequences[s].num_tokens
         while True:
             live = [s for s in sorted(want) if len(guesses[s]) < want[s]]
             if not live:
@@ -110,7 +134,7 @@ class DraftModelProposer:
         return guesses
 
     def _next_tokens(self, live: list[int]) -> dict[int, int]:
-        """Score every live draft's uncached tokens; return each one's greedy next token."""
+        """Score every live draft's uncached tokens; return each one's next token."""
         work = []  # (slot, draft, start, end): rows start..end-1, context end
         for s in live:
             draft = self.drafts[s]
@@ -167,11 +191,27 @@ class DraftModelProposer:
             return
         last_rows = torch.tensor([q_start[i] + q_len[i] - 1 for i in ends], dtype=torch.long, device=dev)
         last = hidden.index_select(0, last_rows)
-        _, partials = self.model.compute_logits(last, logits=False, argmax=True)
         n, o = len(ends), len(done)
-        kernels.accept(
-            self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], self.model.config.vocab_size,
-            argmax_partials=partials, temperature=0.0, out_tokens=self.out_tokens[o : o + n],
-            num_out=self.num_out[o : o + n],
-        )
+        vocab = self.model.config.vocab_size
+        if self.temperature == 0.0:
+            _, partials = self.model.compute_logits(last, logits=False, argmax=True)
+            kernels.accept(
+                self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], vocab, argmax_partials=partials,
+                temperature=0.0, out_tokens=self.out_tokens[o : o + n], num_out=self.num_out[o : o + n],
+            )
+        else:
+            slots = [pieces[i][0] for i in ends]
+            # guess j of slot s: the draft's row s * k + j (j = tokens past the target's)
+            rows = [s * self.k + len(pieces[i][1].token_ids) - self.target_len[s] for i, s in zip(ends, slots)]
+            logits, _ = self.model.compute_logits(last, logits=True, argmax=False)
+            self.logits.index_copy_(0, torch.tensor(rows, dtype=torch.long, device=dev), logits)
+            sel = torch.tensor(slots, dtype=torch.long, device=dev)
+            steps = np.array([int(self.steps[s]) + ((r - s * self.k + 1) << 48) for s, r in zip(slots, rows)],
+                             dtype=np.int64)
+            kernels.accept(
+                self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], vocab, logits=logits,
+                temperature=self.temperature, seeds=self.seeds.index_select(0, sel),
+                steps=torch.from_numpy(steps).to(dev), out_tokens=self.out_tokens[o : o + n],
+                num_out=self.num_out[o : o + n],
+            )
         done.extend(pieces[i][0] for i in ends)

@@ -574,8 +574,14 @@ def accept(
     history: torch.Tensor | None = None,
     history_len: torch.Tensor | None = None,
     num_cached: torch.Tensor | None = None,
+    draft_logits: torch.Tensor | None = None,
+    draft_row_start: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Accepted guesses plus one target token per sequence: ``(out_tokens [b, k+1], num_out [b])``."""
+    """Accepted guesses plus one target token per sequence: ``(out_tokens [b, k+1], num_out [b])``.
+
+    ``draft_logits`` (sampled mode): the draft model's bf16 logits for each guess, row
+    ``draft_row_start[b] + i`` for guess i of sequence b; without them the guesses count
+    as deterministic (one-hot draft distribution)."""
     device = _require_gpu(drafts, num_drafts, row_start, logits, argmax_partials)
     _int32(drafts, "drafts")
     _int32(num_drafts, "num_drafts")
@@ -589,6 +595,12 @@ def accept(
         _check(logits is not None, "sampled acceptance needs logits")
         _check(seeds is not None and steps is not None, "sampled acceptance needs seeds and steps")
         _check(seeds.dtype == torch.int64 and steps.dtype == torch.int64, "seeds/steps int64")
+    if draft_logits is not None:
+        _check(mode == ACCEPT_SAMPLED, "draft logits need sampled acceptance")
+        _check(draft_logits.dtype == torch.bfloat16 and draft_logits.stride(1) == 1, "draft logits must be bf16 rows")
+        _check(draft_logits.shape[1] == vocab, "draft logits width must equal vocab")
+        _check(draft_row_start is not None, "draft logits need draft_row_start")
+        _int32(draft_row_start, "draft_row_start")
     if out_tokens is None:
         out_tokens = torch.empty((num_seqs, max_drafts + 1), dtype=torch.int32, device=device)
     if num_out is None:
@@ -602,7 +614,9 @@ def accept(
         float(temperature), _ptr(seeds), _ptr(steps),
         _ptr(out_tokens), _ptr(num_out),
         _ptr(history), history.stride(0) if history is not None else 0,
-        _ptr(history_len), _ptr(num_cached), _stream(device),
+        _ptr(history_len), _ptr(num_cached),
+        _ptr(draft_logits), draft_logits.stride(0) if draft_logits is not None else 0, _ptr(draft_row_start),
+        _stream(device),
     )
     return out_tokens, num_out
 

@@ -167,9 +167,6 @@ class VerifyRunner:
         if params.temperature != GREEDY_TEMPERATURE and params.top_p < 1.0:
             raise NotImplementedError("top_p < 1 is not implemented on the HIP acceptance path")
         temp = float(params.temperature)
-        if self.proposer is not None and temp != GREEDY_TEMPERATURE:
-            raise NotImplementedError("draft-model speculation verifies greedy requests only (the acceptance "
-                                      "kernel takes deterministic guesses, not draft distributions)")
         if self.temperature is not None and self.active_slots and temp != self.temperature:
             raise NotImplementedError("one batch verifies with a single temperature")
         self.temperature = temp
@@ -319,6 +316,9 @@ class VerifyRunner:
             temperature=self.temperature or 0.0, seeds=self.seeds, steps=self.steps,
             out_tokens=self.out_tokens, num_out=self.num_out, history=self.history,
             history_len=self.history_len, num_cached=self.num_cached,
+            # a sampled draft model's guesses are verified against its distributions
+            draft_logits=None if greedy or self.proposer is None else self.proposer.logits,
+            draft_row_start=None if greedy or self.proposer is None else self.proposer.row_start,
         )
 
     def _run_device_step(self) -> None:
@@ -356,7 +356,9 @@ class VerifyRunner:
             torch.cuda.current_stream(self.device).synchronize()
         else:
             guesses = self.proposer.propose({s: slots[s] for s in active},
-                                            {s: int(self.np_num_tokens[s]) for s in active})
+                                            {s: int(self.np_num_tokens[s]) for s in active},
+                                            temperature=self.temperature or 0.0, seeds=self.seeds,
+                                            steps=self.np_steps)
             self.np_num_drafts[:] = 0
             np_drafts = self.h_drafts.numpy()
             for s, g in guesses.items():

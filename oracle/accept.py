@@ -39,6 +39,11 @@ def lib() -> ctypes.CDLL:
         handle.oracle_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
         handle.oracle_philox4x32_10.restype = None
         handle.oracle_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        handle.oracle_accept_sampled_draft.restype = ctypes.c_int
+        handle.oracle_accept_sampled_draft.argtypes = [
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+            ctypes.c_int, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p,
+        ]
         handle.oracle_accept_sampled.restype = ctypes.c_int
         handle.oracle_accept_sampled.argtypes = [
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
@@ -97,5 +102,24 @@ def sampled_accept(row_bits: np.ndarray, drafts: list[int], temperature: float, 
     n = lib().oracle_accept_sampled(
         rows.ctypes.data, vocab, vocab, d.ctypes.data if g else None, g, ctypes.c_float(temperature),
         seed, step, out.ctypes.data, scratch.ctypes.data,
+    )
+    return out[:n].tolist()
+
+
+def sampled_accept_draft(row_bits: np.ndarray, draft_bits: np.ndarray, drafts: list[int], temperature: float,
+                         seed: int, step: int) -> list[int]:
+    """Target rows ``[g+1, V]`` and the draft model's rows ``[g, V]`` (uint16 bf16 patterns)
+    -> kept guesses + drawn token (C oracle, verifier.py:36-56 with draft distributions)."""
+    rows = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    drows = np.ascontiguousarray(draft_bits, dtype=np.uint16)
+    g = len(drafts)
+    assert rows.shape[0] == g + 1 and drows.shape[0] >= g
+    vocab = rows.shape[1]
+    d = np.ascontiguousarray(np.asarray(drafts, dtype=np.int32))
+    out = np.zeros(g + 1, dtype=np.int32)
+    scratch = np.zeros(3 * vocab, dtype=np.float32)
+    n = lib().oracle_accept_sampled_draft(
+        rows.ctypes.data, vocab, drows.ctypes.data, vocab, vocab, d.ctypes.data if g else None, g,
+        ctypes.c_float(temperature), seed, step, out.ctypes.data, scratch.ctypes.data,
     )
     return out[:n].tolist()

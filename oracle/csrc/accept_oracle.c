@@ -173,3 +173,49 @@ int oracle_accept_sampled(const uint16_t* logits, int64_t ld, int vocab, const i
   out[kept] = draw(scratch, vocab, -1, oracle_uniform(seed, step, 63));
   return kept + 1;
 }
+
+/*
+ * oracle_accept_sampled with the guesses drawn by a draft model: draft rows
+ * [num_drafts][ldq] hold the draft's logits for each guess (same temperature);
+ * q = its softmax under the same contract.  Guess i is kept iff
+ * a = min(p / max(q, 1e-12), 1) >= 1 or (a > 0 and u_i < a); a rejection draws
+ * from r_j = max(p_j - q_j, 0) (p when r has no mass), verifier.py:36-56.
+ * `scratch` holds 3 * vocab floats.
+ */
+int oracle_accept_sampled_draft(const uint16_t* logits, int64_t ld, const uint16_t* draft, int64_t ldq,
+                                int vocab, const int32_t* drafts, int num_drafts, float temperature,
+                                uint64_t seed, uint64_t step, int32_t* out, float* scratch) {
+  float sums[CHUNKS];
+  float* e = scratch;
+  float* f = scratch + vocab;
+  float* r = scratch + 2 * vocab;
+  int kept = 0;
+  for (int i = 0; i < num_drafts; ++i) {
+    row_exps(logits + (int64_t)i * ld, vocab, temperature, e);
+    chunk_sums(e, vocab, -1, sums);
+    const float z = total(sums);
+    row_exps(draft + (int64_t)i * ldq, vocab, temperature, f);
+    chunk_sums(f, vocab, -1, sums);
+    const float zq = total(sums);
+    const int guess = drafts[i];
+    const float p = e[guess] / z;
+    const float q = fmaxf(f[guess] / zq, 1e-12f);
+    const float a = fminf(p / q, 1.0f);
+    const float u = oracle_uniform(seed, step, i);
+    if (a >= 1.0f || (a > 0.0f && u < a)) {
+      out[kept++] = guess;
+      continue;
+    }
+    for (int j = 0; j < vocab; ++j) {
+      const float rj = e[j] / z - f[j] / zq;
+      r[j] = rj > 0.0f ? rj : 0.0f;
+    }
+    chunk_sums(r, vocab, -1, sums);
+    const float u_draw = oracle_uniform(seed, step, 63);
+    out[kept] = total(sums) > 0.0f ? draw(r, vocab, -1, u_draw) : draw(e, vocab, -1, u_draw);
+    return kept + 1;
+  }
+  row_exps(logits + (int64_t)num_drafts * ld, vocab, temperature, e);
+  out[kept] = draw(e, vocab, -1, oracle_uniform(seed, step, 63));
+  return kept + 1;
+}

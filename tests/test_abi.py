@@ -54,7 +54,8 @@ def test_host_checks_reject_bad_arguments_without_launching(lib):
     # W8A16 GEMM: k must be a multiple of 128
     rc = lib.ne_w8a16_gemm(p, 1000, p, p, 0, 320, 1024, 1000, p, 1024, 0, null)
     assert rc == -2
-    rc = lib.ne_accept(0, null, 0, null, 0, 100, p, 0, p, p, 2, 0.0, null, null, p, p, null, 0, null, null, null)
+    rc = lib.ne_accept(0, null, 0, null, 0, 100, p, 0, p, p, 2, 0.0, null, null, p, p, null, 0, null, null,
+                       null, 0, null, null)
     assert rc == -1  # max_drafts 0
 
 

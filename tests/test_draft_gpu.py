@@ -10,7 +10,8 @@ test_engine_gpu.py); draft: the same shapes with 1 layer and other weights.  Che
   * the emitted tokens equal the target's greedy tokens wherever the target's margin
     is clear (speculation never changes greedy output);
   * with the target's own weights as the draft every clear guess is accepted;
-  * sampled requests are refused (the acceptance kernel takes no draft distributions).
+  * sampled guesses are the draws of the contract from the draft's rows, and the
+    acceptance with draft distributions equals the C oracle bit for bit.
 """
 
 from __future__ import annotations
@@ -139,11 +140,74 @@ def test_target_as_its_own_draft_accepts_every_clear_guess():
     assert proposed > 0 and accepted >= 0.9 * proposed
 
 
-def test_sampled_requests_are_refused_with_a_draft_model():
-    state = random_state_dict(CFG, seed=0, std=0.02)
-    dstate = random_state_dict(DCFG, seed=7, std=0.02)
-    eng = engine(state, DCFG, dstate, 2)
-    params = SamplingParams(max_new_tokens=8, temperature=0.8, seed=1)
-    seq = Sequence.from_request(GenerationRequest("s", prompts(1, seed=1)[0], params))
-    with pytest.raises(NotImplementedError, match="greedy"):
-        eng.runner.add([seq])
+def test_accept_with_draft_rows_matches_the_c_oracle():
+    """ne_accept with draft rows (sampled; verifier.py:36-56) bit for bit against the C
+    oracle: 48 sequences, 0..4 guesses, draft rows near the target rows (acceptances)
+    or independent of them (rejections and residual draws), vocab not a multiple of 256."""
+    from oracle import accept as oacc
+    from nanoengine_amd import kernels
+
+    torch.manual_seed(5)
+    b, k, vocab, temp = 48, 4, 5003, 0.8
+    target = torch.randn(b * (k + 1), vocab) * 2
+    draft = torch.randn(b * k, vocab) * 2
+    near = torch.arange(b) % 2 == 0
+    for s in range(b):
+        if near[s]:
+            draft[s * k : (s + 1) * k] = target[s * (k + 1) : s * (k + 1) + k] + 0.3 * torch.randn(k, vocab)
+    t_bf, d_bf = target.bfloat16(), draft.bfloat16()
+    counts = torch.arange(b, dtype=torch.int32) % (k + 1)
+    drafts = torch.randint(0, vocab, (b, k), dtype=torch.int32)
+    for s in range(b):  # some guesses are the draft row's top tokens
+        drafts[s, 0] = int(d_bf[s * k].float().argmax())
+    seeds = torch.arange(b, dtype=torch.int64) * 7919 + 3
+    steps = torch.arange(b, dtype=torch.int64) + 11
+    dev = torch.device("cuda")
+    out, n = kernels.accept(drafts.to(dev), counts.to(dev), (torch.arange(b, dtype=torch.int32) * (k + 1)).to(dev),
+                            vocab, logits=t_bf.to(dev), temperature=temp, seeds=seeds.to(dev), steps=steps.to(dev),
+                            draft_logits=d_bf.to(dev), draft_row_start=(torch.arange(b, dtype=torch.int32) * k).to(dev))
+    out, n = out.cpu(), n.cpu()
+    tb = t_bf.view(torch.int16).numpy().view("uint16")
+    db = d_bf.view(torch.int16).numpy().view("uint16")
+    rejected = accepted = 0
+    for s in range(b):
+        g = int(counts[s])
+        want = oacc.sampled_accept_draft(tb[s * (k + 1) : s * (k + 1) + g + 1], db[s * k : s * k + max(g, 1)],
+                                         drafts[s, :g].tolist(), temp, int(seeds[s]), int(steps[s]))
+        got = out[s, : int(n[s])].tolist()
+        assert got == want, f"sequence {s}"
+        accepted += len(want) - 1
+        rejected += g > len(want) - 1
+    assert accepted > 0 and rejected > 0
+
+
+def test_sampled_draft_step_matches_the_c_oracle():
+    """One sampled verify step with a draft model: each guess is the draw from its draft
+    row at counter step s + (j + 1) * 2^48, and the emitted tokens are the C oracle's
+    draft-distribution acceptance on the step's target and draft logits."""
+    from oracle import accept as oacc
+
+    state = unit_norms(random_state_dict(CFG, seed=0, std=0.02))
+    dstate = unit_norms(random_state_dict(DCFG, seed=7, std=0.02))
+    eng = engine(state, DCFG, dstate, 4)
+    params = SamplingParams(max_new_tokens=16, temperature=0.8, seed=3, ignore_eos=True)
+    seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts(4, seed=6))]
+    eng.runner.add(seqs)
+    eng.runner.trace = []
+    eng.runner.step()
+    torch.cuda.synchronize()
+    rec_step = eng.runner.trace[0]
+    k = eng.runner.k
+    t_bits = eng.runner.logits.view(torch.int16).cpu().numpy().view("uint16")
+    d_bits = eng.runner.proposer.logits.view(torch.int16).cpu().numpy().view("uint16")
+    for slot, rec in rec_step.items():
+        seed = seqs[slot].sampling_generator.seed
+        step = int(eng.runner.h_steps[slot]) - 1  # the step counter advanced after the step
+        g = len(rec["drafts"])
+        assert g == rec["requested"] > 0
+        for j, guess in enumerate(rec["drafts"]):
+            drawn = oacc.sampled_accept(d_bits[slot * k + j : slot * k + j + 1], [], 0.8, seed, step + ((j + 1) << 48))
+            assert drawn == [guess], f"slot {slot} guess {j}"
+        want = oacc.sampled_accept_draft(t_bits[slot * (k + 1) : slot * (k + 1) + g + 1],
+                                         d_bits[slot * k : slot * k + g], rec["drafts"], 0.8, seed, step)
+        assert rec["out"] == want, f"slot {slot}"

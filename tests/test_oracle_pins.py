@@ -394,3 +394,43 @@ def test_draft_proposals_equal_a_cached_greedy_decode():
     rows = odr.draft_logits(model, prompt, guesses)
     assert rows.shape == (6, 97)
     assert [int(r.argmax()) for r in rows] == guesses
+
+
+def test_draft_distribution_rule_keeps_the_target_distribution():
+    """nt/engine/test_speculative_decoding.py:58-75 under the explicit-uniform contract
+    (C oracle): the guess is drawn from the draft's own distribution q, the rule keeps it
+    with min(1, p/q) and otherwise draws from max(p - q, 0); the first token then
+    follows the target distribution p."""
+    kat = KATS["rejection_sampling_chi_square"]
+    target = np.asarray(kat["target"], dtype=np.float64)
+    draft = np.asarray(kat["draft"], dtype=np.float64)
+    bits = oacc.bf16_bits(np.log(target).astype(np.float32))
+    bits = np.stack([bits, bits])
+    dbits = oacc.bf16_bits(np.log(draft).astype(np.float32))[None, :]
+    p_bf16 = np.exp(oacc.bf16_to_f32(bits[0]).astype(np.float64))
+    p_bf16 /= p_bf16.sum()
+    q_bf16 = np.exp(oacc.bf16_to_f32(dbits[0]).astype(np.float64))
+    q_bf16 /= q_bf16.sum()
+    rng = np.random.default_rng(kat["seed"])
+    trials = kat["trials"]
+    counts = np.zeros(5)
+    kept = 0
+    for step in range(trials):
+        guess = int(rng.choice(5, p=q_bf16))
+        out = oacc.sampled_accept_draft(bits, dbits, [guess], 1.0, seed=12345, step=step)
+        counts[out[0]] += 1
+        kept += len(out) == 2
+    assert _chi_square(counts, p_bf16, trials) < kat["critical_value"]
+    # acceptance rate sum_g min(p_g, q_g) (the overlap of the two distributions)
+    overlap = float(np.minimum(p_bf16, q_bf16).sum())
+    assert abs(kept / trials - overlap) < 4 * math.sqrt(overlap * (1 - overlap) / trials)
+
+
+def test_draft_distribution_rule_equal_distributions_keep_every_guess():
+    """q = p: min(1, p/q) = 1 for every guess (no uniform is consulted)."""
+    rng = np.random.default_rng(3)
+    bits = oacc.bf16_bits(rng.standard_normal((4, 50)).astype(np.float32))
+    for trial in range(20):
+        guesses = [int(x) for x in rng.integers(0, 50, 3)]
+        out = oacc.sampled_accept_draft(bits, bits[:3], guesses, 0.7, seed=trial, step=trial)
+        assert out[:3] == guesses and len(out) == 4
