@@ -102,7 +102,11 @@ def gemm_traffic(m, n, k):
 
 
 def run_verify(args, torch, temperature: float | None = None, steps: int | None = None,
-               warmup: int | None = None):
+               warmup: int | None = None, draft: bool = False):
+    """The verify step at 64 sequences, k = 4.  draft=True: guesses from a draft model
+    (DraftModelProposer) with the target's own weights as the draft (the reference's
+    default draft model id names the same Qwen3-0.6B), so every guess a greedy target
+    would make is proposed and the step pays four draft forwards."""
     from nanoengine_amd import _native
     from nanoengine_amd.config import EngineSettings
     from nanoengine_amd.interface import GenerationRequest, SamplingParams
@@ -123,10 +127,12 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     state = random_state_dict(cfg, seed=0, std=0.02)
     log(f"random init {time.perf_counter() - t0:.1f}s")
     settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
-                              quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                              quantization="int8", kv_cache_dtype="int8",
+                              speculative="draft" if draft else "ngram",
                               num_speculative_tokens=K_DRAFT, ngram_max_size=3, max_num_seqs=NUM_SEQS,
                               max_model_len=max_len, kv_cache_memory_mb=2048, cuda_graphs=args.graph)
-    eng = create_verify_engine(cfg, state, settings, max_prefill_rows=NUM_SEQS * PROMPT_MOTIF * PROMPT_REPEATS)
+    eng = create_verify_engine(cfg, state, settings, max_prefill_rows=NUM_SEQS * PROMPT_MOTIF * PROMPT_REPEATS,
+                               draft_config=cfg if draft else None, draft_state_dict=state if draft else None)
     del state
     log(f"engine ready {time.perf_counter() - t0:.1f}s")
     params = SamplingParams(max_new_tokens=max_new, temperature=temperature, seed=0, ignore_eos=True)
@@ -766,7 +772,7 @@ def main() -> int:
     parser.add_argument("--temperature", type=float, default=0.0)
     parser.add_argument("--eager", dest="graph", action="store_false",
                         help="launch the step's kernels one by one instead of replaying a HIP graph")
-    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline", "long"),
+    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline", "long", "draft"),
                         default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-torch-baseline", action="store_true")
@@ -826,6 +832,17 @@ def main() -> int:
                    "accepted_tok_s": round(s_res["tokens"] / s_res["elapsed"], 1),
                    "accepted_per_step_hist": {str(k): v for k, v in sorted(s_res["kept_hist"].items())}}
         log(f"sampled: {sampled['verify_step_us']} us per step")
+    draft_verify = None
+    if args.only in ("all", "draft"):
+        # draft-model speculation (the target's own weights as the draft), greedy
+        d_res = run_verify(args, torch, temperature=0.0, steps=10, warmup=2, draft=True)
+        d_step_us = 1e6 * d_res["elapsed"] / 10
+        draft_verify = {"workload": "verify step with a draft model (DraftModelProposer; Qwen3-0.6B architecture, "
+                                    "the target's weights as the draft), 64 seqs, k=4, greedy, int8 W + KV",
+                        "steps": 10, "verify_step_us": round(d_step_us, 1),
+                        "accepted_tok_s": round(d_res["tokens"] / d_res["elapsed"], 1),
+                        "accepted_per_step_hist": {str(k): v for k, v in sorted(d_res["kept_hist"].items())}}
+        log(f"draft-model verify: {draft_verify['verify_step_us']} us per step")
     long_verify = None
     if args.only in ("all", "long"):
         long_verify = run_verify_long(args, torch)
@@ -836,7 +853,7 @@ def main() -> int:
         log(f"cpu baseline: {cpu['value']} tok/s")
     if res is None:
         print(json.dumps({"attention": attention, "gemm": gemm, "torch_baseline": torch_base,
-                          "long_context_verify": long_verify}), flush=True)
+                          "long_context_verify": long_verify, "draft_verify": draft_verify}), flush=True)
         return 0
     value = res["tokens"] / res["elapsed"]
     step_us = 1e6 * res["elapsed"] / args.steps
@@ -868,6 +885,7 @@ def main() -> int:
         "roofline": attention,
         "gemm": gemm,
         "sampled": sampled,
+        "draft_verify": draft_verify,
         "long_context_verify": long_verify,
         "torch_baseline": torch_base,
         "cpu_baseline": cpu,
