@@ -33,7 +33,9 @@ from nanoengine_amd.sequence_state import Sequence
 @dataclass(frozen=True)
 class Proposal:
     token_ids: list[int]
-    probabilities: torch.Tensor | None = None  # always None: n-gram guesses are deterministic
+    # [len(token_ids), vocab] distributions the guesses were drawn from (a sampled draft
+    # model); None: deterministic guesses (n-gram)
+    probabilities: torch.Tensor | None = None
 
 
 class NgramProposer:
@@ -63,9 +65,11 @@ class NgramProposer:
 
 def verify_proposal(proposal: Proposal, target_logits: torch.Tensor, params: SamplingParams,
                     generator: SamplingStream) -> list[int]:
-    """Kept guesses plus one target token (verifier.py:27-60) from device logits."""
-    if proposal.probabilities is not None:
-        raise NotImplementedError("the HIP acceptance path verifies deterministic (n-gram) guesses")
+    """Kept guesses plus one target token (verifier.py:27-60) from device logits.
+
+    With ``proposal.probabilities`` (sampled), the kernel takes the draft's distributions
+    as rows of logits ``T * log(q)``, whose softmax at temperature T is q again (up to the
+    bf16 rounding of the rows); greedy acceptance does not use them."""
     if params.temperature != GREEDY_TEMPERATURE and params.top_p < 1.0:
         raise NotImplementedError("top_p < 1 is not implemented on the HIP acceptance path")
     guesses = proposal.token_ids
@@ -76,12 +80,21 @@ def verify_proposal(proposal: Proposal, target_logits: torch.Tensor, params: Sam
     k = max(g, 1)
     drafts = torch.zeros(1, k, dtype=torch.int32)
     drafts[0, :g] = torch.tensor(guesses, dtype=torch.int32)
+    sampled = params.temperature != GREEDY_TEMPERATURE
+    draft_logits = None
+    if sampled and proposal.probabilities is not None and g > 0:
+        q = proposal.probabilities.to(dev, torch.float32)
+        if q.shape != (g, target_logits.shape[1]):
+            raise ValueError("probabilities must be [len(guesses), vocab]")
+        draft_logits = (torch.log(q) * float(params.temperature)).to(torch.bfloat16).contiguous()
     out, n = kernels.accept(
         drafts.to(dev), torch.tensor([g], dtype=torch.int32, device=dev),
         torch.zeros(1, dtype=torch.int32, device=dev), target_logits.shape[1],
         logits=target_logits.to(torch.bfloat16).contiguous(), temperature=float(params.temperature),
         seeds=torch.tensor([generator.seed], dtype=torch.int64, device=dev),
         steps=torch.tensor([generator.step], dtype=torch.int64, device=dev),
+        draft_logits=draft_logits,
+        draft_row_start=torch.zeros(1, dtype=torch.int32, device=dev) if draft_logits is not None else None,
     )
     generator.step += 1
     count = int(n.cpu()[0])

@@ -211,3 +211,29 @@ def test_sampled_draft_step_matches_the_c_oracle():
         want = oacc.sampled_accept_draft(t_bits[slot * (k + 1) : slot * (k + 1) + g + 1],
                                          d_bits[slot * k : slot * k + g], rec["drafts"], 0.8, seed, step)
         assert rec["out"] == want, f"slot {slot}"
+
+
+def test_verify_proposal_with_draft_probabilities_matches_the_c_oracle():
+    """speculative.verify_proposal (verifier.py:27-60) with Proposal.probabilities: the
+    distributions enter the kernel as rows T * log(q), and the result equals the C
+    oracle's draft-distribution rule on the same rows."""
+    from oracle import accept as oacc
+    from nanoengine_amd.interface import create_sampling_generator
+    from nanoengine_amd.speculative import Proposal, verify_proposal
+
+    torch.manual_seed(9)
+    vocab, temp = 3001, 0.7
+    for trial in range(12):
+        g = 1 + trial % 4
+        target = (torch.randn(g + 1, vocab) * 2).bfloat16()
+        q = torch.softmax(torch.randn(g, vocab) * 2 / temp, dim=-1)
+        guesses = [int(torch.multinomial(q[i], 1)) for i in range(g)]
+        gen = create_sampling_generator(100 + trial)
+        step = gen.step
+        params = SamplingParams(max_new_tokens=8, temperature=temp)
+        got = verify_proposal(Proposal(guesses, q), target.to("cuda"), params, gen)
+        d_rows = (torch.log(q.to("cuda")) * temp).bfloat16().cpu()  # as verify_proposal forms them
+        want = oacc.sampled_accept_draft(target.view(torch.int16).numpy().view("uint16"),
+                                         d_rows.view(torch.int16).numpy().view("uint16"), guesses, temp,
+                                         gen.seed, step)
+        assert got == want, f"trial {trial}"
