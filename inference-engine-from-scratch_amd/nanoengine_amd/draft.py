@@ -41,7 +41,8 @@ class DraftModelProposer:
     """Draft-model guesses for the slots of a batched verify step."""
 
     def __init__(self, model: Qwen3VerifyModel, pool: KVCachePool, allocator: PagedSlotAllocator,
-                 max_seqs: int, max_tokens: int, device: torch.device, k: int = 1) -> None:
+                 max_seqs: int, max_tokens: int, device: torch.device, k: int = 1,
+                 use_graph: bool = False) -> None:
         self.model = model
         self.pool = pool
         self.allocator = allocator
@@ -69,6 +70,12 @@ class DraftModelProposer:
         self.seeds: torch.Tensor | None = None
         self.steps: np.ndarray | None = None
         self.target_len: dict[int, int] = {}  # this proposal's target length per slot
+        # greedy guesses after the first: one row per slot, replayed from a HIP graph
+        self.use_graph = use_graph
+        self.max_tokens = max_tokens
+        self._dec: dict[str, torch.Tensor] | None = None
+        self._dec_graph: torch.cuda.CUDAGraph | None = None
+        model.ensure_rope(max_tokens)
 
     # ------------------------------------------------------------------ state
     def _sync(self, slot: int, sequence: Sequence) -> Sequence:
@@ -124,6 +131,12 @@ class DraftModelProposer:
         for s in want:
             self._sync(s, sequences[s])
             self.target_len[s] = sequences[s].num_tokens
+        if self.use_graph and self.temperature == 0.0 and want and max(want.values()) > 1:
+            for s, token in self._next_tokens(sorted(want)).items():  # catch-up: guess 0
+                self.drafts[s].token_ids.append(token)
+                guesses[s].append(token)
+            self._decode_graphed(want, guesses)
+            return guesses
         while True:
             live = [s for s in sorted(want) if len(guesses[s]) < want[s]]
             if not live:
@@ -157,6 +170,86 @@ class DraftModelProposer:
         torch.cuda.current_stream(self.device).synchronize()
         self.h_out.copy_(self.out_tokens)
         return {s: int(self.h_out[i, 0]) for i, s in enumerate(done)}
+
+    # ------------------------------------------------------- graphed decode steps
+    def _decode_body(self) -> None:
+        """One greedy decode row per slot (rows with q_len 0 are pads): forward, LM-head
+        argmax partials, the argmax through the acceptance kernel, fed back as the next
+        step's tokens."""
+        d = self._dec
+        n = self.max_seqs
+        batch = AttentionBatch(d["positions"], d["slots"], d["q_start"], d["q_len"], d["ctx"], d["tables"], 1,
+                               self.max_tokens)
+        hidden = self.model.forward(n, d["tokens"], batch, self.pool)
+        self.model.compute_logits(hidden, logits=False, argmax=d["partials"])
+        kernels.accept(self.no_drafts, self.zero_counts, self.last_rows, self.model.config.vocab_size,
+                       argmax_partials=d["partials"], temperature=0.0, out_tokens=d["out"], num_out=d["num_out"])
+        d["tokens"].copy_(d["out"][:, 0])
+
+    def _decode_graphed(self, want: dict[int, int], guesses: dict[int, list[int]]) -> None:
+        """Guesses 1 .. want[s] - 1 of every slot: the metadata of each step is staged on
+        the host up front, and each step replays the captured decode row per slot."""
+        dev, n, k = self.device, self.max_seqs, self.k
+        if self._dec is None:
+            i32 = dict(dtype=torch.int32, device=dev)
+            tiles = kernels.lm_head_num_tiles(self.model.config.vocab_size)
+            self._dec = dict(tokens=torch.zeros(n, **i32), positions=torch.zeros(n, **i32),
+                             slots=torch.zeros(n, **i32), q_start=torch.arange(n, **i32),
+                             q_len=torch.zeros(n, **i32), ctx=torch.zeros(n, **i32),
+                             tables=torch.zeros((n, self.max_blocks), **i32),
+                             partials=torch.zeros((n, tiles), dtype=torch.int64, device=dev),
+                             out=torch.zeros((n, 2), **i32), num_out=torch.zeros(n, **i32),
+                             guesses=torch.zeros((n, k), **i32))
+            self._dec_host = torch.zeros((k, 4, n), dtype=torch.int32, pin_memory=True)
+            self._dec_tokens = torch.zeros(n, dtype=torch.int32, pin_memory=True)
+            self._dec_tables = torch.zeros((n, self.max_blocks), dtype=torch.int32, pin_memory=True)
+        d = self._dec
+        stage = self._dec_host.numpy()
+        stage[:] = 0
+        steps = max(want.values())
+        toks = self._dec_tokens.numpy()
+        toks[:] = 0
+        for s, count in want.items():
+            draft = self.drafts[s]
+            length = self.target_len[s]
+            self._reserve(s, draft, length + count)
+            toks[s] = guesses[s][0]
+            pos = np.arange(length, length + count - 1)  # guess j reads guess j - 1 at L + j - 1
+            slot_ids = self.allocator.slots_for(draft, pos)
+            for j in range(1, count):
+                stage[j, 0, s] = length + j - 1
+                stage[j, 1, s] = slot_ids[j - 1]
+                stage[j, 2, s] = 1
+                stage[j, 3, s] = length + j
+        for j in range(1, steps):  # pads write the pool's scratch slot
+            stage[j, 1, stage[j, 2] == 0] = self.pool.scratch_slot
+        self._dec_tables.numpy()[:] = self.tables
+        d["tables"].copy_(self._dec_tables, non_blocking=True)
+        d["tokens"].copy_(self._dec_tokens, non_blocking=True)
+        for j in range(1, steps):
+            for i, name in enumerate(("positions", "slots", "q_len", "ctx")):
+                d[name].copy_(self._dec_host[j, i], non_blocking=True)
+            if self._dec_graph is None:
+                self._decode_body()  # eager once (allocates lazily created workspaces)
+                torch.cuda.current_stream(dev).synchronize()
+                graph = torch.cuda.CUDAGraph()
+                # re-stage this step's tokens: the eager pass already advanced them
+                d["tokens"].copy_(self._dec_tokens, non_blocking=True)
+                torch.cuda.current_stream(dev).synchronize()
+                with torch.cuda.graph(graph):
+                    self._decode_body()
+                self._dec_graph = graph
+            self._dec_graph.replay()
+            self.forwards += 1
+            d["guesses"][:, j].copy_(d["out"][:, 0])
+        torch.cuda.current_stream(dev).synchronize()
+        got = d["guesses"].cpu().numpy()
+        for s, count in want.items():
+            draft = self.drafts[s]
+            for j in range(1, count):
+                draft.token_ids.append(int(got[s, j]))
+                guesses[s].append(int(got[s, j]))
+            draft.num_cached_tokens = self.target_len[s] + count - 1
 
     def _forward(self, pieces, rows: int, done: list[int]) -> None:
         """One draft forward over packed pieces; the pieces that reach their draft's last

@@ -80,7 +80,7 @@ def create_verify_engine(config: Qwen3Config, state_dict: dict[str, torch.Tensor
         draft_model = Qwen3VerifyModel(draft_weights, rows, device)
         draft_allocator = PagedSlotAllocator(draft_blocks, settings.kv_block_size, device)
         proposer = DraftModelProposer(draft_model, draft_pool, draft_allocator, max_seqs, tokens, device,
-                                      k=settings.num_speculative_tokens)
+                                      k=settings.num_speculative_tokens, use_graph=settings.cuda_graphs)
     runner = VerifyRunner(model, pool, allocator, max_seqs, settings.num_speculative_tokens,
                           settings.ngram_max_size, settings.max_model_len, stop_token_ids,
                           use_graph=settings.cuda_graphs, proposer=proposer)
