@@ -366,6 +366,8 @@ def run_attention_kernel_only(torch, kind: str, layers: int, reps: int = 3):
             w.launch(p)
     torch.cuda.synchronize()
     _native.set_launch_timer("ne_paged_verify_attention", None)
+    if w.ws.error_flag() != 0:
+        raise RuntimeError(f"{kind} attention workload raised the workspace error flag (keys dropped)")
     dur = timer.durations_ms()
     avg_ms = sum(dur) / len(dur)
     achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
@@ -407,6 +409,8 @@ def run_attention_roofline(torch, reps: int = 5):
     torch.cuda.synchronize()
     for name in timers:
         _native.set_launch_timer(name, None)
+    if w.ws.error_flag() != 0:
+        raise RuntimeError("int8 attention workload raised the workspace error flag (keys dropped)")
     plan_ms = sum(timers["ne_paged_attention_plan"].durations_ms())
     calls = timers["ne_paged_verify_attention_planned"].durations_ms()
     avg_ms = (plan_ms + sum(calls)) / len(calls)
@@ -423,61 +427,143 @@ def run_attention_roofline(torch, reps: int = 5):
             "sum_ctx": int(w.ctx.sum())}
 
 
-def run_gemm_roofline(torch, layers: int = 28, reps: int = 10):
+class GemmWorkload:
+    """The verify step's projections at M = 64 x 5 = 320 rows and its LM head, each over
+    `layers` distinct random weights (so the last-level cache cannot hold them):
+
+      qkv_fused      QKV projection with QK-norm, RoPE and the int8 KV write in its epilogue
+                     (the call the step makes), N = 4096, K = 1024
+      gate_up_swiglu gate|up with the SwiGLU epilogue, N = 6144 (paired rows), K = 1024
+      o_proj         N = 1024, K = 2048, with its residual add + RMSNorm
+      down_proj      N = 1024, K = 3072, with its residual add + RMSNorm
+      lm_head        bf16 [151936, 1024] tied embedding, argmax partials only
+
+    Each launch function runs one call of its shape on layer `i`'s weights exactly as
+    Qwen3VerifyModel.forward does."""
+
+    def __init__(self, torch, layers: int = 28):
+        from nanoengine_amd import kernels
+        from nanoengine_amd.qwen3 import QWEN3_0_6B as cfg
+
+        self.torch = torch
+        self.kernels = kernels
+        self.layers = layers
+        dev = torch.device("cuda")
+        self.m = m = NUM_SEQS * (K_DRAFT + 1)
+        h, inter = cfg.hidden_size, cfg.intermediate_size
+        hq, hkv = cfg.num_attention_heads, cfg.num_key_value_heads
+        self.hq, self.hkv, self.eps = hq, hkv, cfg.rms_norm_eps
+        qkv = (hq + 2 * hkv) * cfg.head_dim
+        o_in = hq * cfg.head_dim
+        self.shapes = {"qkv_fused": (qkv, h), "gate_up_swiglu": (2 * inter, h), "o_proj": (h, o_in),
+                       "down_proj": (h, inter)}
+        self.weights = {}
+        for name, (n, k) in self.shapes.items():
+            self.weights[name] = [(torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev),
+                                   (torch.rand(n, device=dev) * 0.01 / math.sqrt(k)).to(torch.bfloat16))
+                                  for _ in range(layers)]
+        self.x = {k: torch.randn(m, k, device=dev).to(torch.bfloat16) for k in {h, o_in, inter}}
+        self.y = {"gate_up_swiglu": torch.empty(m, inter, dtype=torch.bfloat16, device=dev)}
+        self.res = torch.randn(m, h, device=dev).to(torch.bfloat16)
+        self.normed = torch.empty(m, h, dtype=torch.bfloat16, device=dev)
+        self.delta = torch.empty(m, h, dtype=torch.bfloat16, device=dev)
+        self.norm_w = torch.ones(h, dtype=torch.bfloat16, device=dev)
+        self.splits = {"o_proj": kernels.splitk_splits(m, h, o_in), "down_proj": kernels.splitk_splits(m, h, inter)}
+        self.partials = torch.empty(max(self.splits.values()) * m * h, dtype=torch.float32, device=dev)
+        # the fused QKV epilogue writes this step's keys/values into a 64-sequence pool
+        slots = 4096 * 16 + 1
+        self.kv = (torch.zeros(slots, hkv, 128, dtype=torch.int8, device=dev),
+                   torch.zeros(slots, hkv, 128, dtype=torch.int8, device=dev),
+                   torch.zeros(slots, hkv, dtype=torch.bfloat16, device=dev),
+                   torch.zeros(slots, hkv, dtype=torch.bfloat16, device=dev))
+        g = torch.Generator().manual_seed(3)
+        self.positions = torch.randint(64, 200, (m,), generator=g, dtype=torch.int32).to(dev)
+        self.slot_mapping = torch.randperm(slots - 1, generator=g)[:m].to(torch.int32).to(dev)
+        self.rope = kernels.rope_table(4096, cfg.rope_theta).to(dev)
+        self.q_out = torch.empty(m, hq, 128, dtype=torch.bfloat16, device=dev)
+        self.ones128 = torch.ones(128, dtype=torch.bfloat16, device=dev)
+        self.vocab = cfg.vocab_size
+        self.embed = (torch.randn(cfg.vocab_size, h, device=dev) * 0.02).to(torch.bfloat16)
+        self.hidden = (torch.randn(m, h, device=dev) * 0.02).to(torch.bfloat16)
+        self.argmax = torch.empty(m, kernels.lm_head_num_tiles(cfg.vocab_size), dtype=torch.int64, device=dev)
+
+    def flops(self, name: str) -> int:
+        if name == "lm_head":
+            return 2 * self.m * self.vocab * self.hidden.shape[1]
+        n, k = self.shapes[name]
+        return 2 * self.m * n * k
+
+    def weight_bytes(self, name: str) -> int:
+        if name == "lm_head":
+            return self.embed.numel() * 2
+        n, k = self.shapes[name]
+        return n * k + 2 * n
+
+    def launch(self, name: str, i: int) -> None:
+        from nanoengine_amd._native import EPILOGUE_SWIGLU
+
+        kernels = self.kernels
+        if name == "lm_head":
+            kernels.lm_head(self.hidden, self.embed, logits=False, argmax_partials=self.argmax)
+            return
+        w, s = self.weights[name][i]
+        n, k = self.shapes[name]
+        x = self.x[k]
+        if name == "qkv_fused":
+            kernels.w8a16_qkv_norm_rope_kv(x, w, s, self.hq, self.hkv, self.ones128, self.ones128, self.eps,
+                                           self.positions, self.rope, self.slot_mapping, *self.kv, q_out=self.q_out)
+        elif name == "gate_up_swiglu":
+            kernels.w8a16_gemm(x, w, s, epilogue=EPILOGUE_SWIGLU, out=self.y[name])
+        else:
+            splits = self.splits[name]
+            if splits > 1:
+                parts = self.partials[: splits * self.m * n]
+                kernels.w8a16_gemm_splitk(x, w, s, splits, out=parts)
+                kernels.splitk_add_rmsnorm(self.res, parts, splits, self.norm_w, self.eps, out=self.normed)
+            else:
+                kernels.w8a16_gemm(x, w, s, out=self.delta)
+                kernels.add_rmsnorm(self.res, self.delta, self.norm_w, self.eps, out=self.normed)
+
+    def launch_all(self, name: str) -> None:
+        for i in range(1 if name == "lm_head" else self.layers):
+            self.launch(name, i)
+
+
+GEMM_NAMES = ("qkv_fused", "gate_up_swiglu", "o_proj", "down_proj", "lm_head")
+
+
+def run_gemm_roofline(torch, layers: int = 28, reps: int = 10, counters: dict | None = None):
     """The W8A16 projections and the LM head of the verify step at M = 64 x 5 = 320 rows,
     kernel-only: `layers` calls with distinct random weights captured in one HIP graph
-    and replayed `reps` times, so the time is GPU time without host launch cost."""
-    from nanoengine_amd import kernels
-    from nanoengine_amd._native import EPILOGUE_SWIGLU
-    from nanoengine_amd.qwen3 import QWEN3_0_6B as cfg
-
-    dev = torch.device("cuda")
-    m = NUM_SEQS * (K_DRAFT + 1)
-    h, inter = cfg.hidden_size, cfg.intermediate_size
-    qkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
-    o_in = cfg.num_attention_heads * cfg.head_dim
-    shapes = [("qkv", qkv, h, 0), ("gate_up_swiglu", 2 * inter, h, 0), ("o_proj_splitk4", h, o_in, 4),
-              ("down_splitk4", h, inter, 4)]
+    and replayed `reps` times, so the time is GPU time without host launch cost.  o_proj
+    and down_proj include their residual add + RMSNorm (what the step runs after them).
+    `counters` (from measure_counters) adds each shape's rocprofv3 counter readings."""
+    w = GemmWorkload(torch, layers=layers)
     out = {}
-    for name, n, k, splits in shapes:
-        ws = [(torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev),
-               (torch.rand(n, device=dev) * 0.01).to(torch.bfloat16)) for _ in range(layers)]
-        x = torch.randn(m, k, device=dev).to(torch.bfloat16)
-        part = torch.empty(max(splits, 1), m, n, dtype=torch.float32, device=dev)
-        y = torch.empty(m, n // 2 if name.startswith("gate") else n, dtype=torch.bfloat16, device=dev)
-
-        def run(w):
-            if splits:
-                kernels.w8a16_gemm_splitk(x, w[0], w[1], splits, out=part)
-            else:
-                kernels.w8a16_gemm(x, w[0], w[1], epilogue=EPILOGUE_SWIGLU if name.startswith("gate") else 0,
-                                   out=y)
-
-        us = _graph_time_us(torch, lambda: [run(w) for w in ws], reps) / layers
-        flops = 2 * m * n * k
-        out[name] = {"m": m, "n": n, "k": k, "splits": splits, "avg_us": round(us, 2),
-                     "TFLOP_s": round(flops / us / 1e6, 1), "mfma_frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
-                     "weight_GB_s": round(n * k / us / 1e3, 1)}
-        del ws
-    v = cfg.vocab_size
-    embed = (torch.randn(v, h, device=dev) * 0.02).to(torch.bfloat16)
-    hid = (torch.randn(m, h, device=dev) * 0.02).to(torch.bfloat16)
-    parts = torch.empty(m, kernels.lm_head_num_tiles(v), dtype=torch.int64, device=dev)
-    us = _graph_time_us(torch, lambda: kernels.lm_head(hid, embed, logits=False, argmax_partials=parts), reps)
-    out["lm_head_argmax"] = {"m": m, "n": v, "k": h, "avg_us": round(us, 2),
-                             "TFLOP_s": round(2 * m * v * h / us / 1e6, 1),
-                             "mfma_frac": round(2 * m * v * h / us / 1e6 / BF16_PEAK_TFLOPS, 4),
-                             "weight_GB_s": round(2 * v * h / us / 1e3, 1),
-                             "hbm_frac": round(2 * v * h / us / 1e3 / HBM_PEAK_GBS, 4)}
-    del embed
+    for name in GEMM_NAMES:
+        calls = 1 if name == "lm_head" else layers
+        us = _graph_time_us(torch, lambda: w.launch_all(name), reps) / calls
+        flops = w.flops(name)
+        entry = {"avg_us": round(us, 2), "TFLOP_s": round(flops / us / 1e6, 1),
+                 "mfma_frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                 "weight_GB_s": round(w.weight_bytes(name) / us / 1e3, 1)}
+        if name != "lm_head":
+            entry["n"], entry["k"] = w.shapes[name]
+        entry["m"] = w.m
+        if counters is not None and name in counters:
+            entry["counters"] = counters[name]
+        out[name] = entry
+    del w
     torch.cuda.empty_cache()
-    qkv_gu = out["qkv"], out["gate_up_swiglu"]
-    flops = sum(2 * e["m"] * e["n"] * e["k"] for e in qkv_gu)
-    us = sum(e["avg_us"] for e in qkv_gu)
-    return {"kernel": "proj_kernel (W8A16) and lm_head_kernel", "bound": "mfma",
-            "achieved": round(flops / us / 1e6, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+    proj = [n for n in GEMM_NAMES if n != "lm_head"]
+    flops = sum(2 * out[n]["m"] * out[n]["n"] * out[n]["k"] for n in proj)
+    us = sum(out[n]["avg_us"] for n in proj)
+    return {"kernel": "W8A16 projections (qkv fused, gate|up SwiGLU, o, down incl. add+RMSNorm) and lm_head_kernel",
+            "bound": "mfma", "achieved": round(flops / us / 1e6, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
-            "note": "achieved/frac over the QKV and gate|up projections; per-shape detail below",
+            "per_layer_us": round(us, 2),
+            "note": "achieved/frac over one layer's four projection calls (MFMA TFLOP/s at M=320); per-shape "
+                    "detail, counter traffic and MFMA busy below",
             "shapes": out}
 
 
@@ -502,63 +588,160 @@ def _graph_time_us(torch, body, reps: int) -> float:
     return start.elapsed_time(stop) * 1e3 / reps
 
 
-def pmc_child(torch) -> int:
-    """What the rocprofv3 --pmc passes profile: one call per pool, then a copy of
-    CALIBRATION_BYTES whose counter reading calibrates the scale."""
+MARKER_BYTES = 4096
+# counter passes, each its own child run (rocprofv3 does not split counters over passes):
+# HBM bytes, then MFMA / LDS activity, then vector-L1 -> L2 requests and L2 hits
+PMC_PASSES = {
+    "fetch": ("FETCH_SIZE",),
+    "write": ("WRITE_SIZE",),
+    "sq": ("MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE",
+           "SQ_BUSY_CU_CYCLES"),
+    "l2": ("TCP_TCC_READ_REQ_sum", "TCP_TCC_READ_REQ_LATENCY_sum", "TCC_HIT_sum", "TCC_MISS_sum"),
+}
+PMC_GROUPS = ("attention",) + GEMM_NAMES
+
+
+def pmc_child(torch, groups: tuple[str, ...]) -> int:
+    """What the rocprofv3 --pmc passes profile: each group's calls (attention: one plan and
+    28 planned calls; each projection: 28 distinct-weight calls; the LM head: one call),
+    every group followed by a MARKER_BYTES copy, then a copy of CALIBRATION_BYTES whose
+    counter reading calibrates the byte counters."""
     import ctypes
 
     from nanoengine_amd import _native
 
-    w = AttentionWorkload(torch)
-    w.plan()
-    for p in w.pools:
-        w.launch(p, planned=True)
-    torch.cuda.synchronize()
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    m = torch.empty(MARKER_BYTES, dtype=torch.uint8, device="cuda")
+    marker = lambda: _native.call("ne_copy_bytes", ctypes.c_void_p(m.data_ptr()),
+                                  ctypes.c_void_p(m.data_ptr() + MARKER_BYTES // 2), MARKER_BYTES // 2, stream())
+    calls = {}
+    if "attention" in groups:
+        w = AttentionWorkload(torch)
+        w.plan()
+        for p in w.pools:
+            w.launch(p, planned=True)
+        torch.cuda.synchronize()
+        marker()
+        calls["attention"] = len(w.pools)
+        del w
+    gemm = [g for g in groups if g in GEMM_NAMES]
+    if gemm:
+        gw = GemmWorkload(torch)
+        for name in gemm:
+            gw.launch_all(name)
+            torch.cuda.synchronize()
+            marker()
+            calls[name] = 1 if name == "lm_head" else gw.layers
+        del gw
+    torch.cuda.empty_cache()
     a = torch.empty(CALIBRATION_BYTES, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
-    _native.call("ne_copy_bytes", ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()), a.numel(),
-                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _native.call("ne_copy_bytes", ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()), a.numel(), stream())
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_child": "done", "launches": len(w.pools)}), flush=True)
+    print(json.dumps({"pmc_child": "done", "calls": calls}), flush=True)
     return 0
 
 
-def measure_traffic() -> dict | None:
-    """HBM bytes per attention call from two rocprofv3 --pmc passes over `--pmc-child`
-    (run before this process touches the GPU).  Each counter is scaled by the reading
-    it gives for the CALIBRATION_BYTES copy (which reads and writes that many bytes)."""
+def _pmc_run(prof: str, counters: tuple[str, ...], groups: tuple[str, ...]) -> list[dict] | None:
+    """One rocprofv3 --pmc child run; the per-dispatch rows of our kernels in dispatch order."""
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
+        cmd = ["timeout", "-s", "KILL", "150", prof, "--pmc", *counters, "--output-format", "csv", "-d", tmp,
+               "-o", "run", "--", sys.executable, str(ROOT / "bench.py"), "--pmc-child", "--pmc-groups",
+               ",".join(groups)]
+        log(f"pmc pass {' '.join(counters)}")
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        found = list(Path(tmp).rglob("*counter_collection.csv"))
+        if r.returncode != 0 and not found:
+            log(f"pmc pass failed ({r.returncode}): {r.stderr[-400:]}")
+            return None
+        rows = list(csv.DictReader(open(found[0])))
+    rows = [x for x in rows if x["Kernel_Name"].removeprefix("void ").startswith("ne::")]
+    rows.sort(key=lambda x: int(x["Dispatch_Id"]))
+    return rows
+
+
+def _split_groups(rows: list[dict], groups: tuple[str, ...]):
+    """Dispatches between marker copies, by group, plus the calibration copy's rows."""
+    by_dispatch: dict[int, list[dict]] = {}
+    for x in rows:
+        by_dispatch.setdefault(int(x["Dispatch_Id"]), []).append(x)
+    out = {g: [] for g in groups}
+    gi = 0
+    calib = None
+    for did in sorted(by_dispatch):
+        recs = by_dispatch[did]
+        if "copy_kernel" in recs[0]["Kernel_Name"]:
+            if gi < len(groups):
+                gi += 1
+            else:
+                calib = recs
+            continue
+        if gi < len(groups):
+            out[groups[gi]].append(recs)
+    return out, calib
+
+
+def measure_counters(groups: tuple[str, ...] = PMC_GROUPS) -> dict | None:
+    """Per-call counter readings of each group's kernels from the PMC_PASSES rocprofv3
+    runs over `--pmc-child` (made before this process touches the GPU).
+
+    fetch_bytes / write_bytes: HBM bytes per call, FETCH_SIZE / WRITE_SIZE scaled by
+    the reading each gives for the CALIBRATION_BYTES copy (which reads and writes that
+    many bytes).  mfma_util: MfmaUtil (MFMA busy cycles over GPU-active cycles x SIMDs),
+    averaged over the group's GEMM dispatches.  l1_l2_read_bytes: vector-L1 -> L2 read
+    requests per call, scaled to bytes by the copy's requests per byte."""
     prof = shutil.which("rocprofv3")
     if prof is None:
-        log("rocprofv3 not found: traffic not measured")
+        log("rocprofv3 not found: counters not measured")
         return None
-    per_counter = {}
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
-            cmd = ["timeout", "-s", "KILL", "120", prof, "--pmc", counter, "--output-format", "csv", "-d", tmp,
-                   "-o", "run", "--", sys.executable, str(ROOT / "bench.py"), "--pmc-child"]
-            log(f"pmc pass {counter}")
-            r = subprocess.run(cmd, capture_output=True, text=True)
-            found = list(Path(tmp).rglob("*counter_collection.csv"))
-            if r.returncode != 0 and not found:
-                log(f"pmc pass {counter} failed ({r.returncode}): {r.stderr[-400:]}")
-                return None
-            rows = list(csv.DictReader(open(found[0])))
-        ours = [x for x in rows if x["Kernel_Name"].removeprefix("void ").startswith("ne::")]
-        attn = [float(x["Counter_Value"]) for x in ours if "attention" in x["Kernel_Name"]]
-        calib = [float(x["Counter_Value"]) for x in ours if "copy_kernel" in x["Kernel_Name"]]
-        # one main attention kernel per call (the merge kernel, when launched, adds its own
-        # traffic to the same call)
-        launches = sum(1 for x in ours if "paged_attention" in x["Kernel_Name"])
-        if not attn or not calib or not launches:
-            log(f"pmc pass {counter}: kernels not found in the counter output")
+    res: dict[str, dict] = {g: {"calls": 0} for g in groups}
+    for pass_name, counters in PMC_PASSES.items():
+        rows = _pmc_run(prof, counters, groups)
+        if rows is None:
             return None
-        scale = (CALIBRATION_BYTES / 1024.0) / calib[0]  # true KiB per counted KiB
-        per_counter[counter] = {"kib_per_launch": sum(attn) / launches, "scale": scale,
-                                "bytes_per_launch": sum(attn) / launches * scale * 1024.0}
-    return {"fetch_bytes": int(per_counter["FETCH_SIZE"]["bytes_per_launch"]),
-            "write_bytes": int(per_counter["WRITE_SIZE"]["bytes_per_launch"]),
-            "fetch_scale": round(per_counter["FETCH_SIZE"]["scale"], 4),
-            "write_scale": round(per_counter["WRITE_SIZE"]["scale"], 4)}
+        per_group, calib = _split_groups(rows, groups)
+        if calib is None:
+            log(f"pmc pass {pass_name}: calibration copy not found")
+            return None
+
+        def total(recs_list, name):
+            return sum(float(r["Counter_Value"]) for recs in recs_list for r in recs if r["Counter_Name"] == name)
+
+        for g in groups:
+            disp = per_group[g]
+            calls = 1 if g == "lm_head" else 28
+            res[g]["calls"] = calls
+            res[g]["dispatches_per_call"] = round(len(disp) / calls, 2)
+            if pass_name == "fetch":
+                scale = (CALIBRATION_BYTES / 1024.0) / total([calib], "FETCH_SIZE")
+                res[g]["fetch_bytes"] = int(total(disp, "FETCH_SIZE") * scale * 1024 / calls)
+                res[g]["fetch_scale"] = round(scale, 4)
+            elif pass_name == "write":
+                scale = (CALIBRATION_BYTES / 1024.0) / total([calib], "WRITE_SIZE")
+                res[g]["write_bytes"] = int(total(disp, "WRITE_SIZE") * scale * 1024 / calls)
+                res[g]["write_scale"] = round(scale, 4)
+            elif pass_name == "sq":
+                # the main (longest) kernel of each call: the first dispatch of the call
+                mains = [recs for recs in disp if not any(s in recs[0]["Kernel_Name"] for s in
+                                                          ("rmsnorm", "plan_kernel", "merge"))]
+                util = [float(r["Counter_Value"]) for recs in mains for r in recs if r["Counter_Name"] == "MfmaUtil"]
+                res[g]["mfma_util_pct"] = round(sum(util) / len(util), 2) if util else None
+                res[g]["mfma_mops_bf16"] = int(total(disp, "SQ_INSTS_VALU_MFMA_MOPS_BF16") / calls)
+                res[g]["lds_bank_conflict_cycles"] = int(total(disp, "SQ_LDS_BANK_CONFLICT") / calls)
+                res[g]["lds_active_cycles"] = int(total(disp, "SQ_LDS_IDX_ACTIVE") / calls)
+                res[g]["busy_cu_quad_cycles"] = int(total(disp, "SQ_BUSY_CU_CYCLES") / calls)
+            else:
+                per_byte = total([calib], "TCP_TCC_READ_REQ_sum") / CALIBRATION_BYTES
+                req = total(disp, "TCP_TCC_READ_REQ_sum")
+                res[g]["l1_l2_read_req"] = int(req / calls)
+                res[g]["l1_l2_read_bytes"] = int(req / per_byte / calls) if per_byte else None
+                res[g]["l2_hit_pct"] = round(100 * total(disp, "TCC_HIT_sum") / max(
+                    total(disp, "TCC_HIT_sum") + total(disp, "TCC_MISS_sum"), 1), 2)
+                res[g]["l1_l2_read_latency_cycles"] = round(total(disp, "TCP_TCC_READ_REQ_LATENCY_sum") / max(req, 1), 1)
+    for g in groups:
+        if "fetch_bytes" in res[g] and "write_bytes" in res[g]:
+            res[g]["traffic"] = res[g]["fetch_bytes"] + res[g]["write_bytes"]
+    return res
 
 
 class TorchReferenceStep:
@@ -778,6 +961,7 @@ def main() -> int:
     parser.add_argument("--no-torch-baseline", action="store_true")
     parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
     parser.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    parser.add_argument("--pmc-groups", default=",".join(PMC_GROUPS), help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the verify step "
@@ -786,11 +970,12 @@ def main() -> int:
     if args.pmc_child:
         import torch
 
-        return pmc_child(torch)
+        return pmc_child(torch, tuple(args.pmc_groups.split(",")))
     # counter passes first, as child processes, before this process initialises the GPU
-    traffic = None
-    if args.only in ("all", "attention") and not args.no_traffic:
-        traffic = measure_traffic()
+    counters = None
+    if args.only in ("all", "attention", "gemm") and not args.no_traffic:
+        groups = PMC_GROUPS if args.only == "all" else (("attention",) if args.only == "attention" else GEMM_NAMES)
+        counters = measure_counters(groups)
     import torch
 
     if not torch.cuda.is_available():
@@ -804,9 +989,9 @@ def main() -> int:
     if args.only in ("all", "attention"):
         attention = run_attention_roofline(torch)
         attention["traffic"] = None
-        if traffic is not None:
-            attention["traffic"] = traffic["fetch_bytes"] + traffic["write_bytes"]
-            attention["traffic_detail"] = traffic
+        if counters is not None and "attention" in counters:
+            attention["traffic"] = counters["attention"].get("traffic")
+            attention["counters"] = counters["attention"]
         log(f"attention: {attention['avg_us']} us, {attention['achieved']} GB/s")
         attention["bf16_config"] = run_attention_kernel_only(torch, "bf16", layers=28)
         log(f"attention bf16: {attention['bf16_config']['avg_us']} us")
@@ -814,7 +999,7 @@ def main() -> int:
         log(f"attention long context: {attention['long_context_config']['avg_us']} us")
     gemm = None
     if args.only in ("all", "gemm"):
-        gemm = run_gemm_roofline(torch)
+        gemm = run_gemm_roofline(torch, counters=counters)
         log(f"gemm: {gemm['achieved']} TFLOP/s over QKV and gate|up")
     torch_base = None
     if args.only in ("all", "baseline") and not args.no_torch_baseline:

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 5
+#define NE_ABI_VERSION 6
 
 /* status codes */
 #define NE_OK 0
@@ -44,10 +44,6 @@ extern "C" {
 /* GEMM epilogues */
 #define NE_EPILOGUE_STORE 0  /* y = bf16(acc * scale[n]) */
 #define NE_EPILOGUE_SWIGLU 1 /* y[:, j] = bf16(silu(gate_j) * up_j), weight rows paired per 16 */
-
-/* acceptance modes */
-#define NE_ACCEPT_GREEDY 0
-#define NE_ACCEPT_SAMPLED 1
 
 int ne_abi_version(void);
 const char* ne_last_error(void);
@@ -257,38 +253,45 @@ int ne_w8a16_qkv_norm_rope_kv(const void* x, int64_t ldx, const int8_t* w, const
 
 /*
  * A9/A10 - fused acceptance (replaces verify_proposal and the sampling helpers,
- * ne/engine/speculative/verifier.py:21-60, ne/engine/sampling.py:30-42, and the
+ * ne/engine/speculative/verifier.py:21-60, ne/engine/sampling.py:21-42, and the
  * rollback of ne/engine/speculative/speculative_generator.py:78-83).
  * Sequence b has num_drafts[b] guesses drafts[b, :] and target rows
  * row_start[b] .. row_start[b]+num_drafts[b] (one more than its guesses).
- * Greedy: target token of a row = argmax of its bf16 logits, first index on
- * ties, from `logits` or, when logits is null, from the ne_lm_head partials.
- * Keep guesses while guess == target; then append the target of the first
- * mismatching row (or the bonus row).
- * Sampled (temperature > 0): p = softmax(fp32(logit) / T) with the fixed-order
- * contract documented in accept.hip; guess i is kept iff p_i >= 1 or
- * (p_i > 0 and u_i < p_i); a rejection resamples from p with the guess removed
- * (p itself if that is empty) and the bonus samples p of the last row, both by
- * inverse CDF with u_draw.  Uniforms u_i, u_draw come from Philox4x32-10 keyed
- * by seeds[b] at counter (steps[b], j/4), word j%4, j = i (guesses) and 63.
- * With draft_logits (sampled only; guesses drawn by a draft model): the draft's
- * logits for guess i of sequence b are row draft_row_start[b] + i (stride
- * ld_draft); q = its softmax under the same contract; guess i is kept iff
- * a = min(p/max(q,1e-12), 1) >= 1 or (a > 0 and u_i < a), and a rejection draws
- * from max(p - q, 0) (p when that is empty), verifier.py:36-56.  Null: the
+ * temperature[b] (device fp32; null: every sequence greedy) selects per sequence:
+ * Greedy (temperature 0): target token of a row = argmax of its bf16 logits, first
+ * index on ties, from `logits` or, when logits is null, from the ne_lm_head
+ * partials.  Keep guesses while guess == target; then append the target of the
+ * first mismatching row (or the bonus row).
+ * Sampled (temperature > 0): p' = softmax(fp32(logit) / T), cut to top_p[b]
+ * (device fp32; null: 1) and renormalised (sampling.py:21-38), under the fixed-order
+ * contract documented in accept.hip; guess i is kept iff p'_i >= 1 or (p'_i > 0 and
+ * u_i < p'_i); a rejection resamples from p' with the guess removed (p' itself if
+ * that is empty) and the bonus samples p' of the last row, both by inverse CDF with
+ * u_draw.  Uniforms u_i, u_draw come from Philox4x32-10 keyed by seeds[b] at
+ * counter (steps[b], j/4), word j%4, j = i (guesses) and 63.  any_sampled must be
+ * non-zero when some temperature is positive (logits, seeds and steps are then
+ * required).
+ * draft_rows (sampled sequences; guesses drawn by a draft model): the draft's
+ * distribution for guess i of sequence b is row draft_row_start[b] + i (stride
+ * ld_draft) -- bf16 logits (draft_dtype NE_DTYPE_BF16; q = the same temperature /
+ * top-p softmax) or fp32 probabilities used as given (NE_DTYPE_FP32); guess i is
+ * kept iff a = min(p'/max(q,1e-12), 1) >= 1 or (a > 0 and u_i < a), and a rejection
+ * draws from max(p' - q, 0) (p' when that is empty), verifier.py:36-56.  Null: the
  * guesses are deterministic (one-hot q), as above.
  * Outputs: out_tokens[b, 0..num_out[b]-1] (kept guesses + 1 target token),
- * the rest of the row [b, 0..max_drafts] set to -1; num_out[b] = kept + 1.  When history is given, the kept tokens and the target
- * token are appended at history[b, history_len[b]..] and history_len[b] and
- * num_cached[b] (set to history_len_before + kept) are updated; a sequence
- * whose history_len is 0 is inactive (num_out 0, nothing written).
+ * the rest of the row [b, 0..max_drafts] set to -1; num_out[b] = kept + 1.  When
+ * history is given, the kept tokens and the target token are appended at
+ * history[b, history_len[b]..] (within the row's history_stride tokens) and
+ * history_len[b] and num_cached[b] (set to history_len_before + kept) are updated; a
+ * sequence whose history_len is 0 is inactive (num_out 0, nothing written).
  */
-int ne_accept(int32_t mode, const void* logits, int64_t ld_logits, const uint64_t* argmax_partials,
+int ne_accept(const void* logits, int64_t ld_logits, const uint64_t* argmax_partials,
               int32_t num_tiles, int32_t vocab, const int32_t* drafts, int32_t max_drafts,
               const int32_t* num_drafts, const int32_t* row_start, int32_t num_seqs,
-              float temperature, const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens,
-              int32_t* num_out, int32_t* history, int64_t history_stride, int32_t* history_len,
-              int32_t* num_cached, const void* draft_logits, int64_t ld_draft,
+              const float* temperature, const float* top_p, int32_t any_sampled,
+              const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens, int32_t* num_out,
+              int32_t* history, int64_t history_stride, int32_t* history_len, int32_t* num_cached,
+              const void* draft_rows, int32_t draft_dtype, int64_t ld_draft,
               const int32_t* draft_row_start, void* stream);
 
 /*

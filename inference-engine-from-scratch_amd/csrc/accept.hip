@@ -2,11 +2,11 @@
 // rejection sampling, correction/bonus token, KV-count rollback and history
 // append, one 256-thread work-group per sequence.
 //
-// Restates verify_proposal (ne/engine/speculative/verifier.py:27-60) for the
-// n-gram proposer, whose draft distribution is one-hot: the acceptance
-// probability of guess g is min(1, p[g]), the residual max(p - onehot(g), 0)
-// is p with g removed, and the rollback is num_cached = len_before + kept
-// (ne/engine/speculative/speculative_generator.py:78-83).
+// Restates verify_proposal (ne/engine/speculative/verifier.py:27-60) and
+// compute_token_probabilities / apply_top_p (ne/engine/sampling.py:21-38); the
+// rollback is num_cached = len_before + kept
+// (ne/engine/speculative/speculative_generator.py:78-83).  Each sequence has its
+// own temperature and top-p, so greedy and sampled requests share one call.
 //
 // Greedy (temperature 0, ne/engine/sampling.py:32-34): target token of a row is
 // the argmax of its bf16 logits, first index on ties (torch.argmax order).
@@ -17,27 +17,35 @@
 // bit with the CPU oracle:
 //   z_j  = fp32(logit_j) / T                  (IEEE fp32 division)
 //   e_j  = cephes_exp(z_j - max_j z_j)        (Cephes expf, Moshier; 0 below -86)
-//   S_c  = sequential fp32 sum of e_j over chunk c = [c*CH, min((c+1)*CH, V)),
-//          CH = ceil(V / 256), c = 0..255;  Z = sequential sum of S_0..S_255
-//   guess g of row i is kept iff p >= 1 or (p > 0 and u_i < p), p = e_g / Z
-//   draw from row r excluding x (x = -1: none): r_j = e_j, r_x = 0; chunk sums
-//          R_c and total R as above (if R <= 0 the exclusion is dropped);
-//          t = u_draw * R; c* = first chunk with prefix_c + R_c > t (prefix
-//          summed sequentially); j = first index in c* with prefix_c* + q_j > t,
-//          q_j the sequential in-chunk sum from the chunk start.  If no chunk
-//          qualifies (rounding), the last index with r_j > 0 is taken.
+//   chunked total of a row vector w: S_c = sequential fp32 sum of w_j over chunk
+//          c = [c*CH, min((c+1)*CH, V)), CH = ceil(V / 256), c = 0..255; total =
+//          sequential sum of S_0..S_255.  Z = chunked total of e.
+//   top-p (top_p < 1): tokens rank by bf16 logit (larger first, -0 as +0), ties by
+//          index.  M(v) = chunked total of e_j over tokens whose 16-bit key exceeds
+//          v; thr = top_p * Z; tau = smallest key v with M(v) < thr (bisection over
+//          the 65536 keys); m = number of r in [0, H) with M(tau) + r * E(tau) < thr
+//          (H tokens of key tau, E(tau) their e value); kept: key > tau, or key ==
+//          tau and fewer than m tokens of key tau precede it.  Without top-p every
+//          token is kept.  w_j = e_j when kept, else 0; K = chunked total of w;
+//          p'_j = w_j / K.
+//   guess g of row i (n-gram, one-hot draft) is kept iff a >= 1 or (a > 0 and
+//          u_i < a), a = p'_g; a rejection draws from w with g removed.
+//   draw from a weight row r with x removed (x = -1: none): R = chunked total (if
+//          R <= 0 the exclusion is dropped); t = u_draw * R; c* = first chunk with
+//          prefix_c + R_c > t (prefix summed sequentially); j = first index in c*
+//          with prefix_c* + q_j > t, q_j the sequential in-chunk sum from the chunk
+//          start.  If no chunk qualifies (rounding), the last index with r_j > 0.
 //   uniforms: Philox4x32-10 (Salmon et al., SC'11), key = seed, counter =
 //          (step lo, step hi, j / 4, 0), word j % 4, u = (word >> 8) * 2^-24;
 //          j = i for guess i, j = 63 for the draw.
-//   with draft rows (a draft model's logits for each guess, the same T): f_j and
-//          Zq as e_j and Z over the draft row; p = e_g / Z, q = max(f_g / Zq, 1e-12),
-//          a = min(p / q, 1); guess i is kept iff a >= 1 or (a > 0 and u_i < a)
-//          (verifier.py:44-51).  At the first rejection the draw is from the
-//          residual r_j = max(e_j / Z - f_j / Zq, 0) (each term one fp32 op), chunk
-//          sums and total as above, falling back to e when the total is not > 0
-//          (verifier.py:52-56).
-// FP contraction is disabled in this file's arithmetic on that path so that
-// every operation is a single IEEE-rounded fp32 op, as in the C oracle.
+//   with draft rows (a draft model's distribution per guess): bf16 draft logits
+//          give q' by the same procedure (same T and top-p); fp32 rows are
+//          probabilities q used as given.  a = min(p'_g / max(q_g, 1e-12), 1);
+//          a rejection draws from r_j = max(p'_j - q_j, 0) (p'_j = w_j / K one fp32
+//          division, q'_j likewise, the difference one op), falling back to w when
+//          r has no mass (verifier.py:44-56).
+// FP contraction is disabled in this file's arithmetic so that every operation on
+// that path is a single IEEE-rounded fp32 op, as in the C oracle.
 #include "ne_common.hpp"
 
 namespace ne {
@@ -99,6 +107,16 @@ __device__ __forceinline__ uint64_t key_of(float v, uint32_t idx) {
   return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - idx);
 }
 
+// 16-bit order key of a bf16 logit (larger logit, larger key; -0 as +0) and back
+__device__ __forceinline__ uint32_t key16(uint16_t b) {
+  if ((b & 0x7FFFu) == 0) b = 0;
+  return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
+}
+
+__device__ __forceinline__ uint16_t bf16_of_key16(uint32_t k) {
+  return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k & 0xFFFFu);
+}
+
 __device__ uint64_t block_max_u64(uint64_t v, uint64_t* s_red) {
   for (int o = 32; o >= 1; o >>= 1) {
     const uint32_t lo = __shfl_xor((uint32_t)v, o);
@@ -125,7 +143,6 @@ __device__ float block_max_f32(float v, float* s_red) {
 }
 
 struct AcceptParams {
-  int mode;
   const uint16_t* logits;
   int64_t ld;
   const uint64_t* partials;
@@ -135,7 +152,8 @@ struct AcceptParams {
   int max_drafts;
   const int32_t* num_drafts;
   const int32_t* row_start;
-  float temperature;
+  const float* temperature;  // per sequence; null: every sequence greedy
+  const float* top_p;        // per sequence; null: 1
   const uint64_t* seeds;
   const uint64_t* steps;
   int32_t* out_tokens;
@@ -144,21 +162,21 @@ struct AcceptParams {
   int64_t hist_stride;
   int32_t* history_len;
   int32_t* num_cached;
-  const uint16_t* draft_logits;  // sampled mode: the draft's row per guess, or null (one-hot)
+  const void* draft_rows;  // sampled: the draft's distribution per guess, or null (one-hot)
+  int draft_dtype;         // NE_DTYPE_BF16: logits, NE_DTYPE_FP32: probabilities
   int64_t dld;
   const int32_t* draft_row_start;
 };
-
-__device__ __forceinline__ float logit_at(const AcceptParams& p, int row, int j) {
-  return bf16_to_f32(p.logits[(int64_t)row * p.ld + j]);
-}
 
 // greedy target of one row: argmax over bf16 logits or the LM-head partials
 __device__ int row_argmax(const AcceptParams& p, int row, uint64_t* s_red) {
   uint64_t best = 0;
   if (p.logits != nullptr) {
-    for (int j = threadIdx.x; j < p.vocab; j += kThreads)
-      best = best > key_of(logit_at(p, row, j), j) ? best : key_of(logit_at(p, row, j), j);
+    const uint16_t* src = p.logits + (int64_t)row * p.ld;
+    for (int j = threadIdx.x; j < p.vocab; j += kThreads) {
+      const uint64_t k = key_of(bf16_to_f32(src[j]), j);
+      best = best > k ? best : k;
+    }
   } else {
     const uint64_t* src = p.partials + (int64_t)row * p.num_tiles;
     for (int t = threadIdx.x; t < p.num_tiles; t += kThreads) best = best > src[t] ? best : src[t];
@@ -167,51 +185,151 @@ __device__ int row_argmax(const AcceptParams& p, int row, uint64_t* s_red) {
   return (int)(0xFFFFFFFFu - (uint32_t)best);
 }
 
-// fp32 softmax pieces of one row under the fixed-order contract
-struct RowSums {
-  float mx;  // max z
-  float Z;   // total of chunk sums
+// ---- one row's distribution under the contract ------------------------------------
+// LDS of a distribution: its kept-weight chunk sums and, with top-p, the number of
+// threshold-key tokens before each chunk (the tie rank at the chunk's start).
+struct DistLds {
+  float chunk[kChunks];
+  int tie_base[kChunks];
 };
 
-__device__ __forceinline__ float logit_of(const uint16_t* base, int64_t ld, int row, int j) {
-  return bf16_to_f32(base[(int64_t)row * ld + j]);
+struct Dist {
+  const uint16_t* row;
+  float T, mx, total;
+  bool topp;
+  uint32_t tau;
+  int m;
+};
+
+__device__ __forceinline__ int chunk_len(int V) { return (V + kChunks - 1) / kChunks; }
+
+__device__ __forceinline__ float dist_e(const Dist& d, int j) {
+  return cephes_exp(bf16_to_f32(d.row[j]) / d.T - d.mx);
 }
 
-// over the target's logits (base = p.logits) or the draft's (base = p.draft_logits)
-__device__ RowSums row_sums(const AcceptParams& p, const uint16_t* base, int64_t ld, int row, float* s_chunk,
-                            float* s_redf) {
-  const int V = p.vocab;
-  const int CH = (V + kChunks - 1) / kChunks;
-  float m = -INFINITY;
-  for (int j = threadIdx.x; j < V; j += kThreads) m = fmaxf(m, logit_of(base, ld, row, j) / p.temperature);
-  const float mx = block_max_f32(m, s_redf);
-  const int c = threadIdx.x;
+// every thread: the sequential fp32 sum of v[0..255] (from LDS)
+__device__ __forceinline__ float lds_total(const float* v) {
+  float t = 0.f;
+  for (int c = 0; c < kChunks; ++c) t = t + v[c];
+  return t;
+}
+
+// M(v): chunked total of e over tokens with key > v (all threads; uniform result)
+__device__ float masked_total(const Dist& d, int V, uint32_t v, float* s_tmp) {
+  const int CH = chunk_len(V);
+  const int lo = threadIdx.x * CH, hi = min(lo + CH, V);
   float s = 0.f;
-  const int lo = c * CH, hi = min(lo + CH, V);
-  for (int j = lo; j < hi; ++j) s = s + cephes_exp(logit_of(base, ld, row, j) / p.temperature - mx);
-  s_chunk[c] = s;
+  for (int j = lo; j < hi; ++j)
+    if (key16(d.row[j]) > v) s = s + dist_e(d, j);
   __syncthreads();
-  float Z = 0.f;
-  for (int k = 0; k < kChunks; ++k) Z = Z + s_chunk[k];
+  s_tmp[threadIdx.x] = s;
   __syncthreads();
-  return RowSums{mx, Z};
+  return lds_total(s_tmp);
 }
 
-// inverse-CDF draw excluding index x (x < 0: none); run after row_sums(row)
-// left the chunk sums in s_chunk.  Executed by thread 0 only.
-__device__ int draw_row(const AcceptParams& p, int row, const RowSums& rs, int x, float u,
-                        const float* s_chunk) {
-  const int V = p.vocab;
-  const int CH = (V + kChunks - 1) / kChunks;
-  const float T = p.temperature;
-  auto r_at = [&](int j, int excl) -> float {
-    return (j == excl) ? 0.f : cephes_exp(logit_at(p, row, j) / T - rs.mx);
-  };
+// sets up d for `row`; leaves the kept chunk sums and tie bases in L
+__device__ void dist_setup(Dist& d, const uint16_t* row, int V, float T, float top_p, DistLds& L, float* s_tmp,
+                           float* s_redf) {
+  d.row = row;
+  d.T = T;
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < V; j += kThreads) m = fmaxf(m, bf16_to_f32(row[j]) / T);
+  d.mx = block_max_f32(m, s_redf);
+  d.topp = top_p < 1.0f;
+  d.tau = 0;
+  d.m = 0;
+  const int CH = chunk_len(V);
+  const int lo = threadIdx.x * CH, hi = min(lo + CH, V);
+  float s = 0.f;
+  for (int j = lo; j < hi; ++j) s = s + dist_e(d, j);
+  __syncthreads();
+  L.chunk[threadIdx.x] = s;
+  __syncthreads();
+  const float z = lds_total(L.chunk);
+  d.total = z;
+  if (!d.topp) return;
+  const float thr = top_p * z;
+  uint32_t a = 0, b = 65535;
+  while (a < b) {  // uniform across the work-group
+    const uint32_t mid = (a + b) / 2;
+    if (masked_total(d, V, mid, s_tmp) < thr) b = mid; else a = mid + 1;
+  }
+  d.tau = a;
+  const float mt = masked_total(d, V, a, s_tmp);
+  int cnt = 0;
+  for (int j = lo; j < hi; ++j) cnt += key16(row[j]) == a;
+  __syncthreads();
+  L.tie_base[threadIdx.x] = cnt;
+  __syncthreads();
+  int h = 0, base = 0;
+  for (int c = 0; c < kChunks; ++c) {
+    if (c == (int)threadIdx.x) base = h;
+    h += L.tie_base[c];
+  }
+  const float e_tau = cephes_exp(bf16_to_f32(bf16_of_key16(a)) / T - d.mx);
+  int r0 = 0, r1 = h;  // m = number of r in [0, h) with mt + r * e_tau < thr
+  while (r0 < r1) {
+    const int mid = (r0 + r1) / 2;
+    if (mt + (float)mid * e_tau < thr) r0 = mid + 1; else r1 = mid;
+  }
+  d.m = r0;
+  __syncthreads();
+  L.tie_base[threadIdx.x] = base;
+  // kept chunk sums
+  float k = 0.f;
+  int tie = base;
+  for (int j = lo; j < hi; ++j) {
+    const uint32_t key = key16(row[j]);
+    const bool kept = key > d.tau || (key == d.tau && tie < d.m);
+    tie += key == d.tau;
+    if (kept) k = k + dist_e(d, j);
+  }
+  L.chunk[threadIdx.x] = k;
+  __syncthreads();
+  d.total = lds_total(L.chunk);
+}
+
+// scans one chunk in index order, calling f(j, w_j) with each token's kept weight until
+// f returns false
+template <typename F>
+__device__ __forceinline__ void scan_chunk(const Dist& d, const DistLds& L, int V, int c, F&& f) {
+  const int CH = chunk_len(V);
+  const int lo = c * CH, hi = min(lo + CH, V);
+  int tie = d.topp ? L.tie_base[c] : 0;
+  for (int j = lo; j < hi; ++j) {
+    bool kept = true;
+    if (d.topp) {
+      const uint32_t key = key16(d.row[j]);
+      kept = key > d.tau || (key == d.tau && tie < d.m);
+      tie += key == d.tau;
+    }
+    if (!f(j, kept ? dist_e(d, j) : 0.f)) return;
+  }
+}
+
+// kept weight of token x (one thread)
+__device__ float weight_at(const Dist& d, const DistLds& L, int V, int x) {
+  float w = 0.f;
+  scan_chunk(d, L, V, x / chunk_len(V), [&](int j, float wj) {
+    if (j == x) {
+      w = wj;
+      return false;
+    }
+    return true;
+  });
+  return w;
+}
+
+// inverse-CDF draw from d's kept weights with token x removed (x < 0: none); one thread
+__device__ int draw_dist(const Dist& d, const DistLds& L, int V, int x, float u) {
+  const int CH = chunk_len(V);
   auto chunk_sum = [&](int c, int excl) -> float {
-    if (excl < 0 || excl / CH != c) return s_chunk[c];
+    if (excl < 0 || excl / CH != c) return L.chunk[c];
     float s = 0.f;
-    const int lo = c * CH, hi = min(lo + CH, V);
-    for (int j = lo; j < hi; ++j) s = s + r_at(j, excl);
+    scan_chunk(d, L, V, c, [&](int j, float wj) {
+      s = s + (j == excl ? 0.f : wj);
+      return true;
+    });
     return s;
   };
   int excl = x;
@@ -228,47 +346,79 @@ __device__ int draw_row(const AcceptParams& p, int row, const RowSums& rs, int x
     const float rc = chunk_sum(c, excl);
     if (prefix + rc > t) {
       float q = 0.f;
-      const int lo = c * CH, hi = min(lo + CH, V);
-      for (int j = lo; j < hi; ++j) {
-        q = q + r_at(j, excl);
-        if (prefix + q > t) return j;
-      }
+      int res = -1;
+      scan_chunk(d, L, V, c, [&](int j, float wj) {
+        q = q + (j == excl ? 0.f : wj);
+        if (prefix + q > t) {
+          res = j;
+          return false;
+        }
+        return true;
+      });
+      if (res >= 0) return res;
     }
     prefix = prefix + rc;
   }
-  for (int j = V - 1; j >= 0; --j)
-    if (r_at(j, excl) > 0.f) return j;
+  for (int c = kChunks - 1; c >= 0; --c) {
+    int found = -1;
+    scan_chunk(d, L, V, c, [&](int j, float wj) {
+      if (j != excl && wj > 0.f) found = j;
+      return true;
+    });
+    if (found >= 0) return found;
+  }
   return 0;
 }
 
-// residual draw: r_j = max(e_j / Z - f_j / Zq, 0) over the target row `row` (sums rs)
-// and the draft row `drow` (sums rq); every thread sums its chunk, thread 0 scans.
-// Falls back to the target row (no exclusion) when the residual total is not > 0.
-__device__ int draw_residual(const AcceptParams& p, int row, const RowSums& rs, int drow, const RowSums& rq,
-                             float u, float* s_chunk, float* s_rchunk) {
-  const int V = p.vocab;
-  const int CH = (V + kChunks - 1) / kChunks;
-  const float T = p.temperature;
-  auto r_at = [&](int j) -> float {
-    const float pj = cephes_exp(logit_at(p, row, j) / T - rs.mx) / rs.Z;
-    const float qj = cephes_exp(logit_of(p.draft_logits, p.dld, drow, j) / T - rq.mx) / rq.Z;
-    const float r = pj - qj;
-    return r > 0.f ? r : 0.f;
-  };
-  {
-    const int c = threadIdx.x;
-    float sr = 0.f;
+// residual draw: r_j = max(p'_j - q_j, 0) over the target d and the draft (bf16 logits dq,
+// or fp32 probabilities qp); every thread sums its chunk, thread 0 scans.  Falls back to
+// the target's kept weights (no exclusion) when the residual has no mass.
+__device__ int draw_residual(const Dist& d, const DistLds& L, const Dist& dq, const DistLds& Lq,
+                             const float* qp, int V, float u, float* s_rchunk) {
+  const int CH = chunk_len(V);
+  // r over one chunk, in index order
+  auto scan_r = [&](int c, auto&& f) {
     const int lo = c * CH, hi = min(lo + CH, V);
-    for (int j = lo; j < hi; ++j) sr = sr + r_at(j);
-    s_rchunk[c] = sr;
-  }
+    int tie = d.topp ? L.tie_base[c] : 0;
+    int tieq = (qp == nullptr && dq.topp) ? Lq.tie_base[c] : 0;
+    for (int j = lo; j < hi; ++j) {
+      bool kept = true;
+      if (d.topp) {
+        const uint32_t key = key16(d.row[j]);
+        kept = key > d.tau || (key == d.tau && tie < d.m);
+        tie += key == d.tau;
+      }
+      const float pj = kept ? dist_e(d, j) / d.total : 0.f;
+      float qj;
+      if (qp != nullptr) {
+        qj = qp[j];
+      } else {
+        bool keptq = true;
+        if (dq.topp) {
+          const uint32_t key = key16(dq.row[j]);
+          keptq = key > dq.tau || (key == dq.tau && tieq < dq.m);
+          tieq += key == dq.tau;
+        }
+        qj = keptq ? dist_e(dq, j) / dq.total : 0.f;
+      }
+      const float r = pj - qj;
+      if (!f(j, r > 0.f ? r : 0.f)) return;
+    }
+  };
+  float sr = 0.f;
+  scan_r((int)threadIdx.x, [&](int, float r) {
+    sr = sr + r;
+    return true;
+  });
+  __syncthreads();
+  s_rchunk[threadIdx.x] = sr;
   __syncthreads();
   int res = 0;
   if (threadIdx.x == 0) {
     float R = 0.f;
     for (int c = 0; c < kChunks; ++c) R = R + s_rchunk[c];
     if (!(R > 0.f)) {
-      res = draw_row(p, row, rs, -1, u, s_chunk);
+      res = draw_dist(d, L, V, -1, u);
     } else {
       const float t = u * R;
       float prefix = 0.f;
@@ -277,23 +427,23 @@ __device__ int draw_residual(const AcceptParams& p, int row, const RowSums& rs, 
         const float rc = s_rchunk[c];
         if (prefix + rc > t) {
           float q = 0.f;
-          const int lo = c * CH, hi = min(lo + CH, V);
-          for (int j = lo; j < hi; ++j) {
-            q = q + r_at(j);
+          scan_r(c, [&](int j, float r) {
+            q = q + r;
             if (prefix + q > t) {
               res = j;
-              break;
+              return false;
             }
-          }
+            return true;
+          });
         }
         prefix = prefix + rc;
       }
       if (res < 0) {
-        for (int j = V - 1; j >= 0; --j)
-          if (r_at(j) > 0.f) {
-            res = j;
-            break;
-          }
+        for (int c = kChunks - 1; c >= 0 && res < 0; --c)
+          scan_r(c, [&](int j, float r) {
+            if (r > 0.f) res = j;
+            return true;
+          });
         if (res < 0) res = 0;
       }
     }
@@ -304,10 +454,11 @@ __device__ int draw_residual(const AcceptParams& p, int row, const RowSums& rs, 
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
   __shared__ uint64_t s_red[kThreads / kWave];
   __shared__ float s_redf[kThreads / kWave];
-  __shared__ float s_chunk[kChunks];
-  __shared__ float s_qchunk[kChunks];
+  __shared__ DistLds s_d, s_dq;
+  __shared__ float s_tmp[kChunks];
   __shared__ int s_target[kMaxRows];
   __shared__ int s_kept, s_final;
+  __shared__ float s_accept;
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -321,8 +472,10 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
   const int g = min(max(p.num_drafts[b], 0), p.max_drafts);
   const int rs0 = p.row_start[b];
   const int32_t* dr = p.drafts + (int64_t)b * p.max_drafts;
+  const float T = p.temperature != nullptr ? p.temperature[b] : 0.f;
+  const int V = p.vocab;
 
-  if (p.mode == NE_ACCEPT_GREEDY) {
+  if (!(T > 0.f)) {
     for (int i = 0; i <= g; ++i) {
       const int t = row_argmax(p, rs0 + i, s_red);
       if (tid == 0) s_target[i] = t;
@@ -336,41 +489,55 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
     }
     __syncthreads();
   } else {
+    const float top_p = p.top_p != nullptr ? p.top_p[b] : 1.f;
     const uint64_t seed = p.seeds[b], step = p.steps[b];
+    const int dr0 = p.draft_rows != nullptr ? p.draft_row_start[b] : 0;
+    const bool draft_logits = p.draft_rows != nullptr && p.draft_dtype == NE_DTYPE_BF16;
     int kept = 0;
     bool done = false;
-    const int dr0 = p.draft_logits != nullptr ? p.draft_row_start[b] : 0;
+    Dist d{}, dq{};
     for (int i = 0; i < g && !done; ++i) {
-      const RowSums rs = row_sums(p, p.logits, p.ld, rs0 + i, s_chunk, s_redf);
+      dist_setup(d, p.logits + (int64_t)(rs0 + i) * p.ld, V, T, top_p, s_d, s_tmp, s_redf);
       const int guess = dr[i];
-      const float pg = cephes_exp(logit_at(p, rs0 + i, guess) / p.temperature - rs.mx) / rs.Z;
       const float u = philox_uniform(seed, step, i);
-      if (p.draft_logits == nullptr) {
-        if (pg >= 1.f || (pg > 0.f && u < pg)) {
-          ++kept;
-          continue;
+      const float* qp = nullptr;
+      if (draft_logits)
+        dist_setup(dq, (const uint16_t*)p.draft_rows + (int64_t)(dr0 + i) * p.dld, V, T, top_p, s_dq, s_tmp,
+                   s_redf);
+      else if (p.draft_rows != nullptr)
+        qp = (const float*)p.draft_rows + (int64_t)(dr0 + i) * p.dld;
+      // the acceptance test is made by thread 0 (the weight scans are serial) and broadcast
+      if (tid == 0) {
+        const float wg = weight_at(d, s_d, V, guess);
+        const float pg = wg > 0.f ? wg / d.total : 0.f;
+        float a = pg;
+        if (draft_logits) {
+          const float wq = weight_at(dq, s_dq, V, guess);
+          const float q = wq > 0.f ? wq / dq.total : 0.f;
+          a = fminf(pg / fmaxf(q, 1e-12f), 1.f);
+        } else if (qp != nullptr) {
+          a = fminf(pg / fmaxf(qp[guess], 1e-12f), 1.f);
         }
-        if (tid == 0) {
-          s_final = draw_row(p, rs0 + i, rs, guess, philox_uniform(seed, step, 63), s_chunk);
-        }
+        s_accept = a;
+      }
+      __syncthreads();
+      const float a = s_accept;
+      if (a >= 1.f || (a > 0.f && u < a)) {
+        ++kept;
+        continue;
+      }
+      const float u_draw = philox_uniform(seed, step, 63);
+      if (p.draft_rows == nullptr) {
+        if (tid == 0) s_final = draw_dist(d, s_d, V, guess, u_draw);
       } else {
-        const RowSums rq = row_sums(p, p.draft_logits, p.dld, dr0 + i, s_qchunk, s_redf);
-        const float qg = fmaxf(
-            cephes_exp(logit_of(p.draft_logits, p.dld, dr0 + i, guess) / p.temperature - rq.mx) / rq.Z, 1e-12f);
-        const float a = fminf(pg / qg, 1.f);
-        if (a >= 1.f || (a > 0.f && u < a)) {
-          ++kept;
-          continue;
-        }
-        const int t = draw_residual(p, rs0 + i, rs, dr0 + i, rq, philox_uniform(seed, step, 63), s_chunk,
-                                    s_qchunk);
+        const int t = draw_residual(d, s_d, dq, s_dq, qp, V, u_draw, s_tmp);
         if (tid == 0) s_final = t;
       }
       done = true;
     }
     if (!done) {
-      const RowSums rs = row_sums(p, p.logits, p.ld, rs0 + g, s_chunk, s_redf);
-      if (tid == 0) s_final = draw_row(p, rs0 + g, rs, -1, philox_uniform(seed, step, 63), s_chunk);
+      dist_setup(d, p.logits + (int64_t)(rs0 + g) * p.ld, V, T, top_p, s_d, s_tmp, s_redf);
+      if (tid == 0) s_final = draw_dist(d, s_d, V, -1, philox_uniform(seed, step, 63));
     }
     if (tid == 0) s_kept = kept;
     __syncthreads();
@@ -382,12 +549,15 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
     p.out_tokens[(int64_t)b * (p.max_drafts + 1) + i] = (i < kept) ? dr[i] : (i == kept ? fin : -1);
   if (tid == 0) p.num_out[b] = kept + 1;
   if (p.history != nullptr) {
+    // a history row holds hist_stride tokens: tokens past it are not written (the host
+    // refuses requests whose prompt + max_new_tokens exceed the rows' capacity)
     const int len = p.history_len[b];
+    const int room = (int)min((int64_t)(kept + 1), max(p.hist_stride - len, (int64_t)0));
     int32_t* h = p.history + (int64_t)b * p.hist_stride;
-    for (int i = tid; i <= kept; i += kThreads) h[len + i] = (i < kept) ? dr[i] : fin;
+    for (int i = tid; i < room; i += kThreads) h[len + i] = (i < kept) ? dr[i] : fin;
     __syncthreads();
     if (tid == 0) {
-      p.history_len[b] = len + kept + 1;
+      p.history_len[b] = len + room;
       if (p.num_cached != nullptr) p.num_cached[b] = len + kept;
     }
   }
@@ -399,35 +569,35 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
 
 using namespace ne;
 
-extern "C" int ne_accept(int32_t mode, const void* logits, int64_t ld_logits,
-                         const uint64_t* argmax_partials, int32_t num_tiles, int32_t vocab,
-                         const int32_t* drafts, int32_t max_drafts, const int32_t* num_drafts,
-                         const int32_t* row_start, int32_t num_seqs, float temperature,
+extern "C" int ne_accept(const void* logits, int64_t ld_logits, const uint64_t* argmax_partials,
+                         int32_t num_tiles, int32_t vocab, const int32_t* drafts, int32_t max_drafts,
+                         const int32_t* num_drafts, const int32_t* row_start, int32_t num_seqs,
+                         const float* temperature, const float* top_p, int32_t any_sampled,
                          const uint64_t* seeds, const uint64_t* steps, int32_t* out_tokens,
                          int32_t* num_out, int32_t* history, int64_t history_stride,
-                         int32_t* history_len, int32_t* num_cached, const void* draft_logits,
-                         int64_t ld_draft, const int32_t* draft_row_start, void* stream) {
+                         int32_t* history_len, int32_t* num_cached, const void* draft_rows,
+                         int32_t draft_dtype, int64_t ld_draft, const int32_t* draft_row_start,
+                         void* stream) {
   NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
   if (num_seqs == 0) return NE_OK;
-  NE_CHECK_ARG(mode == NE_ACCEPT_GREEDY || mode == NE_ACCEPT_SAMPLED, "unknown mode %d", mode);
   NE_CHECK_ARG(vocab > 0, "vocab must be positive");
   NE_CHECK_ARG(drafts && num_drafts && row_start && out_tokens && num_out, "null pointer argument");
   NE_CHECK_ARG(max_drafts >= 1 && max_drafts < kMaxRows, "max_drafts must be in [1, %d]",
                kMaxRows - 1);
-  if (mode == NE_ACCEPT_GREEDY) {
-    NE_CHECK_ARG(logits || (argmax_partials && num_tiles > 0),
-                 "greedy acceptance needs logits or argmax partials");
-  } else {
+  NE_CHECK_ARG(logits || (argmax_partials && num_tiles > 0),
+               "acceptance needs logits or argmax partials");
+  if (any_sampled) {
+    NE_CHECK_ARG(temperature != nullptr, "sampled acceptance needs per-sequence temperatures");
     NE_CHECK_ARG(logits != nullptr, "sampled acceptance needs logits");
-    NE_CHECK_ARG(temperature > 0.f, "sampled acceptance needs temperature > 0");
     NE_CHECK_ARG(seeds && steps, "sampled acceptance needs seeds and steps");
   }
   NE_CHECK_ARG(!logits || ld_logits >= vocab, "ld_logits < vocab");
   NE_CHECK_ARG(!history || (history_len && history_stride > 0), "history needs history_len");
-  NE_CHECK_ARG(!draft_logits || (mode == NE_ACCEPT_SAMPLED && draft_row_start && ld_draft >= vocab),
-               "draft rows need sampled mode, draft_row_start and ld_draft >= vocab");
+  NE_CHECK_ARG(!draft_rows || (any_sampled && draft_row_start && ld_draft >= vocab &&
+                               (draft_dtype == NE_DTYPE_BF16 || draft_dtype == NE_DTYPE_FP32)),
+               "draft rows need sampled sequences, draft_row_start, ld_draft >= vocab and a bf16 or "
+               "fp32 dtype");
   AcceptParams p{};
-  p.mode = mode;
   p.logits = (const uint16_t*)logits;
   p.ld = ld_logits;
   p.partials = argmax_partials;
@@ -437,7 +607,8 @@ extern "C" int ne_accept(int32_t mode, const void* logits, int64_t ld_logits,
   p.max_drafts = max_drafts;
   p.num_drafts = num_drafts;
   p.row_start = row_start;
-  p.temperature = temperature;
+  p.temperature = any_sampled ? temperature : nullptr;
+  p.top_p = top_p;
   p.seeds = seeds;
   p.steps = steps;
   p.out_tokens = out_tokens;
@@ -446,7 +617,8 @@ extern "C" int ne_accept(int32_t mode, const void* logits, int64_t ld_logits,
   p.hist_stride = history_stride;
   p.history_len = history_len;
   p.num_cached = num_cached;
-  p.draft_logits = (const uint16_t*)draft_logits;
+  p.draft_rows = draft_rows;
+  p.draft_dtype = draft_dtype;
   p.dld = ld_draft;
   p.draft_row_start = draft_row_start;
   hipLaunchKernelGGL(accept_kernel, dim3(num_seqs), dim3(kThreads), 0, (hipStream_t)stream, p);

@@ -24,7 +24,8 @@ __global__ __launch_bounds__(256) void prepare_verify_kernel(
   const int b = row / R;
   const int i = row % R;
   const int L = history_len[b];
-  const int g = (L > 0) ? num_drafts[b] : -1;
+  // a count outside [0, max_drafts] would read past the sequence's rows and table
+  const int g = (L > 0) ? min(max(num_drafts[b], 0), max_drafts) : -1;
   if (i <= g) {
     const int pos = L - 1 + i;
     tokens[row] = (i == 0) ? history[(int64_t)b * hist_stride + L - 1]

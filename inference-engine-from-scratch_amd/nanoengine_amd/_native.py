@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -28,8 +28,6 @@ DTYPE_INT8 = 3
 
 EPILOGUE_STORE = 0
 EPILOGUE_SWIGLU = 1
-ACCEPT_GREEDY = 0
-ACCEPT_SAMPLED = 1
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -104,12 +102,12 @@ SIGNATURES: dict[str, tuple] = {
     "ne_accept": (
         ctypes.c_int,
         [
-            _i32, _vp, _i64, _u64p, _i32, _i32,  # mode, logits, ld, partials, tiles, vocab
+            _vp, _i64, _u64p, _i32, _i32,  # logits, ld, partials, tiles, vocab
             _vp, _i32, _vp, _vp, _i32,  # drafts, max drafts, num drafts, row start, seqs
-            _f32, _u64p, _u64p,  # temperature, seeds, steps
+            _vp, _vp, _i32, _u64p, _u64p,  # temperatures, top-p, any sampled, seeds, steps
             _vp, _vp,  # out tokens, num out
             _vp, _i64, _vp, _vp,  # history, stride, history len, num cached
-            _vp, _i64, _vp,  # draft logits, ld, draft row start
+            _vp, _i32, _i64, _vp,  # draft rows, their dtype, ld, draft row start
             _vp,  # stream
         ],
     ),

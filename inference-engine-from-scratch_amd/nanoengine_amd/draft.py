@@ -67,6 +67,7 @@ class DraftModelProposer:
         self.logits: torch.Tensor | None = None
         self.row_start = torch.arange(max_seqs, **i32) * k
         self.temperature = 0.0
+        self.top_p = 1.0
         self.seeds: torch.Tensor | None = None
         self.steps: np.ndarray | None = None
         self.target_len: dict[int, int] = {}  # this proposal's target length per slot
@@ -112,10 +113,13 @@ class DraftModelProposer:
 
     # -------------------------------------------------------------- proposals
     def propose(self, sequences: dict[int, Sequence], counts: dict[int, int], temperature: float = 0.0,
-                seeds: torch.Tensor | None = None, steps: np.ndarray | None = None) -> dict[int, list[int]]:
+                seeds: torch.Tensor | None = None, steps: np.ndarray | None = None,
+                top_p: float = 1.0) -> dict[int, list[int]]:
         """``counts[slot]`` guesses for each slot (proposers.py:70-88): greedy, or sampled at
-        ``temperature`` with the slots' ``seeds`` (device int64) at verify ``steps`` (host)."""
+        ``temperature`` and ``top_p`` (compute_token_probabilities, sampling.py:30-38) with the
+        slots' ``seeds`` (device int64) at verify ``steps`` (host)."""
         self.temperature = float(temperature)
+        self.top_p = float(top_p)
         if self.temperature > 0.0:
             if seeds is None or steps is None:
                 raise ValueError("sampled draft proposals need seeds and steps")
@@ -238,6 +242,7 @@ class DraftModelProposer:
                 torch.cuda.current_stream(dev).synchronize()
                 with torch.cuda.graph(graph):
                     self._decode_body()
+                self.model.bind_graph()
                 self._dec_graph = graph
             self._dec_graph.replay()
             self.forwards += 1
@@ -275,7 +280,7 @@ class DraftModelProposer:
         bt = torch.from_numpy(np.stack(tables)).to(dev)
         batch = AttentionBatch(posn, slots, qs, ql, cl, bt, max(q_len), max(ctx_len))
         self.model.ensure_rope(max(ctx_len))
-        hidden = self.model.forward(rows, tok, batch, self.pool)
+        hidden = self.model.forward(rows, tok, batch, self.pool, workspace=self.model.eager_workspace)
         self.forwards += 1
         for s, draft, a, b, e in pieces:
             draft.num_cached_tokens = b
@@ -303,7 +308,7 @@ class DraftModelProposer:
                              dtype=np.int64)
             kernels.accept(
                 self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], vocab, logits=logits,
-                temperature=self.temperature, seeds=self.seeds.index_select(0, sel),
+                temperature=self.temperature, top_p=self.top_p, seeds=self.seeds.index_select(0, sel),
                 steps=torch.from_numpy(steps).to(dev), out_tokens=self.out_tokens[o : o + n],
                 num_out=self.num_out[o : o + n],
             )

@@ -15,8 +15,6 @@ import torch
 
 from nanoengine_amd import _native
 from nanoengine_amd._native import (
-    ACCEPT_GREEDY,
-    ACCEPT_SAMPLED,
     DTYPE_BF16,
     DTYPE_FP16,
     DTYPE_FP32,
@@ -142,14 +140,21 @@ class AttentionWorkspace:
     """Caller-owned scratch for split-K attention; re-zeroed when its layout changes.
 
     ``plan_key`` names the metadata the last :func:`paged_attention_plan` call used, so
-    that a planned attention call on other metadata is refused."""
+    that a planned attention call on other metadata is refused.  ``frozen`` is set once a
+    captured HIP graph holds the buffer's address: from then on a call that would need a
+    larger buffer raises instead of reallocating under the graph."""
 
     buffer: torch.Tensor | None = None
     layout: tuple | None = None
     plan_key: tuple | None = None
+    frozen: bool = False
 
     def get(self, device: torch.device, nbytes: int, layout: tuple) -> torch.Tensor:
         if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
+            if self.frozen:
+                have = 0 if self.buffer is None else self.buffer.numel()
+                raise RuntimeError(f"attention workspace of {have} bytes is held by a captured HIP graph; "
+                                   f"this call needs {nbytes} bytes on {device}: size it before capture")
             self.buffer = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
             self.layout = layout
             self.plan_key = None
@@ -566,7 +571,8 @@ def accept(
     vocab: int,
     logits: torch.Tensor | None = None,
     argmax_partials: torch.Tensor | None = None,
-    temperature: float = 0.0,
+    temperature: float | torch.Tensor = 0.0,
+    top_p: float | torch.Tensor = 1.0,
     seeds: torch.Tensor | None = None,
     steps: torch.Tensor | None = None,
     out_tokens: torch.Tensor | None = None,
@@ -575,32 +581,56 @@ def accept(
     history_len: torch.Tensor | None = None,
     num_cached: torch.Tensor | None = None,
     draft_logits: torch.Tensor | None = None,
+    draft_probs: torch.Tensor | None = None,
     draft_row_start: torch.Tensor | None = None,
+    any_sampled: bool | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Accepted guesses plus one target token per sequence: ``(out_tokens [b, k+1], num_out [b])``.
 
-    ``draft_logits`` (sampled mode): the draft model's bf16 logits for each guess, row
-    ``draft_row_start[b] + i`` for guess i of sequence b; without them the guesses count
-    as deterministic (one-hot draft distribution)."""
+    ``temperature`` / ``top_p``: one value for every sequence, or per-sequence fp32 device
+    tensors (0 = greedy); with tensors, ``any_sampled`` says whether any temperature is
+    positive (the host knows it without reading the device).  The draft distribution of
+    each guess (sampled sequences): ``draft_logits`` (bf16, the draft model's logits; its
+    distribution is the same temperature/top-p softmax) or ``draft_probs`` (fp32
+    probabilities used as given), row ``draft_row_start[b] + i`` for guess i of sequence b;
+    neither: the guesses count as deterministic (one-hot draft distribution)."""
     device = _require_gpu(drafts, num_drafts, row_start, logits, argmax_partials)
     _int32(drafts, "drafts")
     _int32(num_drafts, "num_drafts")
     _int32(row_start, "row_start")
     num_seqs, max_drafts = drafts.shape
-    mode = ACCEPT_GREEDY if temperature == 0.0 else ACCEPT_SAMPLED
+    if isinstance(temperature, torch.Tensor):
+        _check(temperature.dtype == torch.float32 and temperature.numel() >= num_seqs, "temperature [b] fp32")
+        _check(any_sampled is not None, "per-sequence temperatures need any_sampled")
+        temps = temperature
+    else:
+        any_sampled = float(temperature) > 0.0
+        temps = torch.full((num_seqs,), float(temperature), dtype=torch.float32, device=device) if any_sampled \
+            else None
+    if isinstance(top_p, torch.Tensor):
+        _check(top_p.dtype == torch.float32 and top_p.numel() >= num_seqs, "top_p [b] fp32")
+        top_ps = top_p
+    else:
+        top_ps = None if float(top_p) >= 1.0 else torch.full((num_seqs,), float(top_p), dtype=torch.float32,
+                                                                device=device)
     if logits is not None:
         _check(logits.dtype == torch.bfloat16 and logits.stride(1) == 1, "logits must be bf16 rows")
         _check(logits.shape[1] == vocab, "logits width must equal vocab")
-    if mode == ACCEPT_SAMPLED:
+    if any_sampled:
         _check(logits is not None, "sampled acceptance needs logits")
         _check(seeds is not None and steps is not None, "sampled acceptance needs seeds and steps")
         _check(seeds.dtype == torch.int64 and steps.dtype == torch.int64, "seeds/steps int64")
-    if draft_logits is not None:
-        _check(mode == ACCEPT_SAMPLED, "draft logits need sampled acceptance")
-        _check(draft_logits.dtype == torch.bfloat16 and draft_logits.stride(1) == 1, "draft logits must be bf16 rows")
-        _check(draft_logits.shape[1] == vocab, "draft logits width must equal vocab")
-        _check(draft_row_start is not None, "draft logits need draft_row_start")
+    _check(draft_logits is None or draft_probs is None, "give draft logits or draft probabilities, not both")
+    draft = draft_logits if draft_logits is not None else draft_probs
+    draft_dtype = DTYPE_BF16
+    if draft is not None:
+        _check(any_sampled, "draft distributions need sampled acceptance")
+        want = torch.bfloat16 if draft_logits is not None else torch.float32
+        _check(draft.dtype == want and draft.stride(1) == 1, f"draft rows must be {want} rows")
+        _check(draft.shape[1] == vocab, "draft rows' width must equal vocab")
+        _check(draft_row_start is not None, "draft rows need draft_row_start")
         _int32(draft_row_start, "draft_row_start")
+        draft_dtype = dtype_code(draft.dtype)
     if out_tokens is None:
         out_tokens = torch.empty((num_seqs, max_drafts + 1), dtype=torch.int32, device=device)
     if num_out is None:
@@ -608,14 +638,14 @@ def accept(
     num_tiles = argmax_partials.shape[1] if argmax_partials is not None else 0
     _native.call(
         "ne_accept",
-        mode, _ptr(logits), logits.stride(0) if logits is not None else 0,
+        _ptr(logits), logits.stride(0) if logits is not None else 0,
         _ptr(argmax_partials), num_tiles, vocab,
         _ptr(drafts), max_drafts, _ptr(num_drafts), _ptr(row_start), num_seqs,
-        float(temperature), _ptr(seeds), _ptr(steps),
+        _ptr(temps), _ptr(top_ps), int(bool(any_sampled)), _ptr(seeds), _ptr(steps),
         _ptr(out_tokens), _ptr(num_out),
         _ptr(history), history.stride(0) if history is not None else 0,
         _ptr(history_len), _ptr(num_cached),
-        _ptr(draft_logits), draft_logits.stride(0) if draft_logits is not None else 0, _ptr(draft_row_start),
+        _ptr(draft), draft_dtype, draft.stride(0) if draft is not None else 0, _ptr(draft_row_start),
         _stream(device),
     )
     return out_tokens, num_out

@@ -223,8 +223,14 @@ class Qwen3VerifyModel:
         # reference computes them per step; grown when a longer position appears
         self.rope_positions = 0
         self.rope = None
+        self.graph_bound = False
         self.ensure_rope(4096)
+        # attention scratch of the forwards a HIP graph captures (verify steps, graphed
+        # draft decode rows) and, separately, of eager forwards (prefill, a draft's
+        # catch-up): an eager forward of another shape must never move a buffer whose
+        # address a graph holds
         self.workspace = kernels.AttentionWorkspace()
+        self.eager_workspace = kernels.AttentionWorkspace()
         # QKV projection with QK-norm, RoPE and the KV write in its epilogue; False
         # runs the GEMM and the row kernel separately (the same bits, one more launch)
         self.fuse_qkv = True
@@ -236,17 +242,29 @@ class Qwen3VerifyModel:
         most = max(max(a * r, b * r) for r, (a, b) in enumerate(zip(self.o_splits, self.down_splits)))
         self.partials = torch.empty(max(most, 1) * h, dtype=torch.float32, device=device)
 
+    def bind_graph(self) -> None:
+        """A HIP graph now holds this model's buffers (activations, RoPE table, the graph
+        workspace): they must keep their addresses from here on."""
+        self.graph_bound = True
+        self.workspace.frozen = True
+
     def ensure_rope(self, positions: int) -> None:
         """Make the RoPE table cover positions 0 .. positions-1 (before any graph capture)."""
         if positions > self.rope_positions:
+            if self.graph_bound:
+                raise RuntimeError(f"RoPE table of {self.rope_positions} positions is held by a captured HIP "
+                                   f"graph; {positions} positions must be reserved before capture")
             self.rope = kernels.rope_table(positions, self.config.rope_theta).to(self.device)
             self.rope_positions = positions
 
-    def forward(self, rows: int, tokens: torch.Tensor, batch: AttentionBatch, pool) -> torch.Tensor:
+    def forward(self, rows: int, tokens: torch.Tensor, batch: AttentionBatch, pool,
+                workspace: kernels.AttentionWorkspace | None = None) -> torch.Tensor:
         """Hidden states after the final norm for ``rows`` packed query rows; writes this
-        step's keys/values into ``pool`` at ``batch.slot_mapping``."""
+        step's keys/values into ``pool`` at ``batch.slot_mapping``.  ``workspace``: the
+        attention scratch (default: the one graph-captured forwards use)."""
         if rows > self.max_rows:
             raise ValueError(f"{rows} rows exceed the model's capacity of {self.max_rows}")
+        ws = self.workspace if workspace is None else workspace
         c = self.config
         w = self.weights
         eps = c.rms_norm_eps
@@ -261,7 +279,7 @@ class Qwen3VerifyModel:
         if planned:
             kernels.paged_attention_plan(batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start,
                                          batch.q_len, c.num_attention_heads, c.num_key_value_heads,
-                                         batch.max_q_len, batch.max_ctx_len, self.workspace)
+                                         batch.max_q_len, batch.max_ctx_len, ws)
         fuse = self.fuse_qkv and kernels.qkv_fusion_supported(pool.key_caches[0], pool.key_scale_2d(0))
         for i, layer in enumerate(w.layers):
             if fuse:  # QK-norm + RoPE + KV write in the QKV GEMM's epilogue (same bits)
@@ -282,7 +300,7 @@ class Qwen3VerifyModel:
             kernels.paged_verify_attention(
                 q, pool.key_caches[i], pool.value_caches[i], pool.key_scale_2d(i), pool.value_scale_2d(i),
                 batch.block_tables, pool.block_size, batch.ctx_len, batch.q_start, batch.q_len,
-                batch.max_q_len, batch.max_ctx_len, self.softmax_scale, out=attn, workspace=self.workspace,
+                batch.max_q_len, batch.max_ctx_len, self.softmax_scale, out=attn, workspace=ws,
                 planned=planned,
             )
             self._project_add_norm(attn.view(rows, -1), layer.o_int8, layer.o_scale, self.o_splits[rows],

@@ -39,16 +39,25 @@ import numpy as np
 import torch
 
 from nanoengine_amd import kernels
-from nanoengine_amd.interface import (
-    GREEDY_TEMPERATURE,
-    find_finish_reason,
-)
+from nanoengine_amd.interface import find_finish_reason
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
 from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
 from nanoengine_amd.sequence_state import Sequence
 
 if TYPE_CHECKING:
     from nanoengine_amd.draft import DraftModelProposer
+
+
+def request_length_error(num_prompt_tokens: int, max_new_tokens: int, max_model_len: int) -> str | None:
+    """Why a request cannot be admitted, or None (api/routes.py:98-111): an empty prompt,
+    or prompt + max_new_tokens past max_model_len.  The device history rows hold
+    max_model_len + k + 1 tokens; this keeps every append of a verify step inside them."""
+    if num_prompt_tokens == 0:
+        return "prompt is empty"
+    total = num_prompt_tokens + max_new_tokens
+    if total > max_model_len:
+        return f"prompt + max_new_tokens = {total} exceeds max_model_len {max_model_len}"
+    return None
 
 
 @dataclass
@@ -89,6 +98,7 @@ class VerifyRunner:
         self.max_ngram = max_ngram
         self.stop_token_ids = stop_token_ids
         self.block_size = allocator.block_size
+        self.max_model_len = max_model_len
         self.capacity = max_model_len + self.R
         self.max_blocks = math.ceil(self.capacity / self.block_size)
         self.use_graph = use_graph
@@ -106,6 +116,9 @@ class VerifyRunner:
         self.num_drafts = torch.zeros(max_seqs, **i32)
         self.seeds = torch.zeros(max_seqs, dtype=torch.int64, device=dev)
         self.steps = torch.zeros(max_seqs, dtype=torch.int64, device=dev)
+        # per-slot sampling parameters (sampling.py:30-38): temperature 0 verifies greedily
+        self.temperatures = torch.zeros(max_seqs, dtype=torch.float32, device=dev)
+        self.top_ps = torch.ones(max_seqs, dtype=torch.float32, device=dev)
         rows = max_seqs * self.R
         self.tokens = torch.zeros(rows, **i32)
         self.positions = torch.zeros(rows, **i32)
@@ -144,10 +157,13 @@ class VerifyRunner:
         self.np_gen = np.zeros(max_seqs, dtype=np.int64)
         self.np_max_new = np.zeros(max_seqs, dtype=np.int64)
         self.np_owned = np.zeros(max_seqs, dtype=np.int64)
+        self.np_temp = np.zeros(max_seqs, dtype=np.float32)
+        self.np_top_p = np.ones(max_seqs, dtype=np.float32)
         self.slots: list[Sequence | None] = [None] * max_seqs
-        self.temperature: float | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
-        self.graph_temperature: float | None = None
+        # whether the captured step computes full logits (some slot samples) or only the
+        # LM head's argmax partials (every slot greedy)
+        self.graph_sampled: bool | None = None
         self.batch = AttentionBatch(self.positions, self.slot_mapping, self.q_start, self.q_len,
                                     self.ctx_len, self.block_tables, self.R, self.capacity)
         # set to a list to record, per verify step, each slot's history, drafts,
@@ -162,14 +178,32 @@ class VerifyRunner:
     def free_slots(self) -> list[int]:
         return [i for i, s in enumerate(self.slots) if s is None]
 
-    def _check_sampling(self, sequence: Sequence) -> None:
-        params = sequence.sampling_params
-        if params.temperature != GREEDY_TEMPERATURE and params.top_p < 1.0:
-            raise NotImplementedError("top_p < 1 is not implemented on the HIP acceptance path")
-        temp = float(params.temperature)
-        if self.temperature is not None and self.active_slots and temp != self.temperature:
-            raise NotImplementedError("one batch verifies with a single temperature")
-        self.temperature = temp
+    @property
+    def any_sampled(self) -> bool:
+        """Whether some active slot samples (temperature > 0)."""
+        return bool((self.np_temp[self.np_active] > 0).any())
+
+    def _check_sampling(self, sequences: list[Sequence]) -> None:
+        """A draft-model proposer guesses for the whole batch with one temperature and
+        top-p; n-gram batches take every slot's own."""
+        if self.proposer is None:
+            return
+        params = {(s.sampling_params.temperature, s.sampling_params.top_p) for s in sequences}
+        params |= {(self.slots[s].sampling_params.temperature, self.slots[s].sampling_params.top_p)
+                   for s in self.active_slots}
+        if len(params) > 1:
+            raise NotImplementedError("a draft-model batch verifies with one temperature and top-p")
+
+    @property
+    def batch_temperature(self) -> float:
+        """The draft-model proposer's temperature (every slot's, see _check_sampling)."""
+        act = self.active_slots
+        return float(self.np_temp[act[0]]) if act else 0.0
+
+    @property
+    def batch_top_p(self) -> float:
+        act = self.active_slots
+        return float(self.np_top_p[act[0]]) if act else 1.0
 
     def add(self, sequences: list[Sequence]) -> list[int]:
         """Place sequences in free slots, reserve their prompts, prefill them and emit
@@ -178,9 +212,10 @@ class VerifyRunner:
         if len(sequences) > len(free):
             raise ValueError(f"only {len(free)} free sequence slots")
         for seq in sequences:
-            self._check_sampling(seq)
-            if seq.num_tokens + self.R > self.capacity:
-                raise ValueError(f"prompt of {seq.request_id} exceeds max_model_len")
+            problem = request_length_error(seq.num_tokens, seq.sampling_params.max_new_tokens, self.max_model_len)
+            if problem is not None:
+                raise ValueError(f"{seq.request_id}: {problem}")
+        self._check_sampling(sequences)
         slots = free[: len(sequences)]
         results = {}
         # prefill contiguous runs of slots together
@@ -220,6 +255,11 @@ class VerifyRunner:
             self.history_len[slot] = p
             self.seeds[slot] = seq.sampling_generator.seed
             self.steps[slot] = seq.sampling_generator.step
+            params = seq.sampling_params
+            self.np_temp[slot] = max(float(params.temperature), 0.0)
+            self.np_top_p[slot] = float(params.top_p)
+            self.temperatures[slot] = float(self.np_temp[slot])
+            self.top_ps[slot] = float(self.np_top_p[slot])
             pending.append([slot, seq, c, p])
         self.block_tables.copy_(self.h_tables, non_blocking=True)
         while pending:
@@ -273,26 +313,29 @@ class VerifyRunner:
         s0 = pieces[0][0]
         batch = AttentionBatch(posn, slot_map, qs, ql, cl, self.block_tables[s0 : s0 + len(pieces)], max(q_len),
                                max(ctx_len))
-        hidden = self.model.forward(row, tok, batch, self.pool)
+        hidden = self.model.forward(row, tok, batch, self.pool, workspace=self.model.eager_workspace)
         nf = sum(1 for piece in pieces if piece[3] == piece[4])
         if nf == 0:
             return
         last = hidden.index_select(0, (qs[:nf] + ql[:nf] - 1).long())
-        greedy = self.temperature == GREEDY_TEMPERATURE
-        logits, partials = self.model.compute_logits(last, logits=not greedy, argmax=greedy)
+        sampled = bool((self.np_temp[s0 : s0 + nf] > 0).any())
+        logits, partials = self.model.compute_logits(last, logits=sampled, argmax=not sampled)
         zeros = torch.zeros(nf, dtype=torch.int32, device=dev)
         sl = slice(s0, s0 + nf)
         kernels.accept(
             self.drafts[sl], zeros, torch.arange(nf, dtype=torch.int32, device=dev),
             self.model.config.vocab_size, logits=logits, argmax_partials=partials,
-            temperature=self.temperature, seeds=self.seeds[sl], steps=self.steps[sl],
+            temperature=self.temperatures[sl], top_p=self.top_ps[sl], any_sampled=sampled,
+            seeds=self.seeds[sl], steps=self.steps[sl],
             out_tokens=self.out_tokens[sl], num_out=self.num_out[sl], history=self.history[sl],
             history_len=self.history_len[sl], num_cached=self.num_cached[sl],
         )
 
     # ------------------------------------------------------------- verify step
-    def _device_step(self) -> None:
-        """Fixed-shape part of the verify step: pack, forward, LM head, accept."""
+    def _device_step(self, sampled: bool) -> None:
+        """Fixed-shape part of the verify step: pack, forward, LM head, accept.  ``sampled``:
+        some slot samples, so the LM head writes every row's logits (greedy slots take
+        their argmax from them); otherwise it writes only the argmax partials."""
         kernels.prepare_verify_step(
             self.history, self.history_len, self.drafts, self.num_drafts, self.block_tables,
             self.block_size, self.pool.scratch_slot, self.tokens, self.positions, self.slot_mapping,
@@ -300,8 +343,7 @@ class VerifyRunner:
         )
         rows = self.max_seqs * self.R
         hidden = self.model.forward(rows, self.tokens, self.batch, self.pool)
-        greedy = self.temperature == GREEDY_TEMPERATURE
-        if greedy:
+        if not sampled:
             self.model.compute_logits(hidden, logits=False, argmax=self.argmax_partials)
             logits = None
         else:
@@ -310,30 +352,34 @@ class VerifyRunner:
                                           device=self.device)
             self.model.compute_logits(hidden, logits=self.logits, argmax=False)
             logits = self.logits
+        draft_logits = None if not sampled or self.proposer is None else self.proposer.logits
         kernels.accept(
             self.drafts, self.num_drafts, self.row_start, self.model.config.vocab_size, logits=logits,
-            argmax_partials=self.argmax_partials if greedy else None,
-            temperature=self.temperature or 0.0, seeds=self.seeds, steps=self.steps,
+            argmax_partials=None if sampled else self.argmax_partials,
+            temperature=self.temperatures, top_p=self.top_ps, any_sampled=sampled,
+            seeds=self.seeds, steps=self.steps,
             out_tokens=self.out_tokens, num_out=self.num_out, history=self.history,
             history_len=self.history_len, num_cached=self.num_cached,
             # a sampled draft model's guesses are verified against its distributions
-            draft_logits=None if greedy or self.proposer is None else self.proposer.logits,
-            draft_row_start=None if greedy or self.proposer is None else self.proposer.row_start,
+            draft_logits=draft_logits,
+            draft_row_start=None if draft_logits is None else self.proposer.row_start,
         )
 
     def _run_device_step(self) -> None:
+        sampled = self.any_sampled
         if not self.use_graph:
-            self._device_step()
+            self._device_step(sampled)
             return
-        if self.graph is None or self.graph_temperature != self.temperature:
+        if self.graph is None or self.graph_sampled != sampled:
             # this step runs eagerly (which also allocates lazily created buffers and
             # workspaces); the capture below only records, so nothing runs twice
-            self._device_step()
+            self._device_step(sampled)
             torch.cuda.current_stream(self.device).synchronize()
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph):
-                self._device_step()
-            self.graph_temperature = self.temperature
+                self._device_step(sampled)
+            self.model.bind_graph()
+            self.graph_sampled = sampled
             return
         self.graph.replay()
 
@@ -357,7 +403,8 @@ class VerifyRunner:
         else:
             guesses = self.proposer.propose({s: slots[s] for s in active},
                                             {s: int(self.np_num_tokens[s]) for s in active},
-                                            temperature=self.temperature or 0.0, seeds=self.seeds,
+                                            temperature=self.batch_temperature, top_p=self.batch_top_p,
+                                            seeds=self.seeds,
                                             steps=self.np_steps)
             self.np_num_drafts[:] = 0
             np_drafts = self.h_drafts.numpy()
@@ -458,5 +505,5 @@ class VerifyRunner:
         self.np_owned[slot] = 0
         self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
         self.h_tables[slot].zero_()
-        if not self.active_slots:
-            self.temperature = None
+        self.np_temp[slot] = 0.0
+        self.np_top_p[slot] = 1.0

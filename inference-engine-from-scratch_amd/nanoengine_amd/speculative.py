@@ -65,36 +65,36 @@ class NgramProposer:
 
 def verify_proposal(proposal: Proposal, target_logits: torch.Tensor, params: SamplingParams,
                     generator: SamplingStream) -> list[int]:
-    """Kept guesses plus one target token (verifier.py:27-60) from device logits.
+    """Kept guesses plus one target token (verifier.py:27-60) from device logits, with the
+    request's temperature and top-p (sampling.py:21-38).
 
-    With ``proposal.probabilities`` (sampled), the kernel takes the draft's distributions
-    as rows of logits ``T * log(q)``, whose softmax at temperature T is q again (up to the
-    bf16 rounding of the rows); greedy acceptance does not use them."""
-    if params.temperature != GREEDY_TEMPERATURE and params.top_p < 1.0:
-        raise NotImplementedError("top_p < 1 is not implemented on the HIP acceptance path")
+    ``proposal.probabilities`` (a sampled draft) are the fp32 distributions the guesses
+    were drawn from; the kernel uses them as given, as the reference does
+    (verifier.py:44-45).  Greedy acceptance does not use them."""
     guesses = proposal.token_ids
     g = len(guesses)
     if target_logits.shape[0] != g + 1:
         raise ValueError("target_logits must have one row per guess plus one")
     dev = target_logits.device
+    vocab = target_logits.shape[1]
     k = max(g, 1)
     drafts = torch.zeros(1, k, dtype=torch.int32)
     drafts[0, :g] = torch.tensor(guesses, dtype=torch.int32)
     sampled = params.temperature != GREEDY_TEMPERATURE
-    draft_logits = None
+    draft_probs = None
     if sampled and proposal.probabilities is not None and g > 0:
-        q = proposal.probabilities.to(dev, torch.float32)
-        if q.shape != (g, target_logits.shape[1]):
+        draft_probs = proposal.probabilities.to(dev, torch.float32).contiguous()
+        if draft_probs.shape != (g, vocab):
             raise ValueError("probabilities must be [len(guesses), vocab]")
-        draft_logits = (torch.log(q) * float(params.temperature)).to(torch.bfloat16).contiguous()
     out, n = kernels.accept(
         drafts.to(dev), torch.tensor([g], dtype=torch.int32, device=dev),
-        torch.zeros(1, dtype=torch.int32, device=dev), target_logits.shape[1],
+        torch.zeros(1, dtype=torch.int32, device=dev), vocab,
         logits=target_logits.to(torch.bfloat16).contiguous(), temperature=float(params.temperature),
+        top_p=float(params.top_p),
         seeds=torch.tensor([generator.seed], dtype=torch.int64, device=dev),
         steps=torch.tensor([generator.step], dtype=torch.int64, device=dev),
-        draft_logits=draft_logits,
-        draft_row_start=torch.zeros(1, dtype=torch.int32, device=dev) if draft_logits is not None else None,
+        draft_probs=draft_probs,
+        draft_row_start=torch.zeros(1, dtype=torch.int32, device=dev) if draft_probs is not None else None,
     )
     generator.step += 1
     count = int(n.cpu()[0])

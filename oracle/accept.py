@@ -44,6 +44,17 @@ def lib() -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
             ctypes.c_int, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p,
         ]
+        handle.oracle_accept_sampled_v2.restype = ctypes.c_int
+        handle.oracle_accept_sampled_v2.argtypes = [
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
+            ctypes.c_float, ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64,
+            ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        handle.oracle_top_p_kept.restype = ctypes.c_float
+        handle.oracle_top_p_kept.argtypes = [
+            ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p,
+        ]
         handle.oracle_accept_sampled.restype = ctypes.c_int
         handle.oracle_accept_sampled.argtypes = [
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
@@ -123,3 +134,48 @@ def sampled_accept_draft(row_bits: np.ndarray, draft_bits: np.ndarray, drafts: l
         ctypes.c_float(temperature), seed, step, out.ctypes.data, scratch.ctypes.data,
     )
     return out[:n].tolist()
+
+
+def sampled_accept_v2(row_bits: np.ndarray, drafts: list[int], temperature: float, top_p: float, seed: int,
+                      step: int, draft_bits: np.ndarray | None = None,
+                      draft_probs: np.ndarray | None = None) -> list[int]:
+    """The contract with top-p and an optional draft distribution per guess (C oracle):
+    ``row_bits [g+1, V]`` target bf16 patterns; ``draft_bits [g, V]`` the draft model's
+    bf16 logits (its distribution: the same top-p softmax) or ``draft_probs [g, V]``
+    fp32 probabilities used as given; neither: one-hot (n-gram) guesses."""
+    rows = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    g = len(drafts)
+    assert rows.shape[0] == g + 1
+    vocab = rows.shape[1]
+    d = np.ascontiguousarray(np.asarray(drafts, dtype=np.int32))
+    out = np.zeros(g + 1, dtype=np.int32)
+    scratch = np.zeros(4 * vocab + vocab // 2 + 1, dtype=np.float32)
+    if draft_bits is not None:
+        dr = np.ascontiguousarray(draft_bits, dtype=np.uint16)
+        is_probs = 0
+    elif draft_probs is not None:
+        dr = np.ascontiguousarray(draft_probs, dtype=np.float32)
+        is_probs = 1
+    else:
+        dr, is_probs = None, 0
+    assert dr is None or (dr.shape[0] >= g and dr.shape[1] == vocab)
+    n = lib().oracle_accept_sampled_v2(
+        rows.ctypes.data, vocab, vocab, d.ctypes.data if g else None, g, ctypes.c_float(temperature),
+        ctypes.c_float(top_p), None if dr is None else dr.ctypes.data, is_probs, vocab, seed, step,
+        out.ctypes.data, scratch.ctypes.data,
+    )
+    return out[:n].tolist()
+
+
+def top_p_kept(row_bits: np.ndarray, temperature: float, top_p: float) -> tuple[np.ndarray, float, int, int]:
+    """Kept flags of one row under the contract's top-p, with K, the threshold key and
+    the count of threshold ties kept."""
+    row = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    vocab = row.shape[0]
+    kept = np.zeros(vocab, dtype=np.uint8)
+    w = np.zeros(vocab, dtype=np.float32)
+    tau = ctypes.c_uint32(0)
+    m = ctypes.c_int(0)
+    k = lib().oracle_top_p_kept(row.ctypes.data, vocab, ctypes.c_float(temperature), ctypes.c_float(top_p),
+                                kept.ctypes.data, w.ctypes.data, ctypes.byref(tau), ctypes.byref(m))
+    return kept.astype(bool), float(k), int(tau.value), int(m.value)

@@ -144,6 +144,193 @@ static int draw(const float* e, int vocab, int excl, float u) {
   return 0;
 }
 
+/* ---- top-p (sampling.py:21-27) under the contract ----------------------------
+ * Tokens rank by bf16 logit (larger first; -0 ranks as +0), ties by index.  With
+ * M(v) = the chunked fp32 total of e_j over tokens whose key exceeds v, thr = top_p * Z:
+ *   tau = the smallest key v with M(v) < thr (found by bisection over 16-bit keys);
+ *   m   = the number of r in [0, H) with M(tau) + r * E(tau) < thr, H = tokens with
+ *         key tau, E(tau) their common e value;
+ *   a token is kept iff key > tau, or key == tau and fewer than m tokens of key tau
+ *   precede it; K = chunked fp32 total of the kept e_j; p'_j = e_j / K when kept, else 0.
+ * top_p >= 1 keeps every token (K = Z). */
+static uint32_t key_of_bf16(uint16_t b) {
+  if ((b & 0x7FFFu) == 0) b = 0;
+  return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
+}
+
+static uint16_t bf16_of_key(uint32_t k) {
+  return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k & 0xFFFFu);
+}
+
+typedef struct {
+  const uint16_t* row; /* bf16 logits */
+  int vocab;
+  float temperature;
+  float mx;
+  float z;     /* chunked total of e */
+  float total; /* K: chunked total of the kept e (z without top-p) */
+  int topp;
+  uint32_t tau;
+  int m;
+} row_dist;
+
+static float dist_e(const row_dist* d, int j) {
+  return oracle_cephes_exp(bf16_value(d->row[j]) / d->temperature - d->mx);
+}
+
+static float masked_total(const row_dist* d, uint32_t v) {
+  const int ch = (d->vocab + CHUNKS - 1) / CHUNKS;
+  float t = 0.0f;
+  for (int c = 0; c < CHUNKS; ++c) {
+    float s = 0.0f;
+    const int lo = c * ch;
+    const int hi = lo + ch < d->vocab ? lo + ch : d->vocab;
+    for (int j = lo; j < hi; ++j)
+      if (key_of_bf16(d->row[j]) > v) s = s + dist_e(d, j);
+    t = t + s;
+  }
+  return t;
+}
+
+/* kept flags of a whole row in index order (the tie rank runs over the row) */
+static void dist_kept(const row_dist* d, unsigned char* kept) {
+  int ties = 0;
+  for (int j = 0; j < d->vocab; ++j) {
+    const uint32_t k = key_of_bf16(d->row[j]);
+    if (!d->topp || k > d->tau) {
+      kept[j] = 1;
+    } else if (k == d->tau) {
+      kept[j] = ties < d->m;
+      ++ties;
+    } else {
+      kept[j] = 0;
+    }
+  }
+}
+
+static void dist_setup(row_dist* d, const uint16_t* row, int vocab, float temperature, float top_p,
+                       unsigned char* kept, float* w) {
+  d->row = row;
+  d->vocab = vocab;
+  d->temperature = temperature;
+  float mx = -INFINITY;
+  for (int j = 0; j < vocab; ++j) {
+    const float zj = bf16_value(row[j]) / temperature;
+    if (zj > mx) mx = zj;
+  }
+  d->mx = mx;
+  for (int j = 0; j < vocab; ++j) w[j] = dist_e(d, j);
+  float sums[CHUNKS];
+  chunk_sums(w, vocab, -1, sums);
+  d->z = total(sums);
+  d->topp = top_p < 1.0f;
+  d->tau = 0;
+  d->m = 0;
+  if (d->topp) {
+    const float thr = top_p * d->z;
+    uint32_t lo = 0, hi = 65535;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (masked_total(d, mid) < thr) hi = mid; else lo = mid + 1;
+    }
+    d->tau = lo;
+    int h = 0;
+    for (int j = 0; j < vocab; ++j) h += key_of_bf16(row[j]) == lo;
+    const float mt = masked_total(d, lo);
+    const float e_tau = oracle_cephes_exp(bf16_value(bf16_of_key(lo)) / temperature - mx);
+    int a = 0, b = h; /* m = number of r in [0, h) with mt + r * e_tau < thr */
+    while (a < b) {
+      const int mid = (a + b) / 2;
+      if (mt + (float)mid * e_tau < thr) a = mid + 1; else b = mid;
+    }
+    d->m = a;
+  }
+  dist_kept(d, kept);
+  for (int j = 0; j < vocab; ++j) w[j] = kept[j] ? w[j] : 0.0f;
+  chunk_sums(w, vocab, -1, sums);
+  d->total = total(sums);
+}
+
+/*
+ * Acceptance of one sequence under the contract with per-sequence top-p and an
+ * optional draft distribution per guess:
+ *   draft_rows == NULL     n-gram guesses (one-hot draft)
+ *   draft_is_probs == 0    bf16 draft logits; q' = the same top-p softmax of the draft row
+ *   draft_is_probs == 1    fp32 draft probabilities, used as given
+ * Guess i is kept iff a >= 1 or (a > 0 and u_i < a), a = p'_g (one-hot) or
+ * min(p'_g / max(q_g, 1e-12), 1); a rejection draws from p' without g (one-hot) or
+ * from max(p' - q, 0) (each p'_j = e_j / K one fp32 division, each difference one op),
+ * falling back to p' when that has no mass; the bonus draws from p'.
+ * `scratch` holds 4 * vocab floats + 2 * vocab bytes.
+ */
+int oracle_accept_sampled_v2(const uint16_t* logits, int64_t ld, int vocab, const int32_t* drafts, int num_drafts,
+                             float temperature, float top_p, const void* draft_rows, int draft_is_probs,
+                             int64_t ldq, uint64_t seed, uint64_t step, int32_t* out, void* scratch) {
+  float* w = (float*)scratch;
+  float* f = w + vocab;
+  float* r = f + vocab;
+  unsigned char* kept = (unsigned char*)(r + vocab);
+  unsigned char* keptq = kept + vocab;
+  float sums[CHUNKS];
+  int n_out = 0;
+  for (int i = 0; i < num_drafts; ++i) {
+    row_dist d;
+    dist_setup(&d, logits + (int64_t)i * ld, vocab, temperature, top_p, kept, w);
+    const int guess = drafts[i];
+    const float p = kept[guess] ? w[guess] / d.total : 0.0f;
+    const float u = oracle_uniform(seed, step, i);
+    float a;
+    row_dist dq;
+    if (draft_rows == NULL) {
+      a = p;
+    } else if (draft_is_probs) {
+      const float* q = (const float*)draft_rows + (int64_t)i * ldq;
+      a = fminf(p / fmaxf(q[guess], 1e-12f), 1.0f);
+    } else {
+      dist_setup(&dq, (const uint16_t*)draft_rows + (int64_t)i * ldq, vocab, temperature, top_p, keptq, f);
+      const float q = keptq[guess] ? f[guess] / dq.total : 0.0f;
+      a = fminf(p / fmaxf(q, 1e-12f), 1.0f);
+    }
+    if (a >= 1.0f || (a > 0.0f && u < a)) {
+      out[n_out++] = guess;
+      continue;
+    }
+    const float u_draw = oracle_uniform(seed, step, 63);
+    if (draft_rows == NULL) {
+      out[n_out] = draw(w, vocab, guess, u_draw);
+      return n_out + 1;
+    }
+    for (int j = 0; j < vocab; ++j) {
+      const float pj = kept[j] ? w[j] / d.total : 0.0f;
+      float qj;
+      if (draft_is_probs) {
+        qj = ((const float*)draft_rows)[(int64_t)i * ldq + j];
+      } else {
+        qj = keptq[j] ? f[j] / dq.total : 0.0f;
+      }
+      const float rj = pj - qj;
+      r[j] = rj > 0.0f ? rj : 0.0f;
+    }
+    chunk_sums(r, vocab, -1, sums);
+    out[n_out] = total(sums) > 0.0f ? draw(r, vocab, -1, u_draw) : draw(w, vocab, -1, u_draw);
+    return n_out + 1;
+  }
+  row_dist d;
+  dist_setup(&d, logits + (int64_t)num_drafts * ld, vocab, temperature, top_p, kept, w);
+  out[n_out] = draw(w, vocab, -1, oracle_uniform(seed, step, 63));
+  return n_out + 1;
+}
+
+/* kept flags and K of one row under top-p (for the pins) */
+float oracle_top_p_kept(const uint16_t* row, int vocab, float temperature, float top_p, unsigned char* kept,
+                        float* w, uint32_t* tau, int* m) {
+  row_dist d;
+  dist_setup(&d, row, vocab, temperature, top_p, kept, w);
+  *tau = d.tau;
+  *m = d.m;
+  return d.total;
+}
+
 /*
  * One sequence: rows [num_drafts + 1][ld] bf16 logits (bit patterns), guesses
  * drafts[0..num_drafts).  Writes kept guesses + 1 token to out, returns the

@@ -107,6 +107,11 @@ class ContiguousSlotAllocator:
         self._free_regions = list(range(num_regions - 1, -1, -1))
         self._region: dict[str, int] = {}
 
+    @property
+    def num_reserved_slots(self) -> int:
+        """contiguous_allocator.py:25-27: a whole region per sequence holding one."""
+        return len(self._region) * self.region_length
+
     def can_reserve(self, request_id: str, num_tokens: int) -> bool:
         if num_tokens > self.region_length:
             return False

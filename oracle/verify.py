@@ -173,6 +173,7 @@ class SpeculativeStats:
     steps: int = 0
     step_seconds: list[float] = field(default_factory=list)
     accepted_per_step: list[int] = field(default_factory=list)
+    finish_reason: str | None = None
 
 
 def generate_speculative(runner: ModelRunner, sequence: Sequence, k: int, max_ngram: int,
@@ -191,6 +192,7 @@ def generate_speculative(runner: ModelRunner, sequence: Sequence, k: int, max_ng
                                         sequence.ignore_eos, stop_token_ids)
             if reason is not None:
                 runner.allocator.free(sequence.request_id)
+                stats.finish_reason = reason
                 return emitted
         started = time.perf_counter()
         g = ngram.num_guesses(sequence.max_new_tokens, sequence.num_generated, k)

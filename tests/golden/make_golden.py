@@ -105,6 +105,36 @@ REFERENCE_KATS = {
         "logits": [0.1, 3.0, -1.0, 2.9],
         "expected": 1,
     },
+    "contiguous_allocator": {
+        "source": "nanoengine/tests/engine/test_memory_allocators.py:34-49",
+        "num_regions": 2,
+        "region_length": 8,
+        "reserve": [["a", 2], ["b", 8]],
+        "expected_reserved_slots": 16,
+        "refused": [["c", 1], ["a", 9]],
+        "free": "a",
+        "accepted_after_free": ["c", 1],
+        "context": ["b", 3],
+        "region_start_multiple": 8,
+    },
+    "speculative_stop_token": {
+        "source": "nanoengine/tests/engine/test_speculative_decoding.py:100-112; prompt "
+        "nanoengine/tests/engine/test_batch_engine_loop.py:20 (PROMPTS[0]); settings "
+        "test_batch_engine_loop.py:30-39 and nanoengine/src/nanoengine/config.py:55,64-67; "
+        "model nanoengine/tests/conftest.py:23-43",
+        "model": {"vocab_size": 64, "hidden_size": 32, "intermediate_size": 64, "num_hidden_layers": 2,
+                  "num_attention_heads": 4, "num_key_value_heads": 2, "head_dim": 16, "rms_norm_eps": 1e-6,
+                  "rope_theta": 10000.0, "seed": 7, "std": 0.5},
+        "prompt": [3, 9, 27],
+        "max_new_tokens": 12,
+        "greedy_reference_new_tokens": 12,
+        "stop_token_greedy_index": 3,
+        "kv_block_size": 4,
+        "num_speculative_tokens": 4,
+        "ngram_max_size": 3,
+        "expected_finish_reason": "stop",
+        "max_events": 4,
+    },
 }
 
 

@@ -54,9 +54,17 @@ def test_host_checks_reject_bad_arguments_without_launching(lib):
     # W8A16 GEMM: k must be a multiple of 128
     rc = lib.ne_w8a16_gemm(p, 1000, p, p, 0, 320, 1024, 1000, p, 1024, 0, null)
     assert rc == -2
-    rc = lib.ne_accept(0, null, 0, null, 0, 100, p, 0, p, p, 2, 0.0, null, null, p, p, null, 0, null, null,
-                       null, 0, null, null)
-    assert rc == -1  # max_drafts 0
+    rc = lib.ne_accept(null, 0, p, 10, 100, p, 0, p, p, 2, null, null, 0, null, null, p, p, null, 0, null, null,
+                       null, 0, 0, null, null)
+    assert rc == -1 and b"max_drafts" in lib.ne_last_error()
+    # sampled sequences need per-sequence temperatures and logits
+    rc = lib.ne_accept(null, 0, p, 10, 100, p, 4, p, p, 2, null, null, 1, p, p, p, p, null, 0, null, null,
+                       null, 0, 0, null, null)
+    assert rc == -1 and b"temperature" in lib.ne_last_error()
+    # draft rows must be bf16 logits or fp32 probabilities
+    rc = lib.ne_accept(p, 100, null, 0, 100, p, 4, p, p, 2, p, null, 1, p, p, p, p, null, 0, null, null,
+                       p, 3, 100, p, null)
+    assert rc == -1 and b"draft rows" in lib.ne_last_error()
 
 
 def test_workspace_and_tile_queries(lib):

@@ -262,3 +262,81 @@ def test_head_split_planned_path(device, num_seqs, max_ctx):
     assert rel_err(b.cpu()[idx], ref[idx]) < TOL
     # the same values as one wave per head, up to the order of the fp32 sums (bf16 output)
     assert float((b.cpu()[idx].float() - a.cpu()[idx].float()).abs().max()) <= 2e-2 * float(a.cpu()[idx].float().abs().max())
+
+
+def _random_int8_pool(num_slots, scale_dtype, seed):
+    """int8 codes U{-127..127} and per-(slot, head) scales in [0.005, 0.035): the layout the
+    reference's int8 KV pool holds (ne/engine/memory/kv_cache_pool.py:49-69)."""
+    g = torch.Generator().manual_seed(seed)
+    kc = torch.randint(-127, 128, (num_slots, HKV, 128), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (num_slots, HKV, 128), generator=g, dtype=torch.int8)
+    ks = (torch.rand(num_slots, HKV, generator=g) * 0.03 + 0.005).to(scale_dtype)
+    vs = (torch.rand(num_slots, HKV, generator=g) * 0.03 + 0.005).to(scale_dtype)
+    return kc, vc, ks, vs
+
+
+def test_cfg4_long_context_shared_prefix_plan_and_unplanned(device):
+    """The long-context + prefix-sharing configuration: 32 sequences whose tables start with
+    the same 64 blocks (a 1024-token shared prefix) followed by U{4096..16384} own tokens
+    (seed 1), k = 8 (9 queries), int8 KV with bf16 scales; one sequence is stretched to
+    17,408 keys so the plan splits contexts above 8,192 keys over more than one split
+    grid.  The per-step plan + planned call and the unplanned call both match the oracle
+    (gather + dequant + masked softmax in fp32), agree bit for bit, and raise no error flag."""
+    bs, shared, q = 16, 1024, 9
+    rng = np.random.default_rng(1)
+    ctx = [int(shared + s) for s in rng.integers(4096, 16385, size=32)]
+    ctx[7] = 17408
+    own = [(c - shared + bs - 1) // bs for c in ctx]
+    num_blocks = shared // bs + sum(own) + 1
+    kc, vc, ks, vs = _random_int8_pool(num_blocks * bs + 1, torch.bfloat16, seed=21)
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    tables = torch.zeros(32, max((c + bs - 1) // bs for c in ctx), dtype=torch.int32)
+    cur = shared // bs
+    for i, n in enumerate(own):
+        tables[i, : shared // bs] = perm[: shared // bs]
+        tables[i, shared // bs : shared // bs + n] = perm[cur : cur + n]
+        cur += n
+    ctx_t = torch.tensor(ctx, dtype=torch.int32)
+    ql = torch.full((32,), q, dtype=torch.int32)
+    qs = torch.arange(32, dtype=torch.int32) * q
+    qt = torch.randn(32 * q, HQ, 128, generator=torch.Generator().manual_seed(22)).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    tables_d, ctx_d, qs_d, ql_d = d(tables), d(ctx_t), d(qs), d(ql)
+    args = (d(qt), d(kc), d(vc), d(ks), d(vs), tables_d, bs, ctx_d, qs_d, ql_d)
+    ws = kernels.AttentionWorkspace()
+    unplanned = kernels.paged_verify_attention(*args, max_q_len=q, max_ctx_len=max(ctx), workspace=ws)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    kernels.paged_attention_plan(tables_d, bs, ctx_d, qs_d, ql_d, HQ, HKV, q, max(ctx), ws)
+    planned = kernels.paged_verify_attention(*args, max_q_len=q, max_ctx_len=max(ctx), workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    assert torch.equal(planned.cpu(), unplanned.cpu())
+    ref = paged_attention_reference(qt, kc, vc, ks, vs, tables, bs, ctx_t, qs, ql, model_dtype=torch.bfloat16)
+    assert rel_err(planned.cpu(), ref) < TOL
+    for b in (7, int(np.argmin(ctx))):  # the longest and the shortest sequence on their own
+        rows = slice(b * q, (b + 1) * q)
+        assert rel_err(planned.cpu()[rows], ref[rows]) < TOL, f"sequence {b} ({ctx[b]} keys)"
+
+
+def test_cfg2_planned_fp16_scales_roofline_variant(device):
+    """The call the attention roofline times: the per-step plan and the planned call at the
+    int8 configuration (64 sequences, context U{128..1024} seed 1, 5 queries, fp16 scales,
+    4096-block pool), which serves each sequence as one whole item over 4 work-groups with
+    4 waves per KV head merged in LDS."""
+    rng = np.random.default_rng(1)
+    ctx = rng.integers(128, 1025, size=64).tolist()
+    kc, vc, ks, vs = make_pool(4096, 16, HKV, "int8", torch.float16, seed=0)
+    tables, ctx_t, qs, ql, rows = make_batch(ctx, [5] * 64, 4096, 16, seed=1)
+    qt = torch.randn(rows, HQ, 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    d = lambda t: t.to(device)
+    tables_d, ctx_d, qs_d, ql_d = d(tables), d(ctx_t), d(qs), d(ql)
+    assert kernels.plan_supported(HQ, HKV, 5, 64, torch.int8, torch.float16)
+    ws = kernels.AttentionWorkspace()
+    kernels.paged_attention_plan(tables_d, 16, ctx_d, qs_d, ql_d, HQ, HKV, 5, max(ctx), ws)
+    out = kernels.paged_verify_attention(d(qt), d(kc), d(vc), d(ks), d(vs), tables_d, 16, ctx_d, qs_d, ql_d,
+                                         max_q_len=5, max_ctx_len=max(ctx), workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    ref = paged_attention_reference(qt, kc, vc, ks, vs, tables, 16, ctx_t, qs, ql, model_dtype=torch.float16)
+    assert rel_err(out.cpu(), ref) < TOL

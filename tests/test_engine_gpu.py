@@ -168,20 +168,6 @@ def test_serial_generator_matches_batched():
     assert serial_engine.allocator.num_reserved_slots == 0  # freed when each request ends
 
 
-def test_stop_token_ends_a_request_early():
-    state = make_state(norm_ones=True)
-    prompt = motif_prompts(1, seed=9)[0]
-    eng = engine_for(state, 1)
-    params = SamplingParams(max_new_tokens=12, ignore_eos=True)
-    tokens = [e.token_id for e in eng.serial_generator().generate(GenerationRequest("a", prompt, params))]
-    stop = tokens[3]
-    eng.runner.stop_token_ids = frozenset({stop})
-    events = list(eng.serial_generator().generate(
-        GenerationRequest("b", prompt, SamplingParams(max_new_tokens=12))))
-    assert events[-1].finish_reason == "stop" and events[-1].token_id == stop
-    assert len(events) == tokens.index(stop) + 1
-
-
 # ------------------------------------------------------------------ prefix cache
 def prefix_engine(state, num_seqs, graphs=False):
     settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
@@ -299,3 +285,211 @@ def test_prefix_cached_speculation_keeps_shared_blocks_and_matches_oracle(graphs
     hits = eng.allocator.num_prefix_hit_tokens
     eng.runner.add([again])
     assert eng.allocator.num_prefix_hit_tokens - hits == ((len(history) - 1) // 16) * 16
+
+
+# ------------------------------------------------------------------ stop tokens
+def _oracle_fp32(state):
+    ref32 = om.Qwen3ForCausalLM(OCFG)
+    ref32.load_state_dict(state)
+    ref32 = ref32.eval()
+    om.quantize_linear_layers(ref32)
+    return ref32
+
+
+def _clear_greedy_prefix(model, prompt, n):
+    """The oracle's greedy tokens after `prompt` and whether each one's top-2 margin is
+    clear of bf16 rounding (2e-2 of the logit scale)."""
+    ids, out, clear = list(prompt), [], []
+    with torch.inference_mode():
+        for _ in range(n):
+            row = model.compute_logits(model(torch.tensor([ids])))[0, -1]
+            top2 = torch.topk(row, 2)
+            out.append(int(top2.indices[0]))
+            clear.append(float(top2.values[0] - top2.values[1]) > 2e-2 * float(row.abs().max()))
+            ids.append(out[-1])
+    return out, clear
+
+
+def test_stop_token_matches_the_oracle_loop():
+    """nt/engine/test_speculative_decoding.py:100-112 against the oracle: the 4th greedy token
+    is the stop token; the engine's events equal the oracle's serial speculative loop
+    (oracle/verify.py generate_speculative on a paged cache) and end with "stop".  The
+    prompt is the first motif prompt whose first four greedy tokens have clear margins."""
+    from oracle import verify as ov
+    from oracle.paging import PagedSlotAllocator
+
+    state = make_state(norm_ones=True)
+    ref32 = _oracle_fp32(state)
+    for seed in range(9, 40):
+        prompt = motif_prompts(1, seed=seed)[0]
+        greedy, clear = _clear_greedy_prefix(ref32, prompt, 4)
+        if all(clear):
+            break
+    else:
+        pytest.fail("no motif prompt with four clear greedy tokens")
+    stop = greedy[3]
+    runner = ov.ModelRunner(ref32, om.KVCachePool(OCFG, 256, torch.float32), PagedSlotAllocator(16, 16))
+    oseq = ov.Sequence("o", list(prompt), len(prompt), 12, ignore_eos=False)
+    stats = ov.SpeculativeStats()
+    want = ov.generate_speculative(runner, oseq, 4, 3, frozenset({stop}), stats)
+    assert stats.finish_reason == "stop" and want[-1] == stop
+    eng = engine_for(state, 1)
+    eng.runner.stop_token_ids = frozenset({stop})
+    events = list(eng.serial_generator().generate(GenerationRequest("b", prompt, SamplingParams(max_new_tokens=12))))
+    assert [e.token_id for e in events] == want
+    assert events[-1].finish_reason == "stop" and events[-1].is_finished
+    assert eng.allocator.num_reserved_slots == 0
+
+
+# ------------------------------------------------------------------ mixed sampling
+def test_mixed_greedy_and_top_p_sampled_batch():
+    """Greedy and sampled (temperature, top-p) requests share verify steps: the greedy
+    requests emit exactly what they emit in an all-greedy batch, and a sampled step's
+    acceptance equals the C oracle's contract on that step's logits and guesses."""
+    from oracle import accept as oracle_accept
+
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(4, seed=21)
+    greedy_params = SamplingParams(max_new_tokens=24, ignore_eos=True)
+    # the same four prompts all greedy: the same prefill (and its attention split plan)
+    plain = engine_for(state, 4).batched_generator().generate_all(
+        [GenerationRequest(f"g{i}", p, greedy_params) for i, p in enumerate(prompts)])
+    eng = engine_for(state, 4)
+    params = [greedy_params, SamplingParams(max_new_tokens=24, temperature=0.8, top_p=0.9, seed=5, ignore_eos=True),
+              greedy_params, SamplingParams(max_new_tokens=24, temperature=1.0, top_p=0.5, seed=6, ignore_eos=True)]
+    seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params[i])) for i, p in enumerate(prompts)]
+    emitted = {i: [] for i in range(4)}
+    for slot, res in eng.runner.add(seqs).items():
+        emitted[slot] += res.tokens
+    eng.runner.trace = []
+    checked = 0
+    while eng.runner.active_slots:
+        steps = eng.runner.np_steps.copy()
+        results = eng.runner.step()
+        torch.cuda.synchronize()
+        rec = eng.runner.trace[-1]
+        logits = eng.runner.logits.view(torch.int16).cpu().numpy().view(np.uint16)
+        for slot, res in results.items():
+            emitted[slot] += res.tokens
+            p = params[slot]
+            if p.temperature > 0 and checked < 12:
+                g = len(rec[slot]["drafts"])
+                want = oracle_accept.sampled_accept_v2(logits[slot * 5 : slot * 5 + g + 1], rec[slot]["drafts"],
+                                                       p.temperature, p.top_p, seqs[slot].sampling_generator.seed,
+                                                       int(steps[slot]))
+                assert rec[slot]["out"] == want, f"slot {slot}"
+                checked += 1
+    assert checked > 0
+    assert emitted[0] == [e.token_id for e in plain["g0"]]
+    assert emitted[2] == [e.token_id for e in plain["g2"]]
+
+
+# ------------------------------------------------------------------ graphs
+def test_long_prompt_admitted_after_graph_capture_matches_eager():
+    """With HIP graphs, a request admitted after the verify step was captured prefills
+    eagerly with a much larger attention shape; its own workspace keeps the captured
+    graph's buffers in place, and every request's tokens equal an eager engine's."""
+    state = make_state(norm_ones=True)
+    g = torch.Generator().manual_seed(31)
+    motif = torch.randint(0, 512, (16,), generator=g).tolist()
+    prompts = motif_prompts(2, seed=30) + [motif * 75]  # 1200 tokens
+    params = SamplingParams(max_new_tokens=20, ignore_eos=True)
+    reqs = [GenerationRequest(f"r{i}", p, params) for i, p in enumerate(prompts)]
+
+    def run(graphs):
+        settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                                  quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                                  num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=2, max_model_len=1280,
+                                  kv_cache_memory_mb=64, cuda_graphs=graphs)
+        eng = create_verify_engine(CFG, state, settings, max_prefill_rows=2048)
+        out = eng.batched_generator().generate_all(reqs)
+        return eng, {k: [e.token_id for e in v] for k, v in out.items()}
+
+    eng, graphed = run(True)
+    assert eng.runner.graph is not None and eng.model.workspace.frozen
+    _, eager = run(False)
+    assert graphed == eager
+    assert all(len(v) == 20 for v in graphed.values())
+
+
+# ------------------------------------------------------------------ metrics
+def test_acceptance_metrics_equal_the_per_step_recount():
+    """EngineMetrics' proposed / accepted counters (metrics.py:66-75, incremented as
+    speculative_generator.py:87-90 does) equal a recount over the trace: each step's
+    guesses are oracle.ngram.propose on that step's history, and kept = the longest prefix
+    of the guesses the emitted tokens repeat; the benchmark's derived rates follow
+    (ne/benchmarks/speculative.py:104-114)."""
+    from nanoengine_amd.metrics import acceptance_rate, tokens_per_target_pass
+
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(5, seed=41)
+    eng = engine_for(state, 5)
+    eng.runner.trace = []
+    params = SamplingParams(max_new_tokens=30, ignore_eos=True)
+    events = eng.batched_generator().generate_all([GenerationRequest(f"r{i}", p, params) for i, p in enumerate(prompts)])
+    proposed = accepted = 0
+    for step in eng.runner.trace:
+        for slot, rec in step.items():
+            want = oracle_ngram.propose(rec["history"], rec["requested"], 3) if rec["requested"] else []
+            assert rec["drafts"] == want
+            kept = 0
+            while kept < len(want) and kept < len(rec["out"]) - 1 and rec["out"][kept] == want[kept]:
+                kept += 1
+            assert len(rec["out"]) == kept + 1
+            proposed += len(want)
+            accepted += kept
+    assert eng.metrics.proposed == proposed and eng.metrics.accepted == accepted
+    assert proposed > 0
+    tokens = sum(len(v) for v in events.values())
+    rate, per_pass = acceptance_rate(proposed, accepted), tokens_per_target_pass(tokens, accepted)
+    assert rate == accepted / proposed and per_pass == tokens / (tokens - accepted)
+
+
+# ------------------------------------------------------------------ full depth
+def test_full_depth_verify_step_logits_match_oracle():
+    """The Qwen3-0.6B architecture at full depth and vocabulary (28 layers, 151,936 tokens),
+    64 sequences of 64-token motif prompts, k = 4: one verify step's logits for a handful
+    of sequences against the oracle's bf16 model with int8 weights and int8 paged KV
+    (score_tokens, model_runner.py:52-62): max-abs <= 1e-2, relative <= 2e-2."""
+    from nanoengine_amd.qwen3 import QWEN3_0_6B
+
+    full = om.Qwen3Config(151936, 1024, 3072, 28, 16, 8, 128, 1e-6, 1e6, True)
+    state = random_state_dict(QWEN3_0_6B, seed=0, std=0.02)
+    prompts = motif_prompts(64, seed=0)
+    settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                              quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                              num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=64, max_model_len=256,
+                              kv_cache_memory_mb=1024)
+    eng = create_verify_engine(QWEN3_0_6B, state, settings, max_prefill_rows=64 * 64)
+    params = SamplingParams(max_new_tokens=32, temperature=0.8, seed=1, ignore_eos=True)
+    seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts)]
+    eng.runner.add(seqs)
+    eng.runner.trace = []
+    eng.runner.step()  # sampled: the step's logits stay in runner.logits
+    torch.cuda.synchronize()
+    ours = eng.runner.logits
+    step = eng.runner.trace[0]
+    picked = {s: ours[s * 5 : s * 5 + 1 + len(step[s]["drafts"])].float().cpu() for s in (0, 21, 42, 63)}
+    del eng, ours
+    torch.cuda.empty_cache()
+    model = om.Qwen3ForCausalLM(full)
+    model.load_state_dict(state)
+    del state
+    model = model.to(torch.bfloat16).eval()
+    om.quantize_linear_layers(model)
+    pool = om.KVCachePool(full, 16 * 16, torch.bfloat16, is_int8=True)
+    runner = OracleRunner(model, pool, OraclePaged(16, 16))
+    for slot, got in picked.items():
+        rec = step[slot]
+        seq = OracleSequence(f"o{slot}", list(prompts[slot]), 64, 32)
+        runner.allocator.reserve(seq.request_id, len(seq.token_ids))
+        runner.run_step([seq])
+        seq.token_ids = list(rec["history"]) + rec["drafts"]
+        runner.allocator.reserve(seq.request_id, len(seq.token_ids))
+        ref = runner.score_tokens(seq, 1 + len(rec["drafts"])).float()
+        runner.allocator.free(seq.request_id)
+        err = float((got - ref).abs().max())
+        rel = float((got - ref).norm() / ref.norm())
+        print(f"slot {slot}: max-abs {err:.3e}, relative {rel:.3e}, logit scale {float(ref.abs().max()):.3f}")
+        assert err <= 1e-2, f"slot {slot}: max-abs {err:.3e}"
+        assert rel <= 2e-2, f"slot {slot}: relative error {rel:.3e}"

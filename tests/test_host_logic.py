@@ -129,3 +129,25 @@ def test_splitk_split_counts_fill_the_gpu_and_divide_k():
         for k in (2048, 3072):
             s = kernels.splitk_splits(rows, 1024, k)
             assert s in (1, 2, 3, 4) and k % (128 * s) == 0
+
+
+def test_requests_longer_than_max_model_len_are_refused():
+    """api/routes.py:98-111: prompt + max_tokens above max_model_len, or an empty prompt,
+    is refused before admission (the device history rows are sized by max_model_len)."""
+    from nanoengine_amd.runner import request_length_error
+
+    assert request_length_error(64, 128, 192) is None
+    assert request_length_error(64, 129, 192) == "prompt + max_new_tokens = 193 exceeds max_model_len 192"
+    assert request_length_error(0, 4, 192) == "prompt is empty"
+
+
+def test_attention_workspace_held_by_a_graph_refuses_to_grow():
+    """Once a captured graph holds the workspace's address, a larger request raises
+    instead of moving the buffer; a request that fits reuses it."""
+    ws = kernels.AttentionWorkspace()
+    cpu = torch.device("cpu")
+    buf = ws.get(cpu, 4096, ("a",))
+    ws.frozen = True
+    assert ws.get(cpu, 1024, ("b",)) is buf
+    with pytest.raises(RuntimeError, match="captured HIP graph"):
+        ws.get(cpu, 8192, ("c",))

@@ -202,3 +202,88 @@ def test_sampled_golden_fixture(device):
     torch.cuda.synchronize()
     got = [out[s, : nout[s]].tolist() for s in range(len(case["expected"]))]
     assert got == case["expected"]
+
+
+@pytest.mark.parametrize("top_p", [0.5, 0.9])
+def test_top_p_mixed_batch_matches_c_oracle(device, top_p):
+    """A10 with top-p (sampling.py:21-38) at the full vocabulary: per-sequence temperatures
+    (some 0: greedy rows in the same call, read from the logits) and top-p values, each
+    sequence's tokens identical to the C oracle's contract (or to the greedy oracle)."""
+    vocab, b, k = 151936, 24, 4
+    rng = np.random.default_rng(int(top_p * 100))
+    logits, drafts, nd, rs = make_accept_case(rng, b, vocab, k, match_prob=0.5, scale=3.0)
+    temps = rng.choice([0.0, 0.7, 1.0, 1.3], size=b).astype(np.float32)
+    temps[:2] = [0.0, 0.8]
+    tops = np.where(rng.random(b) < 0.75, top_p, 1.0).astype(np.float32)
+    seeds = rng.integers(0, 2**62, size=b).astype(np.int64)
+    steps = rng.integers(0, 1000, size=b).astype(np.int64)
+    d = lambda a: torch.as_tensor(a).to(device)
+    out, nout = kernels.accept(d(drafts), d(nd), d(rs), vocab, logits=logits.to(device), temperature=d(temps),
+                               top_p=d(tops), any_sampled=True, seeds=d(seeds), steps=d(steps))
+    torch.cuda.synchronize()
+    out, nout = out.cpu(), nout.cpu()
+    bits = logits.view(torch.int16).numpy().view(np.uint16)
+    lf = logits.float().numpy()
+    for s in range(b):
+        rows = slice(rs[s], rs[s] + nd[s] + 1)
+        guesses = drafts[s, : nd[s]].tolist()
+        if temps[s] == 0:
+            want = oracle_accept.greedy_accept(lf[rows], guesses)
+        else:
+            want = oracle_accept.sampled_accept_v2(bits[rows], guesses, float(temps[s]), float(tops[s]),
+                                                   int(seeds[s]), int(steps[s]))
+        assert out[s, : nout[s]].tolist() == want, f"sequence {s} (T={temps[s]}, top_p={tops[s]})"
+
+
+@pytest.mark.parametrize("form", ["draft_logits", "draft_probs"])
+def test_draft_distributions_with_top_p_match_c_oracle(device, form):
+    """Guesses verified against a draft distribution (verifier.py:36-56): the draft model's
+    bf16 logits (q' = the same temperature / top-p softmax) or fp32 probabilities used as
+    given; top_p 0.9 on the target; identical to the C oracle."""
+    vocab, b, k, temp, top_p = 32000, 16, 4, 0.9, 0.9
+    rng = np.random.default_rng(77 if form == "draft_probs" else 78)
+    logits, drafts, nd, rs = make_accept_case(rng, b, vocab, k, match_prob=0.5, scale=3.0)
+    drow = (np.arange(b) * k).astype(np.int32)
+    dlog = torch.tensor(rng.standard_normal((b * k, vocab)) * 3.0, dtype=torch.float32).to(torch.bfloat16)
+    dbits = dlog.view(torch.int16).numpy().view(np.uint16)
+    dprobs = torch.softmax(dlog.float() / temp, dim=1).contiguous()
+    seeds = rng.integers(0, 2**62, size=b).astype(np.int64)
+    steps = rng.integers(0, 1000, size=b).astype(np.int64)
+    d = lambda a: torch.as_tensor(a).to(device)
+    kw = {"draft_logits": dlog.to(device)} if form == "draft_logits" else {"draft_probs": dprobs.to(device)}
+    out, nout = kernels.accept(d(drafts), d(nd), d(rs), vocab, logits=logits.to(device), temperature=temp,
+                               top_p=top_p, seeds=d(seeds), steps=d(steps), draft_row_start=d(drow), **kw)
+    torch.cuda.synchronize()
+    out, nout = out.cpu(), nout.cpu()
+    bits = logits.view(torch.int16).numpy().view(np.uint16)
+    for s in range(b):
+        rows = slice(rs[s], rs[s] + nd[s] + 1)
+        dr = slice(drow[s], drow[s] + k)
+        extra = {"draft_bits": dbits[dr]} if form == "draft_logits" else {"draft_probs": dprobs.numpy()[dr]}
+        want = oracle_accept.sampled_accept_v2(bits[rows], drafts[s, : nd[s]].tolist(), temp, top_p,
+                                               int(seeds[s]), int(steps[s]), **extra)
+        assert out[s, : nout[s]].tolist() == want, f"sequence {s}"
+
+
+def test_history_append_stops_at_the_row_capacity(device):
+    """A history row holds history_stride tokens: an append that would pass it writes only
+    what fits (the host refuses such requests; this bounds the kernel regardless)."""
+    vocab = 64
+    logits = torch.full((5, vocab), -5.0)
+    for r, t in enumerate([3, 4, 5, 6, 7]):
+        logits[r, t] = 5.0
+    drafts = torch.tensor([[3, 4, 5, 6]], dtype=torch.int32)
+    history = torch.full((2, 10), -9, dtype=torch.int32)  # row 1 must stay untouched
+    hl = torch.tensor([8, 0], dtype=torch.int32)
+    d = lambda a: a.to(device)
+    h = d(history)
+    hld = d(hl)
+    cached = torch.zeros(2, dtype=torch.int32, device=device)
+    out, nout = kernels.accept(d(torch.cat([drafts, drafts])), d(torch.tensor([4, 4], dtype=torch.int32)),
+                               d(torch.tensor([0, 0], dtype=torch.int32)), vocab,
+                               logits=d(logits.to(torch.bfloat16)), history=h, history_len=hld, num_cached=cached)
+    torch.cuda.synchronize()
+    assert out[0, : nout[0]].tolist() == [3, 4, 5, 6, 7]
+    assert h.cpu()[0].tolist() == [-9] * 8 + [3, 4]
+    assert h.cpu()[1].tolist() == [-9] * 10
+    assert hld.cpu().tolist() == [10, 0]

@@ -181,6 +181,125 @@ def test_top_p_reference_kat():
     assert abs(float(kept.sum()) - 1.0) < 1e-6
 
 
+def test_contract_top_p_reference_kat():
+    """The contract's top-p on the KAT's distribution given as bf16 logits log(p)."""
+    kat = KATS["top_p"]
+    bits = oacc.bf16_bits(np.log(np.asarray(kat["probabilities"], dtype=np.float32)))
+    kept, _, _, _ = oacc.top_p_kept(bits, 1.0, kat["top_p"])
+    assert np.nonzero(kept)[0].tolist() == kat["expected_nonzero"]
+
+
+def test_contract_top_p_closed_forms():
+    """top_p >= 1 keeps everything with K = Z; a tiny top_p keeps only the first index of
+    the largest logit (ties rank by index); K is the kept tokens' chunked total."""
+    rng = np.random.default_rng(5)
+    for trial in range(50):
+        vocab = int(rng.integers(2, 700))
+        vals = (rng.standard_normal(vocab) * 2).astype(np.float32)
+        if trial % 3 == 0:  # many exact ties
+            vals = np.round(vals).astype(np.float32)
+        bits = oacc.bf16_bits(vals)
+        temp = float(rng.uniform(0.3, 2.0))
+        kept_all, k_all, _, _ = oacc.top_p_kept(bits, temp, 1.0)
+        assert kept_all.all()
+        kept, _, _, _ = oacc.top_p_kept(bits, temp, 1e-7)
+        f = oacc.bf16_to_f32(bits)
+        assert np.nonzero(kept)[0].tolist() == [int(np.argmax(f))]
+        # K: the chunked sum of the kept exps equals a plain fp64 sum of them to fp32 accuracy
+        kept9, k9, _, _ = oacc.top_p_kept(bits, temp, 0.9)
+        e = np.exp(f.astype(np.float64) / np.float32(temp) - (f / np.float32(temp)).max())
+        assert abs(k9 - e[kept9].sum()) <= 1e-5 * e.sum()
+        assert abs(k_all - e.sum()) <= 1e-5 * e.sum()
+
+
+def test_contract_top_p_matches_a_sorted_scan():
+    """Brute force: sort by logit (desc), ties by index, and keep a token while the mass
+    before it is below top_p * Z (sampling.py:21-27 with the contract's tie order).  Cases
+    where some token's mass-before lies within rounding of the threshold are skipped."""
+    rng = np.random.default_rng(6)
+    checked = 0
+    for trial in range(300):
+        vocab = int(rng.integers(2, 200))
+        vals = (rng.standard_normal(vocab) * float(rng.uniform(0.5, 4))).astype(np.float32)
+        if trial % 2:
+            vals = (np.round(vals * 2) / 2).astype(np.float32)  # ties
+        bits = oacc.bf16_bits(vals)
+        f = oacc.bf16_to_f32(bits)
+        temp, top_p = float(rng.uniform(0.3, 2.0)), float(rng.uniform(0.05, 0.99))
+        z = f.astype(np.float64) / np.float32(temp)
+        e = np.exp(z - z.max())
+        order = sorted(range(vocab), key=lambda j: (-float(f[j]) + 0.0, j))
+        thr = top_p * e.sum()
+        before, want, ambiguous = 0.0, np.zeros(vocab, dtype=bool), False
+        for j in order:
+            if abs(before - thr) < 1e-4 * e.sum():
+                ambiguous = True
+            want[j] = before < thr
+            before += e[j]
+        if ambiguous:
+            continue
+        kept, _, _, _ = oacc.top_p_kept(bits, temp, top_p)
+        assert np.array_equal(kept, want), (trial, np.nonzero(kept ^ want))
+        checked += 1
+    assert checked > 200
+
+
+def test_contract_top_p_draws_follow_apply_top_p_chi_square():
+    """Bonus draws (no guesses) under the contract follow the reference's apply_top_p
+    distribution (oracle restatement of sampling.py:21-38) on the same bf16 logits."""
+    logits = np.log(np.array([0.3, 0.05, 0.25, 0.15, 0.1, 0.08, 0.07], dtype=np.float32))
+    bits = oacc.bf16_bits(logits)[None, :]
+    temp, top_p, trials = 0.9, 0.75, 6000
+    probs = ov.compute_token_probabilities(torch.from_numpy(oacc.bf16_to_f32(bits[0]).copy()), temp, top_p)
+    probs = probs.double().numpy()
+    keep = probs > 0
+    counts = np.zeros(7)
+    for step in range(trials):
+        counts[oacc.sampled_accept_v2(bits, [], temp, top_p, seed=99, step=step)[0]] += 1
+    assert counts[~keep].sum() == 0
+    critical = {2: 13.82, 3: 16.27, 4: 18.47, 5: 20.52}[int(keep.sum()) - 1]  # 0.999 quantiles
+    assert _chi_square(counts[keep], probs[keep], trials) < critical
+
+
+def test_contract_draft_probabilities_keep_the_target_distribution():
+    """fp32 draft probabilities used as given (verifier.py:44-56): with the guess drawn from
+    q, the first emitted token follows the target p (chi-square, the reference's test
+    distributions) and the acceptance rate is sum min(p, q)."""
+    kat = KATS["rejection_sampling_chi_square"]
+    target = np.asarray(kat["target"], dtype=np.float64)
+    q = np.asarray(kat["draft"], dtype=np.float32)
+    bits = oacc.bf16_bits(np.log(target).astype(np.float32))
+    bits = np.stack([bits, bits])
+    p_bf16 = np.exp(oacc.bf16_to_f32(bits[0]).astype(np.float64))
+    p_bf16 /= p_bf16.sum()
+    rng = np.random.default_rng(kat["seed"])
+    trials, counts, kept = kat["trials"], np.zeros(5), 0
+    for step in range(trials):
+        guess = int(rng.choice(5, p=q.astype(np.float64) / q.astype(np.float64).sum()))
+        out = oacc.sampled_accept_v2(bits, [guess], 1.0, 1.0, seed=777, step=step, draft_probs=q[None, :])
+        counts[out[0]] += 1
+        kept += len(out) == 2
+    assert _chi_square(counts, p_bf16, trials) < kat["critical_value"]
+    overlap = float(np.minimum(p_bf16, q).sum())
+    assert abs(kept / trials - overlap) < 4 * math.sqrt(overlap * (1 - overlap) / trials)
+
+
+def test_contract_v2_without_top_p_is_the_previous_contract():
+    """With top_p = 1 the generalised contract makes the same draws as the one-hot and the
+    draft-logit forms (both pinned above) on random rows."""
+    rng = np.random.default_rng(8)
+    for _ in range(100):
+        vocab, g = int(rng.integers(2, 300)), int(rng.integers(0, 5))
+        rows = oacc.bf16_bits((rng.standard_normal((g + 1, vocab)) * 3).astype(np.float32))
+        drows = oacc.bf16_bits((rng.standard_normal((max(g, 1), vocab)) * 3).astype(np.float32))
+        guesses = [int(x) for x in rng.integers(0, vocab, g)]
+        temp, seed, step = float(rng.uniform(0.3, 2)), int(rng.integers(0, 2**62)), int(rng.integers(0, 99))
+        assert oacc.sampled_accept_v2(rows, guesses, temp, 1.0, seed, step) == oacc.sampled_accept(
+            rows, guesses, temp, seed, step)
+        assert oacc.sampled_accept_v2(rows, guesses, temp, 1.0, seed, step, draft_bits=drows) == \
+            oacc.sampled_accept_draft(rows, drows, guesses, temp, seed, step)
+
+
 # ------------------------------------------------------------------ A7 / A8 int8
 def test_quantize_round_trip_reference_kat():
     torch.manual_seed(0)
@@ -308,6 +427,76 @@ def test_paged_attention_reference_against_textbook_fp64(kv):
 TINY = om.Qwen3Config(vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=2,
                       num_attention_heads=4, num_key_value_heads=2, head_dim=16, rms_norm_eps=1e-6,
                       rope_theta=1e4, tie_word_embeddings=True)
+
+
+def test_contiguous_allocator_reference_kat():
+    """nt/engine/test_memory_allocators.py:34-49: one whole region per sequence, refusals
+    for a third sequence and an over-long reservation, reuse after a free, contiguous
+    context slots starting at a region boundary."""
+    kat = KATS["contiguous_allocator"]
+    alloc = opg.ContiguousSlotAllocator(kat["num_regions"], kat["region_length"])
+    for rid, n in kat["reserve"]:
+        alloc.reserve(rid, n)
+    assert alloc.num_reserved_slots == kat["expected_reserved_slots"]
+    for rid, n in kat["refused"]:
+        assert not alloc.can_reserve(rid, n)
+    with pytest.raises(opg.OutOfKVMemoryError):
+        alloc.reserve(*kat["refused"][0])
+    alloc.free(kat["free"])
+    assert alloc.can_reserve(*kat["accepted_after_free"])
+    rid, c = kat["context"]
+    slots = alloc.build_context_slots([rid], c).tolist()[0]
+    assert slots == list(range(slots[0], slots[0] + c))
+    assert slots[0] % kat["region_start_multiple"] == 0
+    # closed form of the region order (contiguous_allocator.py:17, 36-38): regions are
+    # handed out from the low end, so the second sequence holds region 1
+    assert slots[0] == kat["region_length"]
+    alloc.reserve("c", 1)
+    assert alloc.build_context_slots(["c"], 2).tolist() == [[0, 1]]
+
+
+def test_find_finish_reason_closed_form():
+    """sampling.py:54-62: stop on a stop token unless ignore_eos; length at the limit."""
+    stops = frozenset({7})
+    assert ov.find_finish_reason(7, 1, 12, False, stops) == "stop"
+    assert ov.find_finish_reason(7, 1, 12, True, stops) is None
+    assert ov.find_finish_reason(7, 12, 12, True, stops) == "length"
+    assert ov.find_finish_reason(3, 12, 12, False, stops) == "length"
+    assert ov.find_finish_reason(3, 11, 12, False, stops) is None
+
+
+def _tiny_from_kat(m):
+    cfg = om.Qwen3Config(m["vocab_size"], m["hidden_size"], m["intermediate_size"], m["num_hidden_layers"],
+                         m["num_attention_heads"], m["num_key_value_heads"], m["head_dim"], m["rms_norm_eps"],
+                         m["rope_theta"], True)
+    return cfg, om.build_random_model(cfg, seed=m["seed"], std=m["std"])
+
+
+def test_speculative_stop_token_reference_kat():
+    """nt/engine/test_speculative_decoding.py:100-112: on a paged cache, a stop token (the
+    4th greedy token of a non-speculative full-recompute decode) ends the speculative
+    request with finish reason "stop" after at most 4 events; the tokens up to it equal
+    that greedy decode's."""
+    kat = KATS["speculative_stop_token"]
+    cfg, model = _tiny_from_kat(kat["model"])
+    prompt = kat["prompt"]
+    ids, greedy = list(prompt), []
+    with torch.no_grad():  # NaiveGenerator: full recompute per token
+        for _ in range(kat["greedy_reference_new_tokens"]):
+            tok = int(torch.argmax(model.compute_logits(model(torch.tensor([ids])))[0, -1]))
+            greedy.append(tok)
+            ids.append(tok)
+    stop = greedy[kat["stop_token_greedy_index"]]
+    bs = kat["kv_block_size"]
+    runner = ov.ModelRunner(model, om.KVCachePool(cfg, 64, torch.float32), opg.PagedSlotAllocator(64 // bs, bs))
+    seq = ov.Sequence("stop", list(prompt), len(prompt), kat["max_new_tokens"], ignore_eos=False)
+    stats = ov.SpeculativeStats()
+    out = ov.generate_speculative(runner, seq, kat["num_speculative_tokens"], kat["ngram_max_size"],
+                                  frozenset({stop}), stats)
+    assert stats.finish_reason == kat["expected_finish_reason"] and out[-1] == stop
+    assert len(out) <= kat["max_events"]
+    assert out == greedy[: greedy.index(stop) + 1]
+    assert runner.allocator.num_reserved_slots == 0  # the finished request's blocks are freed
 
 
 def test_model_matches_transformers_qwen3():
