@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 6
+#define NE_ABI_VERSION 7
 
 /* status codes */
 #define NE_OK 0
@@ -120,6 +120,31 @@ int ne_paged_verify_attention(const void* q, int64_t q_token_stride, int64_t q_h
                               int32_t max_ctx_len, float softmax_scale, void* out,
                               int64_t out_token_stride, int64_t out_head_stride, int32_t split_len,
                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free variant of ne_paged_verify_attention (no counterpart in the reference:
+ * for callers that cannot allocate or pass a workspace -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The same arguments and the same
+ * results as ne_paged_verify_attention, except that the work plan and split partials live
+ * in a library-owned device array of NE_NOALLOC_SCRATCH_BYTES per GPU (held until the
+ * process ends), and the error flag is the caller's device word `error_flag` (bits are
+ * OR-ed in as in the workspace's flag; the caller clears it).  A call needing more scratch
+ * (ne_paged_attention_workspace_size() > NE_NOALLOC_SCRATCH_BYTES) returns NE_EWORKSPACE
+ * without launching.  It allocates nothing: the scratch address is looked up once per
+ * device (hipGetSymbolAddress) on the first call with that device current.  Every call on
+ * one GPU shares that GPU's scratch, so calls that overlap on one GPU (concurrent streams)
+ * race; calls ordered on one stream do not.
+ */
+#define NE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ne_paged_verify_attention_noalloc(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
+    int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
+    int32_t block_size, const int32_t* ctx_len, const int32_t* q_start, const int32_t* q_len,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, uint32_t* error_flag,
+    void* stream);
 
 /*
  * A6 with the work plan computed once per step.  ne_paged_attention_plan writes into

@@ -47,6 +47,8 @@
 // which is legal because a dot product does not depend on summation order.
 #include <type_traits>
 
+#include <mutex>
+
 #include "ne_common.hpp"
 
 namespace ne {
@@ -1700,6 +1702,57 @@ int make_params(const void* q, int64_t q_token_stride, int64_t q_head_stride, co
   return NE_OK;
 }
 
+// Device scratch of the allocation-free entry point: the work plan and split partials of
+// one call, in a file-scope array each GPU holds for the life of the process.  Host code
+// never passes `scratch` itself (a host-side stand-in for the symbol): it passes the
+// device address hipGetSymbolAddress gives for the current device.
+constexpr size_t kNoAllocScratchBytes = (size_t)NE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the current device's scratch address, looked up once per device
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("no current HIP device (%s, device %d)", hipGetErrorString(err), dev);
+    return NE_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+      return NE_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NE_OK;
+}
+
+// the unplanned call on a prepared parameter block (shared by both unplanned entry points)
+int run_unplanned(AttnParams& p, int32_t kv_dtype, int32_t scale_dtype, int32_t num_kv_heads,
+                  int32_t num_seqs, const void* k_scale, const void* v_scale, hipStream_t stream) {
+  // int8 with 8 KV heads, one M tile and 2-byte scales: the DMA kernel on the
+  // balanced plan.  Other int8 shapes: one wave per KV head, registers
+  // double-buffered (154 VGPRs); bf16: single-buffered (double-buffered it needs
+  // 244 VGPRs).  Both on fixed-length splits.
+  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles <= kMaxRowTiles &&
+                      num_seqs <= kPlanMaxSeqs && scale_dtype != NE_DTYPE_FP32 &&
+                      ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
+  if (dma_ok) {
+    return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, false>(p, stream)
+                                        : launch_attention_dma<NE_DTYPE_FP16, false>(p, stream);
+  }
+  if (kv_dtype == NE_DTYPE_INT8) return launch_attention<1, true>(p, kv_dtype, scale_dtype, stream);
+  return launch_attention<1, false>(p, kv_dtype, scale_dtype, stream);
+}
+
 }  // namespace
 
 }  // namespace ne
@@ -1738,19 +1791,43 @@ extern "C" int ne_paged_verify_attention(
                              max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
                              out_head_stride, split_len, workspace, workspace_bytes, p);
   if (rc != NE_OK) return rc;
-  // int8 with 8 KV heads, one M tile and 2-byte scales: the DMA kernel on the
-  // balanced plan.  Other int8 shapes: one wave per KV head, registers
-  // double-buffered (154 VGPRs); bf16: single-buffered (double-buffered it needs
-  // 244 VGPRs).  Both on fixed-length splits.
-  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles <= kMaxRowTiles &&
-                      num_seqs <= kPlanMaxSeqs && scale_dtype != NE_DTYPE_FP32 &&
-                      ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
-  if (dma_ok) {
-    return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, false>(p, (hipStream_t)stream)
-                                        : launch_attention_dma<NE_DTYPE_FP16, false>(p, (hipStream_t)stream);
+  return run_unplanned(p, kv_dtype, scale_dtype, num_kv_heads, num_seqs, k_scale, v_scale, (hipStream_t)stream);
+}
+
+extern "C" int ne_paged_verify_attention_noalloc(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, const void* k_scale, const void* v_scale, int32_t kv_dtype,
+    int32_t scale_dtype, const int32_t* block_tables, int32_t block_table_stride,
+    int32_t block_size, const int32_t* ctx_len, const int32_t* q_start, const int32_t* q_len,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
+    int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, uint32_t* error_flag,
+    void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(error_flag != nullptr && ((uintptr_t)error_flag % 4) == 0,
+               "error_flag must be a 4-byte aligned device word");
+  NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && max_q_len > 0 &&
+                   max_ctx_len > 0,
+               "bad attention shape");
+  const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len, kv_dtype);
+  if (L.total > kNoAllocScratchBytes) {
+    set_error("this call needs %zu bytes of scratch; the allocation-free entry point holds at most %zu "
+              "(%d sequences, max_q_len %d, max_ctx_len %d): use ne_paged_verify_attention with a workspace",
+              L.total, kNoAllocScratchBytes, num_seqs, max_q_len, max_ctx_len);
+    return NE_EWORKSPACE;
   }
-  if (kv_dtype == NE_DTYPE_INT8) return launch_attention<1, true>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
-  return launch_attention<1, false>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&ws);
+  if (rc != NE_OK) return rc;
+  AttnParams p;
+  rc = make_params(q, q_token_stride, q_head_stride, k_cache, v_cache, k_scale, v_scale, kv_dtype, scale_dtype,
+                   block_tables, block_table_stride, block_size, ctx_len, q_start, q_len, num_seqs, num_q_heads,
+                   num_kv_heads, head_dim, max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
+                   out_head_stride, split_len, ws, kNoAllocScratchBytes, p);
+  if (rc != NE_OK) return rc;
+  p.error_flag = error_flag;  // the caller's word, not the scratch's
+  return run_unplanned(p, kv_dtype, scale_dtype, num_kv_heads, num_seqs, k_scale, v_scale, (hipStream_t)stream);
 }
 
 extern "C" int ne_paged_attention_plan(const int32_t* block_tables, int32_t block_table_stride,

@@ -14,11 +14,12 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
 STATUS_NAMES = {-1: "NE_EINVAL", -2: "NE_EUNSUPPORTED", -3: "NE_ELAUNCH", -4: "NE_EWORKSPACE"}
+NOALLOC_SCRATCH_BYTES = 64 << 20  # NE_NOALLOC_SCRATCH_BYTES
 
 # dtype codes
 DTYPE_BF16 = 0
@@ -61,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
         ],
     ),
     "ne_paged_verify_attention_planned": (ctypes.c_int, []),  # filled below: same as ne_paged_verify_attention
+    "ne_paged_verify_attention_noalloc": (ctypes.c_int, []),  # filled below
     "ne_paged_attention_plan": (
         ctypes.c_int,
         [_vp, _i32, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
@@ -118,6 +120,9 @@ SIGNATURES: dict[str, tuple] = {
     "ne_copy_bytes": (ctypes.c_int, [_vp, _vp, _sz, _vp]),
 }
 SIGNATURES["ne_paged_verify_attention_planned"] = SIGNATURES["ne_paged_verify_attention"]
+# the allocation-free variant: (workspace, bytes) replaced by the caller's error-flag word
+SIGNATURES["ne_paged_verify_attention_noalloc"] = (
+    ctypes.c_int, SIGNATURES["ne_paged_verify_attention"][1][:-3] + [_vp, _vp])
 
 
 class NativeError(RuntimeError):

@@ -251,6 +251,53 @@ def paged_verify_attention(
     return out
 
 
+def paged_verify_attention_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    block_tables: torch.Tensor,
+    block_size: int,
+    ctx_len: torch.Tensor,
+    q_start: torch.Tensor,
+    q_len: torch.Tensor,
+    max_q_len: int,
+    max_ctx_len: int,
+    error_flag: torch.Tensor,
+    out: torch.Tensor,
+    softmax_scale: float | None = None,
+    split_len: int = 0,
+) -> torch.Tensor:
+    """:func:`paged_verify_attention` without a workspace: the work plan and split partials
+    live in the library's per-GPU scratch (``NOALLOC_SCRATCH_BYTES``), ``error_flag`` is a
+    caller-owned int32 device word that receives the error bits, and ``out`` is given, so
+    the call allocates nothing (usable where allocation is not allowed).  Calls that
+    overlap on one GPU share the scratch and race."""
+    device = _require_gpu(q, k_cache, v_cache, k_scale, v_scale, block_tables, ctx_len, q_start, q_len,
+                          error_flag, out)
+    _check(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == HEAD_DIM and q.stride(2) == 1,
+           "q must be [rows, heads, 128] bf16")
+    _check(out.shape == q.shape and out.dtype == torch.bfloat16 and out.stride(2) == 1, "out must match q")
+    _check(error_flag.dtype == torch.int32 and error_flag.numel() >= 1, "error_flag must be an int32 word")
+    is_int8 = k_cache.dtype == torch.int8
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(HEAD_DIM)
+    _native.call(
+        "ne_paged_verify_attention_noalloc",
+        _ptr(q), q.stride(0), q.stride(1),
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        dtype_code(k_cache.dtype), dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16,
+        _ptr(block_tables), block_tables.stride(0), block_size,
+        _ptr(ctx_len), _ptr(q_start), _ptr(q_len),
+        ctx_len.shape[0], q.shape[1], k_cache.shape[1], HEAD_DIM, max_q_len, max_ctx_len,
+        float(softmax_scale),
+        _ptr(out), out.stride(0), out.stride(1),
+        split_len, _ptr(error_flag), _stream(device),
+    )
+    return out
+
+
 def _plan_key(block_tables, block_size, ctx_len, q_start, q_len, max_q_len, max_ctx_len, split_len) -> tuple:
     return (block_tables.data_ptr(), tuple(block_tables.shape), block_tables.stride(0), block_size,
             ctx_len.data_ptr(), q_start.data_ptr(), q_len.data_ptr(), ctx_len.shape[0], max_q_len, max_ctx_len,
