@@ -77,6 +77,8 @@ __device__ __forceinline__ float scale_at(const void* s, int64_t i) {
 // MFMA fragment reads bank-conflict free.
 constexpr int kArgmaxCols = 64;  // columns per LM-head argmax partial
 constexpr int kStageK = 128;     // k per stage of the projection kernel
+// the projection kernels address X rows with 32-bit byte offsets from a scalar base
+constexpr int64_t kMaxXElems = (int64_t(1) << 31) - 256;
 
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
@@ -94,15 +96,20 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Work-group tile: 80 token rows (5 MFMA subtiles) x 16 * NSUB weight rows, sized so
 // that the verify-step shapes give about one work-group per CU (M = 320: QKV
 // N = 4096 and gate|up N = 6144 give 256 tiles; o / down N = 1024 give 64 tiles,
-// split 4 ways over K).  The waves form kKGroups x NSUB/2: wave (kg, nw) runs k-step
-// kg (32 wide) of every 128-wide stage for all 5 token subtiles against weight
+// split 4 ways over K).  The MFMA waves form kKGroups x NSUB/2: wave (kg, nw) runs
+// k-step kg (32 wide) of every 128-wide stage for all 5 token subtiles against weight
 // subtiles 2 nw and 2 nw + 1, so each X fragment read from LDS feeds 2 MFMAs and
 // each weight fragment 5.  The k-groups' partial tiles are summed through LDS at
 // the end, each wave finishing some of the token subtiles.
+//
+// Stages are copied by DMA into two LDS rings: X rows (from L2, where every column
+// tile re-reads them) run kRX - 1 stages ahead and weight rows (from HBM, the longer
+// way) kRW - 1 stages ahead.  A wave copies either X or weight rows, never both, so
+// its vmcnt counts one stream and its wait for a stage is exact.  Each wave reads the
+// fragments of stage t from LDS before it runs the MFMAs of stage t - 1 (held in
+// registers), so the LDS latency hides under the multiplies.
 constexpr int kPM = 5;  // token subtiles per work-group (the fused QKV epilogue uses 3)
 constexpr int kKGroups = 4;
-constexpr int kProjStages = 3;
-constexpr int kDmaPerWave = 4;  // DMA instructions per issuing wave per stage
 
 template <int NSUB, int PM = kPM>
 struct ProjLayout {
@@ -110,70 +117,186 @@ struct ProjLayout {
   static constexpr int kNW = NSUB / 2;
   static constexpr int kWaves = kKGroups * kNW;
   static constexpr int kThreads = kWaves * kWave;
-  static constexpr int kXBytes = kPRows * kStageK * 2;  // 20 KiB at 5 subtiles
-  static constexpr int kWBytes = NSUB * 16 * kStageK;   // int8 rows of 128 bytes
-  static constexpr int kStage = kXBytes + kWBytes;
-  static constexpr int kXInstr = kXBytes / 1024;
-  static constexpr int kInstr = kXInstr + kWBytes / 1024;
-  static constexpr int kIssuers = kInstr / kDmaPerWave;
-  static_assert(kInstr % kDmaPerWave == 0 && kIssuers <= kWaves, "DMA split");
+  static constexpr int kXI = PM * 4;    // 1 KiB copies per stage: X rows of 256 B ...
+  static constexpr int kWI = NSUB * 2;  // ... and weight rows of 128 B
+  static constexpr int kXBytes = kXI * 1024;
+  static constexpr int kWBytes = kWI * 1024;
+  static constexpr int kRX = 3;
+  static constexpr int kRW = 6;
+  // copies per X-copying / weight-copying wave: the fewest per wave that fit the waves
+  static constexpr int split() {
+    int best = -1, cost = 1 << 30;
+    for (int dx = 1; dx <= kXI; ++dx)
+      for (int dw = 1; dw <= kWI; ++dw)
+        if (kXI % dx == 0 && kWI % dw == 0 && kXI / dx + kWI / dw <= kWaves && (dx > dw ? dx : dw) < cost) {
+          cost = dx > dw ? dx : dw;
+          best = dx * 256 + dw;
+        }
+    return best;
+  }
+  static constexpr int kDX = split() / 256;
+  static constexpr int kDW = split() % 256;
+  static constexpr int kNXW = kXI / kDX;  // waves [0, kNXW) copy X
+  static constexpr int kNWW = kWI / kDW;  // waves [kNXW, kNXW + kNWW) copy weights
   static constexpr int kRedBytes = kKGroups * kNW * PM * 2 * 1024;
-  static constexpr int kLds = kProjStages * kStage > kRedBytes ? kProjStages * kStage : kRedBytes;
+  static constexpr int kRing = kRX * kXBytes + kRW * kWBytes;
+  static constexpr int kLds = kRing > kRedBytes ? kRing : kRedBytes;
+  static_assert(split() > 0, "copy split");
+  static_assert(kDX * (kRX - 2) < 64 && kDW * (kRW - 2) < 64, "vmcnt range");
+  static_assert(kLds <= 160 * 1024, "LDS");
 };
 
-// Copy one 128-wide k stage: X rows m0..m0+79 (rows past m re-read row m-1 and are
-// never stored) and weight rows n0..n0+16*NSUB-1.  Issuing waves copy exactly
-// kDmaPerWave KiB each, so every wave's vmcnt bookkeeping is the same.
-template <int NSUB, int PM>
-__device__ __forceinline__ void proj_issue(const GemmParams& p, char* stage, int m0, int n0, int k0,
-                                           int wave, int lane) {
-  using L = ProjLayout<NSUB, PM>;
-  if (wave >= L::kIssuers) return;
-#pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
-    const int i = wave * kDmaPerWave + j;
-    if (i < L::kXInstr) {  // 4 rows x 16 chunks of 16 bytes
-      const int row = i * 4 + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 15);
-      const int grow = min(m0 + row, p.m - 1);
-      lds_dma16(p.x + (int64_t)grow * p.ldx + k0 + chunk * 8, stage + i * 1024);
-    } else {  // 8 weight rows x 8 chunks
-      const int b = i - L::kXInstr;
-      const int row = b * 8 + (lane >> 3);
-      const int chunk = (lane & 7) ^ (row & 7);
-      lds_dma16((const int8_t*)p.w + (int64_t)(n0 + row) * p.k + k0 + chunk * 16,
-                stage + L::kXBytes + b * 1024);
+// a wave-uniform pointer kept in SGPRs, so that a copy's address is a scalar base plus
+// a 32-bit lane offset
+__device__ __forceinline__ const char* uniform_ptr(const char* ptr) {
+  const uint64_t v = (uint64_t)ptr;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const char*)(((uint64_t)hi << 32) | lo);
+}
+
+// s_waitcnt vmcnt(D * pend) for a run-time pend in [0, P]
+template <int D, int P>
+__device__ __forceinline__ void wait_pending(int pend) {
+  if constexpr (P <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (pend >= P) {
+      wait_vmcnt<D * P>();
+    } else {
+      wait_pending<D, P - 1>(pend);
     }
   }
 }
 
-// k-step kg of a stage.  Lane group g = lane / 16 supplies logical
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// The k loop of a work-group: kt_n stages of 128 from k = kbase (KT > 0: kt_n = KT).  X rows m0.. (rows past
+// m re-read row m - 1 and are never stored) and weight rows n0.. are copied with the
+// chunk swizzles below; lane group g = lane / 16 of k-group kg supplies logical
 // k = 64 (kg / 2) + 16 g + 8 (kg % 2) + e, e < 8: X chunk 8 (kg / 2) + 2 g + kg % 2 of
 // its 256-byte row, weight bytes 16 (4 (kg / 2) + g) + 8 (kg % 2) of its 128-byte row.
-template <int NSUB, int PM>
-__device__ __forceinline__ void proj_mma(const char* stage, int kg, int nw, int lane,
-                                         floatx4 (&acc)[PM][2]) {
+template <int NSUB, int PM, int KT>
+__device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, int m0, int n0, int kbase,
+                                              int kt_runtime, int wave, int lane, int kg, int nw,
+                                              floatx4 (&acc)[PM][2]) {
   using L = ProjLayout<NSUB, PM>;
+  // a stage count known at compile time turns every wait below into one instruction
+  const int kt_n = KT > 0 ? KT : kt_runtime;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const char* xs = stage;
-  const char* ws = stage + L::kXBytes;
-  bf16x8 a[2];
+  const bool xwave = wave < L::kNXW;
+  const bool wwave = wave >= L::kNXW && wave < L::kNXW + L::kNWW;
+  constexpr int D = L::kDX > L::kDW ? L::kDX : L::kDW;
+  // copy j of this wave: LDS position c ^ (row % chunks-per-row) for 16-byte chunk c of
+  // LDS row `row`, which makes the fragment reads bank-conflict free
+  uint32_t off[D];
 #pragma unroll
-  for (int ns = 0; ns < 2; ++ns) {
-    const int row = (2 * nw + ns) * 16 + r;
-    const int chunk = (4 * (kg >> 1) + g) ^ (row & 7);
-    const u32x2 v = *(const u32x2*)(ws + row * 128 + chunk * 16 + (kg & 1) * 8);
-    a[ns] = int8x8_to_bf16x8(v[0], v[1]);
+  for (int j = 0; j < D; ++j) {
+    if (xwave) {  // 4 X rows x 16 chunks
+      const int row = (wave * L::kDX + j) * 4 + (lane >> 4);
+      const int chunk = (lane & 15) ^ (row & 15);
+      const int grow = min(m0 + row, p.m - 1);
+      off[j] = (uint32_t)grow * (uint32_t)(p.ldx * 2) + (uint32_t)chunk * 16u;
+    } else {  // 8 weight rows x 8 chunks
+      const int row = ((wave - L::kNXW) * L::kDW + j) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ (row & 7);
+      off[j] = (uint32_t)row * (uint32_t)p.k + (uint32_t)chunk * 16u;
+    }
   }
+  const char* xbase = (const char*)p.x + (int64_t)kbase * 2;
+  const char* wbase = (const char*)p.w + (int64_t)n0 * p.k + kbase;
+  char* xring = smem;
+  char* wring = smem + L::kRX * L::kXBytes;
+  auto issue_x = [&](int s) {
+    if (!xwave) return;
+    char* slot = xring + (s % L::kRX) * L::kXBytes + wave * L::kDX * 1024;
+    const char* src = uniform_ptr(xbase + s * (kStageK * 2));
 #pragma unroll
-  for (int mi = 0; mi < PM; ++mi) {
-    const int row = mi * 16 + r;
-    const int chunk = (8 * (kg >> 1) + 2 * g + (kg & 1)) ^ (row & 15);
-    const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(xs + row * 256 + chunk * 16));
+    for (int j = 0; j < L::kDX; ++j) {
+      uint32_t o = off[j];
+      __asm__("" : "+v"(o));  // keep the lane offset 32-bit: scalar base + offset addressing
+      lds_dma16(src + o, slot + j * 1024);
+    }
+  };
+  auto issue_w = [&](int s) {
+    if (!wwave) return;
+    char* slot = wring + (s % L::kRW) * L::kWBytes + (wave - L::kNXW) * L::kDW * 1024;
+    const char* src = uniform_ptr(wbase + s * kStageK);
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns)
-      acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ns], b, acc[mi][ns], 0, 0, 0);
+    for (int j = 0; j < L::kDW; ++j) {
+      uint32_t o = off[j];
+      __asm__("" : "+v"(o));
+      lds_dma16(src + o, slot + j * 1024);
+    }
+  };
+  // stage t needs this wave's copies of stage t; those of later stages may still fly
+  auto wait_stage = [&](int t) {
+    if (xwave) wait_pending<L::kDX, L::kRX - 2>(min(kt_n - t - 1, L::kRX - 2));
+    if (wwave) wait_pending<L::kDW, L::kRW - 2>(min(kt_n - t - 1, L::kRW - 2));
+  };
+  const int cx = 8 * (kg >> 1) + 2 * g + (kg & 1);
+  const uint32_t xr = (uint32_t)(r * 256 + ((cx ^ r) * 16));
+  const int cw = 4 * (kg >> 1) + g;
+  const uint32_t wr = (uint32_t)((2 * nw * 16 + r) * 128 + ((cw ^ (r & 7)) * 16) + (kg & 1) * 8);
+  auto read = [&](int s, u32x4 (&xf)[PM], u32x2 (&wf)[2]) {
+    const char* xs = xring + (s % L::kRX) * L::kXBytes;
+    const char* ws = wring + (s % L::kRW) * L::kWBytes;
+#pragma unroll
+    for (int mi = 0; mi < PM; ++mi) xf[mi] = *(const u32x4*)(xs + xr + mi * 4096);
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) wf[ns] = *(const u32x2*)(ws + wr + ns * 2048);
+  };
+  auto mma = [&](const u32x4 (&xf)[PM], const u32x2 (&wf)[2]) {
+    bf16x8 a[2];
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) a[ns] = int8x8_to_bf16x8(wf[ns][0], wf[ns][1]);
+#pragma unroll
+    for (int mi = 0; mi < PM; ++mi)
+#pragma unroll
+      for (int ns = 0; ns < 2; ++ns)
+        acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ns], __builtin_bit_cast(bf16x8, xf[mi]),
+                                                              acc[mi][ns], 0, 0, 0);
+  };
+  // stage t: its copies are in LDS after the barrier, and every wave has read stage
+  // t - 1 into registers before it (lgkmcnt(0)), so the slots of stage t - 1 take the
+  // copies of stages t + kRX - 1 and t + kRW - 1
+  auto step = [&](int t, u32x4 (&xr_)[PM], u32x2 (&wr_)[2], const u32x4 (&xm)[PM], const u32x2 (&wm)[2]) {
+    wait_stage(t);
+    wait_lgkmcnt0();
+    asm volatile("s_barrier" ::: "memory");
+    if (t + L::kRX - 1 < kt_n) issue_x(t + L::kRX - 1);
+    if (t + L::kRW - 1 < kt_n) issue_w(t + L::kRW - 1);
+    read(t, xr_, wr_);
+    __builtin_amdgcn_sched_barrier(0);  // the reads go out before the multiplies
+    mma(xm, wm);
+  };
+
+#pragma unroll
+  for (int s = 0; s < L::kRW - 1; ++s)
+    if (s < kt_n) issue_w(s);  // the weights first: they have the longer way to come
+#pragma unroll
+  for (int s = 0; s < L::kRX - 1; ++s)
+    if (s < kt_n) issue_x(s);
+  u32x4 xa[PM], xb[PM];
+  u32x2 wa[2], wb[2];
+  wait_stage(0);
+  asm volatile("s_barrier" ::: "memory");
+  if (L::kRX - 1 < kt_n) issue_x(L::kRX - 1);
+  if (L::kRW - 1 < kt_n) issue_w(L::kRW - 1);
+  read(0, xa, wa);
+  int t = 1;
+  for (; t + 1 < kt_n; t += 2) {
+    step(t, xb, wb, xa, wa);
+    step(t + 1, xa, wa, xb, wb);
+  }
+  if (t < kt_n) {
+    step(t, xb, wb, xa, wa);
+    wait_lgkmcnt0();
+    mma(xb, wb);
+  } else {
+    wait_lgkmcnt0();
+    mma(xa, wa);
   }
 }
 
@@ -183,7 +306,7 @@ __device__ __forceinline__ void proj_mma(const char* stage, int kg, int nw, int 
 // through QK-norm + RoPE into q_out or quantised into the KV cache (qk_rope_kv.hpp) --
 // the bits the GEMM with EPI 0 followed by the row kernel produce, without the qkv round
 // trip through memory.  KV (EPI 4): 1 bf16 cache, 2 int8 + bf16 scales, 3 int8 + fp16.
-template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM>
+template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM, int KT = 0>
 __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(GemmParams p,
                                                                          int k_per_split,
                                                                          float* partial,
@@ -241,26 +364,7 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
 #pragma unroll
     for (int ns = 0; ns < 2; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int kt_n = k_per_split / kStageK;
-#pragma unroll
-  for (int s = 0; s < kProjStages - 1; ++s)
-    if (s < kt_n) proj_issue<NSUB, PM>(p, smem + s * L::kStage, m0, n0, kbase + s * kStageK, wave, lane);
-  for (int t = 0; t < kt_n; ++t) {
-    // this wave's copies of stage t are done once at most the next stage's remain
-    if (t + 1 < kt_n) {
-      wait_vmcnt<kDmaPerWave>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    // every wave's stage t is in LDS after the barrier; a __syncthreads fence would
-    // also wait for the stage still in flight
-    asm volatile("s_barrier" ::: "memory");
-    const int tn2 = t + kProjStages - 1;
-    if (tn2 < kt_n)
-      proj_issue<NSUB, PM>(p, smem + (tn2 % kProjStages) * L::kStage, m0, n0, kbase + tn2 * kStageK, wave,
-                       lane);
-    proj_mma<NSUB, PM>(smem + (t % kProjStages) * L::kStage, kg, nw, lane, acc);
-  }
+  proj_mainloop<NSUB, PM, KT>(p, smem, m0, n0, kbase, k_per_split / kStageK, wave, lane, kg, nw, acc);
 
   // EPI 4: the rows' cos / sin, in flight while the k-groups are summed
   uint16_t e_rc[kEpiRows], e_rs[kEpiRows];
@@ -381,23 +485,39 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
   }
 }
 
-template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM>
-int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
-                const QkvRopeArgs& qa = QkvRopeArgs{}) {
+template <int NSUB, int SDT, int EPI, int KV, int PM, int KT>
+int launch_proj_kt(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
+                   const QkvRopeArgs& qa) {
   using L = ProjLayout<NSUB, PM>;
   p.tiles_m = ceil_div(p.m, L::kPRows);
   p.tiles_n = p.n / (NSUB * 16);
   const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
   const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
-  static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)proj_kernel<NSUB, SDT, EPI, KV, PM>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
+  static const hipError_t attr = hipFuncSetAttribute((const void*)proj_kernel<NSUB, SDT, EPI, KV, PM, KT>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
   if (attr != hipSuccess) {
     set_error("%s: cannot reserve %d bytes of LDS: %s", name, L::kLds, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI, KV, PM>), grid, dim3(L::kThreads), L::kLds, stream, p,
+  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI, KV, PM, KT>), grid, dim3(L::kThreads), L::kLds, stream, p,
                      p.k / splits, partial, qa);
   return check_launch(name);
+}
+
+// Stage counts with a kernel of their own: 8 (K = 1024, the QKV and gate|up
+// projections of the 0.6B model), 4 and 6 (o and down split 4 ways over K = 2048 and
+// 3072); any other count runs the loop with a run-time count.
+template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM>
+int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
+                const QkvRopeArgs& qa = QkvRopeArgs{}) {
+  const int kt = p.k / splits / kStageK;
+  if constexpr (EPI == 3) {
+    if (kt == 4) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 4>(p, splits, partial, stream, name, qa);
+    if (kt == 6) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 6>(p, splits, partial, stream, name, qa);
+  } else {
+    if (kt == 8) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 8>(p, splits, partial, stream, name, qa);
+  }
+  return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 0>(p, splits, partial, stream, name, qa);
 }
 
 template <int SDT>
@@ -635,6 +755,7 @@ extern "C" int ne_w8a16_gemm(const void* x, int64_t ldx, const int8_t* w, const 
   NE_CHECK_SUPPORTED(k % 128 == 0, "k must be a multiple of 128 (got %d)", k);
   NE_CHECK_SUPPORTED(n % 64 == 0, "n must be a multiple of 64 (got %d)", n);
   NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
+  NE_CHECK_SUPPORTED((int64_t)m * ldx < kMaxXElems, "x spans more than 4 GiB (m=%d, ldx=%lld)", m, (long long)ldx);
   NE_CHECK_ARG(ldy >= (epilogue == NE_EPILOGUE_SWIGLU ? n / 2 : n) && ldy % 4 == 0,
                "ldy too small or not a multiple of 4");
   NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 8) == 0,
@@ -653,6 +774,7 @@ extern "C" int ne_w8a16_gemm_splitk(const void* x, int64_t ldx, const int8_t* w,
                      k, splits);
   NE_CHECK_SUPPORTED(n % 64 == 0, "n must be a multiple of 64 (got %d)", n);
   NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
+  NE_CHECK_SUPPORTED((int64_t)m * ldx < kMaxXElems, "x spans more than 4 GiB (m=%d, ldx=%lld)", m, (long long)ldx);
   NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)partials % 16) == 0,
                "x, w and partials must be 16-byte aligned");
   return w8a16_common(x, ldx, w, scale, scale_dtype, m, n, k, nullptr, 0, NE_EPILOGUE_STORE, splits,
@@ -673,6 +795,7 @@ extern "C" int ne_w8a16_qkv_norm_rope_kv(
   NE_CHECK_ARG(rope_positions > 0, "rope_positions must be > 0");
   NE_CHECK_SUPPORTED(k % 128 == 0, "k must be a multiple of 128 (got %d)", k);
   NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
+  NE_CHECK_SUPPORTED((int64_t)m * ldx < kMaxXElems, "x spans more than 4 GiB (m=%d, ldx=%lld)", m, (long long)ldx);
   NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0, "x and w must be 16-byte aligned");
   int kv_mode = 0;
   if (kv_dtype == NE_DTYPE_BF16) {
