@@ -333,11 +333,13 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
 
   // the epilogue's weight-row scales, fetched now so that their latency hides under
   // the k loop: lane (r, g) stores columns (2 nw + ns) 16 + 4 g + i
-  float sc[2][4];
+  float sc[2][4] = {};
+  if constexpr (EPI != 4) {  // EPI 4 scales its rows' columns instead (e_sc)
 #pragma unroll
-  for (int ns = 0; ns < 2; ++ns)
+    for (int ns = 0; ns < 2; ++ns)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sc[ns][i] = scale_at<SDT>(p.scale, n0 + (2 * nw + ns) * 16 + 4 * g + i);
+      for (int i = 0; i < 4; ++i) sc[ns][i] = scale_at<SDT>(p.scale, n0 + (2 * nw + ns) * 16 + 4 * g + i);
+  }
 
   // EPI 4: wave w finishes rows w, w + kWaves, ... of the tile (head tn).  Their slots
   // and positions (scalar loads) and the head's norm weights are requested now and
@@ -346,10 +348,13 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
   constexpr int kEpiRows = (kPRows + L::kWaves - 1) / L::kWaves;
   int e_slot[kEpiRows], e_pos[kEpiRows];
   uint16_t e_w[2] = {0, 0};
+  float e_sc[2] = {0.f, 0.f};  // weight-row scales of head columns lane and lane + 64
   if constexpr (EPI == 4) {
     const uint16_t* w = (tn < qa.hq) ? qa.q_norm_w : qa.k_norm_w;  // v heads do not use it
     e_w[0] = w[lane];
     e_w[1] = w[lane + 64];
+    e_sc[0] = scale_at<SDT>(p.scale, n0 + lane);
+    e_sc[1] = scale_at<SDT>(p.scale, n0 + 64 + lane);
 #pragma unroll
     for (int i = 0; i < kEpiRows; ++i) {
       const int m = min(m0 + wave + L::kWaves * i, p.m - 1);
@@ -371,8 +376,7 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
   if constexpr (EPI == 4) {
     // the loads issued before the k loop are long done: take their values now, so that
     // the compiler's wait for them does not land after the loads below
-    __asm__ __volatile__("" ::"v"(sc[0][0]), "v"(sc[0][1]), "v"(sc[0][2]), "v"(sc[0][3]), "v"(sc[1][0]),
-                         "v"(sc[1][1]), "v"(sc[1][2]), "v"(sc[1][3]), "v"(e_w[0]), "v"(e_w[1]));
+    __asm__ __volatile__("" ::"v"(e_sc[0]), "v"(e_sc[1]), "v"(e_w[0]), "v"(e_w[1]));
 #pragma unroll
     for (int i = 0; i < kEpiRows; ++i) {
       const int64_t pos = min(max(e_pos[i], 0), qa.rope_positions - 1);
@@ -383,43 +387,21 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
 
   // ---- sum the k-groups through LDS (the stage ring is free once all waves pass) ----
   lds_barrier();
-  floatx4* red = (floatx4*)smem;  // [kg][nw][mi][ns][lane]
-#pragma unroll
-  for (int mi = 0; mi < PM; ++mi)
-#pragma unroll
-    for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
-  lds_barrier();
-
   if constexpr (EPI == 4) {
-    static_assert(NSUB == 8 && PM <= 2 * kKGroups, "one head per tile, two row subtiles per wave");
+    // partials as rows [kg][row][128 + 4 pad] fp32, so that the row pass below reads a
+    // row's columns lane and lane + 64 as consecutive words; each row is summed over the
+    // k-groups in order and scaled, the bits the GEMM epilogue stores
+    static_assert(NSUB == 8, "one head per tile");
+    constexpr int kRowF = 132;
+    static_assert(kKGroups * kPRows * kRowF * 4 <= L::kLds, "partials fit the stage ring");
     constexpr bool kInt8 = KV >= 2;
     constexpr int kKvSdt = KV == 3 ? NE_DTYPE_FP16 : NE_DTYPE_BF16;
-    u32x2 bits[2][2];
+    float* part = (float*)smem;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int mi = kg + t * kKGroups;
-      if (mi < PM) {
+    for (int mi = 0; mi < PM; ++mi)
 #pragma unroll
-        for (int ns = 0; ns < 2; ++ns) {
-          floatx4 v = red[((nw * PM + mi) * 2 + ns) * kWave + lane];
-#pragma unroll
-          for (int q = 1; q < kKGroups; ++q) v += red[(((q * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane];
-          bits[t][ns] = u32x2{pack_bf16x2(v[0] * sc[ns][0], v[1] * sc[ns][1]),
-                              pack_bf16x2(v[2] * sc[ns][2], v[3] * sc[ns][3])};
-        }
-      }
-    }
-    lds_barrier();  // the reduction buffer is read: reuse it for the bf16 tile [80][128]
-    uint16_t* tile = (uint16_t*)smem;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int mi = kg + t * kKGroups;
-      if (mi < PM) {
-#pragma unroll
-        for (int ns = 0; ns < 2; ++ns)
-          *(u32x2*)(tile + (mi * 16 + r) * 128 + (2 * nw + ns) * 16 + 4 * g) = bits[t][ns];
-      }
-    }
+      for (int ns = 0; ns < 2; ++ns)
+        *(floatx4*)(part + (kg * kPRows + mi * 16 + r) * kRowF + (2 * nw + ns) * 16 + 4 * g) = acc[mi][ns];
     lds_barrier();
     // this wave's rows all at once, so that their reductions overlap
     int rows_e[kEpiRows];
@@ -431,8 +413,15 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
       const int rr = min(wave + L::kWaves * i, kPRows - 1);
       rows_e[i] = m0 + rr;
       valid_e[i] = wave + L::kWaves * i < kPRows && m0 + rr < p.m;
-      a_e[i] = bf16_to_f32(tile[rr * 128 + lane]);
-      b_e[i] = bf16_to_f32(tile[rr * 128 + 64 + lane]);
+      float va = part[rr * kRowF + lane];
+      float vb = part[rr * kRowF + 64 + lane];
+#pragma unroll
+      for (int q = 1; q < kKGroups; ++q) {
+        va += part[(q * kPRows + rr) * kRowF + lane];
+        vb += part[(q * kPRows + rr) * kRowF + 64 + lane];
+      }
+      a_e[i] = bf16_round(va * e_sc[0]);
+      b_e[i] = bf16_round(vb * e_sc[1]);
       c_e[i] = bf16_to_f32(e_rc[i]);
       s_e[i] = bf16_to_f32(e_rs[i]);
       slot_e[i] = e_slot[i];
@@ -441,6 +430,12 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
                                                      bf16_to_f32(e_w[0]), bf16_to_f32(e_w[1]), c_e, s_e);
     return;
   }
+  floatx4* red = (floatx4*)smem;  // [kg][nw][mi][ns][lane]
+#pragma unroll
+  for (int mi = 0; mi < PM; ++mi)
+#pragma unroll
+    for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
+  lds_barrier();
 
   for (int mi = kg; mi < PM; mi += kKGroups) {
     floatx4 v[2];

@@ -30,31 +30,59 @@ struct QkvRopeArgs {
   uint16_t* q_out;               // [rows][hq][128] bf16
 };
 
-// Sums / maxima over the wave of N independent values, the butterflies interleaved so
-// that the N exchange chains overlap; each value sees the same order as wave_sum /
-// wave_max would give it alone.
+// Sums / maxima over the wave of N independent values, every lane ending with the same
+// result.  Lanes combine within quads (DPP quad permutes), then 8 and 16 lanes (DPP
+// half-row and row mirrors), then 32 (ds_swizzle xor 16), and the two halves are
+// added through scalar reads of lanes 0 and 32; the N chains are interleaved so that
+// their latencies overlap.  Every pairing is symmetric, so all lanes compute the same
+// value in the same order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+template <bool MAX, int N>
+__device__ __forceinline__ void wave_reduce_n(float (&v)[N]) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  float t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = dpp_f32<0xB1>(v[i]);  // quad_perm [1, 0, 3, 2]
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], t[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = dpp_f32<0x4E>(v[i]);  // quad_perm [2, 3, 0, 1]
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], t[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = dpp_f32<0x141>(v[i]);  // row_half_mirror
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], t[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = dpp_f32<0x140>(v[i]);  // row_mirror
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], t[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = swizzle_xor16(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], t[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(lane_f32(v[i], 0), lane_f32(v[i], 32));
+}
+
 template <int N>
 __device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    float t[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], o);
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] += t[i];
-  }
+  wave_reduce_n<false, N>(v);
 }
 
 template <int N>
 __device__ __forceinline__ void wave_max_n(float (&v)[N]) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    float t[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], o);
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], t[i]);
-  }
+  wave_reduce_n<true, N>(v);
 }
 
 // Quantise (int8 cache) or copy N 128-vectors of one head, each held as lane /
