@@ -146,19 +146,23 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     ctx_per_step, lengths_per_step = [], []
     torch.cuda.synchronize()
     start = time.perf_counter()
+    # per step: the runner's slot lengths before it (its host mirror of each sequence's
+    # token count) and what it emitted; the statistics are tallied after the timed loop
+    records = []
+    for _ in range(steps):
+        lengths = eng.runner.np_len.copy()
+        records.append((lengths, eng.runner.step()))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
     tokens = 0
     kept_hist: dict[int, int] = {}
-    for _ in range(steps):
-        lengths = {i: s.num_tokens for i, s in enumerate(eng.runner.slots) if s is not None}
-        results = eng.runner.step()
+    for lengths, results in records:
         # context of sequence b in this step = its length before the step + its guesses
-        ctx_per_step.append([lengths[i] + results[i].num_guesses for i in lengths])
-        lengths_per_step.append([lengths[i] for i in lengths])
+        ctx_per_step.append([int(lengths[i]) + r.num_guesses for i, r in results.items()])
+        lengths_per_step.append([int(lengths[i]) for i in results])
         for r in results.values():
             tokens += len(r.tokens)
             kept_hist[r.num_kept] = kept_hist.get(r.num_kept, 0) + 1
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
     active = sum(1 for s in eng.runner.slots if s is not None)
     return {
         "elapsed": elapsed,

@@ -337,6 +337,19 @@ int ne_prepare_verify_step(const int32_t* history, int64_t history_stride,
                            int32_t* slot_mapping, int32_t* q_start, int32_t* q_len,
                            int32_t* ctx_len, void* stream);
 
+/*
+ * Counters of the next verify step, advanced on the device after ne_accept so that
+ * the next step's n-gram proposal can run without a host round trip (replaces the
+ * per-step num_guesses of ne/engine/speculative/speculative_generator.py:71-72 and
+ * the generator's step counter).  For every sequence b with history_len[b] > 0:
+ * num_generated[b] += num_out[b]; steps[b] += 1;
+ * num_guesses[b] = max(0, min(k, max_new_tokens[b] - num_generated[b] - 1)).
+ * Sequences with history_len 0 are inactive: num_guesses[b] = 0, nothing else written.
+ */
+int ne_advance_step_counts(const int32_t* history_len, const int32_t* num_out,
+                           const int32_t* max_new_tokens, int32_t* num_generated, uint64_t* steps,
+                           int32_t* num_guesses, int32_t k, int32_t num_seqs, void* stream);
+
 /* Plain device copy of `bytes` bytes (16-byte aligned); used to calibrate the
  * hardware byte counters against a kernel of known traffic. */
 int ne_copy_bytes(const void* src, void* dst, size_t bytes, void* stream);

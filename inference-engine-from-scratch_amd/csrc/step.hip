@@ -45,10 +45,44 @@ __global__ __launch_bounds__(256) void prepare_verify_kernel(
   }
 }
 
+// After a verify step, per sequence b: when active (history_len > 0) add the tokens it
+// emitted to its generated count, advance its sampling step and set the next step's
+// guess count min(k, max_new - generated - 1) clipped at 0
+// (speculative_generator.py:71-72, the rule of num_guesses); inactive: 0 guesses.
+__global__ __launch_bounds__(256) void advance_counts_kernel(const int32_t* history_len,
+                                                             const int32_t* num_out,
+                                                             const int32_t* max_new, int32_t* generated,
+                                                             uint64_t* steps, int32_t* num_guesses, int k,
+                                                             int num_seqs) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= num_seqs) return;
+  if (history_len[b] <= 0) {
+    num_guesses[b] = 0;
+    return;
+  }
+  const int gen = generated[b] + num_out[b];
+  generated[b] = gen;
+  steps[b] += 1;
+  num_guesses[b] = max(0, min(k, max_new[b] - gen - 1));
+}
+
 }  // namespace
 }  // namespace ne
 
 using namespace ne;
+
+extern "C" int ne_advance_step_counts(const int32_t* history_len, const int32_t* num_out,
+                                      const int32_t* max_new_tokens, int32_t* num_generated,
+                                      uint64_t* steps, int32_t* num_guesses, int32_t k, int32_t num_seqs,
+                                      void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0 && k >= 0, "bad sizes (num_seqs=%d, k=%d)", num_seqs, k);
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(history_len && num_out && max_new_tokens && num_generated && steps && num_guesses,
+               "null pointer argument");
+  hipLaunchKernelGGL(advance_counts_kernel, dim3(ceil_div(num_seqs, 256)), dim3(256), 0, (hipStream_t)stream,
+                     history_len, num_out, max_new_tokens, num_generated, steps, num_guesses, k, num_seqs);
+  return check_launch("advance_step_counts");
+}
 
 extern "C" int ne_prepare_verify_step(const int32_t* history, int64_t history_stride,
                                       const int32_t* history_len, const int32_t* drafts,

@@ -117,6 +117,7 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
+    "ne_advance_step_counts": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u64p, _vp, _i32, _i32, _vp]),
     "ne_copy_bytes": (ctypes.c_int, [_vp, _vp, _sz, _vp]),
 }
 SIGNATURES["ne_paged_verify_attention_planned"] = SIGNATURES["ne_paged_verify_attention"]

@@ -732,6 +732,24 @@ def prepare_verify_step(
     )
 
 
+def advance_step_counts(history_len: torch.Tensor, num_out: torch.Tensor, max_new_tokens: torch.Tensor,
+                        num_generated: torch.Tensor, steps: torch.Tensor, num_guesses: torch.Tensor,
+                        k: int) -> None:
+    """After a verify step: active sequences add their emitted tokens to the generated
+    count, advance the sampling step and get the next step's guess count
+    (speculative_generator.py:71-72); inactive ones (history_len 0) get 0 guesses."""
+    device = _require_gpu(history_len, num_out, max_new_tokens, num_generated, steps, num_guesses)
+    for name, t in (("history_len", history_len), ("num_out", num_out), ("max_new_tokens", max_new_tokens),
+                    ("num_generated", num_generated), ("num_guesses", num_guesses)):
+        _int32(t, name)
+    _check(steps.dtype == torch.int64 and steps.is_contiguous(), "steps must be contiguous int64")
+    n = history_len.numel()
+    _check(all(t.numel() >= n for t in (num_out, max_new_tokens, num_generated, steps, num_guesses)),
+           "per-sequence arrays shorter than history_len")
+    _native.call("ne_advance_step_counts", _ptr(history_len), _ptr(num_out), _ptr(max_new_tokens),
+                 _ptr(num_generated), _ptr(steps), _ptr(num_guesses), k, n, _stream(device))
+
+
 def copy_bytes(src: torch.Tensor, dst: torch.Tensor) -> None:
     device = _require_gpu(src, dst)
     nbytes = src.numel() * src.element_size()

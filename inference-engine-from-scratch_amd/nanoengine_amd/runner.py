@@ -8,9 +8,13 @@ semantics to up to ``max_seqs`` sequences at once, with the token histories,
 lengths, block tables and cached counts resident on the device:
 
   1. n-gram drafting on the device histories (ne_ngram_propose), or a draft
-     model's greedy guesses (``DraftModelProposer``, nanoengine_amd/draft.py)
-  2. read back the draft counts; reserve KV blocks on the host allocator for
-     L + g tokens per sequence (paged_allocator.py:50-55) and upload new table rows
+     model's greedy guesses (``DraftModelProposer``, nanoengine_amd/draft.py).  With
+     n-gram drafting the previous step already proposed them: its device work ends by
+     advancing the per-sequence counters (ne_advance_step_counts) and running the
+     n-gram kernel for the next step, and its one readback brings the counts home; only
+     a step after new sequences were admitted proposes (and reads back) first
+  2. reserve KV blocks on the host allocator for L + g tokens per sequence
+     (paged_allocator.py:50-55) and upload new table rows
   3. pack rows on the device (ne_prepare_verify_step), run the Qwen3 forward,
      the LM head (argmax partials only when greedy) and the fused acceptance,
      which appends kept tokens + 1 to the device history and rolls
@@ -60,7 +64,7 @@ def request_length_error(num_prompt_tokens: int, max_new_tokens: int, max_model_
     return None
 
 
-@dataclass
+@dataclass(slots=True)
 class StepResult:
     """Tokens emitted for one sequence by one step, with its finish reason if it ended."""
 
@@ -89,14 +93,16 @@ class VerifyRunner:
         self.proposer = proposer
         self.pool = pool
         self.allocator = allocator
-        # the shared-block guard only has something to check with a prefix cache
+        # the shared-block guard only has something to check with a prefix cache, and only
+        # a prefix cache acts on newly cached tokens
         self._guard_shared = type(allocator).first_writable_position is not PagedSlotAllocator.first_writable_position
+        self._track_cached = type(allocator).on_tokens_cached is not PagedSlotAllocator.on_tokens_cached
         self.device = model.device
         self.k = num_speculative_tokens
         self.R = self.k + 1
         self.max_seqs = max_seqs
         self.max_ngram = max_ngram
-        self.stop_token_ids = stop_token_ids
+        self.stop_token_ids = frozenset(stop_token_ids)
         self.block_size = allocator.block_size
         self.max_model_len = max_model_len
         self.capacity = max_model_len + self.R
@@ -114,6 +120,10 @@ class VerifyRunner:
         self.num_tokens = torch.zeros(max_seqs, **i32)
         self.drafts = torch.zeros(max_seqs, self.k, **i32)
         self.num_drafts = torch.zeros(max_seqs, **i32)
+        # length limit and generated count per slot, advanced on the device after each
+        # step so that the next step's n-gram guesses need no host round trip
+        self.max_new = torch.zeros(max_seqs, **i32)
+        self.generated = torch.zeros(max_seqs, **i32)
         self.seeds = torch.zeros(max_seqs, dtype=torch.int64, device=dev)
         self.steps = torch.zeros(max_seqs, dtype=torch.int64, device=dev)
         # per-slot sampling parameters (sampling.py:30-38): temperature 0 verifies greedily
@@ -138,6 +148,8 @@ class VerifyRunner:
         self.h_num_tokens = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         self.h_steps = torch.zeros(max_seqs, dtype=torch.int64, **pin)
         self.h_num_drafts = torch.zeros(max_seqs, dtype=torch.int32, **pin)
+        # the next step's counts, read back with this step's tokens (n-gram drafting)
+        self.h_num_drafts_next = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         self.h_out = torch.zeros(max_seqs, self.R, dtype=torch.int32, **pin)
         self.h_drafts = torch.zeros(max_seqs, self.k, dtype=torch.int32, **pin)
         self.h_num_out = torch.zeros(max_seqs, dtype=torch.int32, **pin)
@@ -147,6 +159,10 @@ class VerifyRunner:
         self.np_num_tokens = self.h_num_tokens.numpy()
         self.np_steps = self.h_steps.numpy()
         self.np_num_drafts = self.h_num_drafts.numpy()
+        self.np_num_drafts_next = self.h_num_drafts_next.numpy()
+        # whether the device drafts / num_drafts already hold this step's n-gram guesses
+        # (proposed at the end of the previous step, no sequence admitted since)
+        self._drafts_ready = False
         self.np_out = self.h_out.numpy()
         self.np_num_out = self.h_num_out.numpy()
         # per-slot host state mirrored from the Sequence objects, so that a step's counts
@@ -288,6 +304,10 @@ class VerifyRunner:
             results[slot] = self._emit(slot, seq, [int(self.h_out[s0 + i, 0])], 0, 0)
             self.np_len[slot] = seq.num_tokens
             self.np_gen[slot] = seq.num_generated_tokens
+        sl = slice(s0, s0 + n)
+        self.max_new[sl] = torch.from_numpy(self.np_max_new[sl].astype(np.int32))
+        self.generated[sl] = torch.from_numpy(self.np_gen[sl].astype(np.int32))
+        self._drafts_ready = False  # the new slots have no guesses yet
         return results
 
     def _prefill_forward(self, pieces: list[tuple[int, Sequence, int, int, int]]) -> None:
@@ -364,6 +384,12 @@ class VerifyRunner:
             draft_logits=draft_logits,
             draft_row_start=None if draft_logits is None else self.proposer.row_start,
         )
+        if self.proposer is None:
+            # the next step's guess counts, then its n-gram guesses on the updated histories
+            kernels.advance_step_counts(self.history_len, self.num_out, self.max_new, self.generated, self.steps,
+                                        self.num_tokens, self.k)
+            kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
+                                  drafts=self.drafts, num_drafts=self.num_drafts)
 
     def _run_device_step(self) -> None:
         sampled = self.any_sampled
@@ -393,14 +419,18 @@ class VerifyRunner:
         # num_guesses for every slot at once (speculative_generator.py:71-72)
         counts = np.clip(np.minimum(self.k, self.np_max_new - self.np_gen - 1), 0, None)
         self.np_num_tokens[:] = np.where(act, counts, 0)
-        self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
-        self.steps.copy_(self.h_steps, non_blocking=True)
         if self.proposer is None:
-            kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
-                                  drafts=self.drafts, num_drafts=self.num_drafts)
-            self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
-            torch.cuda.current_stream(self.device).synchronize()
+            if not self._drafts_ready:
+                self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
+                self.steps.copy_(self.h_steps, non_blocking=True)
+                kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
+                                      drafts=self.drafts, num_drafts=self.num_drafts)
+                self.h_num_drafts.copy_(self.num_drafts, non_blocking=True)
+                torch.cuda.current_stream(self.device).synchronize()
+            # else: the previous step proposed them and read back their counts
         else:
+            self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
+            self.steps.copy_(self.h_steps, non_blocking=True)
             guesses = self.proposer.propose({s: slots[s] for s in active},
                                             {s: int(self.np_num_tokens[s]) for s in active},
                                             temperature=self.batch_temperature, top_p=self.batch_top_p,
@@ -431,36 +461,67 @@ class VerifyRunner:
         tables_changed = len(grow) > 0
         if tables_changed:
             self.block_tables.copy_(self.h_tables, non_blocking=True)
+        ngram = self.proposer is None
+        if self.trace is not None:  # the device step overwrites the guesses with the next step's
+            torch.cuda.current_stream(self.device).synchronize()
+            traced_drafts = {s: self.drafts[s, : int(np_num_drafts[s])].tolist() for s in active}
         self._run_device_step()
         self.h_out.copy_(self.out_tokens, non_blocking=True)
         self.h_num_out.copy_(self.num_out, non_blocking=True)
+        if ngram:
+            self.h_num_drafts_next.copy_(self.num_drafts, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
         if self.trace is not None:
             self.trace.append({
                 s: {
                     "history": list(self.slots[s].token_ids),
-                    "requested": int(self.h_num_tokens[s]),
-                    "drafts": self.drafts[s, : int(self.h_num_drafts[s])].tolist(),
+                    "requested": int(self.np_num_tokens[s]),
+                    "drafts": traced_drafts[s],
                     "out": self.h_out[s, : int(self.h_num_out[s])].tolist(),
                     "table": self.allocator.block_table(self.slots[s]),
                 }
                 for s in active
             })
         results = {}
-        np_out, np_num_out = self.np_out, self.np_num_out
+        np_num_out = self.np_num_out
         # the mirrors advance by the emitted counts (a slot that finishes is released)
         emitted = np.where(act, np_num_out, 0)
         self.np_len += emitted
         self.np_gen += emitted
         self.np_steps[act] += 1
+        out_rows, nout, ndrafts = self.np_out.tolist(), np_num_out.tolist(), np_num_drafts.tolist()
+        # slots that may finish this step: at the length limit, or a stop token emitted by
+        # a slot that honours stops; every other slot takes the plain append below
+        may_finish = act & (self.np_gen >= self.np_max_new)
+        if self.stop_token_ids:
+            honours = np.fromiter((s is not None and not s.sampling_params.ignore_eos for s in slots), bool,
+                                  count=len(slots))
+            if honours.any():
+                rows = np.arange(self.R)[None, :] < np_num_out[:, None]
+                hit = (np.isin(self.np_out, list(self.stop_token_ids)) & rows).any(axis=1)
+                may_finish |= act & honours & hit
+        track_cached = self._track_cached
+        may_finish = may_finish.tolist()
         for s in active:
             seq = slots[s]
-            n = int(np_num_out[s])
-            g = int(np_num_drafts[s])
+            n = nout[s]
             kept = n - 1
-            cached = seq.num_tokens + kept  # L-1 .. L-1+kept now hold the kept tokens
             seq.sampling_generator.step += 1
-            results[s] = self._emit(s, seq, np_out[s, :n].tolist(), g, kept, cached)
+            if may_finish[s]:
+                cached = len(seq.token_ids) + kept  # L-1 .. L-1+kept now hold the kept tokens
+                results[s] = self._emit(s, seq, out_rows[s][:n], ndrafts[s], kept, cached)
+                continue
+            tokens = out_rows[s][:n]
+            ids = seq.token_ids
+            ids.extend(tokens)
+            seq.num_cached_tokens = len(ids) - 1  # L-1 .. L-1+kept hold the kept tokens
+            if track_cached:
+                self.allocator.on_tokens_cached(seq)
+            results[s] = StepResult(tokens, None, ndrafts[s], kept)
+        if ngram:  # the counts read back with this step's tokens are the next step's
+            self.h_num_drafts, self.h_num_drafts_next = self.h_num_drafts_next, self.h_num_drafts
+            self.np_num_drafts, self.np_num_drafts_next = self.np_num_drafts_next, self.np_num_drafts
+            self._drafts_ready = True
         return results
 
     def _emit(self, slot: int, seq: Sequence, tokens: list[int], g: int, kept: int,
@@ -473,8 +534,9 @@ class VerifyRunner:
         sequence is released, so its verified blocks stay reusable."""
         params = seq.sampling_params
         reason = None
-        stops = () if params.ignore_eos else self.stop_token_ids
-        if seq.num_generated_tokens + len(tokens) < params.max_new_tokens and not any(t in stops for t in tokens):
+        stops = self.stop_token_ids
+        if (len(seq.token_ids) - seq.num_prompt_tokens + len(tokens) < params.max_new_tokens
+                and (params.ignore_eos or stops.isdisjoint(tokens))):
             # no token can end the sequence: the checks below would all pass
             seq.token_ids.extend(tokens)
             emitted = tokens

@@ -65,6 +65,12 @@ def test_host_checks_reject_bad_arguments_without_launching(lib):
     rc = lib.ne_accept(p, 100, null, 0, 100, p, 4, p, p, 2, p, null, 1, p, p, p, p, null, 0, null, null,
                        p, 3, 100, p, null)
     assert rc == -1 and b"draft rows" in lib.ne_last_error()
+    # next-step counters: sizes and pointers are checked before any launch
+    rc = lib.ne_advance_step_counts(p, p, p, p, p, p, -1, 4, null)
+    assert rc == -1 and b"bad sizes" in lib.ne_last_error()
+    rc = lib.ne_advance_step_counts(p, null, p, p, p, p, 4, 4, null)
+    assert rc == -1 and b"null" in lib.ne_last_error()
+    assert lib.ne_advance_step_counts(null, null, null, null, null, null, 4, 0, null) == 0  # nothing to do
 
 
 def test_workspace_and_tile_queries(lib):

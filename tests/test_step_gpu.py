@@ -123,3 +123,38 @@ def test_prepare_verify_step_clamps_an_out_of_range_draft_count(device):
     assert slots[:5] == [5 * 16 + 3, 5 * 16 + 4, 5 * 16 + 5, 5 * 16 + 6, 5 * 16 + 7]
     assert tokens[5:] == [39, 0, 0, 0, 0] and slots[5:] == [1 * 16 + 3, 999, 999, 999, 999]
     assert ql == [5, 1] and cl == [24, 20] and qs == [0, 5]
+
+
+@pytest.mark.parametrize("k", [1, 4, 15])
+def test_advance_step_counts_follow_num_guesses(k):
+    """ne_advance_step_counts (the n-gram path's next-step counters) against the
+    reference's rule num_guesses = max(0, min(k, max_new - generated - 1))
+    (speculative_generator.py:71-72, interface.num_guesses): generated advances by the
+    emitted tokens and the sampling step by one for active slots; inactive slots get 0
+    guesses and keep their counters.  Covers the limit boundary (0 guesses at
+    max_new - 1 generated and beyond)."""
+    from nanoengine_amd.interface import SamplingParams, num_guesses
+
+    rng = np.random.default_rng(k)
+    n = 300
+    dev = torch.device("cuda:0")
+    history_len = rng.integers(0, 50, size=n).astype(np.int32)
+    history_len[::7] = 0
+    num_out = rng.integers(1, k + 2, size=n).astype(np.int32)
+    max_new = rng.integers(1, 64, size=n).astype(np.int32)
+    generated = np.minimum(rng.integers(0, 64, size=n), max_new).astype(np.int32)
+    steps = rng.integers(0, 1 << 40, size=n).astype(np.int64)
+    t = lambda a: torch.from_numpy(a.copy()).to(dev)
+    d_gen, d_steps = t(generated), t(steps)
+    d_guess = torch.full((n,), -5, dtype=torch.int32, device=dev)
+    kernels.advance_step_counts(t(history_len), t(num_out), t(max_new), d_gen, d_steps, d_guess, k)
+    torch.cuda.synchronize()
+    active = history_len > 0
+    exp_gen = np.where(active, generated + num_out, generated)
+    exp_steps = np.where(active, steps + 1, steps)
+    exp_guess = np.array([num_guesses(SamplingParams(max_new_tokens=int(m)), int(g), k) if a else 0
+                          for a, m, g in zip(active, max_new, exp_gen)], dtype=np.int32)
+    assert np.array_equal(d_gen.cpu().numpy(), exp_gen)
+    assert np.array_equal(d_steps.cpu().numpy(), exp_steps)
+    assert np.array_equal(d_guess.cpu().numpy(), exp_guess)
+    assert (exp_guess == 0).any() and (exp_guess == k).any()
