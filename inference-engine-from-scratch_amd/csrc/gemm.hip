@@ -13,10 +13,12 @@
 // int8 weights become bf16 in registers after the LDS read (exact); the per-row
 // scale is applied to the fp32 sum.
 //
-// At M = 320 every N-tile re-reads X, so what bounds these GEMMs is the L2 -> CU
-// traffic (about 25 B per clock per CU), not HBM or the MFMAs: the tiles are sized
-// to keep that traffic per CU near its minimum for 256 independent tiles, and the
-// LM head keeps all 320 rows resident per work-group to read X once per 256 columns.
+// At M = 320 every N-tile re-reads X; the tiles are sized to keep that traffic per CU
+// near its minimum for 256 independent tiles, and the LM head keeps all 320 rows
+// resident per work-group to read X once per 256 columns.  A projection's time is its
+// work-group's chain (first weight fetch from HBM, then per stage a barrier, the copy
+// issue, the fragment reads and the MFMAs, then the k-group exchange), not L2 -> CU
+// bandwidth (~30 TB/s with enough loads in flight), HBM or the MFMAs.
 #include "ne_common.hpp"
 #include "qk_rope_kv.hpp"
 
@@ -93,14 +95,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---- W8A16 projections ----------------------------------------------------------
-// Work-group tile: 80 token rows (5 MFMA subtiles) x 16 * NSUB weight rows, sized so
-// that the verify-step shapes give about one work-group per CU (M = 320: QKV
-// N = 4096 and gate|up N = 6144 give 256 tiles; o / down N = 1024 give 64 tiles,
-// split 4 ways over K).  The MFMA waves form kKGroups x NSUB/2: wave (kg, nw) runs
-// k-step kg (32 wide) of every 128-wide stage for all 5 token subtiles against weight
-// subtiles 2 nw and 2 nw + 1, so each X fragment read from LDS feeds 2 MFMAs and
-// each weight fragment 5.  The k-groups' partial tiles are summed through LDS at
-// the end, each wave finishing some of the token subtiles.
+// Work-group tile: PM * 16 token rows (80 for the plain shapes) x 16 * NSUB weight rows,
+// sized so that the verify-step shapes give about one work-group per CU (M = 320: QKV
+// N = 4096 and gate|up N = 6144 give 256 tiles; o / down N = 1024 give 64 tiles, split
+// 4 ways over K).  The MFMA waves form KG k-groups x NSUB / NPW: wave (kg, nw) runs the
+// 4 / KG k-steps kg * 4 / KG .. (32 wide each) of every 128-wide stage for all PM token
+// subtiles against weight subtiles nw * NPW .. + NPW, so each X fragment read from LDS
+// feeds NPW MFMAs and each weight fragment PM.  At the end, wave (kg, nw) finishes the
+// token subtiles mi with mi % KG == kg: the other k-groups' partial tiles of those come
+// through LDS and are added in k-group order.  Two k-groups halve that exchange (and
+// its barrier wait) against four, for twice the X fragment reads in the loop.
 //
 // Stages are copied by DMA into two LDS rings: X rows (from L2, where every column
 // tile re-reads them) run kRX - 1 stages ahead and weight rows (from HBM, the longer
@@ -109,13 +113,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // fragments of stage t from LDS before it runs the MFMAs of stage t - 1 (held in
 // registers), so the LDS latency hides under the multiplies.
 constexpr int kPM = 5;  // token subtiles per work-group (the fused QKV epilogue uses 3)
-constexpr int kKGroups = 4;
 
-template <int NSUB, int PM = kPM>
+template <int NSUB, int PM, int KG, int NPW>
 struct ProjLayout {
+  static_assert(KG == 1 || KG == 2 || KG == 4, "k-groups split the 4 k-steps of a stage");
+  static_assert(NSUB % NPW == 0, "weight subtiles per wave");
+  static constexpr int kKS = 4 / KG;  // k-steps per wave per stage
   static constexpr int kPRows = PM * 16;
-  static constexpr int kNW = NSUB / 2;
-  static constexpr int kWaves = kKGroups * kNW;
+  static constexpr int kNW = NSUB / NPW;
+  static constexpr int kWaves = KG * kNW;
   static constexpr int kThreads = kWaves * kWave;
   static constexpr int kXI = PM * 4;    // 1 KiB copies per stage: X rows of 256 B ...
   static constexpr int kWI = NSUB * 2;  // ... and weight rows of 128 B
@@ -138,7 +144,7 @@ struct ProjLayout {
   static constexpr int kDW = split() % 256;
   static constexpr int kNXW = kXI / kDX;  // waves [0, kNXW) copy X
   static constexpr int kNWW = kWI / kDW;  // waves [kNXW, kNXW + kNWW) copy weights
-  static constexpr int kRedBytes = kKGroups * kNW * PM * 2 * 1024;
+  static constexpr int kRedBytes = KG * kNW * PM * NPW * 1024;
   static constexpr int kRing = kRX * kXBytes + kRW * kWBytes;
   static constexpr int kLds = kRing > kRedBytes ? kRing : kRedBytes;
   static_assert(split() > 0, "copy split");
@@ -173,14 +179,16 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 
 
 // The k loop of a work-group: kt_n stages of 128 from k = kbase (KT > 0: kt_n = KT).  X rows m0.. (rows past
 // m re-read row m - 1 and are never stored) and weight rows n0.. are copied with the
-// chunk swizzles below; lane group g = lane / 16 of k-group kg supplies logical
-// k = 64 (kg / 2) + 16 g + 8 (kg % 2) + e, e < 8: X chunk 8 (kg / 2) + 2 g + kg % 2 of
-// its 256-byte row, weight bytes 16 (4 (kg / 2) + g) + 8 (kg % 2) of its 128-byte row.
-template <int NSUB, int PM, int KT>
+// chunk swizzles below; in k-step kk (0..3) of a stage, lane group g = lane / 16
+// supplies logical k = 64 (kk / 2) + 16 g + 8 (kk % 2) + e, e < 8: X chunk
+// 8 (kk / 2) + 2 g + kk % 2 of its 256-byte row, weight bytes 16 (4 (kk / 2) + g) +
+// 8 (kk % 2) of its 128-byte row.  Wave (kg, nw) runs k-steps kk = kg * KS + s.
+template <int NSUB, int PM, int KG, int NPW, int KT>
 __device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, int m0, int n0, int kbase,
                                               int kt_runtime, int wave, int lane, int kg, int nw,
-                                              floatx4 (&acc)[PM][2]) {
-  using L = ProjLayout<NSUB, PM>;
+                                              floatx4 (&acc)[PM][NPW]) {
+  using L = ProjLayout<NSUB, PM, KG, NPW>;
+  constexpr int KS = L::kKS;
   // a stage count known at compile time turns every wait below into one instruction
   const int kt_n = KT > 0 ? KT : kt_runtime;
   const int r = lane & 15;
@@ -235,33 +243,53 @@ __device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, i
     if (xwave) wait_pending<L::kDX, L::kRX - 2>(min(kt_n - t - 1, L::kRX - 2));
     if (wwave) wait_pending<L::kDW, L::kRW - 2>(min(kt_n - t - 1, L::kRW - 2));
   };
-  const int cx = 8 * (kg >> 1) + 2 * g + (kg & 1);
-  const uint32_t xr = (uint32_t)(r * 256 + ((cx ^ r) * 16));
-  const int cw = 4 * (kg >> 1) + g;
-  const uint32_t wr = (uint32_t)((2 * nw * 16 + r) * 128 + ((cw ^ (r & 7)) * 16) + (kg & 1) * 8);
-  auto read = [&](int s, u32x4 (&xf)[PM], u32x2 (&wf)[2]) {
+  uint32_t xr[KS], wr[KS];
+#pragma unroll
+  for (int q = 0; q < KS; ++q) {
+    const int kk = kg * KS + q;
+    const int cx = 8 * (kk >> 1) + 2 * g + (kk & 1);
+    xr[q] = (uint32_t)(r * 256 + ((cx ^ r) * 16));
+    const int cw = 4 * (kk >> 1) + g;
+    wr[q] = (uint32_t)((nw * NPW * 16 + r) * 128 + ((cw ^ (r & 7)) * 16) + (kk & 1) * 8);
+  }
+  using XFrag = u32x4[KS][PM];
+  using WFrag = u32x2[KS][NPW];
+  using AFrag = bf16x8[KS][NPW];
+  // weight fragments first: their conversion is the first thing waiting on them
+  auto read = [&](int s, XFrag& xf, WFrag& wf) {
     const char* xs = xring + (s % L::kRX) * L::kXBytes;
     const char* ws = wring + (s % L::kRW) * L::kWBytes;
 #pragma unroll
-    for (int mi = 0; mi < PM; ++mi) xf[mi] = *(const u32x4*)(xs + xr + mi * 4096);
+    for (int q = 0; q < KS; ++q)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) wf[ns] = *(const u32x2*)(ws + wr + ns * 2048);
+      for (int ns = 0; ns < NPW; ++ns) wf[q][ns] = *(const u32x2*)(ws + wr[q] + ns * 2048);
+#pragma unroll
+    for (int q = 0; q < KS; ++q)
+#pragma unroll
+      for (int mi = 0; mi < PM; ++mi) xf[q][mi] = *(const u32x4*)(xs + xr[q] + mi * 4096);
   };
-  auto mma = [&](const u32x4 (&xf)[PM], const u32x2 (&wf)[2]) {
-    bf16x8 a[2];
+  auto convert = [&](const WFrag& wf, AFrag& a) {
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) a[ns] = int8x8_to_bf16x8(wf[ns][0], wf[ns][1]);
+    for (int q = 0; q < KS; ++q)
 #pragma unroll
-    for (int mi = 0; mi < PM; ++mi)
+      for (int ns = 0; ns < NPW; ++ns) a[q][ns] = int8x8_to_bf16x8(wf[q][ns][0], wf[q][ns][1]);
+  };
+  auto mma = [&](const XFrag& xf, const AFrag& a) {
 #pragma unroll
-      for (int ns = 0; ns < 2; ++ns)
-        acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ns], __builtin_bit_cast(bf16x8, xf[mi]),
-                                                              acc[mi][ns], 0, 0, 0);
+    for (int q = 0; q < KS; ++q)
+#pragma unroll
+      for (int mi = 0; mi < PM; ++mi)
+#pragma unroll
+        for (int ns = 0; ns < NPW; ++ns)
+          acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[q][ns], __builtin_bit_cast(bf16x8, xf[q][mi]),
+                                                                acc[mi][ns], 0, 0, 0);
   };
   // stage t: its copies are in LDS after the barrier, and every wave has read stage
   // t - 1 into registers before it (lgkmcnt(0)), so the slots of stage t - 1 take the
-  // copies of stages t + kRX - 1 and t + kRW - 1
-  auto step = [&](int t, u32x4 (&xr_)[PM], u32x2 (&wr_)[2], const u32x4 (&xm)[PM], const u32x2 (&wm)[2]) {
+  // copies of stages t + kRX - 1 and t + kRW - 1.  The MFMAs of stage t - 1 run on
+  // weights converted to bf16 during step t - 1, and stage t's weights are converted
+  // after them, so the conversion overlaps the MFMAs still in the pipeline.
+  auto step = [&](int t, XFrag& xr_, WFrag& wr_, AFrag& ar, const XFrag& xm, const AFrag& am) {
     wait_stage(t);
     wait_lgkmcnt0();
     asm volatile("s_barrier" ::: "memory");
@@ -269,7 +297,9 @@ __device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, i
     if (t + L::kRW - 1 < kt_n) issue_w(t + L::kRW - 1);
     read(t, xr_, wr_);
     __builtin_amdgcn_sched_barrier(0);  // the reads go out before the multiplies
-    mma(xm, wm);
+    mma(xm, am);
+    convert(wr_, ar);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
 #pragma unroll
@@ -278,25 +308,27 @@ __device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, i
 #pragma unroll
   for (int s = 0; s < L::kRX - 1; ++s)
     if (s < kt_n) issue_x(s);
-  u32x4 xa[PM], xb[PM];
-  u32x2 wa[2], wb[2];
+  XFrag xa, xb;
+  WFrag wa, wb;
+  AFrag aa, ab;
   wait_stage(0);
   asm volatile("s_barrier" ::: "memory");
   if (L::kRX - 1 < kt_n) issue_x(L::kRX - 1);
   if (L::kRW - 1 < kt_n) issue_w(L::kRW - 1);
   read(0, xa, wa);
+  convert(wa, aa);
   int t = 1;
   for (; t + 1 < kt_n; t += 2) {
-    step(t, xb, wb, xa, wa);
-    step(t + 1, xa, wa, xb, wb);
+    step(t, xb, wb, ab, xa, aa);
+    step(t + 1, xa, wa, aa, xb, ab);
   }
   if (t < kt_n) {
-    step(t, xb, wb, xa, wa);
+    step(t, xb, wb, ab, xa, aa);
     wait_lgkmcnt0();
-    mma(xb, wb);
+    mma(xb, ab);
   } else {
     wait_lgkmcnt0();
-    mma(xa, wa);
+    mma(xa, aa);
   }
 }
 
@@ -306,14 +338,25 @@ __device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, i
 // through QK-norm + RoPE into q_out or quantised into the KV cache (qk_rope_kv.hpp) --
 // the bits the GEMM with EPI 0 followed by the row kernel produce, without the qkv round
 // trip through memory.  KV (EPI 4): 1 bf16 cache, 2 int8 + bf16 scales, 3 int8 + fp16.
-template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM, int KT = 0>
-__global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(GemmParams p,
-                                                                         int k_per_split,
-                                                                         float* partial,
-                                                                         QkvRopeArgs qa) {
-  using L = ProjLayout<NSUB, PM>;
+template <int NSUB, int SDT, int EPI, int KV, int PM, int KG, int NPW, int KT>
+__global__ __launch_bounds__((ProjLayout<NSUB, PM, KG, NPW>::kThreads)) void proj_kernel(
+    GemmParams p, int k_per_split, float* partial, QkvRopeArgs qa) {
+  using L = ProjLayout<NSUB, PM, KG, NPW>;
   constexpr int kPRows = L::kPRows;
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  // Every kernel argument the work-group uses, requested in one batch: left to itself
+  // the compiler loads each next to its first use, and the tile index, the copy
+  // addresses and the epilogue then wait on one scalar-cache round trip after another.
+  asm volatile("" ::"s"(p.x), "s"(p.ldx), "s"(p.w), "s"(p.scale), "s"(p.m), "s"(p.k), "s"(p.tiles_m),
+               "s"(p.tiles_n), "s"(k_per_split));
+  if constexpr (EPI == 3) {
+    asm volatile("" ::"s"(partial), "s"(p.n));
+  } else if constexpr (EPI != 4) {
+    asm volatile("" ::"s"(p.y), "s"(p.ldy));
+  } else {
+    asm volatile("" ::"s"(qa.q_norm_w), "s"(qa.k_norm_w), "s"(qa.positions), "s"(qa.slot_mapping),
+                 "s"(qa.rope), "s"(qa.rope_positions), "s"(qa.hq));
+  }
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
   const int jj = bid / kNumXcd;
@@ -332,13 +375,13 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
   const int g = lane >> 4;
 
   // the epilogue's weight-row scales, fetched now so that their latency hides under
-  // the k loop: lane (r, g) stores columns (2 nw + ns) 16 + 4 g + i
-  float sc[2][4] = {};
+  // the k loop: lane (r, g) stores columns (nw NPW + ns) 16 + 4 g + i
+  float sc[NPW][4] = {};
   if constexpr (EPI != 4) {  // EPI 4 scales its rows' columns instead (e_sc)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns)
+    for (int ns = 0; ns < NPW; ++ns)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[ns][i] = scale_at<SDT>(p.scale, n0 + (2 * nw + ns) * 16 + 4 * g + i);
+      for (int i = 0; i < 4; ++i) sc[ns][i] = scale_at<SDT>(p.scale, n0 + (nw * NPW + ns) * 16 + 4 * g + i);
   }
 
   // EPI 4: wave w finishes rows w, w + kWaves, ... of the tile (head tn).  Their slots
@@ -363,13 +406,14 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
     }
   }
 
-  floatx4 acc[PM][2];
+  floatx4 acc[PM][NPW];
 #pragma unroll
   for (int mi = 0; mi < PM; ++mi)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int ns = 0; ns < NPW; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  proj_mainloop<NSUB, PM, KT>(p, smem, m0, n0, kbase, k_per_split / kStageK, wave, lane, kg, nw, acc);
+  proj_mainloop<NSUB, PM, KG, NPW, KT>(p, smem, m0, n0, kbase, k_per_split / kStageK, wave, lane, kg, nw,
+                                       acc);
 
   // EPI 4: the rows' cos / sin, in flight while the k-groups are summed
   uint16_t e_rc[kEpiRows], e_rs[kEpiRows];
@@ -393,15 +437,15 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
     // k-groups in order and scaled, the bits the GEMM epilogue stores
     static_assert(NSUB == 8, "one head per tile");
     constexpr int kRowF = 132;
-    static_assert(kKGroups * kPRows * kRowF * 4 <= L::kLds, "partials fit the stage ring");
+    static_assert(KG * kPRows * kRowF * 4 <= L::kLds, "partials fit the stage ring");
     constexpr bool kInt8 = KV >= 2;
     constexpr int kKvSdt = KV == 3 ? NE_DTYPE_FP16 : NE_DTYPE_BF16;
     float* part = (float*)smem;
 #pragma unroll
     for (int mi = 0; mi < PM; ++mi)
 #pragma unroll
-      for (int ns = 0; ns < 2; ++ns)
-        *(floatx4*)(part + (kg * kPRows + mi * 16 + r) * kRowF + (2 * nw + ns) * 16 + 4 * g) = acc[mi][ns];
+      for (int ns = 0; ns < NPW; ++ns)
+        *(floatx4*)(part + (kg * kPRows + mi * 16 + r) * kRowF + (nw * NPW + ns) * 16 + 4 * g) = acc[mi][ns];
     lds_barrier();
     // this wave's rows all at once, so that their reductions overlap
     int rows_e[kEpiRows];
@@ -416,7 +460,7 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
       float va = part[rr * kRowF + lane];
       float vb = part[rr * kRowF + 64 + lane];
 #pragma unroll
-      for (int q = 1; q < kKGroups; ++q) {
+      for (int q = 1; q < KG; ++q) {
         va += part[(q * kPRows + rr) * kRowF + lane];
         vb += part[(q * kPRows + rr) * kRowF + 64 + lane];
       }
@@ -430,33 +474,43 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
                                                      bf16_to_f32(e_w[0]), bf16_to_f32(e_w[1]), c_e, s_e);
     return;
   }
-  floatx4* red = (floatx4*)smem;  // [kg][nw][mi][ns][lane]
+  // Token subtile mi is finished by k-group mi % KG: each wave hands the partial tiles of
+  // the other subtiles to their finishing wave through LDS, [kg][nw][mi][ns][lane].
+  floatx4* red = (floatx4*)smem;
+  auto red_at = [&](int q, int mi, int ns) -> floatx4& {
+    return red[(((q * L::kNW + nw) * PM + mi) * NPW + ns) * kWave + lane];
+  };
 #pragma unroll
   for (int mi = 0; mi < PM; ++mi)
+    if (KG > 1 && mi % KG != kg)
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) red[(((kg * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane] = acc[mi][ns];
-  lds_barrier();
+      for (int ns = 0; ns < NPW; ++ns) red_at(kg, mi, ns) = acc[mi][ns];
+  if constexpr (KG > 1) lds_barrier();
 
-  for (int mi = kg; mi < PM; mi += kKGroups) {
-    floatx4 v[2];
 #pragma unroll
-    for (int ns = 0; ns < 2; ++ns) {
-      v[ns] = red[((nw * PM + mi) * 2 + ns) * kWave + lane];
+  for (int mi = 0; mi < PM; ++mi) {
+    if (mi % KG != kg) continue;
+    floatx4 v[NPW];
 #pragma unroll
-      for (int q = 1; q < kKGroups; ++q) v[ns] += red[(((q * L::kNW + nw) * PM + mi) * 2 + ns) * kWave + lane];
+    for (int ns = 0; ns < NPW; ++ns) {
+      // in k-group order, this wave's own partial from its registers
+      v[ns] = kg == 0 ? acc[mi][ns] : red_at(0, mi, ns);
+#pragma unroll
+      for (int q = 1; q < KG; ++q) v[ns] += q == kg ? acc[mi][ns] : red_at(q, mi, ns);
     }
-    // lane holds D[n = 4 g + i][m = r] of weight subtiles 2 nw + ns
+    // lane holds D[n = 4 g + i][m = r] of weight subtiles nw NPW + ns
     const int m = m0 + mi * 16 + r;
     if (m >= p.m) continue;
     if constexpr (EPI == 0) {
 #pragma unroll
-      for (int ns = 0; ns < 2; ++ns) {
-        const int n = n0 + (2 * nw + ns) * 16 + 4 * g;
+      for (int ns = 0; ns < NPW; ++ns) {
+        const int n = n0 + (nw * NPW + ns) * 16 + 4 * g;
         const u32x2 bits = {pack_bf16x2(v[ns][0] * sc[ns][0], v[ns][1] * sc[ns][1]),
                             pack_bf16x2(v[ns][2] * sc[ns][2], v[ns][3] * sc[ns][3])};
         *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
       }
     } else if constexpr (EPI == 1) {
+      static_assert(NPW == 2, "a wave holds paired gate / up subtiles");
       float out[4];  // gate rows are subtile 2 nw, the paired up rows subtile 2 nw + 1
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -470,8 +524,8 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
       *(u32x2*)(p.y + (int64_t)m * p.ldy + ncol) = bits;
     } else {
 #pragma unroll
-      for (int ns = 0; ns < 2; ++ns) {
-        const int n = n0 + (2 * nw + ns) * 16 + 4 * g;
+      for (int ns = 0; ns < NPW; ++ns) {
+        const int n = n0 + (nw * NPW + ns) * 16 + 4 * g;
         const floatx4 sv = {v[ns][0] * sc[ns][0], v[ns][1] * sc[ns][1], v[ns][2] * sc[ns][2],
                             v[ns][3] * sc[ns][3]};
         *(floatx4*)(partial + ((int64_t)split * p.m + m) * p.n + n) = sv;
@@ -480,59 +534,70 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM>::kThreads)) void proj_kernel(
   }
 }
 
-template <int NSUB, int SDT, int EPI, int KV, int PM, int KT>
+template <int NSUB, int SDT, int EPI, int KV, int PM, int KG, int NPW, int KT>
 int launch_proj_kt(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
                    const QkvRopeArgs& qa) {
-  using L = ProjLayout<NSUB, PM>;
+  using L = ProjLayout<NSUB, PM, KG, NPW>;
   p.tiles_m = ceil_div(p.m, L::kPRows);
   p.tiles_n = p.n / (NSUB * 16);
   const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
   const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
-  static const hipError_t attr = hipFuncSetAttribute((const void*)proj_kernel<NSUB, SDT, EPI, KV, PM, KT>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds);
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)proj_kernel<NSUB, SDT, EPI, KV, PM, KG, NPW, KT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+      L::kLds);
   if (attr != hipSuccess) {
     set_error("%s: cannot reserve %d bytes of LDS: %s", name, L::kLds, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI, KV, PM, KT>), grid, dim3(L::kThreads), L::kLds, stream, p,
-                     p.k / splits, partial, qa);
+  hipLaunchKernelGGL((proj_kernel<NSUB, SDT, EPI, KV, PM, KG, NPW, KT>), grid, dim3(L::kThreads), L::kLds,
+                     stream, p, p.k / splits, partial, qa);
   return check_launch(name);
 }
 
 // Stage counts with a kernel of their own: 8 (K = 1024, the QKV and gate|up
 // projections of the 0.6B model), 4 and 6 (o and down split 4 ways over K = 2048 and
 // 3072); any other count runs the loop with a run-time count.
-template <int NSUB, int SDT, int EPI, int KV = 0, int PM = kPM>
+template <int NSUB, int SDT, int EPI, int KV, int PM, int KG, int NPW>
 int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
                 const QkvRopeArgs& qa = QkvRopeArgs{}) {
   const int kt = p.k / splits / kStageK;
   if constexpr (EPI == 3) {
-    if (kt == 4) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 4>(p, splits, partial, stream, name, qa);
-    if (kt == 6) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 6>(p, splits, partial, stream, name, qa);
+    if (kt == 4) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 4>(p, splits, partial, stream, name, qa);
+    if (kt == 6) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 6>(p, splits, partial, stream, name, qa);
   } else {
-    if (kt == 8) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 8>(p, splits, partial, stream, name, qa);
+    if (kt == 8) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 8>(p, splits, partial, stream, name, qa);
   }
-  return launch_proj_kt<NSUB, SDT, EPI, KV, PM, 0>(p, splits, partial, stream, name, qa);
+  return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 0>(p, splits, partial, stream, name, qa);
 }
+
+// Wave layouts (k-groups, weight subtiles per wave).  The plain and split-K products and
+// the fused QKV projection share two k-groups, so the fused epilogue sums every output in
+// the order the plain GEMM does and both round to the same bits; SwiGLU pairs gate and
+// up subtiles in one wave and keeps four k-groups to keep 12 waves.
+constexpr int kKgPlain = 2, kNpwPlain = 1;
+constexpr int kKgQkv = 2, kNpwQkv = 2;
+constexpr int kKgSwiglu = 4, kNpwSwiglu = 2;
 
 template <int SDT>
 int dispatch_qkv_fused(GemmParams p, const QkvRopeArgs& qa, int kv_mode, hipStream_t s) {
   switch (kv_mode) {
     // 48-row tiles: 7 x 32 = 224 work-groups for 320 rows, 3 rows per wave in the epilogue
-    case 1: return launch_proj<8, SDT, 4, 1, 3>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
-    case 2: return launch_proj<8, SDT, 4, 2, 3>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
-    default: return launch_proj<8, SDT, 4, 3, 3>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
+    case 1: return launch_proj<8, SDT, 4, 1, 3, kKgQkv, kNpwQkv>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
+    case 2: return launch_proj<8, SDT, 4, 2, 3, kKgQkv, kNpwQkv>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
+    default: return launch_proj<8, SDT, 4, 3, 3, kKgQkv, kNpwQkv>(p, 1, nullptr, s, "w8a16_qkv_norm_rope_kv", qa);
   }
 }
 
 template <int SDT>
 int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipStream_t s) {
   if (epilogue == NE_EPILOGUE_SWIGLU) {
-    if (p.n % 96 == 0) return launch_proj<6, SDT, 1>(p, 1, nullptr, s, "w8a16_swiglu");
-    return launch_proj<4, SDT, 1>(p, 1, nullptr, s, "w8a16_swiglu");
+    if (p.n % 96 == 0)
+      return launch_proj<6, SDT, 1, 0, kPM, kKgSwiglu, kNpwSwiglu>(p, 1, nullptr, s, "w8a16_swiglu");
+    return launch_proj<4, SDT, 1, 0, kPM, kKgSwiglu, kNpwSwiglu>(p, 1, nullptr, s, "w8a16_swiglu");
   }
-  if (partial != nullptr) return launch_proj<4, SDT, 3>(p, splits, partial, s, "w8a16_splitk");
-  return launch_proj<4, SDT, 0>(p, 1, nullptr, s, "w8a16_gemm");
+  if (partial != nullptr)
+    return launch_proj<4, SDT, 3, 0, kPM, kKgPlain, kNpwPlain>(p, splits, partial, s, "w8a16_splitk");
+  return launch_proj<4, SDT, 0, 0, kPM, kKgPlain, kNpwPlain>(p, 1, nullptr, s, "w8a16_gemm");
 }
 
 // ---- LM head: persistent work-groups over the vocabulary -------------------------
