@@ -18,9 +18,7 @@ import torch
 
 from nanoengine_amd import kernels
 from nanoengine_amd._native import EPILOGUE_SWIGLU
-
-INT8_MAX = 127
-MIN_SCALE = 1e-8
+from nanoengine_amd.int8_quantization import quantize_vectors
 
 
 @dataclass(frozen=True)
@@ -96,11 +94,10 @@ def random_state_dict(config: Qwen3Config, seed: int, std: float) -> dict[str, t
 
 
 def quantize_rows(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-output-row symmetric int8 (Int8Linear.from_linear, int8_quantization.py:30-34,
-    50-53): s = max(|w|) clamped to 1e-8, / 127 in fp32; q = round-half-even(w / s)."""
-    scales = weight.abs().amax(dim=-1, keepdim=True).float().clamp(min=MIN_SCALE) / INT8_MAX
-    q = torch.round(weight.float() / scales).clamp(-INT8_MAX, INT8_MAX).to(torch.int8)
-    return q, scales.squeeze(-1).to(weight.dtype)
+    """Per-output-row symmetric int8, the codes and row scales of Int8Linear.from_linear
+    (int8_quantization.py:50-53)."""
+    q, scales = quantize_vectors(weight)
+    return q, scales.squeeze(-1)
 
 
 def pair_rows(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:

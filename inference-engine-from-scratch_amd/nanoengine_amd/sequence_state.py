@@ -15,7 +15,9 @@ from nanoengine_amd.interface import (
 
 @dataclass(eq=False)
 class Sequence:
-    """Prompt plus generated tokens; ``num_cached_tokens`` of them have keys/values cached."""
+    """A request's tokens so far, prompt first, then the generated ones.  The keys and
+    values of the first ``num_cached_tokens`` are in the KV pool.  Instances compare by
+    identity, so a sequence is found in a list only as the same object."""
 
     request: GenerationRequest
     sampling_generator: SamplingStream
