@@ -101,12 +101,23 @@ def gemm_traffic(m, n, k):
     return n * k + 2 * n + 2 * m * k + 2 * m * n
 
 
+def speculation_stats(tokens: int, proposed: int, accepted: int) -> dict:
+    """The reference benchmark's figures (benchmarks/speculative.py:104-114): acceptance =
+    accepted / proposed guesses; a target pass emits its kept guesses plus one token, so
+    passes = tokens - accepted and tokens per target pass = tokens / passes."""
+    return {"proposed": proposed, "accepted": accepted,
+            "acceptance_rate": round(accepted / proposed, 4) if proposed else 0.0,
+            "tokens_per_target_pass": round(tokens / max(tokens - accepted, 1), 4)}
+
+
 def run_verify(args, torch, temperature: float | None = None, steps: int | None = None,
-               warmup: int | None = None, draft: bool = False):
+               warmup: int | None = None, draft: bool = False, to_completion: bool = False):
     """The verify step at 64 sequences, k = 4.  draft=True: guesses from a draft model
     (DraftModelProposer) with the target's own weights as the draft (the reference's
     default draft model id names the same Qwen3-0.6B), so every guess a greedy target
-    would make is proposed and the step pays four draft forwards."""
+    would make is proposed and the step pays four draft forwards.  to_completion=True:
+    the 128-token generation from its first verify step until every sequence has
+    finished, each step timed (the batch shrinks as sequences end)."""
     from nanoengine_amd import _native
     from nanoengine_amd.config import EngineSettings
     from nanoengine_amd.interface import GenerationRequest, SamplingParams
@@ -121,7 +132,7 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     total_steps = warmup + steps
     # every sequence must still be generating in the last timed step: a step emits at
     # most k + 1 tokens, so 128 tokens last >= 26 steps; longer runs get longer outputs
-    max_new = max(OUTPUT_TOKENS, (K_DRAFT + 1) * total_steps + 2)
+    max_new = OUTPUT_TOKENS if to_completion else max(OUTPUT_TOKENS, (K_DRAFT + 1) * total_steps + 2)
     max_len = PROMPT_MOTIF * PROMPT_REPEATS + max_new + K_DRAFT + 1
     t0 = time.perf_counter()
     state = random_state_dict(cfg, seed=0, std=0.02)
@@ -149,12 +160,17 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     # per step: the runner's slot lengths before it (its host mirror of each sequence's
     # token count) and what it emitted; the statistics are tallied after the timed loop
     records = []
-    for _ in range(steps):
-        lengths = eng.runner.np_len.copy()
-        records.append((lengths, eng.runner.step()))
+    if to_completion:
+        while eng.runner.active_slots:
+            lengths = eng.runner.np_len.copy()
+            records.append((lengths, eng.runner.step()))
+    else:
+        for _ in range(steps):
+            lengths = eng.runner.np_len.copy()
+            records.append((lengths, eng.runner.step()))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
-    tokens = 0
+    tokens = proposed = accepted = 0
     kept_hist: dict[int, int] = {}
     for lengths, results in records:
         # context of sequence b in this step = its length before the step + its guesses
@@ -162,14 +178,18 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
         lengths_per_step.append([int(lengths[i]) for i in results])
         for r in results.values():
             tokens += len(r.tokens)
+            proposed += r.num_guesses
+            accepted += r.num_kept
             kept_hist[r.num_kept] = kept_hist.get(r.num_kept, 0) + 1
     active = sum(1 for s in eng.runner.slots if s is not None)
     return {
         "elapsed": elapsed,
+        "steps": len(records),
         "tokens": tokens,
         "kept_hist": kept_hist,
         "active_at_end": active,
         "max_new": max_new,
+        "stats": speculation_stats(tokens, proposed, accepted),
         "mean_context": sum(sum(c) for c in ctx_per_step) / max(1, sum(len(c) for c in ctx_per_step)),
     }
 
@@ -235,7 +255,7 @@ def run_verify_long(args, torch, steps: int = 10, warmup: int = 2):
         eng.runner.step()
     torch.cuda.synchronize()
     ctx = []
-    tokens = 0
+    tokens = proposed = accepted = 0
     kept_hist: dict[int, int] = {}
     start = time.perf_counter()
     for _ in range(steps):
@@ -244,6 +264,8 @@ def run_verify_long(args, torch, steps: int = 10, warmup: int = 2):
         ctx += [lengths[i] + results[i].num_guesses for i in lengths]
         for r in results.values():
             tokens += len(r.tokens)
+            proposed += r.num_guesses
+            accepted += r.num_kept
             kept_hist[r.num_kept] = kept_hist.get(r.num_kept, 0) + 1
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
@@ -259,6 +281,7 @@ def run_verify_long(args, torch, steps: int = 10, warmup: int = 2):
         "prefill_s": round(prefill_s, 2),
         "active_at_end": sum(1 for s in eng.runner.slots if s is not None),
         "accepted_per_step_hist": {str(k): v for k, v in sorted(kept_hist.items())},
+        **speculation_stats(tokens, proposed, accepted),
         "hip_graph": bool(args.graph),
     }
     del eng
@@ -1019,7 +1042,8 @@ def main() -> int:
         s_step_us = 1e6 * s_res["elapsed"] / 10
         sampled = {"temperature": 0.8, "steps": 10, "verify_step_us": round(s_step_us, 1),
                    "accepted_tok_s": round(s_res["tokens"] / s_res["elapsed"], 1),
-                   "accepted_per_step_hist": {str(k): v for k, v in sorted(s_res["kept_hist"].items())}}
+                   "accepted_per_step_hist": {str(k): v for k, v in sorted(s_res["kept_hist"].items())},
+                   **s_res["stats"]}
         log(f"sampled: {sampled['verify_step_us']} us per step")
     draft_verify = None
     if args.only in ("all", "draft"):
@@ -1030,8 +1054,23 @@ def main() -> int:
                                     "the target's weights as the draft), 64 seqs, k=4, greedy, int8 W + KV",
                         "steps": 10, "verify_step_us": round(d_step_us, 1),
                         "accepted_tok_s": round(d_res["tokens"] / d_res["elapsed"], 1),
-                        "accepted_per_step_hist": {str(k): v for k, v in sorted(d_res["kept_hist"].items())}}
+                        "accepted_per_step_hist": {str(k): v for k, v in sorted(d_res["kept_hist"].items())},
+                        **d_res["stats"]}
         log(f"draft-model verify: {draft_verify['verify_step_us']} us per step")
+    full_generation = None
+    if args.only in ("all", "verify"):
+        # the whole 128-token generation, first verify step to last, so that the later,
+        # longer-context steps (and the shrinking batch at the end) are measured too
+        f_res = run_verify(args, torch, warmup=0, to_completion=True)
+        full_generation = {
+            "workload": "64 seqs x 64-token motif prompts, 128 output tokens each, every verify step from the "
+                        "first until all sequences finished, n-gram k=4, greedy, int8 W + int8 paged KV",
+            "steps": f_res["steps"], "verify_step_us_mean": round(1e6 * f_res["elapsed"] / max(f_res["steps"], 1), 1),
+            "accepted_tok_s": round(f_res["tokens"] / f_res["elapsed"], 1), "tokens": f_res["tokens"],
+            "mean_context": round(f_res["mean_context"], 1),
+            "accepted_per_step_hist": {str(k): v for k, v in sorted(f_res["kept_hist"].items())},
+            **f_res["stats"]}
+        log(f"full generation: {full_generation['steps']} steps, {full_generation['accepted_tok_s']} tok/s")
     long_verify = None
     if args.only in ("all", "long"):
         long_verify = run_verify_long(args, torch)
@@ -1071,6 +1110,8 @@ def main() -> int:
                    "global_batch": NUM_SEQS, "seq_len": PROMPT_MOTIF * PROMPT_REPEATS, "parallelism": "single GPU",
                    "hip_graph": bool(args.graph)},
         "accepted_per_step_hist": {str(k): v for k, v in sorted(res["kept_hist"].items())},
+        **res["stats"],
+        "full_generation": full_generation,
         "roofline": attention,
         "gemm": gemm,
         "sampled": sampled,
