@@ -295,6 +295,8 @@ class AttentionWorkload:
 
     int8: 64 seqs, ctx U{128..1024} (seed 1), 5 queries, fp16 scales, 4096-block pool.
     bf16: 16 seqs, ctx U{256..2048} (seed 1), 5 queries, Q/K/V ~ N(0, 1), 4096-block pool.
+    bf16_step: 64 seqs, ctx U{64..192} (seed 2), 5 queries: a verify step's contexts on a
+          bf16 pool.
     long: 32 seqs sharing a 1024-token prefix (the same 64 blocks at the head of every
           table), then a suffix of U{4096..16384} tokens (seed 1); 9 queries (k = 8),
           int8 KV with bf16 scales."""
@@ -314,6 +316,9 @@ class AttentionWorkload:
             self.ql = 5
         elif kind == "bf16":
             self.ctx = rng.integers(256, 2049, size=16).astype(np.int32)
+            self.ql = 5
+        elif kind == "bf16_step":
+            self.ctx = np.random.default_rng(2).integers(64, 193, size=NUM_SEQS).astype(np.int32)
             self.ql = 5
         else:
             shared = 1024
@@ -335,7 +340,7 @@ class AttentionWorkload:
         slots = blocks * bs + 1
         self.pools = []
         for _ in range(layers):
-            if kind == "bf16":
+            if kind.startswith("bf16"):
                 kc = torch.randn(slots, hkv, 128, device=dev).to(torch.bfloat16)
                 vc = torch.randn(slots, hkv, 128, device=dev).to(torch.bfloat16)
                 self.pools.append((kc, vc, None, None))
@@ -354,9 +359,11 @@ class AttentionWorkload:
         self.q_start = torch.arange(b, dtype=torch.int32, device=dev) * self.ql
         self.q_len = torch.full((b,), self.ql, dtype=torch.int32, device=dev)
         self.ws = kernels.AttentionWorkspace()
-        int8 = kind != "bf16"
+        int8 = not kind.startswith("bf16")
         self.bytes_per_launch = attention_bytes(self.ctx.tolist(), self.rows, int8=int8) + tables.numel() * 4
-        self.plannable = kind == "int8"
+        pool = self.pools[0]
+        self.plannable = kernels.plan_supported(hq, hkv, self.ql, b, pool[0].dtype,
+                                                None if pool[2] is None else pool[2].dtype)
         self._kernels = kernels
 
     def plan(self) -> None:
@@ -369,38 +376,85 @@ class AttentionWorkload:
             self.q, pool[0], pool[1], pool[2], pool[3], self.tables, 16, self.ctx_d, self.q_start,
             self.q_len, self.ql, int(self.ctx.max()), out=self.out, workspace=self.ws, planned=planned)
 
+    def stream(self, pool) -> None:
+        """The planned call's K/V reads alone, on the current plan (the memory ceiling)."""
+        self._kernels.paged_kv_stream_planned(pool[0], pool[1], pool[2], pool[3], len(self.ctx), 16, self.ql,
+                                              int(self.ctx.max()), self.ws)
+
+
+def stream_ceiling(torch, w: AttentionWorkload, reps: int) -> dict:
+    """Time per call of the planned call's K/V streamed alone (ne_paged_kv_stream_planned,
+    same plan, tiles, ring and copies, no arithmetic) over the same pools, from HIP events
+    on the launching stream: what the access pattern costs the memory system."""
+    from nanoengine_amd import _native
+
+    w.plan()
+    for p in w.pools:
+        w.stream(p)
+    torch.cuda.synchronize()
+    timer = _native.LaunchTimer()
+    _native.set_launch_timer("ne_paged_kv_stream_planned", timer)
+    for _ in range(reps):
+        for p in w.pools:
+            w.stream(p)
+    torch.cuda.synchronize()
+    _native.set_launch_timer("ne_paged_kv_stream_planned", None)
+    dur = timer.durations_ms()
+    us = 1e3 * sum(dur) / len(dur)
+    kv_bytes = attention_bytes(w.ctx.tolist(), 0, int8=w.pools[0][2] is not None)
+    return {"us": round(us, 2), "kv_bytes": int(kv_bytes), "GB_s": round(kv_bytes / us / 1e3, 1),
+            "frac_of_peak": round(kv_bytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
 
 ATTENTION_WORKLOADS = {
     "bf16": "bf16 KV, 16 seqs, ctx U{256..2048} seed 1, q=5, Q/K/V N(0,1), 4096-block pool",
+    "bf16_step": "bf16 KV, 64 seqs, ctx U{64..192} seed 2, q=5 (a verify step's contexts), 4096-block pool",
     "long": "int8 KV (bf16 scales), 32 seqs sharing a 1024-token prefix + U{4096..16384} suffix seed 1, "
             "q=9 (k=8)",
 }
 
 
 def run_attention_kernel_only(torch, kind: str, layers: int, reps: int = 3):
-    """Average time per unplanned attention call (HIP events around each call) for the bf16
-    and long-context workloads."""
+    """Average time per attention call (HIP events around each call on its stream) for the
+    bf16 and long-context workloads: the planned call a step makes (the plan's time spread
+    over its pass of `layers` calls), and the entry point that plans inside the kernel."""
     from nanoengine_amd import _native
 
     w = AttentionWorkload(torch, layers=layers, kind=kind)
     for p in w.pools:
         w.launch(p)
     torch.cuda.synchronize()
-    timer = _native.LaunchTimer()
-    _native.set_launch_timer("ne_paged_verify_attention", timer)
+    timers = {name: _native.LaunchTimer() for name in
+              ("ne_paged_attention_plan", "ne_paged_verify_attention_planned", "ne_paged_verify_attention")}
+    for name, t in timers.items():
+        _native.set_launch_timer(name, t)
     for _ in range(reps):
         for p in w.pools:
             w.launch(p)
+    if w.plannable:
+        for _ in range(reps):
+            w.plan()
+            for p in w.pools:
+                w.launch(p, planned=True)
     torch.cuda.synchronize()
-    _native.set_launch_timer("ne_paged_verify_attention", None)
+    for name in timers:
+        _native.set_launch_timer(name, None)
     if w.ws.error_flag() != 0:
         raise RuntimeError(f"{kind} attention workload raised the workspace error flag (keys dropped)")
-    dur = timer.durations_ms()
-    avg_ms = sum(dur) / len(dur)
+    unplanned = timers["ne_paged_verify_attention"].durations_ms()
+    unplanned_ms = sum(unplanned) / len(unplanned)
+    avg_ms = unplanned_ms
+    ceiling = None
+    if w.plannable:
+        calls = timers["ne_paged_verify_attention_planned"].durations_ms()
+        avg_ms = (sum(timers["ne_paged_attention_plan"].durations_ms()) + sum(calls)) / len(calls)
+        ceiling = stream_ceiling(torch, w, reps)
     achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
     out = {"workload": ATTENTION_WORKLOADS[kind], "achieved": round(achieved, 1), "unit": "GB/s",
            "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
-           "bytes_per_launch": int(w.bytes_per_launch), "sum_ctx": int(w.ctx.sum()), "launches": len(dur)}
+           "call": "plan + planned" if w.plannable else "unplanned",
+           "unplanned_avg_us": round(unplanned_ms * 1e3, 2), "kv_stream_ceiling": ceiling,
+           "bytes_per_launch": int(w.bytes_per_launch), "sum_ctx": int(w.ctx.sum()), "launches": len(unplanned)}
     del w
     torch.cuda.empty_cache()
     return out
@@ -443,6 +497,7 @@ def run_attention_roofline(torch, reps: int = 5):
     avg_ms = (plan_ms + sum(calls)) / len(calls)
     unplanned = timers["ne_paged_verify_attention"].durations_ms()
     achieved = w.bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    ceiling = stream_ceiling(torch, w, reps)
     return {"kernel": "paged_attention_dma_kernel<fp16 scales, planned> (whole-sequence items, 4 work-groups "
                       "per sequence, no merge kernel at this shape)",
             "workload": "int8 KV, 64 seqs, ctx U{128..1024} seed 1, q=5, fp16 scales, 28 pools",
@@ -450,6 +505,7 @@ def run_attention_roofline(torch, reps: int = 5):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(avg_ms * 1e3, 2),
             "plan_us": round(plan_ms * 1e3 / reps, 2),
             "unplanned_avg_us": round(1e3 * sum(unplanned) / len(unplanned), 2),
+            "kv_stream_ceiling": ceiling,
             "bytes_per_launch": int(w.bytes_per_launch), "launches": len(calls),
             "sum_ctx": int(w.ctx.sum())}
 
@@ -1022,6 +1078,8 @@ def main() -> int:
         log(f"attention: {attention['avg_us']} us, {attention['achieved']} GB/s")
         attention["bf16_config"] = run_attention_kernel_only(torch, "bf16", layers=28)
         log(f"attention bf16: {attention['bf16_config']['avg_us']} us")
+        attention["bf16_step_config"] = run_attention_kernel_only(torch, "bf16_step", layers=28)
+        log(f"attention bf16 at step contexts: {attention['bf16_step_config']['avg_us']} us")
         attention["long_context_config"] = run_attention_kernel_only(torch, "long", layers=8)
         log(f"attention long context: {attention['long_context_config']['avg_us']} us")
     gemm = None

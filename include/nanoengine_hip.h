@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 7
+#define NE_ABI_VERSION 8
 
 /* status codes */
 #define NE_OK 0
@@ -155,10 +155,11 @@ int ne_paged_verify_attention_noalloc(
  * exactly ne_paged_verify_attention's arguments and reads that plan instead of
  * deriving it, which saves one dependent memory round trip per call.  Valid while
  * ctx_len, q_start, q_len, block_tables, num_seqs, max_q_len, max_ctx_len and
- * split_len stay as they were for the plan (a verify step's layers).  Both serve int8
- * caches with 8 KV heads, 2-byte scales and at most 32 query rows per KV head
- * (num_q_heads / num_kv_heads * max_q_len <= 32, i.e. up to k = 15 drafts) and return
- * NE_EUNSUPPORTED otherwise; the workspace size is ne_paged_attention_workspace_size()'s.
+ * split_len stay as they were for the plan (a verify step's layers).  Both serve caches
+ * with 8 KV heads and at most 32 query rows per KV head (num_q_heads / num_kv_heads *
+ * max_q_len <= 32, i.e. up to k = 15 drafts), bf16 or int8 with 2-byte scales, and return
+ * NE_EUNSUPPORTED otherwise; the workspace size is ne_paged_attention_workspace_size()'s
+ * and its layout does not depend on the cache dtype.
  */
 int ne_paged_attention_plan(const int32_t* block_tables, int32_t block_table_stride,
                             int32_t block_size, const int32_t* ctx_len, const int32_t* q_start,
@@ -175,6 +176,19 @@ int ne_paged_verify_attention_planned(
     int32_t max_q_len, int32_t max_ctx_len, float softmax_scale, void* out,
     int64_t out_token_stride, int64_t out_head_stride, int32_t split_len, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* Measurement entry point, no counterpart in the reference: the K/V (and scale) reads of
+ * ne_paged_verify_attention_planned alone.  It follows the plan that
+ * ne_paged_attention_plan wrote into `workspace` for the same metadata, gives every wave
+ * the same tiles and streams them through the same LDS ring with the same copies, and
+ * computes and stores nothing.  Its time is what the planned call's access pattern costs
+ * the memory system: the ceiling that call is measured against (bench.py).  Same shapes
+ * as the planned call; NE_EUNSUPPORTED otherwise. */
+int ne_paged_kv_stream_planned(const void* k_cache, const void* v_cache, const void* k_scale,
+                               const void* v_scale, int32_t kv_dtype, int32_t scale_dtype,
+                               int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t max_q_len, int32_t max_ctx_len, int32_t split_len,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * A8 - W8A16 projection: y[m, n] = bf16(sum_k x[m, k] * w[n, k] * scale[n])

@@ -796,14 +796,16 @@ __global__ __launch_bounds__(kHeadWaves * KG * kWave) void paged_attention_kerne
   }
 }
 
-// ---- DMA-fed variant (int8 cache, 8 KV heads, 2-byte scales) -----------------
+// ---- DMA-fed variant (8 KV heads; int8 cache with 2-byte scales, or bf16) ---------
 // Same work item as paged_attention_kernel, but each wave (one KV head) streams its
 // head's rows of every 16-key tile, plus all heads' scales of the tile, from HBM
 // straight into its own LDS ring with global_load_lds: no registers hold data in
 // flight, so every wave keeps kDmaRing tiles (18 KB) on the way while it computes,
 // and the loop needs no block barrier.  The scores run on the int8 MFMA with the K
 // codes as they sit in LDS and Q in two int8 planes (quantize_q_row); P V stays on
-// the fp16 MFMA.
+// the fp16 MFMA.  A bf16 cache has twice the bytes per tile (8 KB for a head's K and V
+// of 16 keys, no scales), so its ring holds two tiles per wave (the next iteration's,
+// 128 KB per work-group) and the scores and P V run on the bf16 MFMA.
 constexpr int kDmaRing = 4;                          // 16-key tiles in flight per wave
 constexpr int kRowBytes = kHeadDim;                  // one int8 head row
 constexpr int kTileRows = kTileKeys * kRowBytes;     // 2 KB: one head's K (or V) rows of a tile
@@ -815,20 +817,28 @@ constexpr int kMaxRowTiles = 2;                      // row tiles per KV head in
 constexpr int kPartRows = kRows * kMaxRowTiles;      // rows per (work-group, KV head) partial
 constexpr int kPlanMaxSeqs = 2 * kHeadWaves * kWave;  // two sequences per thread
 
-// Work-group shape of the DMA kernel by KS, the waves per KV head: waves per
-// work-group, KV heads per work-group, work-groups per work item, ring tiles per wave
-// and the dynamic LDS layout (rings, slot list, per-wave scales, plan).
-template <int KS>
+constexpr int kBfRowBytes = kHeadDim * 2;                // one bf16 head row
+constexpr int kBfTileRows = kTileKeys * kBfRowBytes;      // 4 KB: one head's K (or V) rows of a tile
+constexpr int kBfDmaSlot = 2 * kBfTileRows;               // K | V
+constexpr int kBfDmaPerTile = 8;                          // 4 K + 4 V copies of 1 KB
+
+// Work-group shape of the DMA kernel by KS, the waves per KV head, and the cache dtype:
+// waves per work-group, KV heads per work-group, work-groups per work item, ring tiles
+// per wave, the ring slot's bytes and copies, and the dynamic LDS layout (rings, slot
+// list, per-wave scales, plan).
+template <int KS, bool BF16 = false>
 struct DmaShape {
   static constexpr int waves = kHeadWaves;
   static constexpr int heads = waves / KS;               // KV heads per work-group
   static constexpr int groups = kHeadWaves / heads;      // work-groups per work item
-  static constexpr int ring = kDmaRing;                  // tiles in flight per wave
+  static constexpr int ring = BF16 ? 2 : kDmaRing;       // tiles in flight per wave
+  static constexpr int slot_bytes = BF16 ? kBfDmaSlot : kDmaSlot;
+  static constexpr int per_tile = BF16 ? kBfDmaPerTile : kDmaPerTile;  // copies per tile
   // tiles issued before the first iteration; the rest of the ring follows once the
   // first two have landed, which keeps the launch's opening burst of copies (and the
   // queueing delay every wave's first tiles see behind it) at half the ring
   static constexpr int first = 2;
-  static constexpr int slot_off = waves * ring * kDmaSlot;
+  static constexpr int slot_off = waves * ring * slot_bytes;
   static constexpr int sc_off = slot_off + kPlanMaxTiles * 4;
   static constexpr int plan_off = sc_off + waves * kWave * 4;
   static constexpr int lds = plan_off + kPlanInts * 4;
@@ -1128,6 +1138,151 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
   R.sc = (!MASK || kb + kk < kend) ? s : 0.f;
 }
 
+// bf16 cache: copy j of a head's K (or V) tile brings keys 4j .. 4j + 3, 256 B each,
+// with 16-byte chunk c of key k stored at chunk position c ^ k (k < 16), which makes the
+// fragment reads below conflict-free.  Offsets are 32-bit from a wave-uniform base, as
+// for the int8 tiles.
+struct DmaLaneBf {
+  uint32_t kv[4];  // copy j: key 4j + lane / 16, chunk (lane % 16) ^ key
+};
+
+__device__ __forceinline__ DmaLaneBf dma_lane_bf(int lane) {
+  constexpr uint32_t slot_bytes = kHeadWaves * kBfRowBytes;
+  DmaLaneBf d;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int key = 4 * j + (lane >> 4);
+    const int chunk = (lane & 15) ^ key;
+    d.kv[j] = (uint32_t)key * slot_bytes + (uint32_t)chunk * 16u;
+  }
+  return d;
+}
+
+// Copy tile `t` (clamped to the split's last tile) of head `head` of a bf16 cache into
+// ring slot `dst`: K rows, then V rows, 4 KB each.
+__device__ __forceinline__ void dma_tile_bf(const AttnParams& p, const int* s_slot, int n_tiles, int t, int head,
+                                            const DmaLaneBf& dl, char* dst) {
+  const int ti = min(t, n_tiles - 1);
+  const int64_t slot0 = __builtin_amdgcn_readfirstlane(s_slot[ti]);
+  const int64_t slot_bytes = (int64_t)kHeadWaves * kBfRowBytes;
+  const char* kbase = (const char*)p.k_cache + slot0 * slot_bytes + head * kBfRowBytes;
+  const char* vbase = (const char*)p.v_cache + slot0 * slot_bytes + head * kBfRowBytes;
+  uint32_t o0 = dl.kv[0], o1 = dl.kv[1], o2 = dl.kv[2], o3 = dl.kv[3];
+  __asm__("" : "+v"(o0), "+v"(o1), "+v"(o2), "+v"(o3));
+  lds_dma(kbase + o0, dst, 16);
+  lds_dma(vbase + o0, dst + kBfTileRows, 16);
+  lds_dma(kbase + o1, dst + 1024, 16);
+  lds_dma(vbase + o1, dst + kBfTileRows + 1024, 16);
+  lds_dma(kbase + o2, dst + 2048, 16);
+  lds_dma(vbase + o2, dst + kBfTileRows + 2048, 16);
+  lds_dma(kbase + o3, dst + 3072, 16);
+  lds_dma(vbase + o3, dst + kBfTileRows + 3072, 16);
+}
+
+// Registers of one 32-key iteration of a bf16 cache from two ring slots: k[t][c] holds
+// dims 32 g + 8 c .. + 8 of key r (the layout of the Q fragments), v[4 t + i] dims
+// 8 r .. + 8 of key 16 t + 4 g + i (the layout compute_iter_bf transposes for P V).
+__device__ __forceinline__ void lds_iter_bf(const char* slot_a, const char* slot_b, int lane,
+                                            IterRegs<false>& R) {
+  const int r = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const char* sl = t ? slot_b : slot_a;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) R.k[t][c] = *(const u32x4*)(sl + r * kBfRowBytes + (((4 * g + c) ^ r) * 16));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 4 * g + i;
+      R.v[4 * t + i] = *(const u32x4*)(sl + kBfTileRows + key * kBfRowBytes + ((r ^ key) * 16));
+    }
+  }
+}
+
+// One 32-key iteration of a bf16 cache for MT row tiles: scores on the bf16 MFMA, the
+// lazy online softmax, P V on the bf16 MFMA (the register kernel's arithmetic, each K
+// and V operand feeding every row tile).  MASK: keys at or past a row's end are masked,
+// and the V rows of keys at or past kend (where a partial or clamped tile holds other or
+// stale slots) are zeroed, so that 0 * NaN cannot reach the product.
+template <int MT, bool MASK>
+__device__ __forceinline__ void compute_iter_bf(const IterRegs<false>& R, const QFrag<false> (&qf)[MT],
+                                                float qk_scale, int kb, int kend, const int (&kend_row)[MT],
+                                                int lane, float (&m)[MT], float (&l)[MT],
+                                                floatx4 (&o)[MT][8]) {
+  const int g = lane >> 4;
+  // ---- S^T = K . Q^T: two 16x16 tiles (keys x rows) per row tile ----
+  floatx4 s[MT][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) s[mt][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 a = __builtin_bit_cast(bf16x8, R.k[t][c]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        s[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[mt].q[c], s[mt][t], 0, 0, 0);
+    }
+  }
+  // ---- masked scores, lazy online softmax, P (row = lane % 16) ----
+  bf16x8 pb[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    float sc[8];
+    float mx = kNegBig;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = s[mt][t][i] * qk_scale;
+        if constexpr (MASK) v = (kb + 16 * t + 4 * g + i < kend_row[mt]) ? v : kNegBig;
+        sc[4 * t + i] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+    if (__ballot(mx > m[mt] + kLazyLog2)) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m[mt], mx);
+      const float alpha = __builtin_amdgcn_exp2f(m[mt] - m_new);
+      l[mt] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[mt][j] *= alpha;
+      m[mt] = m_new;
+    }
+    float pr[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pr[e] = __builtin_amdgcn_exp2f(sc[e] - m[mt]);
+      if constexpr (MASK) pr[e] = (kb + 16 * (e >> 2) + 4 * g + (e & 3) < kend_row[mt]) ? pr[e] : 0.f;
+      psum += pr[e];
+    }
+    l[mt] += psum;
+    const u32x4 pb_bits = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
+                           pack_bf16x2(pr[6], pr[7])};
+    pb[mt] = __builtin_bit_cast(bf16x8, pb_bits);
+  }
+  // ---- O^T += V^T . P^T: eight 16x16 tiles (dims x rows) per row tile ----
+  u32x4 vz[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int key = kb + 16 * (e >> 2) + 4 * g + (e & 3);
+    vz[e] = (MASK && key >= kend) ? u32x4{0, 0, 0, 0} : R.v[e];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = j >> 1;
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    const u32x4 abits = {__builtin_amdgcn_perm(vz[1][w], vz[0][w], sel), __builtin_amdgcn_perm(vz[3][w], vz[2][w], sel),
+                         __builtin_amdgcn_perm(vz[5][w], vz[4][w], sel), __builtin_amdgcn_perm(vz[7][w], vz[6][w], sel)};
+    const bf16x8 a = __builtin_bit_cast(bf16x8, abits);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      o[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[mt], o[mt][j], 0, 0, 0);
+  }
+}
+
 // PLANNED: the work item and the split's slots come from attention_plan_kernel's
 // output instead of being derived here (one round trip instead of two).
 // MT: row tiles of 16 per KV head handled by each wave (1, or 2 for up to 32 rows).
@@ -1136,10 +1291,11 @@ __device__ __forceinline__ void lds_iter(const char* slot_a, const char* slot_b,
 // item, each taking 8 / KS heads, and a head's KS waves take consecutive parts of the
 // item's tiles, their (m, l, O) merged through LDS before the store -- so that short
 // contexts fill KS times as many CUs without a merge kernel.
-template <int SDT, bool PLANNED, int MT, int KS = 1>
-__global__ __launch_bounds__(DmaShape<KS>::waves * kWave) void paged_attention_dma_kernel(AttnParams p) {
+// BF16: a bf16 cache (SDT unused): two-tile rings, bf16 MFMA scores (compute_iter_bf).
+template <int SDT, bool PLANNED, int MT, int KS = 1, bool BF16 = false>
+__global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_attention_dma_kernel(AttnParams p) {
   static_assert(KS == 1 || (PLANNED && MT == 1), "head split: planned, one row tile");
-  using Shape = DmaShape<KS>;
+  using Shape = DmaShape<KS, BF16>;
   constexpr int HG = Shape::heads;  // KV heads per work-group
   constexpr int RING = Shape::ring;
   constexpr int FIRST = Shape::first;
@@ -1260,21 +1416,42 @@ __global__ __launch_bounds__(DmaShape<KS>::waves * kWave) void paged_attention_d
   }
   __syncthreads();  // s_slot ready
 
-  char* ring = smem + wave * (RING * kDmaSlot);
+  constexpr int kSlot = Shape::slot_bytes;
+  constexpr int kPerTile = Shape::per_tile;
+  char* ring = smem + wave * (RING * kSlot);
   const int* w_slot = s_slot + (jw0 - j0);  // this wave's tiles in the item's slot list
   const DmaLane dl = dma_lane(lane);
+  const DmaLaneBf dlb = dma_lane_bf(lane);
+  auto copy_tile = [&](int t, char* dst) {
+    if constexpr (BF16) {
+      dma_tile_bf(p, w_slot, n_tiles, t, head, dlb, dst);
+    } else {
+      dma_tile(p, w_slot, n_tiles, t, head, dl, dst);
+    }
+  };
   if (n_tiles > 0) {
 #pragma unroll
-    for (int j = 0; j < FIRST; ++j) dma_tile(p, w_slot, n_tiles, j, head, dl, ring + j * kDmaSlot);
+    for (int j = 0; j < FIRST; ++j) copy_tile(j, ring + j * kSlot);
     // Q was issued before the ring's copies: wait for it alone (the compiler's own wait
     // would also drain the copies, since it does not order them after the Q loads)
-    dma_wait_vmcnt<kDmaPerTile * FIRST>();
+    dma_wait_vmcnt<kPerTile * FIRST>();
   } else {
     dma_wait_vmcnt<0>();  // a wave with no tiles of the item (KS > 1) only loads Q
   }
-  QFragI8 qf[MT];
+  // Q of a row tile: two int8 planes for the int8 scores, or the bf16 rows as they are
+  // (an invalid row zeroed)
+  using QF = std::conditional_t<BF16, QFrag<false>, QFragI8>;
+  QF qf[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) quantize_q_row(raw[mt], row_valid[mt], p.qk_scale, qf[mt]);
+  for (int mt = 0; mt < MT; ++mt) {
+    if constexpr (BF16) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        qf[mt].q[c] = __builtin_bit_cast(bf16x8, row_valid[mt] ? raw[mt][c] : u32x4{0, 0, 0, 0});
+    } else {
+      quantize_q_row(raw[mt], row_valid[mt], p.qk_scale, qf[mt]);
+    }
+  }
 
   float m[MT], l[MT];
   floatx4 o[MT][8];
@@ -1294,24 +1471,33 @@ __global__ __launch_bounds__(DmaShape<KS>::waves * kWave) void paged_attention_d
   auto iteration = [&](int it, auto mask, auto first) {
     constexpr bool kMask = decltype(mask)::value;
     constexpr bool kFirst = decltype(first)::value;
-    // this wave's DMA of tiles 2it, 2it+1 has landed once at most the two tiles
-    // issued after them are still in flight (none before the first iteration)
-    dma_wait_vmcnt<kFirst ? kDmaPerTile * (FIRST - 2) : kDmaPerTile * (RING - 2)>();
-    const char* sa = ring + ((2 * it) % RING) * kDmaSlot;
-    const char* sb = ring + ((2 * it + 1) % RING) * kDmaSlot;
+    // this wave's DMA of tiles 2it, 2it+1 has landed once at most the tiles issued
+    // after them are still in flight (none before the first iteration, and none with a
+    // two-tile ring)
+    dma_wait_vmcnt<kFirst ? kPerTile * (FIRST - 2) : kPerTile * (RING - 2)>();
+    const char* sa = ring + ((2 * it) % RING) * kSlot;
+    const char* sb = ring + ((2 * it + 1) % RING) * kSlot;
     const int kb = kstart + it * kIterKeys;
-    IterRegs<true> A;
-    lds_iter<SDT, kMask>(sa, sb, kb, kend, head, lane, A);
+    IterRegs<!BF16> A;
+    if constexpr (BF16) {
+      lds_iter_bf(sa, sb, lane, A);
+    } else {
+      lds_iter<SDT, kMask>(sa, sb, kb, kend, head, lane, A);
+    }
     // the two slots are free once their reads have returned: refill them before the
-    // arithmetic, so that each copy has two iterations to land
+    // arithmetic, so that each copy has the next iterations to land
     dma_wait_lgkmcnt0();
     if constexpr (kFirst) {
 #pragma unroll
-      for (int j = FIRST; j < RING; ++j) dma_tile(p, w_slot, n_tiles, j, head, dl, ring + j * kDmaSlot);
+      for (int j = FIRST; j < RING; ++j) copy_tile(j, ring + j * kSlot);
     }
-    dma_tile(p, w_slot, n_tiles, 2 * it + RING, head, dl, ring + ((2 * it) % RING) * kDmaSlot);
-    dma_tile(p, w_slot, n_tiles, 2 * it + 1 + RING, head, dl, ring + ((2 * it + 1) % RING) * kDmaSlot);
-    compute_iter_q8<MT, kMask>(A, qf, sc_row, kb, kend_row, lane, m, l, o);
+    copy_tile(2 * it + RING, ring + ((2 * it) % RING) * kSlot);
+    copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
+    if constexpr (BF16) {
+      compute_iter_bf<MT, kMask>(A, qf, p.qk_scale, kb, kend, kend_row, lane, m, l, o);
+    } else {
+      compute_iter_q8<MT, kMask>(A, qf, sc_row, kb, kend_row, lane, m, l, o);
+    }
   };
   int it = 0;
   if (n_iter > 0) {
@@ -1398,6 +1584,73 @@ __global__ __launch_bounds__(DmaShape<KS>::waves * kWave) void paged_attention_d
       }
     }
   }
+}
+
+// Measurement kernel: the planned attention's K/V (and scale) traffic alone.  It takes
+// the same work items from the plan, gives each wave the same tiles, and streams them
+// through the same LDS ring with the same copies and waits, but computes nothing and
+// stores nothing: its time is what this access pattern costs the memory system, the
+// ceiling the attention kernel is measured against.
+template <int KS, bool BF16>
+__global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_kv_stream_kernel(AttnParams p) {
+  using Shape = DmaShape<KS, BF16>;
+  constexpr int HG = Shape::heads;
+  constexpr int RING = Shape::ring;
+  constexpr int FIRST = Shape::first;
+  constexpr int kSlot = Shape::slot_bytes;
+  constexpr int kPerTile = Shape::per_tile;
+  constexpr int kThreads = Shape::waves * kWave;
+  static_assert(kPlanMaxTiles == kThreads, "one slot per thread");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* s_slot = (int*)(smem + Shape::slot_off);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int widx = (int)blockIdx.x / Shape::groups;
+  const int head = ((int)blockIdx.x % Shape::groups) * HG + wave % HG;
+  const int ks = wave / HG;
+  const int32_t my_slot = p.plan_slots[(int64_t)widx * kPlanMaxTiles + tid];
+  const ConstI32* d = (const ConstI32*)(p.plan_desc + (int64_t)widx * kDescInts);
+  const int seq = d[0], split = d[1], n_splits = d[2], j0 = d[3], ctx = d[4], j1 = d[7];
+  const bool sane = seq < p.num_seqs && n_splits >= 1 && split >= 0 && split < n_splits && ctx > 0 &&
+                    ctx <= p.max_ctx && j0 >= 0 && j0 < j1 && j1 - j0 <= kPlanMaxTiles &&
+                    (j1 - 1) * kTileKeys < ctx;
+  if (seq < 0 || !sane) {
+    if (seq >= 0 && tid == 0) atomicOr(p.error_flag, 2u);
+    return;
+  }
+  s_slot[tid] = my_slot;
+  __syncthreads();
+  const int jw0 = __builtin_amdgcn_readfirstlane(j0 + (j1 - j0) * ks / KS);
+  const int jw1 = __builtin_amdgcn_readfirstlane(j0 + (j1 - j0) * (ks + 1) / KS);
+  const int n_tiles = jw1 - jw0;
+  if (n_tiles <= 0) return;
+  char* ring = smem + wave * (RING * kSlot);
+  const int* w_slot = s_slot + (jw0 - j0);
+  const DmaLane dl = dma_lane(lane);
+  const DmaLaneBf dlb = dma_lane_bf(lane);
+  auto copy_tile = [&](int t, char* dst) {
+    if constexpr (BF16) {
+      dma_tile_bf(p, w_slot, n_tiles, t, head, dlb, dst);
+    } else {
+      dma_tile(p, w_slot, n_tiles, t, head, dl, dst);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < FIRST; ++j) copy_tile(j, ring + j * kSlot);
+  const int n_iter = (n_tiles + 1) / 2;
+  for (int it = 0; it < n_iter; ++it) {
+    if (it == 0) {
+      dma_wait_vmcnt<kPerTile * (FIRST - 2)>();
+#pragma unroll
+      for (int j = FIRST; j < RING; ++j) copy_tile(j, ring + j * kSlot);
+    } else {
+      dma_wait_vmcnt<kPerTile * (RING - 2)>();
+    }
+    copy_tile(2 * it + RING, ring + ((2 * it) % RING) * kSlot);
+    copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
+  }
+  dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
 }
 
 // Partials of a row requested together by the merge kernels: a split-length plan gives
@@ -1543,11 +1796,19 @@ Layout make_layout(int num_seqs, int num_q_heads, int num_kv_heads, int max_q_le
   // error flag at byte 0, so callers can inspect and clear it without knowing the
   // partial-sum layout that follows
   // the fixed-split kernels index partials by (unit, split); the DMA kernel's plan
-  // by (work-group, KV head) and needs (B + 1) plan entries
-  const bool plan = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && L.mtiles <= kMaxRowTiles;
+  // by (work-group, KV head) and needs (B + 1) plan entries.  The sizes do not depend
+  // on the cache dtype (the partials take room for either dtype's default split), so
+  // the plan that ne_paged_attention_plan writes sits where a planned call of either
+  // dtype reads it.
+  const bool plan = num_kv_heads == kHeadWaves && L.mtiles <= kMaxRowTiles;
   L.plan_grid = plan ? plan_grid(num_seqs, max_ctx, fixed_split) : 0;
   L.plan_w = fixed_split / kTileKeys;
-  size_t parts = (L.max_splits > 1) ? (size_t)L.units * L.max_splits * kRows : 0;
+  int splits_room = L.max_splits;
+  if (fixed_split == 0) {
+    for (int dt : {NE_DTYPE_INT8, NE_DTYPE_BF16})
+      splits_room = max(splits_room, ceil_div(max(max_ctx, 1), default_split_len(dt, max_ctx)));
+  }
+  size_t parts = (splits_room > 1) ? (size_t)L.units * splits_room * kRows : 0;
   const int plan_min_w = fixed_split > 0 ? fixed_split / kTileKeys : kPlanMinTiles;
   const bool plan_splits = ceil_div((int64_t)max(max_ctx, 1), kTileKeys) > plan_min_w;
   if (plan && plan_splits) parts = max(parts, (size_t)L.plan_grid * kHeadWaves * kPartRows);
@@ -1580,48 +1841,68 @@ int launch_attention(const AttnParams& p, int kv_dtype, int scale_dtype, hipStre
   return check_launch("attention_merge_kernel");
 }
 
-// The DMA kernel serves int8 caches with 8 KV heads and 2-byte scales; it needs
-// the attribute for more than the default dynamic LDS once per instantiation.
-template <int SDT, bool PLANNED, int MT, int KS = 1>
+// The DMA kernel serves caches with 8 KV heads: int8 with 2-byte scales, or bf16
+// (BF16); it needs the attribute for more than the default dynamic LDS once per
+// instantiation.
+template <int SDT, bool PLANNED, int MT, int KS = 1, bool BF16 = false>
 int launch_attention_dma_ks(const AttnParams& p, unsigned grid, hipStream_t s) {
-  constexpr int lds = DmaShape<KS>::lds;
+  constexpr int lds = DmaShape<KS, BF16>::lds;
   static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)paged_attention_dma_kernel<SDT, PLANNED, MT, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
-      lds);
+      (const void*)paged_attention_dma_kernel<SDT, PLANNED, MT, KS, BF16>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) {
     set_error("paged_attention_dma_kernel: cannot reserve %d bytes of LDS: %s", lds, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT, KS>), dim3(grid),
-                     dim3(DmaShape<KS>::waves * kWave), lds, s, p);
+  hipLaunchKernelGGL((paged_attention_dma_kernel<SDT, PLANNED, MT, KS, BF16>), dim3(grid),
+                     dim3(DmaShape<KS, BF16>::waves * kWave), lds, s, p);
   return check_launch("paged_attention_dma_kernel");
 }
 
-template <int SDT, bool PLANNED, int MT>
+template <int SDT, bool PLANNED, int MT, bool BF16>
 int launch_attention_dma_mt(const AttnParams& p, hipStream_t s) {
   if constexpr (PLANNED && MT == 1) {
     // whole-sequence items: 4 (or 2) work-groups per sequence, each over 2 (or 4) KV
     // heads, the waves of a head over consecutive parts of its tiles
     if (p.plan_whole) {
       if (whole_plan_ks(p.num_seqs, p.max_ctx, 0, 1) == 4)
-        return launch_attention_dma_ks<SDT, PLANNED, MT, 4>(p, (unsigned)p.num_seqs * DmaShape<4>::groups, s);
-      return launch_attention_dma_ks<SDT, PLANNED, MT, 2>(p, (unsigned)p.num_seqs * DmaShape<2>::groups, s);
+        return launch_attention_dma_ks<SDT, PLANNED, MT, 4, BF16>(p, (unsigned)p.num_seqs * DmaShape<4>::groups, s);
+      return launch_attention_dma_ks<SDT, PLANNED, MT, 2, BF16>(p, (unsigned)p.num_seqs * DmaShape<2>::groups, s);
     }
   }
   // no sequence is split when every context fits in one split's minimum length
   const int min_w = p.plan_w > 0 ? p.plan_w : kPlanMinTiles;
   const bool no_splits = ceil_div(p.max_ctx, kTileKeys) <= min_w;
-  const int rc = launch_attention_dma_ks<SDT, PLANNED, MT>(p, (unsigned)p.plan_grid, s);
+  const int rc = launch_attention_dma_ks<SDT, PLANNED, MT, 1, BF16>(p, (unsigned)p.plan_grid, s);
   if (rc != NE_OK || no_splits) return rc;
   hipLaunchKernelGGL(attention_plan_merge_kernel, dim3((unsigned)p.num_seqs * kHeadWaves),
                      dim3(kPartRows * 16), 0, s, p);
   return check_launch("attention_plan_merge_kernel");
 }
 
-template <int SDT, bool PLANNED>
+template <int SDT, bool PLANNED, bool BF16 = false>
 int launch_attention_dma(const AttnParams& p, hipStream_t s) {
-  return p.mtiles == 1 ? launch_attention_dma_mt<SDT, PLANNED, 1>(p, s)
-                       : launch_attention_dma_mt<SDT, PLANNED, 2>(p, s);
+  return p.mtiles == 1 ? launch_attention_dma_mt<SDT, PLANNED, 1, BF16>(p, s)
+                       : launch_attention_dma_mt<SDT, PLANNED, 2, BF16>(p, s);
+}
+
+// the DMA kernel of a parameter block whose cache dtype and scales it serves
+template <bool PLANNED>
+int launch_attention_dma_for(const AttnParams& p, int32_t kv_dtype, int32_t scale_dtype, hipStream_t s) {
+  if (kv_dtype == NE_DTYPE_BF16) return launch_attention_dma<NE_DTYPE_BF16, PLANNED, true>(p, s);
+  return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, PLANNED>(p, s)
+                                      : launch_attention_dma<NE_DTYPE_FP16, PLANNED>(p, s);
+}
+
+// whether the DMA kernel serves this call: 8 KV heads, at most two row tiles per KV
+// head, at most kPlanMaxSeqs sequences, and a bf16 cache or an int8 one with 2-byte,
+// 4-byte-aligned scales
+bool dma_serves(int32_t kv_dtype, int32_t scale_dtype, int32_t num_kv_heads, int mtiles, int32_t num_seqs,
+                const void* k_scale, const void* v_scale) {
+  if (num_kv_heads != kHeadWaves || mtiles > kMaxRowTiles || num_seqs > kPlanMaxSeqs) return false;
+  if (kv_dtype == NE_DTYPE_BF16) return true;
+  return kv_dtype == NE_DTYPE_INT8 && (scale_dtype == NE_DTYPE_BF16 || scale_dtype == NE_DTYPE_FP16) &&
+         ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
 }
 
 // Validates the arguments and fills the kernel parameters; NE_OK or an error code.
@@ -1738,17 +2019,12 @@ int scratch_for_current_device(void** out) {
 // the unplanned call on a prepared parameter block (shared by both unplanned entry points)
 int run_unplanned(AttnParams& p, int32_t kv_dtype, int32_t scale_dtype, int32_t num_kv_heads,
                   int32_t num_seqs, const void* k_scale, const void* v_scale, hipStream_t stream) {
-  // int8 with 8 KV heads, one M tile and 2-byte scales: the DMA kernel on the
-  // balanced plan.  Other int8 shapes: one wave per KV head, registers
-  // double-buffered (154 VGPRs); bf16: single-buffered (double-buffered it needs
-  // 244 VGPRs).  Both on fixed-length splits.
-  const bool dma_ok = kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles <= kMaxRowTiles &&
-                      num_seqs <= kPlanMaxSeqs && scale_dtype != NE_DTYPE_FP32 &&
-                      ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0;
-  if (dma_ok) {
-    return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, false>(p, stream)
-                                        : launch_attention_dma<NE_DTYPE_FP16, false>(p, stream);
-  }
+  // 8 KV heads, up to two M tiles, bf16 or int8 with 2-byte scales: the DMA kernel on
+  // the balanced plan.  Other int8 shapes: one wave per KV head, registers
+  // double-buffered (154 VGPRs); other bf16 shapes: single-buffered (double-buffered it
+  // needs 244 VGPRs).  Both on fixed-length splits.
+  if (dma_serves(kv_dtype, scale_dtype, num_kv_heads, p.mtiles, num_seqs, k_scale, v_scale))
+    return launch_attention_dma_for<false>(p, kv_dtype, scale_dtype, stream);
   if (kv_dtype == NE_DTYPE_INT8) return launch_attention<1, true>(p, kv_dtype, scale_dtype, stream);
   return launch_attention<1, false>(p, kv_dtype, scale_dtype, stream);
 }
@@ -1897,14 +2173,80 @@ extern "C" int ne_paged_verify_attention_planned(
                              max_q_len, max_ctx_len, softmax_scale, out, out_token_stride,
                              out_head_stride, split_len, workspace, workspace_bytes, p);
   if (rc != NE_OK) return rc;
-  NE_CHECK_SUPPORTED(kv_dtype == NE_DTYPE_INT8 && num_kv_heads == kHeadWaves && p.mtiles <= kMaxRowTiles &&
-                         num_seqs <= kPlanMaxSeqs &&
-                         (scale_dtype == NE_DTYPE_BF16 || scale_dtype == NE_DTYPE_FP16) &&
-                         ((uintptr_t)k_scale % 4) == 0 && ((uintptr_t)v_scale % 4) == 0,
-                     "the planned path serves int8 caches with 8 KV heads, 2-byte 4-byte-aligned "
-                     "scales and at most 32 query rows per KV head");
+  NE_CHECK_SUPPORTED(dma_serves(kv_dtype, scale_dtype, num_kv_heads, p.mtiles, num_seqs, k_scale, v_scale),
+                     "the planned path serves 8 KV heads, at most 32 query rows per KV head and %d "
+                     "sequences, and bf16 caches or int8 ones with 2-byte 4-byte-aligned scales",
+                     kPlanMaxSeqs);
   // the same choice as ne_paged_attention_plan made from the same metadata
   p.plan_whole = whole_plan_ks(num_seqs, max_ctx_len, split_len, p.mtiles) > 0;
-  return scale_dtype == NE_DTYPE_BF16 ? launch_attention_dma<NE_DTYPE_BF16, true>(p, (hipStream_t)stream)
-                                      : launch_attention_dma<NE_DTYPE_FP16, true>(p, (hipStream_t)stream);
+  return launch_attention_dma_for<true>(p, kv_dtype, scale_dtype, (hipStream_t)stream);
+}
+
+namespace ne {
+namespace {
+template <int KS, bool BF16>
+int launch_kv_stream_ks(const AttnParams& p, unsigned grid, hipStream_t s) {
+  constexpr int lds = DmaShape<KS, BF16>::lds;
+  static const hipError_t attr = hipFuncSetAttribute((const void*)paged_kv_stream_kernel<KS, BF16>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) {
+    set_error("paged_kv_stream_kernel: cannot reserve %d bytes of LDS: %s", lds, hipGetErrorString(attr));
+    return NE_ELAUNCH;
+  }
+  hipLaunchKernelGGL((paged_kv_stream_kernel<KS, BF16>), dim3(grid), dim3(DmaShape<KS, BF16>::waves * kWave), lds,
+                     s, p);
+  return check_launch("paged_kv_stream_kernel");
+}
+
+template <bool BF16>
+int launch_kv_stream(const AttnParams& p, hipStream_t s) {
+  if (p.plan_whole) {
+    if (whole_plan_ks(p.num_seqs, p.max_ctx, 0, 1) == 4)
+      return launch_kv_stream_ks<4, BF16>(p, (unsigned)p.num_seqs * DmaShape<4>::groups, s);
+    return launch_kv_stream_ks<2, BF16>(p, (unsigned)p.num_seqs * DmaShape<2>::groups, s);
+  }
+  return launch_kv_stream_ks<1, BF16>(p, (unsigned)p.plan_grid, s);
+}
+}  // namespace
+}  // namespace ne
+
+extern "C" int ne_paged_kv_stream_planned(const void* k_cache, const void* v_cache, const void* k_scale,
+                                          const void* v_scale, int32_t kv_dtype, int32_t scale_dtype,
+                                          int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                                          int32_t max_q_len, int32_t max_ctx_len, int32_t split_len,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(k_cache && v_cache && workspace, "null pointer argument");
+  NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && max_q_len > 0 &&
+                   max_ctx_len > 0,
+               "bad attention shape");
+  NE_CHECK_ARG(kv_dtype == NE_DTYPE_BF16 || kv_dtype == NE_DTYPE_INT8, "kv_dtype must be bf16 or int8");
+  NE_CHECK_ARG(split_len == 0 || (split_len > 0 && split_len % 128 == 0 && split_len <= kMaxSplitLen),
+               "split_len must be 0 or a positive multiple of 128 up to %d", kMaxSplitLen);
+  const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, split_len, kv_dtype);
+  NE_CHECK_SUPPORTED(dma_serves(kv_dtype, scale_dtype, num_kv_heads, L.mtiles, num_seqs, k_scale, v_scale),
+                     "the stream follows the planned path's shapes");
+  NE_CHECK_ARG(workspace_bytes >= L.total, "workspace of %zu bytes is smaller than the %zu required",
+               workspace_bytes, L.total);
+  AttnParams p{};
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.num_seqs = num_seqs;
+  p.num_kv_heads = num_kv_heads;
+  p.group = L.group;
+  p.mtiles = L.mtiles;
+  p.max_ctx = max_ctx_len;
+  p.plan_w = L.plan_w;
+  p.plan_grid = L.plan_grid;
+  p.plan_whole = whole_plan_ks(num_seqs, max_ctx_len, split_len, L.mtiles) > 0;
+  char* ws = (char*)workspace;
+  p.error_flag = (uint32_t*)(ws + L.error_off);
+  p.plan = (int32_t*)(ws + L.plan_off);
+  p.plan_desc = (int32_t*)(ws + L.desc_off);
+  p.plan_slots = (int32_t*)(ws + L.slots_off);
+  return kv_dtype == NE_DTYPE_BF16 ? launch_kv_stream<true>(p, (hipStream_t)stream)
+                                   : launch_kv_stream<false>(p, (hipStream_t)stream);
 }

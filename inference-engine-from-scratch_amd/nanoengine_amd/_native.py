@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -66,6 +66,10 @@ SIGNATURES: dict[str, tuple] = {
     "ne_paged_attention_plan": (
         ctypes.c_int,
         [_vp, _i32, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "ne_paged_kv_stream_planned": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
     ),
     "ne_w8a16_gemm": (
         ctypes.c_int,

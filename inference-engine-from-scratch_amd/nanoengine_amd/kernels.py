@@ -317,8 +317,8 @@ def paged_attention_plan(
     workspace: AttentionWorkspace,
     split_len: int = 0,
 ) -> None:
-    """Write the attention work plan for this metadata into ``workspace`` (int8 pools with
-    8 KV heads and at most 32 query rows per KV head)."""
+    """Write the attention work plan for this metadata into ``workspace`` (8 KV heads and
+    at most 32 query rows per KV head; bf16 pools or int8 ones with 2-byte scales)."""
     device = _require_gpu(block_tables, ctx_len, q_start, q_len)
     _int32(block_tables, "block_tables")
     for name, t in (("ctx_len", ctx_len), ("q_start", q_start), ("q_len", q_len)):
@@ -339,11 +339,40 @@ def paged_attention_plan(
                                    split_len)
 
 
+def paged_kv_stream_planned(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    num_seqs: int,
+    num_q_heads: int,
+    max_q_len: int,
+    max_ctx_len: int,
+    workspace: AttentionWorkspace,
+    split_len: int = 0,
+) -> None:
+    """Measurement: the K/V reads of the planned attention call alone (its plan, tiles, ring
+    and copies; nothing computed or stored), on the plan ``workspace`` holds for the same
+    metadata.  Its time is the memory ceiling of that call's access pattern."""
+    device = _require_gpu(k_cache, v_cache, k_scale, v_scale)
+    _check(workspace.buffer is not None and workspace.plan_key is not None,
+           "the stream reads the plan paged_attention_plan wrote into the workspace")
+    num_kv_heads = k_cache.shape[1]
+    is_int8 = k_cache.dtype == torch.int8
+    _native.call(
+        "ne_paged_kv_stream_planned",
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), dtype_code(k_cache.dtype),
+        dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16, num_seqs, num_q_heads, num_kv_heads, max_q_len,
+        max_ctx_len, split_len, _ptr(workspace.buffer), workspace.buffer.numel(), _stream(device),
+    )
+
+
 def plan_supported(num_q_heads: int, num_kv_heads: int, max_q_len: int, num_seqs: int, kv_dtype, scale_dtype) -> bool:
     """Whether :func:`paged_attention_plan` / ``planned=True`` serve this shape."""
-    return (kv_dtype == torch.int8 and scale_dtype in (torch.bfloat16, torch.float16) and num_kv_heads == 8
-            and num_q_heads % num_kv_heads == 0 and (num_q_heads // num_kv_heads) * max_q_len <= 32
-            and num_seqs <= 1024)
+    cache_ok = kv_dtype == torch.bfloat16 or (kv_dtype == torch.int8 and scale_dtype in (torch.bfloat16,
+                                                                                        torch.float16))
+    return (cache_ok and num_kv_heads == 8 and num_q_heads % num_kv_heads == 0
+            and (num_q_heads // num_kv_heads) * max_q_len <= 32 and num_seqs <= 1024)
 
 
 # --------------------------------------------------------------------------- A8

@@ -98,9 +98,12 @@ def test_plan_entry_points_refuse_shapes_off_the_planned_path(lib):
     # 2 q heads per KV head x 17 queries = 34 rows per KV head
     rc = lib.ne_paged_attention_plan(p, 64, 16, p, p, p, 8, 16, 8, 17, 1024, 0, p, ws, null)
     assert rc == -2
-    # bf16 cache on the planned attention call
-    rc = lib.ne_paged_verify_attention_planned(p, 2048, 128, p, p, null, null, 0, 0, p, 64, 16, p, p, p,
+    # int8 cache with fp32 scales on the planned attention call (bf16 and 2-byte scales only)
+    rc = lib.ne_paged_verify_attention_planned(p, 2048, 128, p, p, p, p, 3, 2, p, 64, 16, p, p, p,
                                                 8, 16, 8, 128, 5, 1024, 0.088, p, 2048, 128, 0, p, ws, null)
+    assert rc == -2 and b"planned path" in lib.ne_last_error()
+    # the K/V stream (measurement) follows the planned path's shapes: 4 KV heads refused
+    rc = lib.ne_paged_kv_stream_planned(p, p, null, null, 0, 0, 8, 16, 4, 5, 1024, 0, p, ws, null)
     assert rc == -2 and b"planned path" in lib.ne_last_error()
     # a workspace smaller than the plan's layout
     rc = lib.ne_paged_attention_plan(p, 64, 16, p, p, p, 8, 16, 8, 5, 1024, 0, p, ctypes.c_size_t(64), null)

@@ -73,14 +73,16 @@ def engine_for(state, num_seqs, kv_int8=True, graphs=False, prefill_rows=None):
     return create_verify_engine(CFG, state, settings, max_prefill_rows=prefill_rows or 64 * num_seqs)
 
 
-@pytest.mark.parametrize("norm_ones,prefill_rows", [(False, None), (True, None), (False, 24)],
-                         ids=["small-norms", "unit-norms", "chunked-prefill-24-rows"])
-def test_verify_step_logits_match_oracle(norm_ones, prefill_rows):
+@pytest.mark.parametrize("norm_ones,prefill_rows,kv_int8", [(False, None, True), (True, None, True),
+                                                             (False, 24, True), (True, None, False)],
+                         ids=["small-norms", "unit-norms", "chunked-prefill-24-rows", "unit-norms-bf16-kv"])
+def test_verify_step_logits_match_oracle(norm_ones, prefill_rows, kv_int8):
     """prefill_rows=24: the 64-token prompts prefill in forwards of at most 24 rows
-    (chunks over 24, 48 and 64 keys, cut across sequence boundaries)."""
+    (chunks over 24, 48 and 64 keys, cut across sequence boundaries).  kv_int8=False: a
+    bf16 pool (kv_cache_dtype auto), on the bf16 attention kernel."""
     state = make_state(norm_ones)
     prompts = motif_prompts(4)
-    eng = engine_for(state, 4, prefill_rows=prefill_rows)
+    eng = engine_for(state, 4, kv_int8=kv_int8, prefill_rows=prefill_rows)
     assert prefill_rows is None or eng.model.max_rows == prefill_rows
     params = SamplingParams(max_new_tokens=32, temperature=0.8, seed=1, ignore_eos=True)
     seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts)]
@@ -91,7 +93,7 @@ def test_verify_step_logits_match_oracle(norm_ones, prefill_rows):
     ours = eng.runner.logits.float().cpu()
     step = eng.runner.trace[0]
     ref_model = oracle_model(state, torch.bfloat16)
-    pool = om.KVCachePool(OCFG, 64 * 16, torch.bfloat16, is_int8=True)
+    pool = om.KVCachePool(OCFG, 64 * 16, torch.bfloat16, is_int8=kv_int8)
     runner = OracleRunner(ref_model, pool, OraclePaged(64, 16))
     for slot, rec in step.items():
         seq = OracleSequence(f"o{slot}", list(prompts[slot]), 64, 32)
