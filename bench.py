@@ -155,6 +155,19 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     for _ in range(warmup):
         eng.runner.step()
     ctx_per_step, lengths_per_step = [], []
+    # HIP events around each step's device work (graph replay, or the eager launches) on
+    # the stream it runs on: the step's wall time minus this is the host's share
+    device_events = []
+    device_step = eng.runner._run_device_step
+
+    def timed_device_step():
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        device_step()
+        end.record()
+        device_events.append((begin, end))
+
+    eng.runner._run_device_step = timed_device_step
     torch.cuda.synchronize()
     start = time.perf_counter()
     # per step: the runner's slot lengths before it (its host mirror of each sequence's
@@ -170,6 +183,8 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
             records.append((lengths, eng.runner.step()))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
+    eng.runner._run_device_step = device_step
+    device_us = 1e3 * sum(b.elapsed_time(e) for b, e in device_events) / max(len(device_events), 1)
     tokens = proposed = accepted = 0
     kept_hist: dict[int, int] = {}
     for lengths, results in records:
@@ -185,6 +200,8 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     return {
         "elapsed": elapsed,
         "steps": len(records),
+        "device_us_per_step": device_us,
+        "host_us_per_step": 1e6 * elapsed / max(len(records), 1) - device_us,
         "tokens": tokens,
         "kept_hist": kept_hist,
         "active_at_end": active,
@@ -1124,6 +1141,8 @@ def main() -> int:
             "workload": "64 seqs x 64-token motif prompts, 128 output tokens each, every verify step from the "
                         "first until all sequences finished, n-gram k=4, greedy, int8 W + int8 paged KV",
             "steps": f_res["steps"], "verify_step_us_mean": round(1e6 * f_res["elapsed"] / max(f_res["steps"], 1), 1),
+            "device_step_us_mean": round(f_res["device_us_per_step"], 1),
+            "host_us_per_step": round(f_res["host_us_per_step"], 1),
             "accepted_tok_s": round(f_res["tokens"] / f_res["elapsed"], 1), "tokens": f_res["tokens"],
             "mean_context": round(f_res["mean_context"], 1),
             "accepted_per_step_hist": {str(k): v for k, v in sorted(f_res["kept_hist"].items())},
@@ -1156,6 +1175,8 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(step_us / 1e3, 4),
         "verify_step_us": round(step_us, 1),
+        "device_step_us": round(res["device_us_per_step"], 1),
+        "host_us_per_step": round(res["host_us_per_step"], 1),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -69,7 +69,28 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, OUTPUT)
     if verbose:
         print(f"built {OUTPUT}")
+    build_host_step(verbose)
     return OUTPUT
+
+
+def build_host_step(verbose: bool = False) -> Path:
+    """The CPython extension of the verify step's host bookkeeping (csrc/host_step.c)."""
+    import sysconfig
+
+    out = PACKAGE_DIR / "nanoengine_amd" / ("_host_step" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("gcc not found; it builds the host-step extension")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-std=c11", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "host_step.c"), "-o", str(tmp)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"gcc failed on host_step.c:\n{result.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":

@@ -11,6 +11,7 @@ is the scratch slot that padded rows write to.
 
 from __future__ import annotations
 
+import itertools
 import math
 from collections import OrderedDict, deque
 
@@ -83,6 +84,14 @@ class BlockAllocator:
         self._used.add(block)
         return block
 
+    def allocate_many(self, count: int) -> list[int]:
+        """``count`` blocks from the head, as ``count`` calls of ``allocate``."""
+        if count > len(self._free):
+            raise OutOfKVMemoryError("no free KV blocks")
+        blocks = [self._free.popleft() for _ in range(count)]
+        self._used.update(blocks)
+        return blocks
+
     def free(self, block: int) -> None:
         if block not in self._used:
             raise ValueError(f"block {block} is not allocated")
@@ -141,12 +150,37 @@ class PagedSlotAllocator:
     def reserve(self, sequence, num_tokens: int) -> list[int]:
         """Grow the table to hold ``num_tokens``; returns the newly allocated blocks."""
         rid = _request_id(sequence)
-        if self.count_missing_blocks(rid, num_tokens) > self._blocks.num_free_blocks:
+        table = self._tables.get(rid)
+        missing = -(-num_tokens // self.block_size) - (0 if table is None else len(table))
+        if missing > self._blocks.num_free_blocks:
             raise OutOfKVMemoryError(f"no blocks for {num_tokens} tokens of {rid}")
-        table = self._tables.setdefault(rid, [])
-        added = [self._blocks.allocate() for _ in range(self.count_missing_blocks(rid, num_tokens))]
+        if table is None:
+            table = self._tables[rid] = []
+        if missing <= 0:
+            return []
+        added = [self._blocks.allocate() for _ in range(missing)]
         table.extend(added)
         return added
+
+    def peek_free(self, count: int) -> list[int] | None:
+        """The next ``count`` blocks ``reserve`` would hand out (the head of the FIFO free
+        list), or None when fewer are free."""
+        free = self._blocks._free
+        if count > len(free):
+            return None
+        return list(itertools.islice(free, count))
+
+    def take_free(self, sequences: list, counts: list[int], blocks: list[int]) -> None:
+        """Record what ``peek_free`` showed as reserved: sequence i grows by the next
+        counts[i] blocks, in order -- the state ``reserve`` would leave for each of them
+        in turn."""
+        taken = self._blocks.allocate_many(len(blocks))
+        if taken != blocks:
+            raise RuntimeError("the free list changed between peek_free and take_free")
+        at = 0
+        for sequence, count in zip(sequences, counts):
+            self._tables.setdefault(_request_id(sequence), []).extend(blocks[at : at + count])
+            at += count
 
     def free(self, sequence) -> None:
         for block in self._tables.pop(_request_id(sequence), []):

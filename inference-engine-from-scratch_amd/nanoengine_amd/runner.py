@@ -36,13 +36,13 @@ from __future__ import annotations
 
 import math
 from collections import deque
-from typing import TYPE_CHECKING
+from typing import TYPE_CHECKING, NamedTuple
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
-from nanoengine_amd import kernels
+from nanoengine_amd import host_step, kernels
 from nanoengine_amd.interface import find_finish_reason
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
 from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
@@ -64,8 +64,7 @@ def request_length_error(num_prompt_tokens: int, max_new_tokens: int, max_model_
     return None
 
 
-@dataclass(slots=True)
-class StepResult:
+class StepResult(NamedTuple):
     """Tokens emitted for one sequence by one step, with its finish reason if it ended."""
 
     tokens: list[int]
@@ -103,6 +102,7 @@ class VerifyRunner:
         self.max_seqs = max_seqs
         self.max_ngram = max_ngram
         self.stop_token_ids = frozenset(stop_token_ids)
+        self._stop_ids = tuple(sorted(self.stop_token_ids))
         self.block_size = allocator.block_size
         self.max_model_len = max_model_len
         self.capacity = max_model_len + self.R
@@ -119,7 +119,10 @@ class VerifyRunner:
         self.block_tables = torch.zeros(max_seqs, self.max_blocks, **i32)
         self.num_tokens = torch.zeros(max_seqs, **i32)
         self.drafts = torch.zeros(max_seqs, self.k, **i32)
-        self.num_drafts = torch.zeros(max_seqs, **i32)
+        # what the host reads back after a step -- emitted tokens, their counts and the
+        # next step's guess counts -- in one buffer, so that one copy fetches it
+        self.step_out = torch.zeros(max_seqs * (self.R + 2), **i32)
+        self.out_tokens, self.num_out, self.num_drafts = self._step_out_views(self.step_out)
         # length limit and generated count per slot, advanced on the device after each
         # step so that the next step's n-gram guesses need no host round trip
         self.max_new = torch.zeros(max_seqs, **i32)
@@ -137,8 +140,6 @@ class VerifyRunner:
         self.q_len = torch.zeros(max_seqs, **i32)
         self.ctx_len = torch.zeros(max_seqs, **i32)
         self.row_start = torch.arange(max_seqs, **i32) * self.R
-        self.out_tokens = torch.zeros(max_seqs, self.R, **i32)
-        self.num_out = torch.zeros(max_seqs, **i32)
         vocab = model.config.vocab_size
         self.argmax_partials = torch.zeros(rows, kernels.lm_head_num_tiles(vocab), dtype=torch.int64,
                                            device=dev)
@@ -147,24 +148,23 @@ class VerifyRunner:
         self.h_tables = torch.zeros(max_seqs, self.max_blocks, dtype=torch.int32, **pin)
         self.h_num_tokens = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         self.h_steps = torch.zeros(max_seqs, dtype=torch.int64, **pin)
-        self.h_num_drafts = torch.zeros(max_seqs, dtype=torch.int32, **pin)
-        # the next step's counts, read back with this step's tokens (n-gram drafting)
-        self.h_num_drafts_next = torch.zeros(max_seqs, dtype=torch.int32, **pin)
-        self.h_out = torch.zeros(max_seqs, self.R, dtype=torch.int32, **pin)
         self.h_drafts = torch.zeros(max_seqs, self.k, dtype=torch.int32, **pin)
-        self.h_num_out = torch.zeros(max_seqs, dtype=torch.int32, **pin)
+        # two host copies of step_out: a step reads back into one while its guess counts
+        # (read back by the previous step, n-gram drafting) sit in the other
+        self.h_step_out = [torch.zeros(max_seqs * (self.R + 2), dtype=torch.int32, **pin) for _ in range(2)]
+        self._read_back = 0
+        self._bind_read_back()
         # numpy views of the pinned buffers: the per-step host work indexes them per
         # sequence, which costs ~1 us through torch and ~0.1 us through numpy
         self.np_tables = self.h_tables.numpy()
         self.np_num_tokens = self.h_num_tokens.numpy()
         self.np_steps = self.h_steps.numpy()
-        self.np_num_drafts = self.h_num_drafts.numpy()
-        self.np_num_drafts_next = self.h_num_drafts_next.numpy()
         # whether the device drafts / num_drafts already hold this step's n-gram guesses
         # (proposed at the end of the previous step, no sequence admitted since)
         self._drafts_ready = False
-        self.np_out = self.h_out.numpy()
-        self.np_num_out = self.h_num_out.numpy()
+        # a plain paged allocator hands out blocks from the head of a FIFO free list, so a
+        # step's new table entries are known before the allocator records them
+        self._fifo_blocks = type(allocator) is PagedSlotAllocator
         # per-slot host state mirrored from the Sequence objects, so that a step's counts
         # and block checks are array operations: active, length L, generated tokens,
         # length limit, blocks owned
@@ -175,7 +175,12 @@ class VerifyRunner:
         self.np_owned = np.zeros(max_seqs, dtype=np.int64)
         self.np_temp = np.zeros(max_seqs, dtype=np.float32)
         self.np_top_p = np.ones(max_seqs, dtype=np.float32)
+        # whether each slot's sequence ends at a stop token (ignore_eos unset)
+        self.np_honours_stop = np.zeros(max_seqs, dtype=bool)
         self.slots: list[Sequence | None] = [None] * max_seqs
+        # the active slot list and whether any samples, kept between slot changes
+        self._active: list[int] | None = None
+        self._sampled: bool | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
         # whether the captured step computes full logits (some slot samples) or only the
         # LM head's argmax partials (every slot greedy)
@@ -186,10 +191,33 @@ class VerifyRunner:
         # emitted tokens and block table (used by the parity tests)
         self.trace: list | None = None
 
+    def _step_out_views(self, buf: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """out_tokens [max_seqs, R], num_out [max_seqs], num_drafts [max_seqs] of a step_out buffer."""
+        n, r = self.max_seqs, self.R
+        return buf[: n * r].view(n, r), buf[n * r : n * (r + 1)], buf[n * (r + 1) :]
+
+    def _bind_read_back(self) -> None:
+        """Host views: this step reads back into h_step_out[_read_back]; its guess counts
+        are the num_drafts part of the other buffer."""
+        if not hasattr(self, "_read_back_views"):
+            views = [self._step_out_views(buf) for buf in self.h_step_out]
+            self._read_back_views = [(v, tuple(t.numpy() for t in v)) for v in views]
+        (self.h_out, self.h_num_out, self.h_num_drafts_next), (self.np_out, self.np_num_out,
+                                                                self.np_num_drafts_next) = \
+            self._read_back_views[self._read_back]
+        other = self._read_back_views[1 - self._read_back]
+        self.h_num_drafts, self.np_num_drafts = other[0][2], other[1][2]
+
     # ------------------------------------------------------------------ slots
     @property
     def active_slots(self) -> list[int]:
-        return [i for i, s in enumerate(self.slots) if s is not None]
+        if self._active is None:
+            self._active = [i for i, s in enumerate(self.slots) if s is not None]
+        return list(self._active)
+
+    def _slots_changed(self) -> None:
+        self._active = None
+        self._sampled = None
 
     def free_slots(self) -> list[int]:
         return [i for i, s in enumerate(self.slots) if s is None]
@@ -197,7 +225,9 @@ class VerifyRunner:
     @property
     def any_sampled(self) -> bool:
         """Whether some active slot samples (temperature > 0)."""
-        return bool((self.np_temp[self.np_active] > 0).any())
+        if self._sampled is None:
+            self._sampled = bool((self.np_temp[self.np_active] > 0).any())
+        return self._sampled
 
     def _check_sampling(self, sequences: list[Sequence]) -> None:
         """A draft-model proposer guesses for the whole batch with one temperature and
@@ -256,6 +286,7 @@ class VerifyRunner:
         s0 = run[0][0]
         n = len(run)
         pending: deque[list] = deque()
+        self._slots_changed()
         for slot, seq in run:
             self.slots[slot] = seq
             p = seq.num_tokens
@@ -298,6 +329,7 @@ class VerifyRunner:
             self.allocator.on_tokens_cached(seq)  # the whole prompt is verified and cached
             seq.sampling_generator.step += 1
             self.np_active[slot] = True
+            self.np_honours_stop[slot] = not seq.sampling_params.ignore_eos
             self.np_max_new[slot] = seq.sampling_params.max_new_tokens
             self.np_owned[slot] = self.allocator.num_blocks_of(seq)
             self.np_steps[slot] = seq.sampling_generator.step
@@ -308,6 +340,7 @@ class VerifyRunner:
         self.max_new[sl] = torch.from_numpy(self.np_max_new[sl].astype(np.int32))
         self.generated[sl] = torch.from_numpy(self.np_gen[sl].astype(np.int32))
         self._drafts_ready = False  # the new slots have no guesses yet
+        self._slots_changed()
         return results
 
     def _prefill_forward(self, pieces: list[tuple[int, Sequence, int, int, int]]) -> None:
@@ -411,15 +444,22 @@ class VerifyRunner:
 
     def step(self) -> dict[int, StepResult]:
         """One verify step over every active slot; returns what each slot emitted."""
-        active = self.active_slots
+        if self._active is None:
+            self._active = [i for i, s in enumerate(self.slots) if s is not None]
+        active = self._active
         if not active:
             return {}
         slots = self.slots
         act = self.np_active.copy()
-        # num_guesses for every slot at once (speculative_generator.py:71-72)
-        counts = np.clip(np.minimum(self.k, self.np_max_new - self.np_gen - 1), 0, None)
-        self.np_num_tokens[:] = np.where(act, counts, 0)
-        if self.proposer is None:
+        ngram = self.proposer is None
+        if not (ngram and self._drafts_ready) or self.trace is not None:
+            # num_guesses for every slot at once (speculative_generator.py:71-72); n-gram
+            # guesses proposed at the end of the previous step come with the device's counts
+            counts = np.minimum(self.np_max_new - self.np_gen - 1, self.k)
+            np.maximum(counts, 0, out=counts)
+            counts *= act
+            self.np_num_tokens[:] = counts
+        if ngram:
             if not self._drafts_ready:
                 self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
                 self.steps.copy_(self.h_steps, non_blocking=True)
@@ -451,25 +491,31 @@ class VerifyRunner:
                 seq = slots[s]
                 if seq.num_tokens - 1 < allocator.first_writable_position(seq):
                     raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
-        need = self.np_len + np_num_drafts
-        grow = np.nonzero(act & (need > self.np_owned * bs))[0]  # (paged_allocator.py:50-55)
-        for s in grow.tolist():
-            owned = int(self.np_owned[s])
-            added = allocator.reserve(slots[s], int(need[s]))
-            self.np_tables[s, owned : owned + len(added)] = added
-            self.np_owned[s] = owned + len(added)
-        tables_changed = len(grow) > 0
-        if tables_changed:
+        # slots whose length + guesses outgrow their blocks (paged_allocator.py:50-55)
+        grow, counts, targets, total = host_step.plan_growth(self.np_len, np_num_drafts, self.np_owned, act, bs)
+        deferred = None
+        if grow:
+            np_tables, np_owned = self.np_tables, self.np_owned
+            # a FIFO allocator's next blocks, in slot order, go into the tables now; the
+            # allocator records them while the device runs the step
+            blocks = allocator.peek_free(total) if self._fifo_blocks else None
+            if blocks is not None:
+                host_step.assign_blocks(np_tables, np_owned, grow, counts, blocks)
+                deferred = (grow, counts, blocks)
+            else:
+                for s, target in zip(grow, targets):
+                    owned = int(np_owned[s])
+                    added = allocator.reserve(slots[s], target)
+                    np_tables[s, owned : owned + len(added)] = added
+                    np_owned[s] = owned + len(added)
             self.block_tables.copy_(self.h_tables, non_blocking=True)
-        ngram = self.proposer is None
         if self.trace is not None:  # the device step overwrites the guesses with the next step's
             torch.cuda.current_stream(self.device).synchronize()
             traced_drafts = {s: self.drafts[s, : int(np_num_drafts[s])].tolist() for s in active}
         self._run_device_step()
-        self.h_out.copy_(self.out_tokens, non_blocking=True)
-        self.h_num_out.copy_(self.num_out, non_blocking=True)
-        if ngram:
-            self.h_num_drafts_next.copy_(self.num_drafts, non_blocking=True)
+        self.h_step_out[self._read_back].copy_(self.step_out, non_blocking=True)
+        if deferred is not None:
+            allocator.take_free([slots[s] for s in deferred[0]], deferred[1], deferred[2])
         torch.cuda.current_stream(self.device).synchronize()
         if self.trace is not None:
             self.trace.append({
@@ -482,45 +528,23 @@ class VerifyRunner:
                 }
                 for s in active
             })
-        results = {}
-        np_num_out = self.np_num_out
-        # the mirrors advance by the emitted counts (a slot that finishes is released)
-        emitted = np.where(act, np_num_out, 0)
-        self.np_len += emitted
-        self.np_gen += emitted
-        self.np_steps[act] += 1
-        out_rows, nout, ndrafts = self.np_out.tolist(), np_num_out.tolist(), np_num_drafts.tolist()
-        # slots that may finish this step: at the length limit, or a stop token emitted by
-        # a slot that honours stops; every other slot takes the plain append below
-        may_finish = act & (self.np_gen >= self.np_max_new)
-        if self.stop_token_ids:
-            honours = np.fromiter((s is not None and not s.sampling_params.ignore_eos for s in slots), bool,
-                                  count=len(slots))
-            if honours.any():
-                rows = np.arange(self.R)[None, :] < np_num_out[:, None]
-                hit = (np.isin(self.np_out, list(self.stop_token_ids)) & rows).any(axis=1)
-                may_finish |= act & honours & hit
-        track_cached = self._track_cached
-        may_finish = may_finish.tolist()
-        for s in active:
+        # the mirrors advance by the emitted counts and every slot that cannot finish this
+        # step appends its tokens; slots at their length limit or with a stop token
+        # emitted (when they honour stops) finish one token at a time below
+        finish = host_step.finish_step if len(self._stop_ids) <= 64 else host_step.finish_step_py
+        results, finishing = finish(
+            active, slots, self.np_out, self.np_num_out, np_num_drafts, act, self.np_len, self.np_gen,
+            self.np_steps, self.np_max_new, self.np_honours_stop, self._stop_ids, StepResult,
+            self.allocator.on_tokens_cached if self._track_cached else None,
+        )
+        for s, tokens in finishing:
             seq = slots[s]
-            n = nout[s]
-            kept = n - 1
-            seq.sampling_generator.step += 1
-            if may_finish[s]:
-                cached = len(seq.token_ids) + kept  # L-1 .. L-1+kept now hold the kept tokens
-                results[s] = self._emit(s, seq, out_rows[s][:n], ndrafts[s], kept, cached)
-                continue
-            tokens = out_rows[s][:n]
-            ids = seq.token_ids
-            ids.extend(tokens)
-            seq.num_cached_tokens = len(ids) - 1  # L-1 .. L-1+kept hold the kept tokens
-            if track_cached:
-                self.allocator.on_tokens_cached(seq)
-            results[s] = StepResult(tokens, None, ndrafts[s], kept)
+            kept = len(tokens) - 1
+            cached = len(seq.token_ids) + kept  # L-1 .. L-1+kept now hold the kept tokens
+            results[s] = self._emit(s, seq, tokens, int(np_num_drafts[s]), kept, cached)
         if ngram:  # the counts read back with this step's tokens are the next step's
-            self.h_num_drafts, self.h_num_drafts_next = self.h_num_drafts_next, self.h_num_drafts
-            self.np_num_drafts, self.np_num_drafts_next = self.np_num_drafts_next, self.np_num_drafts
+            self._read_back ^= 1
+            self._bind_read_back()
             self._drafts_ready = True
         return results
 
@@ -563,7 +587,9 @@ class VerifyRunner:
         if self.proposer is not None:
             self.proposer.release(slot)
         self.slots[slot] = None
+        self._slots_changed()
         self.np_active[slot] = False
+        self.np_honours_stop[slot] = False
         self.np_owned[slot] = 0
         self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
         self.h_tables[slot].zero_()

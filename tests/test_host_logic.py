@@ -151,3 +151,32 @@ def test_attention_workspace_held_by_a_graph_refuses_to_grow():
     assert ws.get(cpu, 1024, ("b",)) is buf
     with pytest.raises(RuntimeError, match="captured HIP graph"):
         ws.get(cpu, 8192, ("c",))
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.lists(st.lists(st.tuples(st.integers(0, 5), st.integers(1, 40)), max_size=6), max_size=12),
+       st.lists(st.integers(0, 5), max_size=12))
+def test_peek_then_take_equals_reserving_in_slot_order(steps, frees):
+    """The verify step writes a step's new table entries from peek_free and records them
+    with take_free while the device runs: tables and free list must end as the
+    reference's reserve, called for each growing sequence in slot order, leaves them
+    (paged_allocator.py:50-55, block_allocator.py:20-27)."""
+    one, two = PagedSlotAllocator(64, 4, CPU), PagedSlotAllocator(64, 4, CPU)
+    for i, grows in enumerate(steps):
+        targets = {}
+        for rid, n in grows:  # one target per sequence, the largest, as a step has
+            targets[f"r{rid}"] = max(n, targets.get(f"r{rid}", 0))
+        names = sorted(targets)
+        counts = [max(0, -(-targets[r] // 4) - two.num_blocks_of(r)) for r in names]
+        blocks = two.peek_free(sum(counts))
+        if blocks is None:
+            continue
+        for r in names:
+            one.reserve(r, targets[r])
+        two.take_free(names, counts, blocks)
+        if i < len(frees):
+            one.free(f"r{frees[i]}")
+            two.free(f"r{frees[i]}")
+        for r in (f"r{j}" for j in range(6)):
+            assert one.block_table(r) == two.block_table(r)
+        assert list(one._blocks._free) == list(two._blocks._free)

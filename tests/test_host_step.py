@@ -1,0 +1,75 @@
+"""The verify step's host bookkeeping (nanoengine_amd.host_step): the CPython extension
+built from csrc/host_step.c against the Python definitions of the same contract
+(speculative_generator.py:54-72, paged_allocator.py:50-55) on random slot states --
+mirrors, tables, token lists, sampling steps and results must all agree."""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+
+from nanoengine_amd import host_step
+from nanoengine_amd.interface import GenerationRequest, SamplingParams
+from nanoengine_amd.runner import StepResult
+from nanoengine_amd.sequence_state import Sequence
+
+pytestmark = pytest.mark.skipif(not host_step.NATIVE, reason="the _host_step extension is not built")
+
+
+def _state(seed: int, S: int = 64, R: int = 5):
+    rng = np.random.default_rng(seed)
+    act = rng.random(S) < 0.8
+    lengths = rng.integers(1, 300, S).astype(np.int64)
+    owned = ((lengths + 15) // 16 - rng.integers(0, 2, S)).clip(0).astype(np.int64)
+    nd = rng.integers(0, R, S).astype(np.int32)
+    out = rng.integers(0, 600, (S, R)).astype(np.int32)
+    nout = np.minimum(nd + 1, rng.integers(1, R + 1, S)).astype(np.int32)
+    gen = rng.integers(0, 100, S).astype(np.int64)
+    max_new = rng.integers(50, 140, S).astype(np.int64)
+    steps = rng.integers(0, 50, S).astype(np.int64)
+    honours = rng.random(S) < 0.5
+    slots = [Sequence.from_request(GenerationRequest(f"s{i}", rng.integers(0, 600, int(lengths[i])).tolist(),
+                                                     SamplingParams(max_new_tokens=int(max_new[i]))))
+             if act[i] else None for i in range(S)]
+    return dict(act=act, lengths=lengths, owned=owned, nd=nd, out=out, nout=nout, gen=gen, max_new=max_new,
+                steps=steps, honours=honours, slots=slots)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_plan_and_assign_match_python(seed):
+    st = _state(seed)
+    want = host_step.plan_growth_py(st["lengths"], st["nd"], st["owned"], st["act"], 16)
+    got = host_step.plan_growth(st["lengths"], st["nd"], st["owned"], st["act"], 16)
+    assert got == want
+    slots, counts, _, total = got
+    blocks = list(range(1000, 1000 + total))
+    t1, t2 = np.zeros((64, 40), np.int32), np.zeros((64, 40), np.int32)
+    o1, o2 = st["owned"].copy(), st["owned"].copy()
+    host_step.assign_blocks_py(t1, o1, slots, counts, blocks)
+    host_step.assign_blocks(t2, o2, slots, counts, blocks)
+    assert np.array_equal(t1, t2) and np.array_equal(o1, o2)
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("stops", [(), (7, 300, 599)])
+def test_finish_step_matches_python(seed, stops):
+    st = _state(100 + seed)
+    active = np.flatnonzero(st["act"]).tolist()
+    runs = []
+    for fn in (host_step.finish_step_py, host_step.finish_step):
+        s = copy.deepcopy(st)
+        cached = []
+        results, finishing = fn(active, s["slots"], s["out"], s["nout"], s["nd"], s["act"], s["lengths"], s["gen"],
+                                s["steps"], s["max_new"], s["honours"], stops, StepResult, cached.append)
+        runs.append((results, finishing, s, [q.request_id for q in cached]))
+    (r1, f1, s1, c1), (r2, f2, s2, c2) = runs
+    assert list(r1) == list(r2) and r1 == r2
+    assert f1 == f2 and c1 == c2
+    for key in ("lengths", "gen", "steps"):
+        assert np.array_equal(s1[key], s2[key])
+    for a, b in zip(s1["slots"], s2["slots"]):
+        if a is not None:
+            assert a.token_ids == b.token_ids and a.num_cached_tokens == b.num_cached_tokens
+            assert a.sampling_generator.step == b.sampling_generator.step
