@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 8
+#define NE_ABI_VERSION 9
 
 /* status codes */
 #define NE_OK 0
@@ -221,9 +221,11 @@ int ne_w8a16_gemm_splitk(const void* x, int64_t ldx, const int8_t* w, const void
 /*
  * A8b - bf16 GEMM for the tied LM head: logits[m, n] = bf16(sum_k x[m,k] w[n,k])
  * (replaces compute_logits, ne/models/qwen3.py:197-203).  Either output may be
- * null.  When argmax_partials is given, it receives per (row, 64-column tile) the
- * largest bf16-rounded logit and its first index, packed for an ordered max, for
- * ne_accept to finish; ne_lm_head_num_tiles(n) gives the tile count per row.
+ * null.  When argmax_partials is given, it receives per row ne_lm_head_num_tiles(n)
+ * keys, each the largest bf16-rounded logit of a disjoint set of columns with its first
+ * index, packed for an ordered max (the row's argmax is the largest key), for ne_accept
+ * to finish.  The sets are each work-group's column range split between its two column
+ * waves: ne_lm_head_num_tiles(n) = 2 * min(n / 64, 256).
  */
 int32_t ne_lm_head_num_tiles(int32_t n);
 int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, int32_t n, int32_t k,

@@ -476,9 +476,43 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
   const int V = p.vocab;
 
   if (!(T > 0.f)) {
-    for (int i = 0; i <= g; ++i) {
-      const int t = row_argmax(p, rs0 + i, s_red);
-      if (tid == 0) s_target[i] = t;
+    if (p.logits == nullptr) {
+      // the rows' LM-head partials are loaded together, then reduced one row after
+      // another: one memory round trip for all of them
+      uint64_t best[kMaxRows];
+      if (p.num_tiles <= 2 * kThreads) {  // the LM head's 512 keys per row: two per thread
+        uint64_t v[kMaxRows][2];
+#pragma unroll
+        for (int i = 0; i < kMaxRows; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int t = tid + j * kThreads;
+            v[i][j] = (i <= g && t < p.num_tiles) ? p.partials[(int64_t)(rs0 + i) * p.num_tiles + t] : 0;
+          }
+#pragma unroll
+        for (int i = 0; i < kMaxRows; ++i) best[i] = v[i][0] > v[i][1] ? v[i][0] : v[i][1];
+      } else {
+#pragma unroll
+        for (int i = 0; i < kMaxRows; ++i) {
+          best[i] = 0;
+          if (i <= g) {
+            const uint64_t* src = p.partials + (int64_t)(rs0 + i) * p.num_tiles;
+            for (int t = tid; t < p.num_tiles; t += kThreads) best[i] = best[i] > src[t] ? best[i] : src[t];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kMaxRows; ++i) {
+        if (i <= g) {
+          const uint64_t v = block_max_u64(best[i], s_red);
+          if (tid == 0) s_target[i] = (int)(0xFFFFFFFFu - (uint32_t)v);
+        }
+      }
+    } else {
+      for (int i = 0; i <= g; ++i) {
+        const int t = row_argmax(p, rs0 + i, s_red);
+        if (tid == 0) s_target[i] = t;
+      }
     }
     __syncthreads();
     if (tid == 0) {

@@ -602,7 +602,10 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
 
 // ---- LM head: persistent work-groups over the vocabulary -------------------------
 // logits = X . W^T for X [m, k] bf16 and the tied embedding W [vocab, k] bf16, plus
-// per-(row, 64 columns) argmax partials.  The weight (311 MB for 151936 x 1024) is
+// argmax partials: per row, one (value, index) key for each half of each work-group's
+// column range (the range's 128-column halves of every block, kept as a running
+// maximum, so that the acceptance kernel reduces 512 keys per row, not one per 64
+// columns).  The weight (311 MB for 151936 x 1024) is
 // read from HBM once; what limits a tiled GEMM at m = 320 is the L2 -> CU traffic
 // of X, which every column tile re-reads (about 2.3 GB over 64 x 128 tiles).  So
 // one work-group per CU owns a contiguous range of 64-column groups and walks it in
@@ -614,6 +617,7 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
 // that waits for the memory pipeline does not hold up the multiplies.  Stages run
 // on across blocks.  Rows beyond m re-read row m - 1 and are never stored; more
 // than 320 rows take further passes.
+constexpr int kLmMaxGrid = 256;  // persistent work-groups (one per CU)
 constexpr int kLmRows = 320;
 constexpr int kLmCols = 256;
 constexpr int kLmWaves = 8;
@@ -629,27 +633,48 @@ struct LmStage {
   int m0, c0, ccols, k0;
 };
 
-// Copy instruction j of this wave for a stage: 128-byte rows (64 bf16), 8 rows per
-// 1 KiB instruction; row r keeps its 16-byte chunk c at position c ^ (r & 7).
-__device__ __forceinline__ void lm_issue_one(const GemmParams& p, char* stage, const LmStage& st,
-                                             int wave, int j, int lane) {
-  const int i = wave * kLmInstr + j;
-  if (i < kLmXBytes / 1024) {
-    const int row = i * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ (row & 7);
-    const int grow = min(st.m0 + row, p.m - 1);
-    lds_dma16(p.x + (int64_t)grow * p.ldx + st.k0 + chunk * 8, stage + i * 1024);
-  } else {
-    const int wrow = (i - kLmXBytes / 1024) * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ (wrow & 7);
-    const int crow = st.c0 + min(wrow, st.ccols - 1);  // a short block re-reads its last column
-    lds_dma16((const uint16_t*)p.w + (int64_t)crow * p.k + st.k0 + chunk * 8, stage + i * 1024);
+// This wave's 9 copies of a stage: instruction i = wave * 9 + j moves 8 rows of 128 bytes
+// (64 bf16), X rows for i < 40, weight rows after; row r keeps its 16-byte chunk c at
+// position c ^ (r & 7).  A copy's source is a scalar base for the stage (X: k0; W: the
+// block's first column and k0) plus a 32-bit lane offset that depends only on the pass's
+// first row (X) or the block's width (W), so a stage's copies need no 64-bit arithmetic.
+struct LmCopies {
+  uint32_t off[kLmInstr];
+  int nx;  // copies j < nx are X rows, the rest weight rows
+};
+
+__device__ __forceinline__ void lm_offsets(const GemmParams& p, const LmStage& st, int wave, int lane,
+                                           LmCopies& c) {
+  c.nx = min(max(kLmXBytes / 1024 - wave * kLmInstr, 0), kLmInstr);
+#pragma unroll
+  for (int j = 0; j < kLmInstr; ++j) {
+    const int i = wave * kLmInstr + j;
+    if (i < kLmXBytes / 1024) {
+      const int row = i * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ (row & 7);
+      const int grow = min(st.m0 + row, p.m - 1);
+      c.off[j] = (uint32_t)grow * (uint32_t)(p.ldx * 2) + (uint32_t)chunk * 16u;
+    } else {
+      const int wrow = (i - kLmXBytes / 1024) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ (wrow & 7);
+      // a short block re-reads its last column
+      c.off[j] = (uint32_t)min(wrow, st.ccols - 1) * (uint32_t)(p.k * 2) + (uint32_t)chunk * 16u;
+    }
   }
 }
 
+__device__ __forceinline__ void lm_issue_one(const GemmParams& p, char* stage, const LmStage& st,
+                                             const LmCopies& c, int wave, int j) {
+  const char* src = (j < c.nx) ? (const char*)p.x + st.k0 * 2
+                               : (const char*)p.w + ((int64_t)st.c0 * p.k + st.k0) * 2;
+  uint32_t o = c.off[j];
+  __asm__("" : "+v"(o));  // scalar base + 32-bit lane offset addressing
+  lds_dma16(uniform_ptr(src) + o, stage + (wave * kLmInstr + j) * 1024);
+}
+
 __device__ __forceinline__ void lm_mma(const GemmParams& p, const char* stage, char* next,
-                                       const LmStage& nst, int mw, int nw, int wave, int lane,
-                                       floatx4 (&acc)[5][8]) {
+                                       const LmStage& nst, const LmCopies& c, int mw, int nw, int wave,
+                                       int lane, floatx4 (&acc)[5][8]) {
   const int r = lane & 15;
   const int g = lane >> 4;
   const char* xs = stage;
@@ -667,7 +692,7 @@ __device__ __forceinline__ void lm_mma(const GemmParams& p, const char* stage, c
       const int row = mw * 80 + mi * 16 + r;
       const bf16x8 a = __builtin_bit_cast(bf16x8, *(const u32x4*)(xs + row * 128 + (((4 * s + g) ^ (row & 7)) * 16)));
       const int j = s * 5 + mi;  // copy slot between MFMA groups
-      if (next != nullptr && j < kLmInstr) lm_issue_one(p, next, nst, wave, j, lane);
+      if (next != nullptr && j < kLmInstr) lm_issue_one(p, next, nst, c, wave, j);
 #pragma unroll
       for (int ns = 0; ns < 8; ++ns)
         acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[ns], a, acc[mi][ns], 0, 0, 0);
@@ -690,17 +715,22 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
   const int nblk = (grp1 - grp0 + 3) / 4;
   const int kt = p.k / kLmSK;
   const int mpass = (p.m + kLmRows - 1) / kLmRows;
-  const int total = mpass * nblk * kt;  // stage u = (pass * nblk + block) * kt + t
+  const int total = mpass * nblk * kt;  // stages, in order pass, block, k
   if (total == 0) return;
-  auto stage_of = [&](int u) {
-    const int bi = (u / kt) % nblk;
+  // stages advance by counters (pass, block, k), so no stage needs a division
+  auto make = [&](int pass, int bi, int t) {
     LmStage st;
-    st.m0 = (u / (kt * nblk)) * kLmRows;
+    st.m0 = pass * kLmRows;
     st.c0 = (grp0 + 4 * bi) * kArgmaxCols;
     st.ccols = min(4, grp1 - grp0 - 4 * bi) * kArgmaxCols;
-    st.k0 = (u % kt) * kLmSK;
+    st.k0 = t * kLmSK;
     return st;
   };
+  int pass = 0, bi = 0, t = 0;
+  // per token subtile: the best (value, index) key of row 16 mi + r over this wave's
+  // columns of the pass so far; written once per pass as partial (row, 2 block + nw)
+  uint64_t row_best[5] = {0, 0, 0, 0, 0};
+  const int tiles = 2 * (int)gridDim.x;
 
   floatx4 acc[5][8];
 #pragma unroll
@@ -708,21 +738,41 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
 #pragma unroll
     for (int ns = 0; ns < 8; ++ns) acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  {
-    const LmStage st = stage_of(0);
-    for (int j = 0; j < kLmInstr; ++j) lm_issue_one(p, smem, st, wave, j, lane);
-  }
+  LmStage cur = make(0, 0, 0);
+  LmCopies copies;
+  lm_offsets(p, cur, wave, lane, copies);
+  int off_m0 = cur.m0, off_cols = cur.ccols;  // what the offsets were built for
+  for (int j = 0; j < kLmInstr; ++j) lm_issue_one(p, smem, cur, copies, wave, j);
   for (int u = 0; u < total; ++u) {
     wait_vmcnt<0>();                                   // this wave's copies of stage u
     asm volatile("s_barrier" ::: "memory");           // everyone's; stage u - 1 fully read
     const bool more = u + 1 < total;
-    const LmStage nst = stage_of(more ? u + 1 : u);
-    lm_mma(p, smem + (u & 1) * kLmStage, more ? smem + ((u + 1) & 1) * kLmStage : nullptr, nst, mw, nw,
+    int npass = pass, nbi = bi, nt = t + 1;
+    if (nt == kt) {
+      nt = 0;
+      if (++nbi == nblk) {
+        nbi = 0;
+        ++npass;
+      }
+    }
+    const LmStage nst = more ? make(npass, nbi, nt) : cur;
+    if (more && (nst.m0 != off_m0 || nst.ccols != off_cols)) {
+      lm_offsets(p, nst, wave, lane, copies);
+      off_m0 = nst.m0;
+      off_cols = nst.ccols;
+    }
+    lm_mma(p, smem + (u & 1) * kLmStage, more ? smem + ((u + 1) & 1) * kLmStage : nullptr, nst, copies, mw, nw,
            wave, lane, acc);
-    if (u % kt != kt - 1) continue;
+    const bool block_done = t == kt - 1;
+    const bool pass_done = block_done && (!more || npass != pass);
+    const LmStage st = cur;
+    cur = nst;
+    pass = npass;
+    bi = nbi;
+    t = nt;
+    if (!block_done) continue;
 
     // ---- block done: logits and argmax partials, then clear the accumulators ----
-    const LmStage st = stage_of(u);
     const int ngrp = st.ccols / kArgmaxCols;
 #pragma unroll
     for (int mi = 0; mi < 5; ++mi) {
@@ -745,10 +795,14 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
           }
           acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
+        if (grp < ngrp) row_best[mi] = max_u64(row_best[mi], best);
+      }
+      if (pass_done) {
+        uint64_t best = row_best[mi];
         best = max_u64(best, shfl_xor_u64(best, 16));
         best = max_u64(best, shfl_xor_u64(best, 32));
-        if (p.argmax != nullptr && g == 0 && m < p.m && grp < ngrp)
-          p.argmax[(int64_t)m * groups + (st.c0 / kArgmaxCols) + grp] = best;
+        if (p.argmax != nullptr && g == 0 && m < p.m) p.argmax[(int64_t)m * tiles + 2 * blockIdx.x + nw] = best;
+        row_best[mi] = 0;
       }
     }
   }
@@ -762,7 +816,7 @@ int launch_lm_head(GemmParams p, hipStream_t stream) {
     return NE_ELAUNCH;
   }
   const int groups = p.n / kArgmaxCols;
-  const int grid = groups < 256 ? groups : 256;
+  const int grid = groups < kLmMaxGrid ? groups : kLmMaxGrid;
   hipLaunchKernelGGL(lm_head_kernel, dim3((unsigned)grid), dim3(kLmWaves * kWave), kLmRing * kLmStage, stream, p);
   return check_launch("lm_head");
 }
@@ -891,7 +945,9 @@ extern "C" int ne_w8a16_qkv_norm_rope_kv(
   }
 }
 
-extern "C" int32_t ne_lm_head_num_tiles(int32_t n) { return n > 0 ? n / kArgmaxCols : 0; }
+extern "C" int32_t ne_lm_head_num_tiles(int32_t n) {
+  return n > 0 ? 2 * min(n / kArgmaxCols, kLmMaxGrid) : 0;  // two waves' halves per work-group
+}
 
 extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, int32_t n,
                           int32_t k, void* logits, int64_t ld_logits, uint64_t* argmax_partials,
@@ -907,6 +963,9 @@ extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, 
   NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
                    ((uintptr_t)logits % 8) == 0,
                "x and w must be 16-byte aligned, logits 8-byte aligned");
+  // X copies address rows with 32-bit byte offsets, weight rows of a block likewise
+  NE_CHECK_SUPPORTED((int64_t)m * ldx < kMaxXElems, "x spans more than 4 GiB (m=%d, ldx=%lld)", m, (long long)ldx);
+  NE_CHECK_SUPPORTED((int64_t)kLmCols * k * 2 < (int64_t(1) << 32), "k too large for the LM head (k=%d)", k);
   GemmParams p{};
   p.x = (const uint16_t*)x;
   p.ldx = ldx;

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0

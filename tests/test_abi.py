@@ -74,7 +74,8 @@ def test_host_checks_reject_bad_arguments_without_launching(lib):
 
 
 def test_workspace_and_tile_queries(lib):
-    assert lib.ne_lm_head_num_tiles(151936) == 151936 // 64
+    assert lib.ne_lm_head_num_tiles(151936) == 2 * 256  # two halves of 256 work-groups' ranges
+    assert lib.ne_lm_head_num_tiles(4096) == 2 * (4096 // 64)
     assert lib.ne_paged_attention_workspace_size(0, 16, 8, 5, 1024, 0) == 0
     assert lib.ne_paged_attention_workspace_size(64, 16, 7, 5, 1024, 0) == 0  # 16 % 7 != 0
     one_split = lib.ne_paged_attention_workspace_size(64, 16, 8, 5, 256, 256)

@@ -10,6 +10,7 @@ the kernel's own bf16 logits.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -114,10 +115,11 @@ def test_lm_head_logits_and_argmax(device, m, vocab):
     torch.cuda.synchronize()
     assert float((logits.float().cpu() - ref).abs().max()) < 1e-2
     assert rel_err(logits, ref) < TOL
-    # partial argmax reduces to the first-index argmax of the kernel's own bf16 logits
-    p = partials.cpu()
-    best = p.max(dim=1).values
-    idx = (0xFFFFFFFF - (best & 0xFFFFFFFF)).to(torch.int64)
+    # partial argmax reduces to the first-index argmax of the kernel's own bf16 logits;
+    # keys order as unsigned 64-bit integers (a set with no columns holds key 0)
+    p = partials.cpu().numpy().view(np.uint64)
+    best = torch.from_numpy((p.max(axis=1) & np.uint64(0xFFFFFFFF)).astype(np.int64))
+    idx = 0xFFFFFFFF - best
     assert torch.equal(idx, torch.argmax(logits.float().cpu(), dim=1))
     # and equals the fp32 argmax wherever the top-2 margin exceeds the bf16 error
     top2 = torch.topk(ref, 2, dim=1).values
