@@ -66,8 +66,10 @@ class DraftModelProposer:
         # sampled proposals: the draft's logits per (slot, guess), read by the verifier
         self.logits: torch.Tensor | None = None
         self.row_start = torch.arange(max_seqs, **i32) * k
-        self.temperature = 0.0
-        self.top_p = 1.0
+        # each slot's temperature (0: greedy) and top-p for the current proposal
+        self.temperatures = np.zeros(max_seqs, dtype=np.float32)
+        self.top_ps = np.ones(max_seqs, dtype=np.float32)
+        self.sampled = False  # some slot of the current proposal samples
         self.seeds: torch.Tensor | None = None
         self.steps: np.ndarray | None = None
         self.target_len: dict[int, int] = {}  # this proposal's target length per slot
@@ -112,15 +114,19 @@ class DraftModelProposer:
         self.owned[slot] = 0
 
     # -------------------------------------------------------------- proposals
-    def propose(self, sequences: dict[int, Sequence], counts: dict[int, int], temperature: float = 0.0,
-                seeds: torch.Tensor | None = None, steps: np.ndarray | None = None,
-                top_p: float = 1.0) -> dict[int, list[int]]:
+    def propose(self, sequences: dict[int, Sequence], counts: dict[int, int],
+                temperature: float | np.ndarray = 0.0, seeds: torch.Tensor | None = None,
+                steps: np.ndarray | None = None, top_p: float | np.ndarray = 1.0) -> dict[int, list[int]]:
         """``counts[slot]`` guesses for each slot (proposers.py:70-88): greedy, or sampled at
         ``temperature`` and ``top_p`` (compute_token_probabilities, sampling.py:30-38) with the
-        slots' ``seeds`` (device int64) at verify ``steps`` (host)."""
-        self.temperature = float(temperature)
-        self.top_p = float(top_p)
-        if self.temperature > 0.0:
+        slots' ``seeds`` (device int64) at verify ``steps`` (host).  ``temperature`` and
+        ``top_p`` are one value for every slot or arrays indexed by slot (temperature 0:
+        that slot's guesses are the draft's greedy tokens)."""
+        self.temperatures[:] = np.maximum(np.broadcast_to(np.asarray(temperature, dtype=np.float32),
+                                                          self.temperatures.shape), 0.0)
+        self.top_ps[:] = np.broadcast_to(np.asarray(top_p, dtype=np.float32), self.top_ps.shape)
+        self.sampled = bool(any(self.temperatures[s] > 0.0 for s, n in counts.items() if n > 0))
+        if self.sampled:
             if seeds is None or steps is None:
                 raise ValueError("sampled draft proposals need seeds and steps")
             if self.logits is None:
@@ -135,7 +141,7 @@ class DraftModelProposer:
         for s in want:
             self._sync(s, sequences[s])
             self.target_len[s] = sequences[s].num_tokens
-        if self.use_graph and self.temperature == 0.0 and want and max(want.values()) > 1:
+        if self.use_graph and not self.sampled and want and max(want.values()) > 1:
             for s, token in self._next_tokens(sorted(want)).items():  # catch-up: guess 0
                 self.drafts[s].token_ids.append(token)
                 guesses[s].append(token)
@@ -291,7 +297,7 @@ class DraftModelProposer:
         last = hidden.index_select(0, last_rows)
         n, o = len(ends), len(done)
         vocab = self.model.config.vocab_size
-        if self.temperature == 0.0:
+        if not self.sampled:
             _, partials = self.model.compute_logits(last, logits=False, argmax=True)
             kernels.accept(
                 self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], vocab, argmax_partials=partials,
@@ -306,10 +312,12 @@ class DraftModelProposer:
             sel = torch.tensor(slots, dtype=torch.long, device=dev)
             steps = np.array([int(self.steps[s]) + ((r - s * self.k + 1) << 48) for s, r in zip(slots, rows)],
                              dtype=np.int64)
+            temps = self.temperatures[slots]  # a greedy slot's row takes its argmax
             kernels.accept(
                 self.no_drafts[:n], self.zero_counts[:n], self.last_rows[:n], vocab, logits=logits,
-                temperature=self.temperature, top_p=self.top_p, seeds=self.seeds.index_select(0, sel),
-                steps=torch.from_numpy(steps).to(dev), out_tokens=self.out_tokens[o : o + n],
-                num_out=self.num_out[o : o + n],
+                temperature=torch.from_numpy(temps).to(dev),
+                top_p=torch.from_numpy(self.top_ps[slots]).to(dev), any_sampled=bool((temps > 0).any()),
+                seeds=self.seeds.index_select(0, sel), steps=torch.from_numpy(steps).to(dev),
+                out_tokens=self.out_tokens[o : o + n], num_out=self.num_out[o : o + n],
             )
         done.extend(pieces[i][0] for i in ends)

@@ -229,27 +229,6 @@ class VerifyRunner:
             self._sampled = bool((self.np_temp[self.np_active] > 0).any())
         return self._sampled
 
-    def _check_sampling(self, sequences: list[Sequence]) -> None:
-        """A draft-model proposer guesses for the whole batch with one temperature and
-        top-p; n-gram batches take every slot's own."""
-        if self.proposer is None:
-            return
-        params = {(s.sampling_params.temperature, s.sampling_params.top_p) for s in sequences}
-        params |= {(self.slots[s].sampling_params.temperature, self.slots[s].sampling_params.top_p)
-                   for s in self.active_slots}
-        if len(params) > 1:
-            raise NotImplementedError("a draft-model batch verifies with one temperature and top-p")
-
-    @property
-    def batch_temperature(self) -> float:
-        """The draft-model proposer's temperature (every slot's, see _check_sampling)."""
-        act = self.active_slots
-        return float(self.np_temp[act[0]]) if act else 0.0
-
-    @property
-    def batch_top_p(self) -> float:
-        act = self.active_slots
-        return float(self.np_top_p[act[0]]) if act else 1.0
 
     def add(self, sequences: list[Sequence]) -> list[int]:
         """Place sequences in free slots, reserve their prompts, prefill them and emit
@@ -261,7 +240,6 @@ class VerifyRunner:
             problem = request_length_error(seq.num_tokens, seq.sampling_params.max_new_tokens, self.max_model_len)
             if problem is not None:
                 raise ValueError(f"{seq.request_id}: {problem}")
-        self._check_sampling(sequences)
         slots = free[: len(sequences)]
         results = {}
         # prefill contiguous runs of slots together
@@ -473,7 +451,7 @@ class VerifyRunner:
             self.steps.copy_(self.h_steps, non_blocking=True)
             guesses = self.proposer.propose({s: slots[s] for s in active},
                                             {s: int(self.np_num_tokens[s]) for s in active},
-                                            temperature=self.batch_temperature, top_p=self.batch_top_p,
+                                            temperature=self.np_temp, top_p=self.np_top_p,
                                             seeds=self.seeds,
                                             steps=self.np_steps)
             self.np_num_drafts[:] = 0

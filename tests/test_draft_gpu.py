@@ -237,3 +237,51 @@ def test_verify_proposal_with_draft_probabilities_matches_the_c_oracle():
                                          d_rows.view(torch.int16).numpy().view("uint16"), guesses, temp,
                                          gen.seed, step)
         assert got == want, f"trial {trial}"
+
+
+def test_mixed_greedy_and_sampled_draft_batch_matches_the_oracles():
+    """A draft-model batch whose slots sample at their own temperatures (0, 0.8, 0, 1.3):
+    a sampled slot's guesses are the contract's draws from its draft rows at its own
+    temperature and its tokens the C oracle's draft-distribution acceptance; a greedy
+    slot's guesses are its draft rows' first-index argmax and its tokens the greedy
+    acceptance of its target rows (verifier.py:27-60 per sequence)."""
+    from oracle import accept as oacc
+    import numpy as np
+
+    state = unit_norms(random_state_dict(CFG, seed=0, std=0.02))
+    dstate = unit_norms(random_state_dict(DCFG, seed=7, std=0.02))
+    eng = engine(state, DCFG, dstate, 4)
+    temps = [0.0, 0.8, 0.0, 1.3]
+    seqs = [Sequence.from_request(GenerationRequest(
+        f"r{i}", p, SamplingParams(max_new_tokens=16, temperature=t, seed=10 + i, ignore_eos=True)))
+        for i, (p, t) in enumerate(zip(prompts(4, seed=8), temps))]
+    eng.runner.add(seqs)
+    eng.runner.trace = []
+    for _ in range(2):
+        eng.runner.step()
+    torch.cuda.synchronize()
+    rec_step = eng.runner.trace[-1]
+    k = eng.runner.k
+    t_bits = eng.runner.logits.view(torch.int16).cpu().numpy().view("uint16")
+    d_bits = eng.runner.proposer.logits.view(torch.int16).cpu().numpy().view("uint16")
+    checked = set()
+    for slot, rec in rec_step.items():
+        g = len(rec["drafts"])
+        assert g == rec["requested"] > 0
+        temp = temps[slot]
+        t_rows = t_bits[slot * (k + 1) : slot * (k + 1) + g + 1]
+        d_rows = d_bits[slot * k : slot * k + g]
+        if temp == 0.0:
+            draft_argmax = np.argmax(oacc.bf16_to_f32(d_rows), axis=1).tolist()
+            assert rec["drafts"] == draft_argmax, f"slot {slot}"
+            assert rec["out"] == oacc.greedy_accept(oacc.bf16_to_f32(t_rows), rec["drafts"]), f"slot {slot}"
+        else:
+            seed = seqs[slot].sampling_generator.seed
+            step = int(eng.runner.h_steps[slot]) - 1
+            for j, guess in enumerate(rec["drafts"]):
+                drawn = oacc.sampled_accept(d_bits[slot * k + j : slot * k + j + 1], [], temp, seed,
+                                            step + ((j + 1) << 48))
+                assert drawn == [guess], f"slot {slot} guess {j}"
+            assert rec["out"] == oacc.sampled_accept_draft(t_rows, d_rows, rec["drafts"], temp, seed, step)
+        checked.add(temp > 0)
+    assert checked == {False, True}
