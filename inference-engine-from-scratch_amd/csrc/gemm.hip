@@ -612,11 +612,13 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
 // blocks of 256 columns against all rows at once: 8 waves, wave (mw, nw) holding
 // rows 80 mw .. +80 and columns 128 nw .. +128 of the block in 160 accumulators,
 // which cuts the X traffic to one read per 256 columns.  K advances in stages of 64
-// (X 40 KiB + W 32 KiB) copied by DMA into a two-stage LDS ring; each wave places
-// its 9 copy instructions for the next stage between its MFMA groups, so a copy
-// that waits for the memory pipeline does not hold up the multiplies.  Stages run
-// on across blocks.  Rows beyond m re-read row m - 1 and are never stored; more
-// than 320 rows take further passes.
+// (X 40 KiB + W 32 KiB) copied by DMA into a two-stage LDS ring: right after the
+// barrier that frees a slot, every wave issues 9 copies of the next stage, 5 of X and 4
+// of W, then runs its 80 MFMAs on the current one.  Spreading the weight copies (HBM
+// misses) over all waves keeps any one wave from queueing behind them; the two waves of
+// a SIMD still finish a stage apart, the older one ahead.  Stages run on across
+// blocks.  Rows beyond m re-read row m - 1 and are never stored; more than 320 rows
+// take further passes.
 constexpr int kLmMaxGrid = 256;  // persistent work-groups (one per CU)
 constexpr int kLmRows = 320;
 constexpr int kLmCols = 256;
@@ -633,23 +635,25 @@ struct LmStage {
   int m0, c0, ccols, k0;
 };
 
-// This wave's 9 copies of a stage: instruction i = wave * 9 + j moves 8 rows of 128 bytes
-// (64 bf16), X rows for i < 40, weight rows after; row r keeps its 16-byte chunk c at
-// position c ^ (r & 7).  A copy's source is a scalar base for the stage (X: k0; W: the
-// block's first column and k0) plus a 32-bit lane offset that depends only on the pass's
-// first row (X) or the block's width (W), so a stage's copies need no 64-bit arithmetic.
+// This wave's 9 copies of a stage: copy j moves 8 rows of 128 bytes (64 bf16) into LDS
+// slot i = 8 j + wave, so copies 0..4 of every wave are X slots (i < 40) and 5..8 weight
+// slots; row r keeps its 16-byte chunk c at position c ^ (r & 7).  A copy's source is a
+// scalar base for the stage (X: k0; W: the block's first column and k0) plus a 32-bit
+// lane offset that depends only on the pass's first row (X) or the block's width (W), so
+// a stage's copies need no 64-bit arithmetic.
+constexpr int kLmXCopies = kLmXBytes / 1024 / kLmWaves;  // 5
+static_assert(kLmXBytes % (1024 * kLmWaves) == 0, "X slots split evenly over the waves");
+
 struct LmCopies {
   uint32_t off[kLmInstr];
-  int nx;  // copies j < nx are X rows, the rest weight rows
 };
 
 __device__ __forceinline__ void lm_offsets(const GemmParams& p, const LmStage& st, int wave, int lane,
                                            LmCopies& c) {
-  c.nx = min(max(kLmXBytes / 1024 - wave * kLmInstr, 0), kLmInstr);
 #pragma unroll
   for (int j = 0; j < kLmInstr; ++j) {
-    const int i = wave * kLmInstr + j;
-    if (i < kLmXBytes / 1024) {
+    const int i = j * kLmWaves + wave;
+    if (j < kLmXCopies) {
       const int row = i * 8 + (lane >> 3);
       const int chunk = (lane & 7) ^ (row & 7);
       const int grow = min(st.m0 + row, p.m - 1);
@@ -663,39 +667,43 @@ __device__ __forceinline__ void lm_offsets(const GemmParams& p, const LmStage& s
   }
 }
 
-__device__ __forceinline__ void lm_issue_one(const GemmParams& p, char* stage, const LmStage& st,
-                                             const LmCopies& c, int wave, int j) {
-  const char* src = (j < c.nx) ? (const char*)p.x + st.k0 * 2
-                               : (const char*)p.w + ((int64_t)st.c0 * p.k + st.k0) * 2;
-  uint32_t o = c.off[j];
-  __asm__("" : "+v"(o));  // scalar base + 32-bit lane offset addressing
-  lds_dma16(uniform_ptr(src) + o, stage + (wave * kLmInstr + j) * 1024);
+__device__ __forceinline__ void lm_issue(const GemmParams& p, char* stage, const LmStage& st, const LmCopies& c,
+                                         int wave) {
+  const char* xsrc = uniform_ptr((const char*)p.x + st.k0 * 2);
+  const char* wsrc = uniform_ptr((const char*)p.w + ((int64_t)st.c0 * p.k + st.k0) * 2);
+#pragma unroll
+  for (int j = 0; j < kLmInstr; ++j) {
+    uint32_t o = c.off[j];
+    __asm__("" : "+v"(o));  // scalar base + 32-bit lane offset addressing
+    lds_dma16((j < kLmXCopies ? xsrc : wsrc) + o, stage + (j * kLmWaves + wave) * 1024);
+  }
 }
 
-__device__ __forceinline__ void lm_mma(const GemmParams& p, const char* stage, char* next,
-                                       const LmStage& nst, const LmCopies& c, int mw, int nw, int wave,
-                                       int lane, floatx4 (&acc)[5][8]) {
+__device__ __forceinline__ bf16x8 lm_frag(const char* base, int row, int chunk) {
+  return __builtin_bit_cast(bf16x8, *(const u32x4*)(base + row * 128 + ((chunk ^ (row & 7)) * 16)));
+}
+
+// A stage's 80 MFMAs: two k-steps of 32 (lane group g holds k = 32 s + 8 g .. +8), the
+// X fragment of token subtile mi + 1 read while the MFMAs of subtile mi run.
+__device__ __forceinline__ void lm_mma(const char* stage, int mw, int nw, int lane, floatx4 (&acc)[5][8]) {
   const int r = lane & 15;
   const int g = lane >> 4;
   const char* xs = stage;
   const char* ws = stage + kLmXBytes;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {  // two k-steps of 32; lane group g holds k = 32 s + 8 g .. +8
+  for (int s = 0; s < 2; ++s) {
     bf16x8 b[8];
 #pragma unroll
-    for (int ns = 0; ns < 8; ++ns) {
-      const int row = nw * 128 + ns * 16 + r;
-      b[ns] = __builtin_bit_cast(bf16x8, *(const u32x4*)(ws + row * 128 + (((4 * s + g) ^ (row & 7)) * 16)));
-    }
+    for (int ns = 0; ns < 8; ++ns) b[ns] = lm_frag(ws, nw * 128 + ns * 16 + r, 4 * s + g);
+    bf16x8 a = lm_frag(xs, mw * 80 + r, 4 * s + g);
 #pragma unroll
     for (int mi = 0; mi < 5; ++mi) {
-      const int row = mw * 80 + mi * 16 + r;
-      const bf16x8 a = __builtin_bit_cast(bf16x8, *(const u32x4*)(xs + row * 128 + (((4 * s + g) ^ (row & 7)) * 16)));
-      const int j = s * 5 + mi;  // copy slot between MFMA groups
-      if (next != nullptr && j < kLmInstr) lm_issue_one(p, next, nst, c, wave, j);
+      bf16x8 an = a;
+      if (mi < 4) an = lm_frag(xs, mw * 80 + (mi + 1) * 16 + r, 4 * s + g);
 #pragma unroll
       for (int ns = 0; ns < 8; ++ns)
         acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[ns], a, acc[mi][ns], 0, 0, 0);
+      a = an;
     }
   }
 }
@@ -742,7 +750,7 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
   LmCopies copies;
   lm_offsets(p, cur, wave, lane, copies);
   int off_m0 = cur.m0, off_cols = cur.ccols;  // what the offsets were built for
-  for (int j = 0; j < kLmInstr; ++j) lm_issue_one(p, smem, cur, copies, wave, j);
+  lm_issue(p, smem, cur, copies, wave);
   for (int u = 0; u < total; ++u) {
     wait_vmcnt<0>();                                   // this wave's copies of stage u
     asm volatile("s_barrier" ::: "memory");           // everyone's; stage u - 1 fully read
@@ -761,8 +769,8 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
       off_m0 = nst.m0;
       off_cols = nst.ccols;
     }
-    lm_mma(p, smem + (u & 1) * kLmStage, more ? smem + ((u + 1) & 1) * kLmStage : nullptr, nst, copies, mw, nw,
-           wave, lane, acc);
+    if (more) lm_issue(p, smem + ((u + 1) & 1) * kLmStage, nst, copies, wave);
+    lm_mma(smem + (u & 1) * kLmStage, mw, nw, lane, acc);
     const bool block_done = t == kt - 1;
     const bool pass_done = block_done && (!more || npass != pass);
     const LmStage st = cur;

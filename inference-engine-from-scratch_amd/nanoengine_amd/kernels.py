@@ -466,6 +466,7 @@ def lm_head(
     _check(x.dim() == 2 and x.stride(1) == 1, "x must be [m, k]")
     _contig(weight, "weight")
     m, k = x.shape
+    _check(weight.dim() == 2 and weight.shape[1] == k, f"k mismatch: x has {k}, weight {tuple(weight.shape)}")
     n = weight.shape[0]
     if logits is True:
         logits = torch.empty((m, n), dtype=torch.bfloat16, device=device)
