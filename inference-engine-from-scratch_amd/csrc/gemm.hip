@@ -605,7 +605,8 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
 // argmax partials: per row, one (value, index) key for each half of each work-group's
 // column range (the range's 128-column halves of every block, kept as a running
 // maximum, so that the acceptance kernel reduces 512 keys per row, not one per 64
-// columns).  The weight (311 MB for 151936 x 1024) is
+// columns).  Inside the kernel a key is 32 bits: a 16-bit order code of the bf16 value
+// over 16 bits of column within the range.  The weight (311 MB for 151936 x 1024) is
 // read from HBM once; what limits a tiled GEMM at m = 320 is the L2 -> CU traffic
 // of X, which every column tile re-reads (about 2.3 GB over 64 x 128 tiles).  So
 // one work-group per CU owns a contiguous range of 64-column groups and walks it in
@@ -708,6 +709,17 @@ __device__ __forceinline__ void lm_mma(const char* stage, int mw, int nw, int la
   }
 }
 
+// A bf16 pair (lo in bits 0..15) as two unsigned 16-bit codes in value order: positives
+// 0x8000 + magnitude, negatives 0x8000 - magnitude, so -0 and +0 share 0x8000 (as
+// torch.argmax treats them) and any finite value codes above 0.
+__device__ __forceinline__ uint32_t bf16x2_order(uint32_t pair) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t sgn = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, pair) >> (short)15);
+  const uint32_t t = pair ^ ((sgn & 0x7FFF7FFFu) | 0x80008000u);
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, t) - __builtin_bit_cast(u16x2, sgn));
+}
+
 __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -737,7 +749,10 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
   int pass = 0, bi = 0, t = 0;
   // per token subtile: the best (value, index) key of row 16 mi + r over this wave's
   // columns of the pass so far; written once per pass as partial (row, 2 block + nw)
-  uint64_t row_best[5] = {0, 0, 0, 0, 0};
+  // per token subtile: (order code << 16) | (0xFFFF - column within the range) of the best
+  // value of row 16 mi + r over this lane's columns of the pass so far (0: none yet)
+  uint32_t row_best[5] = {0, 0, 0, 0, 0};
+  const int rc0 = grp0 * kArgmaxCols;
   const int tiles = 2 * (int)gridDim.x;
 
   floatx4 acc[5][8];
@@ -781,14 +796,17 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
     if (!block_done) continue;
 
     // ---- block done: logits and argmax partials, then clear the accumulators ----
+    // a lane's 32 values of a row are ranked by (order code << 16) | (31 - position),
+    // position 4 ns + i in column order, then turned into a range column once per row
     const int ngrp = st.ccols / kArgmaxCols;
+    const uint32_t col0 = (uint32_t)(st.c0 - rc0 + nw * 128 + 4 * g);
 #pragma unroll
     for (int mi = 0; mi < 5; ++mi) {
       const int m = st.m0 + mw * 80 + mi * 16 + r;
+      uint32_t best = 0;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {  // the wave's two 64-column groups
         const int grp = 2 * nw + q;
-        uint64_t best = 0;
 #pragma unroll
         for (int nq = 0; nq < 4; ++nq) {
           const int ns = 4 * q + nq;
@@ -796,20 +814,30 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
           const floatx4 v = acc[mi][ns];
           const u32x2 bits = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           if (p.y != nullptr && m < p.m && grp < ngrp) *(u32x2*)(p.y + (int64_t)m * p.ldy + n) = bits;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float rv = bf16_to_f32((uint16_t)(bits[i >> 1] >> (16 * (i & 1))));
-            best = max_u64(best, argmax_key(rv, (uint32_t)(n + i)));
+          if (grp < ngrp) {
+            const uint32_t o0 = bf16x2_order(bits[0]);
+            const uint32_t o1 = bf16x2_order(bits[1]);
+            const uint32_t rank = 31u - 4u * ns;
+            best = max(best, (o0 << 16) | rank);
+            best = max(best, (o0 & 0xFFFF0000u) | (rank - 1u));
+            best = max(best, (o1 << 16) | (rank - 2u));
+            best = max(best, (o1 & 0xFFFF0000u) | (rank - 3u));
           }
           acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
-        if (grp < ngrp) row_best[mi] = max_u64(row_best[mi], best);
       }
+      const uint32_t pos = 31u - (best & 31u);
+      const uint32_t col = col0 + (pos >> 2) * 16u + (pos & 3u);
+      if (best != 0) row_best[mi] = max(row_best[mi], (best & 0xFFFF0000u) | (0xFFFFu - col));
       if (pass_done) {
-        uint64_t best = row_best[mi];
-        best = max_u64(best, shfl_xor_u64(best, 16));
-        best = max_u64(best, shfl_xor_u64(best, 32));
-        if (p.argmax != nullptr && g == 0 && m < p.m) p.argmax[(int64_t)m * tiles + 2 * blockIdx.x + nw] = best;
+        uint32_t b2 = row_best[mi];
+        b2 = max(b2, (uint32_t)__shfl_xor(b2, 16));
+        b2 = max(b2, (uint32_t)__shfl_xor(b2, 32));
+        if (p.argmax != nullptr && g == 0 && m < p.m) {
+          const uint32_t n = (uint32_t)rc0 + 0xFFFFu - (b2 & 0xFFFFu);
+          p.argmax[(int64_t)m * tiles + 2 * blockIdx.x + nw] =
+              b2 == 0 ? 0 : ((uint64_t)(b2 >> 16) << 32) | (uint64_t)(0xFFFFFFFFu - n);
+        }
         row_best[mi] = 0;
       }
     }
@@ -966,6 +994,8 @@ extern "C" int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, 
   NE_CHECK_ARG(logits || argmax_partials, "lm head needs logits and/or argmax_partials");
   NE_CHECK_SUPPORTED(k % 128 == 0, "k must be a multiple of 128 (got %d)", k);
   NE_CHECK_SUPPORTED(n % 128 == 0, "vocab must be a multiple of 128 (got %d)", n);
+  // argmax keys hold a column within a work-group's range in 16 bits
+  NE_CHECK_SUPPORTED(n <= (1 << 24), "vocab above 2^24 (got %d)", n);
   NE_CHECK_ARG(ldx >= k && ldx % 8 == 0, "ldx must be >= k and a multiple of 8");
   NE_CHECK_ARG(!logits || (ld_logits >= n && ld_logits % 4 == 0), "bad ld_logits");
   NE_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 &&

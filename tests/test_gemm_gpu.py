@@ -127,6 +127,30 @@ def test_lm_head_logits_and_argmax(device, m, vocab):
     assert torch.equal(idx[clear], torch.argmax(ref, dim=1)[clear])
 
 
+def test_lm_head_argmax_ties_pick_the_first_column(device):
+    """Exact ties: copies of a winning embedding row placed after it -- in the same lane,
+    the next 16 columns, other blocks of the range and other work-groups' ranges -- must
+    lose to the first copy (torch.argmax's first-index rule)."""
+    vocab, m = 16512, 24
+    g = torch.Generator().manual_seed(7)
+    embed = (torch.randn(vocab, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    targets = torch.randint(0, vocab - 4096, (m,), generator=g)
+    for j, t in enumerate(targets.tolist()):
+        for off in (1, 2, 17, 64, 130, 256 + j, 700, 4000):
+            embed[t + off] = embed[t]
+    # a copy may land on another row's target: the winner is the first row equal to the
+    # (final) target row, whose own logit 40 |e|^2 ~ 16 dwarfs any other row's (~N(0, 0.5))
+    first = torch.tensor([int((embed == embed[t]).all(dim=1).nonzero().min()) for t in targets.tolist()])
+    assert len(set(first.tolist())) > m // 2
+    hidden = (embed[targets].float() * 40).to(torch.bfloat16)
+    logits, partials = kernels.lm_head(hidden.to(device), embed.to(device), logits=True, argmax_partials=True)
+    torch.cuda.synchronize()
+    p = partials.cpu().numpy().view(np.uint64)
+    idx = torch.from_numpy((0xFFFFFFFF - (p.max(axis=1) & np.uint64(0xFFFFFFFF))).astype(np.int64))
+    assert torch.equal(idx, torch.argmax(logits.float().cpu(), dim=1))
+    assert torch.equal(idx, first)
+
+
 def test_lm_head_argmax_only_matches_logits_path(device):
     hidden = (torch.randn(64, 1024) * 0.02).to(torch.bfloat16).to(device)
     embed = (torch.randn(8192, 1024) * 0.02).to(torch.bfloat16).to(device)
