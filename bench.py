@@ -154,6 +154,10 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
     log("prefill done")
     for _ in range(warmup):
         eng.runner.step()
+    # no step in flight when the clock starts: the runner may have launched one ahead
+    eng.runner.drain()
+    if eng.runner.pending:
+        eng.runner.step()
     ctx_per_step, lengths_per_step = [], []
     # HIP events around each step's device work (graph replay, or the eager launches) on
     # the stream it runs on: the step's wall time minus this is the host's share
@@ -181,9 +185,13 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
         for _ in range(steps):
             lengths = eng.runner.np_len.copy()
             records.append((lengths, eng.runner.step()))
-    torch.cuda.synchronize()
+    # step() returns once its step's outputs are on the host; the runner may already
+    # have launched the next step (its outputs are not counted, so neither is its time)
     elapsed = time.perf_counter() - start
+    eng.runner.drain()
+    torch.cuda.synchronize()
     eng.runner._run_device_step = device_step
+    device_events = device_events[: len(records)]
     device_us = 1e3 * sum(b.elapsed_time(e) for b, e in device_events) / max(len(device_events), 1)
     tokens = proposed = accepted = 0
     kept_hist: dict[int, int] = {}

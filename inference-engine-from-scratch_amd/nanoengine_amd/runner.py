@@ -101,8 +101,7 @@ class VerifyRunner:
         self.R = self.k + 1
         self.max_seqs = max_seqs
         self.max_ngram = max_ngram
-        self.stop_token_ids = frozenset(stop_token_ids)
-        self._stop_ids = tuple(sorted(self.stop_token_ids))
+        self.stop_token_ids = stop_token_ids
         self.block_size = allocator.block_size
         self.max_model_len = max_model_len
         self.capacity = max_model_len + self.R
@@ -162,6 +161,12 @@ class VerifyRunner:
         # whether the device drafts / num_drafts already hold this step's n-gram guesses
         # (proposed at the end of the previous step, no sequence admitted since)
         self._drafts_ready = False
+        # a step launched ahead by the previous step() call (not yet waited for), and the
+        # results of one finished early because the batch changed
+        self._ahead = None
+        self._pending: dict[int, StepResult] | None = None
+        self.run_ahead = True  # False: every step launches and finishes in its own call
+        self.ahead_launches = 0
         # a plain paged allocator hands out blocks from the head of a FIFO free list, so a
         # step's new table entries are known before the allocator records them
         self._fifo_blocks = type(allocator) is PagedSlotAllocator
@@ -223,6 +228,16 @@ class VerifyRunner:
         return [i for i, s in enumerate(self.slots) if s is None]
 
     @property
+    def stop_token_ids(self) -> frozenset[int]:
+        return self._stop_token_ids
+
+    @stop_token_ids.setter
+    def stop_token_ids(self, ids) -> None:
+        """The per-step bookkeeping matches emitted tokens against a sorted tuple."""
+        self._stop_token_ids = frozenset(ids)
+        self._stop_ids = tuple(sorted(self._stop_token_ids))
+
+    @property
     def any_sampled(self) -> bool:
         """Whether some active slot samples (temperature > 0)."""
         if self._sampled is None:
@@ -236,6 +251,7 @@ class VerifyRunner:
         free = self.free_slots()
         if len(sequences) > len(free):
             raise ValueError(f"only {len(free)} free sequence slots")
+        self.drain()
         for seq in sequences:
             problem = request_length_error(seq.num_tokens, seq.sampling_params.max_new_tokens, self.max_model_len)
             if problem is not None:
@@ -421,12 +437,47 @@ class VerifyRunner:
         self.graph.replay()
 
     def step(self) -> dict[int, StepResult]:
-        """One verify step over every active slot; returns what each slot emitted."""
+        """One verify step over every active slot; returns what each slot emitted.
+
+        When nothing can change the batch before the next step (no slot can finish in
+        this one, n-gram guesses, the plain paged allocator, a captured graph, no trace),
+        the next step is launched as soon as this one's outputs are read back, before its
+        tokens are appended to the sequences: the device runs it while the host does that
+        bookkeeping, and the next call waits for it instead of launching one.  A batch
+        change (add, release) first finishes such a step and keeps its results for the
+        next call."""
+        if self._pending is not None:
+            results, self._pending = self._pending, None
+            return results
+        launched, self._ahead = self._ahead, None
+        if launched is None:
+            launched = self._launch()
+            if launched is None:
+                return {}
+        torch.cuda.current_stream(self.device).synchronize()
+        return self._complete(launched, allow_ahead=True)
+
+    @property
+    def pending(self) -> bool:
+        """Whether a finished step's results wait for the next step() call."""
+        return self._pending is not None
+
+    def drain(self) -> None:
+        """Finish a step launched ahead (before the batch changes, or before the device
+        is used for something else); its results are returned by the next step() call."""
+        if self._ahead is not None:
+            launched, self._ahead = self._ahead, None
+            torch.cuda.current_stream(self.device).synchronize()
+            self._pending = self._complete(launched, allow_ahead=False) or None
+
+    def _launch(self):
+        """Guesses, block growth and the device step of one verify step, up to its
+        outputs' read-back copy (not waited for); None when no slot is active."""
         if self._active is None:
             self._active = [i for i, s in enumerate(self.slots) if s is not None]
         active = self._active
         if not active:
-            return {}
+            return None
         slots = self.slots
         act = self.np_active.copy()
         ngram = self.proposer is None
@@ -487,6 +538,7 @@ class VerifyRunner:
                     np_tables[s, owned : owned + len(added)] = added
                     np_owned[s] = owned + len(added)
             self.block_tables.copy_(self.h_tables, non_blocking=True)
+        traced_drafts = None
         if self.trace is not None:  # the device step overwrites the guesses with the next step's
             torch.cuda.current_stream(self.device).synchronize()
             traced_drafts = {s: self.drafts[s, : int(np_num_drafts[s])].tolist() for s in active}
@@ -494,7 +546,32 @@ class VerifyRunner:
         self.h_step_out[self._read_back].copy_(self.step_out, non_blocking=True)
         if deferred is not None:
             allocator.take_free([slots[s] for s in deferred[0]], deferred[1], deferred[2])
-        torch.cuda.current_stream(self.device).synchronize()
+        return active, act, traced_drafts
+
+    def _may_run_ahead(self, act: np.ndarray) -> bool:
+        """Whether the next step can be launched before this one's bookkeeping: nothing
+        but this step's own outputs decides it, and no slot finishes in this step."""
+        if (not self.run_ahead or self.proposer is not None or self.trace is not None or not self._fifo_blocks
+                or not self.use_graph
+                or self.graph is None or self.graph_sampled != self.any_sampled or len(self._stop_ids) > 64):
+            return False
+        out, num_out = self.np_out, self.np_num_out
+        if ((self.np_gen + num_out * act >= self.np_max_new) & act).any():
+            return False
+        if self._stop_ids:
+            hon = self.np_honours_stop & act
+            if hon.any():
+                rows = np.arange(out.shape[1])[None, :] < num_out[:, None]
+                if (np.isin(out, self._stop_ids) & rows & hon[:, None]).any():
+                    return False
+        return True
+
+    def _complete(self, launched, allow_ahead: bool) -> dict[int, StepResult]:
+        """The host side of a step whose outputs have been read back."""
+        active, act, traced_drafts = launched
+        slots = self.slots
+        np_num_drafts = self.np_num_drafts
+        ngram = self.proposer is None
         if self.trace is not None:
             self.trace.append({
                 s: {
@@ -506,6 +583,28 @@ class VerifyRunner:
                 }
                 for s in active
             })
+        if allow_ahead and self._may_run_ahead(act):
+            # the mirrors advance now (finish_step below advances copies of the old ones);
+            # this step's outputs stay in their read-back buffer, which the next step does
+            # not write; its guess counts are in the buffer the next step reads back into
+            out, num_out = self.np_out, self.np_num_out
+            guesses = np_num_drafts.copy()
+            lengths, generated, steps = self.np_len.copy(), self.np_gen.copy(), self.np_steps.copy()
+            emitted = num_out * act
+            self.np_len += emitted
+            self.np_gen += emitted
+            self.np_steps += act
+            self._read_back ^= 1
+            self._bind_read_back()
+            self._drafts_ready = True
+            self._ahead = self._launch()
+            self.ahead_launches += 1
+            results, finishing = host_step.finish_step(
+                active, slots, out, num_out, guesses, act, lengths, generated, steps, self.np_max_new,
+                self.np_honours_stop, self._stop_ids, StepResult, None,
+            )
+            assert not finishing
+            return results
         # the mirrors advance by the emitted counts and every slot that cannot finish this
         # step appends its tokens; slots at their length limit or with a stop token
         # emitted (when they honour stops) finish one token at a time below
@@ -561,6 +660,13 @@ class VerifyRunner:
         seq = self.slots[slot]
         if seq is None:
             return
+        if self._ahead is not None:
+            self.drain()
+            self._pending.pop(slot, None)
+            if not self._pending:
+                self._pending = None
+            if self.slots[slot] is None:  # it finished in the drained step
+                return
         self.allocator.free(seq)
         if self.proposer is not None:
             self.proposer.release(slot)

@@ -414,6 +414,52 @@ def test_long_prompt_admitted_after_graph_capture_matches_eager():
     assert all(len(v) == 20 for v in graphed.values())
 
 
+# ------------------------------------------------------------------ launch-ahead
+def test_launch_ahead_matches_step_by_step():
+    """With HIP graphs the runner launches a step before the previous one's host
+    bookkeeping when the batch cannot change in between.  More requests than slots
+    (admissions between steps, which finish the early step first), differing lengths
+    and a stop token (a slot finishing, where no step may be launched early) exercise
+    the points where it must not; every request's events equal those of the same run
+    with launch-ahead off, and a serial request closed early (release of a slot whose
+    next step is already running) leaves no reserved blocks and the next request intact."""
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(6, seed=51)
+    lens = [10, 24, 17, 31, 12, 20]
+
+    def run(ahead, stop):
+        eng = engine_for(state, 3, graphs=True)
+        eng.runner.run_ahead = ahead
+        if stop is not None:
+            eng.runner.stop_token_ids = frozenset({stop})
+        reqs = [GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=n, ignore_eos=i % 2 == 0))
+                for i, (p, n) in enumerate(zip(prompts, lens))]
+        out = eng.batched_generator().generate_all(reqs)
+        return eng, {k: [(e.token_id, e.finish_reason) for e in v] for k, v in out.items()}
+
+    _, free_run = run(False, None)
+    stop = free_run["r3"][9][0]  # a token r3 emits mid-way; r1, r3, r5 honour stops
+    eng, ahead = run(True, stop)
+    assert eng.runner.ahead_launches > 0
+    _, plain = run(False, stop)
+    assert ahead == plain
+    assert any(v[-1][1] == "stop" for v in plain.values())
+    assert eng.allocator.num_reserved_slots == 0
+
+    serial = engine_for(state, 1, graphs=True)
+    params = SamplingParams(max_new_tokens=40, ignore_eos=True)
+    gen = serial.serial_generator().generate(GenerationRequest("a", prompts[0], params))
+    first = [next(gen).token_id for _ in range(15)]
+    assert serial.runner.ahead_launches > 0
+    gen.close()
+    assert serial.allocator.num_reserved_slots == 0
+    full = [e.token_id for e in serial.serial_generator().generate(GenerationRequest("b", prompts[0], params))]
+    off = engine_for(state, 1, graphs=True)
+    off.runner.run_ahead = False
+    want = [e.token_id for e in off.serial_generator().generate(GenerationRequest("c", prompts[0], params))]
+    assert full == want and full[:15] == first and len(full) == 40
+
+
 # ------------------------------------------------------------------ metrics
 def test_acceptance_metrics_equal_the_per_step_recount():
     """EngineMetrics' proposed / accepted counters (metrics.py:66-75, incremented as

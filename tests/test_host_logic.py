@@ -180,3 +180,15 @@ def test_peek_then_take_equals_reserving_in_slot_order(steps, frees):
         for r in (f"r{j}" for j in range(6)):
             assert one.block_table(r) == two.block_table(r)
         assert list(one._blocks._free) == list(two._blocks._free)
+
+
+def test_stop_ids_set_after_construction_reach_the_step_bookkeeping():
+    """The per-step bookkeeping (the C finish_step) matches tokens against the sorted
+    tuple behind VerifyRunner.stop_token_ids; assigning the set later updates it."""
+    from nanoengine_amd.runner import VerifyRunner
+
+    runner = VerifyRunner.__new__(VerifyRunner)
+    runner.stop_token_ids = {7, 3}
+    assert runner.stop_token_ids == frozenset({3, 7}) and runner._stop_ids == (3, 7)
+    runner.stop_token_ids = frozenset()
+    assert runner._stop_ids == ()
