@@ -99,8 +99,19 @@ __device__ __forceinline__ void write_vectors(const float (&a)[N], const float (
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       s[i] = fmaxf(s[i], 1e-8f) / 127.f;
-      const float qa = fminf(fmaxf(rintf(a[i] / s[i]), -127.f), 127.f);
-      const float qb = fminf(fmaxf(rintf(b[i] / s[i]), -127.f), 127.f);
+      // x / s as x * v_rcp_f32(s): relative error < 2e-7, so < 3e-5 at |x / s| <= 127,
+      // and rint of it equals rint of the correctly rounded quotient unless it lies
+      // within 1e-4 of a rounding tie; a wave with such a lane takes the exact divisions
+      // (a uniform branch, skipped by most waves)
+      const float rcp = __builtin_amdgcn_rcpf(s[i]);
+      float ta = a[i] * rcp, tb = b[i] * rcp;
+      const bool near = fabsf(ta - rintf(ta)) > 0.4999f || fabsf(tb - rintf(tb)) > 0.4999f;
+      if (__builtin_amdgcn_ballot_w64(near) != 0) {
+        ta = a[i] / s[i];
+        tb = b[i] / s[i];
+      }
+      const float qa = fminf(fmaxf(rintf(ta), -127.f), 127.f);
+      const float qb = fminf(fmaxf(rintf(tb), -127.f), 127.f);
       if (valid[i]) {
         int8_t* c = (int8_t*)cache + (slot[i] * num_heads + head) * 128;
         c[lane] = (int8_t)(int)qa;

@@ -84,6 +84,15 @@ def test_kv_write_int8_bit_exact(device, vec_dtype):
     n, heads = 40, 8
     vectors = (torch.randn(n, heads, 128) * torch.rand(n, heads, 1) * 4).to(vec_dtype)
     vectors[3, 2] = 0  # all-zero vector: scale clamps to 1e-8 / 127
+    # exact rounding ties: max 127 / 8 gives scale 1 / 8, so x / s = k + 0.5 (rint: to even)
+    ties = (torch.arange(128) % 64 - 32 + 0.5) / 8
+    ties[0] = 127 / 8
+    vectors[5, 1] = ties.to(vec_dtype)
+    vectors[6, 4] = (-ties).to(vec_dtype)
+    # quotients near k + 0.5 for a scale that is not a power of two
+    near = ((torch.arange(128) % 100) - 50 + 0.5) * (3.7 / 127)
+    near[0] = 3.7
+    vectors[7, 0] = near.to(vec_dtype)
     slots = torch.randperm(100)[:n].to(torch.int32)
     cache = torch.zeros(101, heads, 128, dtype=torch.int8, device=device)
     scales = torch.zeros(101, heads, dtype=vec_dtype, device=device)
