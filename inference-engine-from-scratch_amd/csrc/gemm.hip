@@ -113,6 +113,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // fragments of stage t from LDS before it runs the MFMAs of stage t - 1 (held in
 // registers), so the LDS latency hides under the multiplies.
 constexpr int kPM = 5;  // token subtiles per work-group (the fused QKV epilogue uses 3)
+constexpr int kQkvKRows = 32;  // rows per work-group of the fused QKV kernel's k heads (q / v: 48)
 
 template <int NSUB, int PM, int KG, int NPW>
 struct ProjLayout {
@@ -360,11 +361,31 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM, KG, NPW>::kThreads)) void pro
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
   const int jj = bid / kNumXcd;
-  const int tm = jj % p.tiles_m;
-  const int tn = (jj / p.tiles_m) * kNumXcd + xcd;  // the M tiles of one weight tile share an XCD
+  int tm = jj % p.tiles_m;
+  int tn = (jj / p.tiles_m) * kNumXcd + xcd;  // the M tiles of one weight tile share an XCD
+  int tile_rows = kPRows;
+  if constexpr (EPI == 4) {
+    // heads xcd, xcd + 8, ... on this XCD, each with all its row tiles: kPRows rows for
+    // q / v heads, kQkvKRows for k heads (whose epilogue also quantises, so fewer rows
+    // per work-group even out the work-groups' end times)
+    int j = jj;
+    tn = -1;
+    for (int h = xcd; h < p.tiles_n; h += kNumXcd) {
+      const bool kh = h >= qa.hq && h < qa.hq + qa.hkv;
+      const int t = kh ? qa.tiles_k : p.tiles_m;
+      if (j < t) {
+        tn = h;
+        tm = j;
+        tile_rows = kh ? kQkvKRows : kPRows;
+        break;
+      }
+      j -= t;
+    }
+    if (tn < 0) return;
+  }
   if (tn >= p.tiles_n) return;
   const int split = blockIdx.y;
-  const int m0 = tm * kPRows;
+  const int m0 = tm * tile_rows;
   const int n0 = tn * NSUB * 16;
   const int kbase = split * k_per_split;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -448,30 +469,39 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM, KG, NPW>::kThreads)) void pro
         *(floatx4*)(part + (kg * kPRows + mi * 16 + r) * kRowF + (nw * NPW + ns) * 16 + 4 * g) = acc[mi][ns];
     lds_barrier();
     // this wave's rows all at once, so that their reductions overlap
-    int rows_e[kEpiRows];
-    bool valid_e[kEpiRows];
-    float a_e[kEpiRows], b_e[kEpiRows], c_e[kEpiRows], s_e[kEpiRows];
-    int64_t slot_e[kEpiRows];
+    auto rows_pass = [&](auto n_rows) {
+      constexpr int N = decltype(n_rows)::value;
+      int rows_e[N];
+      bool valid_e[N];
+      float a_e[N], b_e[N], c_e[N], s_e[N];
+      int64_t slot_e[N];
 #pragma unroll
-    for (int i = 0; i < kEpiRows; ++i) {
-      const int rr = min(wave + L::kWaves * i, kPRows - 1);
-      rows_e[i] = m0 + rr;
-      valid_e[i] = wave + L::kWaves * i < kPRows && m0 + rr < p.m;
-      float va = part[rr * kRowF + lane];
-      float vb = part[rr * kRowF + 64 + lane];
+      for (int i = 0; i < N; ++i) {
+        const int rr = min(wave + L::kWaves * i, kPRows - 1);
+        rows_e[i] = m0 + rr;
+        valid_e[i] = wave + L::kWaves * i < tile_rows && m0 + rr < p.m;
+        float va = part[rr * kRowF + lane];
+        float vb = part[rr * kRowF + 64 + lane];
 #pragma unroll
-      for (int q = 1; q < KG; ++q) {
-        va += part[(q * kPRows + rr) * kRowF + lane];
-        vb += part[(q * kPRows + rr) * kRowF + 64 + lane];
+        for (int q = 1; q < KG; ++q) {
+          va += part[(q * kPRows + rr) * kRowF + lane];
+          vb += part[(q * kPRows + rr) * kRowF + 64 + lane];
+        }
+        a_e[i] = bf16_round(va * e_sc[0]);
+        b_e[i] = bf16_round(vb * e_sc[1]);
+        c_e[i] = bf16_to_f32(e_rc[i]);
+        s_e[i] = bf16_to_f32(e_rs[i]);
+        slot_e[i] = e_slot[i];
       }
-      a_e[i] = bf16_round(va * e_sc[0]);
-      b_e[i] = bf16_round(vb * e_sc[1]);
-      c_e[i] = bf16_to_f32(e_rc[i]);
-      s_e[i] = bf16_to_f32(e_rs[i]);
-      slot_e[i] = e_slot[i];
+      qk_norm_rope_kv_vectors<kInt8, kKvSdt, N>(qa, rows_e, valid_e, tn, lane, a_e, b_e, slot_e,
+                                                bf16_to_f32(e_w[0]), bf16_to_f32(e_w[1]), c_e, s_e);
+    };
+    static_assert(kQkvKRows % L::kWaves == 0 && kQkvKRows / L::kWaves <= kEpiRows, "k-tile rows per wave");
+    if (tile_rows == kQkvKRows) {
+      rows_pass(std::integral_constant<int, kQkvKRows / L::kWaves>{});
+    } else {
+      rows_pass(std::integral_constant<int, kEpiRows>{});
     }
-    qk_norm_rope_kv_vectors<kInt8, kKvSdt, kEpiRows>(qa, rows_e, valid_e, tn, lane, a_e, b_e, slot_e,
-                                                     bf16_to_f32(e_w[0]), bf16_to_f32(e_w[1]), c_e, s_e);
     return;
   }
   // Token subtile mi is finished by k-group mi % KG: each wave hands the partial tiles of
@@ -536,12 +566,24 @@ __global__ __launch_bounds__((ProjLayout<NSUB, PM, KG, NPW>::kThreads)) void pro
 
 template <int NSUB, int SDT, int EPI, int KV, int PM, int KG, int NPW, int KT>
 int launch_proj_kt(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
-                   const QkvRopeArgs& qa) {
+                   QkvRopeArgs qa) {
   using L = ProjLayout<NSUB, PM, KG, NPW>;
   p.tiles_m = ceil_div(p.m, L::kPRows);
   p.tiles_n = p.n / (NSUB * 16);
   const int tiles_n_padded = ceil_div(p.tiles_n, kNumXcd) * kNumXcd;
-  const dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
+  dim3 grid((unsigned)(p.tiles_m * tiles_n_padded), (unsigned)splits);
+  if constexpr (EPI == 4) {
+    // per XCD: its heads' row tiles (k heads in tiles of kQkvKRows); the grid covers the
+    // XCD with the most
+    qa.tiles_k = ceil_div(p.m, kQkvKRows);
+    int most = 0;
+    for (int x = 0; x < kNumXcd; ++x) {
+      int t = 0;
+      for (int h = x; h < p.tiles_n; h += kNumXcd) t += (h >= qa.hq && h < qa.hq + qa.hkv) ? qa.tiles_k : p.tiles_m;
+      most = t > most ? t : most;
+    }
+    grid.x = (unsigned)(most * kNumXcd);
+  }
   static const hipError_t attr = hipFuncSetAttribute(
       (const void*)proj_kernel<NSUB, SDT, EPI, KV, PM, KG, NPW, KT>, hipFuncAttributeMaxDynamicSharedMemorySize,
       L::kLds);

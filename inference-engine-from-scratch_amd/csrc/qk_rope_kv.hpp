@@ -28,6 +28,7 @@ struct QkvRopeArgs {
   void* k_scale;                 // [slots][hkv] (int8 cache only)
   void* v_scale;
   uint16_t* q_out;               // [rows][hq][128] bf16
+  int tiles_k;                   // row tiles of the k heads (set by the launch)
 };
 
 // Sums / maxima over the wave of N independent values, every lane ending with the same
