@@ -660,8 +660,10 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
 // of W, then runs its 80 MFMAs on the current one.  Spreading the weight copies (HBM
 // misses) over all waves keeps any one wave from queueing behind them; the two waves of
 // a SIMD still finish a stage apart, the older one ahead.  Stages run on across
-// blocks.  Rows beyond m re-read row m - 1 and are never stored; more than 320 rows
-// take further passes.
+// blocks.  A range of ~9.3 groups ends in a short block of one or two groups: there the
+// waves whose 128 columns are all past the end skip their MFMAs and the weight copies of
+// absent rows are not issued (~23 % of the MFMAs were on such columns).  Rows beyond m
+// re-read row m - 1 and are never stored; more than 320 rows take further passes.
 constexpr int kLmMaxGrid = 256;  // persistent work-groups (one per CU)
 constexpr int kLmRows = 320;
 constexpr int kLmCols = 256;
@@ -716,6 +718,9 @@ __device__ __forceinline__ void lm_issue(const GemmParams& p, char* stage, const
   const char* wsrc = uniform_ptr((const char*)p.w + ((int64_t)st.c0 * p.k + st.k0) * 2);
 #pragma unroll
   for (int j = 0; j < kLmInstr; ++j) {
+    // weight slot j * 8 + wave - 40 holds rows (slot) 8 .. + 8 of the block: not copied when
+    // they are all past a short block's end (those rows' MFMA outputs are never used)
+    if (j >= kLmXCopies && (j * kLmWaves + wave - kLmXBytes / 1024) * 8 >= st.ccols) continue;
     uint32_t o = c.off[j];
     __asm__("" : "+v"(o));  // scalar base + 32-bit lane offset addressing
     lds_dma16((j < kLmXCopies ? xsrc : wsrc) + o, stage + (j * kLmWaves + wave) * 1024);
@@ -826,8 +831,9 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
       off_m0 = nst.m0;
       off_cols = nst.ccols;
     }
+    const int cur_cols = cur.ccols;
     if (more) lm_issue(p, smem + ((u + 1) & 1) * kLmStage, nst, copies, wave);
-    lm_mma(smem + (u & 1) * kLmStage, mw, nw, lane, acc);
+    if (nw * 128 < cur_cols) lm_mma(smem + (u & 1) * kLmStage, mw, nw, lane, acc);
     const bool block_done = t == kt - 1;
     const bool pass_done = block_done && (!more || npass != pass);
     const LmStage st = cur;
