@@ -73,3 +73,33 @@ def test_finish_step_matches_python(seed, stops):
         if a is not None:
             assert a.token_ids == b.token_ids and a.num_cached_tokens == b.num_cached_tokens
             assert a.sampling_generator.step == b.sampling_generator.step
+
+
+@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("stops", [(), (7, 300, 599)])
+def test_launch_ahead_check_matches_the_finishing_slots(seed, stops):
+    """VerifyRunner._may_run_ahead (numpy, before the next step is launched) is True
+    exactly when finish_step would report no finishing slot for the same outputs: the
+    length limit and the stop tokens of slots that honour them, read the same way."""
+    from nanoengine_amd.runner import VerifyRunner
+
+    st = _state(seed)
+    rng = np.random.default_rng(100 + seed)
+    # limits near the emitted counts, so that some seeds finish nothing and some finish a few
+    st["max_new"] = st["gen"] + st["nout"] + rng.integers(0 if seed % 2 else 1, 4, st["gen"].shape[0])
+    if not stops:
+        st["honours"][:] = False
+    runner = VerifyRunner.__new__(VerifyRunner)
+    runner.run_ahead, runner.proposer, runner.trace = True, None, None
+    runner._fifo_blocks, runner.use_graph, runner.graph = True, True, object()
+    runner.graph_sampled, runner._sampled = False, False
+    runner.stop_token_ids = stops
+    runner.np_out, runner.np_num_out = st["out"], st["nout"]
+    runner.np_gen, runner.np_max_new, runner.np_honours_stop = st["gen"], st["max_new"], st["honours"]
+    ahead = runner._may_run_ahead(st["act"])
+    slots = copy.deepcopy(st["slots"])
+    _, finishing = host_step.finish_step_py(
+        [i for i in range(len(slots)) if slots[i] is not None], slots, st["out"], st["nout"], st["nd"],
+        st["act"], st["lengths"].copy(), st["gen"].copy(), st["steps"].copy(), st["max_new"], st["honours"],
+        tuple(sorted(stops)), StepResult, None)
+    assert ahead == (not finishing)
