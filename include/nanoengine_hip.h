@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NE_ABI_VERSION 9
+#define NE_ABI_VERSION 10
 
 /* status codes */
 #define NE_OK 0
@@ -366,6 +366,20 @@ int ne_prepare_verify_step(const int32_t* history, int64_t history_stride,
 int ne_advance_step_counts(const int32_t* history_len, const int32_t* num_out,
                            const int32_t* max_new_tokens, int32_t* num_generated, uint64_t* steps,
                            int32_t* num_guesses, int32_t k, int32_t num_seqs, void* stream);
+
+/*
+ * ne_advance_step_counts followed by ne_ngram_propose in one launch (the tail of a
+ * verify step: speculative_generator.py:71-72, then NgramProposer.propose of
+ * ne/engine/speculative/proposers.py:39-57 for the next step).  The work-group of
+ * sequence b advances b's counters exactly as ne_advance_step_counts does, writes
+ * num_guesses[b], and proposes up to min(num_guesses[b], max_drafts) guesses from b's
+ * history as ne_ngram_propose does with num_tokens = num_guesses.
+ */
+int ne_advance_and_propose(const int32_t* history, int64_t history_stride, const int32_t* history_len,
+                           const int32_t* num_out, const int32_t* max_new_tokens, int32_t* num_generated,
+                           uint64_t* steps, int32_t* num_guesses, int32_t k, int32_t num_seqs,
+                           int32_t max_ngram, int32_t min_ngram, int32_t max_drafts, int32_t* drafts,
+                           int32_t* num_drafts, void* stream);
 
 /* Plain device copy of `bytes` bytes (16-byte aligned); used to calibrate the
  * hardware byte counters against a kernel of known traffic. */

@@ -22,17 +22,49 @@ constexpr int kMaxNgram = 16;
 constexpr int kScanPerThread = 4;
 constexpr int kScanChunk = 256 * kScanPerThread;
 
+// The counters a verify step leaves for the next one (adv != nullptr): the work-group of
+// sequence b first advances b's counters and takes its guess count from them.
+struct StepCounters {
+  const int32_t* num_out;
+  const int32_t* max_new;
+  int32_t* generated;
+  uint64_t* steps;
+  int32_t* num_guesses;
+  int k;
+};
+
 __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int64_t stride,
                                                     const int32_t* history_len,
                                                     const int32_t* num_tokens, int max_ngram,
                                                     int min_ngram, int max_drafts, int32_t* drafts,
-                                                    int32_t* num_drafts) {
+                                                    int32_t* num_drafts, StepCounters adv) {
   __shared__ int s_best[kMaxNgram][256 / kWave];
+  __shared__ int s_want;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int32_t* h = history + (int64_t)b * stride;
   const int len = history_len[b];
-  const int want = min(num_tokens[b], max_drafts);
+  int requested;
+  if (adv.num_out != nullptr) {
+    // ne_advance_step_counts for slot b, by one thread; the others take its count after
+    // the barrier, so none reads a counter after it was advanced
+    if (tid == 0) {
+      int g = 0;
+      if (len > 0) {
+        const int gen = adv.generated[b] + adv.num_out[b];
+        adv.generated[b] = gen;
+        adv.steps[b] += 1;
+        g = max(0, min(adv.k, adv.max_new[b] - gen - 1));
+      }
+      adv.num_guesses[b] = g;
+      s_want = g;
+    }
+    __syncthreads();
+    requested = s_want;
+  } else {
+    requested = num_tokens[b];
+  }
+  const int want = min(requested, max_drafts);
   const int nmax = min(max_ngram, len - 1);  // n < len
   if (want <= 0 || nmax < min_ngram) {
     if (tid == 0) num_drafts[b] = 0;
@@ -131,6 +163,29 @@ extern "C" int ne_ngram_propose(const int32_t* history, int64_t history_stride,
   NE_CHECK_ARG(history_stride >= 1, "history_stride must be >= 1");
   hipLaunchKernelGGL(ngram_kernel, dim3(num_seqs), dim3(256), 0, (hipStream_t)stream, history,
                      history_stride, history_len, num_tokens, max_ngram, min_ngram, max_drafts,
-                     drafts, num_drafts);
+                     drafts, num_drafts, StepCounters{});
   return check_launch("ngram_propose");
+}
+
+extern "C" int ne_advance_and_propose(const int32_t* history, int64_t history_stride,
+                                      const int32_t* history_len, const int32_t* num_out,
+                                      const int32_t* max_new_tokens, int32_t* num_generated,
+                                      uint64_t* steps, int32_t* num_guesses, int32_t k, int32_t num_seqs,
+                                      int32_t max_ngram, int32_t min_ngram, int32_t max_drafts,
+                                      int32_t* drafts, int32_t* num_drafts, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0 && k >= 0, "bad sizes (num_seqs=%d, k=%d)", num_seqs, k);
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(history && history_len && num_out && max_new_tokens && num_generated && steps && num_guesses &&
+                   drafts && num_drafts,
+               "null pointer argument");
+  NE_CHECK_ARG(min_ngram >= 1 && max_ngram >= min_ngram, "need 1 <= min_ngram <= max_ngram");
+  NE_CHECK_SUPPORTED(max_ngram <= kMaxNgram, "max_ngram must be <= %d (got %d)", kMaxNgram,
+                     max_ngram);
+  NE_CHECK_ARG(max_drafts >= 1, "max_drafts must be >= 1");
+  NE_CHECK_ARG(history_stride >= 1, "history_stride must be >= 1");
+  const StepCounters adv{num_out, max_new_tokens, num_generated, steps, num_guesses, k};
+  hipLaunchKernelGGL(ngram_kernel, dim3(num_seqs), dim3(256), 0, (hipStream_t)stream, history,
+                     history_stride, history_len, num_guesses, max_ngram, min_ngram, max_drafts,
+                     drafts, num_drafts, adv);
+  return check_launch("advance_and_propose");
 }

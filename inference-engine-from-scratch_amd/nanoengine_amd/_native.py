@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libnanoengine_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # status codes (nanoengine_hip.h)
 NE_OK = 0
@@ -122,6 +122,10 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "ne_advance_step_counts": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u64p, _vp, _i32, _i32, _vp]),
+    "ne_advance_and_propose": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _vp, _vp, _vp, _u64p, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp],
+    ),
     "ne_copy_bytes": (ctypes.c_int, [_vp, _vp, _sz, _vp]),
 }
 SIGNATURES["ne_paged_verify_attention_planned"] = SIGNATURES["ne_paged_verify_attention"]

@@ -780,6 +780,30 @@ def advance_step_counts(history_len: torch.Tensor, num_out: torch.Tensor, max_ne
                  _ptr(num_generated), _ptr(steps), _ptr(num_guesses), k, n, _stream(device))
 
 
+def advance_and_propose(history: torch.Tensor, history_len: torch.Tensor, num_out: torch.Tensor,
+                        max_new_tokens: torch.Tensor, num_generated: torch.Tensor, steps: torch.Tensor,
+                        num_guesses: torch.Tensor, k: int, max_ngram: int, drafts: torch.Tensor,
+                        num_drafts: torch.Tensor, min_ngram: int = 1) -> None:
+    """:func:`advance_step_counts` then :func:`ngram_propose` with ``num_tokens =
+    num_guesses`` in one launch (the same results): the tail of a verify step."""
+    device = _require_gpu(history, history_len, num_out, max_new_tokens, num_generated, steps, num_guesses,
+                          drafts, num_drafts)
+    for name, t in (("history", history), ("history_len", history_len), ("num_out", num_out),
+                    ("max_new_tokens", max_new_tokens), ("num_generated", num_generated),
+                    ("num_guesses", num_guesses), ("drafts", drafts), ("num_drafts", num_drafts)):
+        _int32(t, name)
+    _check(steps.dtype == torch.int64 and steps.is_contiguous(), "steps must be contiguous int64")
+    _check(history.dim() == 2 and drafts.dim() == 2 and drafts.is_contiguous(),
+           "history [num_seqs, capacity], drafts [num_seqs, max_drafts]")
+    n = history.shape[0]
+    _check(all(t.numel() >= n for t in (history_len, num_out, max_new_tokens, num_generated, steps, num_guesses,
+                                        num_drafts)) and drafts.shape[0] >= n,
+           "per-sequence arrays shorter than the histories")
+    _native.call("ne_advance_and_propose", _ptr(history), history.stride(0), _ptr(history_len), _ptr(num_out),
+                 _ptr(max_new_tokens), _ptr(num_generated), _ptr(steps), _ptr(num_guesses), k, n, max_ngram,
+                 min_ngram, drafts.shape[1], _ptr(drafts), _ptr(num_drafts), _stream(device))
+
+
 def copy_bytes(src: torch.Tensor, dst: torch.Tensor) -> None:
     device = _require_gpu(src, dst)
     nbytes = src.numel() * src.element_size()

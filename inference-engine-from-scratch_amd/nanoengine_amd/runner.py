@@ -413,10 +413,9 @@ class VerifyRunner:
         )
         if self.proposer is None:
             # the next step's guess counts, then its n-gram guesses on the updated histories
-            kernels.advance_step_counts(self.history_len, self.num_out, self.max_new, self.generated, self.steps,
-                                        self.num_tokens, self.k)
-            kernels.ngram_propose(self.history, self.history_len, self.num_tokens, self.max_ngram, self.k,
-                                  drafts=self.drafts, num_drafts=self.num_drafts)
+            kernels.advance_and_propose(self.history, self.history_len, self.num_out, self.max_new,
+                                        self.generated, self.steps, self.num_tokens, self.k, self.max_ngram,
+                                        self.drafts, self.num_drafts)
 
     def _run_device_step(self) -> None:
         sampled = self.any_sampled

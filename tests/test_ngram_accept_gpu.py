@@ -53,6 +53,44 @@ def test_ngram_random_matches_oracle(device, vocab):
     assert got == want
 
 
+@pytest.mark.parametrize("k", [4, 8])
+def test_advance_and_propose_equals_advance_then_propose(device, k):
+    """The verify step's tail in one launch: counters, guess counts and drafts equal those
+    of ne_advance_step_counts followed by ne_ngram_propose on the same state, for active
+    and inactive slots and limits that leave 0 .. k guesses; the drafts equal the oracle's."""
+    rng = np.random.default_rng(40 + k)
+    n, cap = 64, 700
+    lens = rng.integers(0, 600, n).astype(np.int32)
+    lens[::9] = 0  # inactive slots
+    hist = torch.from_numpy(rng.integers(0, 6, (n, cap)).astype(np.int32))
+    num_out = torch.from_numpy(rng.integers(1, k + 2, n).astype(np.int32))
+    generated = torch.from_numpy(rng.integers(0, 100, n).astype(np.int32))
+    max_new = (generated + num_out + torch.from_numpy(rng.integers(0, k + 3, n).astype(np.int32))).to(torch.int32)
+    steps = torch.from_numpy(rng.integers(0, 1000, n).astype(np.int64))
+    hl = torch.from_numpy(lens)
+    ins = [t.to(device) for t in (hist, hl, num_out, max_new, generated, steps)]
+    a = [t.clone() for t in ins]  # separate launches
+    guesses_a = torch.full((n,), -1, dtype=torch.int32, device=device)
+    kernels.advance_step_counts(a[1], a[2], a[3], a[4], a[5], guesses_a, k)
+    drafts_a, count_a = kernels.ngram_propose(a[0], a[1], guesses_a, 3, k)
+    b = [t.clone() for t in ins]  # one launch
+    guesses_b = torch.full((n,), -1, dtype=torch.int32, device=device)
+    drafts_b = torch.zeros(n, k, dtype=torch.int32, device=device)
+    count_b = torch.full((n,), -1, dtype=torch.int32, device=device)
+    kernels.advance_and_propose(b[0], b[1], b[2], b[3], b[4], b[5], guesses_b, k, 3, drafts_b, count_b)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    assert torch.equal(guesses_a, guesses_b) and torch.equal(count_a, count_b)
+    counts = count_b.cpu().tolist()
+    assert all(torch.equal(drafts_a[i, : counts[i]], drafts_b[i, : counts[i]]) for i in range(n))
+    g = guesses_b.cpu().tolist()
+    assert sorted(set(g)) == list(range(0, k + 1)) or len(set(g)) > 3
+    for i in range(n):
+        want = oracle_ngram.propose(hist[i, : lens[i]].tolist(), g[i], 3) if g[i] and lens[i] else []
+        assert drafts_b[i, : counts[i]].cpu().tolist() == want
+
+
 def test_ngram_long_history_k8(device):
     rng = np.random.default_rng(5)
     histories = [rng.integers(0, 20, size=17417).tolist() for _ in range(4)]
