@@ -104,7 +104,7 @@ def test_swiglu_epilogue(device, m):
     assert rel_err(out, ref) < TOL
 
 
-@pytest.mark.parametrize("m,vocab", [(320, 151936), (5, 4096), (70, 8192), (400, 16512)])
+@pytest.mark.parametrize("m,vocab", [(320, 151936), (5, 4096), (70, 8192), (400, 16512), (8, 180224)])
 def test_lm_head_logits_and_argmax(device, m, vocab):
     g = torch.Generator().manual_seed(vocab + m)
     hidden = (torch.randn(m, 1024, generator=g) * 0.02).to(torch.bfloat16)
