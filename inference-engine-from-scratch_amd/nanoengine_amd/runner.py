@@ -549,7 +549,9 @@ class VerifyRunner:
 
     def _may_run_ahead(self, act: np.ndarray) -> bool:
         """Whether the next step can be launched before this one's bookkeeping: nothing
-        but this step's own outputs decides it, and no slot finishes in this step."""
+        but this step's own outputs decides it, no slot finishes in this step, and the
+        free list holds the blocks the next step grows into (a pool that runs out raises
+        at the next call, after this step's tokens are appended)."""
         if (not self.run_ahead or self.proposer is not None or self.trace is not None or not self._fifo_blocks
                 or not self.use_graph
                 or self.graph is None or self.graph_sampled != self.any_sampled or len(self._stop_ids) > 64):
@@ -563,7 +565,9 @@ class VerifyRunner:
                 rows = np.arange(out.shape[1])[None, :] < num_out[:, None]
                 if (np.isin(out, self._stop_ids) & rows & hon[:, None]).any():
                     return False
-        return True
+        *_, blocks = host_step.plan_growth(self.np_len + num_out * act, self.np_num_drafts_next, self.np_owned, act,
+                                           self.block_size)
+        return blocks <= self.allocator.num_free_blocks
 
     def _complete(self, launched, allow_ahead: bool) -> dict[int, StepResult]:
         """The host side of a step whose outputs have been read back."""

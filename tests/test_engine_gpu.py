@@ -460,6 +460,45 @@ def test_launch_ahead_matches_step_by_step():
     assert full == want and full[:15] == first and len(full) == 40
 
 
+def test_launch_ahead_running_out_of_kv_blocks_keeps_every_emitted_token():
+    """A pool too small for the requests' growth: the runner raises OutOfKVMemoryError
+    from step() after the same number of steps with and without launch-ahead (which is
+    not taken when the free list cannot hold the next step's growth), and every token a
+    step() returned is in the sequence's token_ids."""
+    from nanoengine_amd.memory import OutOfKVMemoryError
+
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(3, seed=61)
+
+    def run(ahead):
+        # ~30 blocks of 16 tokens: three requests of 64 + up to 150 tokens cannot all grow
+        settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                                  quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                                  num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=3, max_model_len=256,
+                                  kv_cache_memory_mb=2, cuda_graphs=True)
+        eng = create_verify_engine(CFG, state, settings, max_prefill_rows=192)
+        eng.runner.run_ahead = ahead
+        seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=150,
+                                                                                   ignore_eos=True)))
+                for i, p in enumerate(prompts)]
+        emitted = {}
+        for s, r in eng.runner.add(seqs).items():
+            emitted.setdefault(s, []).extend(r.tokens)
+        steps = 0
+        with pytest.raises(OutOfKVMemoryError):
+            while True:
+                for s, r in eng.runner.step().items():
+                    emitted[s].extend(r.tokens)
+                steps += 1
+        return steps, emitted, [list(s.token_ids) for s in seqs], eng.runner.ahead_launches
+
+    steps, emitted, ids, launches = run(True)
+    assert launches > 0 and steps > 2
+    for slot, seq_ids in enumerate(ids):
+        assert seq_ids[len(prompts[slot]):] == emitted[slot]
+    assert (steps, emitted, ids) == run(False)[:3]
+
+
 # ------------------------------------------------------------------ metrics
 def test_acceptance_metrics_equal_the_per_step_recount():
     """EngineMetrics' proposed / accepted counters (metrics.py:66-75, incremented as

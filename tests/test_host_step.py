@@ -96,10 +96,18 @@ def test_launch_ahead_check_matches_the_finishing_slots(seed, stops):
     runner.stop_token_ids = stops
     runner.np_out, runner.np_num_out = st["out"], st["nout"]
     runner.np_gen, runner.np_max_new, runner.np_honours_stop = st["gen"], st["max_new"], st["honours"]
+    runner.np_len, runner.np_owned, runner.block_size = st["lengths"], st["owned"], 16
+    runner.np_num_drafts_next = st["nd"]
+    _, _, _, need = host_step.plan_growth(st["lengths"] + st["nout"] * st["act"], st["nd"], st["owned"], st["act"], 16)
+
+    class Pool:
+        num_free_blocks = need + (seed % 3) - 1  # one short, exactly enough, one spare
+
+    runner.allocator = Pool()
     ahead = runner._may_run_ahead(st["act"])
     slots = copy.deepcopy(st["slots"])
     _, finishing = host_step.finish_step_py(
         [i for i in range(len(slots)) if slots[i] is not None], slots, st["out"], st["nout"], st["nd"],
         st["act"], st["lengths"].copy(), st["gen"].copy(), st["steps"].copy(), st["max_new"], st["honours"],
         tuple(sorted(stops)), StepResult, None)
-    assert ahead == (not finishing)
+    assert ahead == (not finishing and Pool.num_free_blocks >= need)
