@@ -575,7 +575,7 @@ class VerifyRunner:
         slots = self.slots
         np_num_drafts = self.np_num_drafts
         ngram = self.proposer is None
-        if self.trace is not None:
+        if self.trace is not None and traced_drafts is not None:  # a step launched before tracing began is not recorded
             self.trace.append({
                 s: {
                     "history": list(self.slots[s].token_ids),
