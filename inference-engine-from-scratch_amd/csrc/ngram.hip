@@ -86,11 +86,16 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
     for (int j = 0; j < kScanPerThread; ++j) {
       const int e = hi - j * 256 - tid;
       if (e >= 0) {
+        // the window's tokens are all requested before the first comparison, so the
+        // loads overlap instead of waiting on one another's match
+        int tok[kMaxNgram];
+#pragma unroll
+        for (int i = 0; i < kMaxNgram; ++i) tok[i] = (i < nmax && e - i >= 0) ? h[e - i] : 0;
         int c = 0;  // tokens ending at e that equal those ending at len - 1
         bool same = true;
 #pragma unroll
         for (int i = 0; i < kMaxNgram; ++i) {
-          if (same && i < nmax && e - i >= 0 && h[e - i] == suffix[i]) {
+          if (same && i < nmax && e - i >= 0 && tok[i] == suffix[i]) {
             ++c;
           } else {
             same = false;
