@@ -453,32 +453,38 @@ __device__ int draw_residual(const Dist& d, const DistLds& L, const Dist& dq, co
 
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
   __shared__ uint64_t s_red[kThreads / kWave];
+  __shared__ uint64_t s_rows[kMaxRows][kThreads / kWave];
   __shared__ float s_redf[kThreads / kWave];
   __shared__ DistLds s_d, s_dq;
   __shared__ float s_tmp[kChunks];
   __shared__ int s_target[kMaxRows];
   __shared__ int s_kept, s_final;
   __shared__ float s_accept;
+  static_assert(kMaxRows <= kWave, "one lane of wave 0 per row");
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  if (p.history != nullptr && p.history_len[b] == 0) {  // inactive sequence slot
-    for (int i = tid; i <= p.max_drafts; i += kThreads)
-      p.out_tokens[(int64_t)b * (p.max_drafts + 1) + i] = -1;
+  // the sequence's scalars and thread i's guess (i < max_drafts) are requested together:
+  // one memory round trip before the LM-head partials
+  const int len = p.history != nullptr ? p.history_len[b] : 0;
+  const int nd = p.num_drafts[b];
+  const int rs0 = p.row_start[b];
+  const float T = p.temperature != nullptr ? p.temperature[b] : 0.f;
+  const int32_t* dr = p.drafts + (int64_t)b * p.max_drafts;
+  const int my_draft = tid < p.max_drafts ? dr[tid] : 0;
+  if (p.history != nullptr && len == 0) {  // inactive sequence slot
+    if (tid <= p.max_drafts) p.out_tokens[(int64_t)b * (p.max_drafts + 1) + tid] = -1;
     if (tid == 0) p.num_out[b] = 0;
     return;
   }
   // a draft count beyond max_drafts would index past s_target and the draft row
-  const int g = min(max(p.num_drafts[b], 0), p.max_drafts);
-  const int rs0 = p.row_start[b];
-  const int32_t* dr = p.drafts + (int64_t)b * p.max_drafts;
-  const float T = p.temperature != nullptr ? p.temperature[b] : 0.f;
+  const int g = min(max(nd, 0), p.max_drafts);
   const int V = p.vocab;
 
   if (!(T > 0.f)) {
     if (p.logits == nullptr) {
-      // the rows' LM-head partials are loaded together, then reduced one row after
-      // another: one memory round trip for all of them
+      // the rows' LM-head partials are loaded together and reduced together: one
+      // memory round trip and one barrier for all of them
       uint64_t best[kMaxRows];
       if (p.num_tiles <= 2 * kThreads) {  // the LM head's 512 keys per row: two per thread
         uint64_t v[kMaxRows][2];
@@ -503,10 +509,24 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
       }
 #pragma unroll
       for (int i = 0; i < kMaxRows; ++i) {
-        if (i <= g) {
-          const uint64_t v = block_max_u64(best[i], s_red);
-          if (tid == 0) s_target[i] = (int)(0xFFFFFFFFu - (uint32_t)v);
+        if (i <= g) {  // uniform
+          uint64_t v = best[i];
+#pragma unroll
+          for (int o = 32; o >= 1; o >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)v, o);
+            const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o);
+            const uint64_t w = ((uint64_t)hi << 32) | lo;
+            v = v > w ? v : w;
+          }
+          if (tid % kWave == 0) s_rows[i][tid / kWave] = v;
         }
+      }
+      __syncthreads();
+      if (tid <= g) {  // lane i of wave 0 finishes row i
+        uint64_t r = s_rows[tid][0];
+#pragma unroll
+        for (int w = 1; w < kThreads / kWave; ++w) r = r > s_rows[tid][w] ? r : s_rows[tid][w];
+        s_target[tid] = (int)(0xFFFFFFFFu - (uint32_t)r);
       }
     } else {
       for (int i = 0; i <= g; ++i) {
@@ -515,11 +535,15 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
       }
     }
     __syncthreads();
-    if (tid == 0) {
-      int kept = 0;
-      while (kept < g && dr[kept] == s_target[kept]) ++kept;
-      s_kept = kept;
-      s_final = s_target[kept];
+    if (tid < kWave) {
+      // kept = the number of leading guesses equal to their row's target (bit g of the
+      // ballot is clear, so kept <= g)
+      const uint64_t same = __builtin_amdgcn_ballot_w64(tid < g && my_draft == s_target[tid]);
+      if (tid == 0) {
+        const int kept = __builtin_ctzll(~same);
+        s_kept = kept;
+        s_final = s_target[kept];
+      }
     }
     __syncthreads();
   } else {
@@ -579,16 +603,16 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
 
   const int kept = s_kept;
   const int fin = s_final;
-  for (int i = tid; i <= p.max_drafts; i += kThreads)
-    p.out_tokens[(int64_t)b * (p.max_drafts + 1) + i] = (i < kept) ? dr[i] : (i == kept ? fin : -1);
+  // thread i writes token i (kept < g <= max_drafts, so my_draft holds guess i < kept)
+  if (tid <= p.max_drafts)
+    p.out_tokens[(int64_t)b * (p.max_drafts + 1) + tid] = (tid < kept) ? my_draft : (tid == kept ? fin : -1);
   if (tid == 0) p.num_out[b] = kept + 1;
   if (p.history != nullptr) {
     // a history row holds hist_stride tokens: tokens past it are not written (the host
     // refuses requests whose prompt + max_new_tokens exceed the rows' capacity)
-    const int len = p.history_len[b];
     const int room = (int)min((int64_t)(kept + 1), max(p.hist_stride - len, (int64_t)0));
     int32_t* h = p.history + (int64_t)b * p.hist_stride;
-    for (int i = tid; i < room; i += kThreads) h[len + i] = (i < kept) ? dr[i] : fin;
+    if (tid < room) h[len + tid] = (tid < kept) ? my_draft : fin;
     __syncthreads();
     if (tid == 0) {
       p.history_len[b] = len + room;
