@@ -44,39 +44,39 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
   const int tid = threadIdx.x;
   const int32_t* h = history + (int64_t)b * stride;
   const int len = history_len[b];
-  int requested;
+  int requested = 0;
   if (adv.num_out != nullptr) {
-    // ne_advance_step_counts for slot b, by one thread; the others take its count after
-    // the barrier, so none reads a counter after it was advanced
+    // ne_advance_step_counts for slot b, by one thread, whose loads go out with the
+    // length's; the others take its count after the scan's first barrier (or the one
+    // below when there is no scan), so none reads a counter after it was advanced
     if (tid == 0) {
+      const int gen0 = adv.generated[b], out = adv.num_out[b], cap = adv.max_new[b];
+      const uint64_t steps = adv.steps[b];
       int g = 0;
       if (len > 0) {
-        const int gen = adv.generated[b] + adv.num_out[b];
+        const int gen = gen0 + out;
         adv.generated[b] = gen;
-        adv.steps[b] += 1;
-        g = max(0, min(adv.k, adv.max_new[b] - gen - 1));
+        adv.steps[b] = steps + 1;
+        g = max(0, min(adv.k, cap - gen - 1));
       }
       adv.num_guesses[b] = g;
       s_want = g;
     }
-    __syncthreads();
-    requested = s_want;
   } else {
     requested = num_tokens[b];
   }
-  const int want = min(requested, max_drafts);
   const int nmax = min(max_ngram, len - 1);  // n < len
-  if (want <= 0 || nmax < min_ngram) {
-    if (tid == 0) num_drafts[b] = 0;
-    return;
-  }
+  // the scan does not depend on the guess count, so it starts before the count is known;
+  // a slot that wants no guesses still scans (its answer is then dropped)
+  const bool scan = nmax >= min_ngram;  // uniform; then len >= 2 and the loop runs
   int suffix[kMaxNgram];  // the history read backwards from its last token
 #pragma unroll
   for (int i = 0; i < kMaxNgram; ++i) suffix[i] = (i < nmax) ? h[len - 1 - i] : 0;
   int found[kMaxNgram];  // found[n - 1]: the largest end e of an n-window match so far
 #pragma unroll
   for (int i = 0; i < kMaxNgram; ++i) found[i] = -1;
-  for (int hi = len - 2; hi >= 0; hi -= kScanChunk) {
+  if (!scan) __syncthreads();  // uniform: publishes s_want
+  for (int hi = scan ? len - 2 : -1; hi >= 0; hi -= kScanChunk) {
     // thread tid tests ends hi - tid, hi - tid - 256, ...: its first hit for each n is
     // its largest, and the owner of the chunk's largest hit has no larger one
     int best[kMaxNgram];
@@ -130,6 +130,12 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
     for (int i = 0; i < kMaxNgram; ++i)
       if (i == nmax - 1) done = found[i] >= 0;
     if (done) break;  // uniform: the largest n has its answer
+  }
+  if (adv.num_out != nullptr) requested = s_want;
+  const int want = min(requested, max_drafts);
+  if (want <= 0 || !scan) {
+    if (tid == 0) num_drafts[b] = 0;
+    return;
   }
   // the largest n with a match
   int e = -1;
