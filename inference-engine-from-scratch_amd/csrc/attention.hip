@@ -1008,6 +1008,13 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
   __shared__ int s_seq[8];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
+  // tile j = tid's block-table entry is requested before the scan, for a tile that
+  // starts below max_ctx and an entry inside the row's stride (a table narrower than
+  // max_ctx needs is not read past its rows); it is used only when tid < tiles, and
+  // every such tile passes both bounds
+  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+  const int first_entry = tid * kTileKeys / p.block_size;
+  const int first_block = tid * kTileKeys < p.max_ctx && first_entry < p.bt_stride ? bt_row[first_entry] : 0;
   const PlanScan ps = plan_scan(p, s_plan);
   if (2 * tid == b || 2 * tid + 1 == b) {
     const int k = (2 * tid == b) ? 0 : 1;
@@ -1036,7 +1043,6 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
     d[6] = s_seq[5];
     d[7] = (int)((int64_t)tiles * (s + 1) / n);
   }
-  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   for (int j = tid; j < tiles; j += kHeadWaves * kWave) {
     // split s holds tiles [tiles s / n, tiles (s + 1) / n); tile j is in the last split
     // whose start is <= j
@@ -1045,7 +1051,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attention_plan_kernel(Attn
     if (w >= p.plan_grid) continue;
     const int t = j - (int)((int64_t)tiles * s / n);
     const int key0 = j * kTileKeys;
-    p.plan_slots[(int64_t)w * kPlanMaxTiles + t] = bt_row[key0 / p.block_size] * p.block_size + key0 % p.block_size;
+    const int block = j == tid ? first_block : bt_row[key0 / p.block_size];
+    p.plan_slots[(int64_t)w * kPlanMaxTiles + t] = block * p.block_size + key0 % p.block_size;
   }
 }
 
