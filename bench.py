@@ -141,7 +141,8 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
                               quantization="int8", kv_cache_dtype="int8",
                               speculative="draft" if draft else "ngram",
                               num_speculative_tokens=K_DRAFT, ngram_max_size=3, max_num_seqs=NUM_SEQS,
-                              max_model_len=max_len, kv_cache_memory_mb=2048, cuda_graphs=args.graph)
+                              max_model_len=max_len, kv_cache_memory_mb=2048, cuda_graphs=args.graph,
+                              cuda_graph_max_batch=NUM_SEQS, cuda_graph_max_context=max_len + K_DRAFT + 1)
     eng = create_verify_engine(cfg, state, settings, max_prefill_rows=NUM_SEQS * PROMPT_MOTIF * PROMPT_REPEATS,
                                draft_config=cfg if draft else None, draft_state_dict=state if draft else None)
     del state
@@ -264,6 +265,7 @@ def run_verify_long(args, torch, steps: int = 10, warmup: int = 2):
                               quantization="int8", kv_cache_dtype="int8", speculative="ngram",
                               num_speculative_tokens=LONG_K, ngram_max_size=3, max_num_seqs=LONG_SEQS,
                               max_model_len=max_len, prefix_cache=True, cuda_graphs=args.graph,
+                              cuda_graph_max_batch=LONG_SEQS, cuda_graph_max_context=max_len + LONG_K + 1,
                               kv_cache_memory_mb=int(math.ceil(tokens_needed * per_token / 2**20)) + 64)
     eng = create_verify_engine(cfg, state, settings, max_prefill_rows=LONG_PREFILL_ROWS)
     del state

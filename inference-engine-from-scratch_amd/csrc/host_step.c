@@ -178,6 +178,67 @@ static PyObject* make_result(PyObject* type, PyObject* tokens, long guesses, lon
   return PyObject_CallFunction(type, "NOll", tokens, Py_None, guesses, kept);
 }
 
+/* One active slot of finish_step: advance its sampling step, then either queue it for the
+   one-token-at-a-time finish (fin[s]) or append its tokens, set num_cached_tokens, call
+   on_cached and record its result.  Returns nonzero with a Python error set. */
+static int finish_slot(PyObject* seq, PyObject* key, Py_ssize_t s, Py_ssize_t R, const int32_t* out,
+                       const int32_t* nout, const int32_t* nd, const unsigned char* fin, PyObject* o_type,
+                       PyObject* o_cached, PyObject* results, PyObject* finishing) {
+  const int32_t n = nout[s];
+  /* seq.sampling_generator.step += 1 */
+  PyObject* gobj = PyObject_GetAttr(seq, s_sampling_generator);
+  if (!gobj) return 1;
+  PyObject* st = PyObject_GetAttr(gobj, s_step);
+  PyObject* st1 = st ? PyNumber_Add(st, s_one) : NULL;
+  int err = !st1 || PyObject_SetAttr(gobj, s_step, st1);
+  Py_XDECREF(st);
+  Py_XDECREF(st1);
+  Py_DECREF(gobj);
+  if (err) return 1;
+  PyObject* tokens = PyList_New(n);
+  if (!tokens) return 1;
+  for (int32_t j = 0; j < n; ++j) {
+    PyObject* v = PyLong_FromLong(out[s * R + j]);
+    if (!v) {
+      Py_DECREF(tokens);
+      return 1;
+    }
+    PyList_SET_ITEM(tokens, j, v);
+  }
+  if (fin[s]) {
+    PyObject* pair = Py_BuildValue("(nN)", s, tokens);
+    err = !pair || PyDict_SetItem(results, key, Py_None) || PyList_Append(finishing, pair);
+    Py_XDECREF(pair);
+    return err;
+  }
+  PyObject* ids = PyObject_GetAttr(seq, s_token_ids);
+  if (!ids || !PyList_Check(ids)) {
+    Py_XDECREF(ids);
+    Py_DECREF(tokens);
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "token_ids must be a list");
+    return 1;
+  }
+  const Py_ssize_t old = PyList_GET_SIZE(ids);
+  err = PyList_SetSlice(ids, old, old, tokens);
+  PyObject* cached = err ? NULL : PyLong_FromSsize_t(PyList_GET_SIZE(ids) - 1);
+  Py_DECREF(ids);
+  err = err || !cached || PyObject_SetAttr(seq, s_num_cached_tokens, cached);
+  Py_XDECREF(cached);
+  if (!err && o_cached != Py_None) {
+    PyObject* r = PyObject_CallOneArg(o_cached, seq);
+    err = !r;
+    Py_XDECREF(r);
+  }
+  if (err) {
+    Py_DECREF(tokens);
+    return 1;
+  }
+  PyObject* res = make_result(o_type, tokens, nd[s], n - 1);
+  err = !res || PyDict_SetItem(results, key, res);
+  Py_XDECREF(res);
+  return err;
+}
+
 static PyObject* finish_step(PyObject* self, PyObject* args) {
   PyObject *o_active, *o_slots, *o_out, *o_nout, *o_nd, *o_act, *o_len, *o_gen, *o_steps, *o_max, *o_hon,
       *o_stops, *o_type, *o_cached;
@@ -225,13 +286,25 @@ static PyObject* finish_step(PyObject* self, PyObject* args) {
     PyErr_NoMemory();
     goto fail;
   }
+  /* every input check comes before the first change to a mirror */
+  for (Py_ssize_t s = 0; s < S; ++s) {
+    if (act[s] && (nout[s] < 0 || nout[s] > R)) {
+      PyErr_Format(PyExc_ValueError, "slot %zd emitted %d tokens (at most %zd)", s, nout[s], R);
+      goto fail;
+    }
+  }
+  const Py_ssize_t na = PyList_GET_SIZE(o_active), ns = PyList_GET_SIZE(o_slots);
+  for (Py_ssize_t i = 0; i < na; ++i) {
+    const Py_ssize_t s = PyLong_AsSsize_t(PyList_GET_ITEM(o_active, i));
+    if (PyErr_Occurred()) goto fail;
+    if (s < 0 || s >= S || s >= ns || !act[s] || PyList_GET_ITEM(o_slots, s) == Py_None) {
+      PyErr_Format(PyExc_ValueError, "active slot %zd out of range, inactive or empty", s);
+      goto fail;
+    }
+  }
   for (Py_ssize_t s = 0; s < S; ++s) {
     if (!act[s]) continue;
     const int32_t e = nout[s];
-    if (e < 0 || e > R) {
-      PyErr_Format(PyExc_ValueError, "slot %zd emitted %d tokens (at most %zd)", s, e, R);
-      goto fail;
-    }
     len[s] += e;
     gen[s] += e;
     steps[s] += 1;
@@ -249,70 +322,15 @@ static PyObject* finish_step(PyObject* self, PyObject* args) {
   results = PyDict_New();
   finishing = PyList_New(0);
   if (!results || !finishing) goto fail;
-  const Py_ssize_t na = PyList_GET_SIZE(o_active), ns = PyList_GET_SIZE(o_slots);
   for (Py_ssize_t i = 0; i < na; ++i) {
     PyObject* key = PyList_GET_ITEM(o_active, i);
     const Py_ssize_t s = PyLong_AsSsize_t(key);
-    if (PyErr_Occurred()) goto fail;
-    if (s < 0 || s >= S || s >= ns || !act[s]) {
-      PyErr_Format(PyExc_ValueError, "active slot %zd out of range or inactive", s);
-      goto fail;
-    }
+    /* held across the calls back into Python below (a callback may change the slot list) */
     PyObject* seq = PyList_GET_ITEM(o_slots, s);
-    const int32_t n = nout[s];
-    /* seq.sampling_generator.step += 1 */
-    PyObject* gobj = PyObject_GetAttr(seq, s_sampling_generator);
-    if (!gobj) goto fail;
-    PyObject* st = PyObject_GetAttr(gobj, s_step);
-    PyObject* st1 = st ? PyNumber_Add(st, s_one) : NULL;
-    int err = !st1 || PyObject_SetAttr(gobj, s_step, st1);
-    Py_XDECREF(st);
-    Py_XDECREF(st1);
-    Py_DECREF(gobj);
-    if (err) goto fail;
-    PyObject* tokens = PyList_New(n);
-    if (!tokens) goto fail;
-    for (int32_t j = 0; j < n; ++j) {
-      PyObject* v = PyLong_FromLong(out[s * R + j]);
-      if (!v) {
-        Py_DECREF(tokens);
-        goto fail;
-      }
-      PyList_SET_ITEM(tokens, j, v);
-    }
-    if (fin[s]) {
-      PyObject* pair = Py_BuildValue("(nN)", s, tokens);
-      err = !pair || PyDict_SetItem(results, key, Py_None) || PyList_Append(finishing, pair);
-      Py_XDECREF(pair);
-      if (err) goto fail;
-      continue;
-    }
-    PyObject* ids = PyObject_GetAttr(seq, s_token_ids);
-    if (!ids || !PyList_Check(ids)) {
-      Py_XDECREF(ids);
-      Py_DECREF(tokens);
-      if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "token_ids must be a list");
-      goto fail;
-    }
-    const Py_ssize_t old = PyList_GET_SIZE(ids);
-    err = PyList_SetSlice(ids, old, old, tokens);
-    PyObject* cached = err ? NULL : PyLong_FromSsize_t(PyList_GET_SIZE(ids) - 1);
-    Py_DECREF(ids);
-    err = err || !cached || PyObject_SetAttr(seq, s_num_cached_tokens, cached);
-    Py_XDECREF(cached);
-    if (!err && o_cached != Py_None) {
-      PyObject* r = PyObject_CallOneArg(o_cached, seq);
-      err = !r;
-      Py_XDECREF(r);
-    }
-    if (err) {
-      Py_DECREF(tokens);
-      goto fail;
-    }
-    PyObject* res = make_result(o_type, tokens, nd[s], n - 1);
-    err = !res || PyDict_SetItem(results, key, res);
-    Py_XDECREF(res);
-    if (err) goto fail;
+    Py_INCREF(seq);
+    const int err_seq = finish_slot(seq, key, s, R, out, nout, nd, fin, o_type, o_cached, results, finishing);
+    Py_DECREF(seq);
+    if (err_seq) goto fail;
   }
   PyMem_Free(fin);
   release(b, 10);
@@ -324,7 +342,6 @@ fail:
   Py_XDECREF(finishing);
   return NULL;
 }
-
 static PyMethodDef methods[] = {
     {"plan_growth", plan_growth, METH_VARARGS, "slots that need KV blocks this step, their counts and targets"},
     {"assign_blocks", assign_blocks, METH_VARARGS, "write peeked blocks into the host block tables"},

@@ -66,9 +66,10 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
     requested = num_tokens[b];
   }
   const int nmax = min(max_ngram, len - 1);  // n < len
-  // the scan does not depend on the guess count, so it starts before the count is known;
-  // a slot that wants no guesses still scans (its answer is then dropped)
-  const bool scan = nmax >= min_ngram;  // uniform; then len >= 2 and the loop runs
+  // the scan does not depend on the guess count, so with the step counters it starts
+  // before the count is known and stops after its first chunk when the count is 0; a
+  // count passed in (num_tokens, read by every thread) of 0 skips it
+  const bool scan = nmax >= min_ngram && (adv.num_out != nullptr || requested > 0);  // uniform
   int suffix[kMaxNgram];  // the history read backwards from its last token
 #pragma unroll
   for (int i = 0; i < kMaxNgram; ++i) suffix[i] = (i < nmax) ? h[len - 1 - i] : 0;
@@ -130,6 +131,7 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
     for (int i = 0; i < kMaxNgram; ++i)
       if (i == nmax - 1) done = found[i] >= 0;
     if (done) break;  // uniform: the largest n has its answer
+    if (adv.num_out != nullptr && s_want <= 0) break;  // uniform: published before the barriers above
   }
   if (adv.num_out != nullptr) requested = s_want;
   const int want = min(requested, max_drafts);

@@ -40,7 +40,20 @@ def finish_step_py(active, slots, out, num_out, num_drafts, act, lengths, genera
     """(results, finishing): mirrors advance by the emitted counts; each active slot's
     sampling step advances; a slot that may finish (length limit, or a stop token emitted
     by a slot that honours stops) gets None in results and (slot, tokens) in finishing;
-    any other appends its tokens and gets result_type(tokens, None, guesses, emitted - 1)."""
+    any other appends its tokens and gets result_type(tokens, None, guesses, emitted - 1).
+
+    Emitted counts outside [0, out.shape[1]] and active slots that are out of range,
+    inactive or empty raise ValueError before any mirror changes.  A failure after that
+    (token_ids not a list, on_cached raising) leaves the mirrors advanced and only some
+    slots' tokens appended: the runner that called it must then be discarded."""
+    width = out.shape[1]
+    bad = act.astype(bool) & ((num_out < 0) | (num_out > width))
+    if bad.any():
+        s = int(np.flatnonzero(bad)[0])
+        raise ValueError(f"slot {s} emitted {int(num_out[s])} tokens (at most {width})")
+    for s in active:
+        if not (0 <= s < len(act) and s < len(slots) and act[s] and slots[s] is not None):
+            raise ValueError(f"active slot {s} out of range, inactive or empty")
     emitted = num_out * act
     lengths += emitted
     generated += emitted

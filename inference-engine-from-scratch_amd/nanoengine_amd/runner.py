@@ -64,6 +64,18 @@ def request_length_error(num_prompt_tokens: int, max_new_tokens: int, max_model_
     return None
 
 
+def verify_graph_allowed(num_active: int, step_context: int, max_batch: int | None,
+                         max_context: int | None) -> bool:
+    """Whether a verify step may replay the captured HIP graph.  As the reference bounds
+    its decode graphs by ``cuda_graph_max_batch`` and ``cuda_graph_max_context``
+    (config.py:58-61, runtime.py:150-160, cuda_graph_runner.py:106-117), a step with more
+    active sequences, or whose longest sequence attends to more tokens (its length plus
+    the k guess rows), runs eagerly.  None leaves that bound off."""
+    if max_batch is not None and num_active > max_batch:
+        return False
+    return max_context is None or step_context <= max_context
+
+
 class StepResult(NamedTuple):
     """Tokens emitted for one sequence by one step, with its finish reason if it ended."""
 
@@ -86,6 +98,8 @@ class VerifyRunner:
         stop_token_ids: frozenset[int] = frozenset(),
         use_graph: bool = False,
         proposer: "DraftModelProposer | None" = None,
+        graph_max_batch: int | None = None,
+        graph_max_context: int | None = None,
     ) -> None:
         self.model = model
         # None: n-gram drafting on the device histories; else a draft model's greedy guesses
@@ -107,6 +121,11 @@ class VerifyRunner:
         self.capacity = max_model_len + self.R
         self.max_blocks = math.ceil(self.capacity / self.block_size)
         self.use_graph = use_graph
+        # steps beyond these bounds run eagerly (verify_graph_allowed); a capture that ran
+        # out of device memory leaves the runner eager for good
+        self.graph_max_batch = graph_max_batch
+        self.graph_max_context = graph_max_context
+        self.graph_failed = False
         model.ensure_rope(self.capacity)
         if self.max_seqs * self.R > model.max_rows:
             raise ValueError("model activation buffers are smaller than max_seqs * (k + 1) rows")
@@ -225,7 +244,11 @@ class VerifyRunner:
         self._sampled = None
 
     def free_slots(self) -> list[int]:
-        return [i for i, s in enumerate(self.slots) if s is None]
+        """Empty slots.  A slot whose sequence finished in a step whose results wait for
+        the next step() call (``pending``) is not free until that call has returned them,
+        so a result is never reported under a slot that a new request already holds."""
+        waiting = self._pending or ()
+        return [i for i, s in enumerate(self.slots) if s is None and i not in waiting]
 
     @property
     def stop_token_ids(self) -> frozenset[int]:
@@ -248,10 +271,10 @@ class VerifyRunner:
     def add(self, sequences: list[Sequence]) -> list[int]:
         """Place sequences in free slots, reserve their prompts, prefill them and emit
         the first token of each (model_runner.py:33-50 + speculative_generator.py:50-53)."""
+        self.drain()
         free = self.free_slots()
         if len(sequences) > len(free):
             raise ValueError(f"only {len(free)} free sequence slots")
-        self.drain()
         for seq in sequences:
             problem = request_length_error(seq.num_tokens, seq.sampling_params.max_new_tokens, self.max_model_len)
             if problem is not None:
@@ -417,9 +440,20 @@ class VerifyRunner:
                                         self.generated, self.steps, self.num_tokens, self.k, self.max_ngram,
                                         self.drafts, self.num_drafts)
 
+    def graph_allowed(self, lengths: np.ndarray | None = None) -> bool:
+        """Whether the step over the active slots, at ``lengths`` (default: the current
+        host mirrors), replays the captured graph rather than running eagerly."""
+        if not self.use_graph or self.graph_failed:
+            return False
+        act = self.np_active
+        n = int(act.sum())
+        lengths = self.np_len if lengths is None else lengths
+        context = int(lengths[act].max()) + self.k if n else 0
+        return verify_graph_allowed(n, context, self.graph_max_batch, self.graph_max_context)
+
     def _run_device_step(self) -> None:
         sampled = self.any_sampled
-        if not self.use_graph:
+        if not self.graph_allowed():
             self._device_step(sampled)
             return
         if self.graph is None or self.graph_sampled != sampled:
@@ -427,9 +461,18 @@ class VerifyRunner:
             # workspaces); the capture below only records, so nothing runs twice
             self._device_step(sampled)
             torch.cuda.current_stream(self.device).synchronize()
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
-                self._device_step(sampled)
+            graph = torch.cuda.CUDAGraph()
+            try:
+                with torch.cuda.graph(graph):
+                    self._device_step(sampled)
+            except torch.cuda.OutOfMemoryError:
+                # as cuda_graph_runner.py:193-207: without the memory to capture, every
+                # later step runs eagerly (this one already ran)
+                self.graph, self.graph_failed = None, True
+                del graph
+                torch.cuda.empty_cache()
+                return
+            self.graph = graph
             self.model.bind_graph()
             self.graph_sampled = sampled
             return
@@ -553,10 +596,11 @@ class VerifyRunner:
         free list holds the blocks the next step grows into (a pool that runs out raises
         at the next call, after this step's tokens are appended)."""
         if (not self.run_ahead or self.proposer is not None or self.trace is not None or not self._fifo_blocks
-                or not self.use_graph
                 or self.graph is None or self.graph_sampled != self.any_sampled or len(self._stop_ids) > 64):
             return False
         out, num_out = self.np_out, self.np_num_out
+        if not self.graph_allowed(self.np_len + num_out * act):  # the next step would run eagerly
+            return False
         if ((self.np_gen + num_out * act >= self.np_max_new) & act).any():
             return False
         if self._stop_ids:
@@ -660,16 +704,16 @@ class VerifyRunner:
         return StepResult(emitted, reason, g, kept)
 
     def release(self, slot: int) -> None:
-        seq = self.slots[slot]
-        if seq is None:
-            return
-        if self._ahead is not None:
-            self.drain()
+        """Free a slot.  A result of the slot still waiting for the next step() call is
+        dropped with it (the caller has given the slot up)."""
+        self.drain()
+        if self._pending is not None:
             self._pending.pop(slot, None)
             if not self._pending:
                 self._pending = None
-            if self.slots[slot] is None:  # it finished in the drained step
-                return
+        seq = self.slots[slot]
+        if seq is None:  # empty, or it finished in the drained step
+            return
         self.allocator.free(seq)
         if self.proposer is not None:
             self.proposer.release(slot)

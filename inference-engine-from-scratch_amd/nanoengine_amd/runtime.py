@@ -83,5 +83,7 @@ def create_verify_engine(config: Qwen3Config, state_dict: dict[str, torch.Tensor
                                       k=settings.num_speculative_tokens, use_graph=settings.cuda_graphs)
     runner = VerifyRunner(model, pool, allocator, max_seqs, settings.num_speculative_tokens,
                           settings.ngram_max_size, settings.max_model_len, stop_token_ids,
-                          use_graph=settings.cuda_graphs, proposer=proposer)
+                          use_graph=settings.cuda_graphs, proposer=proposer,
+                          graph_max_batch=settings.cuda_graph_max_batch,
+                          graph_max_context=settings.cuda_graph_max_context)
     return VerifyEngine(settings, model, pool, allocator, runner, EngineMetrics())

@@ -142,7 +142,7 @@ class BatchedSpeculativeGenerator:
         events: dict[str, list[TokenEvent]] = {r.request_id: [] for r in requests}
         pending = list(zip(requests, sequences, strict=True))
         slot_request: dict[int, GenerationRequest] = {}
-        while pending or self._runner.active_slots:
+        while pending or self._runner.active_slots or self._runner.pending:
             free = self._runner.free_slots()
             if pending and free:
                 batch = pending[: len(free)]

@@ -55,7 +55,8 @@ def engine(state, draft_cfg, draft_state, num_seqs, graphs=False):
     settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
                               quantization="int8", kv_cache_dtype="int8", speculative="draft",
                               num_speculative_tokens=4, max_num_seqs=num_seqs, max_model_len=256,
-                              kv_cache_memory_mb=64, cuda_graphs=graphs)
+                              kv_cache_memory_mb=64, cuda_graphs=graphs,
+                              cuda_graph_max_batch=num_seqs, cuda_graph_max_context=262)
     return create_verify_engine(CFG, state, settings, max_prefill_rows=64 * num_seqs,
                                 draft_config=draft_cfg, draft_state_dict=draft_state)
 

@@ -69,7 +69,7 @@ def engine_for(state, num_seqs, kv_int8=True, graphs=False, prefill_rows=None):
                               quantization="int8", kv_cache_dtype="int8" if kv_int8 else "auto",
                               speculative="ngram", num_speculative_tokens=4, ngram_max_size=3,
                               max_num_seqs=num_seqs, max_model_len=256, kv_cache_memory_mb=64,
-                              cuda_graphs=graphs)
+                              cuda_graphs=graphs, cuda_graph_max_batch=num_seqs, cuda_graph_max_context=262)
     return create_verify_engine(CFG, state, settings, max_prefill_rows=prefill_rows or 64 * num_seqs)
 
 
@@ -176,7 +176,7 @@ def prefix_engine(state, num_seqs, graphs=False):
                               quantization="int8", kv_cache_dtype="int8", speculative="ngram",
                               num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=num_seqs,
                               max_model_len=256, kv_cache_memory_mb=64, cuda_graphs=graphs,
-                              prefix_cache=True)
+                              prefix_cache=True, cuda_graph_max_batch=num_seqs, cuda_graph_max_context=262)
     return create_verify_engine(CFG, state, settings, max_prefill_rows=64 * num_seqs)
 
 
@@ -402,7 +402,7 @@ def test_long_prompt_admitted_after_graph_capture_matches_eager():
         settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
                                   quantization="int8", kv_cache_dtype="int8", speculative="ngram",
                                   num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=2, max_model_len=1280,
-                                  kv_cache_memory_mb=64, cuda_graphs=graphs)
+                                  kv_cache_memory_mb=64, cuda_graphs=graphs, cuda_graph_max_context=1286)
         eng = create_verify_engine(CFG, state, settings, max_prefill_rows=2048)
         out = eng.batched_generator().generate_all(reqs)
         return eng, {k: [e.token_id for e in v] for k, v in out.items()}
@@ -458,6 +458,159 @@ def test_launch_ahead_matches_step_by_step():
     off.runner.run_ahead = False
     want = [e.token_id for e in off.serial_generator().generate(GenerationRequest("c", prompts[0], params))]
     assert full == want and full[:15] == first and len(full) == 40
+
+
+def test_finished_slot_is_not_reused_before_its_pending_result_is_returned():
+    """A step launched ahead in which a sequence finishes, then finished early by add()
+    (a batch change): the finished slot's result waits for the next step() call, and until
+    then the slot is not free, so a later add() can neither take it nor have its first
+    result confused with the old sequence's last one.  Every request's tokens equal those
+    of the same admissions with launch-ahead off.
+
+    r0's limit is set one token past its length after a chosen step (its per-step counts
+    come from a calibration run with no limit; a capped guess count keeps the same
+    accepted prefix), so the next step has no guesses, emits one token and finishes it --
+    that step is the one launched ahead."""
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(4, seed=71)
+
+    def new_seqs(limit0):
+        return [Sequence.from_request(GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=n,
+                                                                                   ignore_eos=True)))
+                for i, (p, n) in enumerate(zip(prompts, [limit0, 60, 60, 60]))]
+
+    calib = engine_for(state, 1, graphs=True)
+    calib.runner.run_ahead = False
+    seq0 = new_seqs(150)[0]
+    counts = [len(r.tokens) for r in calib.runner.add([seq0]).values()]
+    while len(counts) < 4:
+        counts += [len(r.tokens) for r in calib.runner.step().values()]
+    made = np.cumsum(counts).tolist()  # r0's tokens after the prefill and steps 1, 2, 3
+    limit0 = made[3] + 1  # after step 3 one token short: step 4 (launched ahead) finishes r0
+
+    def run(ahead):
+        eng = engine_for(state, 3, graphs=True)
+        runner = eng.runner
+        runner.run_ahead = ahead
+        seqs = new_seqs(limit0)
+        got = {i: [] for i in range(4)}
+        owner = {}
+
+        def record(results):
+            for slot, r in results.items():
+                got[owner[slot]].extend(r.tokens)
+
+        def admit(i):
+            res = runner.add([seqs[i]])
+            for slot in res:
+                owner[slot] = i
+            record(res)
+
+        res = runner.add(seqs[:2])
+        for slot in res:
+            owner[slot] = seqs.index(runner.slots[slot])
+        record(res)
+        while len(got[0]) < made[3]:
+            record(runner.step())
+        assert len(got[0]) == made[3]
+        admit(2)  # with launch-ahead: finishes step 4 first, in which r0 ends
+        r0_slot = next(s for s, i in owner.items() if i == 0)
+        if ahead:
+            assert runner.pending and r0_slot not in runner.free_slots()
+            with pytest.raises(ValueError):
+                runner.add([seqs[3]])  # r0's slot stays taken until its result is returned
+        while runner.active_slots or runner.pending or not got[3]:
+            if not got[3] and runner.free_slots():
+                admit(3)
+                continue
+            record(runner.step())
+        return got, [list(q.token_ids) for q in seqs], runner.ahead_launches
+
+    got, ids, launches = run(True)
+    assert launches > 0
+    assert len(got[0]) == limit0 and all(len(got[i]) == 60 for i in (1, 2, 3))
+    for i in range(4):
+        assert ids[i][len(prompts[i]):] == got[i]
+    assert (got, ids) == run(False)[:2]
+
+
+@pytest.mark.parametrize("bound", ["batch", "context"])
+def test_graph_bounds_run_larger_steps_eagerly(bound):
+    """cuda_graph_max_batch / cuda_graph_max_context (ne/config.py:58-61): while a step is
+    above the bound it runs eagerly (no graph captured); once the batch shrinks (one
+    request finishes) or below the context bound it replays a graph.  Tokens equal the
+    all-eager run."""
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(3, seed=81)
+    reqs = [GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=n, ignore_eos=True))
+            for i, (p, n) in enumerate(zip(prompts, [12, 40, 40]))]
+    kw = {"cuda_graph_max_batch": 2} if bound == "batch" else {"cuda_graph_max_context": 64 + 12 + 4}
+
+    replays = [0]
+    replay = torch.cuda.CUDAGraph.replay
+
+    def counted(self):
+        replays[0] += 1
+        return replay(self)
+
+    def run(graphs, **extra):
+        settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                                  quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                                  num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=3, max_model_len=256,
+                                  kv_cache_memory_mb=64, cuda_graphs=graphs, **extra)
+        eng = create_verify_engine(CFG, state, settings, max_prefill_rows=192)
+        seen = []  # per verify step: (graph allowed, graph replays in the step)
+        step = eng.runner._run_device_step
+
+        def spy():
+            allowed, before = eng.runner.graph_allowed(), replays[0]
+            step()
+            seen.append((allowed, replays[0] - before))
+        eng.runner._run_device_step = spy
+        out = eng.batched_generator().generate_all(reqs)
+        return {k: [e.token_id for e in v] for k, v in out.items()}, seen
+
+    eager, _ = run(False)
+    torch.cuda.CUDAGraph.replay = counted
+    try:
+        gated, seen = run(True, **kw)
+    finally:
+        torch.cuda.CUDAGraph.replay = replay
+    assert gated == eager
+    assert all(n == 0 for allowed, n in seen if not allowed)  # eager above the bounds
+    assert any(allowed and n == 1 for allowed, n in seen)  # graph replays within them
+    if bound == "batch":  # three active until r0 finishes, then two
+        assert not seen[0][0] and seen[-1][0]
+    else:  # contexts grow past the bound
+        assert seen[0][0] and not seen[-1][0]
+
+
+def test_graph_capture_out_of_memory_falls_back_to_eager(monkeypatch):
+    """cuda_graph_runner.py:193-207: a capture that runs out of device memory leaves the
+    runner eager; the step that tried to capture already ran, and the tokens equal the
+    all-eager run."""
+    state = make_state(norm_ones=True)
+    prompts = motif_prompts(2, seed=91)
+    reqs = [GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=30, ignore_eos=True))
+            for i, p in enumerate(prompts)]
+    eager = {k: [e.token_id for e in v] for k, v in engine_for(state, 2).batched_generator().generate_all(reqs).items()}
+    eng = engine_for(state, 2, graphs=True)
+
+    class NoMemory:
+        def __init__(self, *a, **k):
+            pass
+
+        def __enter__(self):
+            raise torch.cuda.OutOfMemoryError("no memory for the capture")
+
+        def __exit__(self, *exc):
+            return False
+
+    monkeypatch.setattr(torch.cuda, "graph", NoMemory)
+    out = {k: [e.token_id for e in v] for k, v in eng.batched_generator().generate_all(reqs).items()}
+    assert out == eager
+    assert eng.runner.graph is None and eng.runner.graph_failed
+    assert not eng.runner.graph_allowed()
 
 
 def test_launch_ahead_running_out_of_kv_blocks_keeps_every_emitted_token():
@@ -580,3 +733,91 @@ def test_full_depth_verify_step_logits_match_oracle():
         print(f"slot {slot}: max-abs {err:.3e}, relative {rel:.3e}, logit scale {float(ref.abs().max()):.3f}")
         assert err <= 1e-2, f"slot {slot}: max-abs {err:.3e}"
         assert rel <= 2e-2, f"slot {slot}: relative error {rel:.3e}"
+
+
+def test_full_depth_greedy_tokens_and_logits_match_oracle():
+    """The Qwen3-0.6B architecture at full depth and vocabulary (28 layers, 151,936 tokens)
+    with unit norm weights, so that logits are of order one and both bars below bite: 64
+    sequences of 64-token motif prompts, k = 4, greedy, the verify step replayed from a HIP
+    graph, three verify steps.  For four sequences, against the oracle's bf16 model with
+    int8 weights and an int8 paged KV cache (score_tokens, model_runner.py:52-62), teacher
+    forced on the tokens the engine emitted:
+
+      * every emitted token equals the oracle's argmax wherever the oracle's top-2 margin
+        exceeds 2e-2 of that row's logit scale (test_sampling_and_generation.py:63-79
+        checks greedy output identity on the reference);
+      * the last step's logits (the LM head re-run on that step's final hidden rows) agree
+        with the oracle's rows at the same positions: relative error <= 2e-2 and max-abs
+        <= 2e-2 of the logit scale.  An absolute 1e-2 bar cannot hold here: bf16's own
+        rounding of a logit near 4 is 1.6e-2."""
+    from nanoengine_amd.qwen3 import QWEN3_0_6B
+
+    full = om.Qwen3Config(151936, 1024, 3072, 28, 16, 8, 128, 1e-6, 1e6, True)
+    state = random_state_dict(QWEN3_0_6B, seed=0, std=0.02)
+    for name in state:
+        if name.endswith("norm.weight") or "layernorm" in name:
+            state[name] = torch.ones_like(state[name])
+    prompts = motif_prompts(64, seed=0)
+    settings = EngineSettings(device="cuda", dtype="bfloat16", kv_cache="paged", scheduler="continuous",
+                              quantization="int8", kv_cache_dtype="int8", speculative="ngram",
+                              num_speculative_tokens=4, ngram_max_size=3, max_num_seqs=64, max_model_len=256,
+                              kv_cache_memory_mb=1024, cuda_graphs=True, cuda_graph_max_batch=64,
+                              cuda_graph_max_context=262)
+    eng = create_verify_engine(QWEN3_0_6B, state, settings, max_prefill_rows=64 * 64)
+    params = SamplingParams(max_new_tokens=64, ignore_eos=True)
+    seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, params)) for i, p in enumerate(prompts)]
+    emitted = {s: list(r.tokens) for s, r in eng.runner.add(seqs).items()}
+    eng.runner.trace = []  # also keeps every step from being launched ahead
+    for _ in range(3):
+        for s, r in eng.runner.step().items():
+            emitted[s].extend(r.tokens)
+    last = eng.runner.trace[-1]
+    picked = (0, 21, 42, 63)
+    rows = 64 * eng.runner.R
+    logits, _ = eng.model.compute_logits(eng.model.normed[:rows], logits=True, argmax=False)
+    torch.cuda.synchronize()
+    ours = {s: logits[s * 5 : s * 5 + 1 + len(last[s]["drafts"])].float().cpu() for s in picked}
+    del eng, logits
+    torch.cuda.empty_cache()
+    model = om.Qwen3ForCausalLM(full)
+    model.load_state_dict(state)
+    del state
+    model = model.to(torch.bfloat16).eval()
+    om.quantize_linear_layers(model)
+    pool = om.KVCachePool(full, 16 * 16, torch.bfloat16, is_int8=True)
+    runner = OracleRunner(model, pool, OraclePaged(16, 16))
+    checked = total = 0
+    for slot in picked:
+        rec, prompt, out = last[slot], prompts[slot], emitted[slot]
+        history, drafts = list(rec["history"]), rec["drafts"]
+        assert history == prompt + out[: len(history) - len(prompt)]
+        L = len(history)
+        seq = OracleSequence(f"o{slot}", list(history), len(prompt), 64)
+        runner.allocator.reserve(seq.request_id, L + 8)
+        head = runner.score_tokens(seq, L).float()  # rows 0 .. L-1 (shared by both checks)
+        seq.token_ids = history + drafts  # the last step's rows: L-1 .. L-1+g
+        ref = head[L - 1 : L]
+        if drafts:
+            ref = torch.cat([ref, runner.score_tokens(seq, len(drafts)).float()])
+        seq.token_ids, seq.num_cached_tokens = prompt + out[:-1], L  # teacher forcing on what it emitted
+        forced = head  # row p: the logits after token p
+        if len(seq.token_ids) > L:
+            forced = torch.cat([head, runner.score_tokens(seq, len(seq.token_ids) - L).float()])
+        runner.allocator.free(seq.request_id)
+        for j, tok in enumerate(out):
+            row = forced[len(prompt) - 1 + j]
+            top2 = torch.topk(row, 2)
+            total += 1
+            if float(top2.values[0] - top2.values[1]) > 2e-2 * float(row.abs().max()):
+                assert tok == int(top2.indices[0]), f"slot {slot} token {j}"
+                checked += 1
+        got = ours[slot]
+        scale = float(ref.abs().max())
+        err = float((got - ref).abs().max())
+        rel = float((got - ref).norm() / ref.norm())
+        print(f"slot {slot}: {len(out)} tokens, last-step logits max-abs {err:.3e} (scale {scale:.2f}), "
+              f"relative {rel:.3e}")
+        assert rel <= 2e-2, f"slot {slot}: relative error {rel:.3e}"
+        assert err <= 2e-2 * scale, f"slot {slot}: max-abs {err:.3e} at logit scale {scale:.2f}"
+    print(f"{checked} of {total} emitted tokens had a clear oracle margin and matched")
+    assert checked >= total // 2

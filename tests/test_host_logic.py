@@ -119,6 +119,32 @@ def test_settings_select_the_hip_path_and_keep_the_reference_checks():
     assert s.device == "cuda" and s.cuda_graphs is True and s.num_speculative_tokens == 8
 
 
+def test_verify_graph_gating_follows_the_reference_bounds():
+    """cuda_graph_max_batch / cuda_graph_max_context (ne/config.py:58-61) bound which verify
+    steps replay the captured graph, as they bound the reference's decode graphs
+    (runtime.py:150-160, cuda_graph_runner.py:106-117): more active sequences than the
+    batch bound, or a step context (length + k guess rows) above the context bound, runs
+    eagerly; the settings reach the runner through create_verify_engine's arguments."""
+    from nanoengine_amd.runner import verify_graph_allowed
+
+    assert verify_graph_allowed(8, 1024, 8, 1024)
+    assert not verify_graph_allowed(9, 100, 8, 1024)
+    assert not verify_graph_allowed(1, 1025, 8, 1024)
+    assert verify_graph_allowed(64, 10**6, None, None)
+    assert verify_graph_allowed(0, 0, 8, 1024)
+    d = EngineSettings()
+    assert (d.cuda_graph_max_batch, d.cuda_graph_max_context) == (8, 1024)  # ne/config.py:59-61
+    env = {"NANOENGINE_CUDA_GRAPH_MAX_BATCH": "64", "NANOENGINE_CUDA_GRAPH_MAX_CONTEXT": "4096"}
+    s = EngineSettings.from_env(env)
+    assert (s.cuda_graph_max_batch, s.cuda_graph_max_context) == (64, 4096)
+    for bad in ("cuda_graph_max_batch", "cuda_graph_max_context"):
+        with pytest.raises(ValueError):
+            EngineSettings(**{bad: 0})
+    src = (Path(__file__).parents[1] / "inference-engine-from-scratch_amd" / "nanoengine_amd" / "runtime.py").read_text()
+    assert "graph_max_batch=settings.cuda_graph_max_batch" in src
+    assert "graph_max_context=settings.cuda_graph_max_context" in src
+
+
 def test_num_guesses_never_passes_the_length_limit():
     p = SamplingParams(max_new_tokens=128)
     assert [num_guesses(p, n, 4) for n in (0, 124, 126, 127)] == [4, 3, 1, 0]

@@ -92,6 +92,8 @@ def test_launch_ahead_check_matches_the_finishing_slots(seed, stops):
     runner = VerifyRunner.__new__(VerifyRunner)
     runner.run_ahead, runner.proposer, runner.trace = True, None, None
     runner._fifo_blocks, runner.use_graph, runner.graph = True, True, object()
+    runner.graph_failed, runner.graph_max_batch, runner.graph_max_context, runner.k = False, None, None, 4
+    runner.np_active = st["act"]
     runner.graph_sampled, runner._sampled = False, False
     runner.stop_token_ids = stops
     runner.np_out, runner.np_num_out = st["out"], st["nout"]
@@ -111,3 +113,60 @@ def test_launch_ahead_check_matches_the_finishing_slots(seed, stops):
         st["act"], st["lengths"].copy(), st["gen"].copy(), st["steps"].copy(), st["max_new"], st["honours"],
         tuple(sorted(stops)), StepResult, None)
     assert ahead == (not finishing and Pool.num_free_blocks >= need)
+
+
+@pytest.mark.parametrize("fn_name", ["finish_step_py", "finish_step"])
+@pytest.mark.parametrize("case", ["emitted-too-many", "emitted-negative", "inactive-slot", "empty-slot",
+                                  "slot-out-of-range"])
+def test_finish_step_refuses_bad_inputs_before_changing_any_mirror(fn_name, case):
+    """Both implementations check every slot's inputs first: a bad emitted count or a bad
+    active slot raises ValueError with the mirrors, token lists and sampling steps untouched."""
+    fn = getattr(host_step, fn_name)
+    st = _state(7)
+    active = np.flatnonzero(st["act"]).tolist()
+    victim = active[len(active) // 2]
+    if case == "emitted-too-many":
+        st["nout"][victim] = st["out"].shape[1] + 1
+    elif case == "emitted-negative":
+        st["nout"][victim] = -1
+    elif case == "inactive-slot":
+        active.append(int(np.flatnonzero(~st["act"])[0]))
+    elif case == "empty-slot":
+        st["slots"][victim] = None
+    else:
+        active.append(len(st["slots"]))
+    before = copy.deepcopy(st)
+    with pytest.raises(ValueError):
+        fn(active, st["slots"], st["out"], st["nout"], st["nd"], st["act"], st["lengths"], st["gen"], st["steps"],
+           st["max_new"], st["honours"], (), StepResult, None)
+    for key in ("lengths", "gen", "steps"):
+        assert np.array_equal(st[key], before[key])
+    for a, b in zip(st["slots"], before["slots"]):
+        if a is not None:
+            assert a.token_ids == b.token_ids and a.sampling_generator.step == b.sampling_generator.step
+
+
+def test_finish_step_keeps_a_sequence_alive_while_its_callback_drops_it_from_the_slot_list():
+    """on_cached may change the slot list it was given: here it removes the list's entry
+    for the sequence it is called with, so during the call the list no longer holds it.
+    The extension holds each sequence across its own calls; the step completes, every
+    slot gets its result and every sequence its tokens."""
+    st = _state(9)
+    st["max_new"][:] = 10_000  # no slot finishes: every slot appends and calls on_cached
+    active = np.flatnonzero(st["act"]).tolist()
+    slots = list(st["slots"])
+    want = {s: slots[s].token_ids + st["out"][s, : st["nout"][s]].tolist() for s in active}
+    seen = {}
+
+    def on_cached(seq):
+        s = slots.index(seq)
+        slots[s] = None
+        seen[s] = seq
+
+    results, finishing = host_step.finish_step(active, slots, st["out"], st["nout"], st["nd"], st["act"],
+                                               st["lengths"], st["gen"], st["steps"], st["max_new"],
+                                               st["honours"], (), StepResult, on_cached)
+    assert not finishing and sorted(results) == active
+    assert sorted(seen) == active
+    for s in active:
+        assert seen[s].token_ids == want[s]
