@@ -60,8 +60,34 @@ def lib() -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
             ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p,
         ]
+        handle.oracle_exp3.restype = ctypes.c_float
+        handle.oracle_exp3.argtypes = [ctypes.c_float]
+        handle.oracle_v3_scratch_bytes.restype = ctypes.c_size_t
+        handle.oracle_v3_scratch_bytes.argtypes = []
+        handle.oracle_accept_sampled_v3.restype = ctypes.c_int
+        handle.oracle_accept_sampled_v3.argtypes = [
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
+            ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        handle.oracle_v3_row.restype = ctypes.c_uint64
+        handle.oracle_v3_row.argtypes = [
+            ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        handle.oracle_v3_weight.restype = ctypes.c_uint32
+        handle.oracle_v3_weight.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_uint32,
+                                            ctypes.c_void_p]
         _lib = handle
     return _lib
+
+
+def _v3_scratch() -> np.ndarray:
+    return np.zeros(int(lib().oracle_v3_scratch_bytes()) // 8 + 1, dtype=np.uint64)
+
+
+def exp3(x: float) -> float:
+    """The integer-mass contract's exp (Cephes' reduction and polynomial, one fmaf per step)."""
+    return float(lib().oracle_exp3(ctypes.c_float(x)))
 
 
 def cephes_exp(x: float) -> float:
@@ -179,3 +205,47 @@ def top_p_kept(row_bits: np.ndarray, temperature: float, top_p: float) -> tuple[
     k = lib().oracle_top_p_kept(row.ctypes.data, vocab, ctypes.c_float(temperature), ctypes.c_float(top_p),
                                 kept.ctypes.data, w.ctypes.data, ctypes.byref(tau), ctypes.byref(m))
     return kept.astype(bool), float(k), int(tau.value), int(m.value)
+
+
+def sampled_accept_v3(row_bits: np.ndarray, drafts: list[int], temperature: float, top_p: float, seed: int,
+                      step: int) -> list[int]:
+    """The integer-mass contract for one-hot (n-gram) guesses (C oracle): ``row_bits
+    [g+1, V]`` bf16 patterns -> kept guesses + drawn token."""
+    rows = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    g = len(drafts)
+    assert rows.shape[0] == g + 1
+    vocab = rows.shape[1]
+    d = np.ascontiguousarray(np.asarray(drafts, dtype=np.int32))
+    out = np.zeros(g + 1, dtype=np.int32)
+    scratch = _v3_scratch()
+    n = lib().oracle_accept_sampled_v3(
+        rows.ctypes.data, vocab, vocab, d.ctypes.data if g else None, g, ctypes.c_float(temperature),
+        ctypes.c_float(top_p), seed, step, out.ctypes.data, scratch.ctypes.data,
+    )
+    return out[:n].tolist()
+
+
+def v3_row(row_bits: np.ndarray, temperature: float, top_p: float) -> tuple[np.ndarray, int, int, int, int]:
+    """(kept flags, K, Z, tau, m) of one row under the integer-mass contract."""
+    row = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    vocab = row.shape[0]
+    kept = np.zeros(vocab, dtype=np.uint8)
+    z, tau, m = ctypes.c_uint64(0), ctypes.c_uint32(0), ctypes.c_uint32(0)
+    k = lib().oracle_v3_row(row.ctypes.data, vocab, ctypes.c_float(temperature), ctypes.c_float(top_p),
+                            kept.ctypes.data, ctypes.byref(z), ctypes.byref(tau), ctypes.byref(m),
+                            _v3_scratch().ctypes.data)
+    return kept.astype(bool), int(k), int(z.value), int(tau.value), int(m.value)
+
+
+def v3_weight(row_bits: np.ndarray, temperature: float, key: int) -> int:
+    """E(key) of a row: the integer weight of a token whose bf16 order key is ``key``."""
+    row = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    return int(lib().oracle_v3_weight(row.ctypes.data, row.shape[0], ctypes.c_float(temperature), key,
+                                      _v3_scratch().ctypes.data))
+
+
+def key16(bits: np.ndarray) -> np.ndarray:
+    """16-bit order keys of bf16 bit patterns (larger value, larger key; -0 as +0)."""
+    b = np.asarray(bits, dtype=np.uint32)
+    b = np.where((b & 0x7FFF) == 0, 0, b)
+    return np.where(b & 0x8000, (~b) & 0xFFFF, b | 0x8000).astype(np.uint32)

@@ -406,3 +406,209 @@ int oracle_accept_sampled_draft(const uint16_t* logits, int64_t ld, const uint16
   out[kept] = draw(e, vocab, -1, oracle_uniform(seed, step, 63));
   return kept + 1;
 }
+
+/* ---- v3: integer masses for one-hot (n-gram) guesses -------------------------------
+ * The contract the GPU's sampled n-gram path implements (csrc/accept.hip states it in
+ * full).  Every token's weight is an integer that depends only on its bf16 key, so sums
+ * in any order are exact and equal:
+ *   invT = 1 / T (fp32 division); kmax = the row's largest key; mx = val(kmax) * invT;
+ *   E(k) = (uint32)(exp3(val(k) * invT - mx) * 2^31), truncated; cnt(k) = tokens of key k;
+ *   Z = sum cnt(k) E(k).  Top-p (P < 1): thr = max(1, (uint64)((double)Z * (double)P));
+ *   M(v) = sum_{k > v} cnt(k) E(k); tau = the smallest v with M(v) < thr;
+ *   m = min(cnt(tau), ceil((thr - M(tau)) / E(tau))); kept: key > tau, or key == tau
+ *   and fewer than m tokens of key tau precede it; K = M(tau) + m E(tau).  P >= 1 keeps
+ *   every token, K = Z.  w_j = E(key_j) when kept, else 0.
+ *   Guess g of row i (U_i = the uniform's 24-bit integer) is kept iff w_g >= K or
+ *   (w_g > 0 and U_i K < w_g 2^24).  A draw with x excluded (the rejected guess; none
+ *   for the bonus): the kept tokens in order of key (descending) then index (ascending),
+ *   x removed (kept if that leaves no weight); R = their total weight;
+ *   t = floor(U R / 2^24); the token is the first whose running weight exceeds t.
+ *   exp3: Cephes' Cody-Waite reduction and polynomial with each step one fused
+ *   multiply-add (fmaf), 0 below -86. */
+float oracle_exp3(float x) {
+  if (x < -86.0f) return 0.0f;
+  const float fx = floorf(fmaf(x, 1.44269504088896341f, 0.5f));
+  float r = fmaf(fx, -0.693359375f, x);
+  r = fmaf(fx, 2.12194440e-4f, r);
+  float y = fmaf(1.9875691500E-4f, r, 1.3981999507E-3f);
+  y = fmaf(y, r, 8.3334519073E-3f);
+  y = fmaf(y, r, 4.1665795894E-2f);
+  y = fmaf(y, r, 1.6666665459E-1f);
+  y = fmaf(y, r, 5.0000001201E-1f);
+  const float z = r * r;
+  y = fmaf(y, z, r);
+  y = y + 1.0f;
+  const int n = (int)fx;
+  uint32_t bits = (uint32_t)(n + 127) << 23;
+  float scale;
+  memcpy(&scale, &bits, sizeof(scale));
+  return y * scale;
+}
+
+typedef struct {
+  uint32_t cnt[65536];
+  uint32_t kmax;
+  float invT, mx;
+  uint64_t z, k_total, thr;
+  int topp;
+  uint32_t tau, m;
+} v3_row;
+
+static uint32_t v3_weight(const v3_row* d, uint32_t k) {
+  const float e = oracle_exp3(bf16_value(bf16_of_key(k)) * d->invT - d->mx);
+  return (uint32_t)(e * 2147483648.0f);
+}
+
+static void v3_setup(v3_row* d, const uint16_t* row, int vocab, float temperature, float top_p) {
+  memset(d->cnt, 0, sizeof(d->cnt));
+  d->kmax = 0;
+  for (int j = 0; j < vocab; ++j) {
+    const uint32_t k = key_of_bf16(row[j]);
+    d->cnt[k] += 1;
+    if (k > d->kmax) d->kmax = k;
+  }
+  d->invT = 1.0f / temperature;
+  d->mx = bf16_value(bf16_of_key(d->kmax)) * d->invT;
+  uint64_t z = 0;
+  for (uint32_t k = 0; k < 65536; ++k)
+    if (d->cnt[k]) z += (uint64_t)d->cnt[k] * v3_weight(d, k);
+  d->z = z;
+  d->topp = top_p < 1.0f;
+  d->tau = 0;
+  d->m = 0;
+  d->k_total = z;
+  d->thr = 0;
+  if (!d->topp) return;
+  uint64_t thr = (uint64_t)((double)z * (double)top_p);
+  if (thr < 1) thr = 1;
+  d->thr = thr;
+  uint64_t above = 0; /* M(k) while walking down */
+  for (int k = 65535; k >= 0; --k) {
+    const uint64_t mass = d->cnt[k] ? (uint64_t)d->cnt[k] * v3_weight(d, (uint32_t)k) : 0;
+    if (above + mass >= thr) { /* M(k) = above < thr <= M(k - 1) */
+      const uint64_t e = v3_weight(d, (uint32_t)k);
+      uint64_t m = (thr - above + e - 1) / e;
+      if (m > d->cnt[k]) m = d->cnt[k];
+      d->tau = (uint32_t)k;
+      d->m = (uint32_t)m;
+      d->k_total = above + m * e;
+      return;
+    }
+    above += mass;
+  }
+}
+
+/* kept (1) or not (0) for token j of the row */
+static int v3_kept(const v3_row* d, const uint16_t* row, int j) {
+  const uint32_t k = key_of_bf16(row[j]);
+  if (!d->topp || k > d->tau) return 1;
+  if (k < d->tau) return 0;
+  uint32_t rank = 0;
+  for (int i = 0; i < j; ++i) rank += key_of_bf16(row[i]) == d->tau;
+  return rank < d->m;
+}
+
+/* floor(u * r / 2^24) for u < 2^24, exactly */
+static uint64_t v3_scale(uint32_t u, uint64_t r) {
+  return (uint64_t)u * (r >> 24) + (((uint64_t)u * (r & 0xFFFFFFu)) >> 24);
+}
+
+static int v3_draw(const v3_row* d, const uint16_t* row, int vocab, int x, uint32_t u) {
+  uint64_t wx = 0;
+  if (x >= 0 && v3_kept(d, row, x)) wx = v3_weight(d, key_of_bf16(row[x]));
+  uint64_t r = d->k_total - wx;
+  if (r == 0) { /* x held all the kept weight: draw without the exclusion */
+    x = -1;
+    wx = 0;
+    r = d->k_total;
+  }
+  const uint64_t t = v3_scale(u, r);
+  const uint32_t kx = x >= 0 ? key_of_bf16(row[x]) : 0xFFFFFFFFu;
+  uint64_t run = 0;
+  for (int k = (int)d->kmax; k >= 0; --k) {
+    uint64_t c = d->cnt[k];
+    if (d->topp && (uint32_t)k < d->tau) break;
+    if (d->topp && (uint32_t)k == d->tau) c = d->m;
+    if (wx && (uint32_t)k == kx) c -= 1;
+    if (!c) continue;
+    const uint64_t e = v3_weight(d, (uint32_t)k);
+    if (!e) continue;
+    if (run + c * e > t) {
+      const uint64_t want = (t - run) / e; /* the want-th kept occurrence of k, x skipped */
+      uint64_t seen = 0;
+      for (int j = 0; j < vocab; ++j) {
+        if (key_of_bf16(row[j]) != (uint32_t)k || j == x) continue;
+        if (seen == want) return j;
+        ++seen;
+      }
+      return -1; /* unreachable */
+    }
+    run += c * e;
+  }
+  return -1; /* unreachable: t < r */
+}
+
+/*
+ * One sequence under v3: rows [num_drafts + 1][ld] bf16 logit bit patterns, guesses
+ * drafts[0..num_drafts).  Writes kept guesses + 1 token to out and returns the count.
+ * `scratch` holds sizeof(v3_row) bytes (oracle_v3_scratch_bytes()).
+ */
+int oracle_accept_sampled_v3(const uint16_t* logits, int64_t ld, int vocab, const int32_t* drafts, int num_drafts,
+                             float temperature, float top_p, uint64_t seed, uint64_t step, int32_t* out,
+                             void* scratch) {
+  v3_row* d = (v3_row*)scratch;
+  int n_out = 0;
+  for (int i = 0; i <= num_drafts; ++i) {
+    const uint16_t* row = logits + (int64_t)i * ld;
+    v3_setup(d, row, vocab, temperature, top_p);
+    const float u_draw = oracle_uniform(seed, step, 63);
+    const uint32_t ud = (uint32_t)(u_draw * 16777216.0f);
+    if (i == num_drafts) {
+      out[n_out] = v3_draw(d, row, vocab, -1, ud);
+      return n_out + 1;
+    }
+    const int guess = drafts[i];
+    const uint64_t w = v3_kept(d, row, guess) ? v3_weight(d, key_of_bf16(row[guess])) : 0;
+    const uint32_t ui = (uint32_t)(oracle_uniform(seed, step, i) * 16777216.0f);
+    const int accept = w >= d->k_total || (w > 0 && (unsigned __int128)ui * d->k_total < (unsigned __int128)w << 24);
+    if (accept) {
+      out[n_out++] = guess;
+      continue;
+    }
+    out[n_out] = v3_draw(d, row, vocab, guess, ud);
+    return n_out + 1;
+  }
+  return n_out; /* unreachable */
+}
+
+size_t oracle_v3_scratch_bytes(void) { return sizeof(v3_row); }
+
+/* the v3 kept flags, K, Z, tau and m of one row (for the pins) */
+uint64_t oracle_v3_row(const uint16_t* row, int vocab, float temperature, float top_p, unsigned char* kept,
+                       uint64_t* z, uint32_t* tau, uint32_t* m, void* scratch) {
+  v3_row* d = (v3_row*)scratch;
+  v3_setup(d, row, vocab, temperature, top_p);
+  uint32_t ties = 0;
+  for (int j = 0; j < vocab; ++j) {
+    const uint32_t k = key_of_bf16(row[j]);
+    if (!d->topp || k > d->tau) {
+      kept[j] = 1;
+    } else if (k == d->tau) {
+      kept[j] = ties < d->m;
+      ++ties;
+    } else {
+      kept[j] = 0;
+    }
+  }
+  *z = d->z;
+  *tau = d->tau;
+  *m = d->m;
+  return d->k_total;
+}
+
+/* E(k) of a row (for the pins): the weight of a token with key k */
+uint32_t oracle_v3_weight(const uint16_t* row, int vocab, float temperature, uint32_t key, void* scratch) {
+  v3_row* d = (v3_row*)scratch;
+  v3_setup(d, row, vocab, temperature, 1.0f);
+  return v3_weight(d, key);
+}

@@ -300,6 +300,168 @@ def test_contract_v2_without_top_p_is_the_previous_contract():
             oacc.sampled_accept_draft(rows, drows, guesses, temp, seed, step)
 
 
+# ---- the integer-mass contract (one-hot guesses; the GPU's sampled n-gram path)
+def test_v3_exp_is_within_two_ulp_of_exp():
+    for x in np.linspace(-85.0, 20.0, 3001, dtype=np.float32):
+        got, want = oacc.exp3(float(x)), math.exp(float(x))
+        assert abs(got - want) <= 2 * 2.0 ** -23 * want, float(x)
+    assert oacc.exp3(0.0) == 1.0 and oacc.exp3(-87.0) == 0.0
+
+
+def test_v3_weights_are_the_scaled_softmax_numerators():
+    """E(k) / 2^31 equals exp(val(k) / T - max / T) computed in fp64 (to fp32 accuracy plus
+    the 2^-31 truncation), E(kmax) = 2^31, and tokens more than ~21.5 T below the largest
+    logit weigh 0 -- a wrong sign, a missing 1/T or a wrong maximum fails."""
+    rng = np.random.default_rng(31)
+    for trial in range(20):
+        vocab = int(rng.integers(5, 400))
+        vals = (rng.standard_normal(vocab) * float(rng.uniform(0.5, 8))).astype(np.float32)
+        bits = oacc.bf16_bits(vals)
+        temp = float(rng.uniform(0.2, 2.0))
+        keys = oacc.key16(bits)
+        f = oacc.bf16_to_f32(bits).astype(np.float64)
+        mx = f.max() / np.float32(temp)
+        for j in rng.integers(0, vocab, 10).tolist() + [int(np.argmax(f))]:
+            e = oacc.v3_weight(bits, temp, int(keys[j]))
+            want = math.exp(f[j] / np.float32(temp) - mx)
+            # fp32 rounding of z = logit / T and of z - max (relative 2^-24 each) plus the exp's 2 ulp
+            tol = 2.0 ** -23 * (abs(f[j] / temp) + abs(mx) + 4)
+            assert abs(e / 2.0 ** 31 - want) <= tol * want + 2.0 ** -31, (trial, j)
+        assert oacc.v3_weight(bits, temp, int(keys.max())) == 2 ** 31
+    bits = oacc.bf16_bits(np.array([0.0, -30.0, -5.0], dtype=np.float32))
+    assert oacc.v3_weight(bits, 1.0, int(oacc.key16(bits)[1])) == 0
+
+
+def test_v3_top_p_reference_kat():
+    """sampling.py:21-27 KAT ([.05, .6, .3, .05] at 0.8 keeps [1, 2]) on bf16 logits log(p)."""
+    kat = KATS["top_p"]
+    bits = oacc.bf16_bits(np.log(np.asarray(kat["probabilities"], dtype=np.float32)))
+    kept, _, _, _, _ = oacc.v3_row(bits, 1.0, kat["top_p"])
+    assert np.nonzero(kept)[0].tolist() == kat["expected_nonzero"]
+
+
+def test_v3_top_p_closed_forms():
+    """top_p >= 1 keeps everything with K = Z; a tiny top_p keeps only the first index of
+    the largest logit (ties rank by index); K is the exact integer sum of the kept weights
+    and the smallest such sum reaching top_p * Z."""
+    rng = np.random.default_rng(32)
+    for trial in range(50):
+        vocab = int(rng.integers(2, 700))
+        vals = (rng.standard_normal(vocab) * 2).astype(np.float32)
+        if trial % 3 == 0:  # many exact ties
+            vals = np.round(vals).astype(np.float32)
+        bits = oacc.bf16_bits(vals)
+        temp = float(rng.uniform(0.3, 2.0))
+        kept, k_all, z, _, _ = oacc.v3_row(bits, temp, 1.0)
+        assert kept.all() and k_all == z
+        kept, _, _, _, _ = oacc.v3_row(bits, temp, 1e-9)
+        f = oacc.bf16_to_f32(bits)
+        assert np.nonzero(kept)[0].tolist() == [int(np.argmax(f))]
+        kept9, k9, z9, tau, m = oacc.v3_row(bits, temp, 0.9)
+        keys = oacc.key16(bits)
+        w = np.array([oacc.v3_weight(bits, temp, int(k)) for k in keys], dtype=object)
+        assert k9 == sum(w[kept9]) and z9 == sum(w)
+        thr = max(1, int(float(z9) * float(np.float32(0.9))))
+        assert k9 >= thr and k9 - w[np.nonzero(kept9 & (keys == tau))[0][-1]] < thr
+        assert int(((keys == tau) & kept9).sum()) == m
+
+
+def test_v3_top_p_matches_a_sorted_scan():
+    """Brute force in fp64: sort by logit (desc), ties by index, keep a token while the mass
+    before it is below top_p * Z.  Cases where some token's mass-before lies within
+    rounding of the threshold are skipped."""
+    rng = np.random.default_rng(33)
+    checked = 0
+    for trial in range(300):
+        vocab = int(rng.integers(2, 200))
+        vals = (rng.standard_normal(vocab) * float(rng.uniform(0.5, 4))).astype(np.float32)
+        if trial % 2:
+            vals = (np.round(vals * 2) / 2).astype(np.float32)
+        bits = oacc.bf16_bits(vals)
+        f = oacc.bf16_to_f32(bits)
+        temp, top_p = float(rng.uniform(0.3, 2.0)), float(rng.uniform(0.05, 0.99))
+        z = f.astype(np.float64) / np.float32(temp)
+        e = np.exp(z - z.max())
+        order = sorted(range(vocab), key=lambda j: (-float(f[j]) + 0.0, j))
+        thr = top_p * e.sum()
+        before, want, ambiguous = 0.0, np.zeros(vocab, dtype=bool), False
+        for j in order:
+            if abs(before - thr) < 1e-4 * e.sum():
+                ambiguous = True
+            want[j] = before < thr
+            before += e[j]
+        if ambiguous:
+            continue
+        kept, _, _, _, _ = oacc.v3_row(bits, temp, top_p)
+        assert np.array_equal(kept, want), (trial, np.nonzero(kept ^ want))
+        checked += 1
+    assert checked > 200
+
+
+def test_v3_top_p_draws_follow_apply_top_p_chi_square():
+    """Bonus draws (no guesses) follow the reference's apply_top_p distribution (the
+    oracle's restatement of sampling.py:21-38) on the same bf16 logits."""
+    logits = np.log(np.array([0.3, 0.05, 0.25, 0.15, 0.1, 0.08, 0.07], dtype=np.float32))
+    bits = oacc.bf16_bits(logits)[None, :]
+    temp, top_p, trials = 0.9, 0.75, 6000
+    probs = ov.compute_token_probabilities(torch.from_numpy(oacc.bf16_to_f32(bits[0]).copy()), temp, top_p)
+    probs = probs.double().numpy()
+    keep = probs > 0
+    counts = np.zeros(7)
+    for step in range(trials):
+        counts[oacc.sampled_accept_v3(bits, [], temp, top_p, seed=99, step=step)[0]] += 1
+    assert counts[~keep].sum() == 0
+    critical = {2: 13.82, 3: 16.27, 4: 18.47, 5: 20.52}[int(keep.sum()) - 1]  # 0.999 quantiles
+    assert _chi_square(counts[keep], probs[keep], trials) < critical
+
+
+def test_v3_keeps_the_target_distribution():
+    """The reference's chi-square (test_speculative_decoding.py:58-74) for n-gram guesses:
+    a guess drawn from the reversed distribution is kept with probability p[g], else the
+    token is drawn from p without it -- the first emitted token follows the target p, and
+    the acceptance rate is sum_g q[g] p[g]."""
+    kat = KATS["rejection_sampling_chi_square"]
+    target = np.asarray(kat["target"], dtype=np.float64)
+    bits = oacc.bf16_bits(np.log(target).astype(np.float32))
+    bits = np.stack([bits, bits])
+    p_bf16 = np.exp(oacc.bf16_to_f32(bits[0]).astype(np.float64))
+    p_bf16 /= p_bf16.sum()
+    q = np.asarray(kat["draft"], dtype=np.float64)
+    rng = np.random.default_rng(kat["seed"])
+    trials, counts, kept = kat["trials"], np.zeros(5), 0
+    for step in range(trials):
+        guess = int(rng.choice(5, p=q))
+        out = oacc.sampled_accept_v3(bits, [guess], 1.0, 1.0, seed=4242, step=step)
+        counts[out[0]] += 1
+        kept += len(out) == 2
+    assert _chi_square(counts, p_bf16, trials) < kat["critical_value"]
+    rate = float((q * p_bf16).sum())
+    assert abs(kept / trials - rate) < 4 * math.sqrt(rate * (1 - rate) / trials)
+
+
+def test_v3_draw_walks_keys_down_then_indices_up():
+    """The inverse CDF orders kept tokens by key (descending) then index: as the draw's
+    uniform grows the token moves monotonically along that order, and a token holding
+    every kept weight with the guess removed is drawn only through the fallback that
+    keeps it."""
+    vals = np.array([1.0, 3.0, 1.0, 2.0, 3.0, 0.5], dtype=np.float32)
+    bits = oacc.bf16_bits(vals)[None, :]
+    order = [1, 4, 3, 0, 2, 5]  # key descending, index ascending
+    seen = []
+    for step in range(4000):
+        u = oacc.uniform(5, step, 63)
+        seen.append((u, oacc.sampled_accept_v3(bits, [], 0.7, 1.0, seed=5, step=step)[0]))
+    seen.sort()
+    ranks = [order.index(t) for _, t in seen]
+    assert ranks == sorted(ranks) and set(ranks) == set(range(6))
+    one = oacc.bf16_bits(np.array([5.0, -200.0], dtype=np.float32))
+    rows = np.stack([one, one])
+    outs = {tuple(oacc.sampled_accept_v3(rows, [1], 1.0, 1.0, seed=1, step=s)) for s in range(50)}
+    assert outs == {(0,)}  # guess 1 weighs 0: rejected, and the draw without it is token 0
+    outs = {tuple(oacc.sampled_accept_v3(rows, [0], 1.0, 1.0, seed=1, step=s)) for s in range(50)}
+    assert outs == {(0, 0)}  # guess 0 holds all the weight: always kept
+
+
 # ------------------------------------------------------------------ A7 / A8 int8
 def test_quantize_round_trip_reference_kat():
     torch.manual_seed(0)
