@@ -639,6 +639,51 @@ class GemmWorkload:
             self.launch(name, i)
 
 
+def run_accept_sampled_kernel_only(torch, reps: int = 20) -> dict:
+    """Sampled acceptance alone (ne_accept) at the verify step's shape: 64 sequences x 5
+    rows x 151,936 bf16 logits, 4 n-gram guesses each, T = 0.8, top-p 1 and 0.9.  Logits
+    N(0, 1) with one token per row raised to 10.6 (about 0.63 of the row's probability at
+    T = 0.8); a guess is that token with probability 0.8, else a random one, so that
+    sequences keep 0..4 guesses.  HIP-graph replays, timed with events on the replay
+    stream; reports the kept-guess histogram of the call."""
+    from nanoengine_amd import kernels
+    from nanoengine_amd.qwen3 import QWEN3_0_6B as cfg
+
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(5)
+    vocab, b, k = cfg.vocab_size, NUM_SEQS, K_DRAFT
+    logits = torch.randn(b * (k + 1), vocab, generator=g)
+    top = torch.randint(0, vocab, (b * (k + 1),), generator=g)
+    logits[torch.arange(b * (k + 1)), top] = 10.6
+    logits = logits.to(torch.bfloat16)
+    targets = top.view(b, k + 1)[:, :k].to(torch.int32)
+    drafts = torch.where(torch.rand(b, k, generator=g) < 0.8, targets,
+                         torch.randint(0, vocab, (b, k), generator=g, dtype=torch.int32))
+    d = lambda t: t.contiguous().to(dev)
+    logits, drafts = d(logits), d(drafts)
+    nd = d(torch.full((b,), k, dtype=torch.int32))
+    rs = d(torch.arange(b, dtype=torch.int32) * (k + 1))
+    seeds = d(torch.arange(b, dtype=torch.int64) * 1000003 + 17)
+    steps = d(torch.zeros(b, dtype=torch.int64))
+    temps = d(torch.full((b,), 0.8, dtype=torch.float32))
+    out = {"workload": f"ne_accept, {b} seqs x {k + 1} rows x {vocab} bf16 logits N(0, 1), one token per row at "
+                       f"10.6, {k} guesses per sequence (that token w.p. 0.8, else random), T = 0.8"}
+    for top_p in (1.0, 0.9):
+        tops = d(torch.full((b,), top_p, dtype=torch.float32))
+        o = torch.empty(b, k + 1, dtype=torch.int32, device=dev)
+        n = torch.empty(b, dtype=torch.int32, device=dev)
+
+        def body():
+            kernels.accept(drafts, nd, rs, vocab, logits=logits, temperature=temps, top_p=tops, any_sampled=True,
+                           seeds=seeds, steps=steps, out_tokens=o, num_out=n)
+
+        us = _graph_time_us(torch, body, reps)
+        kept = (n.cpu() - 1).tolist()
+        out[f"top_p_{top_p}"] = {"avg_us": round(us, 2),
+                                 "kept_hist": {str(c): kept.count(c) for c in range(k + 1)}}
+    return out
+
+
 GEMM_NAMES = ("qkv_fused", "gate_up_swiglu", "o_proj", "down_proj", "lm_head")
 
 
@@ -1065,7 +1110,8 @@ def main() -> int:
     parser.add_argument("--temperature", type=float, default=0.0)
     parser.add_argument("--eager", dest="graph", action="store_false",
                         help="launch the step's kernels one by one instead of replaying a HIP graph")
-    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline", "long", "draft"),
+    parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline", "long", "draft",
+                                           "accept"),
                         default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-torch-baseline", action="store_true")
@@ -1113,6 +1159,12 @@ def main() -> int:
     if args.only in ("all", "gemm"):
         gemm = run_gemm_roofline(torch, counters=counters)
         log(f"gemm: {gemm['achieved']} TFLOP/s over QKV and gate|up")
+    if args.only == "accept":  # the sampled acceptance kernel alone, and the T = 0.8 step
+        s_res = run_verify(args, torch, temperature=0.8, steps=args.steps, warmup=args.warmup)
+        print(json.dumps({"accept_kernel_only": run_accept_sampled_kernel_only(torch),
+                          "sampled_verify_step_us": round(1e6 * s_res["elapsed"] / args.steps, 1),
+                          "sampled_device_step_us": round(s_res["device_us_per_step"], 1)}), flush=True)
+        return 0
     torch_base = None
     if args.only in ("all", "baseline") and not args.no_torch_baseline:
         from nanoengine_amd.qwen3 import QWEN3_0_6B, random_state_dict
@@ -1130,6 +1182,8 @@ def main() -> int:
                    "accepted_per_step_hist": {str(k): v for k, v in sorted(s_res["kept_hist"].items())},
                    **s_res["stats"]}
         log(f"sampled: {sampled['verify_step_us']} us per step")
+        sampled["accept_kernel_only"] = run_accept_sampled_kernel_only(torch)
+        log(f"sampled acceptance kernel-only: {sampled['accept_kernel_only']}")
     draft_verify = None
     if args.only in ("all", "draft"):
         # draft-model speculation (the target's own weights as the draft), greedy

@@ -11,10 +11,36 @@
 // Greedy (temperature 0, ne/engine/sampling.py:32-34): target token of a row is
 // the argmax of its bf16 logits, first index on ties (torch.argmax order).
 //
-// Sampled contract (temperature T > 0).  The reference draws with
-// torch.rand / torch.multinomial, which no other implementation reproduces;
-// this build fixes an explicit, order-defined procedure instead, shared bit for
-// bit with the CPU oracle:
+// Sampled (temperature T > 0).  The reference draws with torch.rand /
+// torch.multinomial, which no other implementation reproduces; this build fixes
+// explicit procedures instead, shared bit for bit with the CPU oracle.
+//
+// One-hot guesses (n-gram, and the draft model's own draws): the integer-mass
+// contract.  Every token's weight is an integer that depends only on its bf16
+// order key k (larger logit, larger key; -0 as +0), so sums in any order are exact:
+//   invT = 1 / T (fp32 division); kmax = the row's largest key; mx = val(kmax) * invT
+//   E(k) = (uint32)(exp3(val(k) * invT - mx) * 2^31), truncated (E(kmax) = 2^31; tokens
+//          more than ~21.5 T below the largest logit weigh 0); exp3 = Cephes' Cody-Waite
+//          reduction and degree-5 polynomial with every step one fused multiply-add,
+//          0 below -86
+//   cnt(k) = tokens of key k; Z = sum_k cnt(k) E(k)
+//   top-p (P < 1): thr = max(1, (uint64)((double)Z * (double)P)); M(v) = sum_{k > v}
+//          cnt(k) E(k); tau = the smallest v with M(v) < thr; m = min(cnt(tau),
+//          ceil((thr - M(tau)) / E(tau))); kept: key > tau, or key == tau and fewer than m
+//          tokens of key tau precede it; K = M(tau) + m E(tau).  P >= 1 keeps all, K = Z.
+//   guess g of row i (U_i = the uniform's 24-bit integer): kept iff w_g >= K or
+//          (w_g > 0 and U_i * K < w_g * 2^24), w_g = E(key_g) if g is kept, else 0 (also
+//          for a guess outside the vocabulary)
+//   draw (a rejected row: its guess removed; the bonus row: nothing removed): the kept
+//          tokens in order of key (descending) then index (ascending), the guess removed
+//          unless that leaves no weight; R = their weight; t = floor(U * R / 2^24); the
+//          token is the first whose running weight exceeds t.
+// accept_rows_kernel decides every sampled row in its own work-group (histogram of the
+// row's keys, then key-space sums and one compare-only pass to place a draw); the
+// finish keeps guesses up to the first row that drew.
+//
+// With draft rows (a draft model's distribution per guess) the earlier fp32 contract
+// applies:
 //   z_j  = fp32(logit_j) / T                  (IEEE fp32 division)
 //   e_j  = cephes_exp(z_j - max_j z_j)        (Cephes expf, Moshier; 0 below -86)
 //   chunked total of a row vector w: S_c = sequential fp32 sum of w_j over chunk
@@ -28,15 +54,13 @@
 //          tau and fewer than m tokens of key tau precede it.  Without top-p every
 //          token is kept.  w_j = e_j when kept, else 0; K = chunked total of w;
 //          p'_j = w_j / K.
-//   guess g of row i (n-gram, one-hot draft) is kept iff a >= 1 or (a > 0 and
-//          u_i < a), a = p'_g; a rejection draws from w with g removed.
 //   draw from a weight row r with x removed (x = -1: none): R = chunked total (if
 //          R <= 0 the exclusion is dropped); t = u_draw * R; c* = first chunk with
 //          prefix_c + R_c > t (prefix summed sequentially); j = first index in c*
 //          with prefix_c* + q_j > t, q_j the sequential in-chunk sum from the chunk
 //          start.  If no chunk qualifies (rounding), the last index with r_j > 0.
-//   uniforms: Philox4x32-10 (Salmon et al., SC'11), key = seed, counter =
-//          (step lo, step hi, j / 4, 0), word j % 4, u = (word >> 8) * 2^-24;
+//   uniforms (both contracts): Philox4x32-10 (Salmon et al., SC'11), key = seed,
+//          counter = (step lo, step hi, j / 4, 0), word j % 4, u = (word >> 8) * 2^-24;
 //          j = i for guess i, j = 63 for the draw.
 //   with draft rows (a draft model's distribution per guess): bf16 draft logits
 //          give q' by the same procedure (same T and top-p); fp32 rows are
@@ -45,7 +69,8 @@
 //          division, q'_j likewise, the difference one op), falling back to w when
 //          r has no mass (verifier.py:44-56).
 // FP contraction is disabled in this file's arithmetic so that every operation on
-// that path is a single IEEE-rounded fp32 op, as in the C oracle.
+// these paths is a single IEEE-rounded fp32 op (exp3's fused multiply-adds are written
+// out), as in the C oracle.
 #include "ne_common.hpp"
 
 namespace ne {
@@ -166,6 +191,7 @@ struct AcceptParams {
   int draft_dtype;         // NE_DTYPE_BF16: logits, NE_DTYPE_FP32: probabilities
   int64_t dld;
   const int32_t* draft_row_start;
+  int rows_done;  // sampled one-hot rows decided by accept_rows_kernel (out_tokens holds them)
 };
 
 // greedy target of one row: argmax over bf16 logits or the LM-head partials
@@ -451,6 +477,444 @@ __device__ int draw_residual(const Dist& d, const DistLds& L, const Dist& dq, co
   return res;
 }
 
+// ---- integer-mass contract for one-hot guesses: one work-group per verify row -------
+// Every token's weight depends only on its bf16 key: E(k) = floor(exp3(val(k) / T - max)
+// * 2^31) (header).  The row's keys are counted once into an LDS histogram; the sum Z,
+// the top-p threshold, the guess's acceptance and the draw's key all come from the
+// histogram (exp3 once per occupied key), and integer sums make every parallel order
+// give the oracle's result.  A draw then finds the r-th occurrence of its key in index
+// order with one compare-only pass.  Row i of sequence b writes out_tokens[b][i]: -2
+// when it keeps its guess, else the token it draws (the bonus row always draws); the
+// finish in accept_kernel keeps the rows up to the first that drew.
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / kWave;
+constexpr int kKeysPerThread = 65536 / kRowThreads;
+constexpr int kMaxWraps = 16;  // 16-bit count wraps recorded per row: vocab < 16 * 65536
+
+struct RowLds {
+  // counts of keys 2w (bits 0..15) and 2w + 1 (bits 16..31), modulo the wraps below
+  uint32_t hist[32768];
+  uint64_t seg_mass[kRowThreads];  // mass of keys [64 s, 64 s + 64)
+  uint64_t wave_part[kRowWaves];
+  uint32_t wrap_key[kMaxWraps];  // bit 31: the high half's running value (count of key +
+  int n_wrap;                    //   low carries) crossed 65536; else the low half did
+  uint32_t wrap_key_spare[kRowWaves];  // occupied segments per wave
+  uint16_t seg_list[kRowThreads];      // occupied segments in order
+  int n_seg;
+  uint64_t k_total, above, want;
+  uint32_t kmax, tau, m, kappa;
+  int seg;
+};
+
+__device__ __forceinline__ float exp3(float x) {
+  if (x < -86.0f) return 0.0f;
+  const float fx = floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
+  float r = __builtin_fmaf(fx, -0.693359375f, x);
+  r = __builtin_fmaf(fx, 2.12194440e-4f, r);
+  float y = __builtin_fmaf(1.9875691500E-4f, r, 1.3981999507E-3f);
+  y = __builtin_fmaf(y, r, 8.3334519073E-3f);
+  y = __builtin_fmaf(y, r, 4.1665795894E-2f);
+  y = __builtin_fmaf(y, r, 1.6666665459E-1f);
+  y = __builtin_fmaf(y, r, 5.0000001201E-1f);
+  const float z = r * r;
+  y = __builtin_fmaf(y, z, r);
+  y = y + 1.0f;
+  const int n = (int)fx;
+  return y * __builtin_bit_cast(float, (uint32_t)(n + 127) << 23);
+}
+
+// count of key k: its 16-bit half plus 65536 per recorded wrap (a high half's running
+// value also holds the low half's carries, which the low half's own wraps count)
+__device__ __forceinline__ uint32_t row_count(const RowLds& L, uint32_t k) {
+  const uint32_t w = L.hist[k >> 1];
+  uint32_t c = (k & 1) ? (w >> 16) : (w & 0xFFFFu);
+  const int n = min(L.n_wrap, kMaxWraps);
+  for (int i = 0; i < n; ++i) {
+    const uint32_t e = L.wrap_key[i], ek = e & 0xFFFFu;
+    if (e >> 31) {  // a high-half crossing of key ek (odd)
+      if (ek == k) c += 65536u;
+    } else if (ek == k) {  // a low-half wrap of key ek (even)
+      c += 65536u;
+    } else if ((k & 1) && ek == k - 1) {  // its carry went into key k's half
+      c -= 1u;
+    }
+  }
+  return c;
+}
+
+__device__ __forceinline__ uint32_t row_weight(uint32_t k, float invT, float mx) {
+  const float e = exp3(bf16_to_f32(bf16_of_key16(k)) * invT - mx);
+  return (uint32_t)(e * 2147483648.0f);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64v(uint64_t v, int o) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// over the lanes of a wave: the sum of v over higher lanes (integers: any order)
+__device__ __forceinline__ uint64_t wave_suffix_excl_u64(uint64_t v) {
+  const int lane = threadIdx.x % kWave;
+  uint64_t incl = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t lo = __shfl_down((uint32_t)incl, o), hi = __shfl_down((uint32_t)(incl >> 32), o);
+    if (lane + o < kWave) incl += ((uint64_t)hi << 32) | lo;
+  }
+  return incl - v;
+}
+
+// exclusive sum over the work-group's threads (ascending) of a u64, and the total
+__device__ __forceinline__ uint64_t row_scan_u64(uint64_t v, RowLds& L, uint64_t* total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  uint64_t incl = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t lo = __shfl_up((uint32_t)incl, o), hi = __shfl_up((uint32_t)(incl >> 32), o);
+    if (lane >= o) incl += ((uint64_t)hi << 32) | lo;
+  }
+  __syncthreads();
+  if (lane == kWave - 1) L.wave_part[wave] = incl;
+  __syncthreads();
+  uint64_t before = 0, all = 0;
+  for (int w = 0; w < kRowWaves; ++w) {
+    const uint64_t x = L.wave_part[w];
+    before += w < wave ? x : 0;
+    all += x;
+  }
+  *total = all;
+  return before + incl - v;
+}
+
+__global__ __launch_bounds__(kRowThreads) void accept_rows_kernel(AcceptParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  RowLds& L = *(RowLds*)smem;
+  const int R = p.max_drafts + 1;
+  const int b = blockIdx.x / R;
+  const int i = blockIdx.x % R;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave, wave = tid / kWave;
+  const float T = p.temperature[b];
+  if (!(T > 0.f)) return;                                        // greedy: accept_kernel
+  if (p.history != nullptr && p.history_len[b] == 0) return;     // inactive slot
+  const int g = min(max(p.num_drafts[b], 0), p.max_drafts);
+  if (i > g) return;
+  const int V = p.vocab;
+  const uint16_t* row = p.logits + (int64_t)(p.row_start[b] + i) * p.ld;
+  const float top_p = p.top_p != nullptr ? p.top_p[b] : 1.f;
+  const bool topp = top_p < 1.0f;
+  const int guess = i < g ? p.drafts[(int64_t)b * p.max_drafts + i] : -1;
+
+  // ---- histogram of the row's keys
+  for (int w = tid; w < 32768 / 4; w += kRowThreads) ((uint4*)L.hist)[w] = uint4{0u, 0u, 0u, 0u};
+  if (tid == 0) L.n_wrap = 0;
+  __syncthreads();
+  auto count_key = [&](uint32_t k) {
+    const uint32_t sh = (k & 1) * 16;
+    const uint32_t old = atomicAdd(&L.hist[k >> 1], 1u << sh);
+    // a low half that was 0xFFFF wrapped (and carried into the high half); a high half's
+    // running value crosses 65536 when it was 0xFFFF and gains 1 by this add or its carry
+    const bool low_wrap = sh == 0 && (old & 0xFFFFu) == 0xFFFFu;
+    const bool high_cross = (old >> 16) == 0xFFFFu && (sh == 16 || low_wrap);
+    if (low_wrap || high_cross) {
+      const int slot = atomicAdd(&L.n_wrap, (int)low_wrap + (int)high_cross);
+      if (low_wrap && slot < kMaxWraps) L.wrap_key[slot] = k;
+      if (high_cross && slot + (int)low_wrap < kMaxWraps) L.wrap_key[slot + (int)low_wrap] = (k | 1u) | 0x80000000u;
+    }
+  };
+  if ((((uintptr_t)row) & 15) == 0) {
+    // 16-byte loads, four per thread requested before their keys are counted
+    const int nvec = V / 8;
+    const uint4* rv = (const uint4*)row;
+    for (int v0 = tid; v0 < nvec; v0 += 4 * kRowThreads) {
+      uint4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * kRowThreads;
+        q[u] = v < nvec ? rv[v] : uint4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (v0 + u * kRowThreads >= nvec) break;
+        const uint32_t w4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          count_key(key16((uint16_t)(w4[h] & 0xFFFFu)));
+          count_key(key16((uint16_t)(w4[h] >> 16)));
+        }
+      }
+    }
+    for (int j = nvec * 8 + tid; j < V; j += kRowThreads) count_key(key16(row[j]));
+  } else {
+    for (int j = tid; j < V; j += kRowThreads) count_key(key16(row[j]));
+  }
+  __syncthreads();
+
+  // ---- segment tid (keys 64 tid .. 64 tid + 63): its 32 histogram words at once, its
+  // largest key and whether any key is occupied (a count that wrapped to 0 in its 16-bit
+  // half is found through row_count when any wrap was recorded)
+  const uint32_t k0 = (uint32_t)tid * kKeysPerThread;
+  bool occupied = false;
+  uint32_t top = 0;  // largest occupied key + 1
+  {
+    const uint4* hw = (const uint4*)(L.hist + tid * (kKeysPerThread / 2));
+    uint32_t w[kKeysPerThread / 2];
+#pragma unroll
+    for (int q = 0; q < kKeysPerThread / 8; ++q) {
+      const uint4 v = hw[q];
+      w[4 * q] = v.x;
+      w[4 * q + 1] = v.y;
+      w[4 * q + 2] = v.z;
+      w[4 * q + 3] = v.w;
+    }
+    if (L.n_wrap == 0) {
+#pragma unroll
+      for (int j = 0; j < kKeysPerThread / 2; ++j) {
+        if (w[j] & 0xFFFFu) top = k0 + 2 * j + 1;
+        if (w[j] >> 16) top = k0 + 2 * j + 2;
+      }
+    } else {
+      for (int j = 0; j < kKeysPerThread; ++j)
+        if (row_count(L, k0 + j)) top = k0 + j + 1;
+    }
+    occupied = top != 0;
+  }
+  {
+    uint32_t m = top;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor(m, o));
+    if (lane == 0) L.wave_part[wave] = m;
+  }
+  // occupied segments listed in order (their masses need exp3; the rest weigh 0)
+  const uint64_t occ_mask = __builtin_amdgcn_ballot_w64(occupied);
+  if (lane == 0) L.wrap_key_spare[wave] = (uint32_t)__builtin_popcountll(occ_mask);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t mm = 0;
+    for (int w = 0; w < kRowWaves; ++w) mm = max(mm, (uint32_t)L.wave_part[w]);
+    L.kmax = mm - 1;
+  }
+  {
+    uint32_t at = 0, n_occ = 0;
+    for (int w = 0; w < kRowWaves; ++w) {
+      at += w < wave ? L.wrap_key_spare[w] : 0u;
+      n_occ += L.wrap_key_spare[w];
+    }
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(occ_mask >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)occ_mask, 0u));
+    if (occupied) L.seg_list[at + rank] = (uint16_t)tid;
+    L.seg_mass[tid] = 0;
+    if (tid == 0) L.n_seg = (int)n_occ;
+  }
+  __syncthreads();
+  const uint32_t kmax = L.kmax;
+  const float invT = 1.0f / T;
+  const float mx = bf16_to_f32(bf16_of_key16(kmax)) * invT;
+  // mass of key 64 s + lane (every lane of a wave, for one segment s)
+  auto lane_mass = [&](int seg) -> uint64_t {
+    const uint32_t k = (uint32_t)seg * kKeysPerThread + lane;
+    const uint32_t c = row_count(L, k);
+    return c ? (uint64_t)c * row_weight(k, invT, mx) : 0;
+  };
+
+  // ---- masses of the occupied segments: wave w takes list entries w, w + 16, ...
+  for (int e = wave; e < L.n_seg; e += kRowWaves) {
+    const int seg = L.seg_list[e];
+    uint64_t mass = lane_mass(seg);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mass += shfl_xor_u64v(mass, o);
+    if (lane == 0) L.seg_mass[seg] = mass;
+  }
+  __syncthreads();
+  const uint64_t mine = L.seg_mass[tid];
+  uint64_t z;
+  const uint64_t below = row_scan_u64(mine, L, &z);
+  const uint64_t above = z - below - mine;  // mass of the keys above segment tid
+
+  // ---- top-p: thr, then tau in the segment where the mass above crosses it
+  uint64_t thr = 0;
+  if (topp) {
+    thr = (uint64_t)((double)z * (double)top_p);
+    thr = thr < 1 ? 1 : thr;
+    if (above < thr && above + mine >= thr) {
+      L.seg = tid;
+      L.above = above;
+    }
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    if (topp) {
+      const int seg = L.seg;
+      const uint64_t mass = lane_mass(seg);
+      const uint64_t run = L.above + wave_suffix_excl_u64(mass);  // M(key): mass above it
+      const bool here = run < thr && run + mass >= thr;
+      if (here) {
+        const uint32_t k = (uint32_t)seg * kKeysPerThread + lane;
+        const uint32_t c = row_count(L, k);
+        const uint64_t e = row_weight(k, invT, mx);
+        uint64_t m = (thr - run + e - 1) / e;
+        m = m > c ? c : m;
+        L.tau = k;
+        L.m = (uint32_t)m;
+        L.k_total = run + m * e;
+      }
+    } else if (tid == 0) {
+      L.tau = 0;
+      L.m = 0;
+      L.k_total = z;
+    }
+  }
+  __syncthreads();
+  const uint32_t tau = L.tau, m_tau = L.m;
+  const uint64_t K = L.k_total;
+
+  // ---- the guess: its weight if kept (ties at tau kept when fewer than m precede it)
+  uint64_t wg = 0;
+  uint32_t kg = 0;
+  if (guess >= 0) {
+    // a guess outside the vocabulary weighs 0 (never kept, nothing removed from the draw)
+    const bool valid = guess < V;
+    kg = valid ? key16(row[guess]) : 0u;
+    bool kept = valid && (!topp || kg > tau);
+    if (valid && topp && kg == tau) {
+      if (m_tau >= row_count(L, tau)) {
+        kept = true;
+      } else {  // its rank among key-tau tokens, counted over [0, guess)
+        int mine_c = 0;
+        for (int j = tid; j < guess; j += kRowThreads) mine_c += key16(row[j]) == tau;
+        uint64_t rank;
+        row_scan_u64((uint64_t)mine_c, L, &rank);
+        kept = rank < m_tau;
+      }
+    }
+    wg = kept ? row_weight(kg, invT, mx) : 0;
+    const uint32_t u = (uint32_t)(philox_uniform(p.seeds[b], p.steps[b], i) * 16777216.0f);
+    // kept iff w >= K or (w > 0 and u K < w 2^24): u K < 2^74, w 2^24 < 2^56
+    const uint64_t lo = (uint64_t)u * K, hi = __umul64hi((uint64_t)u, K);
+    if (wg >= K || (wg > 0 && hi == 0 && lo < (wg << 24))) {
+      if (tid == 0) p.out_tokens[(int64_t)b * R + i] = -2;
+      return;
+    }
+  }
+
+  // ---- the draw: kept tokens by key (descending) then index, the guess removed
+  int x = guess;
+  uint64_t rw = K - wg;
+  if (rw == 0) {  // the guess held all the kept weight: draw without removing it
+    x = -1;
+    wg = 0;
+    rw = K;
+  }
+  const uint32_t ud = (uint32_t)(philox_uniform(p.seeds[b], p.steps[b], 63) * 16777216.0f);
+  const uint64_t t = (uint64_t)ud * (rw >> 24) + (((uint64_t)ud * (rw & 0xFFFFFFu)) >> 24);
+  const int seg_tau = topp ? (int)(tau / kKeysPerThread) : -1;
+  const int seg_g = wg ? (int)(kg / kKeysPerThread) : -1;
+  // kept mass of segment tid: all of it above tau's segment, K minus the mass above it
+  // in tau's segment, none below; less the removed guess
+  uint64_t kept_seg = mine;
+  if (topp && tid < seg_tau) kept_seg = 0;
+  if (tid == seg_tau) kept_seg = K - above;
+  if (tid == seg_g) kept_seg -= wg;
+  uint64_t tot;
+  const uint64_t kb = row_scan_u64(kept_seg, L, &tot);
+  const uint64_t ka = tot - kb - kept_seg;  // kept mass above segment tid
+  if (ka <= t && t < ka + kept_seg) {
+    L.seg = tid;
+    L.above = ka;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    const int seg = L.seg;
+    const uint32_t k = (uint32_t)seg * kKeysPerThread + lane;
+    uint64_t c = (topp && k < tau) ? 0 : ((topp && k == tau) ? m_tau : row_count(L, k));
+    if (wg && k == kg) c -= 1;
+    const uint64_t e = c ? row_weight(k, invT, mx) : 0;
+    const uint64_t w = c * e;
+    const uint64_t run = L.above + wave_suffix_excl_u64(w);
+    if (w && run <= t && t < run + w) {
+      L.kappa = k;
+      L.want = (t - run) / e;
+    }
+  }
+  __syncthreads();
+  // ---- the want-th occurrence of key kappa in index order, x skipped.  Wave w counts a
+  // contiguous stretch of the row, 8 tokens per lane per 16-byte load (the next load
+  // requested before the current one is used); the waves' counts are summed in order and
+  // the wave holding the token finds its lane by a scan of the lanes' counts.
+  const uint32_t kappa = L.kappa;
+  const uint64_t want = L.want;
+  // 16-byte loads need an aligned row whose length is a multiple of 8 (no load crosses V)
+  const bool vec = (((uintptr_t)row) & 15) == 0 && (V & 7) == 0;
+  const int step_t = vec ? 8 * kWave : kWave;  // tokens per wave iteration
+  const int span = ((V + kRowWaves - 1) / kRowWaves + step_t - 1) / step_t * step_t;
+  const int w_lo = wave * span, w_hi = min(w_lo + span, V);
+  // hits among this lane's tokens j0 + 8 lane .. +8 (vec) or j0 + lane
+  auto lane_hits = [&](int j0, const uint4& q) -> uint32_t {
+    uint32_t bits = 0;
+    if (vec) {
+      const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const int j = j0 + 8 * lane + h;
+        const uint16_t tok = (uint16_t)((h & 1) ? (w4[h >> 1] >> 16) : (w4[h >> 1] & 0xFFFFu));
+        bits |= (uint32_t)(j < w_hi && j != x && key16(tok) == kappa) << h;
+      }
+    } else {
+      const int j = j0 + lane;
+      bits = j < w_hi && j != x && key16(row[j]) == kappa;
+    }
+    return bits;
+  };
+  auto load_at = [&](int j0) -> uint4 {
+    const int j = j0 + 8 * lane;
+    return (vec && j < w_hi) ? *(const uint4*)(row + j) : uint4{0u, 0u, 0u, 0u};
+  };
+  uint32_t occ = 0;
+  for (int j0 = w_lo; j0 < w_hi; j0 += 4 * step_t) {  // four loads per lane in flight
+    uint4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = load_at(j0 + u * step_t);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (j0 + u * step_t < w_hi) occ += __builtin_popcount(lane_hits(j0 + u * step_t, q[u]));
+  }
+  uint32_t wocc = occ;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) wocc += __shfl_xor(wocc, o);
+  if (lane == 0) L.wave_part[wave] = wocc;
+  __syncthreads();
+  uint64_t before = 0;
+  for (int w = 0; w < wave; ++w) before += L.wave_part[w];
+  if (before <= want && want < before + wocc) {  // uniform within the wave
+    uint64_t seen = before;
+    uint4 q = load_at(w_lo);
+    for (int j0 = w_lo; j0 < w_hi; j0 += step_t) {
+      const uint4 nq = j0 + step_t < w_hi ? load_at(j0 + step_t) : q;
+      const uint32_t bits = lane_hits(j0, q);
+      q = nq;
+      const uint32_t n = __builtin_popcount(bits);
+      uint32_t incl = n;  // inclusive scan of the lanes' counts
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t t2 = __shfl_up(incl, o);
+        if (lane >= o) incl += t2;
+      }
+      const uint32_t total = __shfl(incl, kWave - 1);
+      if (want < seen + total) {  // uniform
+        const uint64_t start_l = seen + incl - n;
+        if (start_l <= want && want < start_l + n) {
+          uint32_t r = (uint32_t)(want - start_l), bb = bits;
+          for (uint32_t c = 0; c < r; ++c) bb &= bb - 1;  // drop the r lowest hits
+          const int h = __builtin_ctz(bb);
+          p.out_tokens[(int64_t)b * R + i] = vec ? j0 + 8 * lane + h : j0 + lane;
+        }
+        break;
+      }
+      seen += total;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
   __shared__ uint64_t s_red[kThreads / kWave];
   __shared__ uint64_t s_rows[kMaxRows][kThreads / kWave];
@@ -544,6 +1008,18 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptParams p) {
         s_kept = kept;
         s_final = s_target[kept];
       }
+    }
+    __syncthreads();
+  } else if (p.rows_done) {
+    // rows decided by accept_rows_kernel: -2 where the row kept its guess, else the token
+    // it drew; the sequence keeps guesses up to the first row that drew
+    if (tid <= g) s_target[tid] = p.out_tokens[(int64_t)b * (p.max_drafts + 1) + tid];
+    __syncthreads();
+    if (tid == 0) {
+      int k = 0;
+      while (k < g && s_target[k] == -2) ++k;
+      s_kept = k;
+      s_final = s_target[k];
     }
     __syncthreads();
   } else {
@@ -679,6 +1155,23 @@ extern "C" int ne_accept(const void* logits, int64_t ld_logits, const uint64_t* 
   p.draft_dtype = draft_dtype;
   p.dld = ld_draft;
   p.draft_row_start = draft_row_start;
+  if (any_sampled && draft_rows == nullptr) {
+    // one-hot guesses under the integer-mass contract: every sampled row decided by its
+    // own work-group first, then the per-sequence finish
+    NE_CHECK_SUPPORTED(vocab <= kMaxWraps / 2 * 65536, "sampled acceptance supports a vocabulary up to %d (got %d)",
+                       kMaxWraps / 2 * 65536, vocab);
+    static const hipError_t attr = hipFuncSetAttribute((const void*)accept_rows_kernel,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(RowLds));
+    if (attr != hipSuccess) {
+      set_error("accept: cannot reserve %d bytes of LDS: %s", (int)sizeof(RowLds), hipGetErrorString(attr));
+      return NE_ELAUNCH;
+    }
+    p.rows_done = 1;
+    hipLaunchKernelGGL(accept_rows_kernel, dim3((unsigned)num_seqs * (unsigned)(max_drafts + 1)), dim3(kRowThreads),
+                       sizeof(RowLds), (hipStream_t)stream, p);
+    const int rc = check_launch("accept_rows");
+    if (rc != NE_OK) return rc;
+  }
   hipLaunchKernelGGL(accept_kernel, dim3(num_seqs), dim3(kThreads), 0, (hipStream_t)stream, p);
   return check_launch("accept");
 }

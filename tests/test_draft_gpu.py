@@ -207,7 +207,8 @@ def test_sampled_draft_step_matches_the_c_oracle():
         g = len(rec["drafts"])
         assert g == rec["requested"] > 0
         for j, guess in enumerate(rec["drafts"]):
-            drawn = oacc.sampled_accept(d_bits[slot * k + j : slot * k + j + 1], [], 0.8, seed, step + ((j + 1) << 48))
+            drawn = oacc.sampled_accept_v3(d_bits[slot * k + j : slot * k + j + 1], [], 0.8, 1.0, seed,
+                                           step + ((j + 1) << 48))
             assert drawn == [guess], f"slot {slot} guess {j}"
         want = oacc.sampled_accept_draft(t_bits[slot * (k + 1) : slot * (k + 1) + g + 1],
                                          d_bits[slot * k : slot * k + g], rec["drafts"], 0.8, seed, step)
@@ -280,8 +281,8 @@ def test_mixed_greedy_and_sampled_draft_batch_matches_the_oracles():
             seed = seqs[slot].sampling_generator.seed
             step = int(eng.runner.h_steps[slot]) - 1
             for j, guess in enumerate(rec["drafts"]):
-                drawn = oacc.sampled_accept(d_bits[slot * k + j : slot * k + j + 1], [], temp, seed,
-                                            step + ((j + 1) << 48))
+                drawn = oacc.sampled_accept_v3(d_bits[slot * k + j : slot * k + j + 1], [], temp, 1.0, seed,
+                                               step + ((j + 1) << 48))
                 assert drawn == [guess], f"slot {slot} guess {j}"
             assert rec["out"] == oacc.sampled_accept_draft(t_rows, d_rows, rec["drafts"], temp, seed, step)
         checked.add(temp > 0)

@@ -376,7 +376,7 @@ def test_mixed_greedy_and_top_p_sampled_batch():
             p = params[slot]
             if p.temperature > 0 and checked < 12:
                 g = len(rec[slot]["drafts"])
-                want = oracle_accept.sampled_accept_v2(logits[slot * 5 : slot * 5 + g + 1], rec[slot]["drafts"],
+                want = oracle_accept.sampled_accept_v3(logits[slot * 5 : slot * 5 + g + 1], rec[slot]["drafts"],
                                                        p.temperature, p.top_p, seqs[slot].sampling_generator.seed,
                                                        int(steps[slot]))
                 assert rec[slot]["out"] == want, f"slot {slot}"

@@ -218,8 +218,8 @@ def test_sampled_accept_matches_c_oracle(device, vocab, temperature):
     out, nout = out.cpu(), nout.cpu()
     bits = logits.view(torch.int16).numpy().view(np.uint16)
     for s in range(b):
-        want = oracle_accept.sampled_accept(bits[rs[s] : rs[s] + nd[s] + 1], drafts[s, : nd[s]].tolist(),
-                                            temperature, int(seeds[s]), int(steps[s]))
+        want = oracle_accept.sampled_accept_v3(bits[rs[s] : rs[s] + nd[s] + 1], drafts[s, : nd[s]].tolist(),
+                                               temperature, 1.0, int(seeds[s]), int(steps[s]))
         assert out[s, : nout[s]].tolist() == want, f"sequence {s}"
 
 
@@ -236,7 +236,8 @@ def test_sampled_golden_fixture(device):
     out, nout = kernels.accept(d(np.array(case["drafts"], dtype=np.int32)), d(np.array(case["num_drafts"], dtype=np.int32)),
                                d(np.array(case["row_start"], dtype=np.int32)), vocab, logits=logits.to(device),
                                temperature=case["temperature"], seeds=d(np.array(case["seeds"], dtype=np.int64)),
-                               steps=d(np.array(case["steps"], dtype=np.int64)))
+                               steps=d(np.array(case["steps"], dtype=np.int64)),
+                               top_p=d(np.array(case["top_p"], dtype=np.float32)))
     torch.cuda.synchronize()
     got = [out[s, : nout[s]].tolist() for s in range(len(case["expected"]))]
     assert got == case["expected"]
@@ -268,9 +269,106 @@ def test_top_p_mixed_batch_matches_c_oracle(device, top_p):
         if temps[s] == 0:
             want = oracle_accept.greedy_accept(lf[rows], guesses)
         else:
-            want = oracle_accept.sampled_accept_v2(bits[rows], guesses, float(temps[s]), float(tops[s]),
+            want = oracle_accept.sampled_accept_v3(bits[rows], guesses, float(temps[s]), float(tops[s]),
                                                    int(seeds[s]), int(steps[s]))
         assert out[s, : nout[s]].tolist() == want, f"sequence {s} (T={temps[s]}, top_p={tops[s]})"
+
+
+def _v3_batch(device, rows_per_seq, guesses, temps, tops, seed0=11):
+    """Run ne_accept on explicit rows (uint16 bf16 patterns per sequence) and compare every
+    sequence with the C oracle's integer-mass contract."""
+    vocab = rows_per_seq[0].shape[1]
+    b, k = len(rows_per_seq), max(1, max(len(g) for g in guesses))
+    bits = np.concatenate(rows_per_seq)
+    rs = np.concatenate([[0], np.cumsum([r.shape[0] for r in rows_per_seq])[:-1]]).astype(np.int32)
+    nd = np.array([len(g) for g in guesses], dtype=np.int32)
+    drafts = np.zeros((b, k), dtype=np.int32)
+    for s, g in enumerate(guesses):
+        drafts[s, : len(g)] = g
+    seeds = np.arange(seed0, seed0 + b, dtype=np.int64) * 7919
+    steps = np.arange(b, dtype=np.int64) * 3
+    logits = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    d = lambda a: torch.as_tensor(a).to(device)
+    out, nout = kernels.accept(d(drafts), d(nd), d(rs), vocab, logits=logits.to(device),
+                               temperature=d(np.asarray(temps, dtype=np.float32)),
+                               top_p=d(np.asarray(tops, dtype=np.float32)), any_sampled=True,
+                               seeds=d(seeds), steps=d(steps))
+    torch.cuda.synchronize()
+    out, nout = out.cpu(), nout.cpu()
+    for s in range(b):
+        want = oracle_accept.sampled_accept_v3(rows_per_seq[s], list(guesses[s]), float(temps[s]), float(tops[s]),
+                                               int(seeds[s]), int(steps[s]))
+        assert out[s, : nout[s]].tolist() == want, f"sequence {s}"
+    return [out[s, : nout[s]].tolist() for s in range(b)]
+
+
+def test_v3_count_wraps_on_both_halves_of_a_histogram_word(device):
+    """One bf16 value filling most of a 151,936-token row wraps its 16-bit histogram count
+    (twice): an even key (low half, whose carries enter its neighbour's half), an odd key
+    (high half), and both keys of one word together.  Counts, weights and draws equal the
+    C oracle's."""
+    vocab = 151936
+    rng = np.random.default_rng(41)
+
+    def row_with(values_counts):
+        vals = (rng.standard_normal(vocab) * 0.5).astype(np.float32)
+        pos = rng.permutation(vocab)
+        at = 0
+        for v, n in values_counts:
+            vals[pos[at : at + n]] = v
+            at += n
+        return oracle_accept.bf16_bits(vals)
+
+    even = np.float32(1.0)       # bf16 0x3F80: key 0xBF80 (even)
+    odd = np.float32(1.0078125)  # bf16 0x3F81: key 0xBF81 (odd), the same histogram word
+    assert oracle_accept.key16(oracle_accept.bf16_bits(np.array([even, odd])))[0] % 2 == 0
+    rows, guesses, temps, tops = [], [], [], []
+    for vc in ([(even, 140000)], [(odd, 140000)], [(even, 70000), (odd, 70000)], [(odd, 131072)],
+               [(even, 65536), (odd, 65535)]):
+        r = np.stack([row_with(vc) for _ in range(3)])
+        rows.append(r)
+        guesses.append([int(np.flatnonzero(oracle_accept.bf16_to_f32(r[0]) == vc[0][0])[0]), 5])
+        temps.append(0.7)
+        tops.append(0.95)
+    _v3_batch(device, rows, guesses, temps, tops)
+
+
+def test_v3_top_p_ties_out_of_vocabulary_and_all_weight_guesses(device):
+    """Top-p thresholds inside a run of equal logits (a guess among the ties, before and
+    after the kept ones), a guess outside the vocabulary (weighs 0: always rejected, the
+    draw removes nothing), a guess holding all the kept weight (always kept), a row where
+    only one token has weight, many rows in one call: identical to the C oracle."""
+    rng = np.random.default_rng(42)
+    vocab = 3000
+    rows, guesses, temps, tops = [], [], [], []
+    for s in range(40):
+        vals = np.round(rng.standard_normal((4, vocab)) * 2).astype(np.float32)  # few values: many ties
+        bits = oracle_accept.bf16_bits(vals)
+        f = oracle_accept.bf16_to_f32(bits)
+        g = []
+        for i in range(3):
+            top = np.flatnonzero(f[i] == f[i].max())
+            choice = s % 4
+            if choice == 0:
+                g.append(int(top[-1]))            # the last of the largest ties
+            elif choice == 1:
+                g.append(int(rng.integers(0, vocab)))
+            elif choice == 2:
+                g.append(vocab + 5 if i == 1 else int(top[0]))  # outside the vocabulary
+            else:
+                g.append(int(top[0]))
+        rows.append(bits)
+        guesses.append(g)
+        temps.append(float(rng.choice([0.5, 1.0, 2.0])))
+        tops.append(float(rng.choice([1.0, 0.3, 0.6, 0.9])))
+    one = np.full((2, vocab), -300.0, dtype=np.float32)
+    one[:, 17] = 4.0  # only token 17 has weight: a guess of 17 is always kept, others draw 17
+    rows += [oracle_accept.bf16_bits(one)] * 2
+    guesses += [[17], [3]]
+    temps += [1.0, 1.0]
+    tops += [0.5, 1.0]
+    out = _v3_batch(device, rows, guesses, temps, tops)
+    assert out[-2] == [17, 17] and out[-1] == [17]
 
 
 @pytest.mark.parametrize("form", ["draft_logits", "draft_probs"])
