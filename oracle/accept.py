@@ -231,17 +231,19 @@ def v3_row(row_bits: np.ndarray, temperature: float, top_p: float) -> tuple[np.n
     vocab = row.shape[0]
     kept = np.zeros(vocab, dtype=np.uint8)
     z, tau, m = ctypes.c_uint64(0), ctypes.c_uint32(0), ctypes.c_uint32(0)
+    scratch = _v3_scratch()  # held by name: the C call writes into it
     k = lib().oracle_v3_row(row.ctypes.data, vocab, ctypes.c_float(temperature), ctypes.c_float(top_p),
                             kept.ctypes.data, ctypes.byref(z), ctypes.byref(tau), ctypes.byref(m),
-                            _v3_scratch().ctypes.data)
+                            scratch.ctypes.data)
     return kept.astype(bool), int(k), int(z.value), int(tau.value), int(m.value)
 
 
 def v3_weight(row_bits: np.ndarray, temperature: float, key: int) -> int:
     """E(key) of a row: the integer weight of a token whose bf16 order key is ``key``."""
     row = np.ascontiguousarray(row_bits, dtype=np.uint16)
+    scratch = _v3_scratch()  # held by name: the C call writes into it
     return int(lib().oracle_v3_weight(row.ctypes.data, row.shape[0], ctypes.c_float(temperature), key,
-                                      _v3_scratch().ctypes.data))
+                                      scratch.ctypes.data))
 
 
 def key16(bits: np.ndarray) -> np.ndarray:

@@ -447,6 +447,7 @@ float oracle_exp3(float x) {
 
 typedef struct {
   uint32_t cnt[65536];
+  int vocab;
   uint32_t kmax;
   float invT, mx;
   uint64_t z, k_total, thr;
@@ -461,6 +462,7 @@ static uint32_t v3_weight(const v3_row* d, uint32_t k) {
 
 static void v3_setup(v3_row* d, const uint16_t* row, int vocab, float temperature, float top_p) {
   memset(d->cnt, 0, sizeof(d->cnt));
+  d->vocab = vocab;
   d->kmax = 0;
   for (int j = 0; j < vocab; ++j) {
     const uint32_t k = key_of_bf16(row[j]);
@@ -500,6 +502,7 @@ static void v3_setup(v3_row* d, const uint16_t* row, int vocab, float temperatur
 
 /* kept (1) or not (0) for token j of the row */
 static int v3_kept(const v3_row* d, const uint16_t* row, int j) {
+  if (j < 0 || j >= d->vocab) return 0; /* a guess outside the vocabulary weighs 0 */
   const uint32_t k = key_of_bf16(row[j]);
   if (!d->topp || k > d->tau) return 1;
   if (k < d->tau) return 0;
@@ -516,6 +519,7 @@ static uint64_t v3_scale(uint32_t u, uint64_t r) {
 static int v3_draw(const v3_row* d, const uint16_t* row, int vocab, int x, uint32_t u) {
   uint64_t wx = 0;
   if (x >= 0 && v3_kept(d, row, x)) wx = v3_weight(d, key_of_bf16(row[x]));
+  if (x >= vocab) x = -1;
   uint64_t r = d->k_total - wx;
   if (r == 0) { /* x held all the kept weight: draw without the exclusion */
     x = -1;
@@ -568,7 +572,7 @@ int oracle_accept_sampled_v3(const uint16_t* logits, int64_t ld, int vocab, cons
       return n_out + 1;
     }
     const int guess = drafts[i];
-    const uint64_t w = v3_kept(d, row, guess) ? v3_weight(d, key_of_bf16(row[guess])) : 0;
+    const uint64_t w = v3_kept(d, row, guess) ? v3_weight(d, key_of_bf16(row[guess])) : 0; /* 0 when outside */
     const uint32_t ui = (uint32_t)(oracle_uniform(seed, step, i) * 16777216.0f);
     const int accept = w >= d->k_total || (w > 0 && (unsigned __int128)ui * d->k_total < (unsigned __int128)w << 24);
     if (accept) {
