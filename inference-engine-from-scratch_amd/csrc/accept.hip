@@ -499,6 +499,7 @@ struct RowLds {
   uint32_t wrap_key[kMaxWraps];  // bit 31: the high half's running value (count of key +
   int n_wrap;                    //   low carries) crossed 65536; else the low half did
   uint32_t wrap_key_spare[kRowWaves];  // occupied segments per wave
+  uint32_t wave_cnt[kRowWaves];        // tokens counted per wave's segments
   uint16_t seg_list[kRowThreads];      // occupied segments in order
   int n_seg;
   uint64_t k_total, above, want;
@@ -605,10 +606,11 @@ __global__ __launch_bounds__(kRowThreads) void accept_rows_kernel(AcceptParams p
   const bool topp = top_p < 1.0f;
   const int guess = i < g ? p.drafts[(int64_t)b * p.max_drafts + i] : -1;
 
-  // ---- histogram of the row's keys
-  for (int w = tid; w < 32768 / 4; w += kRowThreads) ((uint4*)L.hist)[w] = uint4{0u, 0u, 0u, 0u};
-  if (tid == 0) L.n_wrap = 0;
-  __syncthreads();
+  // ---- histogram of the row's keys.  First with adds that return nothing: a 16-bit half
+  // that overflows goes unnoticed there, but then the halves no longer sum to V (a wrap
+  // takes 65535 or 65536 off the sum), which the segment pass checks; only such a row is
+  // counted again with adds that return the old word and record every wrap.
+  auto add_key = [&](uint32_t k) { atomicAdd(&L.hist[k >> 1], 1u << ((k & 1) * 16)); };
   auto count_key = [&](uint32_t k) {
     const uint32_t sh = (k & 1) * 16;
     const uint32_t old = atomicAdd(&L.hist[k >> 1], 1u << sh);
@@ -622,41 +624,60 @@ __global__ __launch_bounds__(kRowThreads) void accept_rows_kernel(AcceptParams p
       if (high_cross && slot + (int)low_wrap < kMaxWraps) L.wrap_key[slot + (int)low_wrap] = (k | 1u) | 0x80000000u;
     }
   };
-  if ((((uintptr_t)row) & 15) == 0) {
-    // 16-byte loads, four per thread requested before their keys are counted
-    const int nvec = V / 8;
-    const uint4* rv = (const uint4*)row;
-    for (int v0 = tid; v0 < nvec; v0 += 4 * kRowThreads) {
-      uint4 q[4];
+  auto histogram = [&](bool tracked) {
+    auto add = [&](uint32_t k) {
+      if (tracked)
+        count_key(k);
+      else
+        add_key(k);
+    };
+    if ((((uintptr_t)row) & 15) == 0) {
+      // 16-byte loads in batches of kHistLoads per thread, the next batch requested before
+      // the current one is counted
+      constexpr int kHistLoads = 4;
+      const int nvec = V / 8;
+      const uint4* rv = (const uint4*)row;
+      uint4 qa[kHistLoads], qb[kHistLoads];
+      auto load = [&](uint4 (&q)[kHistLoads], int v0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int v = v0 + u * kRowThreads;
-        q[u] = v < nvec ? rv[v] : uint4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (v0 + u * kRowThreads >= nvec) break;
-        const uint32_t w4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          count_key(key16((uint16_t)(w4[h] & 0xFFFFu)));
-          count_key(key16((uint16_t)(w4[h] >> 16)));
+        for (int u = 0; u < kHistLoads; ++u) {
+          const int v = v0 + u * kRowThreads;
+          q[u] = v < nvec ? rv[v] : uint4{0u, 0u, 0u, 0u};
         }
+      };
+      auto count = [&](const uint4 (&q)[kHistLoads], int v0) {
+#pragma unroll
+        for (int u = 0; u < kHistLoads; ++u) {
+          if (v0 + u * kRowThreads >= nvec) break;
+          const uint32_t w4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            add(key16((uint16_t)(w4[h] & 0xFFFFu)));
+            add(key16((uint16_t)(w4[h] >> 16)));
+          }
+        }
+      };
+      constexpr int kBatch = kHistLoads * kRowThreads;
+      load(qa, tid);
+      for (int v0 = tid; v0 < nvec; v0 += 2 * kBatch) {
+        load(qb, v0 + kBatch);
+        count(qa, v0);
+        load(qa, v0 + 2 * kBatch);
+        count(qb, v0 + kBatch);
       }
+      for (int j = nvec * 8 + tid; j < V; j += kRowThreads) add(key16(row[j]));
+    } else {
+      for (int j = tid; j < V; j += kRowThreads) add(key16(row[j]));
     }
-    for (int j = nvec * 8 + tid; j < V; j += kRowThreads) count_key(key16(row[j]));
-  } else {
-    for (int j = tid; j < V; j += kRowThreads) count_key(key16(row[j]));
-  }
-  __syncthreads();
+  };
 
   // ---- segment tid (keys 64 tid .. 64 tid + 63): its 32 histogram words at once, its
-  // largest key and whether any key is occupied (a count that wrapped to 0 in its 16-bit
-  // half is found through row_count when any wrap was recorded)
+  // largest key, whether any key is occupied, and the sum of its counts (a count that
+  // wrapped to 0 in its 16-bit half is found through row_count once wraps are recorded)
   const uint32_t k0 = (uint32_t)tid * kKeysPerThread;
   bool occupied = false;
   uint32_t top = 0;  // largest occupied key + 1
-  {
+  auto segment_pass = [&](bool tracked) {
     const uint4* hw = (const uint4*)(L.hist + tid * (kKeysPerThread / 2));
     uint32_t w[kKeysPerThread / 2];
 #pragma unroll
@@ -667,17 +688,36 @@ __global__ __launch_bounds__(kRowThreads) void accept_rows_kernel(AcceptParams p
       w[4 * q + 2] = v.z;
       w[4 * q + 3] = v.w;
     }
-    if (L.n_wrap == 0) {
+    top = 0;
+    uint32_t sum = 0;
+    if (!tracked || L.n_wrap == 0) {
 #pragma unroll
       for (int j = 0; j < kKeysPerThread / 2; ++j) {
         if (w[j] & 0xFFFFu) top = k0 + 2 * j + 1;
         if (w[j] >> 16) top = k0 + 2 * j + 2;
+        sum += (w[j] & 0xFFFFu) + (w[j] >> 16);
       }
     } else {
       for (int j = 0; j < kKeysPerThread; ++j)
         if (row_count(L, k0 + j)) top = k0 + j + 1;
     }
     occupied = top != 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    if (lane == 0) L.wave_cnt[wave] = sum;
+  };
+  for (bool tracked = false;; tracked = true) {
+    for (int w = tid; w < 32768 / 4; w += kRowThreads) ((uint4*)L.hist)[w] = uint4{0u, 0u, 0u, 0u};
+    if (tid == 0) L.n_wrap = 0;
+    __syncthreads();
+    histogram(tracked);
+    __syncthreads();
+    segment_pass(tracked);
+    __syncthreads();
+    uint32_t counted = 0;
+    for (int w = 0; w < kRowWaves; ++w) counted += L.wave_cnt[w];
+    if (tracked || counted == (uint32_t)V) break;
+    __syncthreads();  // a 16-bit count overflowed: count again, recording wraps
   }
   {
     uint32_t m = top;
@@ -838,46 +878,74 @@ __global__ __launch_bounds__(kRowThreads) void accept_rows_kernel(AcceptParams p
   }
   __syncthreads();
   // ---- the want-th occurrence of key kappa in index order, x skipped.  Wave w counts a
-  // contiguous stretch of the row, 8 tokens per lane per 16-byte load (the next load
-  // requested before the current one is used); the waves' counts are summed in order and
-  // the wave holding the token finds its lane by a scan of the lanes' counts.
+  // contiguous stretch of the row in chunks of kOccLoads loads per lane (8 tokens per lane
+  // per 16-byte load, a chunk's loads requested together), keeping each load's hit bits;
+  // the waves' counts are summed in order, and the wave holding the token finds it from
+  // the bits (a stretch of more than one chunk loads the chunks again).
   const uint32_t kappa = L.kappa;
   const uint64_t want = L.want;
   // 16-byte loads need an aligned row whose length is a multiple of 8 (no load crosses V)
   const bool vec = (((uintptr_t)row) & 15) == 0 && (V & 7) == 0;
-  const int step_t = vec ? 8 * kWave : kWave;  // tokens per wave iteration
+  const int step_t = vec ? 8 * kWave : kWave;  // tokens per wave per load
   const int span = ((V + kRowWaves - 1) / kRowWaves + step_t - 1) / step_t * step_t;
   const int w_lo = wave * span, w_hi = min(w_lo + span, V);
-  // hits among this lane's tokens j0 + 8 lane .. +8 (vec) or j0 + lane
+  // The bf16 bit patterns of key kappa (two for the key of -0 and +0), compared two tokens
+  // per 32-bit word: half_zero marks each 16-bit half of v that is 0 with its top bit.
+  const uint32_t pat = bf16_of_key16(kappa);  // +0 for the key of -0 and +0
+  const bool zero_key = kappa == 0x8000u;
+  const uint32_t p1 = pat * 0x10001u, p2 = 0x80008000u;
+  auto half_zero = [](uint32_t v) -> uint32_t { return ~(((v & 0x7FFF7FFFu) + 0x7FFF7FFFu) | v) & 0x80008000u; };
+  // hits among this lane's tokens j0 + 8 lane .. +8 (vec; bit h for token h) or j0 + lane
   auto lane_hits = [&](int j0, const uint4& q) -> uint32_t {
-    uint32_t bits = 0;
     if (vec) {
+      const int j = j0 + 8 * lane;
+      if (j >= w_hi) return 0u;
       const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+      uint32_t m = 0;  // token 2c in bit 2c, token 2c + 1 in bit 16 + 2c
 #pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const int j = j0 + 8 * lane + h;
-        const uint16_t tok = (uint16_t)((h & 1) ? (w4[h >> 1] >> 16) : (w4[h >> 1] & 0xFFFFu));
-        bits |= (uint32_t)(j < w_hi && j != x && key16(tok) == kappa) << h;
+      for (int c = 0; c < 4; ++c) {
+        uint32_t z = half_zero(w4[c] ^ p1);
+        if (zero_key) z |= half_zero(w4[c] ^ p2);
+        m |= z >> (15 - 2 * c);
       }
-    } else {
-      const int j = j0 + lane;
-      bits = j < w_hi && j != x && key16(row[j]) == kappa;
+      uint32_t bits = (m | (m >> 15)) & 0xFFu;
+      if ((uint32_t)(x - j) < 8u) bits &= ~(1u << (x - j));
+      return bits;
     }
-    return bits;
+    const int j = j0 + lane;
+    return (uint32_t)(j < w_hi && j != x && key16(row[j]) == kappa);
   };
-  auto load_at = [&](int j0) -> uint4 {
-    const int j = j0 + 8 * lane;
-    return (vec && j < w_hi) ? *(const uint4*)(row + j) : uint4{0u, 0u, 0u, 0u};
+  constexpr int kOccLoads = 20;
+  constexpr int kOccHalf = kOccLoads / 2;
+  const int chunk_t = kOccLoads * step_t;  // tokens per wave per chunk
+  const int n_chunks = (w_hi - w_lo + chunk_t - 1) / chunk_t;
+  uint32_t hb[kOccLoads / 4];  // load u's hit bits in byte u % 4 of hb[u / 4]
+  // chunk c's hit bits into hb, two half-chunks of loads in flight; returns the lane's hits
+  auto chunk_bits = [&](int c) -> uint32_t {
+    uint32_t n = 0;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      uint4 q[kOccHalf];
+#pragma unroll
+      for (int u = 0; u < kOccHalf; ++u) {
+        const int j0 = w_lo + c * chunk_t + (hh * kOccHalf + u) * step_t;
+        const int j = j0 + (vec ? 8 * lane : lane);
+        q[u] = (vec && j < w_hi) ? *(const uint4*)(row + j) : uint4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < kOccHalf; ++u) {
+        const int uu = hh * kOccHalf + u;
+        const int j0 = w_lo + c * chunk_t + uu * step_t;
+        const uint32_t bits = j0 < w_hi ? lane_hits(j0, q[u]) : 0u;
+        if (uu % 4 == 0) hb[uu / 4] = 0;
+        hb[uu / 4] |= bits << (8 * (uu % 4));
+        n += __builtin_popcount(bits);
+      }
+    }
+    return n;
   };
   uint32_t occ = 0;
-  for (int j0 = w_lo; j0 < w_hi; j0 += 4 * step_t) {  // four loads per lane in flight
-    uint4 q[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) q[u] = load_at(j0 + u * step_t);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (j0 + u * step_t < w_hi) occ += __builtin_popcount(lane_hits(j0 + u * step_t, q[u]));
-  }
+  for (int c = 0; c < n_chunks; ++c) occ += chunk_bits(c);
   uint32_t wocc = occ;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) wocc += __shfl_xor(wocc, o);
@@ -887,30 +955,37 @@ __global__ __launch_bounds__(kRowThreads) void accept_rows_kernel(AcceptParams p
   for (int w = 0; w < wave; ++w) before += L.wave_part[w];
   if (before <= want && want < before + wocc) {  // uniform within the wave
     uint64_t seen = before;
-    uint4 q = load_at(w_lo);
-    for (int j0 = w_lo; j0 < w_hi; j0 += step_t) {
-      const uint4 nq = j0 + step_t < w_hi ? load_at(j0 + step_t) : q;
-      const uint32_t bits = lane_hits(j0, q);
-      q = nq;
-      const uint32_t n = __builtin_popcount(bits);
-      uint32_t incl = n;  // inclusive scan of the lanes' counts
+    for (int c = 0; c < n_chunks; ++c) {
+      if (n_chunks > 1) chunk_bits(c);  // one chunk: its bits are still in hb
+      bool found = false;
 #pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t t2 = __shfl_up(incl, o);
-        if (lane >= o) incl += t2;
-      }
-      const uint32_t total = __shfl(incl, kWave - 1);
-      if (want < seen + total) {  // uniform
-        const uint64_t start_l = seen + incl - n;
-        if (start_l <= want && want < start_l + n) {
-          uint32_t r = (uint32_t)(want - start_l), bb = bits;
-          for (uint32_t c = 0; c < r; ++c) bb &= bb - 1;  // drop the r lowest hits
-          const int h = __builtin_ctz(bb);
-          p.out_tokens[(int64_t)b * R + i] = vec ? j0 + 8 * lane + h : j0 + lane;
+      for (int wi = 0; wi < kOccLoads / 4 && !found; ++wi)
+#pragma unroll 1
+      for (int uu = 4 * wi; uu < 4 * wi + 4; ++uu) {
+        const uint32_t bits = (hb[wi] >> (8 * (uu % 4))) & 0xFFu;
+        const uint32_t n = __builtin_popcount(bits);
+        uint32_t incl = n;  // inclusive scan of the lanes' counts
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t t2 = __shfl_up(incl, o);
+          if (lane >= o) incl += t2;
         }
-        break;
+        const uint32_t total = __shfl(incl, kWave - 1);
+        if (want < seen + total) {  // uniform
+          const uint64_t start_l = seen + incl - n;
+          if (start_l <= want && want < start_l + n) {
+            uint32_t r = (uint32_t)(want - start_l), bb = bits;
+            for (uint32_t q = 0; q < r; ++q) bb &= bb - 1;  // drop the r lowest hits
+            const int h = __builtin_ctz(bb);
+            const int j0 = w_lo + c * chunk_t + uu * step_t;
+            p.out_tokens[(int64_t)b * R + i] = vec ? j0 + 8 * lane + h : j0 + lane;
+          }
+          found = true;
+          break;
+        }
+        seen += total;
       }
-      seen += total;
+      if (found) break;
     }
   }
 }
