@@ -157,7 +157,7 @@ def run_verify(args, torch, temperature: float | None = None, steps: int | None 
         eng.runner.step()
     # no step in flight when the clock starts: the runner may have launched one ahead
     eng.runner.drain()
-    if eng.runner.pending:
+    while eng.runner.pending:
         eng.runner.step()
     ctx_per_step, lengths_per_step = [], []
     # HIP events around each step's device work (graph replay, or the eager launches) on

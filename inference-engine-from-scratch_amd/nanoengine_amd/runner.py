@@ -85,6 +85,19 @@ class StepResult(NamedTuple):
     num_kept: int
 
 
+class _Launched(NamedTuple):
+    """A verify step launched and not yet completed on the host: its slots, the read-back
+    buffer its outputs go to (rb), the one holding its guess counts (gb), and the event
+    recorded after its read-back copy."""
+
+    active: list[int]
+    act: np.ndarray
+    traced_drafts: dict | None
+    rb: int
+    gb: int
+    event: torch.cuda.Event
+
+
 class VerifyRunner:
     def __init__(
         self,
@@ -167,11 +180,13 @@ class VerifyRunner:
         self.h_num_tokens = torch.zeros(max_seqs, dtype=torch.int32, **pin)
         self.h_steps = torch.zeros(max_seqs, dtype=torch.int64, **pin)
         self.h_drafts = torch.zeros(max_seqs, self.k, dtype=torch.int32, **pin)
-        # two host copies of step_out: a step reads back into one while its guess counts
-        # (read back by the previous step, n-gram drafting) sit in the other
-        self.h_step_out = [torch.zeros(max_seqs * (self.R + 2), dtype=torch.int32, **pin) for _ in range(2)]
-        self._read_back = 0
-        self._bind_read_back()
+        # three host copies of step_out, used in turn: a step reads back into one while
+        # its guess counts (read back by the step before it, n-gram drafting) sit in the
+        # previous one, and with two steps in flight a third receives the later one's
+        self.h_step_out = [torch.zeros(max_seqs * (self.R + 2), dtype=torch.int32, **pin) for _ in range(3)]
+        self._read_back_events = [torch.cuda.Event() for _ in range(3)]
+        self._last_rb = 0  # read-back buffer of the most recently launched step
+        self._bind_read_back(1, 0)
         # numpy views of the pinned buffers: the per-step host work indexes them per
         # sequence, which costs ~1 us through torch and ~0.1 us through numpy
         self.np_tables = self.h_tables.numpy()
@@ -180,12 +195,13 @@ class VerifyRunner:
         # whether the device drafts / num_drafts already hold this step's n-gram guesses
         # (proposed at the end of the previous step, no sequence admitted since)
         self._drafts_ready = False
-        # a step launched ahead by the previous step() call (not yet waited for), and the
-        # results of one finished early because the batch changed
-        self._ahead = None
-        self._pending: dict[int, StepResult] | None = None
+        # steps launched and not yet waited for (oldest first, at most two), and the
+        # results of steps finished early because the batch changed, in step order
+        self._inflight: deque[_Launched] = deque()
+        self._pending: deque[dict[int, StepResult]] = deque()
         self.run_ahead = True  # False: every step launches and finishes in its own call
-        self.ahead_launches = 0
+        self.ahead_launches = 0  # steps launched before the previous step's bookkeeping
+        self.deep_launches = 0  # of those, launched while the previous step still ran
         # a plain paged allocator hands out blocks from the head of a FIFO free list, so a
         # step's new table entries are known before the allocator records them
         self._fifo_blocks = type(allocator) is PagedSlotAllocator
@@ -220,16 +236,17 @@ class VerifyRunner:
         n, r = self.max_seqs, self.R
         return buf[: n * r].view(n, r), buf[n * r : n * (r + 1)], buf[n * (r + 1) :]
 
-    def _bind_read_back(self) -> None:
-        """Host views: this step reads back into h_step_out[_read_back]; its guess counts
-        are the num_drafts part of the other buffer."""
+    def _bind_read_back(self, rb: int, gb: int) -> None:
+        """Host views of a step: it reads back into h_step_out[rb]; its guess counts are
+        the num_drafts part of h_step_out[gb] (read back by the step before it, or staged
+        there by the host)."""
         if not hasattr(self, "_read_back_views"):
             views = [self._step_out_views(buf) for buf in self.h_step_out]
             self._read_back_views = [(v, tuple(t.numpy() for t in v)) for v in views]
         (self.h_out, self.h_num_out, self.h_num_drafts_next), (self.np_out, self.np_num_out,
                                                                 self.np_num_drafts_next) = \
-            self._read_back_views[self._read_back]
-        other = self._read_back_views[1 - self._read_back]
+            self._read_back_views[rb]
+        other = self._read_back_views[gb]
         self.h_num_drafts, self.np_num_drafts = other[0][2], other[1][2]
 
     # ------------------------------------------------------------------ slots
@@ -247,7 +264,7 @@ class VerifyRunner:
         """Empty slots.  A slot whose sequence finished in a step whose results wait for
         the next step() call (``pending``) is not free until that call has returned them,
         so a result is never reported under a slot that a new request already holds."""
-        waiting = self._pending or ()
+        waiting = set().union(*self._pending) if self._pending else ()
         return [i for i, s in enumerate(self.slots) if s is None and i not in waiting]
 
     @property
@@ -485,36 +502,46 @@ class VerifyRunner:
         this one, n-gram guesses, the plain paged allocator, a captured graph, no trace),
         the next step is launched as soon as this one's outputs are read back, before its
         tokens are appended to the sequences: the device runs it while the host does that
-        bookkeeping, and the next call waits for it instead of launching one.  A batch
-        change (add, release) first finishes such a step and keeps its results for the
-        next call."""
-        if self._pending is not None:
-            results, self._pending = self._pending, None
-            return results
-        launched, self._ahead = self._ahead, None
-        if launched is None:
+        bookkeeping, and the next call waits for it instead of launching one.  When no slot
+        can finish in a launched step whatever it emits (no slot honours stop tokens and
+        none can reach its length limit), the step after it is launched right away too,
+        with blocks reserved for the most it can need, so the device never waits for the
+        host between the two.  A batch change (add, release) first finishes the steps in
+        flight and keeps their results for the next calls."""
+        if self._pending:
+            return self._pending.popleft()
+        if not self._inflight:
             launched = self._launch()
             if launched is None:
                 return {}
-        torch.cuda.current_stream(self.device).synchronize()
+            self._inflight.append(launched)
+            self._maybe_launch_deep()
+        launched = self._inflight.popleft()
+        launched.event.synchronize()
         return self._complete(launched, allow_ahead=True)
 
     @property
     def pending(self) -> bool:
         """Whether a finished step's results wait for the next step() call."""
-        return self._pending is not None
+        return bool(self._pending)
 
     def drain(self) -> None:
-        """Finish a step launched ahead (before the batch changes, or before the device
-        is used for something else); its results are returned by the next step() call."""
-        if self._ahead is not None:
-            launched, self._ahead = self._ahead, None
-            torch.cuda.current_stream(self.device).synchronize()
-            self._pending = self._complete(launched, allow_ahead=False) or None
+        """Finish the steps launched ahead (before the batch changes, or before the device
+        is used for something else); their results are returned by the next step() calls."""
+        while self._inflight:
+            launched = self._inflight.popleft()
+            launched.event.synchronize()
+            results = self._complete(launched, allow_ahead=False)
+            if results:
+                self._pending.append(results)
 
-    def _launch(self):
+    def _launch(self, bound: tuple[np.ndarray, np.ndarray] | None = None) -> _Launched | None:
         """Guesses, block growth and the device step of one verify step, up to its
-        outputs' read-back copy (not waited for); None when no slot is active."""
+        outputs' read-back copy (not waited for); None when no slot is active.
+
+        ``bound`` (a step launched while the one before it still runs): the lengths and
+        guess counts its blocks must cover at most, since its own are not known yet;
+        its guesses are the ones the running step proposes on the device."""
         if self._active is None:
             self._active = [i for i, s in enumerate(self.slots) if s is not None]
         active = self._active
@@ -523,14 +550,20 @@ class VerifyRunner:
         slots = self.slots
         act = self.np_active.copy()
         ngram = self.proposer is None
-        if not (ngram and self._drafts_ready) or self.trace is not None:
+        gb, rb = self._last_rb, (self._last_rb + 1) % len(self.h_step_out)
+        self._bind_read_back(rb, gb)
+        if bound is not None:
+            pass
+        elif not (ngram and self._drafts_ready) or self.trace is not None:
             # num_guesses for every slot at once (speculative_generator.py:71-72); n-gram
             # guesses proposed at the end of the previous step come with the device's counts
             counts = np.minimum(self.np_max_new - self.np_gen - 1, self.k)
             np.maximum(counts, 0, out=counts)
             counts *= act
             self.np_num_tokens[:] = counts
-        if ngram:
+        if bound is not None:
+            pass
+        elif ngram:
             if not self._drafts_ready:
                 self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
                 self.steps.copy_(self.h_steps, non_blocking=True)
@@ -555,6 +588,7 @@ class VerifyRunner:
             self.drafts.copy_(self.h_drafts, non_blocking=True)
             self.num_drafts.copy_(self.h_num_drafts, non_blocking=True)
         np_num_drafts, allocator, bs = self.np_num_drafts, self.allocator, self.block_size
+        lengths, drafts = (self.np_len, np_num_drafts) if bound is None else bound
         if self._guard_shared:
             # rows write positions L-1 .. L-1+g; every block below the allocator's
             # bound may be read by other requests and must never be written
@@ -563,7 +597,7 @@ class VerifyRunner:
                 if seq.num_tokens - 1 < allocator.first_writable_position(seq):
                     raise RuntimeError(f"verify step of {seq.request_id} would write into a shared block")
         # slots whose length + guesses outgrow their blocks (paged_allocator.py:50-55)
-        grow, counts, targets, total = host_step.plan_growth(self.np_len, np_num_drafts, self.np_owned, act, bs)
+        grow, counts, targets, total = host_step.plan_growth(lengths, drafts, self.np_owned, act, bs)
         deferred = None
         if grow:
             np_tables, np_owned = self.np_tables, self.np_owned
@@ -585,10 +619,13 @@ class VerifyRunner:
             torch.cuda.current_stream(self.device).synchronize()
             traced_drafts = {s: self.drafts[s, : int(np_num_drafts[s])].tolist() for s in active}
         self._run_device_step()
-        self.h_step_out[self._read_back].copy_(self.step_out, non_blocking=True)
+        self.h_step_out[rb].copy_(self.step_out, non_blocking=True)
+        event = self._read_back_events[rb]
+        event.record()
+        self._last_rb = rb
         if deferred is not None:
             allocator.take_free([slots[s] for s in deferred[0]], deferred[1], deferred[2])
-        return active, act, traced_drafts
+        return _Launched(active, act, traced_drafts, rb, gb, event)
 
     def _may_run_ahead(self, act: np.ndarray) -> bool:
         """Whether the next step can be launched before this one's bookkeeping: nothing
@@ -613,9 +650,42 @@ class VerifyRunner:
                                            self.block_size)
         return blocks <= self.allocator.num_free_blocks
 
-    def _complete(self, launched, allow_ahead: bool) -> dict[int, StepResult]:
+    def _maybe_launch_deep(self) -> None:
+        """With one step in flight whose outcome cannot change the batch (no active slot
+        honours stop tokens and none can reach its length limit, whatever it emits),
+        launch the step after it now, its blocks reserved for the most the running step
+        can emit plus the most guesses the next can make; the device proposes those
+        guesses at the end of the running step.  The host mirrors are at the running
+        step's start."""
+        if (len(self._inflight) != 1 or not self.run_ahead or self.proposer is not None or self.trace is not None
+                or not self._fifo_blocks or self.graph is None or self.graph_sampled != self.any_sampled):
+            return
+        running = self._inflight[0]
+        act = running.act
+        if (self.np_honours_stop & act).any() or not np.array_equal(act, self.np_active):
+            return
+        guesses = self._read_back_views[running.gb][1][2]  # the running step's guess counts
+        most = (guesses + 1) * act  # the most tokens it can emit per slot
+        if ((self.np_gen + most >= self.np_max_new) & act).any():
+            return
+        lengths = self.np_len + most
+        if not self.graph_allowed(lengths):
+            return
+        # its guesses: at most k, and never past the sequence's last position (prompt +
+        # max_new - 1 tokens hold keys), as the exact count min(k, max_new - gen - 1) is
+        last = self.np_len - self.np_gen + self.np_max_new - 1
+        drafts = (np.minimum(self.k, last - lengths) * act).astype(np.int32)
+        *_, blocks = host_step.plan_growth(lengths, drafts, self.np_owned, act, self.block_size)
+        if blocks > self.allocator.num_free_blocks:
+            return
+        self._inflight.append(self._launch(bound=(lengths, drafts)))
+        self.ahead_launches += 1
+        self.deep_launches += 1
+
+    def _complete(self, launched: _Launched, allow_ahead: bool) -> dict[int, StepResult]:
         """The host side of a step whose outputs have been read back."""
-        active, act, traced_drafts = launched
+        active, act, traced_drafts = launched.active, launched.act, launched.traced_drafts
+        self._bind_read_back(launched.rb, launched.gb)
         slots = self.slots
         np_num_drafts = self.np_num_drafts
         ngram = self.proposer is None
@@ -630,9 +700,9 @@ class VerifyRunner:
                 }
                 for s in active
             })
-        if allow_ahead and self._may_run_ahead(act):
+        if allow_ahead and not self._inflight and self._may_run_ahead(act):
             # the mirrors advance now (finish_step below advances copies of the old ones);
-            # this step's outputs stay in their read-back buffer, which the next step does
+            # this step's outputs stay in their read-back buffer, which the next steps do
             # not write; its guess counts are in the buffer the next step reads back into
             out, num_out = self.np_out, self.np_num_out
             guesses = np_num_drafts.copy()
@@ -641,11 +711,10 @@ class VerifyRunner:
             self.np_len += emitted
             self.np_gen += emitted
             self.np_steps += act
-            self._read_back ^= 1
-            self._bind_read_back()
             self._drafts_ready = True
-            self._ahead = self._launch()
+            self._inflight.append(self._launch())
             self.ahead_launches += 1
+            self._maybe_launch_deep()
             results, finishing = host_step.finish_step(
                 active, slots, out, num_out, guesses, act, lengths, generated, steps, self.np_max_new,
                 self.np_honours_stop, self._stop_ids, StepResult, None,
@@ -654,7 +723,8 @@ class VerifyRunner:
             return results
         # the mirrors advance by the emitted counts and every slot that cannot finish this
         # step appends its tokens; slots at their length limit or with a stop token
-        # emitted (when they honour stops) finish one token at a time below
+        # emitted (when they honour stops) finish one token at a time below (a step
+        # launched behind this one was launched only if no slot can finish in this one)
         finish = host_step.finish_step if len(self._stop_ids) <= 64 else host_step.finish_step_py
         results, finishing = finish(
             active, slots, self.np_out, self.np_num_out, np_num_drafts, act, self.np_len, self.np_gen,
@@ -667,9 +737,9 @@ class VerifyRunner:
             cached = len(seq.token_ids) + kept  # L-1 .. L-1+kept now hold the kept tokens
             results[s] = self._emit(s, seq, tokens, int(np_num_drafts[s]), kept, cached)
         if ngram:  # the counts read back with this step's tokens are the next step's
-            self._read_back ^= 1
-            self._bind_read_back()
             self._drafts_ready = True
+        if allow_ahead:
+            self._maybe_launch_deep()
         return results
 
     def _emit(self, slot: int, seq: Sequence, tokens: list[int], g: int, kept: int,
@@ -700,17 +770,20 @@ class VerifyRunner:
             seq.num_cached_tokens = min(cached, seq.num_tokens)
             self.allocator.on_tokens_cached(seq)
         if reason is not None:
-            self.release(slot)
+            self._free_slot(slot)
         return StepResult(emitted, reason, g, kept)
 
     def release(self, slot: int) -> None:
         """Free a slot.  A result of the slot still waiting for the next step() call is
         dropped with it (the caller has given the slot up)."""
         self.drain()
-        if self._pending is not None:
-            self._pending.pop(slot, None)
-            if not self._pending:
-                self._pending = None
+        for results in self._pending:
+            results.pop(slot, None)
+        self._pending = deque(r for r in self._pending if r)
+        self._free_slot(slot)
+
+    def _free_slot(self, slot: int) -> None:
+        """Free a slot whose sequence finished or was given up (no step in flight)."""
         seq = self.slots[slot]
         if seq is None:  # empty, or it finished in the drained step
             return

@@ -524,10 +524,10 @@ def test_finished_slot_is_not_reused_before_its_pending_result_is_returned():
                 admit(3)
                 continue
             record(runner.step())
-        return got, [list(q.token_ids) for q in seqs], runner.ahead_launches
+        return got, [list(q.token_ids) for q in seqs], (runner.ahead_launches, runner.deep_launches)
 
-    got, ids, launches = run(True)
-    assert launches > 0
+    got, ids, (launches, deep) = run(True)
+    assert launches > 0 and deep > 0  # steps launched while the one before still ran, too
     assert len(got[0]) == limit0 and all(len(got[i]) == 60 for i in (1, 2, 3))
     for i in range(4):
         assert ids[i][len(prompts[i]):] == got[i]

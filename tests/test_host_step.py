@@ -115,6 +115,63 @@ def test_launch_ahead_check_matches_the_finishing_slots(seed, stops):
     assert ahead == (not finishing and Pool.num_free_blocks >= need)
 
 
+@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("honour", [False, True])
+def test_deep_launch_reserves_for_every_outcome_of_the_running_step(seed, honour):
+    """VerifyRunner._maybe_launch_deep (the step after a running one, launched before the
+    running step's outputs are known) is taken exactly when no active slot honours stop
+    tokens and none can reach its length limit whatever the running step emits (1 .. g + 1
+    tokens); its block bound then covers every such outcome followed by the most guesses
+    the next step can make (min(k, max_new - generated - 1)), and never reaches past the
+    sequence's last position (prompt + max_new - 1 tokens)."""
+    from collections import deque
+
+    from nanoengine_amd.runner import VerifyRunner, _Launched
+
+    st = _state(seed)
+    rng = np.random.default_rng(200 + seed)
+    k = 4
+    act = st["act"]
+    # limits from "cannot finish in the running step" to "finishes for some outcome"
+    st["max_new"] = st["gen"] + st["nd"] + 1 + rng.integers(-1, 12, act.shape[0])
+    if seed % 3 == 0:  # every slot far from its limit
+        st["max_new"] = st["gen"] + st["nd"] + 1 + rng.integers(1, 12, act.shape[0])
+    honours = st["honours"] & honour
+    runner = VerifyRunner.__new__(VerifyRunner)
+    runner.run_ahead, runner.proposer, runner.trace = True, None, None
+    runner._fifo_blocks, runner.use_graph, runner.graph = True, True, object()
+    runner.graph_failed, runner.graph_max_batch, runner.graph_max_context, runner.k = False, None, None, k
+    runner.graph_sampled, runner._sampled = False, False
+    runner.np_active, runner.np_honours_stop = act, honours
+    runner.np_len, runner.np_gen, runner.np_max_new = st["lengths"], st["gen"], st["max_new"]
+    runner.np_owned, runner.block_size = st["owned"], 16
+    runner._read_back_views = [(None, (None, None, st["nd"])), None, None]  # the running step's guess counts
+    runner._inflight = deque([_Launched(np.flatnonzero(act).tolist(), act, None, 1, 0, None)])
+    runner.ahead_launches = runner.deep_launches = 0
+
+    class Pool:
+        num_free_blocks = 10 ** 6
+
+    runner.allocator = Pool()
+    bounds = []
+    runner._launch = lambda bound=None: bounds.append(bound) or "launched"
+    runner._maybe_launch_deep()
+    g, gen, lengths, max_new = st["nd"].astype(np.int64), st["gen"], st["lengths"], st["max_new"]
+    can_finish = ((gen + g + 1 >= max_new) & act).any() or (honours & act).any()
+    assert (len(bounds) == 1) == (not can_finish)
+    if not bounds:
+        return
+    b_len, b_drafts = bounds[0]
+    assert b_len.dtype == np.int64 and b_drafts.dtype == np.int32
+    bound = b_len + b_drafts
+    for s in np.flatnonzero(act):
+        for e in range(1, int(g[s]) + 2):  # the running step emits e tokens
+            nxt = min(k, int(max_new[s] - gen[s] - e - 1))
+            assert int(lengths[s]) + e + max(nxt, 0) <= bound[s]
+        assert bound[s] <= lengths[s] - gen[s] + max_new[s] - 1
+    assert runner.deep_launches == 1 and list(runner._inflight)[-1] == "launched"
+
+
 @pytest.mark.parametrize("fn_name", ["finish_step_py", "finish_step"])
 @pytest.mark.parametrize("case", ["emitted-too-many", "emitted-negative", "inactive-slot", "empty-slot",
                                   "slot-out-of-range"])
