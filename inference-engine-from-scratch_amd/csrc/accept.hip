@@ -12,7 +12,7 @@
 // the argmax of its bf16 logits, first index on ties (torch.argmax order).
 //
 // Sampled (temperature T > 0).  The reference draws with torch.rand /
-// torch.multinomial, which no other implementation reproduces; this build fixes
+// torch.multinomial, which no other implementation reproduces; this library fixes
 // explicit procedures instead, shared bit for bit with the CPU oracle.
 //
 // One-hot guesses (n-gram, and the draft model's own draws): the integer-mass

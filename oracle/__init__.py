@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import, call, link or run anything in
-this package, and only as the checker (or the timed CPU baseline).  The
+this package, and only to check results against (or as the timed CPU baseline).  The
 product path (``inference-engine-from-scratch_amd/``) never imports it.
 
 Each module restates one piece of the reference (citations are relative to the
@@ -23,7 +23,7 @@ numpy, C (``csrc/accept_oracle.c``) or torch on the CPU:
   verify.py     verify_proposal (reference        ne/engine/speculative/verifier.py:21-60,
                 semantics) and the serial          ne/engine/sampling.py:11-62,
                 speculative loop                   ne/engine/speculative/speculative_generator.py
-  accept.py     acceptance under this build's
+  accept.py     acceptance under the library's
                 explicit-uniform contract (greedy
                 in numpy; sampled via the C oracle)
 

@@ -1,4 +1,4 @@
-"""Acceptance under this build's explicit-uniform contract (test infrastructure only).
+"""Acceptance under the library's explicit-uniform contract (test infrastructure only).
 
 Greedy (ne/engine/speculative/verifier.py:27-60 with one-hot p and q): keep guesses
 while they equal the row argmax (first index on ties, numpy/torch order), then

@@ -1,6 +1,6 @@
 """Cached GQA attention over a slot pool, restating ne/models/attention_context.py:42-109.
 
-``paged_attention_reference`` is the kernel-level checker for the HIP paged verify
+``paged_attention_reference`` is the kernel-level reference for the HIP paged verify
 attention: for every sequence it gathers the context through the block table,
 dequantises int8 entries exactly as ``read_from_cache`` does (int8 -> model dtype
 times the stored scale), and runs masked softmax attention in fp32.

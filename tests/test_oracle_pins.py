@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker (CPU only).
+"""Pins the CPU oracle before results are checked against it (CPU only).
 
 Every oracle function is checked against something that does not share its
 formula: the known-answer vectors of the reference's own tests (transcribed in
