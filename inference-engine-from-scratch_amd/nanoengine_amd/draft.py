@@ -78,6 +78,12 @@ class DraftModelProposer:
         self.max_tokens = max_tokens
         self._dec: dict[str, torch.Tensor] | None = None
         self._dec_graph: torch.cuda.CUDAGraph | None = None
+        # the catch-up forward (guess 0) of greedy slots with at most k + 1 uncached tokens:
+        # k + 1 rows per slot, padded, replayed from a HIP graph with its own attention
+        # scratch (the decode graph's is sized for one row per slot)
+        self._cu: dict[str, torch.Tensor] | None = None
+        self._cu_graph: torch.cuda.CUDAGraph | None = None
+        self._cu_ws = kernels.AttentionWorkspace()
         model.ensure_rope(max_tokens)
 
     # ------------------------------------------------------------------ state
@@ -142,7 +148,10 @@ class DraftModelProposer:
             self._sync(s, sequences[s])
             self.target_len[s] = sequences[s].num_tokens
         if self.use_graph and not self.sampled and want and max(want.values()) > 1:
-            for s, token in self._next_tokens(sorted(want)).items():  # catch-up: guess 0
+            first = self._catch_up_graphed(sorted(want))
+            if first is None:
+                first = self._next_tokens(sorted(want))
+            for s, token in first.items():  # catch-up: guess 0
                 self.drafts[s].token_ids.append(token)
                 guesses[s].append(token)
             self._decode_graphed(want, guesses)
@@ -180,6 +189,94 @@ class DraftModelProposer:
         torch.cuda.current_stream(self.device).synchronize()
         self.h_out.copy_(self.out_tokens)
         return {s: int(self.h_out[i, 0]) for i, s in enumerate(done)}
+
+    # --------------------------------------------------------- graphed catch-up
+    def _catch_up_body(self) -> None:
+        """k + 1 rows per slot (q_len 0: a pad slot): forward, the last real row of each
+        slot gathered, its LM-head argmax partials and the argmax through the acceptance
+        kernel."""
+        c = self._cu
+        n, r = self.max_seqs, self.k + 1
+        batch = AttentionBatch(c["positions"], c["slots"], c["q_start"], c["q_len"], c["ctx"], c["tables"], r,
+                               self.max_tokens)
+        hidden = self.model.forward(n * r, c["tokens"], batch, self.pool, workspace=self._cu_ws)
+        torch.index_select(hidden, 0, c["last_rows"], out=c["last"])
+        self.model.compute_logits(c["last"], logits=False, argmax=c["partials"])
+        kernels.accept(self.no_drafts, self.zero_counts, self.last_rows, self.model.config.vocab_size,
+                       argmax_partials=c["partials"], temperature=0.0, out_tokens=c["out"], num_out=c["num_out"])
+
+    def _catch_up_graphed(self, live: list[int]) -> dict[int, int] | None:
+        """Guess 0 of every live slot from one replay of the captured catch-up forward
+        (the same rows, positions and context as the eager one, padded to k + 1 rows per
+        slot); None when a slot has no uncached token or more than k + 1 (a new request's
+        prompt), which the eager forward takes."""
+        n, r, dev = self.max_seqs, self.k + 1, self.device
+        spans = {}
+        for s in live:
+            draft = self.drafts[s]
+            a, e = draft.num_cached_tokens, draft.num_tokens
+            if not 1 <= e - a <= r:
+                return None
+            spans[s] = (a, e)
+        if self._cu is None:
+            i32 = dict(dtype=torch.int32, device=dev)
+            tiles = kernels.lm_head_num_tiles(self.model.config.vocab_size)
+            hidden = self.model.config.hidden_size
+            self._cu = dict(tokens=torch.zeros(n * r, **i32), positions=torch.zeros(n * r, **i32),
+                            slots=torch.zeros(n * r, **i32), q_start=torch.arange(n, **i32) * r,
+                            q_len=torch.zeros(n, **i32), ctx=torch.zeros(n, **i32),
+                            tables=torch.zeros((n, self.max_blocks), **i32),
+                            last_rows=torch.zeros(n, dtype=torch.long, device=dev),
+                            last=torch.zeros((n, hidden), dtype=self.model.normed.dtype, device=dev),
+                            partials=torch.zeros((n, tiles), dtype=torch.int64, device=dev),
+                            out=torch.zeros((n, 2), **i32), num_out=torch.zeros(n, **i32))
+            self._cu_rows = torch.zeros((3, n * r), dtype=torch.int32, pin_memory=True)
+            self._cu_seq = torch.zeros((2, n), dtype=torch.int32, pin_memory=True)
+            self._cu_last = torch.zeros(n, dtype=torch.long, pin_memory=True)
+            self._cu_tables = torch.zeros((n, self.max_blocks), dtype=torch.int32, pin_memory=True)
+        c = self._cu
+        rows, seq, last = self._cu_rows.numpy(), self._cu_seq.numpy(), self._cu_last.numpy()
+        rows[0] = 0  # tokens of pads
+        rows[1] = 0  # positions of pads
+        rows[2] = self.pool.scratch_slot  # pads write the pool's scratch slot
+        seq[:] = 0
+        last[:] = np.arange(n) * r
+        for s, (a, e) in spans.items():
+            draft = self.drafts[s]
+            self._reserve(s, draft, e)
+            pos = np.arange(a, e)
+            at = s * r
+            rows[0, at : at + e - a] = draft.token_ids[a:e]
+            rows[1, at : at + e - a] = pos
+            rows[2, at : at + e - a] = self.allocator.slots_for(draft, pos)
+            seq[0, s] = e - a
+            seq[1, s] = e
+            last[s] = at + e - a - 1
+        self._cu_tables.numpy()[:] = self.tables
+        for i, name in enumerate(("tokens", "positions", "slots")):
+            c[name].copy_(self._cu_rows[i], non_blocking=True)
+        c["q_len"].copy_(self._cu_seq[0], non_blocking=True)
+        c["ctx"].copy_(self._cu_seq[1], non_blocking=True)
+        c["last_rows"].copy_(self._cu_last, non_blocking=True)
+        c["tables"].copy_(self._cu_tables, non_blocking=True)
+        if self._cu_graph is None:
+            self._catch_up_body()  # eager once (sizes the scratch and lazily created buffers)
+            torch.cuda.current_stream(dev).synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._catch_up_body()
+            self.model.bind_graph()
+            self._cu_ws.frozen = True
+            self._cu_graph = graph
+        else:
+            self._cu_graph.replay()
+        self.forwards += 1
+        torch.cuda.current_stream(dev).synchronize()
+        self.h_out.copy_(c["out"])
+        out = self.h_out.numpy()
+        for s, (a, e) in spans.items():
+            self.drafts[s].num_cached_tokens = e
+        return {s: int(out[s, 0]) for s in live}
 
     # ------------------------------------------------------- graphed decode steps
     def _decode_body(self) -> None:

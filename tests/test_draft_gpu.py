@@ -85,6 +85,8 @@ def test_draft_guesses_and_output_match_the_oracle(graphs):
     reqs = [GenerationRequest(f"r{i}", p, params) for i, p in enumerate(ps)]
     events = eng.batched_generator().generate_all(reqs)
     assert eng.runner.proposer.forwards > 0
+    # with graphs, the catch-up forwards after the first proposal replay a captured graph
+    assert (eng.runner.proposer._cu_graph is not None) == graphs
     draft32 = oracle(ODCFG, dstate)
     checked_guesses = 0
     for step in eng.runner.trace:
