@@ -50,8 +50,10 @@ class DraftModelProposer:
         self.block_size = allocator.block_size
         self.max_blocks = math.ceil(max_tokens / self.block_size)
         self.max_seqs = max_seqs
-        # per slot: the draft's own Sequence (its tokens and cached count) and block table
+        # per slot: the draft's own Sequence (its tokens and cached count) and block table;
+        # the target's length at the slot's last sync (the two token lists agree up to it)
         self.drafts: dict[int, Sequence] = {}
+        self.synced: dict[int, int] = {}
         self.tables = np.zeros((max_seqs, self.max_blocks), dtype=np.int32)
         self.owned = np.zeros(max_seqs, dtype=np.int64)
         i32 = dict(dtype=torch.int32, device=device)
@@ -94,13 +96,17 @@ class DraftModelProposer:
         if draft is None:
             draft = Sequence.from_request(sequence.request)
             self.drafts[slot] = draft
-        common = 0
-        for draft_token, target_token in zip(draft.token_ids, sequence.token_ids):
-            if draft_token != target_token:
-                break
+        ids, target = draft.token_ids, sequence.token_ids
+        # the target only appends, so the lists agree up to the last sync's length: only
+        # the tokens since then (the draft's guesses against the target's new ones) compare
+        common = min(self.synced.get(slot, 0), len(ids), len(target))
+        stop = min(len(ids), len(target))
+        while common < stop and ids[common] == target[common]:
             common += 1
-        draft.token_ids = list(sequence.token_ids)
+        del ids[common:]
+        ids.extend(target[common:])
         draft.num_cached_tokens = min(draft.num_cached_tokens, common)
+        self.synced[slot] = len(target)
         return draft
 
     def _reserve(self, slot: int, draft: Sequence, num_tokens: int) -> None:
@@ -117,6 +123,7 @@ class DraftModelProposer:
         draft = self.drafts.pop(slot, None)
         if draft is not None:
             self.allocator.free(draft)
+        self.synced.pop(slot, None)
         self.owned[slot] = 0
 
     # -------------------------------------------------------------- proposals
@@ -148,10 +155,10 @@ class DraftModelProposer:
             self._sync(s, sequences[s])
             self.target_len[s] = sequences[s].num_tokens
         if self.use_graph and not self.sampled and want and max(want.values()) > 1:
-            first = self._catch_up_graphed(sorted(want))
-            if first is None:
-                first = self._next_tokens(sorted(want))
-            for s, token in first.items():  # catch-up: guess 0
+            if self._catch_up_graphed(sorted(want)):  # guess 0 stays on the device
+                self._decode_graphed(want, guesses, first_on_device=True)
+                return guesses
+            for s, token in self._next_tokens(sorted(want)).items():  # catch-up: guess 0
                 self.drafts[s].token_ids.append(token)
                 guesses[s].append(token)
             self._decode_graphed(want, guesses)
@@ -205,18 +212,19 @@ class DraftModelProposer:
         kernels.accept(self.no_drafts, self.zero_counts, self.last_rows, self.model.config.vocab_size,
                        argmax_partials=c["partials"], temperature=0.0, out_tokens=c["out"], num_out=c["num_out"])
 
-    def _catch_up_graphed(self, live: list[int]) -> dict[int, int] | None:
-        """Guess 0 of every live slot from one replay of the captured catch-up forward
-        (the same rows, positions and context as the eager one, padded to k + 1 rows per
-        slot); None when a slot has no uncached token or more than k + 1 (a new request's
-        prompt), which the eager forward takes."""
+    def _catch_up_graphed(self, live: list[int]) -> bool:
+        """Guess 0 of every live slot into the catch-up's ``out`` on the device, from one
+        replay of the captured catch-up forward (the same rows, positions and context as
+        the eager one, padded to k + 1 rows per slot); False, with nothing run, when a
+        slot has no uncached token or more than k + 1 (a new request's prompt), which the
+        eager forward takes."""
         n, r, dev = self.max_seqs, self.k + 1, self.device
         spans = {}
         for s in live:
             draft = self.drafts[s]
             a, e = draft.num_cached_tokens, draft.num_tokens
             if not 1 <= e - a <= r:
-                return None
+                return False
             spans[s] = (a, e)
         if self._cu is None:
             i32 = dict(dtype=torch.int32, device=dev)
@@ -271,12 +279,9 @@ class DraftModelProposer:
         else:
             self._cu_graph.replay()
         self.forwards += 1
-        torch.cuda.current_stream(dev).synchronize()
-        self.h_out.copy_(c["out"])
-        out = self.h_out.numpy()
         for s, (a, e) in spans.items():
             self.drafts[s].num_cached_tokens = e
-        return {s: int(out[s, 0]) for s in live}
+        return True
 
     # ------------------------------------------------------- graphed decode steps
     def _decode_body(self) -> None:
@@ -293,9 +298,12 @@ class DraftModelProposer:
                        argmax_partials=d["partials"], temperature=0.0, out_tokens=d["out"], num_out=d["num_out"])
         d["tokens"].copy_(d["out"][:, 0])
 
-    def _decode_graphed(self, want: dict[int, int], guesses: dict[int, list[int]]) -> None:
+    def _decode_graphed(self, want: dict[int, int], guesses: dict[int, list[int]],
+                        first_on_device: bool = False) -> None:
         """Guesses 1 .. want[s] - 1 of every slot: the metadata of each step is staged on
-        the host up front, and each step replays the captured decode row per slot."""
+        the host up front, and each step replays the captured decode row per slot.
+        ``first_on_device``: guess 0 is in the catch-up's ``out`` (not yet in ``guesses``);
+        it feeds the first decode row there and is read back with the others."""
         dev, n, k = self.device, self.max_seqs, self.k
         if self._dec is None:
             i32 = dict(dtype=torch.int32, device=dev)
@@ -320,7 +328,8 @@ class DraftModelProposer:
             draft = self.drafts[s]
             length = self.target_len[s]
             self._reserve(s, draft, length + count)
-            toks[s] = guesses[s][0]
+            if not first_on_device:
+                toks[s] = guesses[s][0]
             pos = np.arange(length, length + count - 1)  # guess j reads guess j - 1 at L + j - 1
             slot_ids = self.allocator.slots_for(draft, pos)
             for j in range(1, count):
@@ -332,7 +341,16 @@ class DraftModelProposer:
             stage[j, 1, stage[j, 2] == 0] = self.pool.scratch_slot
         self._dec_tables.numpy()[:] = self.tables
         d["tables"].copy_(self._dec_tables, non_blocking=True)
-        d["tokens"].copy_(self._dec_tokens, non_blocking=True)
+
+        def stage_tokens():
+            if first_on_device:
+                d["tokens"].copy_(self._cu["out"][:, 0])
+            else:
+                d["tokens"].copy_(self._dec_tokens, non_blocking=True)
+
+        stage_tokens()
+        if first_on_device:
+            d["guesses"][:, 0].copy_(self._cu["out"][:, 0])
         for j in range(1, steps):
             for i, name in enumerate(("positions", "slots", "q_len", "ctx")):
                 d[name].copy_(self._dec_host[j, i], non_blocking=True)
@@ -341,7 +359,7 @@ class DraftModelProposer:
                 torch.cuda.current_stream(dev).synchronize()
                 graph = torch.cuda.CUDAGraph()
                 # re-stage this step's tokens: the eager pass already advanced them
-                d["tokens"].copy_(self._dec_tokens, non_blocking=True)
+                stage_tokens()
                 torch.cuda.current_stream(dev).synchronize()
                 with torch.cuda.graph(graph):
                     self._decode_body()
@@ -354,6 +372,9 @@ class DraftModelProposer:
         got = d["guesses"].cpu().numpy()
         for s, count in want.items():
             draft = self.drafts[s]
+            if first_on_device:
+                draft.token_ids.append(int(got[s, 0]))
+                guesses[s].append(int(got[s, 0]))
             for j in range(1, count):
                 draft.token_ids.append(int(got[s, j]))
                 guesses[s].append(int(got[s, j]))

@@ -218,3 +218,48 @@ def test_stop_ids_set_after_construction_reach_the_step_bookkeeping():
     assert runner.stop_token_ids == frozenset({3, 7}) and runner._stop_ids == (3, 7)
     runner.stop_token_ids = frozenset()
     assert runner._stop_ids == ()
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.lists(st.tuples(st.integers(0, 4), st.integers(0, 5), st.booleans()), min_size=1, max_size=12),
+       st.integers(0, 2 ** 16))
+def test_draft_sync_keeps_the_common_prefix_of_the_draft_and_the_target(steps, seed):
+    """DraftModelProposer._sync (proposers.py:95-106), which compares only the tokens since
+    the slot's last sync, equals the reference rule on whole lists: the draft takes the
+    target's tokens and keeps its cache for their common prefix.  Each round the draft
+    appends guesses, the target keeps a prefix of them and appends a token of its own
+    (which may repeat the next guess), sometimes without the draft having proposed."""
+    import random
+
+    from nanoengine_amd.draft import DraftModelProposer
+    from nanoengine_amd.interface import GenerationRequest
+    from nanoengine_amd.sequence_state import Sequence
+
+    rng = random.Random(seed)
+    proposer = DraftModelProposer.__new__(DraftModelProposer)
+    proposer.drafts, proposer.synced = {}, {}
+    target = Sequence.from_request(GenerationRequest("r", [rng.randrange(50) for _ in range(6)],
+                                                     SamplingParams(max_new_tokens=200)))
+    draft_cached = None
+    for guesses, kept, proposed in steps:
+        before = proposer.drafts.get(0)
+        old_ids = list(before.token_ids) if before is not None else None
+        old_cached = before.num_cached_tokens if before is not None else 0
+        draft = proposer._sync(0, target)
+        want_common = 0
+        if old_ids is not None:
+            for a, b in zip(old_ids, target.token_ids):
+                if a != b:
+                    break
+                want_common += 1
+        assert draft.token_ids == target.token_ids and draft.token_ids is not target.token_ids
+        assert draft.num_cached_tokens == min(old_cached, want_common)
+        # the draft scores its tokens and proposes; the target verifies
+        draft.num_cached_tokens = len(draft.token_ids) + (guesses - 1 if guesses and proposed else 0)
+        if not proposed:
+            guesses = 0
+        g = [rng.randrange(50) for _ in range(guesses)]
+        draft.token_ids.extend(g)
+        keep = min(kept, guesses)
+        target.token_ids.extend(g[:keep])
+        target.token_ids.append(rng.randrange(50))
