@@ -468,6 +468,18 @@ class VerifyRunner:
         context = int(lengths[act].max()) + self.k if n else 0
         return verify_graph_allowed(n, context, self.graph_max_batch, self.graph_max_context)
 
+    def capture_graph(self) -> None:
+        """Capture the verify step's HIP graph before any request is admitted, as the
+        reference captures its decode graphs when the engine is created
+        (runtime.py:150-160, cuda_graph_runner.py:94-105), so that no request waits for a
+        capture: the step runs once with every slot inactive (padding rows only, which
+        write the pool's scratch slot) and is then recorded.  A batch with sampled slots
+        captures its own graph at its first step."""
+        if not self.use_graph or self.graph is not None or self.graph_failed or self.np_active.any():
+            return
+        self._run_device_step()
+        torch.cuda.current_stream(self.device).synchronize()
+
     def _run_device_step(self) -> None:
         sampled = self.any_sampled
         if not self.graph_allowed():
@@ -651,30 +663,28 @@ class VerifyRunner:
         return blocks <= self.allocator.num_free_blocks
 
     def _maybe_launch_deep(self) -> None:
-        """With one step in flight whose outcome cannot change the batch (no active slot
-        honours stop tokens and none can reach its length limit, whatever it emits),
-        launch the step after it now, its blocks reserved for the most the running step
-        can emit plus the most guesses the next can make; the device proposes those
-        guesses at the end of the running step.  The host mirrors are at the running
-        step's start."""
+        """With one step in flight, launch the step after it now over the slots active on
+        the host, its blocks reserved for the most the running step can emit plus the
+        most guesses the next can make; the device proposes those guesses at the end of
+        the running step.  A slot that finishes in the running step (its length limit or
+        a stop token) is still run by the launched step, whose outputs for it are dropped
+        when it completes.  The host mirrors are at the running step's start."""
         if (len(self._inflight) != 1 or not self.run_ahead or self.proposer is not None or self.trace is not None
                 or not self._fifo_blocks or self.graph is None or self.graph_sampled != self.any_sampled):
             return
         running = self._inflight[0]
-        act = running.act
-        if (self.np_honours_stop & act).any() or not np.array_equal(act, self.np_active):
+        act = self.np_active.copy()
+        if not act.any():
             return
         guesses = self._read_back_views[running.gb][1][2]  # the running step's guess counts
         most = (guesses + 1) * act  # the most tokens it can emit per slot
-        if ((self.np_gen + most >= self.np_max_new) & act).any():
-            return
         lengths = self.np_len + most
         if not self.graph_allowed(lengths):
             return
         # its guesses: at most k, and never past the sequence's last position (prompt +
         # max_new - 1 tokens hold keys), as the exact count min(k, max_new - gen - 1) is
         last = self.np_len - self.np_gen + self.np_max_new - 1
-        drafts = (np.minimum(self.k, last - lengths) * act).astype(np.int32)
+        drafts = (np.clip(last - lengths, 0, self.k) * act).astype(np.int32)
         *_, blocks = host_step.plan_growth(lengths, drafts, self.np_owned, act, self.block_size)
         if blocks > self.allocator.num_free_blocks:
             return
@@ -683,8 +693,13 @@ class VerifyRunner:
         self.deep_launches += 1
 
     def _complete(self, launched: _Launched, allow_ahead: bool) -> dict[int, StepResult]:
-        """The host side of a step whose outputs have been read back."""
+        """The host side of a step whose outputs have been read back.  A slot that
+        finished in the step before this one (after this one was launched) is no longer
+        active: its outputs here are dropped."""
         active, act, traced_drafts = launched.active, launched.act, launched.traced_drafts
+        if not np.array_equal(act, act & self.np_active):
+            act = act & self.np_active
+            active = [s for s in active if act[s]]
         self._bind_read_back(launched.rb, launched.gb)
         slots = self.slots
         np_num_drafts = self.np_num_drafts
@@ -700,7 +715,7 @@ class VerifyRunner:
                 }
                 for s in active
             })
-        if allow_ahead and not self._inflight and self._may_run_ahead(act):
+        if allow_ahead and not self._inflight and act.any() and self._may_run_ahead(act):
             # the mirrors advance now (finish_step below advances copies of the old ones);
             # this step's outputs stay in their read-back buffer, which the next steps do
             # not write; its guess counts are in the buffer the next step reads back into
@@ -783,7 +798,12 @@ class VerifyRunner:
         self._free_slot(slot)
 
     def _free_slot(self, slot: int) -> None:
-        """Free a slot whose sequence finished or was given up (no step in flight)."""
+        """Free a slot whose sequence finished or was given up.  A step already in flight
+        still runs the slot (its outputs are dropped when it completes): the slot goes
+        inactive on the device after that step, its freed blocks reach later steps only
+        in stream order, and its pinned table row is left as it is, since the step's copy
+        of the tables may not have run yet (entries past a slot's own blocks are never
+        read)."""
         seq = self.slots[slot]
         if seq is None:  # empty, or it finished in the drained step
             return
@@ -796,6 +816,7 @@ class VerifyRunner:
         self.np_honours_stop[slot] = False
         self.np_owned[slot] = 0
         self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
-        self.h_tables[slot].zero_()
+        if not self._inflight:
+            self.h_tables[slot].zero_()
         self.np_temp[slot] = 0.0
         self.np_top_p[slot] = 1.0

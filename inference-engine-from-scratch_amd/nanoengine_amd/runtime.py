@@ -86,4 +86,6 @@ def create_verify_engine(config: Qwen3Config, state_dict: dict[str, torch.Tensor
                           use_graph=settings.cuda_graphs, proposer=proposer,
                           graph_max_batch=settings.cuda_graph_max_batch,
                           graph_max_context=settings.cuda_graph_max_context)
+    if settings.cuda_graphs:
+        runner.capture_graph()
     return VerifyEngine(settings, model, pool, allocator, runner, EngineMetrics())

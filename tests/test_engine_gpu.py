@@ -586,15 +586,27 @@ def test_graph_bounds_run_larger_steps_eagerly(bound):
 
 
 def test_graph_capture_out_of_memory_falls_back_to_eager(monkeypatch):
-    """cuda_graph_runner.py:193-207: a capture that runs out of device memory leaves the
-    runner eager; the step that tried to capture already ran, and the tokens equal the
-    all-eager run."""
+    """The verify graph is captured when the engine is created (runtime.py:150-160), and
+    the first step replays it.  cuda_graph_runner.py:193-207: a capture that runs out of
+    device memory leaves the runner eager; the tokens equal the all-eager run."""
     state = make_state(norm_ones=True)
     prompts = motif_prompts(2, seed=91)
     reqs = [GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=30, ignore_eos=True))
             for i, p in enumerate(prompts)]
     eager = {k: [e.token_id for e in v] for k, v in engine_for(state, 2).batched_generator().generate_all(reqs).items()}
     eng = engine_for(state, 2, graphs=True)
+    assert eng.runner.graph is not None and eng.runner.graph_sampled is False
+    replays = [0]
+    replay = torch.cuda.CUDAGraph.replay
+
+    def counted(self):
+        replays[0] += 1
+        return replay(self)
+
+    monkeypatch.setattr(torch.cuda.CUDAGraph, "replay", counted)
+    out = {k: [e.token_id for e in v] for k, v in eng.batched_generator().generate_all(reqs).items()}
+    assert out == eager and replays[0] > 0
+    monkeypatch.setattr(torch.cuda.CUDAGraph, "replay", replay)
 
     class NoMemory:
         def __init__(self, *a, **k):
@@ -607,6 +619,8 @@ def test_graph_capture_out_of_memory_falls_back_to_eager(monkeypatch):
             return False
 
     monkeypatch.setattr(torch.cuda, "graph", NoMemory)
+    eng = engine_for(state, 2, graphs=True)  # the capture at creation runs out of memory
+    assert eng.runner.graph is None and eng.runner.graph_failed
     out = {k: [e.token_id for e in v] for k, v in eng.batched_generator().generate_all(reqs).items()}
     assert out == eager
     assert eng.runner.graph is None and eng.runner.graph_failed

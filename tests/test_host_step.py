@@ -119,11 +119,11 @@ def test_launch_ahead_check_matches_the_finishing_slots(seed, stops):
 @pytest.mark.parametrize("honour", [False, True])
 def test_deep_launch_reserves_for_every_outcome_of_the_running_step(seed, honour):
     """VerifyRunner._maybe_launch_deep (the step after a running one, launched before the
-    running step's outputs are known) is taken exactly when no active slot honours stop
-    tokens and none can reach its length limit whatever the running step emits (1 .. g + 1
-    tokens); its block bound then covers every such outcome followed by the most guesses
-    the next step can make (min(k, max_new - generated - 1)), and never reaches past the
-    sequence's last position (prompt + max_new - 1 tokens)."""
+    running step's outputs are known) runs the slots active on the host, whether or not
+    one can finish in the running step; its block bound covers every outcome of the
+    running step (1 .. g + 1 tokens) followed by the guesses the device then requests
+    (min(k, max_new - generated - 1), none at the limit) and the bonus row, and reaches
+    at most one token past the sequence's last position (prompt + max_new - 1 tokens)."""
     from collections import deque
 
     from nanoengine_amd.runner import VerifyRunner, _Launched
@@ -132,10 +132,9 @@ def test_deep_launch_reserves_for_every_outcome_of_the_running_step(seed, honour
     rng = np.random.default_rng(200 + seed)
     k = 4
     act = st["act"]
-    # limits from "cannot finish in the running step" to "finishes for some outcome"
-    st["max_new"] = st["gen"] + st["nd"] + 1 + rng.integers(-1, 12, act.shape[0])
-    if seed % 3 == 0:  # every slot far from its limit
-        st["max_new"] = st["gen"] + st["nd"] + 1 + rng.integers(1, 12, act.shape[0])
+    # limits from "finishes in the running step for some outcome" to far away; the device
+    # never requests more guesses than max_new - generated - 1
+    st["max_new"] = st["gen"] + st["nd"] + 1 + rng.integers(0, 12, act.shape[0])
     honours = st["honours"] & honour
     runner = VerifyRunner.__new__(VerifyRunner)
     runner.run_ahead, runner.proposer, runner.trace = True, None, None
@@ -156,20 +155,26 @@ def test_deep_launch_reserves_for_every_outcome_of_the_running_step(seed, honour
     bounds = []
     runner._launch = lambda bound=None: bounds.append(bound) or "launched"
     runner._maybe_launch_deep()
-    g, gen, lengths, max_new = st["nd"].astype(np.int64), st["gen"], st["lengths"], st["max_new"]
-    can_finish = ((gen + g + 1 >= max_new) & act).any() or (honours & act).any()
-    assert (len(bounds) == 1) == (not can_finish)
-    if not bounds:
-        return
+    assert len(bounds) == 1
     b_len, b_drafts = bounds[0]
     assert b_len.dtype == np.int64 and b_drafts.dtype == np.int32
     bound = b_len + b_drafts
+    g, gen, lengths, max_new = st["nd"].astype(np.int64), st["gen"], st["lengths"], st["max_new"]
     for s in np.flatnonzero(act):
         for e in range(1, int(g[s]) + 2):  # the running step emits e tokens
-            nxt = min(k, int(max_new[s] - gen[s] - e - 1))
-            assert int(lengths[s]) + e + max(nxt, 0) <= bound[s]
-        assert bound[s] <= lengths[s] - gen[s] + max_new[s] - 1
+            nxt = max(0, min(k, int(max_new[s] - gen[s] - e - 1)))
+            assert int(lengths[s]) + e + nxt <= bound[s]
+        assert bound[s] <= lengths[s] - gen[s] + max_new[s]
+    assert not b_drafts[~act].any()
     assert runner.deep_launches == 1 and list(runner._inflight)[-1] == "launched"
+
+    # too few free blocks for the bound: nothing is launched
+    runner._inflight = deque([_Launched(np.flatnonzero(act).tolist(), act, None, 1, 0, None)])
+    *_, need = host_step.plan_growth(b_len, b_drafts, st["owned"], act, 16)
+    Pool.num_free_blocks = need - 1
+    bounds.clear()
+    runner._maybe_launch_deep()
+    assert not bounds or need == 0
 
 
 @pytest.mark.parametrize("fn_name", ["finish_step_py", "finish_step"])
