@@ -321,7 +321,14 @@ class VerifyRunner:
         n = len(run)
         pending: deque[list] = deque()
         self._slots_changed()
-        for slot, seq in run:
+        # the run's device state is staged on the host and copied once per tensor (a host
+        # scalar assigned to a device tensor is one synchronous copy each)
+        width = max(seq.num_tokens for _, seq in run)
+        hist = np.zeros((n, width), dtype=np.int32)
+        lens = np.zeros(n, dtype=np.int32)
+        seeds = np.zeros(n, dtype=np.int64)
+        steps = np.zeros(n, dtype=np.int64)
+        for i, (slot, seq) in enumerate(run):
             self.slots[slot] = seq
             p = seq.num_tokens
             seq.num_cached_tokens = 0
@@ -330,18 +337,23 @@ class VerifyRunner:
             if c < self.allocator.first_writable_position(seq):
                 raise RuntimeError(f"prefill of {seq.request_id} would write into a shared block")
             table = self.allocator.block_table(seq)
-            self.h_tables[slot].zero_()
-            self.h_tables[slot, : len(table)] = torch.tensor(table, dtype=torch.int32)
-            self.history[slot, :p] = torch.tensor(seq.token_ids, dtype=torch.int32)
-            self.history_len[slot] = p
-            self.seeds[slot] = seq.sampling_generator.seed
-            self.steps[slot] = seq.sampling_generator.step
+            self.np_tables[slot] = 0
+            self.np_tables[slot, : len(table)] = table
+            hist[i, :p] = seq.token_ids
+            lens[i] = p
+            seeds[i] = seq.sampling_generator.seed
+            steps[i] = seq.sampling_generator.step
             params = seq.sampling_params
             self.np_temp[slot] = max(float(params.temperature), 0.0)
             self.np_top_p[slot] = float(params.top_p)
-            self.temperatures[slot] = float(self.np_temp[slot])
-            self.top_ps[slot] = float(self.np_top_p[slot])
             pending.append([slot, seq, c, p])
+        sl = slice(s0, s0 + n)
+        self.history[sl, :width] = torch.from_numpy(hist)
+        self.history_len[sl] = torch.from_numpy(lens)
+        self.seeds[sl] = torch.from_numpy(seeds)
+        self.steps[sl] = torch.from_numpy(steps)
+        self.temperatures[sl] = torch.from_numpy(self.np_temp[sl].copy())
+        self.top_ps[sl] = torch.from_numpy(self.np_top_p[sl].copy())
         self.block_tables.copy_(self.h_tables, non_blocking=True)
         while pending:
             pieces, room = [], self.model.max_rows
@@ -370,7 +382,6 @@ class VerifyRunner:
             results[slot] = self._emit(slot, seq, [int(self.h_out[s0 + i, 0])], 0, 0)
             self.np_len[slot] = seq.num_tokens
             self.np_gen[slot] = seq.num_generated_tokens
-        sl = slice(s0, s0 + n)
         self.max_new[sl] = torch.from_numpy(self.np_max_new[sl].astype(np.int32))
         self.generated[sl] = torch.from_numpy(self.np_gen[sl].astype(np.int32))
         self._drafts_ready = False  # the new slots have no guesses yet
@@ -815,7 +826,10 @@ class VerifyRunner:
         self.np_active[slot] = False
         self.np_honours_stop[slot] = False
         self.np_owned[slot] = 0
-        self.history_len[slot] = 0  # inactive: the fused kernels skip this slot
+        # inactive: the fused kernels skip this slot (zero_ on the slice is queued on the
+        # stream; assigning a host scalar would copy it synchronously, waiting for every
+        # step in flight)
+        self.history_len[slot : slot + 1].zero_()
         if not self._inflight:
             self.h_tables[slot].zero_()
         self.np_temp[slot] = 0.0
