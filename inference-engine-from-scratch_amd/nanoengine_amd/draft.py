@@ -27,6 +27,7 @@ where the verify step's acceptance reads them as the draft distributions.
 from __future__ import annotations
 
 import math
+from typing import NamedTuple
 
 import numpy as np
 import torch
@@ -35,6 +36,14 @@ from nanoengine_amd import kernels
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
 from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
 from nanoengine_amd.sequence_state import Sequence
+
+
+class DeviceGuesses(NamedTuple):
+    """Guesses left on the device (in the ``device_out`` tensor given to ``propose``):
+    ``counts[slot]`` of them per slot.  The draft's host state takes them at its next
+    proposal."""
+
+    counts: dict[int, int]
 
 
 class DraftModelProposer:
@@ -64,6 +73,7 @@ class DraftModelProposer:
         self.last_rows = torch.arange(max_seqs, **i32)
         self.h_out = torch.zeros((max_seqs, 2), dtype=torch.int32, pin_memory=True)
         self.forwards = 0  # draft forwards run (a count for tests and benchmarks)
+        self.device_proposals = 0  # proposals whose guesses stayed on the device
         self.k = k
         # sampled proposals: the draft's logits per (slot, guess), read by the verifier
         self.logits: torch.Tensor | None = None
@@ -86,6 +96,9 @@ class DraftModelProposer:
         self._cu: dict[str, torch.Tensor] | None = None
         self._cu_graph: torch.cuda.CUDAGraph | None = None
         self._cu_ws = kernels.AttentionWorkspace()
+        # guesses of the last proposal still only on the device: (counts, guess 0 from the
+        # catch-up), read back at the next proposal
+        self._pending: tuple[dict[int, int], bool] | None = None
         model.ensure_rope(max_tokens)
 
     # ------------------------------------------------------------------ state
@@ -120,6 +133,7 @@ class DraftModelProposer:
 
     def release(self, slot: int) -> None:
         """proposers.py:90-93: the request finished; free the draft's blocks."""
+        self._finish_pending()
         draft = self.drafts.pop(slot, None)
         if draft is not None:
             self.allocator.free(draft)
@@ -129,12 +143,18 @@ class DraftModelProposer:
     # -------------------------------------------------------------- proposals
     def propose(self, sequences: dict[int, Sequence], counts: dict[int, int],
                 temperature: float | np.ndarray = 0.0, seeds: torch.Tensor | None = None,
-                steps: np.ndarray | None = None, top_p: float | np.ndarray = 1.0) -> dict[int, list[int]]:
+                steps: np.ndarray | None = None, top_p: float | np.ndarray = 1.0,
+                device_out: torch.Tensor | None = None) -> dict[int, list[int]] | DeviceGuesses:
         """``counts[slot]`` guesses for each slot (proposers.py:70-88): greedy, or sampled at
         ``temperature`` and ``top_p`` (compute_token_probabilities, sampling.py:30-38) with the
         slots' ``seeds`` (device int64) at verify ``steps`` (host).  ``temperature`` and
         ``top_p`` are one value for every slot or arrays indexed by slot (temperature 0:
-        that slot's guesses are the draft's greedy tokens)."""
+        that slot's guesses are the draft's greedy tokens).
+
+        ``device_out`` (int32 [max_seqs, >= k] on the device): when the guesses come from
+        the captured graphs they are copied there on the stream and not waited for, and
+        the call returns their counts (``DeviceGuesses``); otherwise it returns the guesses."""
+        self._finish_pending()
         self.temperatures[:] = np.maximum(np.broadcast_to(np.asarray(temperature, dtype=np.float32),
                                                           self.temperatures.shape), 0.0)
         self.top_ps[:] = np.broadcast_to(np.asarray(top_p, dtype=np.float32), self.top_ps.shape)
@@ -156,8 +176,11 @@ class DraftModelProposer:
             self.target_len[s] = sequences[s].num_tokens
         if self.use_graph and not self.sampled and want and max(want.values()) > 1:
             if self._catch_up_graphed(sorted(want)):  # guess 0 stays on the device
-                self._decode_graphed(want, guesses, first_on_device=True)
-                return guesses
+                self._decode_graphed(want, guesses, first_on_device=True, device_out=device_out)
+                if device_out is None:
+                    return guesses
+                self.device_proposals += 1
+                return DeviceGuesses(dict(want))
             for s, token in self._next_tokens(sorted(want)).items():  # catch-up: guess 0
                 self.drafts[s].token_ids.append(token)
                 guesses[s].append(token)
@@ -299,11 +322,13 @@ class DraftModelProposer:
         d["tokens"].copy_(d["out"][:, 0])
 
     def _decode_graphed(self, want: dict[int, int], guesses: dict[int, list[int]],
-                        first_on_device: bool = False) -> None:
+                        first_on_device: bool = False, device_out: torch.Tensor | None = None) -> None:
         """Guesses 1 .. want[s] - 1 of every slot: the metadata of each step is staged on
         the host up front, and each step replays the captured decode row per slot.
         ``first_on_device``: guess 0 is in the catch-up's ``out`` (not yet in ``guesses``);
-        it feeds the first decode row there and is read back with the others."""
+        it feeds the first decode row there and is read back with the others.
+        ``device_out``: every guess is copied there on the stream instead of being read back
+        now; the next proposal takes them into the drafts' host state."""
         dev, n, k = self.device, self.max_seqs, self.k
         if self._dec is None:
             i32 = dict(dtype=torch.int32, device=dev)
@@ -368,17 +393,35 @@ class DraftModelProposer:
             self._dec_graph.replay()
             self.forwards += 1
             d["guesses"][:, j].copy_(d["out"][:, 0])
+        if device_out is not None:
+            device_out[:, : k].copy_(d["guesses"])
+            self._pending = (dict(want), first_on_device)
+            return
         torch.cuda.current_stream(dev).synchronize()
-        got = d["guesses"].cpu().numpy()
+        self._take_guesses(d["guesses"].cpu().numpy(), want, first_on_device, guesses)
+
+    def _take_guesses(self, got: np.ndarray, want: dict[int, int], first_on_device: bool,
+                      guesses: dict[int, list[int]] | None) -> None:
+        """The decoded guesses ``got[slot, j]`` into each draft's tokens (and ``guesses``);
+        a slot released since the proposal is skipped."""
         for s, count in want.items():
-            draft = self.drafts[s]
-            if first_on_device:
-                draft.token_ids.append(int(got[s, 0]))
-                guesses[s].append(int(got[s, 0]))
-            for j in range(1, count):
+            draft = self.drafts.get(s)
+            if draft is None:
+                continue
+            for j in range(0 if first_on_device else 1, count):
                 draft.token_ids.append(int(got[s, j]))
-                guesses[s].append(int(got[s, j]))
+                if guesses is not None:
+                    guesses[s].append(int(got[s, j]))
             draft.num_cached_tokens = self.target_len[s] + count - 1
+
+    def _finish_pending(self) -> None:
+        """Take the guesses the last proposal left on the device into the drafts' host
+        state (the read-back waits for the work queued before it)."""
+        if self._pending is None:
+            return
+        want, first_on_device = self._pending
+        self._pending = None
+        self._take_guesses(self._dec["guesses"].cpu().numpy(), want, first_on_device, None)
 
     def _forward(self, pieces, rows: int, done: list[int]) -> None:
         """One draft forward over packed pieces; the pieces that reach their draft's last

@@ -43,6 +43,7 @@ import numpy as np
 import torch
 
 from nanoengine_amd import host_step, kernels
+from nanoengine_amd.draft import DeviceGuesses
 from nanoengine_amd.interface import find_finish_reason
 from nanoengine_amd.memory import KVCachePool, PagedSlotAllocator
 from nanoengine_amd.qwen3 import AttentionBatch, Qwen3VerifyModel
@@ -598,17 +599,24 @@ class VerifyRunner:
         else:
             self.num_tokens.copy_(self.h_num_tokens, non_blocking=True)
             self.steps.copy_(self.h_steps, non_blocking=True)
+            # greedy guesses from the draft's captured graphs stay on the device: the step
+            # reads them there, and the host only needs their counts (not with a trace)
             guesses = self.proposer.propose({s: slots[s] for s in active},
                                             {s: int(self.np_num_tokens[s]) for s in active},
                                             temperature=self.np_temp, top_p=self.np_top_p,
                                             seeds=self.seeds,
-                                            steps=self.np_steps)
+                                            steps=self.np_steps,
+                                            device_out=self.drafts if self.trace is None else None)
             self.np_num_drafts[:] = 0
-            np_drafts = self.h_drafts.numpy()
-            for s, g in guesses.items():
-                np_drafts[s, : len(g)] = g
-                self.np_num_drafts[s] = len(g)
-            self.drafts.copy_(self.h_drafts, non_blocking=True)
+            if isinstance(guesses, DeviceGuesses):
+                for s, n in guesses.counts.items():
+                    self.np_num_drafts[s] = n
+            else:
+                np_drafts = self.h_drafts.numpy()
+                for s, g in guesses.items():
+                    np_drafts[s, : len(g)] = g
+                    self.np_num_drafts[s] = len(g)
+                self.drafts.copy_(self.h_drafts, non_blocking=True)
             self.num_drafts.copy_(self.h_num_drafts, non_blocking=True)
         np_num_drafts, allocator, bs = self.np_num_drafts, self.allocator, self.block_size
         lengths, drafts = (self.np_len, np_num_drafts) if bound is None else bound

@@ -289,3 +289,31 @@ def test_mixed_greedy_and_sampled_draft_batch_matches_the_oracles():
             assert rec["out"] == oacc.sampled_accept_draft(t_rows, d_rows, rec["drafts"], temp, seed, step)
         checked.add(temp > 0)
     assert checked == {False, True}
+
+
+def test_guesses_left_on_the_device_equal_the_read_back_ones():
+    """With graphs, the draft's greedy guesses stay on the device for the verify step and
+    the host takes them at the next proposal; with a trace they are read back before the
+    step.  Every step's tokens, guess counts and kept counts are the same both ways."""
+    state = unit_norms(random_state_dict(CFG, seed=0, std=0.02))
+    dstate = unit_norms(random_state_dict(DCFG, seed=7, std=0.02))
+    ps = prompts(4, seed=3)
+
+    def run(trace):
+        eng = engine(state, DCFG, dstate, 4, graphs=True)
+        if trace:
+            eng.runner.trace = []
+        seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=20,
+                                                                                   ignore_eos=True)))
+                for i, p in enumerate(ps)]
+        steps = [eng.runner.add(seqs)]
+        while eng.runner.active_slots or eng.runner.pending:
+            steps.append(eng.runner.step())
+        out = [{s: (r.tokens, r.num_guesses, r.num_kept) for s, r in res.items()} for res in steps]
+        return out, [list(q.token_ids) for q in seqs], eng.runner.proposer
+
+    read_back, ids_a, _ = run(True)
+    on_device, ids_b, proposer = run(False)
+    assert on_device == read_back and ids_a == ids_b
+    assert proposer._cu_graph is not None and proposer.device_proposals > 0
+    assert sum(r[1] for step in on_device[1:] for r in step.values()) > 0
