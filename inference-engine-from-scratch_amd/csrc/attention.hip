@@ -834,9 +834,10 @@ struct DmaShape {
   static constexpr int ring = BF16 ? 2 : kDmaRing;       // tiles in flight per wave
   static constexpr int slot_bytes = BF16 ? kBfDmaSlot : kDmaSlot;
   static constexpr int per_tile = BF16 ? kBfDmaPerTile : kDmaPerTile;  // copies per tile
-  // tiles issued before the first iteration; the rest of the ring follows once the
-  // first two have landed, which keeps the launch's opening burst of copies (and the
-  // queueing delay every wave's first tiles see behind it) at half the ring
+  // tiles a wave with more tiles than its ring issues before the first iteration; the
+  // rest of the ring follows once the first two have landed, which keeps the launch's
+  // opening burst of copies (and the queueing delay every wave's first tiles see behind
+  // it) at half the ring.  A wave with at most `ring` tiles issues them all at once.
   static constexpr int first = 2;
   static constexpr int slot_off = waves * ring * slot_bytes;
   static constexpr int sc_off = slot_off + kPlanMaxTiles * 4;
@@ -1073,6 +1074,36 @@ __device__ __forceinline__ void dma_wait_vmcnt() {
 __device__ __forceinline__ void dma_wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
 }
+
+// s_waitcnt vmcnt(PER * n) for a wave-uniform n in [0, MAXN]: wait until at most the
+// copies of the n tiles issued last are still in flight
+template <int PER, int MAXN>
+__device__ __forceinline__ void dma_wait_tiles(int n) {
+  if constexpr (MAXN <= 0) {
+    dma_wait_vmcnt<0>();
+  } else {
+    if (n >= MAXN) {
+      dma_wait_vmcnt<PER * MAXN>();
+    } else {
+      dma_wait_tiles<PER, MAXN - 1>(n);
+    }
+  }
+}
+
+// The copy schedule of a wave's ring of R tiles over its n tiles: a wave with at most R
+// tiles requests them all before its first iteration (one round trip); a longer one
+// requests its first F, and the rest of the ring once those have landed.  Iteration it
+// consumes tiles 2 it and 2 it + 1 and then requests tiles 2 it + R and 2 it + 1 + R.  No
+// tile past the wave's last is copied: the odd tile a last iteration lacks is masked
+// there (its keys lie at or past the end), so its ring slot is never used.
+template <int R, int F>
+struct DmaSchedule {
+  __device__ __forceinline__ static int first(int n) { return n <= R ? n : F; }
+  // tiles still in flight behind tiles 2 it, 2 it + 1 when iteration it starts
+  __device__ __forceinline__ static int behind(int it, int n) {
+    return it == 0 ? max(first(n) - 2, 0) : max(min(n - 2 * it - 2, R - 2), 0);
+  }
+};
 
 // Per-lane byte offsets of a tile copy: K/V rows land as [16 keys][128 B] with 16-byte
 // chunk c of key k stored at chunk position c ^ (k & 7), which makes the fragment reads
@@ -1436,12 +1467,15 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_att
       dma_tile(p, w_slot, n_tiles, t, head, dl, dst);
     }
   };
+  using Sched = DmaSchedule<RING, FIRST>;
+  const int n_first = Sched::first(n_tiles);
   if (n_tiles > 0) {
 #pragma unroll
-    for (int j = 0; j < FIRST; ++j) copy_tile(j, ring + j * kSlot);
+    for (int j = 0; j < RING; ++j)
+      if (j < n_first) copy_tile(j, ring + j * kSlot);
     // Q was issued before the ring's copies: wait for it alone (the compiler's own wait
     // would also drain the copies, since it does not order them after the Q loads)
-    dma_wait_vmcnt<kPerTile * FIRST>();
+    dma_wait_tiles<kPerTile, RING>(n_first);
   } else {
     dma_wait_vmcnt<0>();  // a wave with no tiles of the item (KS > 1) only loads Q
   }
@@ -1479,9 +1513,8 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_att
     constexpr bool kMask = decltype(mask)::value;
     constexpr bool kFirst = decltype(first)::value;
     // this wave's DMA of tiles 2it, 2it+1 has landed once at most the tiles issued
-    // after them are still in flight (none before the first iteration, and none with a
-    // two-tile ring)
-    dma_wait_vmcnt<kFirst ? kPerTile * (FIRST - 2) : kPerTile * (RING - 2)>();
+    // after them are still in flight
+    dma_wait_tiles<kPerTile, RING - 2>(Sched::behind(kFirst ? 0 : it, n_tiles));
     const char* sa = ring + ((2 * it) % RING) * kSlot;
     const char* sb = ring + ((2 * it + 1) % RING) * kSlot;
     const int kb = kstart + it * kIterKeys;
@@ -1496,10 +1529,11 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_att
     dma_wait_lgkmcnt0();
     if constexpr (kFirst) {
 #pragma unroll
-      for (int j = FIRST; j < RING; ++j) copy_tile(j, ring + j * kSlot);
+      for (int j = FIRST; j < RING; ++j)
+        if (j >= n_first && j < n_tiles) copy_tile(j, ring + j * kSlot);
     }
-    copy_tile(2 * it + RING, ring + ((2 * it) % RING) * kSlot);
-    copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
+    if (2 * it + RING < n_tiles) copy_tile(2 * it + RING, ring + ((2 * it) % RING) * kSlot);
+    if (2 * it + 1 + RING < n_tiles) copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
     if constexpr (BF16) {
       compute_iter_bf<MT, kMask>(A, qf, p.qk_scale, kb, kend, kend_row, lane, m, l, o);
     } else {
@@ -1643,19 +1677,21 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_kv_
       dma_tile(p, w_slot, n_tiles, t, head, dl, dst);
     }
   };
+  using Sched = DmaSchedule<RING, FIRST>;
+  const int n_first = Sched::first(n_tiles);
 #pragma unroll
-  for (int j = 0; j < FIRST; ++j) copy_tile(j, ring + j * kSlot);
+  for (int j = 0; j < RING; ++j)
+    if (j < n_first) copy_tile(j, ring + j * kSlot);
   const int n_iter = (n_tiles + 1) / 2;
   for (int it = 0; it < n_iter; ++it) {
+    dma_wait_tiles<kPerTile, RING - 2>(Sched::behind(it, n_tiles));
     if (it == 0) {
-      dma_wait_vmcnt<kPerTile * (FIRST - 2)>();
 #pragma unroll
-      for (int j = FIRST; j < RING; ++j) copy_tile(j, ring + j * kSlot);
-    } else {
-      dma_wait_vmcnt<kPerTile * (RING - 2)>();
+      for (int j = FIRST; j < RING; ++j)
+        if (j >= n_first && j < n_tiles) copy_tile(j, ring + j * kSlot);
     }
-    copy_tile(2 * it + RING, ring + ((2 * it) % RING) * kSlot);
-    copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
+    if (2 * it + RING < n_tiles) copy_tile(2 * it + RING, ring + ((2 * it) % RING) * kSlot);
+    if (2 * it + 1 + RING < n_tiles) copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
   }
   dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
 }
