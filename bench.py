@@ -328,7 +328,7 @@ class AttentionWorkload:
           table), then a suffix of U{4096..16384} tokens (seed 1); 9 queries (k = 8),
           int8 KV with bf16 scales."""
 
-    def __init__(self, torch, layers: int = 28, kind: str = "int8"):
+    def __init__(self, torch, layers: int = 28, kind: str = "int8", ctx=None):
         import numpy as np
 
         from nanoengine_amd import kernels
@@ -339,7 +339,9 @@ class AttentionWorkload:
         self.kind = kind
         shared = 0
         if kind == "int8":
-            self.ctx = rng.integers(128, 1025, size=NUM_SEQS).astype(np.int32)
+            # ctx: other contexts for the int8 shape (the context sweep)
+            drawn = rng.integers(128, 1025, size=NUM_SEQS)
+            self.ctx = (drawn if ctx is None else np.asarray(ctx)).astype(np.int32)
             self.ql = 5
         elif kind == "bf16":
             self.ctx = rng.integers(256, 2049, size=16).astype(np.int32)
@@ -485,6 +487,55 @@ def run_attention_kernel_only(torch, kind: str, layers: int, reps: int = 3):
     del w
     torch.cuda.empty_cache()
     return out
+
+
+def run_attention_ctx_sweep(torch, reps: int = 5) -> dict:
+    """The int8 planned call (64 seqs, 5 queries, fp16 scales, 28 pools) over several
+    context draws: U{128..1024} (seed 1, the kernel-only int8 shape), uniform contexts of
+    the same total, and uniform 128, 256, 512 and 1024.  A line through the uniform 128..1024
+    draws' (K/V bytes, us) splits a call into a fixed part and a rate per added byte; the
+    seeded draw against the uniform one of its total is what its spread of lengths costs.
+    Each draw also times the K/V stream alone (the same plan and copies)."""
+    import numpy as np
+
+    from nanoengine_amd import _native
+
+    base = np.random.default_rng(1).integers(128, 1025, size=NUM_SEQS)
+    mean = int(round(float(base.mean())))
+    draws = [("ctx U{128..1024} seed 1", base), (f"uniform {mean}", np.full(NUM_SEQS, mean))]
+    draws += [(f"uniform {c}", np.full(NUM_SEQS, c)) for c in (128, 256, 512, 1024)]
+    rows = []
+    for name, ctx in draws:
+        w = AttentionWorkload(torch, layers=28, kind="int8", ctx=ctx)
+        w.plan()
+        for p in w.pools:
+            w.launch(p, planned=True)
+        torch.cuda.synchronize()
+        timer = _native.LaunchTimer()
+        _native.set_launch_timer("ne_paged_verify_attention_planned", timer)
+        for _ in range(reps):
+            w.plan()
+            for p in w.pools:
+                w.launch(p, planned=True)
+        torch.cuda.synchronize()
+        _native.set_launch_timer("ne_paged_verify_attention_planned", None)
+        if w.ws.error_flag() != 0:
+            raise RuntimeError(f"attention sweep ({name}) raised the workspace error flag")
+        dur = timer.durations_ms()
+        us = 1e3 * sum(dur) / len(dur)
+        kv = attention_bytes(w.ctx.tolist(), 0)
+        rows.append({"contexts": name, "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()),
+                     "kv_bytes": int(kv), "planned_us": round(us, 2),
+                     "GB_s": round(w.bytes_per_launch / us / 1e3, 1),
+                     "stream_us": stream_ceiling(torch, w, reps)["us"]})
+        del w
+        torch.cuda.empty_cache()
+    xs = np.array([r["kv_bytes"] for r in rows[2:]], dtype=np.float64)
+    ys = np.array([r["planned_us"] for r in rows[2:]], dtype=np.float64)
+    slope, icpt = np.polyfit(xs, ys, 1)
+    return {"workload": "int8 KV, 64 seqs, q=5, fp16 scales, 28 pools, planned call; context draws below",
+            "draws": rows,
+            "uniform_fit": {"fixed_us": round(float(icpt), 2), "TB_s_per_added_byte": round(1e-6 / slope, 2)}}
 
 
 def run_attention_roofline(torch, reps: int = 5):
@@ -1111,7 +1162,7 @@ def main() -> int:
     parser.add_argument("--eager", dest="graph", action="store_false",
                         help="launch the step's kernels one by one instead of replaying a HIP graph")
     parser.add_argument("--only", choices=("all", "verify", "attention", "gemm", "baseline", "long", "draft",
-                                           "accept"),
+                                           "accept", "attention_sweep"),
                         default="all")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-torch-baseline", action="store_true")
@@ -1159,6 +1210,9 @@ def main() -> int:
     if args.only in ("all", "gemm"):
         gemm = run_gemm_roofline(torch, counters=counters)
         log(f"gemm: {gemm['achieved']} TFLOP/s over QKV and gate|up")
+    if args.only == "attention_sweep":  # the attention call's fixed part and per-byte rate
+        print(json.dumps({"attention_ctx_sweep": run_attention_ctx_sweep(torch)}), flush=True)
+        return 0
     if args.only == "accept":  # the sampled acceptance kernel alone, and the T = 0.8 step
         s_res = run_verify(args, torch, temperature=0.8, steps=args.steps, warmup=args.warmup)
         print(json.dumps({"accept_kernel_only": run_accept_sampled_kernel_only(torch),
