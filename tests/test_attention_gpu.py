@@ -264,6 +264,46 @@ def test_head_split_planned_path(device, num_seqs, max_ctx):
     assert float((b.cpu()[idx].float() - a.cpu()[idx].float()).abs().max()) <= 2e-2 * float(a.cpu()[idx].float().abs().max())
 
 
+@pytest.mark.parametrize("kv_dtype", ["int8", "bf16"])
+def test_odd_last_tiles_ignore_what_the_previous_call_left_in_lds(device, kv_dtype):
+    """A wave copies no tile past its last one, so when its tile count is odd the second ring
+    slot of its last iteration holds whatever the previous kernel on that CU left in LDS.
+    Calls over a pool of NaN (every K / V value, or every int8 scale) run first and fill
+    the rings with NaN; the same batch over a clean pool, with 0 to 6 tiles per wave (64
+    sequences, 4 waves per KV head in the planned call), must still match the oracle, and so
+    must the unplanned entry point (one wave per head over splits of odd tile counts)."""
+    tiles = [1, 2, 3, 5, 6, 7, 9, 11, 13, 17, 19, 21, 23, 25, 4, 8]
+    ctx = [16 * t - (i % 7) for i, t in enumerate(tiles * 4)]
+    q_lens = [min(5, c) for c in ctx]
+    sdt = torch.float16 if kv_dtype == "int8" else torch.bfloat16
+    num_blocks = sum((c + 15) // 16 for c in ctx) + 8
+    kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, kv_dtype, sdt, seed=21)
+    tables, ctx_t, qs, ql, rows = make_batch(ctx, q_lens, num_blocks, 16, seed=22)
+    q = torch.randn(rows, HQ, 128, generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    d = lambda t: None if t is None else t.to(device)
+    tables_d, ctx_d, qs_d, ql_d, q_d = d(tables), d(ctx_t), d(qs), d(ql), d(q)
+    if kv_dtype == "bf16":
+        poison = (torch.full_like(d(kc), float("nan")), torch.full_like(d(vc), float("nan")), None, None)
+    else:
+        poison = (d(kc), d(vc), torch.full_like(d(ks), float("nan")), torch.full_like(d(vs), float("nan")))
+    clean = (d(kc), d(vc), d(ks), d(vs))
+    ws = kernels.AttentionWorkspace()
+    kernels.paged_attention_plan(tables_d, 16, ctx_d, qs_d, ql_d, HQ, HKV, 5, max(ctx), ws)
+    call = lambda pool, planned, split_len=0: kernels.paged_verify_attention(
+        q_d, *pool, tables_d, 16, ctx_d, qs_d, ql_d, max_q_len=5, max_ctx_len=max(ctx), workspace=ws,
+        planned=planned, split_len=split_len)
+    idx = real_rows(qs, ql)
+    ref = paged_attention_reference(q, kc, vc, ks, vs, tables, 16, ctx_t, qs, ql, model_dtype=sdt)
+    for planned, split_len in ((True, 0), (False, 128)):
+        call(poison, planned, split_len)
+        out = call(clean, planned, split_len)
+        torch.cuda.synchronize()
+        got = out.cpu()[idx]
+        assert bool(torch.isfinite(got.float()).all()), (planned, split_len)
+        assert rel_err(got, ref[idx]) < TOL, (planned, split_len)
+    assert ws.error_flag() == 0
+
+
 def _random_int8_pool(num_slots, scale_dtype, seed):
     """int8 codes U{-127..127} and per-(slot, head) scales in [0.005, 0.035): the layout the
     reference's int8 KV pool holds (ne/engine/memory/kv_cache_pool.py:49-69)."""
