@@ -534,6 +534,82 @@ def test_finished_slot_is_not_reused_before_its_pending_result_is_returned():
     assert (got, ids) == run(False)[:2]
 
 
+@pytest.mark.parametrize("seed", [3, 17, 29, 41])
+def test_random_add_step_release_interleavings_keep_every_request_on_its_generation(seed):
+    """Seeded random driving of the runner: admissions into free slots, releases of running
+    requests (some with a step of theirs in flight or its result waiting), and steps, for 10
+    requests of random lengths on 4 slots, some honouring stop tokens, with launch-ahead on
+    and off.  The tokens a request receives may stop anywhere (a release), and with
+    launch-ahead a request admitted while a step runs joins one step later, so the two runs
+    need not release at the same points; what they must keep is the content: every
+    request's tokens are a prefix of the generation it gets when nothing is released, and a
+    request that finishes by itself gets all of it, with the same finish reason.  At the
+    end no block stays reserved."""
+    state = make_state(norm_ones=True)
+    rng0 = np.random.default_rng(seed)
+    n_req, n_slots = 10, 4
+    prompts = motif_prompts(n_req, seed=100 + seed)
+    lens = [int(x) for x in rng0.integers(3, 41, size=n_req)]
+    honour = [bool(x) for x in rng0.integers(0, 2, size=n_req)]
+
+    def run(ahead, stop_ids, p_release):
+        eng = engine_for(state, n_slots, graphs=True)
+        runner = eng.runner
+        runner.run_ahead = ahead
+        runner.stop_token_ids = stop_ids
+        rng = np.random.default_rng(seed)
+        seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=n,
+                                                                                   ignore_eos=not h)))
+                for i, (p, n, h) in enumerate(zip(prompts, lens, honour))]
+        got = {i: [] for i in range(n_req)}
+        end = {}
+        owner = {}  # slot -> request the caller still sees running there
+        nxt = 0
+
+        def record(results):
+            for slot, r in results.items():
+                i = owner[slot]
+                got[i].extend(r.tokens)
+                if r.finish_reason is not None:
+                    end[i] = r.finish_reason
+                    del owner[slot]
+
+        while nxt < n_req or owner:
+            assert len(runner.free_slots()) == n_slots - len(owner)
+            x = rng.random()
+            if nxt < n_req and len(owner) < n_slots and x < 0.3:
+                k = min(int(rng.integers(1, 3)), n_slots - len(owner), n_req - nxt)
+                free = runner.free_slots()[:k]
+                res = runner.add(seqs[nxt : nxt + k])
+                for j, slot in enumerate(free):
+                    owner[slot] = nxt + j
+                nxt += k
+                record(res)
+            elif owner and x > 1 - p_release:
+                slot = sorted(owner)[int(rng.integers(0, len(owner)))]
+                runner.release(slot)
+                end[owner.pop(slot)] = "released"
+            else:
+                record(runner.step())
+        while runner.pending:
+            assert not runner.step()  # released slots' results are dropped with them
+        assert eng.allocator.num_reserved_slots == 0
+        return got, end, runner.ahead_launches
+
+    free_got, _, _ = run(False, frozenset(), 0.0)
+    # a token from the middle of two stop-honouring requests' generations: they stop there
+    stop_ids = frozenset([free_got[i][len(free_got[i]) // 2] for i in range(n_req) if honour[i]][:2])
+    full, full_end, _ = run(False, stop_ids, 0.0)
+    assert "stop" in full_end.values()
+    for ahead in (False, True):
+        got, end, launches = run(ahead, stop_ids, 0.08)
+        assert "released" in end.values() and (launches > 0) == ahead
+        for i in range(n_req):
+            assert got[i] == full[i][: len(got[i])], (ahead, i)
+            if end[i] != "released":
+                assert (got[i], end[i]) == (full[i], full_end[i]), (ahead, i)
+
+
 @pytest.mark.parametrize("bound", ["batch", "context"])
 def test_graph_bounds_run_larger_steps_eagerly(bound):
     """cuda_graph_max_batch / cuda_graph_max_context (ne/config.py:58-61): while a step is
