@@ -16,6 +16,7 @@ test_engine_gpu.py); draft: the same shapes with 1 layer and other weights.  Che
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -317,3 +318,59 @@ def test_guesses_left_on_the_device_equal_the_read_back_ones():
     assert on_device == read_back and ids_a == ids_b
     assert proposer._cu_graph is not None and proposer.device_proposals > 0
     assert sum(r[1] for step in on_device[1:] for r in step.values()) > 0
+
+
+@pytest.mark.parametrize("seed", [5, 23])
+def test_random_add_step_release_keep_every_draft_request_on_its_generation(seed):
+    """Seeded random admissions, releases and steps of 9 requests on 3 slots with graphed
+    draft proposals (their guesses left on the device and taken by the host at the next
+    proposal or release).  Greedy verification keeps the target's own argmax, so whatever
+    the draft guesses and wherever a release cuts a request off, every request's tokens
+    are a prefix of the generation it gets when nothing is released, and all of it when it
+    finishes by itself."""
+    state = unit_norms(random_state_dict(CFG, seed=0, std=0.02))
+    dstate = unit_norms(random_state_dict(DCFG, seed=7, std=0.02))
+    n_req, n_slots = 9, 3
+    ps = prompts(n_req, seed=40 + seed)
+    lens = [int(x) for x in np.random.default_rng(seed).integers(2, 31, size=n_req)]
+
+    def run(p_release):
+        eng = engine(state, DCFG, dstate, n_slots, graphs=True)
+        runner = eng.runner
+        rng = np.random.default_rng(seed)
+        seqs = [Sequence.from_request(GenerationRequest(f"r{i}", p, SamplingParams(max_new_tokens=n,
+                                                                                   ignore_eos=True)))
+                for i, (p, n) in enumerate(zip(ps, lens))]
+        got = {i: [] for i in range(n_req)}
+        end, owner, nxt = {}, {}, 0
+
+        def record(results):
+            for slot, r in results.items():
+                got[owner[slot]].extend(r.tokens)
+                if r.finish_reason is not None:
+                    end[owner.pop(slot)] = r.finish_reason
+
+        while nxt < n_req or owner:
+            x = rng.random()
+            if nxt < n_req and len(owner) < n_slots and x < 0.3:
+                free = runner.free_slots()[:1]
+                res = runner.add([seqs[nxt]])
+                owner[free[0]] = nxt
+                nxt += 1
+                record(res)
+            elif owner and x > 1 - p_release:
+                slot = sorted(owner)[int(rng.integers(0, len(owner)))]
+                runner.release(slot)
+                end[owner.pop(slot)] = "released"
+            else:
+                record(runner.step())
+        assert eng.allocator.num_reserved_slots == 0
+        return got, end, runner.proposer.device_proposals
+
+    full, full_end, _ = run(0.0)
+    got, end, on_device = run(0.1)
+    assert on_device > 0 and "released" in end.values()
+    for i in range(n_req):
+        assert got[i] == full[i][: len(got[i])], i
+        if end[i] != "released":
+            assert (got[i], end[i]) == (full[i], full_end[i]), i
