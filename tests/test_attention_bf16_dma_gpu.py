@@ -48,7 +48,7 @@ def _run(device, ctx, q_lens, num_blocks=None, pool=None, seed=0):
     return unplanned.cpu()[idx], planned.cpu()[idx], ref[idx]
 
 
-def test_cfg1_bf16_plan_and_planned(device):
+def test_bf16_16_seqs_ctx_256_to_2048_plan_and_planned(device):
     """16 sequences, context U{256..2048} (seed 1), 5 queries, 4096-block pool: split items
     and the partial merge, planned and unplanned (the same items, the same bits)."""
     ctx = np.random.default_rng(1).integers(256, 2049, size=16).tolist()

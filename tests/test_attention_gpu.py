@@ -88,7 +88,7 @@ def test_deterministic(device):
     assert torch.equal(a, b)
 
 
-def test_cfg1_bf16_full_shape(device):
+def test_bf16_16_seqs_ctx_256_to_2048_full_shape(device):
     """16 sequences, context U{256..2048} (seed 1), 5 queries, bf16 KV, 4096-block pool."""
     rng = np.random.default_rng(1)
     ctx = rng.integers(256, 2049, size=16).tolist()
@@ -96,7 +96,7 @@ def test_cfg1_bf16_full_shape(device):
     assert rel_err(got, ref) < TOL
 
 
-def test_cfg2_int8_full_shape(device):
+def test_int8_64_seqs_ctx_128_to_1024_full_shape(device):
     """64 sequences, context U{128..1024}, int8 KV with fp16 scales, 4096-block pool."""
     rng = np.random.default_rng(1)
     ctx = rng.integers(128, 1025, size=64).tolist()
@@ -315,7 +315,7 @@ def _random_int8_pool(num_slots, scale_dtype, seed):
     return kc, vc, ks, vs
 
 
-def test_cfg4_long_context_shared_prefix_plan_and_unplanned(device):
+def test_long_context_32_seqs_shared_prefix_plan_and_unplanned(device):
     """The long-context + prefix-sharing configuration: 32 sequences whose tables start with
     the same 64 blocks (a 1024-token shared prefix) followed by U{4096..16384} own tokens
     (seed 1), k = 8 (9 queries), int8 KV with bf16 scales; one sequence is stretched to
@@ -359,7 +359,7 @@ def test_cfg4_long_context_shared_prefix_plan_and_unplanned(device):
         assert rel_err(planned.cpu()[rows], ref[rows]) < TOL, f"sequence {b} ({ctx[b]} keys)"
 
 
-def test_cfg2_planned_fp16_scales_roofline_variant(device):
+def test_int8_64_seqs_planned_fp16_scales_roofline_variant(device):
     """The call the attention roofline times: the per-step plan and the planned call at the
     int8 configuration (64 sequences, context U{128..1024} seed 1, 5 queries, fp16 scales,
     4096-block pool), which serves each sequence as one whole item over 4 work-groups with
