@@ -892,15 +892,189 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(GemmParams p)
   }
 }
 
+// ---- LM head for at most 80 rows (a draft model's one-row-per-sequence decode, small
+// verify batches) -------------------------------------------------------------------
+// The 320-row kernel's time does not shrink with the rows: its eight waves split the
+// rows four ways, so at m <= 80 two waves of one SIMD do all the MFMAs while the weights
+// stream through the same two-stage ring.  Here wave c of a work-group owns columns
+// 32 c .. +32 of each 256-column block against all 80 rows (5 x 2 subtiles), and a stage
+// is X 10 KiB + W 32 KiB, so the ring holds three stages and the weight copies of a stage
+// go out two stages ahead.  Work-group ranges, blocks, K stages, the chunk swizzle, the
+// MFMA operand order and the argmax key are the 320-row kernel's: every logit is the same
+// sum in the same order, hence the same bits, and so is every argmax partial.
+constexpr int kLsRows = 80;
+constexpr int kLsRing = 3;
+constexpr int kLsXSlots = kLsRows * kLmSK * 2 / 1024;    // 10 copies of 8 rows
+constexpr int kLsWSlots = kLmCols * kLmSK * 2 / 1024;    // 32
+constexpr int kLsSlots = kLsXSlots + kLsWSlots;          // 42 per stage
+constexpr int kLsStage = kLsSlots * 1024;
+constexpr int kLsMaxCopies = (kLsSlots + kLmWaves - 1) / kLmWaves;  // 6 (waves 0, 1), else 5
+static_assert(kLsRing * kLsStage <= 160 * 1024, "LDS");
+
+// copy j of wave w fills stage slot s = 8 j + w (slots 0..9: X rows 8 s .., then W rows)
+__device__ __forceinline__ int ls_copies(int wave) { return (kLsSlots - wave + kLmWaves - 1) / kLmWaves; }
+
+__global__ __launch_bounds__(kLmWaves * kWave) void lm_head_small_kernel(GemmParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int groups = p.n / kArgmaxCols;
+  const int grp0 = (int)((int64_t)groups * blockIdx.x / gridDim.x);
+  const int grp1 = (int)((int64_t)groups * (blockIdx.x + 1) / gridDim.x);
+  const int nblk = (grp1 - grp0 + 3) / 4;
+  const int kt = p.k / kLmSK;
+  const int total = nblk * kt;  // stages, in order block, k
+  if (total == 0) return;
+  const int rc0 = grp0 * kArgmaxCols;
+  const int tiles = 2 * (int)gridDim.x;
+  const int ncp = ls_copies(wave);
+
+  // per copy: the 32-bit lane offset from the stage's scalar base (X: row and chunk; W:
+  // column row within the block and chunk, a short block re-reading its last column)
+  auto offset = [&](int j, int ccols) -> uint32_t {
+    const int s = j * kLmWaves + wave;
+    if (s < kLsXSlots) {
+      const int row = s * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ (row & 7);
+      return (uint32_t)min(row, p.m - 1) * (uint32_t)(p.ldx * 2) + (uint32_t)chunk * 16u;
+    }
+    const int wrow = (s - kLsXSlots) * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (wrow & 7);
+    return (uint32_t)min(wrow, ccols - 1) * (uint32_t)(p.k * 2) + (uint32_t)chunk * 16u;
+  };
+  auto issue = [&](int u) {
+    const int bi = u / kt, t = u % kt;
+    const int c0 = (grp0 + 4 * bi) * kArgmaxCols;
+    const int ccols = min(4, grp1 - grp0 - 4 * bi) * kArgmaxCols;
+    const int k0 = t * kLmSK;
+    char* stage = smem + (u % kLsRing) * kLsStage;
+    const char* xsrc = uniform_ptr((const char*)p.x + k0 * 2);
+    const char* wsrc = uniform_ptr((const char*)p.w + ((int64_t)c0 * p.k + k0) * 2);
+#pragma unroll
+    for (int j = 0; j < kLsMaxCopies; ++j) {
+      if (j >= ncp) break;
+      const int s = j * kLmWaves + wave;
+      uint32_t o = offset(j, ccols);
+      __asm__("" : "+v"(o));  // scalar base + 32-bit lane offset addressing
+      lds_dma16((s < kLsXSlots ? xsrc : wsrc) + o, stage + s * 1024);
+    }
+  };
+
+  floatx4 acc[5][2];
+#pragma unroll
+  for (int mi = 0; mi < 5; ++mi) acc[mi][0] = acc[mi][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+  uint32_t row_best[5] = {0, 0, 0, 0, 0};
+
+  issue(0);
+  if (total > 1) issue(1);
+  for (int u = 0; u < total; ++u) {
+    // this wave's copies of stage u have landed once at most stage u + 1's are in flight
+    if (u + 1 < total) {
+      wait_pending<1, kLsMaxCopies>(ncp);
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("s_barrier" ::: "memory");  // everyone's stage u; stage u - 1 fully read
+    if (u + 2 < total) issue(u + 2);
+    const int bi = u / kt, t = u % kt;
+    const int c0 = (grp0 + 4 * bi) * kArgmaxCols;
+    const int ccols = min(4, grp1 - grp0 - 4 * bi) * kArgmaxCols;
+    const bool live = wave * 32 < ccols;  // a short block's waves past its end skip the MFMAs
+    if (live) {
+      const char* xs = smem + (u % kLsRing) * kLsStage;
+      const char* ws = xs + kLsXSlots * 1024;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        bf16x8 b[2];
+#pragma unroll
+        for (int ns = 0; ns < 2; ++ns) b[ns] = lm_frag(ws, wave * 32 + ns * 16 + r, 4 * s + g);
+#pragma unroll
+        for (int mi = 0; mi < 5; ++mi) {
+          const bf16x8 a = lm_frag(xs, mi * 16 + r, 4 * s + g);
+#pragma unroll
+          for (int ns = 0; ns < 2; ++ns)
+            acc[mi][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[ns], a, acc[mi][ns], 0, 0, 0);
+        }
+      }
+    }
+    if (t != kt - 1) continue;
+
+    // ---- block done: logits, this lane's best of its 8 values per row, clear ----
+    const uint32_t col0 = (uint32_t)(c0 - rc0 + wave * 32 + 4 * g);
+#pragma unroll
+    for (int mi = 0; mi < 5; ++mi) {
+      const int m = mi * 16 + r;
+      uint32_t best = 0;
+#pragma unroll
+      for (int ns = 0; ns < 2; ++ns) {
+        const floatx4 v = acc[mi][ns];
+        const u32x2 bits = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        if (p.y != nullptr && m < p.m && live)
+          *(u32x2*)(p.y + (int64_t)m * p.ldy + c0 + wave * 32 + ns * 16 + 4 * g) = bits;
+        if (live) {
+          const uint32_t o0 = bf16x2_order(bits[0]);
+          const uint32_t o1 = bf16x2_order(bits[1]);
+          const uint32_t rank = 7u - 4u * ns;
+          best = max(best, (o0 << 16) | rank);
+          best = max(best, (o0 & 0xFFFF0000u) | (rank - 1u));
+          best = max(best, (o1 << 16) | (rank - 2u));
+          best = max(best, (o1 & 0xFFFF0000u) | (rank - 3u));
+        }
+        acc[mi][ns] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+      const uint32_t pos = 7u - (best & 7u);
+      const uint32_t col = col0 + (pos >> 2) * 16u + (pos & 3u);
+      if (best != 0) row_best[mi] = max(row_best[mi], (best & 0xFFFF0000u) | (0xFFFFu - col));
+    }
+  }
+
+  // ---- the range's argmax partials: per row, the best of the four waves of each
+  // 128-column half (waves 0..3, 4..7), as the 320-row kernel's waves nw = 0, 1 keep them
+  uint32_t* s_best = (uint32_t*)smem;  // [wave][80 rows]
+  __syncthreads();                     // every wave is past its last stage
+#pragma unroll
+  for (int mi = 0; mi < 5; ++mi) {
+    uint32_t b2 = row_best[mi];
+    b2 = max(b2, (uint32_t)__shfl_xor(b2, 16));
+    b2 = max(b2, (uint32_t)__shfl_xor(b2, 32));
+    if (g == 0) s_best[wave * kLsRows + mi * 16 + r] = b2;
+  }
+  __syncthreads();
+  if (p.argmax != nullptr && (wave & 3) == 0) {
+    const int half = wave >> 2;
+    for (int m = lane; m < p.m; m += kWave) {
+      uint32_t b2 = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) b2 = max(b2, s_best[(half * 4 + w) * kLsRows + m]);
+      const uint32_t n = (uint32_t)rc0 + 0xFFFFu - (b2 & 0xFFFFu);
+      p.argmax[(int64_t)m * tiles + 2 * blockIdx.x + half] =
+          b2 == 0 ? 0 : ((uint64_t)(b2 >> 16) << 32) | (uint64_t)(0xFFFFFFFFu - n);
+    }
+  }
+}
+
 int launch_lm_head(GemmParams p, hipStream_t stream) {
+  const int groups = p.n / kArgmaxCols;
+  const int grid = groups < kLmMaxGrid ? groups : kLmMaxGrid;
+  if (p.m <= kLsRows) {
+    static const hipError_t attr_small = hipFuncSetAttribute(
+        (const void*)lm_head_small_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLsRing * kLsStage);
+    if (attr_small != hipSuccess) {
+      set_error("lm_head: cannot reserve %d bytes of LDS: %s", kLsRing * kLsStage, hipGetErrorString(attr_small));
+      return NE_ELAUNCH;
+    }
+    hipLaunchKernelGGL(lm_head_small_kernel, dim3((unsigned)grid), dim3(kLmWaves * kWave), kLsRing * kLsStage,
+                       stream, p);
+    return check_launch("lm_head");
+  }
   static const hipError_t attr = hipFuncSetAttribute(
       (const void*)lm_head_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLmRing * kLmStage);
   if (attr != hipSuccess) {
     set_error("lm_head: cannot reserve %d bytes of LDS: %s", kLmRing * kLmStage, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  const int groups = p.n / kArgmaxCols;
-  const int grid = groups < kLmMaxGrid ? groups : kLmMaxGrid;
   hipLaunchKernelGGL(lm_head_kernel, dim3((unsigned)grid), dim3(kLmWaves * kWave), kLmRing * kLmStage, stream, p);
   return check_launch("lm_head");
 }

@@ -151,6 +151,24 @@ def test_lm_head_argmax_ties_pick_the_first_column(device):
     assert torch.equal(idx, first)
 
 
+@pytest.mark.parametrize("m", [80, 64, 5, 1])
+def test_lm_head_small_batch_kernel_equals_the_320_row_kernel(device, m):
+    """At most 80 rows run their own LM-head kernel (each wave 32 columns x all rows, a
+    three-stage ring); it sums every logit in the 320-row kernel's order, so its logits and
+    argmax partials equal, bit for bit, those the 320-row kernel gives the same rows (81
+    rows select that kernel).  Full vocabulary, short last blocks included."""
+    vocab = 151936
+    g = torch.Generator().manual_seed(500 + m)
+    hidden = (torch.randn(81, 1024, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    embed = (torch.randn(vocab, 1024, generator=g) * 0.02).to(torch.bfloat16).to(device)
+    big_logits, big_parts = kernels.lm_head(hidden, embed, logits=True, argmax_partials=True)
+    logits, parts = kernels.lm_head(hidden[:m].contiguous(), embed, logits=True, argmax_partials=True)
+    _, parts_only = kernels.lm_head(hidden[:m].contiguous(), embed, logits=False, argmax_partials=True)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, big_logits[:m])
+    assert torch.equal(parts, big_parts[:m]) and torch.equal(parts_only, parts)
+
+
 def test_lm_head_argmax_only_matches_logits_path(device):
     hidden = (torch.randn(64, 1024) * 0.02).to(torch.bfloat16).to(device)
     embed = (torch.randn(8192, 1024) * 0.02).to(torch.bfloat16).to(device)
