@@ -759,6 +759,13 @@ def run_gemm_roofline(torch, layers: int = 28, reps: int = 10, counters: dict | 
         if counters is not None and name in counters:
             entry["counters"] = counters[name]
         out[name] = entry
+    # at most 80 rows the LM head runs its small-batch kernel (a draft model's 64-row decode)
+    from nanoengine_amd import kernels
+
+    h64, a64 = w.hidden[:64], w.argmax[:64]
+    us = _graph_time_us(torch, lambda: kernels.lm_head(h64, w.embed, logits=False, argmax_partials=a64), reps)
+    out["lm_head_64_rows"] = {"avg_us": round(us, 2), "weight_GB_s": round(w.weight_bytes("lm_head") / us / 1e3, 1),
+                              "m": 64, "kernel": "lm_head_small_kernel"}
     del w
     torch.cuda.empty_cache()
     proj = [n for n in GEMM_NAMES if n != "lm_head"]
