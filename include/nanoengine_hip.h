@@ -225,8 +225,10 @@ int ne_w8a16_gemm_splitk(const void* x, int64_t ldx, const int8_t* w, const void
  * keys, each the largest bf16-rounded logit of a disjoint set of columns with its first
  * index, packed for an ordered max (the row's argmax is the largest key as an unsigned
  * 64-bit integer; its low 32 bits hold 0xFFFFFFFF - column; 0 marks an empty set), for
- * ne_accept to finish.  The sets are each work-group's column range split between its two
- * column waves: ne_lm_head_num_tiles(n) = 2 * min(n / 64, 256); n <= 2^24.
+ * ne_accept to finish.  The sets are each work-group's column range split into the two
+ * 128-column halves of its 256-column blocks: ne_lm_head_num_tiles(n) = 2 * min(n / 64,
+ * 256); n <= 2^24.  At most 80 rows run a kernel of their own (each wave 32 columns
+ * against all rows) that gives the same logits and keys, bit for bit.
  */
 int32_t ne_lm_head_num_tiles(int32_t n);
 int ne_lm_head(const void* x, int64_t ldx, const void* w, int32_t m, int32_t n, int32_t k,
