@@ -410,11 +410,23 @@ class AttentionWorkload:
         self._kernels.paged_kv_stream_planned(pool[0], pool[1], pool[2], pool[3], len(self.ctx), 16, self.ql,
                                               int(self.ctx.max()), self.ws)
 
+    def runs_plan(self) -> None:
+        """Balanced whole-slot runs of the same tiles, in place of the work plan."""
+        self._kernels.paged_kv_runs_plan(self.tables, 16, self.ctx_d, 16, 8, self.ql, int(self.ctx.max()), self.ws)
+
+    def stream_runs(self, pool) -> None:
+        """The same K/V bytes read in the runs (all 8 KV heads of a tile per work-group)."""
+        self._kernels.paged_kv_stream_runs(pool[0], pool[1], pool[2], pool[3], len(self.ctx), 16, self.ql,
+                                           int(self.ctx.max()), self.ws)
+
 
 def stream_ceiling(torch, w: AttentionWorkload, reps: int) -> dict:
     """Time per call of the planned call's K/V streamed alone (ne_paged_kv_stream_planned,
     same plan, tiles, ring and copies, no arithmetic) over the same pools, from HIP events
-    on the launching stream: what the access pattern costs the memory system."""
+    on the launching stream: what the access pattern costs the memory system.  Beside it,
+    `whole_slot_runs`: the same bytes through the same ring and copies in balanced runs
+    that cross sequences, each work-group reading all 8 KV heads of its tiles
+    (ne_paged_kv_runs_plan + ne_paged_kv_stream_runs)."""
     from nanoengine_amd import _native
 
     w.plan()
@@ -431,8 +443,30 @@ def stream_ceiling(torch, w: AttentionWorkload, reps: int) -> dict:
     dur = timer.durations_ms()
     us = 1e3 * sum(dur) / len(dur)
     kv_bytes = attention_bytes(w.ctx.tolist(), 0, int8=w.pools[0][2] is not None)
+    # the same bytes in balanced whole-slot runs across sequences: is the ceiling the
+    # planned split's or the memory system's?
+    w.runs_plan()
+    for p in w.pools:
+        w.stream_runs(p)
+    torch.cuda.synchronize()
+    runs_timer = _native.LaunchTimer()
+    _native.set_launch_timer("ne_paged_kv_stream_runs", runs_timer)
+    for _ in range(reps):
+        for p in w.pools:
+            w.stream_runs(p)
+    torch.cuda.synchronize()
+    _native.set_launch_timer("ne_paged_kv_stream_runs", None)
+    runs = runs_timer.durations_ms()
+    runs_us = 1e3 * sum(runs) / len(runs)
+    if w.ws.error_flag() != 0:
+        raise RuntimeError("the K/V stream raised the workspace error flag")
+    w.plan()  # the runs took the work plan's place
     return {"us": round(us, 2), "kv_bytes": int(kv_bytes), "GB_s": round(kv_bytes / us / 1e3, 1),
-            "frac_of_peak": round(kv_bytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            "frac_of_peak": round(kv_bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "whole_slot_runs": {"us": round(runs_us, 2), "GB_s": round(kv_bytes / runs_us / 1e3, 1),
+                                "frac_of_peak": round(kv_bytes / runs_us / 1e3 / HBM_PEAK_GBS, 4),
+                                "split": "the sequences' tiles in order, cut into the plan grid's near-equal "
+                                         "runs across sequences; a work-group reads all 8 KV heads of its run"}}
 
 
 ATTENTION_WORKLOADS = {

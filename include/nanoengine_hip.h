@@ -190,6 +190,25 @@ int ne_paged_kv_stream_planned(const void* k_cache, const void* v_cache, const v
                                int32_t max_q_len, int32_t max_ctx_len, int32_t split_len,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Measurement entry points, no counterpart in the reference: the same K/V bytes read in
+ * whole-slot runs.  ne_paged_kv_runs_plan takes the sequences' 16-key tiles in order and
+ * cuts them into the workspace's plan_grid runs of near-equal length, across sequence
+ * boundaries.  It writes them where ne_paged_attention_plan writes its work items, so a
+ * planned call afterwards needs a fresh ne_paged_attention_plan.  ne_paged_kv_stream_runs
+ * then reads all 8 KV heads of every tile of run w in work-group w, through the planned
+ * call's LDS ring, copies and waits, and computes and stores nothing.  Its time is the
+ * stream of a balanced whole-slot split.  ne_paged_kv_stream_planned gives the stream of
+ * the planned call's own split, for comparison.  Same shapes, workspace and block-table
+ * contract as ne_paged_attention_plan. */
+int ne_paged_kv_runs_plan(const int32_t* block_tables, int32_t block_table_stride, int32_t block_size,
+                          const int32_t* ctx_len, int32_t num_seqs, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t max_q_len, int32_t max_ctx_len, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int ne_paged_kv_stream_runs(const void* k_cache, const void* v_cache, const void* k_scale,
+                            const void* v_scale, int32_t kv_dtype, int32_t scale_dtype, int32_t num_seqs,
+                            int32_t num_q_heads, int32_t num_kv_heads, int32_t max_q_len,
+                            int32_t max_ctx_len, void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * A8 - W8A16 projection: y[m, n] = bf16(sum_k x[m, k] * w[n, k] * scale[n])
  * with int8 weights dequantised in registers onto bf16 MFMA (replaces

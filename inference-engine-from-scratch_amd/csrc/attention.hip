@@ -1631,8 +1631,9 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_att
 // the same work items from the plan, gives each wave the same tiles, and streams them
 // through the same LDS ring with the same copies and waits, but computes nothing and
 // stores nothing: its time is what this access pattern costs the memory system, the
-// ceiling the attention kernel is measured against.
-template <int KS, bool BF16>
+// ceiling the attention kernel is measured against.  RUNS: the items are the balanced
+// runs of kv_runs_plan_kernel (tiles of several sequences, no context of their own).
+template <int KS, bool BF16, bool RUNS = false>
 __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_kv_stream_kernel(AttnParams p) {
   using Shape = DmaShape<KS, BF16>;
   constexpr int HG = Shape::heads;
@@ -1653,9 +1654,10 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_kv_
   const int32_t my_slot = p.plan_slots[(int64_t)widx * kPlanMaxTiles + tid];
   const ConstI32* d = (const ConstI32*)(p.plan_desc + (int64_t)widx * kDescInts);
   const int seq = d[0], split = d[1], n_splits = d[2], j0 = d[3], ctx = d[4], j1 = d[7];
-  const bool sane = seq < p.num_seqs && n_splits >= 1 && split >= 0 && split < n_splits && ctx > 0 &&
-                    ctx <= p.max_ctx && j0 >= 0 && j0 < j1 && j1 - j0 <= kPlanMaxTiles &&
-                    (j1 - 1) * kTileKeys < ctx;
+  const bool sane = RUNS ? (j0 == 0 && j1 > 0 && j1 <= kPlanMaxTiles)
+                         : (seq < p.num_seqs && n_splits >= 1 && split >= 0 && split < n_splits && ctx > 0 &&
+                            ctx <= p.max_ctx && j0 >= 0 && j0 < j1 && j1 - j0 <= kPlanMaxTiles &&
+                            (j1 - 1) * kTileKeys < ctx);
   if (seq < 0 || !sane) {
     if (seq >= 0 && tid == 0) atomicOr(p.error_flag, 2u);
     return;
@@ -1694,6 +1696,90 @@ __global__ __launch_bounds__((DmaShape<KS, BF16>::waves * kWave)) void paged_kv_
     if (2 * it + 1 + RING < n_tiles) copy_tile(2 * it + 1 + RING, ring + ((2 * it + 1) % RING) * kSlot);
   }
   dma_wait_vmcnt<0>();  // no copy may land in LDS after the wave has left
+}
+
+// Measurement plan of whole-slot runs: the sequences' 16-key tiles in order (sequence 0's,
+// then sequence 1's, ...), T in all, cut into plan_grid runs of near-equal length that
+// cross sequence boundaries; run w holds tiles [T w / G, T (w + 1) / G).  Work-group w of
+// paged_kv_stream_kernel<1, BF16, true> then reads all 8 KV heads of every tile in its
+// run (wave h: head h), so each 16-slot block is fetched whole by one work-group and every
+// work-group moves the same bytes.  The stream of that split is what the planned call's
+// own split (whole sequences, 2 KV heads per work-group) is compared against.
+__global__ __launch_bounds__(kHeadWaves * kWave) void kv_runs_plan_kernel(AttnParams p) {
+  __shared__ int s_first[kPlanMaxSeqs + 1];  // first tile of each sequence, then T
+  __shared__ int s_wave[kHeadWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int B = p.num_seqs;
+  int tiles[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = 2 * tid + k;
+    const int ctx = i < B ? min(p.ctx_len[i], p.max_ctx) : 0;
+    tiles[k] = ctx > 0 ? (ctx + kTileKeys - 1) / kTileKeys : 0;
+  }
+  const int c = tiles[0] + tiles[1];
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(incl, d);
+    if (lane >= d) incl += y;
+  }
+  if (lane == kWave - 1) s_wave[wave] = incl;
+  __syncthreads();
+  int base = 0, T = 0;
+#pragma unroll
+  for (int w = 0; w < kHeadWaves; ++w) {
+    const int x = s_wave[w];
+    base += (w < wave) ? x : 0;
+    T += x;
+  }
+  const int f0 = base + incl - c;
+  if (2 * tid < B) s_first[2 * tid] = f0;
+  if (2 * tid + 1 < B) s_first[2 * tid + 1] = f0 + tiles[0];
+  if (tid == 0) s_first[B] = T;
+  __syncthreads();
+  const int G = p.plan_grid;
+  const int w = blockIdx.x;
+  const int start = (int)((int64_t)T * w / G);
+  int n = (int)((int64_t)T * (w + 1) / G) - start;
+  if (n > kPlanMaxTiles) {  // the workspace's plan_grid keeps T / G below this
+    if (tid == 0) atomicOr(p.error_flag, 1u);
+    n = kPlanMaxTiles;
+  }
+  if (tid == 0) {
+    int32_t* d = p.plan_desc + (int64_t)w * kDescInts;
+    d[0] = n > 0 ? 0 : -1;
+    d[1] = 0;
+    d[2] = 1;
+    d[3] = 0;  // the run's tiles [d[3], d[7])
+    d[4] = 0;
+    d[5] = 0;
+    d[6] = 0;
+    d[7] = n;
+  }
+  if (tid < n) {
+    // tile g lies in the last sequence whose first tile is <= g (an empty sequence shares
+    // its first tile with the next one, which then is the last such sequence)
+    const int g = start + tid;
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (s_first[mid] <= g)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int key0 = (g - s_first[lo]) * kTileKeys;
+    const int entry = key0 / p.block_size;
+    int slot = 0;
+    if (entry < p.bt_stride)
+      slot = p.block_tables[(int64_t)lo * p.bt_stride + entry] * p.block_size + key0 % p.block_size;
+    else
+      atomicOr(p.error_flag, 1u);
+    p.plan_slots[(int64_t)w * kPlanMaxTiles + tid] = slot;
+  }
 }
 
 // Partials of a row requested together by the merge kernels: a split-length plan gives
@@ -2227,17 +2313,17 @@ extern "C" int ne_paged_verify_attention_planned(
 
 namespace ne {
 namespace {
-template <int KS, bool BF16>
+template <int KS, bool BF16, bool RUNS = false>
 int launch_kv_stream_ks(const AttnParams& p, unsigned grid, hipStream_t s) {
   constexpr int lds = DmaShape<KS, BF16>::lds;
-  static const hipError_t attr = hipFuncSetAttribute((const void*)paged_kv_stream_kernel<KS, BF16>,
+  static const hipError_t attr = hipFuncSetAttribute((const void*)paged_kv_stream_kernel<KS, BF16, RUNS>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) {
     set_error("paged_kv_stream_kernel: cannot reserve %d bytes of LDS: %s", lds, hipGetErrorString(attr));
     return NE_ELAUNCH;
   }
-  hipLaunchKernelGGL((paged_kv_stream_kernel<KS, BF16>), dim3(grid), dim3(DmaShape<KS, BF16>::waves * kWave), lds,
-                     s, p);
+  hipLaunchKernelGGL((paged_kv_stream_kernel<KS, BF16, RUNS>), dim3(grid),
+                     dim3(DmaShape<KS, BF16>::waves * kWave), lds, s, p);
   return check_launch("paged_kv_stream_kernel");
 }
 
@@ -2292,4 +2378,74 @@ extern "C" int ne_paged_kv_stream_planned(const void* k_cache, const void* v_cac
   p.plan_slots = (int32_t*)(ws + L.slots_off);
   return kv_dtype == NE_DTYPE_BF16 ? launch_kv_stream<true>(p, (hipStream_t)stream)
                                    : launch_kv_stream<false>(p, (hipStream_t)stream);
+}
+
+extern "C" int ne_paged_kv_runs_plan(const int32_t* block_tables, int32_t block_table_stride, int32_t block_size,
+                                     const int32_t* ctx_len, int32_t num_seqs, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t max_q_len, int32_t max_ctx_len, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
+               "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_q_heads, num_kv_heads);
+  NE_CHECK_SUPPORTED(block_size > 0 && block_size % kTileKeys == 0,
+                     "block_size must be a positive multiple of 16 (got %d)", block_size);
+  NE_CHECK_ARG(block_tables && ctx_len, "null pointer argument");
+  NE_CHECK_ARG(max_q_len > 0 && max_ctx_len > 0, "max_q_len and max_ctx_len must be positive");
+  const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, 0, NE_DTYPE_INT8);
+  NE_CHECK_SUPPORTED(num_kv_heads == kHeadWaves && L.mtiles <= kMaxRowTiles && num_seqs <= kPlanMaxSeqs,
+                     "the runs follow the planned path's shapes: 8 KV heads, at most %d query rows per KV "
+                     "head and at most %d sequences", kMaxRowTiles * kRows, kPlanMaxSeqs);
+  NE_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total,
+               "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+  AttnParams p{};
+  p.block_tables = block_tables;
+  p.bt_stride = block_table_stride;
+  p.block_size = block_size;
+  p.ctx_len = ctx_len;
+  p.num_seqs = num_seqs;
+  p.num_kv_heads = num_kv_heads;
+  p.max_ctx = max_ctx_len;
+  p.plan_grid = L.plan_grid;
+  char* ws = (char*)workspace;
+  p.error_flag = (uint32_t*)(ws + L.error_off);
+  p.plan_desc = (int32_t*)(ws + L.desc_off);
+  p.plan_slots = (int32_t*)(ws + L.slots_off);
+  hipLaunchKernelGGL(kv_runs_plan_kernel, dim3((unsigned)L.plan_grid), dim3(kHeadWaves * kWave), 0,
+                     (hipStream_t)stream, p);
+  return check_launch("kv_runs_plan_kernel");
+}
+
+extern "C" int ne_paged_kv_stream_runs(const void* k_cache, const void* v_cache, const void* k_scale,
+                                       const void* v_scale, int32_t kv_dtype, int32_t scale_dtype, int32_t num_seqs,
+                                       int32_t num_q_heads, int32_t num_kv_heads, int32_t max_q_len,
+                                       int32_t max_ctx_len, void* workspace, size_t workspace_bytes, void* stream) {
+  NE_CHECK_ARG(num_seqs >= 0, "num_seqs < 0");
+  if (num_seqs == 0) return NE_OK;
+  NE_CHECK_ARG(k_cache && v_cache && workspace, "null pointer argument");
+  NE_CHECK_ARG(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && max_q_len > 0 &&
+                   max_ctx_len > 0,
+               "bad attention shape");
+  NE_CHECK_ARG(kv_dtype == NE_DTYPE_BF16 || kv_dtype == NE_DTYPE_INT8, "kv_dtype must be bf16 or int8");
+  const Layout L = make_layout(num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, 0, kv_dtype);
+  NE_CHECK_SUPPORTED(dma_serves(kv_dtype, scale_dtype, num_kv_heads, L.mtiles, num_seqs, k_scale, v_scale),
+                     "the stream follows the planned path's shapes");
+  NE_CHECK_ARG(workspace_bytes >= L.total, "workspace of %zu bytes is smaller than the %zu required",
+               workspace_bytes, L.total);
+  AttnParams p{};
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.num_seqs = num_seqs;
+  p.num_kv_heads = num_kv_heads;
+  p.max_ctx = max_ctx_len;
+  p.plan_grid = L.plan_grid;
+  char* ws = (char*)workspace;
+  p.error_flag = (uint32_t*)(ws + L.error_off);
+  p.plan_desc = (int32_t*)(ws + L.desc_off);
+  p.plan_slots = (int32_t*)(ws + L.slots_off);
+  return kv_dtype == NE_DTYPE_BF16
+             ? launch_kv_stream_ks<1, true, true>(p, (unsigned)L.plan_grid, (hipStream_t)stream)
+             : launch_kv_stream_ks<1, false, true>(p, (unsigned)L.plan_grid, (hipStream_t)stream);
 }

@@ -71,6 +71,14 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
     ),
+    "ne_paged_kv_runs_plan": (
+        ctypes.c_int,
+        [_vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
+    "ne_paged_kv_stream_runs": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp],
+    ),
     "ne_w8a16_gemm": (
         ctypes.c_int,
         [_vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],

@@ -147,6 +147,7 @@ class AttentionWorkspace:
     buffer: torch.Tensor | None = None
     layout: tuple | None = None
     plan_key: tuple | None = None
+    runs_key: tuple | None = None  # metadata of the last paged_kv_runs_plan (measurement)
     frozen: bool = False
 
     def get(self, device: torch.device, nbytes: int, layout: tuple) -> torch.Tensor:
@@ -157,11 +158,11 @@ class AttentionWorkspace:
                                    f"this call needs {nbytes} bytes on {device}: size it before capture")
             self.buffer = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
             self.layout = layout
-            self.plan_key = None
+            self.plan_key = self.runs_key = None
         elif self.layout != layout:
             self.buffer.zero_()
             self.layout = layout
-            self.plan_key = None
+            self.plan_key = self.runs_key = None
         return self.buffer
 
     def error_flag(self) -> int:
@@ -337,6 +338,7 @@ def paged_attention_plan(
     )
     workspace.plan_key = _plan_key(block_tables, block_size, ctx_len, q_start, q_len, max_q_len, max_ctx_len,
                                    split_len)
+    workspace.runs_key = None
 
 
 def paged_kv_stream_planned(
@@ -364,6 +366,66 @@ def paged_kv_stream_planned(
         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), dtype_code(k_cache.dtype),
         dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16, num_seqs, num_q_heads, num_kv_heads, max_q_len,
         max_ctx_len, split_len, _ptr(workspace.buffer), workspace.buffer.numel(), _stream(device),
+    )
+
+
+def paged_kv_runs_plan(
+    block_tables: torch.Tensor,
+    block_size: int,
+    ctx_len: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    max_q_len: int,
+    max_ctx_len: int,
+    workspace: AttentionWorkspace,
+) -> None:
+    """Measurement: cut the sequences' 16-key tiles, in order, into the workspace's
+    plan_grid runs of near-equal length across sequence boundaries, for
+    :func:`paged_kv_stream_runs`.  The runs take the place of the attention work plan,
+    so a planned call afterwards needs :func:`paged_attention_plan` again."""
+    device = _require_gpu(block_tables, ctx_len)
+    _int32(block_tables, "block_tables")
+    _int32(ctx_len, "ctx_len")
+    num_seqs = ctx_len.shape[0]
+    nbytes = _native.load().ne_paged_attention_workspace_size(
+        num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, 0
+    )
+    _check(nbytes > 0, "bad attention shape")
+    ws = workspace.get(device, nbytes, (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len, 0))
+    _native.call(
+        "ne_paged_kv_runs_plan",
+        _ptr(block_tables), block_tables.stride(0), block_size, _ptr(ctx_len), num_seqs, num_q_heads,
+        num_kv_heads, max_q_len, max_ctx_len, _ptr(ws), ws.numel(), _stream(device),
+    )
+    workspace.plan_key = None
+    workspace.runs_key = (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len)
+
+
+def paged_kv_stream_runs(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_scale: torch.Tensor | None,
+    v_scale: torch.Tensor | None,
+    num_seqs: int,
+    num_q_heads: int,
+    max_q_len: int,
+    max_ctx_len: int,
+    workspace: AttentionWorkspace,
+) -> None:
+    """Measurement: the same K/V bytes as the planned call, read in the balanced whole-slot
+    runs that :func:`paged_kv_runs_plan` wrote (work-group w reads all 8 KV heads of every
+    tile of run w through the planned call's ring and copies; nothing computed or stored)."""
+    device = _require_gpu(k_cache, v_cache, k_scale, v_scale)
+    num_kv_heads = k_cache.shape[1]
+    _check(workspace.buffer is not None
+           and workspace.runs_key == (num_seqs, num_q_heads, num_kv_heads, max_q_len, max_ctx_len),
+           "the stream reads the runs paged_kv_runs_plan wrote into the workspace for this shape")
+    is_int8 = k_cache.dtype == torch.int8
+    _native.call(
+        "ne_paged_kv_stream_runs",
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), dtype_code(k_cache.dtype),
+        dtype_code(k_scale.dtype) if is_int8 else DTYPE_BF16, num_seqs, num_q_heads, num_kv_heads, max_q_len,
+        max_ctx_len, _ptr(workspace.buffer), workspace.buffer.numel(), _stream(device),
     )
 
 

@@ -109,3 +109,12 @@ def test_plan_entry_points_refuse_shapes_off_the_planned_path(lib):
     # a workspace smaller than the plan's layout
     rc = lib.ne_paged_attention_plan(p, 64, 16, p, p, p, 8, 16, 8, 5, 1024, 0, p, ctypes.c_size_t(64), null)
     assert rc == -1 and b"workspace" in lib.ne_last_error()
+    # the whole-slot runs (measurement): the same shapes, block sizes and workspace
+    rc = lib.ne_paged_kv_runs_plan(p, 64, 16, p, 8, 16, 4, 5, 1024, p, ws, null)
+    assert rc == -2 and b"8 KV heads" in lib.ne_last_error()
+    rc = lib.ne_paged_kv_runs_plan(p, 64, 24, p, 8, 16, 8, 5, 1024, p, ws, null)
+    assert rc == -2 and b"block_size" in lib.ne_last_error()
+    rc = lib.ne_paged_kv_runs_plan(p, 64, 16, p, 8, 16, 8, 5, 1024, p, ctypes.c_size_t(64), null)
+    assert rc == -1 and b"workspace" in lib.ne_last_error()
+    rc = lib.ne_paged_kv_stream_runs(p, p, null, null, 0, 0, 8, 16, 4, 5, 1024, p, ws, null)
+    assert rc == -2 and b"planned path" in lib.ne_last_error()

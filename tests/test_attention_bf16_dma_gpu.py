@@ -113,3 +113,56 @@ def test_kv_stream_follows_the_plan(device, kv_dtype):
         kernels.paged_kv_stream_planned(d(kc), d(vc), d(ks), d(vs), len(ctx), HQ, 5, max(ctx), ws)
         torch.cuda.synchronize()
         assert ws.error_flag() == 0
+
+
+def _runs_in_workspace(ws, grid):
+    """The runs' items [grid][8] and slot lists [grid][512] (int32): the workspace's last two
+    regions, each starting on a 256-byte boundary, the slot lists last."""
+    slots_bytes = grid * 512 * 4
+    items_bytes = -(-grid * 8 * 4 // 256) * 256
+    buf = ws.buffer.cpu()
+    slots = buf[buf.numel() - slots_bytes:].view(torch.int32).view(grid, 512)
+    items = buf[buf.numel() - slots_bytes - items_bytes:][: grid * 32].view(torch.int32).view(grid, 8)
+    return items, slots
+
+
+@pytest.mark.parametrize("kv_dtype", ["int8", "bf16"])
+@pytest.mark.parametrize("case", ["64_seqs_with_empty_ones", "4_short_seqs"])
+def test_kv_stream_runs_cover_every_tile_once_in_order(device, kv_dtype, case):
+    """The whole-slot runs (measurement entry points): the sequences' 16-key tiles in order,
+    cut into the plan grid's near-equal runs across sequence boundaries, empty sequences
+    (inside the order and at its end) and empty runs included; the stream over them leaves
+    no error flag, and a planned call afterwards is refused until the plan is written again."""
+    from nanoengine_amd import _native
+
+    if case == "64_seqs_with_empty_ones":
+        ctx = np.random.default_rng(5).integers(1, 1025, size=64).tolist()
+        ctx[3] = ctx[40] = ctx[63] = 0
+    else:
+        ctx = [17, 0, 5, 40]
+    num_blocks = sum((c + 15) // 16 for c in ctx) + 8
+    kc, vc, ks, vs = make_pool(num_blocks, 16, HKV, kv_dtype, torch.float16, seed=3)
+    tables, ctx_t, qs, ql, _ = make_batch(ctx, [5] * len(ctx), num_blocks, 16, seed=4)
+    d = lambda t: None if t is None else t.to(device)
+    ws = kernels.AttentionWorkspace()
+    kernels.paged_kv_runs_plan(d(tables), 16, d(ctx_t), HQ, HKV, 5, max(ctx), ws)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    assert ws.buffer.numel() == _native.load().ne_paged_attention_workspace_size(len(ctx), HQ, HKV, 5, max(ctx), 0)
+    grid = 256  # max(256, 2 B, B + ceil(B * max_tiles / 512)) at these shapes
+    items, slots = _runs_in_workspace(ws, grid)
+    expected = [int(tables[b, j]) * 16 for b, c in enumerate(ctx) for j in range((c + 15) // 16)]
+    T = len(expected)
+    sizes = [T * (w + 1) // grid - T * w // grid for w in range(grid)]
+    assert items[:, 7].tolist() == sizes
+    assert items[:, 3].tolist() == [0] * grid
+    assert items[:, 0].tolist() == [0 if n > 0 else -1 for n in sizes]
+    got = [int(x) for w in range(grid) for x in slots[w, : sizes[w]]]
+    assert got == expected
+    kernels.paged_kv_stream_runs(d(kc), d(vc), d(ks), d(vs), len(ctx), HQ, 5, max(ctx), ws)
+    torch.cuda.synchronize()
+    assert ws.error_flag() == 0
+    q = torch.zeros(5 * len(ctx), HQ, 128, dtype=torch.bfloat16, device=device)
+    args = (q, d(kc), d(vc), d(ks), d(vs), d(tables), 16, d(ctx_t), d(qs), d(ql))
+    with pytest.raises(ValueError, match="paged_attention_plan"):
+        kernels.paged_verify_attention(*args, max_q_len=5, max_ctx_len=max(ctx), workspace=ws, planned=True)
