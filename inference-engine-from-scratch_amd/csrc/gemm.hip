@@ -95,10 +95,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---- W8A16 projections ----------------------------------------------------------
-// Work-group tile: PM * 16 token rows (80 for the plain shapes) x 16 * NSUB weight rows,
-// sized so that the verify-step shapes give about one work-group per CU (M = 320: QKV
-// N = 4096 and gate|up N = 6144 give 256 tiles; o / down N = 1024 give 64 tiles, split
-// 4 ways over K).  The MFMA waves form KG k-groups x NSUB / NPW: wave (kg, nw) runs the
+// Work-group tile: PM * 16 token rows (80 for the plain shapes, 48 for split-K) x 16 *
+// NSUB weight rows, sized so that the verify-step shapes give about one work-group per
+// CU (M = 320: QKV N = 4096 and gate|up N = 6144 give 256 tiles; o / down N = 1024 give
+// 7 x 16 tiles of 48 rows, split 2 ways over K).  For o / down, 48-row tiles and two
+// splits (224 work-groups) against 80-row tiles and four (256): the split-K sum +
+// RMSNorm that follows reads half the fp32 partials; with 28 distinct weights replayed
+// back to back the pair takes 9.5 / 10.6 us instead of 10.6 / 11.3 us, inside the
+// verify step the GEMMs take the same time and the norm 0.14 us less.  Fewer rows gain
+// more: 288 rows (6 x 16 x 2 work-groups instead of 4 x 16 x 4) and 64 rows (2 x 16 x 4
+// instead of 1 x 16 x 4).  The MFMA waves form KG k-groups x NSUB / NPW: wave (kg, nw) runs the
 // 4 / KG k-steps kg * 4 / KG .. (32 wide each) of every 128-wide stage for all PM token
 // subtiles against weight subtiles nw * NPW .. + NPW, so each X fragment read from LDS
 // feeds NPW MFMAs and each weight fragment PM.  At the end, wave (kg, nw) finishes the
@@ -112,7 +118,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 // its vmcnt counts one stream and its wait for a stage is exact.  Each wave reads the
 // fragments of stage t from LDS before it runs the MFMAs of stage t - 1 (held in
 // registers), so the LDS latency hides under the multiplies.
-constexpr int kPM = 5;  // token subtiles per work-group (the fused QKV epilogue uses 3)
+constexpr int kPM = 5;       // token subtiles per work-group (the fused QKV epilogue uses 3)
+constexpr int kSplitPM = 3;  // token subtiles per work-group of the split-K product
 constexpr int kQkvKRows = 32;  // rows per work-group of the fused QKV kernel's k heads (q / v: 48)
 
 template <int NSUB, int PM, int KG, int NPW>
@@ -597,8 +604,9 @@ int launch_proj_kt(GemmParams p, int splits, float* partial, hipStream_t stream,
 }
 
 // Stage counts with a kernel of their own: 8 (K = 1024, the QKV and gate|up
-// projections of the 0.6B model), 4 and 6 (o and down split 4 ways over K = 2048 and
-// 3072); any other count runs the loop with a run-time count.
+// projections of the 0.6B model), and for split-K 8 and 12 (o and down split 2 ways over
+// K = 2048 and 3072) and 4 and 6 (the same split 4 ways, for fewer rows); any other
+// count runs the loop with a run-time count.
 template <int NSUB, int SDT, int EPI, int KV, int PM, int KG, int NPW>
 int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, const char* name,
                 const QkvRopeArgs& qa = QkvRopeArgs{}) {
@@ -606,6 +614,8 @@ int launch_proj(GemmParams p, int splits, float* partial, hipStream_t stream, co
   if constexpr (EPI == 3) {
     if (kt == 4) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 4>(p, splits, partial, stream, name, qa);
     if (kt == 6) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 6>(p, splits, partial, stream, name, qa);
+    if (kt == 8) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 8>(p, splits, partial, stream, name, qa);
+    if (kt == 12) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 12>(p, splits, partial, stream, name, qa);
   } else {
     if (kt == 8) return launch_proj_kt<NSUB, SDT, EPI, KV, PM, KG, NPW, 8>(p, splits, partial, stream, name, qa);
   }
@@ -638,7 +648,7 @@ int dispatch_w8a16(GemmParams p, int epilogue, int splits, float* partial, hipSt
     return launch_proj<4, SDT, 1, 0, kPM, kKgSwiglu, kNpwSwiglu>(p, 1, nullptr, s, "w8a16_swiglu");
   }
   if (partial != nullptr)
-    return launch_proj<4, SDT, 3, 0, kPM, kKgPlain, kNpwPlain>(p, splits, partial, s, "w8a16_splitk");
+    return launch_proj<4, SDT, 3, 0, kSplitPM, kKgPlain, kNpwPlain>(p, splits, partial, s, "w8a16_splitk");
   return launch_proj<4, SDT, 0, 0, kPM, kKgPlain, kNpwPlain>(p, 1, nullptr, s, "w8a16_gemm");
 }
 

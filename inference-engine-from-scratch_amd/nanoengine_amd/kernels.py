@@ -469,13 +469,15 @@ def w8a16_gemm(
 
 
 PROJ_TILE_ROWS = 80  # token rows per work-group of the W8A16 kernels
+SPLITK_TILE_ROWS = 48  # token rows per work-group of the split-K product
 PROJ_TILE_COLS = 64  # weight rows per work-group of the store / split-K kernels
 TARGET_WORK_GROUPS = 256  # one per CU
 
 
 def splitk_splits(m: int, n: int, k: int, max_splits: int = 4) -> int:
-    """K splits that bring a narrow projection to about one work-group per CU."""
-    tiles = -(-m // PROJ_TILE_ROWS) * (n // PROJ_TILE_COLS)
+    """K splits that bring a narrow projection to about one work-group per CU (at most; 320
+    rows of o / down give 7 x 16 tiles of 48 rows and 2 splits)."""
+    tiles = -(-m // SPLITK_TILE_ROWS) * (n // PROJ_TILE_COLS)
     splits = max(1, min(max_splits, TARGET_WORK_GROUPS // max(tiles, 1)))
     while splits > 1 and k % (128 * splits):
         splits -= 1

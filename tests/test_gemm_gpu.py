@@ -65,8 +65,9 @@ def test_w8a16_splitk_partials(device, m, n, k, splits):
 
 
 def test_splitk_choice_targets_one_work_group_per_cu():
-    assert kernels.splitk_splits(320, 1024, 2048) == 4
-    assert kernels.splitk_splits(320, 1024, 3072) == 4
+    assert kernels.splitk_splits(320, 1024, 2048) == 2  # 7 x 16 tiles of 48 rows
+    assert kernels.splitk_splits(320, 1024, 3072) == 2
+    assert kernels.splitk_splits(64, 1024, 3072) == 4  # 2 x 16 tiles
     assert kernels.splitk_splits(320, 4096, 1024) == 1
     assert kernels.splitk_splits(4096, 1024, 3072) == 1
     assert kernels.splitk_splits(80, 1024, 384) == 3  # 3 parts of 128; 4 would not divide k
