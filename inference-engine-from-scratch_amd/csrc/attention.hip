@@ -1782,10 +1782,11 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void kv_runs_plan_kernel(AttnPa
   }
 }
 
-// Partials of a row requested together by the merge kernels: a split-length plan gives
-// a sequence at most kMergeBatch partials per pass of loads, so every (m, l, O) of a row
-// is requested at once rather than in a dependent chain.
-constexpr int kMergeBatch = 8;
+// Partials of a row requested together by the merge kernels, so that every (m, l, O) of
+// a row is requested at once rather than in a dependent chain.  16 covers the ~14 splits
+// per sequence of 16 sequences of 256-2048 keys in one pass (8 took two: that merge ran
+// 1.1 us longer) and the ~7 of the long-context plan.
+constexpr int kMergeBatch = 16;
 
 // Merges n partial states (m, l, O) of one query row: out = sum_s 2^(m_s - M) O_s /
 // sum_s 2^(m_s - M) l_s over dims cd..cd+7.  pi(s) is the row of partial s in part_ml /
