@@ -847,7 +847,7 @@ struct DmaShape {
   static_assert(lds <= 160 * 1024, "LDS of one CU");
 };
 constexpr int kPlanMinTiles = 16;                     // contexts up to 256 keys are never split
-constexpr int kPlanFloorTiles = 4;                    // no split shorter than 64 keys
+constexpr int kPlanFloorTiles = 8;                    // no split shorter than 128 keys
 constexpr int kPlanCUs = 256;                         // work-groups the plan aims to fill
 constexpr int kWholeMaxTiles = 64;                    // longest context of a whole-sequence plan
 
@@ -866,7 +866,7 @@ int whole_plan_ks(int num_seqs, int max_ctx, int split_len, int mtiles) {
 // covers tiles [tiles_b s / n_b, tiles_b (s+1) / n_b)).  W is p.plan_w when the
 // caller fixed the split length; else 16 when every context fits in 16 tiles (one
 // split per sequence, so no partials and no merge kernel); else
-// max(4, ceil(T / (G - B))) for T = sum_b tiles_b, G = p.plan_grid work-groups and
+// max(8, ceil(T / (G - B))) for T = sum_b tiles_b, G = p.plan_grid work-groups and
 // B sequences -- splitting is paid for already, so W only balances the longest
 // split against the mean.  Both keep sum_b n_b <= G:
 // the longest sequence is spread over as many work-groups as its share of T asks
