@@ -1783,25 +1783,28 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void kv_runs_plan_kernel(AttnPa
 }
 
 // Partials of a row requested together by the merge kernels, so that every (m, l, O) of
-// a row is requested at once rather than in a dependent chain.  16 covers the ~14 splits
-// per sequence of 16 sequences of 256-2048 keys in one pass (8 took two: that merge ran
-// 1.1 us longer) and the ~7 of the long-context plan.
-constexpr int kMergeBatch = 16;
+// a row is requested at once rather than in a dependent chain: batches of 8, or of 16 for
+// a sequence of more than 8 splits.  16 covers the ~14 splits per sequence of 16
+// sequences of 256-2048 keys in one pass (8 took two: that merge ran 1.1 us longer);
+// for 3 splits a batch of 16 made the merge 1 us longer than one of 8.
+constexpr int kMergeBatch = 8;
+constexpr int kMergeBatchWide = 16;
 
 // Merges n partial states (m, l, O) of one query row: out = sum_s 2^(m_s - M) O_s /
 // sum_s 2^(m_s - M) l_s over dims cd..cd+7.  pi(s) is the row of partial s in part_ml /
-// part_o; the partials of a batch of kMergeBatch are all requested before any is used
-// (a slot past the last partial re-reads partial s0 and is ignored).
-template <typename PartIndex>
-__device__ __forceinline__ void merge_partials(const AttnParams& p, int n, int cd, PartIndex pi,
-                                               uint16_t* dst) {
+// part_o; the partials of a batch of B are all requested before any is used (a slot past
+// the last partial re-reads partial s0 and is ignored: loads under a condition were
+// measured to lose the batching).
+template <int B, typename PartIndex>
+__device__ __forceinline__ void merge_partials_batched(const AttnParams& p, int n, int cd, PartIndex pi,
+                                                       uint16_t* dst) {
   float MM = kNegBig, LL = 0.f;
   float tot[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < n; s0 += kMergeBatch) {
-    float ms[kMergeBatch], ls[kMergeBatch];
-    floatx4 x0[kMergeBatch], x1[kMergeBatch];
+  for (int s0 = 0; s0 < n; s0 += B) {
+    float ms[B], ls[B];
+    floatx4 x0[B], x1[B];
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
+    for (int j = 0; j < B; ++j) {
       const int64_t r = pi((s0 + j < n) ? s0 + j : s0);
       const float2 ml = *(const float2*)(p.part_ml + r * 2);
       ms[j] = (s0 + j < n) ? ml.x : kNegBig;
@@ -1812,14 +1815,14 @@ __device__ __forceinline__ void merge_partials(const AttnParams& p, int n, int c
     }
     float Mb = MM;
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, ms[j]);
+    for (int j = 0; j < B; ++j) Mb = fmaxf(Mb, ms[j]);
     const float rescale = __builtin_amdgcn_exp2f(MM - Mb);
     LL *= rescale;
 #pragma unroll
     for (int d = 0; d < 8; ++d) tot[d] *= rescale;
     MM = Mb;
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
+    for (int j = 0; j < B; ++j) {
       const float a = (s0 + j < n) ? __builtin_amdgcn_exp2f(ms[j] - MM) : 0.f;
       LL += a * ls[j];
 #pragma unroll
@@ -1832,6 +1835,15 @@ __device__ __forceinline__ void merge_partials(const AttnParams& p, int n, int c
   const float inv = 1.f / LL;
   *(u32x4*)dst = u32x4{pack_bf16x2(tot[0] * inv, tot[1] * inv), pack_bf16x2(tot[2] * inv, tot[3] * inv),
                        pack_bf16x2(tot[4] * inv, tot[5] * inv), pack_bf16x2(tot[6] * inv, tot[7] * inv)};
+}
+
+// n is the same for every thread of a row's work-group: the choice does not diverge
+template <typename PartIndex>
+__device__ __forceinline__ void merge_partials(const AttnParams& p, int n, int cd, PartIndex pi, uint16_t* dst) {
+  if (n > kMergeBatch)
+    merge_partials_batched<kMergeBatchWide>(p, n, cd, pi, dst);
+  else
+    merge_partials_batched<kMergeBatch>(p, n, cd, pi, dst);
 }
 
 // Combines the partials of every sequence the plan split: one work-group per
