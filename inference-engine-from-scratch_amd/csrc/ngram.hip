@@ -7,10 +7,11 @@
 // at s ends at e = s + n - 1 <= len - 2, and it matches exactly when the tokens ending
 // at e and those ending at len - 1 agree on their last n; so one pass over end
 // positions e = len - 2, len - 3, ..., computing that agreement length c(e) (up to
-// max_ngram), finds for every n the largest matching e at once.  The pass runs 1024
-// ends at a time (4 per thread) and stops after the first chunk holding a max_ngram
-// match, which is the common case in long histories; without one, the same pass has
-// already found the smaller n's answers.  The guesses are the tokens that followed
+// max_ngram), finds for every n the largest matching e at once.  The pass runs 4096
+// ends at a time (16 per thread) against the chunk's stretch of history, staged in LDS
+// with one coalesced load, and stops after the first chunk holding a max_ngram match,
+// which is the common case in long histories; without one, the same pass has already
+// found the smaller n's answers.  The guesses are the tokens that followed
 // the window, clipped to the history, so they are never empty.
 #include "ne_common.hpp"
 
@@ -19,8 +20,9 @@ namespace ne {
 namespace {
 
 constexpr int kMaxNgram = 16;
-constexpr int kScanPerThread = 4;
-constexpr int kScanChunk = 256 * kScanPerThread;
+constexpr int kScanPerThread = 16;
+constexpr int kScanChunk = 256 * kScanPerThread;  // ends per pass
+constexpr int kStage = kScanChunk + kMaxNgram;     // history tokens a pass compares
 
 // The counters a verify step leaves for the next one (adv != nullptr): the work-group of
 // sequence b first advances b's counters and takes its guess count from them.
@@ -39,6 +41,7 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
                                                     int min_ngram, int max_drafts, int32_t* drafts,
                                                     int32_t* num_drafts, StepCounters adv) {
   __shared__ int s_best[kMaxNgram][256 / kWave];
+  __shared__ int s_hist[kStage];
   __shared__ int s_want;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -78,34 +81,51 @@ __global__ __launch_bounds__(256) void ngram_kernel(const int32_t* history, int6
   for (int i = 0; i < kMaxNgram; ++i) found[i] = -1;
   if (!scan) __syncthreads();  // uniform: publishes s_want
   for (int hi = scan ? len - 2 : -1; hi >= 0; hi -= kScanChunk) {
+    // the pass's ends are hi - 4095 .. hi and their windows reach 15 tokens further back:
+    // s_hist[k] = h[base + k] for the history positions 0 .. hi among them.  The previous
+    // pass's reads of s_hist ended before its last barrier.
+    const int base = hi - kScanChunk - kMaxNgram + 2;
+    for (int k = tid; k < kStage; k += 256) {
+      const int pos = base + k;
+      s_hist[k] = (pos >= 0 && pos <= hi) ? h[pos] : 0;
+    }
+    __syncthreads();
     // thread tid tests ends hi - tid, hi - tid - 256, ...: its first hit for each n is
     // its largest, and the owner of the chunk's largest hit has no larger one
     int best[kMaxNgram];
 #pragma unroll
     for (int i = 0; i < kMaxNgram; ++i) best[i] = -1;
+    // the last token of each of this thread's ends first: only an end that matches it
+    // reads the rest of its window (most do not), in the same order, largest end first
+    uint32_t hit = 0;
 #pragma unroll
     for (int j = 0; j < kScanPerThread; ++j) {
       const int e = hi - j * 256 - tid;
-      if (e >= 0) {
-        // the window's tokens are all requested before the first comparison, so the
-        // loads overlap instead of waiting on one another's match
-        int tok[kMaxNgram];
+      if (e >= 0 && s_hist[e - base] == suffix[0]) hit |= 1u << j;
+    }
+    while (hit != 0) {
+      const int j = __builtin_ctz(hit);
+      hit &= hit - 1;
+      const int e = hi - j * 256 - tid;
+      // the window's tokens are all read before the first comparison, so the LDS reads
+      // overlap (e - i - base >= 0 for every i: the stage reaches 15 tokens below the
+      // pass's lowest end)
+      int tok[kMaxNgram];
 #pragma unroll
-        for (int i = 0; i < kMaxNgram; ++i) tok[i] = (i < nmax && e - i >= 0) ? h[e - i] : 0;
-        int c = 0;  // tokens ending at e that equal those ending at len - 1
-        bool same = true;
+      for (int i = 0; i < kMaxNgram; ++i) tok[i] = s_hist[e - i - base];
+      int c = 0;  // tokens ending at e that equal those ending at len - 1
+      bool same = true;
 #pragma unroll
-        for (int i = 0; i < kMaxNgram; ++i) {
-          if (same && i < nmax && e - i >= 0 && tok[i] == suffix[i]) {
-            ++c;
-          } else {
-            same = false;
-          }
+      for (int i = 0; i < kMaxNgram; ++i) {
+        if (same && i < nmax && e - i >= 0 && tok[i] == suffix[i]) {
+          ++c;
+        } else {
+          same = false;
         }
-#pragma unroll
-        for (int i = 0; i < kMaxNgram; ++i)
-          if (i < c && best[i] < 0) best[i] = e;
       }
+#pragma unroll
+      for (int i = 0; i < kMaxNgram; ++i)
+        if (i < c && best[i] < 0) best[i] = e;
     }
 #pragma unroll
     for (int i = 0; i < kMaxNgram; ++i) {
