@@ -295,8 +295,9 @@ __device__ __forceinline__ void proj_mainloop(const GemmParams& p, char* smem, i
   // stage t: its copies are in LDS after the barrier, and every wave has read stage
   // t - 1 into registers before it (lgkmcnt(0)), so the slots of stage t - 1 take the
   // copies of stages t + kRX - 1 and t + kRW - 1.  The MFMAs of stage t - 1 run on
-  // weights converted to bf16 during step t - 1, and stage t's weights are converted
-  // after them, so the conversion overlaps the MFMAs still in the pipeline.
+  // weights converted to bf16 from the int8 read in step t - 1; the compiler places that
+  // conversion just before those MFMAs (it keeps the int8 form live across the barrier),
+  // so a wave converts and then multiplies.
   auto step = [&](int t, XFrag& xr_, WFrag& wr_, AFrag& ar, const XFrag& xm, const AFrag& am) {
     wait_stage(t);
     wait_lgkmcnt0();
