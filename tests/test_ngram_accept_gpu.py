@@ -101,7 +101,7 @@ def test_ngram_long_history_k8(device):
 
 def test_ngram_match_found_deep_in_the_history(device):
     """Distinct tokens with one planted earlier occurrence of the last n tokens, at
-    depths on both sides of the kernel's 1024-start chunk edges, at start 0, only for
+    depths on both sides of 1,024 and 2,048 starts from the newest, at start 0, only for
     n = 2 or n = 1, twice (the later copy wins) or nowhere."""
     L = 5000
     base = list(range(10000, 10000 + L))
@@ -117,6 +117,33 @@ def test_ngram_match_found_deep_in_the_history(device):
     want = [oracle_ngram.propose(h, 8, 3) for h in cases]
     assert got == want
     assert all(w for w in want[:10]) and want[10] == []
+
+
+def test_ngram_sixteen_token_matches_at_the_scan_pass_edges(device):
+    """max_ngram 16 over 12,000 distinct tokens: the kernel compares 4,096 window ends per
+    pass against a stretch of history held in LDS that reaches 15 tokens below the pass's
+    lowest end.  Planted 16-token matches end on both sides of the first and second pass
+    edges (end e = len - 2 - d for d around 4,096 and 8,192), at the history's start, and
+    5-token-only matches (the token before the suffix is new) end at the same edges."""
+    L = 12000
+    base = list(range(20000, 20000 + L))
+    cases = []
+    for d in (4094, 4095, 4096, 4097, 8191, 8192, 8193):
+        # history base + base[p:p+16] has len L + 16, so the planted end p + 15 is len - 2 - d
+        p = L - 1 - d
+        cases.append(base + base[p:p + 16])
+    cases.append(base + base[0:16])  # the match starts at token 0
+    for d in (4095, 4096, 8192):
+        # history base + [new] + base[p:p+5] has len L + 6: the 5-token match ends at p + 4
+        p = L - d
+        cases.append(base + [7] + base[p:p + 5])
+    got = run_ngram(device, cases, [8] * len(cases), max_ngram=16, max_drafts=8)
+    want = [oracle_ngram.propose(h, 8, 16) for h in cases]
+    assert got == want
+    assert all(want)
+    for d, w in zip((4094, 4095, 4096, 4097, 8191, 8192, 8193), want):
+        p = L - 1 - d
+        assert w == base[p + 16:p + 24]  # the planted window, and not some other one
 
 
 def bf16_logits(rows, vocab, rng, scale=1.0):
